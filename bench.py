@@ -1,0 +1,326 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GGUF quantized linear-layer path.
+
+Headline: Q4_K GEMV (M=1) at K=4096 x N=14336, achieved HBM GB/s on the
+packed-weight bytes.  A step is one GEMV launch over one full weight matrix.
+Weights rotate over enough copies (>= 512 MiB) that the 256 MB Infinity Cache
+cannot hold them, so every step streams its matrix from HBM.  Inputs are
+resident in HBM before the timed region; launches are replayed from a captured
+HIP graph on the launch stream, and HIP events on that stream bracket exactly
+the timed launches.
+
+Secondary lines (in "extra"): the other GEMV configurations, the Q8_0 bf16
+MFMA GEMM (M = 16 / 128 / 512; TFLOP/s at M = 512 is the metric's second
+half) and the Q4_K MoE grouped FFN, each timed the same way.
+
+cpu_baseline: the C restatement of the reference's Java raw mat-vec (oracle/)
+on this host's cores, on the same Q4_K matrix (rank 0, N = 1 only).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "Q4_K GEMV achieved HBM GB/s (% peak) @4096x14336; GEMM TFLOP/s M=512"
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0       # MI355X dense bf16 MFMA, published
+ROTATION_BYTES = 640 * 2 ** 20  # > 512 MiB of distinct weight copies
+PROFILE_DIR = REPO / "profiles"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=400)
+    p.add_argument("--warmup", type=int, default=40)
+    p.add_argument("--no-extra", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--only", default="", help="comma list of workload names to run")
+    return p.parse_args()
+
+
+# ---- timing helpers ---------------------------------------------------------
+
+class Rotation:
+    """Device copies of one packed weight matrix, launched round robin."""
+
+    def __init__(self, torch, host_bytes, type_id: int, rows: int, cols: int):
+        from gollek_amd import tensor_ops as ops
+        nbytes = host_bytes.size
+        self.copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
+        base = torch.from_numpy(host_bytes.reshape(-1)).cuda()
+        self.buffers = [base] + [base.clone() for _ in range(self.copies - 1)]
+        self.weights = [ops.DeviceWeight(type_id, b.data_ptr(), rows, cols) for b in self.buffers]
+        self.nbytes = nbytes
+
+    def close(self):
+        for w in self.weights:
+            w.close()
+
+
+def graph_time(torch, launch, copies: int, steps: int, warmup: int):
+    """Capture `copies` launches (one per weight copy) in a graph, replay it;
+    returns (ms per launch, launches timed)."""
+    reps = max(1, math.ceil(steps / copies))
+    wreps = max(1, math.ceil(warmup / copies))
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(copies):  # eager warm-up before capture
+            launch(i, stream.cuda_stream)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        s = torch.cuda.current_stream().cuda_stream
+        for i in range(copies):
+            launch(i, s)
+    with torch.cuda.stream(stream):
+        for _ in range(wreps):
+            g.replay()
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            g.replay()
+        end.record(stream)
+    end.synchronize()
+    torch.cuda.synchronize()
+    n = reps * copies
+    return start.elapsed_time(end) / n, n
+
+
+# ---- workloads ----------------------------------------------------------------
+
+def gemv_workload(torch, type_id: int, rows: int, cols: int, steps: int, warmup: int, seed: int):
+    from gollek_amd import synthetic as syn
+    host = syn.matrix(type_id, rows, cols, seed)
+    rot = Rotation(torch, host, type_id, rows, cols)
+    x = torch.from_numpy(syn.activation(cols, seed + 1)).cuda()
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+
+    def launch(i, stream):
+        rot.weights[i].matvec(x.data_ptr(), y.data_ptr(), rows, stream)
+
+    ms, n = graph_time(torch, launch, rot.copies, steps, warmup)
+    algo_bytes = rot.nbytes + 4 * cols + 4 * rows
+    res = {
+        "ms_per_step": ms, "steps": n, "weight_copies": rot.copies,
+        "weight_bytes": int(rot.nbytes), "algo_bytes": int(algo_bytes),
+        "weight_gbs": rot.nbytes / (ms * 1e-3) / 1e9,
+        "algo_gbs": algo_bytes / (ms * 1e-3) / 1e9,
+        "gflops": 2.0 * rows * cols / (ms * 1e-3) / 1e9,
+    }
+    rot.close()
+    return res, host
+
+
+def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int):
+    from gollek_amd import synthetic as syn
+    rows = cols = 4096
+    host = syn.q8_0_matrix(rows, cols, seed)
+    rot = Rotation(torch, host, syn.Q8_0, rows, cols)
+    xb = torch.from_numpy(syn.activation_bf16(m, cols, seed + 1).view("int16")).cuda()
+    y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+
+    def launch(i, stream):
+        rot.weights[i].gemm_bf16(xb.data_ptr(), m, y.data_ptr(), stream)
+
+    ms, n = graph_time(torch, launch, rot.copies, steps, warmup)
+    flops = 2.0 * m * rows * cols
+    algo_bytes = rot.nbytes + 2 * m * cols + 4 * m * rows
+    res = {
+        "ms_per_step": ms, "steps": n, "m": m, "weight_copies": rot.copies,
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "algo_gbs": algo_bytes / (ms * 1e-3) / 1e9,
+    }
+    rot.close()
+    return res
+
+
+def moe_workload(torch, steps: int, warmup: int, seed: int):
+    import numpy as np
+
+    from gollek_amd import moe as moe_mod
+    from gollek_amd import synthetic as syn
+    E, k, H, I, T = 128, 8, 2048, 768, 16
+    gate = syn.q4_k_matrix(E * I, H, seed)
+    up = syn.q4_k_matrix(E * I, H, seed + 1)
+    down = syn.q4_k_matrix(E * H, I, seed + 2)
+    ids, w = syn.moe_routing(T, E, k, seed + 3)
+    x = syn.activation(T * H, seed + 4).reshape(T, H)
+    layer = moe_mod.DeviceMoe(torch, gate, up, down, E, copies=2)
+    xd = torch.from_numpy(x).cuda()
+    idd = torch.from_numpy(ids).cuda()
+    wd = torch.from_numpy(w).cuda()
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+
+    def launch(i, stream):
+        layer.run(i, xd.data_ptr(), idd.data_ptr(), wd.data_ptr(), T, k, out.data_ptr(), stream)
+
+    ms, n = graph_time(torch, launch, layer.copies, steps, warmup)
+    used = len(np.unique(ids))
+    bytes_used = used * (gate.shape[1] * I + up.shape[1] * I + down.shape[1] * H) + 2 * T * H * 4
+    res = {"ms_per_step": ms, "steps": n, "experts_touched": int(used),
+           "algo_bytes": int(bytes_used), "algo_gbs": bytes_used / (ms * 1e-3) / 1e9}
+    layer.close()
+    return res
+
+
+# ---- CPU baseline -------------------------------------------------------------
+
+def cpu_baseline(host, cols: int):
+    """Oracle (C restatement of the reference's Java raw route) on all host
+    cores over the full Q4_K matrix: median of >= 10 reps after 2 warm-ups;
+    plus a single-thread rate on the first 1024 rows."""
+    from gollek_amd import synthetic as syn
+    from oracle import oracle as o
+    x = syn.activation(cols, 99)
+    threads = o.default_threads()
+    for _ in range(2):
+        o.matvec(syn.Q4_K, host, cols, x, threads=threads)
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while len(times) < 10 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        o.matvec(syn.Q4_K, host, cols, x, threads=threads)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    sample_rows = 1024
+    sub = host[:sample_rows]
+    st = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        o.matvec(syn.Q4_K, sub, cols, x, threads=1)
+        st.append(time.perf_counter() - t0)
+    st_med = statistics.median(st)
+    return {
+        "value": host.size / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"full Q4_K 14336x4096 matrix ({host.size} packed bytes), median of "
+                   f"{len(times)} reps after 2 warm-ups, {threads} threads; C restatement of "
+                   f"the reference Java raw route (oracle/gguf_oracle.c)"),
+        "ms_per_matvec": med * 1e3,
+        "single_thread_gbs": sub.size / st_med / 1e9,
+    }
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel
+    calibration recorded in the same file), or None."""
+    path = PROFILE_DIR / "q4k_gemv_4096x14336_pmc.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "single-GPU build: this path runs on one GPU; "
+                                   f"--gpus {args.gpus} is not supported (use --gpus 1)"}))
+        log(f"--gpus {args.gpus} requested: only the one-GPU path exists; exiting")
+        return 2
+    import torch
+    from gollek_amd import synthetic as syn
+    from gollek_amd import tensor_ops as ops
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    ops.init(0)
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not only or name in only
+
+    log("headline: Q4_K GEMV K=4096 N=14336")
+    head, host = gemv_workload(torch, syn.Q4_K, 14336, 4096, args.steps, args.warmup, seed=2)
+    log(f"headline {head['weight_gbs']:.1f} GB/s, {head['ms_per_step'] * 1e3:.2f} us/launch")
+
+    extra = {}
+    if not args.no_extra:
+        for name, t, rows, cols in (("q8_0_gemv_4096x4096", syn.Q8_0, 4096, 4096),
+                                    ("q4_0_gemv_4096x11008", syn.Q4_0, 11008, 4096),
+                                    ("q4_k_gemv_4096x128256", syn.Q4_K, 128256, 4096)):
+            if not want(name):
+                continue
+            log(f"extra {name}")
+            r, _ = gemv_workload(torch, t, rows, cols, args.steps, args.warmup, seed=5)
+            r["hbm_frac"] = r["weight_gbs"] / HBM_PEAK_GBS
+            extra[name] = r
+        have_gemm = hasattr(ops.DeviceWeight, "gemm_bf16") and _has_symbol("gollek_hip_gemm_bf16_device")
+        for m in (16, 128, 512):
+            name = f"q8_0_gemm_bf16_m{m}_4096x4096"
+            if have_gemm and want(name):
+                log(f"extra {name}")
+                extra[name] = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
+        if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e128_top8_t16"):
+            log("extra moe")
+            extra["moe_q4_k_e128_top8_t16"] = moe_workload(torch, args.steps, args.warmup, seed=11)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle restatement of the reference raw route)")
+        cpu = cpu_baseline(host, 4096)
+
+    ms = head["ms_per_step"]
+    value = head["weight_gbs"]
+    achieved = head["algo_gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded; GGUF Q4_K packed weights, fp32 N(0,1) activation)",
+        "config": {
+            "workload": "q4_k_gemv_m1_k4096_n14336",
+            "type": "Q4_K", "m": 1, "k": 4096, "n": 14336,
+            "weight_bytes": head["weight_bytes"], "weight_copies": head["weight_copies"],
+            "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    g512 = extra.get("q8_0_gemm_bf16_m512_4096x4096")
+    if g512:
+        line["gemm_tflops_m512"] = round(g512["tflops"], 2)
+    print(json.dumps(line))
+    return 0
+
+
+def _has_symbol(name: str) -> bool:
+    from gollek_amd import _native
+    return hasattr(_native.load(), name)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

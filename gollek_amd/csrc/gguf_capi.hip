@@ -1,0 +1,382 @@
+// gguf_capi.hip -- the C ABI declared in include/gollek_hip.h.
+//
+// Validation mirrors the Java facade it replaces (RT/GgufTensorOps.java,
+// RT/GgufMatVec.java, RT/GgufTensorShape.java:53-72, GC/core/GgmlType.java:
+// 70-81; RT/ = runner/gguf/gollek-gguf-core/src/main/java/tech/kayys/gollek/
+// gguf/runtime/) in both the checks and their order, so the Java adapter can
+// rethrow the same exceptions with the same messages.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "gguf_kernels.hpp"
+#include "gollek_hip.h"
+
+struct gollek_hip_weight {
+    int32_t type_id = 0;
+    int64_t rows = 0, cols = 0, row_bytes = 0;
+    int device = 0;
+    uint8_t *data = nullptr;
+    bool owned = false;
+    std::mutex mu;                 // serialises the host-buffer entry points
+    hipStream_t stream = nullptr;  // stream of the host-buffer entry points
+    uint8_t *staging = nullptr;    // device staging for host x / y / dst
+    size_t staging_bytes = 0;
+};
+
+namespace {
+
+constexpr int32_t kAbiVersion = 1 * 10000 + 0 * 100 + 0;
+
+thread_local std::string g_last_error;
+thread_local int32_t g_last_status = GOLLEK_HIP_OK;
+
+int32_t fail(int32_t code, char *err, size_t err_len, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    g_last_status = code;
+    if (err != nullptr && err_len > 0) {
+        size_t n = strlen(buf);
+        if (n >= err_len) n = err_len - 1;
+        memcpy(err, buf, n);
+        err[n] = '\0';
+    }
+    return code;
+}
+
+void ok(char *err, size_t err_len) {
+    g_last_error.clear();
+    g_last_status = GOLLEK_HIP_OK;
+    if (err != nullptr && err_len > 0) err[0] = '\0';
+}
+
+int32_t hip_fail(hipError_t e, const char *what, char *err, size_t err_len) {
+    return fail(e == hipErrorOutOfMemory ? GOLLEK_HIP_ERR_NOMEM : GOLLEK_HIP_ERR_DEVICE, err,
+                err_len, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+const char *type_label(int32_t type_id) {
+    switch (type_id) {
+    case GOLLEK_HIP_Q4_0: return "Q4_0";
+    case GOLLEK_HIP_Q8_0: return "Q8_0";
+    case GOLLEK_HIP_Q4_K: return "Q4_K";
+    default: return "?";
+    }
+}
+
+int block_size(int32_t type_id) { return type_id == GOLLEK_HIP_Q4_K ? 256 : 32; }
+
+int block_bytes(int32_t type_id) {
+    return type_id == GOLLEK_HIP_Q4_K ? 144 : (type_id == GOLLEK_HIP_Q8_0 ? 34 : 18);
+}
+
+bool supported(int32_t type_id) {
+    return type_id == GOLLEK_HIP_Q4_0 || type_id == GOLLEK_HIP_Q8_0 || type_id == GOLLEK_HIP_Q4_K;
+}
+
+std::mutex g_init_mu;
+int g_initialised_device = -1;
+
+// Makes `device` current on this thread and records its CU count once.
+int32_t use_device(int device, char *err, size_t err_len) {
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice", err, err_len);
+    std::lock_guard<std::mutex> lock(g_init_mu);
+    if (g_initialised_device != device) {
+        int cus = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute", err, err_len);
+        if (cus > 0) gollek::tuning().cu_count = cus;
+        g_initialised_device = device;
+    }
+    return GOLLEK_HIP_OK;
+}
+
+// GC/core/GgmlType.java:70-81 and RT/GgufTensorShape.java:185-198.
+int32_t check_shape(int32_t type_id, int64_t rows, int64_t cols, int64_t row_bytes, char *err,
+                    size_t err_len) {
+    if (!supported(type_id))
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "Unsupported GGUF quantized matmul type id: %d", type_id);
+    if (rows < 0 || cols <= 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Invalid matrix shape %lld x %lld",
+                    (long long)rows, (long long)cols);
+    const int bs = block_size(type_id);
+    if (cols % bs != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Element count %lld is not a multiple of block size %d for type %s",
+                    (long long)cols, bs, type_label(type_id));
+    const int64_t expect = cols / bs * block_bytes(type_id);
+    if (row_bytes != expect)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Row byte size %lld does not match %lld for %lld %s columns",
+                    (long long)row_bytes, (long long)expect, (long long)cols,
+                    type_label(type_id));
+    return GOLLEK_HIP_OK;
+}
+
+int32_t ensure_staging(gollek_hip_weight *w, size_t bytes, char *err, size_t err_len) {
+    if (w->staging_bytes >= bytes) return GOLLEK_HIP_OK;
+    if (w->staging != nullptr) {
+        (void)hipFree(w->staging);
+        w->staging = nullptr;
+        w->staging_bytes = 0;
+    }
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&w->staging), bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(staging)", err, err_len);
+    w->staging_bytes = bytes;
+    return GOLLEK_HIP_OK;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+gollek_hip_weight *make_weight(int32_t type_id, int64_t rows, int64_t cols, int64_t row_bytes,
+                               char *err, size_t err_len) {
+    if (check_shape(type_id, rows, cols, row_bytes, err, err_len) != GOLLEK_HIP_OK) return nullptr;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipGetDevice", err, err_len);
+        return nullptr;
+    }
+    if (use_device(device, err, err_len) != GOLLEK_HIP_OK) return nullptr;
+    gollek_hip_weight *w = new (std::nothrow) gollek_hip_weight();
+    if (w == nullptr) {
+        fail(GOLLEK_HIP_ERR_NOMEM, err, err_len, "out of host memory");
+        return nullptr;
+    }
+    w->type_id = type_id;
+    w->rows = rows;
+    w->cols = cols;
+    w->row_bytes = row_bytes;
+    w->device = device;
+    e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipStreamCreate", err, err_len);
+        delete w;
+        return nullptr;
+    }
+    return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t gollek_hip_version(void) { return kAbiVersion; }
+
+int32_t gollek_hip_init(int32_t device, char *err, size_t err_len) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount", err, err_len);
+    if (device < 0 || device >= count)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Device %d is outside [0, %d)", device, count);
+    const int32_t rc = use_device(device, err, err_len);
+    if (rc == GOLLEK_HIP_OK) ok(err, err_len);
+    return rc;
+}
+
+const char *gollek_hip_last_error(void) { return g_last_error.c_str(); }
+
+int32_t gollek_hip_last_status(void) { return g_last_status; }
+
+int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t err_len) {
+    if (key == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "key");
+    gollek::LaunchTuning &t = gollek::tuning();
+    if (strcmp(key, "gemv_rows_per_wave") == 0) t.gemv_rows_per_wave = value;
+    else if (strcmp(key, "gemv_row_batch") == 0) t.gemv_row_batch = (int)value;
+    else if (strcmp(key, "gemv_waves_per_cu") == 0) t.gemv_waves_per_cu = value > 0 ? (int)value : 8;
+    else if (strcmp(key, "gemm_variant") == 0) t.gemm_variant = (int)value;
+    else return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Unknown option %s", key);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+gollek_hip_weight *gollek_hip_weight_upload(int32_t type_id, const void *host_bytes, int64_t rows,
+                                            int64_t cols, int64_t row_bytes, char *err,
+                                            size_t err_len) {
+    if (host_bytes == nullptr) {
+        fail(GOLLEK_HIP_ERR_NULL, err, err_len, "host_bytes");
+        return nullptr;
+    }
+    gollek_hip_weight *w = make_weight(type_id, rows, cols, row_bytes, err, err_len);
+    if (w == nullptr) return nullptr;
+    const size_t bytes = (size_t)rows * (size_t)row_bytes;
+    if (bytes > 0) {
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&w->data), bytes);
+        if (e == hipSuccess) e = hipMemcpy(w->data, host_bytes, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            hip_fail(e, "weight upload", err, err_len);
+            gollek_hip_weight_free(w);
+            return nullptr;
+        }
+    }
+    w->owned = true;
+    ok(err, err_len);
+    return w;
+}
+
+gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *device_bytes,
+                                                 int64_t rows, int64_t cols, int64_t row_bytes,
+                                                 char *err, size_t err_len) {
+    if (device_bytes == nullptr) {
+        fail(GOLLEK_HIP_ERR_NULL, err, err_len, "device_bytes");
+        return nullptr;
+    }
+    gollek_hip_weight *w = make_weight(type_id, rows, cols, row_bytes, err, err_len);
+    if (w == nullptr) return nullptr;
+    w->data = const_cast<uint8_t *>(static_cast<const uint8_t *>(device_bytes));
+    w->owned = false;
+    ok(err, err_len);
+    return w;
+}
+
+void gollek_hip_weight_free(gollek_hip_weight *w) {
+    if (w == nullptr) return;
+    (void)hipSetDevice(w->device);
+    if (w->stream != nullptr) (void)hipStreamSynchronize(w->stream);
+    if (w->owned && w->data != nullptr) (void)hipFree(w->data);
+    if (w->staging != nullptr) (void)hipFree(w->staging);
+    if (w->stream != nullptr) (void)hipStreamDestroy(w->stream);
+    delete w;
+}
+
+int32_t gollek_hip_weight_info(const gollek_hip_weight *w, int32_t *type_id, int64_t *rows,
+                               int64_t *cols, int64_t *row_bytes) {
+    if (w == nullptr) return GOLLEK_HIP_ERR_NULL;
+    if (type_id) *type_id = w->type_id;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (row_bytes) *row_bytes = w->row_bytes;
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_dequantize_rows(gollek_hip_weight *w, int64_t row0, int64_t nrows, float *dst,
+                                   int64_t dst_len, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    if (dst == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "dst");
+    if (nrows < 0) return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Row count %lld is negative", (long long)nrows);
+    if (dst_len < nrows * w->cols)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Vector length %lld is smaller than columns %lld",
+                    (long long)dst_len, (long long)(nrows * w->cols));
+    if (row0 < 0 || row0 + nrows > w->rows || (nrows > 0 && row0 >= w->rows))
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Row %lld is outside tensor row count %lld",
+                    (long long)(row0 < 0 || row0 >= w->rows ? row0 : row0 + nrows - 1),
+                    (long long)w->rows);
+    if (nrows == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    std::lock_guard<std::mutex> lock(w->mu);
+    int32_t rc = use_device(w->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t bytes = (size_t)nrows * (size_t)w->cols * sizeof(float);
+    rc = ensure_staging(w, bytes, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    float *d_out = reinterpret_cast<float *>(w->staging);
+    hipError_t e = gollek::launch_dequant(w->type_id, w->data, w->row_bytes, w->cols, row0, nrows,
+                                          d_out, w->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, d_out, bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+    if (e != hipSuccess) return hip_fail(e, "dequantize", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+static int32_t matvec_host(gollek_hip_weight *w, const uint8_t *rows_base, int64_t nrows,
+                           const float *x, float *y, char *err, size_t err_len) {
+    std::lock_guard<std::mutex> lock(w->mu);
+    int32_t rc = use_device(w->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t x_bytes = align_up((size_t)w->cols * sizeof(float), 256);
+    const size_t y_bytes = (size_t)nrows * sizeof(float);
+    rc = ensure_staging(w, x_bytes + y_bytes, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    float *d_x = reinterpret_cast<float *>(w->staging);
+    float *d_y = reinterpret_cast<float *>(w->staging + x_bytes);
+    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)w->cols * sizeof(float), hipMemcpyHostToDevice,
+                                  w->stream);
+    if (e == hipSuccess)
+        e = gollek::launch_gemv(w->type_id, rows_base, w->row_bytes, w->cols, d_x, d_y, nrows,
+                                w->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+    if (e != hipSuccess) return hip_fail(e, "matvec", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_dot_row(gollek_hip_weight *w, int64_t row, const float *x, int64_t x_len,
+                           float *out, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "vector");
+    if (out == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "output");
+    if (x_len < w->cols)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Vector length %lld is smaller than columns %lld",
+                    (long long)x_len, (long long)w->cols);
+    if (row < 0 || row >= w->rows)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Row %lld is outside tensor row count %lld",
+                    (long long)row, (long long)w->rows);
+    return matvec_host(w, w->data + row * w->row_bytes, 1, x, out, err, err_len);
+}
+
+int32_t gollek_hip_matvec_rows(gollek_hip_weight *w, const float *x, int64_t x_len, float *y,
+                               int64_t y_len, int64_t row_count, char *err, size_t err_len) {
+    // RT/GgufMatVec.java:40-75: null checks, vector length, row count,
+    // output length, then the row_count == 0 no-op.
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "vector");
+    if (y == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "output");
+    if (x_len < w->cols)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Vector length %lld is smaller than columns %lld",
+                    (long long)x_len, (long long)w->cols);
+    if (row_count < 0 || row_count > w->rows)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Requested row count %lld is outside tensor rows %lld",
+                    (long long)row_count, (long long)w->rows);
+    if (y_len < row_count)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Output length %lld is smaller than requested rows %lld",
+                    (long long)y_len, (long long)row_count);
+    if (row_count == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    return matvec_host(w, w->data, row_count, x, y, err, err_len);
+}
+
+int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *w, int64_t row0, int64_t nrows,
+                                          float *dst, void *stream, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    if (dst == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "dst");
+    if (nrows < 0 || row0 < 0 || row0 + nrows > w->rows)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Rows [%lld, %lld) are outside tensor row count %lld",
+                    (long long)row0, (long long)(row0 + nrows), (long long)w->rows);
+    hipError_t e = gollek::launch_dequant(w->type_id, w->data, w->row_bytes, w->cols, row0, nrows,
+                                          dst, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_matvec_device(gollek_hip_weight *w, const float *x, float *y,
+                                 int64_t row_count, void *stream, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "vector");
+    if (y == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "output");
+    if (row_count < 0 || row_count > w->rows)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Requested row count %lld is outside tensor rows %lld",
+                    (long long)row_count, (long long)w->rows);
+    hipError_t e = gollek::launch_gemv(w->type_id, w->data, w->row_bytes, w->cols, x, y, row_count,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "matvec launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,269 @@
+"""Host-side mirror of gollek's GgufTensorOps facade over libgollek_hip.so.
+
+The reference facade is RT/GgufTensorOps.java (RT/ = runner/gguf/
+gollek-gguf-core/src/main/java/tech/kayys/gollek/gguf/runtime/): static
+dequantizeRow / dotRow / matVec / matVecParallel / matVecRows over a
+(GGUFModel, GGUFTensorInfo) pair whose bytes live in an mmapped file.  Here a
+GgufTensor carries the same (name, shape, type id, bytes) facts and uploads its
+bytes once to a device handle, the way the Java drop-in would key a handle by
+(model, tensor).  Calls have the reference's names, argument meaning and
+exceptions:
+
+    NullPointerError       <- GOLLEK_HIP_ERR_NULL      (Objects.requireNonNull)
+    IllegalArgumentError   <- GOLLEK_HIP_ERR_ARG       (IllegalArgumentException)
+    UnsupportedOperationError <- GOLLEK_HIP_ERR_UNSUPPORTED
+    DeviceError            <- GOLLEK_HIP_ERR_DEVICE / NOMEM
+
+Every call goes through the C ABI; there is no host fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _native
+
+BLOCK = {_native.Q4_0: (32, 18), _native.Q8_0: (32, 34), _native.Q4_K: (256, 144)}
+TYPE_NAMES = {_native.Q4_0: "Q4_0", _native.Q8_0: "Q8_0", _native.Q4_K: "Q4_K"}
+
+
+class GgufHipError(RuntimeError):
+    code = 0
+
+
+class NullPointerError(GgufHipError, TypeError):
+    code = _native.ERR_NULL
+
+
+class IllegalArgumentError(GgufHipError, ValueError):
+    code = _native.ERR_ARG
+
+
+class UnsupportedOperationError(GgufHipError, NotImplementedError):
+    code = _native.ERR_UNSUPPORTED
+
+
+class DeviceError(GgufHipError):
+    code = _native.ERR_DEVICE
+
+
+_BY_CODE = {
+    _native.ERR_NULL: NullPointerError,
+    _native.ERR_ARG: IllegalArgumentError,
+    _native.ERR_UNSUPPORTED: UnsupportedOperationError,
+    _native.ERR_DEVICE: DeviceError,
+    _native.ERR_NOMEM: DeviceError,
+}
+
+
+def check(rc: int, err: _native.ErrBuf) -> None:
+    if rc != _native.OK:
+        raise _BY_CODE.get(rc, GgufHipError)(err.text or f"status {rc}")
+
+
+def row_bytes_for(type_id: int, cols: int) -> int:
+    bs, bb = BLOCK[type_id]
+    return cols // bs * bb
+
+
+def init(device: int = 0) -> None:
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_init(device, err.buf, err.size), err)
+
+
+def set_option(key: str, value: int) -> None:
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_set_option(key.encode(), int(value), err.buf, err.size), err)
+
+
+@dataclass
+class GgufTensor:
+    """GGUFTensorInfo(name, shape, typeId, ...) plus its bytes.
+
+    shape[0] is the column count (contiguous); the remaining dimensions form
+    the rows (RT/GgufTensorOps.java:621-630)."""
+
+    name: str
+    shape: tuple[int, ...]
+    type_id: int
+    data: np.ndarray  # uint8, rows * row_bytes
+    _handle: int | None = field(default=None, repr=False)
+
+    @property
+    def columns(self) -> int:
+        return int(self.shape[0])
+
+    @property
+    def rows(self) -> int:
+        r = 1
+        for d in self.shape[1:]:
+            r *= int(d)
+        return r
+
+    @property
+    def row_bytes(self) -> int:
+        bs, bb = BLOCK.get(self.type_id, (1, 1))
+        return self.columns // bs * bb
+
+    def handle(self) -> int:
+        """Device handle, created on first use (the prepared-cache analogue)."""
+        if self._handle is None:
+            lib = _native.load()
+            err = _native.ErrBuf()
+            buf = np.ascontiguousarray(self.data, dtype=np.uint8)
+            h = lib.gollek_hip_weight_upload(self.type_id, buf.ctypes.data, self.rows,
+                                             self.columns, self.row_bytes, err.buf, err.size)
+            if not h:
+                raise _BY_CODE.get(lib.gollek_hip_last_status(), GgufHipError)(err.text)
+            self._handle = h
+        return self._handle
+
+    def close(self) -> None:
+        if self._handle is not None:
+            _native.load().gollek_hip_weight_free(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _f32_out(arr, name: str) -> np.ndarray:
+    if arr is None:
+        raise NullPointerError(name)
+    if not (isinstance(arr, np.ndarray) and arr.dtype == np.float32 and arr.flags.c_contiguous):
+        raise IllegalArgumentError(f"{name} must be a contiguous float32 array")
+    return arr
+
+
+def _f32_in(arr, name: str) -> np.ndarray:
+    if arr is None:
+        raise NullPointerError(name)
+    return np.ascontiguousarray(arr, dtype=np.float32)
+
+
+def dequantize_row(tensor: GgufTensor, row: int, dst: np.ndarray) -> None:
+    """GgufTensorOps.dequantizeRow (RT/GgufTensorOps.java:636-642)."""
+    if tensor is None:
+        raise NullPointerError("tensor")
+    dst = _f32_out(dst, "dst")
+    lib = _native.load()
+    err = _native.ErrBuf()
+    if dst.size < tensor.columns:
+        raise IllegalArgumentError(
+            f"Vector length {dst.size} is smaller than columns {tensor.columns}")
+    check(lib.gollek_hip_dequantize_rows(tensor.handle(), int(row), 1, dst.ctypes.data,
+                                         tensor.columns, err.buf, err.size), err)
+
+
+def dequantize_rows(tensor: GgufTensor, row0: int, nrows: int) -> np.ndarray:
+    """Bit-exact dequantization of a row range (for parity checks)."""
+    out = np.empty((max(nrows, 0), tensor.columns), dtype=np.float32)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_dequantize_rows(tensor.handle(), int(row0), int(nrows),
+                                         out.ctypes.data, out.size, err.buf, err.size), err)
+    return out
+
+
+def dot_row(tensor: GgufTensor, row: int, vector) -> float:
+    """GgufTensorOps.dotRow (RT/GgufTensorOps.java:644-650)."""
+    if tensor is None:
+        raise NullPointerError("tensor")
+    x = _f32_in(vector, "vector")
+    out = np.zeros(1, dtype=np.float32)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_dot_row(tensor.handle(), int(row), x.ctypes.data, x.size,
+                                 out.ctypes.data, err.buf, err.size), err)
+    return float(out[0])
+
+
+def mat_vec_rows(tensor: GgufTensor, vector, output: np.ndarray, row_count: int,
+                 parallel: bool = True) -> None:
+    """GgufTensorOps.matVecRows (RT/GgufTensorOps.java:666-674).
+
+    `parallel` is accepted for signature parity; the GPU always runs all
+    rows concurrently."""
+    if tensor is None:
+        raise NullPointerError("tensor")
+    x = _f32_in(vector, "vector")
+    y = _f32_out(output, "output")
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_matvec_rows(tensor.handle(), x.ctypes.data, x.size, y.ctypes.data,
+                                     y.size, int(row_count), err.buf, err.size), err)
+
+
+def mat_vec(tensor: GgufTensor, vector, output: np.ndarray) -> None:
+    """GgufTensorOps.matVec (RT/GgufTensorOps.java:658-660)."""
+    if tensor is None:
+        raise NullPointerError("tensor")
+    mat_vec_rows(tensor, vector, output, tensor.rows, False)
+
+
+def mat_vec_parallel(tensor: GgufTensor, vector, output: np.ndarray) -> None:
+    """GgufTensorOps.matVecParallel (RT/GgufTensorOps.java:662-664)."""
+    if tensor is None:
+        raise NullPointerError("tensor")
+    mat_vec_rows(tensor, vector, output, tensor.rows, True)
+
+
+# ---- device-pointer entry points (inputs already resident in HBM) ---------
+
+class DeviceWeight:
+    """A handle over GGUF bytes already in device memory (borrowed)."""
+
+    def __init__(self, type_id: int, device_ptr: int, rows: int, cols: int):
+        lib = _native.load()
+        err = _native.ErrBuf()
+        self.type_id, self.rows, self.cols = type_id, rows, cols
+        self.row_bytes = row_bytes_for(type_id, cols)
+        h = lib.gollek_hip_weight_wrap_device(type_id, ctypes.c_void_p(device_ptr), rows, cols,
+                                              self.row_bytes, err.buf, err.size)
+        if not h:
+            raise _BY_CODE.get(lib.gollek_hip_last_status(), GgufHipError)(err.text)
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            _native.load().gollek_hip_weight_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def matvec(self, x_ptr: int, y_ptr: int, row_count: int | None = None,
+               stream: int = 0) -> None:
+        lib = _native.load()
+        err = _native.ErrBuf()
+        rc = lib.gollek_hip_matvec_device(self.handle, ctypes.c_void_p(x_ptr),
+                                          ctypes.c_void_p(y_ptr),
+                                          self.rows if row_count is None else row_count,
+                                          ctypes.c_void_p(stream), err.buf, err.size)
+        check(rc, err)
+
+    def dequantize(self, row0: int, nrows: int, dst_ptr: int, stream: int = 0) -> None:
+        lib = _native.load()
+        err = _native.ErrBuf()
+        rc = lib.gollek_hip_dequantize_rows_device(self.handle, row0, nrows,
+                                                   ctypes.c_void_p(dst_ptr),
+                                                   ctypes.c_void_p(stream), err.buf, err.size)
+        check(rc, err)
+
+    def gemm_bf16(self, x_ptr: int, m: int, y_ptr: int, stream: int = 0) -> None:
+        lib = _native.load()
+        err = _native.ErrBuf()
+        rc = lib.gollek_hip_gemm_bf16_device(self.handle, ctypes.c_void_p(x_ptr), m,
+                                             ctypes.c_void_p(y_ptr), ctypes.c_void_p(stream),
+                                             err.buf, err.size)
+        check(rc, err)

@@ -1,0 +1,148 @@
+/*
+ * gollek_hip.h -- C ABI of the MI355X (gfx950) GGUF quantized linear-layer
+ * library, libgollek_hip.so.
+ *
+ * The library is the native side of a drop-in for gollek's Java GGUF tensor
+ * runtime (RT/ = runner/gguf/gollek-gguf-core/src/main/java/tech/kayys/gollek/
+ * gguf/runtime/).  The Java facade RT/GgufTensorOps keeps its signatures; an
+ * FFM (java.lang.foreign) binding calls these functions from inside
+ * RT/GgufMatVec.rows (RT/GgufMatVec.java:55-96) for ggml type ids 2 (Q4_0),
+ * 8 (Q8_0) and 12 (Q4_K), ahead of the prepared and raw Java routes.
+ *
+ * Conventions (those of the reference's own native bridge,
+ * runner/gguf/gguf-fast-bridge/gollek_gguf_fast.cpp:672-800):
+ *   - plain C types only: pointers, int32/int64 sizes, floats;
+ *   - functions returning int return GOLLEK_HIP_OK (0) or a negative code;
+ *     handle constructors return NULL on failure;
+ *   - a message is written to the caller's `err` buffer (NUL-terminated,
+ *     truncated to err_len) when err != NULL and err_len > 0;
+ *   - the Java adapter maps codes back to the reference's exceptions:
+ *     NULL -> NullPointerException (RT/GgufMatVec.java:32-35),
+ *     ARG -> IllegalArgumentException (RT/GgufMatVec.java:65-71, :196-200;
+ *            RT/GgufTensorOps.java:652-656; GC/core/GgmlType.java:70-81),
+ *     UNSUPPORTED -> UnsupportedOperationException (RT/GgufRowDot.java:77-82,
+ *            RT/GgufRowDequantizer.java:275),
+ *     DEVICE / NOMEM -> IllegalStateException (no reference counterpart: the
+ *            Java path has no device).
+ *
+ * Threading: every function may be called from any thread.  A weight handle
+ * serialises its host-buffer calls with its own mutex (as the reference
+ * bridge does per handle, gollek_gguf_fast.cpp:42) and runs them on its own
+ * HIP stream; they return only when the output is in host memory.  The
+ * *_device functions are asynchronous on the caller's stream and take device
+ * pointers.
+ */
+#ifndef GOLLEK_HIP_H
+#define GOLLEK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GOLLEK_HIP_OK 0
+#define GOLLEK_HIP_ERR_NULL (-1)
+#define GOLLEK_HIP_ERR_ARG (-2)
+#define GOLLEK_HIP_ERR_UNSUPPORTED (-3)
+#define GOLLEK_HIP_ERR_DEVICE (-4)
+#define GOLLEK_HIP_ERR_NOMEM (-5)
+
+/* ggml type ids accepted by this library (GC/core/GgmlType.java:11,16,21). */
+#define GOLLEK_HIP_Q4_0 2
+#define GOLLEK_HIP_Q8_0 8
+#define GOLLEK_HIP_Q4_K 12
+
+/* Opaque device-resident weight matrix. */
+typedef struct gollek_hip_weight gollek_hip_weight;
+
+/* ABI version (major * 10000 + minor * 100 + patch).  No reference
+ * counterpart; lets the Java binding refuse a mismatched library. */
+int32_t gollek_hip_version(void);
+
+/* Select and initialise a GPU.  Replaces the reference bridge's one-time
+ * backend set-up in gollek_gguf_open (gollek_gguf_fast.cpp:692-700).
+ * Calling it again with the same device is a no-op. */
+int32_t gollek_hip_init(int32_t device, char *err, size_t err_len);
+
+/* Thread-local copy of the last error message of this thread ("" if none). */
+const char *gollek_hip_last_error(void);
+
+/* Thread-local status code of this thread's last call (GOLLEK_HIP_OK after a
+ * success).  Lets a caller map a NULL handle back to the exception type. */
+int32_t gollek_hip_last_status(void);
+
+/* Tuning knobs for benchmarks and sweeps (keys: "gemv_rows_per_wave",
+ * "gemv_row_batch", "gemv_waves_per_cu", "gemm_variant").  No reference
+ * counterpart; the reference reads JVM properties instead
+ * (RT/GgufParallelConfig.java:87-101). */
+int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t err_len);
+
+/* Copy a GGUF row-major matrix (rows x cols, cols contiguous; row_bytes =
+ * cols / block_size * block_bytes) from host memory to a device handle.  The
+ * bytes are the tensor's bytes at dataStart + offset in the mmapped file
+ * (RT/GgufTensorData.java:40, GC/loader/GGUFReader.java:30-37).  Replaces the
+ * reference's prepared-matrix build at model load (RT/GgufPreparedMatrixStore
+ * .java:120-127 via PRG/JavaNativeGgufBackend.java:157-180): the layout stays
+ * the packed GGUF layout, only its residency changes.  NULL on failure. */
+gollek_hip_weight *gollek_hip_weight_upload(int32_t type_id, const void *host_bytes,
+                                            int64_t rows, int64_t cols, int64_t row_bytes,
+                                            char *err, size_t err_len);
+
+/* Wrap GGUF bytes that are already in device memory (borrowed: the caller
+ * keeps ownership and must outlive the handle).  Same validation as upload. */
+gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *device_bytes,
+                                                 int64_t rows, int64_t cols,
+                                                 int64_t row_bytes, char *err,
+                                                 size_t err_len);
+
+/* Release a handle (device memory it owns, its stream and staging buffers).
+ * Replaces clearPreparedMatrixCaches on backend close
+ * (PRG/JavaNativeGgufBackend.java:139-143).  NULL is ignored. */
+void gollek_hip_weight_free(gollek_hip_weight *weight);
+
+/* Shape of a handle; any out pointer may be NULL. */
+int32_t gollek_hip_weight_info(const gollek_hip_weight *weight, int32_t *type_id,
+                               int64_t *rows, int64_t *cols, int64_t *row_bytes);
+
+/* ---- host-buffer entry points (synchronous; the Java drop-in) ---------- */
+
+/* Dequantize rows [row0, row0 + nrows) into dst (nrows * cols floats,
+ * dst_len >= that), bit-exact with RT/GgufRowDequantizer.dequantizeRow.
+ * Replaces GgufTensorOps.dequantizeRow (RT/GgufTensorOps.java:636-642) when
+ * nrows == 1; row outside [0, rows) -> ARG (:652-656). */
+int32_t gollek_hip_dequantize_rows(gollek_hip_weight *weight, int64_t row0, int64_t nrows,
+                                   float *dst, int64_t dst_len, char *err, size_t err_len);
+
+/* out[0] = dot(row, x).  Replaces GgufTensorOps.dotRow
+ * (RT/GgufTensorOps.java:644-650): x_len >= cols (extra entries ignored),
+ * row outside [0, rows) -> ARG. */
+int32_t gollek_hip_dot_row(gollek_hip_weight *weight, int64_t row, const float *x,
+                           int64_t x_len, float *out, char *err, size_t err_len);
+
+/* y[r] = sum_k W[r, k] x[k] for r < row_count (a prefix of the rows).
+ * Replaces GgufTensorOps.matVecRows (RT/GgufTensorOps.java:666-674) and,
+ * with row_count = rows, matVec / matVecParallel (:658-664), with the
+ * checks of RT/GgufMatVec.java:63-75, :196-200: row_count outside
+ * [0, rows] -> ARG, y_len < row_count -> ARG, x_len < cols -> ARG,
+ * row_count == 0 -> no-op. */
+int32_t gollek_hip_matvec_rows(gollek_hip_weight *weight, const float *x, int64_t x_len,
+                               float *y, int64_t y_len, int64_t row_count, char *err,
+                               size_t err_len);
+
+/* ---- device-buffer entry points (asynchronous on `stream`) ------------- */
+/* `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
+ * pointers are device pointers.  Same semantics as the host versions. */
+
+int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *weight, int64_t row0,
+                                          int64_t nrows, float *dst, void *stream, char *err,
+                                          size_t err_len);
+
+int32_t gollek_hip_matvec_device(gollek_hip_weight *weight, const float *x, float *y,
+                                 int64_t row_count, void *stream, char *err, size_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GOLLEK_HIP_H */

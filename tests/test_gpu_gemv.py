@@ -1,0 +1,198 @@
+"""GPU parity of dequantization and GEMV through the C ABI (MI355X).
+
+Bar: dequantized weights bit-exact with the oracle; GEMV outputs within
+rel_err <= 1e-3 (max_i |y_i - r_i| / max(|r_i|, 1e-3 ||r||_inf)) of the fp64
+dot over the bit-exact dequantized rows, and within the same bound of the
+oracle's Java-order fp32 mat-vec.  The golden fixtures from gollek's own tests
+are checked at their own tolerances.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+from gollek_amd import synthetic as syn
+from gollek_amd import tensor_ops as ops
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+
+
+def _tensor(type_id, data, cols, name="w"):
+    rows = data.size // o.row_bytes(type_id, cols)
+    return ops.GgufTensor(name, (cols, rows), type_id, np.ascontiguousarray(data).reshape(-1))
+
+
+def _data(fx):
+    return np.frombuffer(bytes.fromhex(fx["data_hex"]), dtype=np.uint8)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    print("[gpu] init device 0", flush=True)
+    ops.init(0)
+
+
+def test_golden_fixtures_on_gpu(golden):
+    for fx in golden:
+        print(f"[gpu] golden {fx['name']}", flush=True)
+        t = _tensor(fx["type_id"], _data(fx), fx["cols"], fx["name"])
+        if fx["expected_dequant_bits"]:
+            got = ops.dequantize_rows(t, 0, fx["rows"])
+            exp = np.asarray(fx["expected_dequant_bits"], dtype=np.uint32)
+            assert np.array_equal(got.view(np.uint32), exp), fx["name"]
+        if fx["expected_matvec"] is not None:
+            vec = np.asarray(fx["vector"], dtype=np.float32)[fx["vector_offset"]:]
+            y = np.zeros(fx["row_count"], np.float32)
+            ops.mat_vec_rows(t, vec, y, fx["row_count"], True)
+            exp = np.asarray(fx["expected_matvec"], dtype=np.float64)
+            assert np.all(np.abs(y - exp) <= max(fx["tolerance"], 1e-6 * np.abs(exp).max())), \
+                (fx["name"], y, exp)
+            for r in range(fx["row_count"]):
+                assert ops.dot_row(t, r, vec) == pytest.approx(float(y[r]), rel=1e-6, abs=1e-6)
+        t.close()
+
+
+def test_f16_scale_decode_exhaustive():
+    # Every fp16 code as a Q8_0 block scale with all quants = 1: the dequantized
+    # block equals the decoded scale, so all 65536 codes are checked bitwise.
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    blocks = np.empty((65536, 34), np.uint8)
+    blocks[:, 0] = (codes & 0xFF).astype(np.uint8)
+    blocks[:, 1] = (codes >> 8).astype(np.uint8)
+    blocks[:, 2:] = 1
+    t = _tensor(syn.Q8_0, blocks.reshape(-1), 1024)
+    got = ops.dequantize_rows(t, 0, t.rows)
+    exp = o.dequantize(syn.Q8_0, blocks.reshape(-1), 1024)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+    t.close()
+
+
+@pytest.mark.parametrize("type_id", [syn.Q8_0, syn.Q4_0, syn.Q4_K])
+def test_dequant_bit_exact_random(type_id):
+    cols, rows = 4096, 257
+    data = syn.matrix(type_id, rows, cols, seed=100 + type_id).copy()
+    if type_id == syn.Q4_K:
+        specials = [0x0000, 0x8000, 0x7E00, 0x7C00, 0xFC00, 0x0001, 0x8001]
+        for r, h in enumerate(specials):
+            data[r, 2::144] = h & 0xFF
+            data[r, 3::144] = h >> 8
+        data[10:20, 4::144] = 0  # zero codes in part of the scale field
+    t = _tensor(type_id, data, cols)
+    got = ops.dequantize_rows(t, 0, rows)
+    exp = o.dequantize(type_id, data, cols)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+    # a middle range through the row0 offset
+    got2 = ops.dequantize_rows(t, 100, 17)
+    assert np.array_equal(got2.view(np.uint32), exp[100:117].view(np.uint32))
+    t.close()
+
+
+CONFIGS = [
+    ("c0_q8_0_4096x4096", syn.Q8_0, 4096, 4096),
+    ("c1_q4_0_4096x11008", syn.Q4_0, 11008, 4096),
+    ("c2a_q4_k_4096x14336", syn.Q4_K, 14336, 4096),
+    ("moe_gate_q4_k_2048x768", syn.Q4_K, 768, 2048),
+    ("moe_down_q4_k_768x2048", syn.Q4_K, 2048, 768),
+    ("q8_0_odd_blocks_160", syn.Q8_0, 7, 160),
+    ("q4_0_odd_blocks_160", syn.Q4_0, 7, 160),
+    ("q4_k_5_superblocks", syn.Q4_K, 5, 1280),
+    ("q4_k_k8192", syn.Q4_K, 333, 8192),
+    ("q4_k_k14336", syn.Q4_K, 129, 14336),
+    ("q8_0_k14336", syn.Q8_0, 65, 14336),
+]
+
+
+@pytest.mark.parametrize("name,type_id,rows,cols", CONFIGS, ids=[c[0] for c in CONFIGS])
+def test_gemv_parity(name, type_id, rows, cols):
+    print(f"[gpu] gemv {name}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=zlib.crc32(name.encode()) & 0xFFFF)
+    x = syn.activation(cols, seed=17)
+    t = _tensor(type_id, data, cols, name)
+    y = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    assert o.rel_err(y, ref) <= GEMV_TOL, (name, o.rel_err(y, ref))
+    java_order = o.matvec(type_id, data, cols, x)
+    assert o.rel_err(y, java_order) <= GEMV_TOL
+    t.close()
+
+
+def test_gemv_lm_head_full_size_sampled_rows():
+    # Q4_K K=4096 x N=128256 (lm_head): full-size GPU run; fp64 oracle on every
+    # 97th row, plus linearity in x over all rows.
+    rows, cols = 128256, 4096
+    print("[gpu] gemv lm_head 128256x4096", flush=True)
+    data = syn.q4_k_matrix(rows, cols, seed=2024)
+    t = _tensor(syn.Q4_K, data, cols, "output.weight")
+    x1, x2 = syn.activation(cols, 1), syn.activation(cols, 2)
+    y1, y2, y12 = (np.zeros(rows, np.float32) for _ in range(3))
+    ops.mat_vec(t, x1, y1)
+    ops.mat_vec(t, x2, y2)
+    ops.mat_vec(t, (x1 + x2).astype(np.float32), y12)
+    sel = np.arange(0, rows, 97)
+    ref = o.matvec_fp64(syn.Q4_K, data[sel], cols, x1)
+    assert o.rel_err(y1[sel], ref) <= GEMV_TOL
+    lin = y1.astype(np.float64) + y2
+    assert o.normwise_err(y12, lin) <= 1e-5
+    t.close()
+
+
+def test_row_count_prefix_zero_and_long_vector():
+    data = syn.q4_k_matrix(300, 4096, seed=8)
+    t = _tensor(syn.Q4_K, data, 4096)
+    x = syn.activation(4096 + 37, seed=9)  # extra entries are ignored
+    full = np.zeros(300, np.float32)
+    ops.mat_vec(t, x, full)
+    part = np.full(300, -7.0, np.float32)
+    ops.mat_vec_rows(t, x, part, 123, True)
+    assert np.array_equal(part[:123], full[:123])
+    assert np.all(part[123:] == -7.0)  # rows beyond row_count untouched
+    ops.mat_vec_rows(t, x, part, 0, True)  # no-op
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.mat_vec_rows(t, x, part, 301, True)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.mat_vec_rows(t, x[:100], part, 10, True)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.mat_vec_rows(t, x, np.zeros(5, np.float32), 10, True)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.dot_row(t, 300, x)
+    t.close()
+
+
+def test_repeated_calls_are_deterministic():
+    data = syn.q8_0_matrix(1000, 4096, seed=21)
+    t = _tensor(syn.Q8_0, data, 4096)
+    x = syn.activation(4096, seed=22)
+    a, b = np.zeros(1000, np.float32), np.zeros(1000, np.float32)
+    ops.mat_vec(t, x, a)
+    ops.mat_vec(t, x, b)
+    assert np.array_equal(a, b)
+    t.close()
+
+
+def test_device_pointer_entry_points_match_host():
+    import torch
+    rows, cols = 4096, 4096
+    for type_id in (syn.Q8_0, syn.Q4_0, syn.Q4_K):
+        data = syn.matrix(type_id, rows, cols, seed=31 + type_id)
+        x = syn.activation(cols, seed=32)
+        host_t = _tensor(type_id, data, cols)
+        yh = np.zeros(rows, np.float32)
+        ops.mat_vec(host_t, x, yh)
+        w_dev = torch.from_numpy(data.reshape(-1)).cuda()
+        x_dev = torch.from_numpy(x).cuda()
+        y_dev = torch.zeros(rows, dtype=torch.float32, device="cuda")
+        dw = ops.DeviceWeight(type_id, w_dev.data_ptr(), rows, cols)
+        stream = torch.cuda.current_stream().cuda_stream
+        dw.matvec(x_dev.data_ptr(), y_dev.data_ptr(), rows, stream)
+        deq = torch.empty((3, cols), dtype=torch.float32, device="cuda")
+        dw.dequantize(5, 3, deq.data_ptr(), stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(y_dev.cpu().numpy(), yh)
+        exp = o.dequantize(type_id, data, cols, 5, 3)
+        assert np.array_equal(deq.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+        dw.close()
+        host_t.close()

@@ -1,0 +1,156 @@
+"""CPU tests that pin the oracle before it is trusted as the GPU checker.
+
+  * every golden fixture from gollek's own tests (closed forms at 0.0, the
+    independent-reference cases at their 1e-3);
+  * fp16 decode against numpy's IEEE half decoder, all 65536 codes;
+  * 6-bit scale/min unpack against the generator's inverse packer;
+  * dequantization bit-exact against an independent numpy restatement;
+  * mat-vec against an fp64 dot over the dequantized rows;
+  * planted mistakes in a copy of the restatement are caught by the fixtures.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from gollek_amd import synthetic as syn
+from tests import npref
+
+
+def _data(fx):
+    return np.frombuffer(bytes.fromhex(fx["data_hex"]), dtype=np.uint8)
+
+
+def _vec(fx):
+    return np.asarray(fx["vector"], dtype=np.float32)[fx["vector_offset"]:]
+
+
+def test_golden_dequant_bit_exact(golden):
+    for fx in golden:
+        if not fx["expected_dequant_bits"]:
+            continue
+        got = o.dequantize(fx["type_id"], _data(fx), fx["cols"])
+        exp = np.asarray(fx["expected_dequant_bits"], dtype=np.uint32)
+        assert np.array_equal(got.view(np.uint32), exp), fx["name"]
+
+
+def test_golden_matvec(golden):
+    for fx in golden:
+        if fx["expected_matvec"] is None:
+            continue
+        y = o.matvec(fx["type_id"], _data(fx), fx["cols"], _vec(fx), fx["row_count"])
+        exp = np.asarray(fx["expected_matvec"], dtype=np.float64)
+        # JUnit assertEquals(expected, actual, delta): absolute difference.
+        assert np.all(np.abs(y - exp) <= fx["tolerance"]), (fx["name"], y, exp)
+
+
+def test_golden_single_row_dot_matches_matvec(golden):
+    # TST/GgufFx.java:26-35: single-row matVecRows equals dotRow exactly.
+    for fx in golden:
+        if fx["vector"] is None:
+            continue
+        data, cols = _data(fx), fx["cols"]
+        rb = o.row_bytes(fx["type_id"], cols)
+        one = o.matvec(fx["type_id"], data[:rb], cols, _vec(fx), 1)[0]
+        assert one == o.dot_row(fx["type_id"], data[:rb], cols, _vec(fx)), fx["name"]
+
+
+def test_f16_decode_exhaustive():
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = o.f16_to_f32(codes)
+    ref = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # The reference maps every NaN to the canonical quiet NaN.
+    assert np.all(got[nan].view(np.uint32) == 0x7FC00000)
+
+
+def test_k4_scale_min_round_trip():
+    g = np.random.default_rng(7)
+    for _ in range(200):
+        sc = g.integers(0, 64, 8)
+        mn = g.integers(0, 64, 8)
+        packed = syn.pack_q4k_scales(sc, mn)
+        for j in range(8):
+            assert o.k4_scale_min(packed, j) == (sc[j], mn[j])
+
+
+@pytest.mark.parametrize("type_id", [syn.Q8_0, syn.Q4_0, syn.Q4_K])
+def test_dequant_matches_numpy_restatement(type_id):
+    cols = 512
+    data = syn.matrix(type_id, 33, cols, seed=11 + type_id)
+    a = o.dequantize(type_id, data, cols)
+    b = npref.dequant(type_id, data, cols)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_q4k_special_scales_match_numpy_restatement():
+    # dmin in {+0, -0, NaN, inf} with random codes: both restatements agree bit
+    # for bit, including the zero-min-code and dMin == 0 branches.
+    data = syn.q4_k_matrix(8, 256, seed=5).copy()
+    specials = [0x0000, 0x8000, 0x7E00, 0x7C00, 0xFC00, 0x0001, 0x3C00, 0x8001]
+    for r, h in enumerate(specials):
+        data[r, 2], data[r, 3] = h & 0xFF, h >> 8
+    data[::2, 4:16] &= np.uint8(0x0F)  # half the rows with many zero min codes
+    a = o.dequantize(syn.Q4_K, data, 256)
+    b = npref.dequant(syn.Q4_K, data, 256)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_id,cols", [(syn.Q8_0, 4096), (syn.Q4_0, 4096), (syn.Q4_K, 4096),
+                                          (syn.Q4_K, 768), (syn.Q8_0, 160)])
+def test_matvec_against_fp64(type_id, cols):
+    rows = 37
+    data = syn.matrix(type_id, rows, cols, seed=3)
+    x = syn.activation(cols, seed=4)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    for threads in (1, 4):
+        y = o.matvec(type_id, data, cols, x, threads=threads)
+        assert o.rel_err(y, ref) <= 1e-3
+
+
+def test_parallel_equals_serial():
+    # TST/GgufParRowsTest.java:14-30: chunked rows equal the serial walk.
+    data = syn.q4_k_matrix(301, 2048, seed=9)
+    x = syn.activation(2048, seed=10)
+    a = o.matvec(syn.Q4_K, data, 2048, x, threads=1)
+    b = o.matvec(syn.Q4_K, data, 2048, x, threads=7)
+    assert np.array_equal(a, b)
+
+
+def test_row_count_prefix_and_zero():
+    data = syn.q8_0_matrix(10, 64, seed=1)
+    x = syn.activation(64, seed=2)
+    full = o.matvec(syn.Q8_0, data, 64, x)
+    assert np.array_equal(o.matvec(syn.Q8_0, data, 64, x, row_count=4), full[:4])
+    assert o.matvec(syn.Q8_0, data, 64, x, row_count=0).size == 0
+
+
+# ---- planted mistakes: the fixtures must catch each one -------------------
+
+def _mutant_dequant(kind, type_id, data, cols):
+    y = npref.dequant(type_id, data, cols).copy()
+    if kind == "q4k_swapped_nibbles" and type_id == syn.Q4_K:
+        y = y.reshape(-1, 4, 2, 32)[:, :, ::-1, :].reshape(-1, cols)
+    elif kind == "q4k_dropped_min" and type_id == syn.Q4_K:
+        d8 = np.asarray(data, np.uint8).reshape(-1, 144).copy()
+        d8[:, 2:4] = 0
+        y = npref.dequant(type_id, d8.reshape(-1), cols)
+    elif kind == "q4_0_no_offset" and type_id == syn.Q4_0:
+        y = y + np.float32(8.0)
+    elif kind == "q8_sign_flip" and type_id == syn.Q8_0:
+        y = -y
+    return y
+
+
+@pytest.mark.parametrize("kind", ["q4k_swapped_nibbles", "q4k_dropped_min", "q4_0_no_offset",
+                                  "q8_sign_flip"])
+def test_planted_mistakes_fail_the_fixtures(golden, kind):
+    caught = False
+    for fx in golden:
+        if not fx["expected_dequant_bits"]:
+            continue
+        got = _mutant_dequant(kind, fx["type_id"], _data(fx), fx["cols"])
+        exp = np.asarray(fx["expected_dequant_bits"], dtype=np.uint32)
+        if not np.array_equal(got.view(np.uint32), exp):
+            caught = True
+    assert caught, kind
