@@ -23,6 +23,7 @@ HIP_SOURCES = (
     "gguf_capi.hip",
     "gguf_dequant.hip",
     "gguf_gemv.hip",
+    "gguf_gemv_dot4.hip",
     "gguf_gemm.hip",
     "gguf_moe.hip",
 )
