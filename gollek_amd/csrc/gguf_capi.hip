@@ -380,4 +380,188 @@ int32_t gollek_hip_matvec_device(gollek_hip_weight *w, const float *x, float *y,
     return GOLLEK_HIP_OK;
 }
 
+static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, int64_t m,
+                          char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "input");
+    if (y == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "output");
+    if (w->type_id != GOLLEK_HIP_Q8_0)
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "Unsupported GGUF bf16 GEMM type id: %d (Q8_0 only)", w->type_id);
+    if (m < 0 || m > (int64_t)0x7FFFFFFF || w->rows > 0x7FFFFFFF || w->cols > 0x7FFFFFFF)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "GEMM shape %lld x %lld x %lld is out of range",
+                    (long long)m, (long long)w->rows, (long long)w->cols);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_len, int64_t m,
+                             float *y, int64_t y_len, char *err, size_t err_len) {
+    int32_t rc = check_gemm(w, x, y, m, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (x_len < m * w->cols)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Input length %lld is smaller than %lld x %lld",
+                    (long long)x_len, (long long)m, (long long)w->cols);
+    if (y_len < m * w->rows)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Output length %lld is smaller than %lld x %lld",
+                    (long long)y_len, (long long)m, (long long)w->rows);
+    if (m == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    std::lock_guard<std::mutex> lock(w->mu);
+    rc = use_device(w->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t x_bytes = align_up((size_t)(m * w->cols) * sizeof(uint16_t), 256);
+    const size_t y_bytes = (size_t)(m * w->rows) * sizeof(float);
+    rc = ensure_staging(w, x_bytes + y_bytes, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    uint16_t *d_x = reinterpret_cast<uint16_t *>(w->staging);
+    float *d_y = reinterpret_cast<float *>(w->staging + x_bytes);
+    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)(m * w->cols) * sizeof(uint16_t),
+                                  hipMemcpyHostToDevice, w->stream);
+    if (e == hipSuccess)
+        e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, d_x, d_y, (int)m, (int)w->rows,
+                                          (int)w->cols, w->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+    if (e != hipSuccess) return hip_fail(e, "gemm", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int64_t m, float *y,
+                                    void *stream, char *err, size_t err_len) {
+    const int32_t rc = check_gemm(w, x, y, m, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    hipError_t e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
+                                                 (int)w->cols, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+struct MoeShape {
+    int E, H, I;
+};
+
+static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_hip_weight *down,
+                         int64_t n_experts, int64_t tokens, int64_t top_k, MoeShape *shape,
+                         char *err, size_t err_len) {
+    if (gate == nullptr || up == nullptr || down == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "expert weights");
+    if (gate->type_id != GOLLEK_HIP_Q4_K || up->type_id != GOLLEK_HIP_Q4_K ||
+        down->type_id != GOLLEK_HIP_Q4_K)
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "Unsupported MoE expert weight types %d/%d/%d (Q4_K only)", gate->type_id,
+                    up->type_id, down->type_id);
+    if (n_experts <= 0 || gate->rows % n_experts != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Gate rows %lld are not a multiple of %lld experts",
+                    (long long)gate->rows, (long long)n_experts);
+    const int64_t H = gate->cols, I = gate->rows / n_experts;
+    if (up->rows != gate->rows || up->cols != H || down->rows != n_experts * H || down->cols != I)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Expert shapes disagree: gate %lldx%lld up %lldx%lld down %lldx%lld",
+                    (long long)gate->rows, (long long)gate->cols, (long long)up->rows,
+                    (long long)up->cols, (long long)down->rows, (long long)down->cols);
+    if (H > 4096 || I > 4096)
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "MoE hidden %lld / inter %lld above 4096 are not supported", (long long)H,
+                    (long long)I);
+    if (tokens < 0 || top_k <= 0 || tokens * top_k > (1 << 24))
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Invalid tokens %lld / top_k %lld",
+                    (long long)tokens, (long long)top_k);
+    for (gollek_hip_weight *w : {gate, up, down})
+        if ((reinterpret_cast<uintptr_t>(w->data) & 15u) != 0)
+            return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Expert weights must be 16-byte aligned");
+    shape->E = (int)n_experts;
+    shape->H = (int)H;
+    shape->I = (int)I;
+    return GOLLEK_HIP_OK;
+}
+
+int64_t gollek_hip_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t hidden,
+                                       int64_t inter, int64_t n_experts) {
+    if (tokens < 0 || top_k <= 0 || hidden <= 0 || inter <= 0 || n_experts <= 0) return -1;
+    return (int64_t)gollek::moe_layout(tokens, top_k, hidden, inter, n_experts).total;
+}
+
+int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                      gollek_hip_weight *down, int64_t n_experts, const float *x,
+                                      const int32_t *ids, const float *weights, int64_t tokens,
+                                      int64_t top_k, float *out, void *workspace,
+                                      int64_t workspace_bytes, void *stream, char *err,
+                                      size_t err_len) {
+    MoeShape sh;
+    int32_t rc = check_moe(gate, up, down, n_experts, tokens, top_k, &sh, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    if (x == nullptr || ids == nullptr || weights == nullptr || out == nullptr || workspace == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE buffers");
+    const int64_t need = gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
+    if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Workspace of %lld bytes (256-byte aligned) needed, got %lld",
+                    (long long)need, (long long)workspace_bytes);
+    hipError_t e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
+                                          down->row_bytes, sh.E, sh.H, sh.I, x, ids, weights,
+                                          (int)tokens, (int)top_k, out,
+                                          static_cast<uint8_t *>(workspace),
+                                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "moe launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
+                               gollek_hip_weight *down, int64_t n_experts, const float *x,
+                               int64_t tokens, const int32_t *ids, const float *weights,
+                               int64_t top_k, float *out, int64_t out_len, char *err,
+                               size_t err_len) {
+    MoeShape sh;
+    int32_t rc = check_moe(gate, up, down, n_experts, tokens, top_k, &sh, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (x == nullptr || ids == nullptr || weights == nullptr || out == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE buffers");
+    if (out_len < tokens * sh.H)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Output length %lld is smaller than %lld x %d",
+                    (long long)out_len, (long long)tokens, sh.H);
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    std::lock_guard<std::mutex> lock(gate->mu);
+    rc = use_device(gate->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t xb = align_up((size_t)(tokens * sh.H) * 4, 256);
+    const size_t rb = align_up((size_t)(tokens * top_k) * 4, 256);
+    const size_t ws = (size_t)gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
+    rc = ensure_staging(gate, 2 * xb + 2 * rb + ws, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    uint8_t *base = gate->staging;
+    float *d_x = reinterpret_cast<float *>(base);
+    float *d_out = reinterpret_cast<float *>(base + xb);
+    int32_t *d_ids = reinterpret_cast<int32_t *>(base + 2 * xb);
+    float *d_w = reinterpret_cast<float *>(base + 2 * xb + rb);
+    uint8_t *d_ws = base + 2 * xb + 2 * rb;
+    hipStream_t s = gate->stream;
+    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)(tokens * sh.H) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d_ids, ids, (size_t)(tokens * top_k) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d_w, weights, (size_t)(tokens * top_k) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
+                                   down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
+                                   (int)top_k, d_out, d_ws, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(out, d_out, (size_t)(tokens * sh.H) * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "moe", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
 }  // extern "C"

@@ -31,6 +31,24 @@ bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, const void *w, const fl
 hipError_t launch_gemv_q4k_dot4(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
+// Y[M, N] = X[M, K] (bf16 bits) . W[N, K]^T for Q8_0 W (gguf_gemm.hip).
+hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
+                                 int M, int N, int K, hipStream_t stream);
+
+// Workspace layout of the grouped MoE FFN (byte offsets; gguf_moe.hip).
+struct MoeLayout {
+    size_t meta, xdig, xdig_stride, h, hdig, hdig_stride, ypair, total;
+    int64_t meta_ints;
+};
+MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inter, int64_t experts);
+
+// out[T, H] = sum_j w[t,j] down_e(silu(gate_e x_t) * up_e x_t) for Q4_K stacked
+// experts; ws must hold moe_layout(...).total bytes.
+hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                          int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
+                          const float *x, const int32_t *ids, const float *wts, int T, int top_k,
+                          float *out, uint8_t *ws, hipStream_t stream);
+
 // Name of the GEMV kernel variant launch_gemv picks (for profiling notes).
 const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, const void *w,
                               const float *x);

@@ -1,0 +1,253 @@
+// gguf_moe.hip -- grouped Q4_K MoE expert FFN on gfx950.
+//
+// Semantics of runner/safetensor/gollek-safetensor-engine/src/main/java/tech/
+// kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:217-240 and
+// :461-472 (MFP below): for each token t and each of its top-k routes j,
+//   out[t] += w[t,j] * down_e(silu(gate_e x_t) * up_e x_t),   e = ids[t,j],
+// accumulated in routing order; routes with an out-of-range expert id or a
+// zero weight are skipped (MFP:222).  swigluFfn = down(silu(gate x) * up x)
+// (.../engine/forward/DirectForwardFfnService.java:40-61).  Expert weights are
+// GGUF Q4_K, stacked the way GGUF stores experts: gate/up have experts * inter
+// rows of `hidden` columns, down has experts * hidden rows of `inter` columns.
+//
+// The reference runs every (token, route) pair separately and so re-reads an
+// expert's weights once per pair.  Here the pairs are grouped by expert on the
+// device and every used expert's weights stream from HBM once:
+//   1. route: count pairs per expert, stable-sort the pair list by expert,
+//      list the used experts (one workgroup);
+//   2. digits: each token's x as integer digit planes (gguf_dot4.hpp);
+//   3. gate/up: per (used expert, row tile) the gate and up rows are loaded
+//      once and contracted against all of the expert's tokens; h = silu(g) u;
+//   4. digits of every pair's h;
+//   5. down: per (used expert, row tile), y_pair = down_e h;
+//   6. combine: out[t] = sum_j w[t,j] y_pair[t,j] in j order (plain fp32
+//      multiply then add, as MFP:461-472 accumulates).
+#include "gguf_dot4.hpp"
+#include "gguf_kernels.hpp"
+
+namespace gollek {
+
+namespace {
+
+constexpr int kMoeTokensPerPass = 8;  // vectors staged in LDS at once
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+}  // namespace
+
+// meta (int32): counts[E] | offsets[E+1] | pairs[P] | used[E] | nused
+MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inter,
+                     int64_t experts) {
+    MoeLayout L;
+    const int64_t P = tokens * top_k;
+    L.meta_ints = 2 * experts + 1 + P + experts + 1;
+    L.meta = 0;
+    L.xdig = align256(L.meta + (size_t)L.meta_ints * 4);
+    L.xdig_stride = align256(digit_lds_bytes((int)(hidden / 32)));
+    L.h = align256(L.xdig + (size_t)tokens * L.xdig_stride);
+    L.hdig = align256(L.h + (size_t)P * inter * 4);
+    L.hdig_stride = align256(digit_lds_bytes((int)(inter / 32)));
+    L.ypair = align256(L.hdig + (size_t)P * L.hdig_stride);
+    L.total = align256(L.ypair + (size_t)P * hidden * 4);
+    return L;
+}
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restrict__ ids,
+                                                        const float *__restrict__ wts, int P,
+                                                        int E, int32_t *__restrict__ meta) {
+    extern __shared__ int32_t sh[];  // counts[E], flags prefix scratch
+    int32_t *cnt = sh;
+    int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
+    int32_t *used = pairs + P, *nused = used + E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int e = ids[p];
+        if (e >= 0 && e < E && wts[p] != 0.0f) atomicAdd(&cnt[e], 1);  // LDS atomic
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0, nu = 0;
+        for (int e = 0; e < E; e++) {
+            offsets[e] = acc;
+            counts[e] = cnt[e];
+            acc += cnt[e];
+            if (cnt[e] > 0) used[nu++] = e;
+        }
+        offsets[E] = acc;
+        *nused = nu;
+    }
+    __syncthreads();
+    // Stable scatter: a pair's slot is its expert's offset plus the number of
+    // earlier valid pairs routed to the same expert.
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int e = ids[p];
+        if (!(e >= 0 && e < E && wts[p] != 0.0f)) continue;
+        int rank = 0;
+        for (int q = 0; q < p; q++) rank += (ids[q] == e && wts[q] != 0.0f) ? 1 : 0;
+        pairs[offsets[e] + rank] = p;
+    }
+}
+
+// Digit planes of `count` vectors of `len` floats, one workgroup per vector.
+__global__ __launch_bounds__(256) void moe_digits_kernel(const float *__restrict__ v, int len,
+                                                         int64_t v_stride, uint8_t *__restrict__ dig,
+                                                         int64_t dig_stride) {
+    const int ngroups = len / 32;
+    uint32_t *d = reinterpret_cast<uint32_t *>(dig + (int64_t)blockIdx.x * dig_stride);
+    float *scl = reinterpret_cast<float *>(d + kDigitWords * ngroups);
+    build_x_digits(v + (int64_t)blockIdx.x * v_stride, ngroups, d, scl, scl + ngroups);
+}
+
+// Rows [r0, r_end) of expert e (of one or two stacked matrices) against the
+// expert's vectors.  GATED: out[p][r] = silu(w0 . v) * (w1 . v), else
+// out[p][r] = w0 . v.  Vector of pair p: digits[by_pair ? p : p / top_k].
+template <int LPR, bool GATED, int RB>
+__global__ __launch_bounds__(256) void moe_expert_kernel(
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, int64_t row_bytes, int nsb,
+    int rows_per_expert, int rows_per_block, const uint8_t *__restrict__ digits,
+    int64_t digit_stride, int by_pair, int top_k, const int32_t *__restrict__ meta, int E, int P,
+    float *__restrict__ out, int64_t out_stride) {
+    extern __shared__ uint32_t smem[];
+    constexpr int RG = 64 / LPR;
+    const int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
+    const int32_t *used = pairs + P;
+    const int nused = used[E];
+    if ((int)blockIdx.y >= nused) return;  // uniform: before any barrier
+    const int e = used[blockIdx.y];
+    const int cnt = counts[e], p0 = offsets[e];
+    const int ngroups = nsb * 8;
+    const int vec_words = (int)(digit_stride / 4);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rg = lane / LPR, gl = lane & (LPR - 1), g = gl & 3, sb = gl >> 2;
+    const bool act = sb < nsb;
+    const int r_lo = blockIdx.x * rows_per_block;
+    const int r_hi = min(rows_per_expert, r_lo + rows_per_block);
+    const int rows_per_wave = (rows_per_block + 3) / 4;
+    const int wr0 = r_lo + wave * rows_per_wave;
+    const int wr1 = min(r_hi, wr0 + rows_per_wave);
+    const uint8_t *w0e = w0 + (int64_t)e * rows_per_expert * row_bytes;
+    const uint8_t *w1e = GATED ? w1 + (int64_t)e * rows_per_expert * row_bytes : nullptr;
+
+    for (int c0 = 0; c0 < cnt; c0 += kMoeTokensPerPass) {
+        const int tc = min(kMoeTokensPerPass, cnt - c0);
+        __syncthreads();
+        // Stage the digit planes of vectors c0 .. c0 + tc into LDS.
+        for (int j = 0; j < tc; j++) {
+            const int p = pairs[p0 + c0 + j];
+            const int vi = by_pair ? p : p / top_k;
+            const uint4 *src = reinterpret_cast<const uint4 *>(digits + (int64_t)vi * digit_stride);
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + j * vec_words);
+            for (int i = threadIdx.x; i < vec_words / 4; i += blockDim.x) dst[i] = src[i];
+        }
+        __syncthreads();
+        for (int r0 = wr0; r0 < wr1; r0 += RG * RB) {
+            RowChunk A[RB], B[RB];
+            load_rows<RB, RG>(A, w0e, row_bytes, r0, wr1, rg, sb, g, act);
+            if (GATED) load_rows<RB, RG>(B, w1e, row_bytes, r0, wr1, rg, sb, g, act);
+            for (int j = 0; j < tc; j++) {
+                const uint32_t *dig = smem + j * vec_words;
+                const float *scl = reinterpret_cast<const float *>(dig + kDigitWords * ngroups);
+                uint32_t dg[2][3][8];
+                float sg[2], xg[2];
+                load_lane_digits(dig, scl, scl + ngroups, sb, g, act, dg, sg, xg);
+                const int p = pairs[p0 + c0 + j];
+                float res[RB];
+#pragma unroll
+                for (int i = 0; i < RB; i++) {
+                    float a = group_sum<LPR>(q4k_dot4_row(A[i].h, A[i].a, A[i].b, dg, sg, xg, g));
+                    if (GATED) {
+                        const float b = group_sum<LPR>(q4k_dot4_row(B[i].h, B[i].a, B[i].b, dg, sg, xg, g));
+                        a = a / (1.0f + expf(-a)) * b;  // silu(gate) * up
+                    }
+                    res[i] = a;
+                }
+                if (gl == 0) {
+#pragma unroll
+                    for (int i = 0; i < RB; i++) {
+                        const int r = r0 + i * RG + rg;
+                        if (r < wr1) out[(int64_t)p * out_stride + r] = res[i];
+                    }
+                }
+            }
+        }
+    }
+}
+
+// out[t][c] = sum_j w[t,j] * y[t*k + j][c] over valid routes, j in order.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *__restrict__ ids,
+                                                          const float *__restrict__ wts,
+                                                          const float *__restrict__ ypair, int T,
+                                                          int top_k, int H, int E,
+                                                          float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * H) return;
+    const int t = (int)(i / H), c = (int)(i % H);
+    float acc = 0.0f;
+    for (int j = 0; j < top_k; j++) {
+        const int p = t * top_k + j;
+        const int e = ids[p];
+        const float wj = wts[p];
+        if (e < 0 || e >= E || wj == 0.0f) continue;
+        const float scaled = ypair[(int64_t)p * H + c] * wj;  // AccelOps.mulScalar
+        acc = acc + scaled;                                    // addToTokenRow
+    }
+    out[i] = acc;
+}
+
+namespace {
+
+template <bool GATED>
+hipError_t launch_expert(int nsb, const uint8_t *w0, const uint8_t *w1, int64_t row_bytes,
+                         int rows_per_expert, int rows_per_block, const uint8_t *digits,
+                         int64_t digit_stride, int by_pair, int top_k, const int32_t *meta, int E,
+                         int P, float *out, int64_t out_stride, hipStream_t stream) {
+    const dim3 grid((rows_per_expert + rows_per_block - 1) / rows_per_block, E);
+    const size_t lds = (size_t)kMoeTokensPerPass * digit_stride;
+#define GOLLEK_MOE_LAUNCH(L)                                                                     \
+    hipLaunchKernelGGL((moe_expert_kernel<L, GATED, 2>), grid, dim3(256), lds, stream, w0, w1,   \
+                       row_bytes, nsb, rows_per_expert, rows_per_block, digits, digit_stride,    \
+                       by_pair, top_k, meta, E, P, out, out_stride)
+    if (nsb > 8) GOLLEK_MOE_LAUNCH(64);
+    else if (nsb > 4) GOLLEK_MOE_LAUNCH(32);
+    else if (nsb > 2) GOLLEK_MOE_LAUNCH(16);
+    else if (nsb > 1) GOLLEK_MOE_LAUNCH(8);
+    else GOLLEK_MOE_LAUNCH(4);
+#undef GOLLEK_MOE_LAUNCH
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                          int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
+                          const float *x, const int32_t *ids, const float *wts, int T, int top_k,
+                          float *out, uint8_t *ws, hipStream_t stream) {
+    const MoeLayout L = moe_layout(T, top_k, H, I, E);
+    const int P = T * top_k;
+    int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), (size_t)E * sizeof(int32_t), stream,
+                       ids, wts, P, E, meta);
+    hipLaunchKernelGGL(moe_digits_kernel, dim3(T), dim3(256), 0, stream, x, H, (int64_t)H,
+                       ws + L.xdig, (int64_t)L.xdig_stride);
+    hipError_t err = launch_expert<true>(H / kQK, gate, up, gate_row_bytes, I, 64, ws + L.xdig,
+                                         (int64_t)L.xdig_stride, 0, top_k, meta, E, P,
+                                         reinterpret_cast<float *>(ws + L.h), I, stream);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(moe_digits_kernel, dim3(P), dim3(256), 0, stream,
+                       reinterpret_cast<const float *>(ws + L.h), I, (int64_t)I, ws + L.hdig,
+                       (int64_t)L.hdig_stride);
+    err = launch_expert<false>(I / kQK, down, nullptr, down_row_bytes, H, 128, ws + L.hdig,
+                               (int64_t)L.hdig_stride, 1, top_k, meta, E, P,
+                               reinterpret_cast<float *>(ws + L.ypair), H, stream);
+    if (err != hipSuccess) return err;
+    const int64_t total = (int64_t)T * H;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       stream, ids, wts, reinterpret_cast<const float *>(ws + L.ypair), T, top_k,
+                       H, E, out);
+    return hipGetLastError();
+}
+
+}  // namespace gollek

@@ -267,3 +267,61 @@ class DeviceWeight:
                                              ctypes.c_void_p(y_ptr), ctypes.c_void_p(stream),
                                              err.buf, err.size)
         check(rc, err)
+
+
+def gemm_bf16(tensor: GgufTensor, x_bf16: np.ndarray, output: np.ndarray) -> None:
+    """Y = X W^T for a Q8_0 tensor: x_bf16 (m, columns) uint16 bf16 bit patterns,
+    output (m, rows) float32.  The reference runs m matVecRows calls instead
+    (RT/GgufTensorOps.java:666-674)."""
+    if tensor is None:
+        raise NullPointerError("tensor")
+    if x_bf16 is None:
+        raise NullPointerError("input")
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    y = _f32_out(output, "output")
+    m = x.shape[0] if x.ndim == 2 else x.size // max(tensor.columns, 1)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_gemm_bf16(tensor.handle(), x.ctypes.data, x.size, int(m), y.ctypes.data,
+                                   y.size, err.buf, err.size), err)
+
+
+def moe_grouped(gate: GgufTensor, up: GgufTensor, down: GgufTensor, n_experts: int, x, ids,
+                weights) -> np.ndarray:
+    """Grouped Q4_K MoE expert FFN (the expert loop of MoeForwardPass.computeAccel,
+    runner/safetensor/gollek-safetensor-engine/src/main/java/tech/kayys/gollek/
+    safetensor/engine/generation/moe/MoeForwardPass.java:217-240): x (tokens,
+    hidden) float32, ids (tokens, top_k) int32, weights (tokens, top_k) float32
+    -> (tokens, hidden) float32."""
+    for name, t in (("gate", gate), ("up", up), ("down", down)):
+        if t is None:
+            raise NullPointerError(name)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    iv = np.ascontiguousarray(ids, dtype=np.int32)
+    wv = np.ascontiguousarray(weights, dtype=np.float32)
+    tokens, top_k = iv.shape
+    out = np.zeros((tokens, gate.columns), dtype=np.float32)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_moe_grouped(gate.handle(), up.handle(), down.handle(), n_experts,
+                                     xv.ctypes.data, tokens, iv.ctypes.data, wv.ctypes.data,
+                                     top_k, out.ctypes.data, out.size, err.buf, err.size), err)
+    return out
+
+
+def moe_workspace_bytes(tokens: int, top_k: int, hidden: int, inter: int, n_experts: int) -> int:
+    return int(_native.load().gollek_hip_moe_workspace_bytes(tokens, top_k, hidden, inter,
+                                                             n_experts))
+
+
+def moe_grouped_device(gate: DeviceWeight, up: DeviceWeight, down: DeviceWeight, n_experts: int,
+                       x_ptr: int, ids_ptr: int, w_ptr: int, tokens: int, top_k: int,
+                       out_ptr: int, ws_ptr: int, ws_bytes: int, stream: int = 0) -> None:
+    lib = _native.load()
+    err = _native.ErrBuf()
+    V = ctypes.c_void_p
+    rc = lib.gollek_hip_moe_grouped_device(gate.handle, up.handle, down.handle, n_experts,
+                                           V(x_ptr), V(ids_ptr), V(w_ptr), tokens, top_k,
+                                           V(out_ptr), V(ws_ptr), ws_bytes, V(stream), err.buf,
+                                           err.size)
+    check(rc, err)

@@ -131,6 +131,39 @@ int32_t gollek_hip_matvec_rows(gollek_hip_weight *weight, const float *x, int64_
                                float *y, int64_t y_len, int64_t row_count, char *err,
                                size_t err_len);
 
+/* Y[m, n] = sum_k X[m, k] W[n, k] (Y = X W^T, the Linear convention of
+ * runner/safetensor/gollek-safetensor-core/src/main/java/tech/kayys/gollek/
+ * safetensor/core/tensor/AccelOps.java:370-376) for a Q8_0 weight, X given
+ * as m x cols bf16 bit patterns (row-major), Y m x rows fp32.  Small-M prefill
+ * and batched decode.  The reference has no GGUF GEMM: it runs m independent
+ * RT/GgufTensorOps.matVecRows calls (RT/GgufTensorOps.java:666-674), which
+ * this replaces.  x_len < m * cols or y_len < m * rows -> ARG; a weight type
+ * other than Q8_0 -> UNSUPPORTED. */
+int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t x_len,
+                             int64_t m, float *y, int64_t y_len, char *err, size_t err_len);
+
+/* Grouped MoE expert FFN over Q4_K expert weights stacked as GGUF stores them:
+ * gate and up have n_experts * inter rows of `hidden` columns, down has
+ * n_experts * hidden rows of `inter` columns.  For each token t (x row-major
+ * tokens x hidden) and route j < top_k (ids / weights row-major tokens x
+ * top_k): out[t] += weights[t,j] * down_e(silu(gate_e x_t) * up_e x_t) with
+ * e = ids[t,j], accumulated in route order; a route whose id is outside
+ * [0, n_experts) or whose weight is 0 is skipped.  Replaces the per-(token,
+ * route) expert loop of runner/safetensor/gollek-safetensor-engine/src/main/
+ * java/tech/kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:
+ * 217-240 with :461-472 (swigluFfn: .../engine/forward/
+ * DirectForwardFfnService.java:40-61), reading each used expert once.  Weight
+ * types other than Q4_K, or hidden / inter above 4096 -> UNSUPPORTED. */
+int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
+                               gollek_hip_weight *down, int64_t n_experts, const float *x,
+                               int64_t tokens, const int32_t *ids, const float *weights,
+                               int64_t top_k, float *out, int64_t out_len, char *err,
+                               size_t err_len);
+
+/* Device workspace bytes gollek_hip_moe_grouped_device needs. */
+int64_t gollek_hip_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t hidden,
+                                       int64_t inter, int64_t n_experts);
+
 /* ---- device-buffer entry points (asynchronous on `stream`) ------------- */
 /* `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
  * pointers are device pointers.  Same semantics as the host versions. */
@@ -141,6 +174,18 @@ int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *weight, int64_t row
 
 int32_t gollek_hip_matvec_device(gollek_hip_weight *weight, const float *x, float *y,
                                  int64_t row_count, void *stream, char *err, size_t err_len);
+
+int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t m,
+                                    float *y, void *stream, char *err, size_t err_len);
+
+/* `workspace` (device, workspace_bytes >= gollek_hip_moe_workspace_bytes) is
+ * scratch owned by the caller; calls sharing one workspace must not overlap. */
+int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                      gollek_hip_weight *down, int64_t n_experts, const float *x,
+                                      const int32_t *ids, const float *weights, int64_t tokens,
+                                      int64_t top_k, float *out, void *workspace,
+                                      int64_t workspace_bytes, void *stream, char *err,
+                                      size_t err_len);
 
 #ifdef __cplusplus
 }

@@ -160,7 +160,8 @@ def gemm_reference(type_id: int, data, cols: int, x_bf16_bits) -> np.ndarray:
 
 
 def silu(v: np.ndarray) -> np.ndarray:
-    return v / (1.0 + np.exp(-v))
+    with np.errstate(over="ignore"):  # exp(-v) = inf for v << 0 gives the right limit, -0
+        return v / (1.0 + np.exp(-v))
 
 
 def moe_reference(gate_w: np.ndarray, up_w: np.ndarray, down_w: np.ndarray, x: np.ndarray,
@@ -178,6 +179,35 @@ def moe_reference(gate_w: np.ndarray, up_w: np.ndarray, down_w: np.ndarray, x: n
             e = int(ids[t, j])
             h = silu(gate_w[e] @ xt) * (up_w[e] @ xt)
             out[t] += float(weights[t, j]) * (down_w[e] @ h)
+    return out
+
+
+def moe_reference_q4k(gate: np.ndarray, up: np.ndarray, down: np.ndarray, n_experts: int,
+                      x: np.ndarray, ids: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """moe_reference over packed stacked Q4_K experts, dequantizing only the
+    experts the routes use (bit-exact dequantization, fp64 arithmetic).
+
+    gate, up: (E * I, H / 256 * 144) bytes; down: (E * H, I / 256 * 144).
+    Routes with an id outside [0, E) or a zero weight are skipped
+    (MoeForwardPass.java:222)."""
+    H = gate.shape[1] // 144 * 256
+    I = gate.shape[0] // n_experts
+    T, k = ids.shape
+    out = np.zeros((T, H), dtype=np.float64)
+    cache = {}
+    for t in range(T):
+        xt = x[t].astype(np.float64)
+        for j in range(k):
+            e, wj = int(ids[t, j]), float(weights[t, j])
+            if e < 0 or e >= n_experts or wj == 0.0:
+                continue
+            if e not in cache:
+                cache[e] = (dequantize(Q4_K, gate[e * I:(e + 1) * I], H).astype(np.float64),
+                            dequantize(Q4_K, up[e * I:(e + 1) * I], H).astype(np.float64),
+                            dequantize(Q4_K, down[e * H:(e + 1) * H], I).astype(np.float64))
+            g, u, d = cache[e]
+            h = silu(g @ xt) * (u @ xt)
+            out[t] += wj * (d @ h)
     return out
 
 

@@ -154,3 +154,31 @@ def test_planted_mistakes_fail_the_fixtures(golden, kind):
         if not np.array_equal(got.view(np.uint32), exp):
             caught = True
     assert caught, kind
+
+
+def test_moe_reference_paths_agree_and_properties():
+    # The packed-expert reference equals the dense one on the same dequantized
+    # weights; the output is linear in the route weights; route order within a
+    # token does not change the fp64 result; invalid routes contribute zero.
+    E, H, I, T, k = 4, 256, 256, 3, 2
+    gate = syn.q4_k_matrix(E * I, H, 1)
+    up = syn.q4_k_matrix(E * I, H, 2)
+    down = syn.q4_k_matrix(E * H, I, 3)
+    ids, w = syn.moe_routing(T, E, k, 4)
+    x = syn.activation(T * H, 5).reshape(T, H)
+    packed = o.moe_reference_q4k(gate, up, down, E, x, ids, w)
+    dense = o.moe_reference(o.dequantize(12, gate, H).reshape(E, I, H).astype(np.float64),
+                            o.dequantize(12, up, H).reshape(E, I, H).astype(np.float64),
+                            o.dequantize(12, down, I).reshape(E, H, I).astype(np.float64),
+                            x, ids, w)
+    assert np.allclose(packed, dense, rtol=1e-12, atol=1e-12)
+    twice = o.moe_reference_q4k(gate, up, down, E, x, ids, 2 * w)
+    assert np.allclose(twice, 2 * packed, rtol=1e-12, atol=1e-12)
+    flipped = o.moe_reference_q4k(gate, up, down, E, x, ids[:, ::-1], w[:, ::-1])
+    assert np.allclose(flipped, packed, rtol=1e-12, atol=1e-12)
+    bad = ids.copy()
+    bad[0, 0] = E  # out of range: skipped
+    wz = w.copy()
+    wz[0, 0] = 0.0
+    assert np.allclose(o.moe_reference_q4k(gate, up, down, E, x, bad, w),
+                       o.moe_reference_q4k(gate, up, down, E, x, ids, wz), rtol=1e-12, atol=1e-12)
