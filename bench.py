@@ -51,6 +51,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", default="", help="comma list of workload names to run")
+    p.add_argument("--eager", action="store_true",
+                   help="launch each step directly instead of replaying a HIP graph")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a 256 MiB device-to-device copy 10 times (known HBM bytes, "
+                        "used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -73,12 +78,31 @@ class Rotation:
             w.close()
 
 
+EAGER = False
+
+
 def graph_time(torch, launch, copies: int, steps: int, warmup: int):
     """Capture `copies` launches (one per weight copy) in a graph, replay it;
-    returns (ms per launch, launches timed)."""
+    returns (ms per launch, launches timed).  With EAGER the launches are made
+    directly on the stream instead."""
     reps = max(1, math.ceil(steps / copies))
     wreps = max(1, math.ceil(warmup / copies))
     stream = torch.cuda.Stream()
+    if EAGER:
+        with torch.cuda.stream(stream):
+            for _ in range(wreps):
+                for i in range(copies):
+                    launch(i, stream.cuda_stream)
+            stream.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(reps):
+                for i in range(copies):
+                    launch(i, stream.cuda_stream)
+            end.record(stream)
+        end.synchronize()
+        return start.elapsed_time(end) / (reps * copies), reps * copies
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         for i in range(copies):  # eager warm-up before capture
@@ -198,6 +222,35 @@ def moe_workload(torch, steps: int, warmup: int, seed: int):
     return res
 
 
+def host_entry_workload(host, rows: int, cols: int, steps: int, warmup: int):
+    """The host-buffer entry point (gollek_hip_matvec_rows): x copied in, y
+    copied back and the stream synchronized on every call, as the Java seam
+    calls it.  Weights are device-resident handles, rotated like the device
+    workloads.  PCIe- and call-overhead inclusive; reported, never `value`."""
+    import numpy as np
+
+    from gollek_amd import synthetic as syn
+    from gollek_amd import tensor_ops as ops
+    copies = max(2, math.ceil(ROTATION_BYTES / host.size))
+    tensors = [ops.GgufTensor(f"blk.{i}.ffn_up.weight", (cols, rows), syn.Q4_K, host)
+               for i in range(copies)]
+    for t in tensors:
+        t.handle()
+    x = syn.activation(cols, 3)
+    y = np.empty(rows, dtype=np.float32)
+    for i in range(max(warmup, copies)):
+        ops.mat_vec_rows(tensors[i % copies], x, y, rows)
+    n = max(steps, copies)
+    t0 = time.perf_counter()
+    for i in range(n):
+        ops.mat_vec_rows(tensors[i % copies], x, y, rows)
+    dt = (time.perf_counter() - t0) / n
+    for t in tensors:
+        t.close()
+    return {"us_per_call": dt * 1e6, "calls": n, "weight_gbs": host.size / dt / 1e9,
+            "note": "host float[] in/out per call (PCIe + sync inclusive); weights resident"}
+
+
 # ---- CPU baseline -------------------------------------------------------------
 
 def cpu_baseline(host, cols: int):
@@ -250,6 +303,19 @@ def traffic_from_profile():
 
 def main() -> int:
     args = parse()
+    global EAGER
+    EAGER = args.eager
+    if args.copy_calibration:
+        import torch
+        n = 256 * 2 ** 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n,
+                          "copies": 10}))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: this path runs on one GPU; "
                                    f"--gpus {args.gpus} is not supported (use --gpus 1)"}))
@@ -287,6 +353,10 @@ def main() -> int:
             if have_gemm and want(name):
                 log(f"extra {name}")
                 extra[name] = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
+        if want("q4_k_gemv_host_entry_4096x14336"):
+            log("extra host-buffer entry point")
+            extra["q4_k_gemv_host_entry_4096x14336"] = host_entry_workload(
+                host, 14336, 4096, args.steps, args.warmup)
         if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e128_top8_t16"):
             log("extra moe")
             extra["moe_q4_k_e128_top8_t16"] = moe_workload(torch, args.steps, args.warmup, seed=11)
