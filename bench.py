@@ -16,7 +16,7 @@ half) and the Q4_K MoE grouped FFN, each timed the same way.
 cpu_baseline: the C restatement of the reference's Java raw mat-vec (oracle/)
 on this host's cores, on the same Q4_K matrix (rank 0, N = 1 only).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--warm-seconds S] [--no-extra] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -46,8 +46,11 @@ def log(msg: str) -> None:
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=400)
-    p.add_argument("--warmup", type=int, default=40)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--warm-seconds", type=float, default=1.0,
+                   help="untimed GPU work before the first workload, so every timed run "
+                        "sees the device at its steady-state clocks")
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", default="", help="comma list of workload names to run")
@@ -79,6 +82,20 @@ class Rotation:
 
 
 EAGER = False
+
+
+def warm_device(torch, seconds: float) -> float:
+    """Untimed fp32 matmuls for about `seconds`: the first timed launches of a
+    cold process otherwise run below the device's steady-state clocks."""
+    if seconds <= 0:
+        return 0.0
+    a = torch.randn(4096, 4096, device="cuda")
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            a = torch.mm(a, a).clamp_(-1.0, 1.0)
+        torch.cuda.synchronize()
+    return time.perf_counter() - t0
 
 
 def graph_time(torch, launch, copies: int, steps: int, warmup: int):
@@ -332,6 +349,8 @@ def main() -> int:
     def want(name):
         return not only or name in only
 
+    warmed = warm_device(torch, args.warm_seconds)
+    log(f"device warm-up {warmed:.2f} s")
     log("headline: Q4_K GEMV K=4096 N=14336")
     head, host = gemv_workload(torch, syn.Q4_K, 14336, 4096, args.steps, args.warmup, seed=2)
     log(f"headline {head['weight_gbs']:.1f} GB/s, {head['ms_per_step'] * 1e3:.2f} us/launch")
@@ -376,6 +395,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": head["steps"],
         "warmup": args.warmup,
+        "device_warmup_s": round(warmed, 2),
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",

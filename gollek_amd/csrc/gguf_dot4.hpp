@@ -119,6 +119,138 @@ __device__ __forceinline__ void load_rows(RowChunk (&d)[RB], const uint8_t *__re
 }
 
 
+// ---- streaming support: buffer descriptors, buffer->LDS row loads --------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+__device__ __forceinline__ uint4 to_uint4(u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+// A 64-bit value the compiler should treat as wave-uniform (it feeds buffer
+// descriptors, which live in scalar registers).
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Buffer descriptor over `bytes` bytes at `base` (wave-uniform).  Raw buffer
+// loads at offsets at or past `bytes` return zeros without touching memory,
+// which is how rows past a wave's range and lanes past a row's end are
+// masked without branches (branches would make the load counters
+// path-dependent and force a wait for every load before the first use).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wave_buffer(const uint8_t *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, (int)bytes,
+                                             0x00020000);
+}
+
+// Offset that is out of range for every descriptor of fewer than 2^31 bytes.
+constexpr uint32_t kMaskedOffset = 0x80000000u;
+
+// Cache policy of streamed weight loads: nontemporal (read once per launch,
+// so they do not displace x, the digit planes and the outputs).
+constexpr int kStreamLoad = 2;
+
+// Copies `row_bytes` bytes at offset `off` of the buffer into the LDS slot
+// (NDMA loads of 1 KB: lane l moves bytes 16 l .. 16 l + 15 of each KB; lanes
+// past the row read zeros and write them into the slot's padding).  A masked
+// row (off == kMaskedOffset) issues the same loads, all out of range, so the
+// number of loads in flight is the same on every path.
+template <int NDMA>
+__device__ __forceinline__ void row_to_lds(__amdgpu_buffer_rsrc_t rs, uint8_t *slot, uint32_t off,
+                                           uint32_t row_bytes, int lane) {
+#pragma unroll
+    for (int k = 0; k < NDMA; k++) {
+        const uint32_t in_row = 1024u * k + 16u * lane;
+        const uint32_t o = in_row < row_bytes ? off + in_row : kMaskedOffset;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(slot + 1024 * k), 16, o, 0, 0,
+                                                 kStreamLoad);
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                              0xF, 0xF, false));
+}
+
+// Sum over the whole wave with DPP (no LDS round trips); valid in lane 63.
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x124>(v);  // row_ror:4
+    v += dpp_f<0x128>(v);  // row_ror:8 -> every lane holds its 16-lane row's sum
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142,
+                                                               0xA, 0xF, false));  // row_bcast:15
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143,
+                                                               0xC, 0xF, false));  // row_bcast:31
+    return v;
+}
+
+// Max / sum over aligned groups of eight lanes (quad xor 1, xor 2, then the
+// half-row mirror, which pairs lanes 0-3 with 7-4 of each eight).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0x141>(v);
+}
+
+// x digit planes built by eight threads per group, four elements each, in two
+// steps so the x loads can be issued before a kernel's weight loads and the
+// conversion can run while the weights stream in.  NT = threads of the
+// workgroup, XL = float4 loads per thread (8 * ngroups <= XL * NT).
+template <int XL>
+struct XPart {
+    float4 v[XL];
+};
+
+template <int NT, int XL>
+__device__ __forceinline__ void load_x_parts(XPart<XL> &p, const float *__restrict__ x, int ngroups) {
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+        // Unconditional load of a clamped index (a branch here would make the
+        // compiler wait for the x loads before the weight loads are issued).
+        // Threads past the last group hold a copy of its last element; their
+        // group index is >= ngroups, so store_x_digits never stores them.
+        const int t = threadIdx.x + i * NT;
+        p.v[i] = reinterpret_cast<const float4 *>(x)[t < 8 * ngroups ? t : 8 * ngroups - 1];
+    }
+}
+
+// Every lane of the wave must execute this (the DPP reductions span eight lanes).
+template <int NT, int XL>
+__device__ __forceinline__ void store_x_digits(const XPart<XL> &p, int ngroups, uint32_t *dig,
+                                               float *scl, float *gsum) {
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+        const int t = threadIdx.x + i * NT;
+        const int G = t >> 3, part = t & 7;
+        const float v[4] = {p.v[i].x, p.v[i].y, p.v[i].z, p.v[i].w};
+        const float mx = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        const float s = sum8((v[0] + v[1]) + (v[2] + v[3]));
+        int e = 0;
+        (void)frexpf(mx, &e);  // mx < 2^e, so |x / 2^(e-23)| < 2^23
+        const bool finite = mx <= 3.402823466e38f;
+        int X[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) X[k] = finite ? (int)ldexpf(v[k], 23 - e) : 0;
+        if (G < ngroups) {
+            uint32_t *out = dig + kDigitWords * G + part;
+#pragma unroll
+            for (int byte = 0; byte < 3; byte++) out[8 * byte] = pack_byte(X, byte);
+            if (part == 0) {
+                scl[G] = finite ? ldexpf(1.0f, e - 23) : __builtin_nanf("");
+                gsum[G] = s;
+            }
+        }
+    }
+}
+
 // Per group: 24 digit dwords in LDS, then (after all groups) the scales and
 // the group sums.  Bytes of LDS for `ngroups` groups.
 __host__ __device__ constexpr size_t digit_lds_bytes(int ngroups) {

@@ -27,7 +27,8 @@ hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t
                        const float *x, float *y, int64_t rows, hipStream_t stream);
 
 // Q4_K GEMV with integer dot products (gguf_gemv_dot4.hip).
-bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, const void *w, const float *x);
+bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
+                        const float *x);
 hipError_t launch_gemv_q4k_dot4(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
