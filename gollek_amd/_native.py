@@ -7,6 +7,7 @@ library has not been built; there is no fallback implementation.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -65,11 +66,12 @@ def load() -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
-        if not LIB_PATH.exists():
+        path = Path(os.environ.get("GOLLEK_HIP_LIBRARY", str(LIB_PATH)))
+        if not path.exists():
             raise RuntimeError(
-                f"{LIB_PATH} is not built; build it with "
+                f"{path} is not built; build it with "
                 "`python -c 'import __graft_entry__ as g; g.build()'`")
-        lib = ctypes.CDLL(str(LIB_PATH))
+        lib = ctypes.CDLL(str(path))
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(lib, name, None)
             if fn is None:

@@ -14,12 +14,16 @@
 // fp32 result before accumulation -- the reference's own block structure.
 // Rounding q * d to bf16 instead would cost ~1e-3 relative error per weight.
 //
-// Tiling: a workgroup of 4 waves owns a BM x BN tile of Y; the waves split it
-// WM x WN and, when WK > 1, also split each K stage (the partial tiles are
-// summed through LDS at the end).  Each stage moves KB = 64 * WK columns of X
-// (bf16) and W (Q8_0 block pairs, 68 aligned bytes, realigned and widened to
-// bf16 once per workgroup) into double-buffered LDS; one barrier per stage.
+// Two kernels.  M >= 256: gemm_q8_0_bf16_big_kernel (128 x 64 workgroup
+// tiles, register-pipelined global loads, described below).  Smaller M:
+// gemm_q8_0_bf16_kernel, where a workgroup of 4 waves owns a BM x BN tile of
+// Y; the waves split it WM x WN and, when WK > 1, also split each K stage
+// (the partial tiles are summed through LDS at the end).  Each stage moves
+// KB = 64 * WK columns of X (bf16) and W (Q8_0 block pairs, 68 aligned bytes,
+// realigned and widened to bf16 once per workgroup) into double-buffered LDS;
+// one barrier per stage.
 #include "gguf_blocks.hpp"
+#include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"
 
 namespace gollek {
@@ -233,6 +237,206 @@ __global__ __launch_bounds__(256) void gemm_q8_0_bf16_kernel(const uint8_t *__re
             }
 }
 
+// ---- large-M kernel -----------------------------------------------------------
+//
+// Workgroup tile 128 (M) x 64 (N), four waves of 64 x 32 (2 x 2), K in stages
+// of one Q8_0 block pair (64 columns).  Operands are staged in LDS as bf16
+// (X as stored, W converted once per workgroup: each int8 quant becomes an
+// exact bf16, each fp16 block scale an fp32), in 128-byte rows whose 16-byte
+// chunks are XOR-swizzled by row so the MFMA fragment reads are free of bank
+// conflicts.  Global loads run kPipe stages ahead in registers (raw buffer
+// loads: rows past M read zeros); one barrier per stage with two LDS buffers.
+// Per Q8_0 block every 16 x 16 output tile takes one v_mfma_f32_16x16x32_bf16
+// with a zero accumulator and the fp32 scale is applied with four FMAs.
+// Workgroups map to tiles so that each XCD's workgroups share M tiles: X,
+// re-read by every N tile, then comes from that XCD's L2.
+
+namespace {
+
+constexpr int kBigBM = 128, kBigBN = 64;
+
+// Byte offset of bf16 chunk kc (8 elements) of row r in a tile of 128-byte
+// rows whose 16-byte chunks are XOR-swizzled by row pair, so the 16-byte
+// fragment reads of 16 consecutive rows fall in distinct banks.
+constexpr int kRowStride = 128;
+__device__ __forceinline__ uint32_t swz(int r, int kc) {
+    return (uint32_t)(r * kRowStride + 16 * (kc ^ ((r >> 1) & 7)));
+}
+
+template <int XCH>
+struct BigRegs {
+    u32x4 x[XCH];  // 16-byte chunks of X
+    u32x4 q;       // W quant dwords
+    uint32_t q5;   // fifth quant dword (even block) or the scale dword (odd block)
+};
+
+struct BigStage {
+    uint8_t x[kBigBM * kRowStride];
+    uint8_t w[kBigBN * kRowStride];
+    float d[kBigBN][4];  // [.][b] block scales; [.][2 + b] unused (see stash)
+};
+
+}  // namespace
+
+template <int kPipe, int WAVES_M, int WAVES_N>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_q8_0_bf16_big_kernel(
+    const uint8_t *__restrict__ W, int64_t row_bytes, const uint16_t *__restrict__ X,
+    float *__restrict__ Y, int M, int N, int K) {
+    constexpr int NTH = 64 * WAVES_M * WAVES_N;
+    constexpr int WM = kBigBM / WAVES_M, WN = kBigBN / WAVES_N;
+    constexpr int MT = WM / 16, NT = WN / 16;
+    constexpr int XCH = kBigBM * 8 / NTH;   // X chunks per thread per stage
+    constexpr int WIT = kBigBN * 4;          // W (row, block, half) items per stage
+    static_assert(XCH * NTH == kBigBM * 8 && WIT <= NTH && NTH % WIT == 0, "staging split");
+    __shared__ __attribute__((aligned(16))) BigStage st[2];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int n_tiles = N / kBigBN;
+    // Tiles in M-major order t = m * n_tiles + n.  Workgroups are dealt to the
+    // eight XCDs round robin (blockIdx % 8), so when the grid divides by 8,
+    // XCD j takes the contiguous tiles [j G/8, (j+1) G/8): its workgroups share
+    // one or two M tiles and the X rows they read stay in that XCD's L2.
+    const int G = (int)gridDim.x;
+    const int t = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int mt_idx = t / n_tiles, nt_idx = t % n_tiles;
+    const int m0 = mt_idx * kBigBM, n0 = nt_idx * kBigBN;
+    const int nst = K / 64;
+
+    // X rows m0.. (zeros past M), W rows n0.. (N % 64 == 0 by dispatch).
+    const __amdgpu_buffer_rsrc_t xs = wave_buffer(
+        reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2,
+        (uint32_t)((int64_t)(M - m0 < kBigBM ? M - m0 : kBigBM) * K * 2));
+    const __amdgpu_buffer_rsrc_t ws =
+        wave_buffer(W + (int64_t)n0 * row_bytes, (uint32_t)(kBigBN * row_bytes));
+
+    // Staging roles.  X: chunks c = tid + NTH i (row c / 8, chunk c % 8).
+    // W: item tid % WIT: row, block (0/1) and 16-quant half of the pair; with
+    // more threads than items the spares repeat an item (same loads, same
+    // values to the same LDS bytes), which keeps the code free of branches.
+    const int wit = tid % WIT;
+    const int wr = wit >> 2, wb = (wit >> 1) & 1, wu = wit & 1;
+    const uint32_t w_q = (uint32_t)(wr * row_bytes) + (wb ? 36u + 16u * wu : 16u * wu);
+    const uint32_t w_5 = (uint32_t)(wr * row_bytes) + (wb ? 32u : 16u * wu + 16u);
+
+    // Loads of stage s; stages past the end read zeros (masked offsets), so
+    // every pipeline step issues the same loads and the load counters stay
+    // exact (a conditional load would make the compiler wait for all of them).
+    auto load = [&](BigRegs<XCH> &R, int s) {
+        const bool live = s < nst;
+        const uint32_t k0b = (uint32_t)s * 128u;  // bf16 bytes
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            const int c = tid + NTH * i;
+            const uint32_t o = (uint32_t)((c >> 3) * K * 2) + k0b + 16u * (c & 7);
+            R.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xs, live ? o : kMaskedOffset, 0, 0);
+        }
+        const uint32_t pb = (uint32_t)s * 68u;
+        R.q = __builtin_amdgcn_raw_buffer_load_b128(ws, live ? w_q + pb : kMaskedOffset, 0, 0);
+        R.q5 = __builtin_amdgcn_raw_buffer_load_b32(ws, live ? w_5 + pb : kMaskedOffset, 0, 0);
+    };
+    auto stash = [&](const BigRegs<XCH> &R, BigStage &S) {
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            const int c = tid + NTH * i;
+            *reinterpret_cast<u32x4 *>(S.x + swz(c >> 3, c & 7)) = R.x[i];
+        }
+        // Even blocks: the quants start 2 bytes into the first dword.
+        const int sh = wb ? 0 : 2;
+        uint32_t qd[4];
+        qd[0] = __builtin_amdgcn_alignbyte(R.q.y, R.q.x, sh);
+        qd[1] = __builtin_amdgcn_alignbyte(R.q.z, R.q.y, sh);
+        qd[2] = __builtin_amdgcn_alignbyte(R.q.w, R.q.z, sh);
+        qd[3] = __builtin_amdgcn_alignbyte(R.q5, R.q.w, sh);
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) i8x4_to_bf16(qd[j], o[2 * j], o[2 * j + 1]);
+        const int kc = 4 * wb + 2 * wu;
+        *reinterpret_cast<u32x4 *>(S.w + swz(wr, kc)) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4 *>(S.w + swz(wr, kc + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+        // Only the first half of an even block holds its scale; the second half
+        // stores into a slot nobody reads (d[.][2 + b]) instead of branching.
+        S.d[wr][wb + 2 * wu] = half_bits_to_float_fast(wb ? (R.q5 >> 16) : R.q.x);
+    };
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++) acc[a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Pipeline: registers hold stages s + 1 .. s + kPipe; LDS buffer s & 1
+    // holds stage s.  In stage s a wave issues its MFMAs, then converts and
+    // writes stage s + 1 into the other buffer while they run, applies the
+    // scales, and meets the others at the one barrier of the stage.
+    // The host guarantees nst % kPipe == 0 and nst >= kPipe, so the steady
+    // state below has no branches around loads.
+    BigRegs<XCH> R[kPipe];
+#pragma unroll
+    for (int j = 0; j < kPipe; j++) load(R[j], j);
+    stash(R[0], st[0]);
+    load(R[0], kPipe);
+    __syncthreads();
+
+    const int lr = lane & 15, lk = lane >> 4;
+    for (int s0 = 0; s0 < nst; s0 += kPipe) {
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) {
+            const int s = s0 + j;
+            const BigStage &S = st[s & 1];
+            f32x4 part[2][MT][NT];
+            float dsc[2][NT];
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+                bf16x8 A[MT], B[NT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    A[mt] = *reinterpret_cast<const bf16x8 *>(S.x + swz(wm * WM + mt * 16 + lr, 4 * kb + lk));
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    B[nt] = *reinterpret_cast<const bf16x8 *>(S.w + swz(wn * WN + nt * 16 + lr, 4 * kb + lk));
+                    dsc[kb][nt] = S.d[wn * WN + nt * 16 + lr][kb];
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+                        part[kb][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            A[mt], B[nt], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            }
+            // Stage s + 1 sits in R[(j + 1) % kPipe]: write it to the other
+            // buffer while the MFMAs run (past the last stage this writes
+            // zeros nobody reads), then refill the slot with s + 1 + kPipe.
+            BigRegs<XCH> &Rn = R[(j + 1) % kPipe];
+            stash(Rn, st[(s + 1) & 1]);
+            load(Rn, s + 1 + kPipe);
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            acc[mt][nt][v] = fmaf(dsc[kb][nt], part[kb][mt][nt][v], acc[mt][nt][v]);
+            __syncthreads();
+        }
+    }
+
+    // D layout of a 16x16 tile: lane holds column lane & 15, rows 4 (lane >> 4) + v.
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * WM + mt * 16 + 4 * lk + v;
+                const int n = n0 + wn * WN + nt * 16 + lr;
+                if (m < M) Y[(int64_t)m * N + n] = acc[mt][nt][v];
+            }
+}
+
 // Any shape: one thread per output, fp32, exact per-block scaling.
 __global__ __launch_bounds__(256) void gemm_q8_0_generic_kernel(const uint8_t *__restrict__ W,
                                                                 int64_t row_bytes,
@@ -275,6 +479,26 @@ hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (row_bytes & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     const int v = tuning().gemm_variant;
+    // Large M: 128 x 64 tiles, register-pipelined (v == 2 forces it where the shape allows).
+    if (aligned && v != 1 && N % kBigBN == 0 && K % 64 == 0 && (M >= 256 || v == 2) &&
+        (int64_t)kBigBN * row_bytes < ((int64_t)1 << 31)) {
+        const unsigned grid = (unsigned)(((M + kBigBM - 1) / kBigBM) * (N / kBigBN));
+        const int nst = K / 64;
+        const int cfg = tuning().gemm_big_config;
+#define GOLLEK_BIG(P, WMW, WNW)                                                                \
+    hipLaunchKernelGGL((gemm_q8_0_bf16_big_kernel<P, WMW, WNW>), dim3(grid),                \
+                       dim3(64 * (WMW) * (WNW)), 0, stream, w, row_bytes, x, y, M, N, K)
+        // Measured on MI355X (4096 x 4096, M = 256 .. 1024): the eight-wave
+        // 2-deep pipeline (112 VGPRs, two workgroups per CU when the grid
+        // has them) matches the deeper ones at M = 512 and wins at M = 1024.
+        if (nst % 4 == 0 && cfg == 1) GOLLEK_BIG(4, 4, 2);
+        else if (nst % 8 == 0 && cfg == 2) GOLLEK_BIG(8, 4, 2);
+        else if (nst % 4 == 0 && cfg == 4) GOLLEK_BIG(4, 2, 2);
+        else if (nst % 2 == 0) GOLLEK_BIG(2, 4, 2);
+        else GOLLEK_BIG(1, 4, 2);
+#undef GOLLEK_BIG
+        return hipGetLastError();
+    }
     if (aligned && v != 1) {
         if (M <= 16 && N % 16 == 0 && K % 256 == 0)
             return launch_tiled<16, 16, 16, 16, 4>(w, row_bytes, x, y, M, N, K, stream);

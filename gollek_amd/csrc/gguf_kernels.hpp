@@ -15,6 +15,7 @@ struct LaunchTuning {
     int gemv_row_batch = 0;      // rows per load batch (1, 2, 4, 8)
     int gemv_waves_per_cu = 8;   // target resident waves per CU
     int gemm_variant = 0;
+    int gemm_big_config = 0;     // large-M GEMM waves / pipeline depth (sweeps)
     int gemv_variant = 0;        // 1 forces the fp32 GEMV kernels
 };
 LaunchTuning &tuning();

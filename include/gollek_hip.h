@@ -74,7 +74,8 @@ const char *gollek_hip_last_error(void);
 int32_t gollek_hip_last_status(void);
 
 /* Tuning knobs for benchmarks and sweeps (keys: "gemv_rows_per_wave",
- * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant").  No reference
+ * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
+ * "gemm_big_config").  No reference
  * counterpart; the reference reads JVM properties instead
  * (RT/GgufParallelConfig.java:87-101). */
 int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t err_len);

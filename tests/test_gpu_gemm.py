@@ -28,7 +28,7 @@ def q8_4096():
     t.close()
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 17, 100, 128, 129, 512])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 100, 128, 129, 256, 512, 1024])
 def test_gemm_parity_4096(q8_4096, m):
     data, t = q8_4096
     print(f"[gpu] gemm m={m}", flush=True)
@@ -60,6 +60,25 @@ def test_gemm_odd_shapes(rows, cols, m):
     x = syn.activation_bf16(m, cols, seed=1)
     y = np.zeros((m, rows), np.float32)
     ops.gemm_bf16(t, x, y)
+    assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
+    t.close()
+
+
+@pytest.mark.parametrize("rows,cols,m,variant", [(128, 256, 300, 0), (64, 128, 5, 2), (192, 4096, 257, 0),
+                                                  (64, 64, 128, 2), (4096, 192, 384, 0)])
+def test_gemm_large_m_kernel_shapes(rows, cols, m, variant):
+    # The 128 x 64 tiled kernel: partial last M tile (rows past M read zeros),
+    # several N tiles, K down to one block pair; variant 2 forces it below M = 256.
+    print(f"[gpu] gemm large-m rows={rows} cols={cols} m={m} variant={variant}", flush=True)
+    data = syn.q8_0_matrix(rows, cols, seed=rows * 7 + cols)
+    t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=m + 3)
+    y = np.full((m, rows), np.nan, np.float32)
+    ops.set_option("gemm_variant", variant)
+    try:
+        ops.gemm_bf16(t, x, y)
+    finally:
+        ops.set_option("gemm_variant", 0)
     assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
     t.close()
 
