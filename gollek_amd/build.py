@@ -24,6 +24,7 @@ HIP_SOURCES = (
     "gguf_dequant.hip",
     "gguf_gemv.hip",
     "gguf_gemv_dot4.hip",
+    "gguf_gemv_mfma.hip",
     "gguf_gemm.hip",
     "gguf_moe.hip",
 )

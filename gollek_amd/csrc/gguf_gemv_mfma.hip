@@ -1,0 +1,741 @@
+// gguf_gemv_mfma.hip -- Q4_K GEMV (decode, M = 1) on the gfx950 matrix cores.
+//
+// Same value as the reference raw Q4_K mat-vec (RT/GgufQ4RawDot.java:603-674,
+// RT/GgufKQuantLayout.java:67-69; RT/ = runner/gguf/gollek-gguf-core/src/main/
+// java/tech/kayys/gollek/gguf/runtime/):
+//   y[n] = sum_sb sum_j [ (d sc_j) (sum_{i in j} q_i x_i) - (m_j ? dmin m_j : 0) X_j ]
+// over the eight 32-element sub-blocks j of every superblock, X_j = sum of x
+// over sub-block j.  Tolerance parity (rel_err <= 1e-3).
+//
+// x.  Per superblock s (256 elements): a power-of-two scale xs = 2^(e-22)
+// with max |x| < 2^e, the integers X_i = trunc(x_i / xs) (|X_i| < 2^22, so the
+// per-element error is below 2^-21 of the superblock's max |x|) as balanced
+// signed bytes X = 65536 a + 256 b + c (c, b in [-128, 127], |a| <= 64), and
+// the sub-block sums xs * sum X_i.  Built once per workgroup in LDS.
+//
+// Matrix cores.  v_mfma_i32_16x16x64_i8 with B = 16 weight rows' nibbles
+// (0..15, one 64-column chunk: lane n + 16 g holds 16 nibbles of row n from
+// run g, i.e. chunk columns 16 g .. 16 g + 15, low nibbles for g < 2, high
+// for g >= 2) and A row m = 4 h + p = plane p of the x digits of sub-block
+// 2 c + h, zero on the other sub-block's columns.  D[4 h + p][n] is then the
+// plane-p sum over one sub-block of row n, sitting in lane n + 16 h, and
+// 65536 D2 + 256 D1 + D0 = sum q_i X_i exactly in int32 (|.| < 32 * 15 * 2^22
+// < 2^31).  A rows 3, 7 and 8..15 are zero.  Per 1024 weights a wave spends
+// one MFMA and ~20 VALU instructions (nibble masks, the plane combine, the
+// per-sub-block scale), about a third of the v_dot4 formulation's cost, so
+// the kernel is bound by HBM rather than by the VALU.
+//
+// A records.  Per (superblock, chunk) 208 bytes: for run g = 0..3 and plane
+// p = 0..2 the 16 digit bytes of chunk columns 16 g .. 16 g + 15, then 16
+// zero bytes.  Lane (m, g) reads record + (3 g + p) * 16 when its A row is
+// live for run g (m < 8, p = m % 4 < 3, h = m / 4 = g / 2) and the zero bytes
+// otherwise, so no lane selects or masks.
+//
+// Streaming.  A workgroup (one per CU) owns an equal share of the rows, cut
+// into 16-row tiles; a tile's columns are split into ks K-parts when there
+// are fewer tiles than waves.  (tile, K-part) items go round-robin to the
+// eight waves.  Each wave streams its items through a ring of NSLOT LDS
+// stages of 16 rows x 2 superblocks (rows at a 304-byte pitch, so the 16
+// rows' 16-byte reads fall on distinct banks), filled by buffer->LDS loads of
+// whole kilobytes whose row and column masks are folded into the offsets.
+// K-part sums meet in LDS and are added in K order.
+#include <type_traits>
+
+#include "gguf_dot4.hpp"
+#include "gguf_kernels.hpp"
+
+namespace gollek {
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfWaves = 8;                       // waves per workgroup
+constexpr int kMfThreads = kMfWaves * 64;
+constexpr int kTileRows = 16;                     // weight rows per MFMA tile
+constexpr int kSps = 2;                           // superblocks per ring stage
+constexpr int kStageCols = kSps * kQKBlockBytes;  // 288 bytes of a row per stage
+constexpr int kRowPitch = kStageCols + 16;        // LDS pitch of a staged row
+constexpr int kStageDma = (kTileRows * kRowPitch + 1023) / 1024;  // 1 KB loads per stage
+constexpr int kSlotBytes = kStageDma * 1024;
+constexpr int kRecBytes = 208;                    // A record of one 64-column chunk
+constexpr int kRecZero = 192;                     // offset of its zero bytes
+constexpr int kSbRecBytes = 4 * kRecBytes;        // A records of one superblock
+constexpr int kMaxParts = 1024;                   // K-part row sums per workgroup
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+// Maximum over the wave (unsigned), returned in every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0xB1>((int)v));   // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)dpp_i<0x4E>((int)v));   // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)dpp_i<0x124>((int)v));  // row_ror:4
+    v = max(v, (uint32_t)dpp_i<0x128>((int)v));  // row_ror:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Sum over aligned groups of eight lanes.
+__device__ __forceinline__ int sum8_i(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    return v + dpp_i<0x141>(v);  // row_half_mirror
+}
+
+// A records, sub-block sums (xsum[8 sb + 4 h + c] for sub-block 2 c + h) and
+// scales of superblocks [0, nsb_pad); superblocks past nsb are zero.  Thread
+// t of the workgroup converted float4 t + i * kMfThreads of x, so wave w holds
+// superblock w + 8 i in lane order.  Every lane of every wave must call this.
+template <int XL>
+__device__ __forceinline__ void store_x_records(const XPart<XL> &xp, int nsb, int nsb_pad,
+                                                uint8_t *xa, float *xsum, float *xsc) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+        const int sb = (int)(threadIdx.x >> 6) + i * kMfWaves;  // wave-uniform
+        const bool live = sb < nsb;
+        const float v[4] = {live ? xp.v[i].x : 0.0f, live ? xp.v[i].y : 0.0f,
+                            live ? xp.v[i].z : 0.0f, live ? xp.v[i].w : 0.0f};
+        uint32_t mb = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
+        mb = wave_max_u32(mb);  // NaN and inf order above every finite |x|
+        const bool finite = mb < 0x7F800000u;
+        int e = 0;
+        (void)frexpf(__uint_as_float(mb), &e);  // max |x| < 2^e
+        uint32_t w0 = 0, w1 = 0, w2 = 0;
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int X = finite ? (int)ldexpf(v[k], 22 - e) : 0;
+            const int c = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - c) >> 8;
+            const int b = (int)(int8_t)(X1 & 0xFF);
+            const int a = (X1 - b) >> 8;
+            w0 |= ((uint32_t)c & 0xFFu) << (8 * k);
+            w1 |= ((uint32_t)b & 0xFFu) << (8 * k);
+            w2 |= ((uint32_t)a & 0xFFu) << (8 * k);
+            s += X;
+        }
+        s = sum8_i(s);
+        const float scale = !live ? 0.0f : finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
+        if (sb < nsb_pad) {
+            // lane l: chunk l / 16, run (l / 4) % 4, bytes 4 (l % 4) .. + 3 of the run
+            uint8_t *rec = xa + sb * kSbRecBytes + (lane >> 4) * kRecBytes;
+            // Inline asm: the compiler drops the alias scope of some of these
+            // stores and would then wait for the ring's buffer->LDS loads
+            // before them.  The caller waits for LDS before its barrier.
+            const uint32_t pw = (uint32_t)(uintptr_t)(lds_ptr)(rec + 48 * ((lane >> 2) & 3) + 4 * (lane & 3));
+            asm volatile(
+                "ds_write_b32 %0, %1\n\t"
+                "ds_write_b32 %0, %2 offset:16\n\t"
+                "ds_write_b32 %0, %3 offset:32"
+                :
+                : "v"(pw), "v"(w0), "v"(w1), "v"(w2)
+                : "memory");
+            if ((lane & 15) == 0) *reinterpret_cast<uint4 *>(rec + kRecZero) = make_uint4(0u, 0u, 0u, 0u);
+            if ((lane & 7) == 0) {
+                const int j = lane >> 3;  // sub-block
+                xsum[sb * 8 + (j & 1) * 4 + (j >> 1)] = (float)s * scale;
+            }
+            if (lane == 0) xsc[sb] = scale;
+        }
+    }
+}
+
+// Reads one ring stage: the two superblock headers of row n and this lane's
+// 16 quant bytes of each of the 2 x 4 chunks.  Inline asm because the
+// compiler cannot tell which buffer->LDS load wrote which bytes and would
+// wait for all of them; the stage is complete once the VM loads issued after
+// it are the only ones outstanding, and the LDS reads finish before the slot
+// is refilled.
+template <int OFF, int VM>
+__device__ __forceinline__ void read_stage(uint32_t a_hdr, uint32_t a_qs, u32x4 (&hd)[2],
+                                           u32x4 (&q)[2][4]) {
+    asm volatile(
+        "s_waitcnt vmcnt(%12)\n\t"
+        "ds_read_b128 %0, %10 offset:%13\n\t"
+        "ds_read_b128 %1, %10 offset:%14\n\t"
+        "ds_read_b128 %2, %11 offset:%13\n\t"
+        "ds_read_b128 %3, %11 offset:%15\n\t"
+        "ds_read_b128 %4, %11 offset:%16\n\t"
+        "ds_read_b128 %5, %11 offset:%17\n\t"
+        "ds_read_b128 %6, %11 offset:%14\n\t"
+        "ds_read_b128 %7, %11 offset:%18\n\t"
+        "ds_read_b128 %8, %11 offset:%19\n\t"
+        "ds_read_b128 %9, %11 offset:%20\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(hd[0]), "=&v"(hd[1]), "=&v"(q[0][0]), "=&v"(q[0][1]), "=&v"(q[0][2]),
+          "=&v"(q[0][3]), "=&v"(q[1][0]), "=&v"(q[1][1]), "=&v"(q[1][2]), "=&v"(q[1][3])
+        : "v"(a_hdr), "v"(a_qs), "n"(VM), "n"(OFF), "n"(OFF + kQKBlockBytes), "n"(OFF + 32),
+          "n"(OFF + 64), "n"(OFF + 96), "n"(OFF + kQKBlockBytes + 32),
+          "n"(OFF + kQKBlockBytes + 64), "n"(OFF + kQKBlockBytes + 96)
+        : "memory");
+}
+
+// Position of a wave's stage in its item sequence (wave-uniform counters).
+struct StagePos {
+    int j = 0;   // item ordinal of the wave (item = wave + 8 j)
+    int st = 0;  // stage within the item
+    __device__ __forceinline__ void advance(int L) {
+        if (++st == L) {
+            st = 0;
+            ++j;
+        }
+    }
+};
+
+}  // namespace
+
+// NSLOT ring stages per wave; MAXSB = superblocks per row the LDS tables hold.
+template <int NSLOT, int MAXSB>
+__global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
+    const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
+    float *__restrict__ y, int64_t rows, int64_t rows_per_wg, int ks) {
+    constexpr int XL = (64 * MAXSB + kMfThreads - 1) / kMfThreads;
+    // x tables and row sums in one LDS array, the ring in another (the ring's
+    // buffer->LDS loads then provably touch none of the tables).
+    constexpr int kXsumOff = MAXSB * kSbRecBytes;
+    constexpr int kXscOff = kXsumOff + MAXSB * 8 * 4;
+    constexpr int kPartsOff = kXscOff + MAXSB * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t tabs[kPartsOff + kMaxParts * 4];
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kMfWaves * NSLOT * kSlotBytes];
+    uint8_t *xa = tabs;
+    float *xsum = reinterpret_cast<float *>(tabs + kXsumOff);
+    float *xsc = reinterpret_cast<float *>(tabs + kXscOff);
+    float *parts = reinterpret_cast<float *>(tabs + kPartsOff);
+
+    const uint32_t row_bytes = (uint32_t)row_bytes64;
+    const int lane = threadIdx.x & 63;
+    const int wib = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // >= 1
+    const int tiles = (nr + kTileRows - 1) / kTileRows;
+    const int nst = (nsb + kSps - 1) / kSps;
+    const int L = nst / ks;  // stages per item (the host picks ks | nst)
+    const int items = tiles * ks;
+    const int my_items = wib < items ? (items - wib + kMfWaves - 1) / kMfWaves : 0;
+    const int total = my_items * L;
+    // The host keeps rows_per_wg * row_bytes < 2^31; rows past the workgroup's
+    // share are out of the descriptor's range and read as zeros.
+    const __amdgpu_buffer_rsrc_t rs = wave_buffer(w + r0 * row_bytes64, (uint32_t)nr * row_bytes);
+    uint8_t *myring = ring + wib * (NSLOT * kSlotBytes);
+
+    // Lane l of load k moves staged byte b = 1024 k + 16 l: row b / pitch,
+    // column b % pitch (columns past the stage are padding).
+    uint32_t dbase[kStageDma];
+    uint32_t dcol[kStageDma];
+#pragma unroll
+    for (int k = 0; k < kStageDma; k++) {
+        const uint32_t b = 1024u * k + 16u * lane;
+        const uint32_t r = b / kRowPitch, col = b - r * kRowPitch;
+        const bool ok = r < (uint32_t)kTileRows && col < (uint32_t)kStageCols;
+        dbase[k] = ok ? r * row_bytes + col : kMaskedOffset;
+        dcol[k] = ok ? col : 0x40000000u;
+    }
+    auto issue = [&](uint8_t *slot, const StagePos &p) {
+        uint32_t uoff = 0, lim = 0;  // lim = 0 masks every lane
+        if (p.j < my_items) {
+            const int item = wib + p.j * kMfWaves;
+            const int tile = item / ks, kp = item - tile * ks;
+            const int sg = kp * L + p.st;
+            uoff = (uint32_t)tile * kTileRows * row_bytes + (uint32_t)sg * kStageCols;
+            const int left = nsb - sg * kSps;
+            lim = (uint32_t)(left < kSps ? left : kSps) * kQKBlockBytes;
+        }
+        uoff = __builtin_amdgcn_readfirstlane(uoff);
+        lim = __builtin_amdgcn_readfirstlane(lim);
+#pragma unroll
+        for (int k = 0; k < kStageDma; k++) {
+            const uint32_t o = dcol[k] < lim ? dbase[k] + uoff : kMaskedOffset;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(slot + 1024 * k), 16, o, 0, 0,
+                                                     kStreamLoad);
+        }
+    };
+
+    XPart<XL> xp;
+    load_x_parts<kMfThreads, XL>(xp, x, nsb * 8);
+    __builtin_amdgcn_sched_barrier(0);  // every x load ahead of the ring loads
+    StagePos pf;
+#pragma unroll
+    for (int j = 0; j < NSLOT; j++) {
+        issue(myring + j * kSlotBytes, pf);
+        pf.advance(L);
+    }
+    store_x_records<XL>(xp, nsb, nst * kSps, xa, xsum, xsc);
+    // LDS-only exchange: no wait on the ring loads still in flight.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+
+    const int n = lane & 15, g = lane >> 4, h = g & 1;
+    const int a_off = (n < 8 && (n & 3) < 3 && (n >> 2) == (g >> 1)) ? (3 * g + (n & 3)) * 16 : kRecZero;
+    const int sh = 4 * (g >> 1);
+    const uint32_t a_hdr = (uint32_t)(uintptr_t)(lds_ptr)myring + n * kRowPitch;
+    const uint32_t a_qs = a_hdr + 16 + 16 * (g & 1);
+    const i32x4 zero = {0, 0, 0, 0};
+
+    StagePos cp;
+    float acc = 0.0f;
+    // One ring stage at slot J (a compile-time slot, so its LDS offsets are
+    // instruction immediates).
+    auto stage = [&](int q, auto slot_tag) {
+        constexpr int J = decltype(slot_tag)::value;
+        u32x4 hd[2], qv[2][4];
+        read_stage<J * kSlotBytes, kStageDma * (NSLOT - 1)>(a_hdr, a_qs, hd, qv);
+        issue(myring + J * kSlotBytes, pf);
+        pf.advance(L);
+        if (q >= total) return;
+        const int item = wib + cp.j * kMfWaves;
+        const int tile = item / ks, kp = item - tile * ks;
+        const int sg = kp * L + cp.st;
+#pragma unroll
+        for (int s2 = 0; s2 < kSps; s2++) {
+            const int sb = sg * kSps + s2;
+            const uint8_t *rec = xa + sb * kSbRecBytes + a_off;
+            i32x4 A[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) A[c] = *reinterpret_cast<const i32x4 *>(rec + c * kRecBytes);
+            const float4 xs4 = *reinterpret_cast<const float4 *>(xsum + sb * 8 + 4 * h);
+            const float xs = xsc[sb];
+            const u32x4 hv = hd[s2];
+            const float d = half_bits_to_float_fast(hv.x);
+            const float dmin = half_bits_to_float_fast(hv.x >> 16);
+            // 6-bit codes of sub-blocks 0-3 and 4-7 (RT/GgufKQuantLayout.java:37-49),
+            // shifted so bytes 0 and 2 are this lane's sub-blocks 2 c + h.
+            const uint32_t sc03 = (hv.y & 0x3F3F3F3Fu) >> (8 * h);
+            const uint32_t mn03 = (hv.z & 0x3F3F3F3Fu) >> (8 * h);
+            const uint32_t sc47 = ((hv.w & 0x0F0F0F0Fu) | ((hv.y >> 2) & 0x30303030u)) >> (8 * h);
+            const uint32_t mn47 =
+                (((hv.w >> 4) & 0x0F0F0F0Fu) | ((hv.z >> 2) & 0x30303030u)) >> (8 * h);
+            const float scf[4] = {(float)(sc03 & 0xFFu), (float)((sc03 >> 16) & 0xFFu),
+                                  (float)(sc47 & 0xFFu), (float)((sc47 >> 16) & 0xFFu)};
+            const float mnf[4] = {(float)(mn03 & 0xFFu), (float)((mn03 >> 16) & 0xFFu),
+                                  (float)(mn47 & 0xFFu), (float)((mn47 >> 16) & 0xFFu)};
+            float acc_sb = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const u32x4 wq = qv[s2][c];
+                const i32x4 B = {(int)((wq.x >> sh) & 0x0F0F0F0Fu), (int)((wq.y >> sh) & 0x0F0F0F0Fu),
+                                 (int)((wq.z >> sh) & 0x0F0F0F0Fu), (int)((wq.w >> sh) & 0x0F0F0F0Fu)};
+                const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[c], B, zero, 0, 0, 0);
+                const int S = (int)((uint32_t)D[0] + ((uint32_t)D[1] << 8) + ((uint32_t)D[2] << 16));
+                acc_sb = fmaf(d * scf[c], (float)S, acc_sb);
+            }
+            // min term: zero codes contribute nothing even for a NaN or
+            // infinite dmin (minContribution, RT/GgufKQuantLayout.java:67-69)
+            const float xsv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+            float mm = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xsv[c], mm);
+            acc = fmaf(xs, acc_sb, acc) - mm;
+        }
+        if (cp.st == L - 1) {
+            // lanes n and n + 16 hold sub-blocks 2 c and 2 c + 1 of row n
+            const float other = __shfl_down(acc, 16, 64);
+            const int row = tile * kTileRows + n;
+            if (lane < 16 && row < nr) parts[kp * nr + row] = acc + other;
+            acc = 0.0f;
+        }
+        cp.advance(L);
+    };
+    for (int q0 = 0; q0 < total; q0 += NSLOT) {
+        stage(q0, std::integral_constant<int, 0>{});
+        stage(q0 + 1, std::integral_constant<int, 1>{});
+        if constexpr (NSLOT > 2) stage(q0 + 2, std::integral_constant<int, 2>{});
+    }
+    // Drain the (masked) ring loads before the workgroup's LDS is released.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int r = threadIdx.x; r < nr; r += kMfThreads) {
+        float s = parts[r];
+        for (int kp = 1; kp < ks; kp++) s += parts[kp * nr + r];
+        y[r0 + r] = s;
+    }
+}
+
+// ---- K <= 4096: whole 16-row tiles shared by the workgroup -------------
+//
+// A 16-row tile of a matrix with at most 16 superblocks per row is one
+// contiguous block of 16 * row_bytes bytes.  The workgroup (16 waves) streams
+// tiles into a shared ring of NSLOT slots (rows at a 2320-byte pitch, so the
+// 16 rows' reads of one superblock fall on distinct banks); every wave issues
+// an equal share of a tile's 1 KB loads and one barrier per tile publishes
+// it.  Wave w owns superblock w of every tile: its A operands are built once,
+// in registers, and per tile it reads the 16 rows' header and quant bytes of
+// that superblock (B lane n + 16 g: bytes 8 g .. 8 g + 7 of each chunk, low
+// nibbles then high nibbles, so A row 4 h + p is zero on the other half).
+// Per-wave row sums meet in LDS and one wave per tile adds them in superblock
+// order.
+namespace {
+
+constexpr int kT2Waves = 16;
+constexpr int kT2Threads = kT2Waves * 64;
+constexpr int kT2Cols = 16 * kQKBlockBytes;                   // 2304
+constexpr int kT2Pitch = kT2Cols + 16;                          // 2320
+constexpr int kT2Stage = kTileRows * kT2Pitch;                  // 37120
+constexpr int kT2Dma = (kT2Stage + 1023) / 1024;                // 37 loads per tile
+constexpr int kT2DmaPerWave = (kT2Dma + kT2Waves - 1) / kT2Waves;  // 3
+constexpr int kT2Slot = kT2Dma * 1024;
+constexpr int kT2MaxRows = 1024;                                // rows per workgroup
+constexpr int kT2K = 16 * kQK;                                  // x elements held
+
+// LDS stores into the ring array outside the ring loads' slots, through
+// inline asm so the compiler does not wait for every buffer->LDS load first.
+__device__ __forceinline__ void lds_store_f32(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+
+
+__device__ __forceinline__ void lds_store4(uint32_t addr, int a, int b, int c) {
+    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(i32x4{a, b, c, 0}) : "memory");
+}
+
+// Plane stores of the x digits through inline asm (see store_x_records).
+__device__ __forceinline__ void lds_store3(uint32_t addr, uint32_t w0, uint32_t w1, uint32_t w2) {
+    asm volatile(
+        "ds_write_b32 %0, %1\n\t"
+        "ds_write_b32 %0, %2 offset:4096\n\t"
+        "ds_write_b32 %0, %3 offset:8192"
+        :
+        : "v"(addr), "v"(w0), "v"(w1), "v"(w2)
+        : "memory");
+}
+
+}  // namespace
+
+template <int NSLOT>
+__global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
+    const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
+    float *__restrict__ y, int64_t rows, int64_t rows_per_wg) {
+    static_assert(kT2DmaPerWave * kT2Waves >= kT2Dma, "tile loads");
+    static_assert(3 * kT2K + 16 * 8 * 4 + 16 * 4 + 16 * 8 * 16 <= kT2Slot, "x tables fit a slot");
+    __shared__ __attribute__((aligned(16))) uint8_t ring[NSLOT * kT2Slot + 1024];  // + sink
+    __shared__ float part[2][kT2Waves][32];  // [tile & 1][wave][lane]
+    __shared__ float yout[kT2MaxRows];
+    // The x tables (digit planes, sub-block sums [superblock][sub-block],
+    // superblock scales) live in the last ring slot, which the loop first
+    // refills after every wave has read them.  They are accessed with inline
+    // asm like the ring itself.
+    const uint32_t xdig = (uint32_t)(uintptr_t)(lds_ptr)(ring + (NSLOT - 1) * kT2Slot);
+    const uint32_t xsum = xdig + 3 * kT2K;
+    const uint32_t xsc = xsum + 16 * 8 * 4;
+    const uint32_t xps = xsc + 16 * 4;  // [superblock][sub-block] 4 ints
+
+    const uint32_t row_bytes = (uint32_t)row_bytes64;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kT2MaxRows
+    const int tiles = (nr + kTileRows - 1) / kTileRows;
+    // Rows past the workgroup's share are out of the descriptor's range.
+    const __amdgpu_buffer_rsrc_t rs = wave_buffer(w + r0 * row_bytes64, (uint32_t)nr * row_bytes);
+
+    // This wave's tile loads: load k = wv + 16 i moves staged bytes 1024 k + 16 lane
+    // (row b / pitch, column b % pitch); loads past the tile write the sink.
+    uint32_t dbase[kT2DmaPerWave];
+#pragma unroll
+    for (int i = 0; i < kT2DmaPerWave; i++) {
+        const uint32_t k = (uint32_t)(wv + kT2Waves * i);
+        const uint32_t b = 1024u * k + 16u * lane;
+        const uint32_t r = b / kT2Pitch, col = b - r * kT2Pitch;
+        dbase[i] = (k < (uint32_t)kT2Dma && col < row_bytes) ? r * row_bytes + col : kMaskedOffset;
+    }
+    auto issue = [&](int slot, int tile) {
+        const uint32_t uoff = tile < tiles ? (uint32_t)tile * kTileRows * row_bytes : kMaskedOffset;
+#pragma unroll
+        for (int i = 0; i < kT2DmaPerWave; i++) {
+            const int k = wv + kT2Waves * i;
+            uint8_t *dst = k < kT2Dma ? ring + slot * kT2Slot + 1024 * k : ring + NSLOT * kT2Slot;
+            const uint32_t o = (dbase[i] != kMaskedOffset && uoff != kMaskedOffset) ? dbase[i] + uoff : kMaskedOffset;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, o, 0, 0, kStreamLoad);
+        }
+    };
+
+    // x: thread t converts elements 4 t .. 4 t + 3, so wave s holds superblock s.
+    // Load order: x, then tile 0; the later tiles only once x has arrived.  A
+    // tile is usable when all of it has arrived, and the memory system serves
+    // requests issued together interleaved, so this head start makes tile 0
+    // complete well before tile 1 instead of together with it.
+    XPart<1> xp;
+    load_x_parts<kT2Threads, 1>(xp, x, nsb * 8);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(0, 0);
+    {
+        // Wave s turns superblock s of x into digits; only this wave reads
+        // them back (so no workgroup barrier here).
+        const int sb = wv;
+        const bool live = sb < nsb;
+        const float v[4] = {live ? xp.v[0].x : 0.0f, live ? xp.v[0].y : 0.0f, live ? xp.v[0].z : 0.0f,
+                            live ? xp.v[0].w : 0.0f};
+        uint32_t mb = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
+        mb = wave_max_u32(mb);
+        const bool finite = mb < 0x7F800000u;
+        int e = 0;
+        (void)frexpf(__uint_as_float(mb), &e);
+        uint32_t w0 = 0, w1 = 0, w2 = 0;
+        int sx = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int X = finite ? (int)ldexpf(v[k], 22 - e) : 0;
+            const int c = (int)(int8_t)(X & 0xFF);
+            const int X1 = (X - c) >> 8;
+            const int b = (int)(int8_t)(X1 & 0xFF);
+            const int a = (X1 - b) >> 8;
+            w0 |= ((uint32_t)c & 0xFFu) << (8 * k);
+            w1 |= ((uint32_t)b & 0xFFu) << (8 * k);
+            w2 |= ((uint32_t)a & 0xFFu) << (8 * k);
+            sx += X;
+        }
+        sx = sum8_i(sx);
+        // 128 x (sum of each digit plane over the sub-block): the MFMA's C
+        // input for the high-nibble half (see the B operand below)
+        int ps0 = 0, ps1 = 0, ps2 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            ps0 += (int)(int8_t)(w0 >> (8 * k));
+            ps1 += (int)(int8_t)(w1 >> (8 * k));
+            ps2 += (int)(int8_t)(w2 >> (8 * k));
+        }
+        ps0 = sum8_i(ps0);
+        ps1 = sum8_i(ps1);
+        ps2 = sum8_i(ps2);
+        const float scale = !live ? 0.0f : finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
+        lds_store3(xdig + sb * kQK + 4 * lane, w0, w1, w2);
+        if ((lane & 7) == 0) {
+            lds_store_f32(xsum + 4 * (sb * 8 + (lane >> 3)), (float)sx * scale);
+            lds_store4(xps + 16 * (sb * 8 + (lane >> 3)), 128 * ps0, 128 * ps1, 128 * ps2);
+        }
+        if (lane == 0) lds_store_f32(xsc + 4 * sb, scale);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // A operands of this wave's superblock (row m = 4 h + p of lane m + 16 g).
+    const int sb = wv;
+    const bool active = sb < nsb;  // wave-uniform
+    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = m >> 2;
+    // Output lane n + 16 h holds sub-blocks 2 c + h of row n.
+    const int n = lane & 15, h = (lane >> 4) & 1;
+    // Digits of elements 64 c + 8 g .. + 7 (sub-block 2 c) and + 32 (2 c + 1),
+    // the sub-block sums of sub-blocks 2 c + h and the scale, in one batch.
+    uint2 dl[4], dh[4];
+    float xs4[4], xs;
+    i32x4 cc[4];  // 128 x plane sums of sub-blocks 2 c + 1
+    asm volatile(
+        "ds_read_b128 %0, %4 offset:16\n\t"
+        "ds_read_b128 %1, %4 offset:48\n\t"
+        "ds_read_b128 %2, %4 offset:80\n\t"
+        "ds_read_b128 %3, %4 offset:112\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(cc[0]), "=&v"(cc[1]), "=&v"(cc[2]), "=&v"(cc[3])
+        : "v"(xps + 128 * (active ? sb : 0))
+        : "memory");
+    asm volatile(
+        "ds_read_b64 %0, %13\n\t"
+        "ds_read_b64 %1, %13 offset:64\n\t"
+        "ds_read_b64 %2, %13 offset:128\n\t"
+        "ds_read_b64 %3, %13 offset:192\n\t"
+        "ds_read_b64 %4, %13 offset:32\n\t"
+        "ds_read_b64 %5, %13 offset:96\n\t"
+        "ds_read_b64 %6, %13 offset:160\n\t"
+        "ds_read_b64 %7, %13 offset:224\n\t"
+        "ds_read_b32 %8, %14\n\t"
+        "ds_read_b32 %9, %14 offset:8\n\t"
+        "ds_read_b32 %10, %14 offset:16\n\t"
+        "ds_read_b32 %11, %14 offset:24\n\t"
+        "ds_read_b32 %12, %15\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
+          "=&v"(dh[2]), "=&v"(dh[3]), "=&v"(xs4[0]), "=&v"(xs4[1]), "=&v"(xs4[2]), "=&v"(xs4[3]),
+          "=&v"(xs)
+        : "v"(xdig + p * kT2K + (active ? sb : 0) * kQK + 8 * g),
+          "v"(xsum + 4 * ((active ? sb : 0) * 8 + h)), "v"(xsc + 4 * (active ? sb : 0))
+        : "memory");
+#pragma unroll
+    for (int j = 1; j < NSLOT - 1; j++) issue(j, j);
+    const bool alive = active && p < 3;
+    i32x4 A[4], C[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        A[c] = i32x4{alive && ha == 0 ? (int)dl[c].x : 0, alive && ha == 0 ? (int)dl[c].y : 0,
+                     alive && ha == 1 ? (int)dh[c].x : 0, alive && ha == 1 ? (int)dh[c].y : 0};
+        const bool hl = lane >= 16 && lane < 32;  // output lanes of the high-nibble half
+        C[c] = i32x4{hl ? cc[c].x : 0, hl ? cc[c].y : 0, hl ? cc[c].z : 0, 0};
+    }
+    // Plane combine of output lane n + 16 h: D_p / 16^h weighted by 256^p.
+    const int sh0 = 4 * h, sh1 = 8 - 4 * h, sh2 = 16 - 4 * h;
+
+    const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
+    const uint32_t a_h0 = ring_base + n * kT2Pitch + sb * kQKBlockBytes;
+    const uint32_t a_q0 = a_h0 + 16 + 8 * g;
+    int slot = 0;
+    for (int t = 0; t < tiles; t++) {
+        // This wave's loads of tile t are done once the later tiles' loads are
+        // the only ones outstanding; the barrier makes every wave's visible and
+        // ends every wave's reads of the slot refilled below.
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kT2DmaPerWave * (NSLOT - 2)) : "memory");
+        if (t >= 1 && wv == (t - 1) % kT2Waves && lane < 16) {
+            const float(*pp)[32] = part[(t - 1) & 1];
+            float s = 0.0f;
+            for (int k = 0; k < nsb; k++) s += pp[k][lane] + pp[k][lane + 16];
+            const int row = (t - 1) * kTileRows + lane;
+            if (row < nr) yout[row] = s;
+        }
+        issue(slot == 0 ? NSLOT - 1 : slot - 1, t + NSLOT - 1);
+        if (active) {
+            u32x4 hv;
+            uint2 q[4];
+            const uint32_t off = (uint32_t)slot * kT2Slot;
+            asm volatile(
+                "ds_read_b128 %0, %5\n\t"
+                "ds_read_b64 %1, %6\n\t"
+                "ds_read_b64 %2, %6 offset:32\n\t"
+                "ds_read_b64 %3, %6 offset:64\n\t"
+                "ds_read_b64 %4, %6 offset:96\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(hv), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+                : "v"(a_h0 + off), "v"(a_q0 + off)
+                : "memory");
+            // B: low nibbles q as they are; high nibbles in place as the signed
+            // byte 16 (q - 8) (one v_bitop3 each), whose -128 sum(digits) the
+            // C input cancels, so the high half's D is 16 sum q digit.
+            int S[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const i32x4 B = {(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
+                                 (int)((q[c].x ^ 0x80808080u) & 0xF0F0F0F0u),
+                                 (int)((q[c].y ^ 0x80808080u) & 0xF0F0F0F0u)};
+                const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[c], B, C[c], 0, 0, 0);
+                S[c] = (D[0] >> sh0) + (int)(((uint32_t)D[1] << sh1) + ((uint32_t)D[2] << sh2));
+            }
+            const float d = half_bits_to_float_fast(hv.x);
+            const float dmin = half_bits_to_float_fast(hv.x >> 16);
+            // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h
+            // (bytes 0 and 2 of sc03 / mn03) and 4 + h, 6 + h (of sc47 / mn47)
+            const uint32_t hy = hv.y >> (8 * h), hz = hv.z >> (8 * h), hw = hv.w >> (8 * h);
+            const uint32_t sc03 = hy & 0x003F003Fu;
+            const uint32_t mn03 = hz & 0x003F003Fu;
+            const uint32_t sc47 = (hw & 0x000F000Fu) | ((hy >> 2) & 0x00300030u);
+            const uint32_t mn47 = ((hw >> 4) & 0x000F000Fu) | ((hz >> 2) & 0x00300030u);
+            const float scf[4] = {(float)(sc03 & 0xFFu), (float)((sc03 >> 16) & 0xFFu),
+                                  (float)(sc47 & 0xFFu), (float)((sc47 >> 16) & 0xFFu)};
+            const float mnf[4] = {(float)(mn03 & 0xFFu), (float)((mn03 >> 16) & 0xFFu),
+                                  (float)(mn47 & 0xFFu), (float)((mn47 >> 16) & 0xFFu)};
+            float v;
+            if (__builtin_isfinite(d) && __builtin_isfinite(dmin)) {
+                float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    qs = fmaf(scf[c], (float)S[c], qs);
+                    mm = fmaf(mnf[c], xs4[c], mm);
+                }
+                v = fmaf(d * xs, qs, -(dmin * mm));
+            } else {
+                // The reference's products: (d sc) per sub-block, and zero min
+                // codes skipped even for a NaN or infinite dmin
+                // (minContribution, RT/GgufKQuantLayout.java:67-69).
+                float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    qs = fmaf(d * scf[c], xs * (float)S[c], qs);
+                    mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4[c], mm);
+                }
+                v = qs - mm;
+            }
+            if (lane < 32) part[t & 1][wv][lane] = v;
+        }
+        slot = slot == NSLOT - 1 ? 0 : slot + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (tiles >= 1 && wv == (tiles - 1) % kT2Waves && lane < 16) {
+        const float(*pp)[32] = part[(tiles - 1) & 1];
+        float s = 0.0f;
+        for (int k = 0; k < nsb; k++) s += pp[k][lane] + pp[k][lane + 16];
+        const int row = (tiles - 1) * kTileRows + lane;
+        if (row < nr) yout[row] = s;
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < nr; r += kT2Threads) y[r0 + r] = yout[r];
+}
+
+namespace {
+
+struct MfmaPlan {
+    int64_t grid = 0, rows_per_wg = 0;
+    int ks = 1;
+};
+
+MfmaPlan plan_mfma(int64_t rows, int nsb) {
+    MfmaPlan p;
+    const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+    int64_t grid = (rows + kTileRows - 1) / kTileRows;  // at least a tile per workgroup
+    if (grid > cus) grid = cus;
+    int64_t per = (rows + grid - 1) / grid;
+    if (per > kMaxParts) per = kMaxParts;
+    grid = (rows + per - 1) / per;
+    per = (rows + grid - 1) / grid;
+    grid = (rows + per - 1) / per;  // every workgroup gets at least one row
+    const int tiles = (int)((per + kTileRows - 1) / kTileRows);
+    const int nst = (nsb + kSps - 1) / kSps;
+    // K-parts: the divisor of the stage count that minimises the busiest
+    // wave's stages (ties to fewer parts), within the LDS row-sum buffer.
+    int best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int k = 1; k <= nst; k++) {
+        if (nst % k != 0 || (int64_t)k * per > kMaxParts) continue;
+        const int64_t cost = (((int64_t)tiles * k + kMfWaves - 1) / kMfWaves) * (nst / k);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = k;
+        }
+    }
+    p.grid = grid;
+    p.rows_per_wg = per;
+    p.ks = best;
+    return p;
+}
+
+}  // namespace
+
+bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
+                        const float *x) {
+    (void)rows;  // a workgroup's descriptor spans <= kMaxParts rows of <= 64 superblocks
+    if (tuning().gemv_variant == 1 || tuning().gemv_variant == 2) return false;
+    const int64_t nsb = cols / kQK;
+    return nsb >= 1 && nsb <= 64 && row_bytes == nsb * kQKBlockBytes &&
+           (reinterpret_cast<uintptr_t>(w) & 15u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
+                                const float *x, float *y, int64_t rows, hipStream_t stream) {
+    const int nsb = (int)(cols / kQK);
+    if (nsb <= 16) {
+        // one workgroup per CU, at most kT2MaxRows rows each, at least one tile each
+        const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+        int64_t grid = (rows + kTileRows - 1) / kTileRows;
+        if (grid > cus) grid = cus;
+        int64_t per = (rows + grid - 1) / grid;
+        if (per > kT2MaxRows) per = kT2MaxRows;
+        grid = (rows + per - 1) / per;
+        per = (rows + grid - 1) / grid;
+        grid = (rows + per - 1) / per;
+        hipLaunchKernelGGL((gemv_q4_k_mfma_tile_kernel<3>), dim3((unsigned)grid), dim3(kT2Threads), 0,
+                           stream, w, row_bytes, nsb, x, y, rows, per);
+        return hipGetLastError();
+    }
+    const MfmaPlan p = plan_mfma(rows, nsb);
+    if (nsb <= 16)
+        hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<3, 16>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
+                           stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
+    else
+        hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
+                           stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
+    return hipGetLastError();
+}
+
+}  // namespace gollek

@@ -16,7 +16,7 @@ struct LaunchTuning {
     int gemv_waves_per_cu = 8;   // target resident waves per CU
     int gemm_variant = 0;
     int gemm_big_config = 0;     // large-M GEMM waves / pipeline depth (sweeps)
-    int gemv_variant = 0;        // 1 forces the fp32 GEMV kernels
+    int gemv_variant = 0;        // Q4_K: 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring
 };
 LaunchTuning &tuning();
 
@@ -26,6 +26,12 @@ hipError_t launch_dequant(int type_id, const uint8_t *w, int64_t row_bytes, int6
 // y[r] = sum_k W[r, k] * x[k] for r < rows.
 hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                        const float *x, float *y, int64_t rows, hipStream_t stream);
+
+// Q4_K GEMV on the matrix cores (gguf_gemv_mfma.hip).
+bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
+                        const float *x);
+hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
+                                const float *x, float *y, int64_t rows, hipStream_t stream);
 
 // Q4_K GEMV with integer dot products (gguf_gemv_dot4.hip).
 bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,

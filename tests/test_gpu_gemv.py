@@ -135,6 +135,72 @@ def test_gemv_parity(name, type_id, rows, cols):
     t.close()
 
 
+# Q4_K shapes at the edges of the matrix-core kernel's work split: one row,
+# rows around a 16-row tile, odd superblock counts (a half-empty last ring
+# stage), K-parts summed across waves (few tiles per workgroup), K = 16384
+# (the 64-superblock tables) and an uneven share of rows per workgroup.
+Q4K_SHAPES = [(1, 256), (15, 512), (17, 768), (33, 4096), (100, 1280), (1000, 2304),
+              (4103, 4096), (64, 16384), (40, 8448), (3000, 14336)]
+
+
+@pytest.mark.parametrize("rows,cols", Q4K_SHAPES, ids=[f"{r}x{c}" for r, c in Q4K_SHAPES])
+def test_q4k_gemv_kernels_agree_with_oracle(rows, cols):
+    print(f"[gpu] q4k gemv variants {rows}x{cols}", flush=True)
+    data = syn.q4_k_matrix(rows, cols, seed=rows * 7 + cols)
+    x = syn.activation(cols, seed=rows + 5)
+    t = _tensor(syn.Q4_K, data, cols)
+    ref = o.matvec_fp64(syn.Q4_K, data, cols, x)
+    try:
+        for variant in (0, 2, 1):  # matrix cores, v_dot4 ring, fp32
+            ops.set_option("gemv_variant", variant)
+            y = np.zeros(rows, np.float32)
+            ops.mat_vec(t, x, y)
+            assert o.rel_err(y, ref) <= GEMV_TOL, (variant, o.rel_err(y, ref))
+    finally:
+        ops.set_option("gemv_variant", 0)
+    t.close()
+
+
+def test_q4k_gemv_special_headers_match_java_order():
+    # NaN / infinite / zero / subnormal d and dmin: non-finite results appear
+    # in the same rows with the same sign as in the oracle's Java-order
+    # mat-vec, and zero min codes keep a non-finite dmin out of the sum
+    # (minContribution, RT/GgufKQuantLayout.java:67-69).
+    rows, cols = 64, 4096
+    data = syn.q4_k_matrix(rows, cols, seed=77).copy()
+    specials = [0x0000, 0x8000, 0x7E00, 0x7C00, 0xFC00, 0x0001, 0x8001]
+    for i, hbits in enumerate(specials):
+        data[i, 0::144] = hbits & 0xFF          # d of every superblock
+        data[i, 1::144] = hbits >> 8
+        data[16 + i, 2::144] = hbits & 0xFF     # dmin of every superblock
+        data[16 + i, 3::144] = hbits >> 8
+        data[32 + i, 2::144] = hbits & 0xFF     # dmin, with every min code zero
+        data[32 + i, 3::144] = hbits >> 8
+        for sb in range(cols // 256):
+            base = sb * 144 + 4
+            sc = data[32 + i, base:base + 12].copy()
+            sc[4:8] = 0      # min codes 0-3 and the high bits of min codes 4-7
+            sc[8:12] &= 0x0F  # low bits of min codes 4-7
+            data[32 + i, base:base + 12] = sc
+    x = syn.activation(cols, seed=78)
+    t = _tensor(syn.Q4_K, data, cols)
+    exp = o.matvec(syn.Q4_K, data, cols, x)
+    assert np.all(np.isfinite(exp[32:39])), "zero min codes must hide dmin"
+    try:
+        for variant in (0, 2):
+            ops.set_option("gemv_variant", variant)
+            y = np.zeros(rows, np.float32)
+            ops.mat_vec(t, x, y)
+            assert np.array_equal(np.isnan(y), np.isnan(exp)), (variant, y, exp)
+            assert np.array_equal(np.isposinf(y), np.isposinf(exp)), variant
+            assert np.array_equal(np.isneginf(y), np.isneginf(exp)), variant
+            fin = np.isfinite(exp)
+            assert o.rel_err(y[fin], exp[fin]) <= GEMV_TOL, variant
+    finally:
+        ops.set_option("gemv_variant", 0)
+    t.close()
+
+
 def test_gemv_lm_head_full_size_sampled_rows():
     # Q4_K K=4096 x N=128256 (lm_head): full-size GPU run; fp64 oracle on every
     # 97th row, plus linearity in x over all rows.
