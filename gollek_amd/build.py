@@ -27,6 +27,7 @@ HIP_SOURCES = (
     "gguf_gemv_mfma.hip",
     "gguf_gemm.hip",
     "gguf_moe.hip",
+    "gguf_moe_mfma.hip",
 )
 
 ARCH = "gfx950"

@@ -196,6 +196,7 @@ int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t 
     else if (strcmp(key, "gemm_variant") == 0) t.gemm_variant = (int)value;
     else if (strcmp(key, "gemm_big_config") == 0) t.gemm_big_config = (int)value;
     else if (strcmp(key, "gemv_variant") == 0) t.gemv_variant = (int)value;
+    else if (strcmp(key, "moe_variant") == 0) t.moe_variant = (int)value;
     else return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Unknown option %s", key);
     ok(err, err_len);
     return GOLLEK_HIP_OK;

@@ -17,6 +17,7 @@ struct LaunchTuning {
     int gemm_variant = 0;
     int gemm_big_config = 0;     // large-M GEMM waves / pipeline depth (sweeps)
     int gemv_variant = 0;        // Q4_K: 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring
+    int moe_variant = 0;         // 0 auto (matrix cores), 1 v_dot4 expert kernels
 };
 LaunchTuning &tuning();
 
@@ -56,6 +57,19 @@ hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t 
                           int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                           const float *x, const int32_t *ids, const float *wts, int T, int top_k,
                           float *out, uint8_t *ws, hipStream_t stream);
+
+// Pieces of the MoE pipeline shared by its two implementations (gguf_moe.hip,
+// gguf_moe_mfma.hip): routing (meta layout of moe_layout; tiles0 / tiles1 =
+// work items per expert and route group of the matrix-core passes) and the
+// route-order combine.
+hipError_t launch_moe_route(const int32_t *ids, const float *wts, int P, int E, int tiles0,
+                            int tiles1, int32_t *meta, hipStream_t stream);
+hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float *ypair, int T,
+                              int top_k, int H, int E, float *out, hipStream_t stream);
+bool moe_q4k_mfma_supported(int E, int H, int I, const float *x);
+hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
+                               int H, int I, const float *x, const int32_t *ids, const float *wts,
+                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);
 
 // Name of the GEMV kernel variant launch_gemv picks (for profiling notes).
 const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, const void *w,

@@ -35,12 +35,14 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
 
-// meta (int32): counts[E] | offsets[E+1] | pairs[P] | used[E] | nused
+// meta (int32): counts[E] | offsets[E+1] | pairs[P] | used[E] | nused |
+// items0[E+1] | items1[E+1] (work-item offsets of the used experts for the
+// gate/up and down passes of the matrix-core kernels)
 MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inter,
                      int64_t experts) {
     MoeLayout L;
     const int64_t P = tokens * top_k;
-    L.meta_ints = 2 * experts + 1 + P + experts + 1;
+    L.meta_ints = 2 * experts + 1 + P + experts + 1 + 2 * (experts + 1);
     L.meta = 0;
     L.xdig = align256(L.meta + (size_t)L.meta_ints * 4);
     L.xdig_stride = align256(digit_lds_bytes((int)(hidden / 32)));
@@ -52,13 +54,22 @@ MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inte
     return L;
 }
 
+// Routing on one workgroup: per-expert counts of the valid routes (expert id
+// in range, weight != 0; MFP:222), their offsets, the route list stably
+// sorted by expert, the used experts in expert order, and per used expert
+// u the work-item offsets items0/items1 = prefix of tiles * ceil(count / 4)
+// for the two expert passes.  Wave 0 scans in chunks of 64 with DPP-free
+// shuffles; the stable scatter ranks equal keys within a chunk by ballots.
 __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restrict__ ids,
                                                         const float *__restrict__ wts, int P,
-                                                        int E, int32_t *__restrict__ meta) {
-    extern __shared__ int32_t sh[];  // counts[E], flags prefix scratch
-    int32_t *cnt = sh;
+                                                        int E, int tiles0, int tiles1,
+                                                        int32_t *__restrict__ meta) {
+    extern __shared__ int32_t sh[];  // cnt[E], run[E]
+    int32_t *cnt = sh, *run = sh + E;
     int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
     int32_t *used = pairs + P, *nused = used + E;
+    int32_t *items0 = nused + 1, *items1 = items0 + E + 1;
+    const int lane = threadIdx.x & 63;
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
     __syncthreads();
     for (int p = threadIdx.x; p < P; p += blockDim.x) {
@@ -66,26 +77,69 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restric
         if (e >= 0 && e < E && wts[p] != 0.0f) atomicAdd(&cnt[e], 1);  // LDS atomic
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0, nu = 0;
-        for (int e = 0; e < E; e++) {
-            offsets[e] = acc;
-            counts[e] = cnt[e];
-            acc += cnt[e];
-            if (cnt[e] > 0) used[nu++] = e;
+    if (threadIdx.x < 64) {
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        int carry = 0, ucount = 0, it0 = 0, it1 = 0;
+        for (int base = 0; base < E; base += 64) {
+            const int e = base + lane;
+            const int c = e < E ? cnt[e] : 0;
+            const int groups = (c + 3) / 4;
+            int a = c, b0 = tiles0 * groups, b1 = tiles1 * groups;
+            // inclusive scans over the 64 lanes
+            for (int d = 1; d < 64; d <<= 1) {
+                const int ta = __shfl_up(a, d, 64), tb0 = __shfl_up(b0, d, 64), tb1 = __shfl_up(b1, d, 64);
+                if (lane >= d) {
+                    a += ta;
+                    b0 += tb0;
+                    b1 += tb1;
+                }
+            }
+            const uint64_t ub = __ballot(c > 0);
+            if (e < E) {
+                offsets[e] = carry + a - c;
+                counts[e] = c;
+                run[e] = carry + a - c;
+            }
+            if (c > 0) {
+                const int u = ucount + __popcll(ub & below);
+                used[u] = e;
+                items0[u] = it0 + b0 - tiles0 * groups;
+                items1[u] = it1 + b1 - tiles1 * groups;
+            }
+            carry += __shfl(a, 63, 64);
+            it0 += __shfl(b0, 63, 64);
+            it1 += __shfl(b1, 63, 64);
+            ucount += __popcll(ub);
         }
-        offsets[E] = acc;
-        *nused = nu;
-    }
-    __syncthreads();
-    // Stable scatter: a pair's slot is its expert's offset plus the number of
-    // earlier valid pairs routed to the same expert.
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-        const int e = ids[p];
-        if (!(e >= 0 && e < E && wts[p] != 0.0f)) continue;
-        int rank = 0;
-        for (int q = 0; q < p; q++) rank += (ids[q] == e && wts[q] != 0.0f) ? 1 : 0;
-        pairs[offsets[e] + rank] = p;
+        if (lane == 0) {
+            offsets[E] = carry;
+            *nused = ucount;
+            items0[ucount] = it0;
+            items1[ucount] = it1;
+        }
+        // Stable scatter, 64 routes at a time in route order: a route's slot is
+        // its expert's running offset plus its rank among the chunk's equal keys.
+        int bits = 1;
+        while ((1 << bits) <= E) bits++;
+        for (int base = 0; base < P; base += 64) {
+            const int p = base + lane;
+            int key = -1;
+            if (p < P) {
+                const int e = ids[p];
+                if (e >= 0 && e < E && wts[p] != 0.0f) key = e;
+            }
+            const uint32_t k1 = (uint32_t)(key + 1);
+            uint64_t same = __ballot(true);
+            for (int bt = 0; bt < bits; bt++) {
+                const uint64_t v = __ballot((k1 >> bt) & 1u);
+                same &= ((k1 >> bt) & 1u) ? v : ~v;
+            }
+            const int rank = __popcll(same & below);
+            const int r0 = key >= 0 ? run[key] : 0;  // read by all lanes before any update
+            if (key >= 0) pairs[r0 + rank] = p;
+            const bool last = (same >> lane) == 1ull;  // highest lane of its key
+            if (key >= 0 && last) run[key] = r0 + __popcll(same);
+        }
     }
 }
 
@@ -221,15 +275,32 @@ hipError_t launch_expert(int nsb, const uint8_t *w0, const uint8_t *w1, int64_t 
 
 }  // namespace
 
+hipError_t launch_moe_route(const int32_t *ids, const float *wts, int P, int E, int tiles0,
+                            int tiles1, int32_t *meta, hipStream_t stream) {
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 2 * (size_t)E * sizeof(int32_t), stream,
+                       ids, wts, P, E, tiles0, tiles1, meta);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float *ypair, int T,
+                              int top_k, int H, int E, float *out, hipStream_t stream) {
+    const int64_t total = (int64_t)T * H;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       stream, ids, wts, ypair, T, top_k, H, E, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                           int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                           const float *x, const int32_t *ids, const float *wts, int T, int top_k,
                           float *out, uint8_t *ws, hipStream_t stream) {
+    if (tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, x))
+        return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream);
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), (size_t)E * sizeof(int32_t), stream,
-                       ids, wts, P, E, meta);
+    hipError_t rerr = launch_moe_route(ids, wts, P, E, 0, 0, meta, stream);
+    if (rerr != hipSuccess) return rerr;
     hipLaunchKernelGGL(moe_digits_kernel, dim3(T), dim3(256), 0, stream, x, H, (int64_t)H,
                        ws + L.xdig, (int64_t)L.xdig_stride);
     hipError_t err = launch_expert<true>(H / kQK, gate, up, gate_row_bytes, I, 64, ws + L.xdig,
@@ -243,11 +314,8 @@ hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t 
                                (int64_t)L.hdig_stride, 1, top_k, meta, E, P,
                                reinterpret_cast<float *>(ws + L.ypair), H, stream);
     if (err != hipSuccess) return err;
-    const int64_t total = (int64_t)T * H;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                       stream, ids, wts, reinterpret_cast<const float *>(ws + L.ypair), T, top_k,
-                       H, E, out);
-    return hipGetLastError();
+    return launch_moe_combine(ids, wts, reinterpret_cast<const float *>(ws + L.ypair), T, top_k, H,
+                              E, out, stream);
 }
 
 }  // namespace gollek
