@@ -14,14 +14,17 @@
 // fp32 result before accumulation -- the reference's own block structure.
 // Rounding q * d to bf16 instead would cost ~1e-3 relative error per weight.
 //
-// Two kernels.  M >= 256: gemm_q8_0_bf16_big_kernel (128 x 64 workgroup
-// tiles, register-pipelined global loads, described below).  Smaller M:
-// gemm_q8_0_bf16_kernel, where a workgroup of 4 waves owns a BM x BN tile of
+// Kernels.  M >= 256: gemm_q8_0_bf16_ring_kernel (128 x 64 workgroup tiles
+// fed by buffer->LDS loads, described below; gemm_q8_0_bf16_big_kernel, the
+// register-pipelined version of the same tiling, remains selectable).
+// Smaller M: gemm_q8_0_bf16_kernel, where a workgroup of 4 waves owns a BM x BN tile of
 // Y; the waves split it WM x WN and, when WK > 1, also split each K stage
 // (the partial tiles are summed through LDS at the end).  Each stage moves
 // KB = 64 * WK columns of X (bf16) and W (Q8_0 block pairs, 68 aligned bytes,
 // realigned and widened to bf16 once per workgroup) into double-buffered LDS;
 // one barrier per stage.
+#include <type_traits>
+
 #include "gguf_blocks.hpp"
 #include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"
@@ -35,11 +38,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPad = 8;  // bf16 elements of row padding in LDS (bank spread)
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    // Exact: |q| <= 128 is representable in bf16.
-    const uint32_t l = __builtin_bit_cast(unsigned short, (__bf16)lo);
-    const uint32_t h = __builtin_bit_cast(unsigned short, (__bf16)hi);
-    return l | (h << 16);
+    // Exact: |q| <= 128 is representable in bf16 (one v_cvt_pk_bf16_f32).
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // 4 int8 in a dword -> 2 dwords of bf16 pairs.
@@ -437,6 +441,414 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_q8_0_bf16_big_ker
             }
 }
 
+// ---- large-M ring kernel --------------------------------------------------------
+//
+// Same 128 x 64 workgroup tile, eight waves of 32 x 32 and the same MFMA /
+// scale arithmetic as gemm_q8_0_bf16_big_kernel, with the operands moved by
+// buffer->LDS loads into a ring of six stage slots:
+//   - X: the stage's 128 rows x 64 columns of bf16 land directly in the
+//     XOR-swizzled layout of swz() (each lane loads the global chunk that
+//     belongs at its LDS position);
+//   - W: each row's 68-byte stage piece (a Q8_0 block pair) lands raw, its
+//     dwords 0..15 as four 16-byte chunks and dword 16 in a separate array.
+// The workgroup widens W to bf16 (and the block scales to fp32) two stages
+// ahead into one of three converted-W buffers.  The work of stage s is spread
+// so that the units overlap: right after the stage's one barrier each wave
+// issues the MFMAs of stage s from fragments it read during stage s - 1,
+// then the loads of stage s + 5, reads the fragments of stage s + 1, widens
+// stage s + 2, and applies the block scales to the MFMA results of stage
+// s - 1.  The loop is unrolled by the six slots so that every LDS address is
+// a per-lane register plus an immediate.  The LDS reads of ring data and all
+// LDS writes in the loop are inline asm: the compiler cannot tell which
+// buffer->LDS load wrote which bytes and would otherwise wait for every load
+// in flight.
+
+namespace {
+
+constexpr int kRgSlots = 6;
+constexpr int kRgXBytes = kBigBM * kRowStride;                  // X stage (bf16, swizzled)
+constexpr int kRgWQBytes = kBigBN * 64;                         // W dwords 0..15 per row
+constexpr int kRgW16Bytes = kBigBN * 4;                         // W dword 16 per row
+constexpr int kRgSlot = kRgXBytes + kRgWQBytes + kRgW16Bytes;   // 20736 bytes
+constexpr int kRgWbBytes = kBigBN * kRowStride;                 // converted W (bf16, swizzled)
+constexpr int kRgWbuf = kRgWbBytes + kBigBN * 8;                // + fp32 scales [row][2]
+constexpr int kRgWbufs = 3;
+constexpr int kRgDmaPerWave = 3;                                // 2 X + 1 W (or sink) per stage
+constexpr int kRgLds = kRgSlots * kRgSlot + kRgWbufs * kRgWbuf + 256;
+static_assert(kRgLds <= 160 * 1024, "LDS budget");
+// Slots 0..2 and 3..5 are addressed from two base registers so that every
+// offset fits the 16-bit immediate of the DS instructions.
+static_assert(2 * kRgSlot + kRgSlot <= 65536, "slot group offsets");
+
+// The stage's MFMA operands of one wave: A for blocks (kb) x rows (mt), B for
+// blocks x columns (nt), and the fp32 scale pairs of its two 16-column groups.
+struct RingFrags {
+    u32x4 a00, a01, a10, a11;  // a[kb][mt]
+    u32x4 b00, b01, b10, b11;  // b[kb][nt]
+    uint2 d0, d1;              // {d[n][0], d[n][1]} for nt = 0, 1
+};
+
+// Issues the reads only: the registers are valid after ring_wait() names them.
+template <int XO, int WO>
+__device__ __forceinline__ void ring_read_frags(uint32_t xa0, uint32_t xa1, uint32_t wb0,
+                                                uint32_t wb1, uint32_t dd, RingFrags &f) {
+    asm volatile(
+        "ds_read_b128 %0, %10 offset:%15\n\t"
+        "ds_read_b128 %1, %10 offset:%16\n\t"
+        "ds_read_b128 %2, %11 offset:%15\n\t"
+        "ds_read_b128 %3, %11 offset:%16\n\t"
+        "ds_read_b128 %4, %12 offset:%17\n\t"
+        "ds_read_b128 %5, %12 offset:%18\n\t"
+        "ds_read_b128 %6, %13 offset:%17\n\t"
+        "ds_read_b128 %7, %13 offset:%18\n\t"
+        "ds_read_b64 %8, %14 offset:%17\n\t"
+        "ds_read_b64 %9, %14 offset:%19"
+        : "=&v"(f.a00), "=&v"(f.a01), "=&v"(f.a10), "=&v"(f.a11), "=&v"(f.b00), "=&v"(f.b01),
+          "=&v"(f.b10), "=&v"(f.b11), "=&v"(f.d0), "=&v"(f.d1)
+        : "v"(xa0), "v"(xa1), "v"(wb0), "v"(wb1), "v"(dd), "n"(XO), "n"(XO + 2048), "n"(WO),
+          "n"(WO + 2048), "n"(WO + 128)
+        : "memory");
+}
+
+// Three raw dwords of a W piece (separate addresses: dword 16 lives apart)
+// and the scale dword; issued only, valid after ring_wait().
+template <int OFF>
+__device__ __forceinline__ void ring_read_raw(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
+                                              uint32_t &d0, uint32_t &d1, uint32_t &d2,
+                                              uint32_t &d3) {
+    asm volatile(
+        "ds_read_b32 %0, %4 offset:%8\n\t"
+        "ds_read_b32 %1, %5 offset:%8\n\t"
+        "ds_read_b32 %2, %6 offset:%8\n\t"
+        "ds_read_b32 %3, %7 offset:%8"
+        : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(OFF)
+        : "memory");
+}
+
+template <int OFF, typename T>
+__device__ __forceinline__ void ring_read(uint32_t a, T &v) {
+    if constexpr (sizeof(T) == 16)
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    else
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+}
+
+// Waits for every LDS read in flight.  The registers the reads write pass
+// through the statement, so no use of them can be scheduled before it.
+__device__ __forceinline__ void ring_wait(RingFrags &f, uint32_t &d0, uint32_t &d1, uint32_t &d2,
+                                          uint32_t &d3) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f.a00), "+v"(f.a01), "+v"(f.a10), "+v"(f.a11), "+v"(f.b00), "+v"(f.b01),
+                   "+v"(f.b10), "+v"(f.b11), "+v"(f.d0), "+v"(f.d1), "+v"(d0), "+v"(d1), "+v"(d2),
+                   "+v"(d3)
+                 :
+                 : "memory");
+}
+
+template <int OFF>
+__device__ __forceinline__ void ring_store4(uint32_t addr, u32x4 v) {
+    asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF) : "memory");
+}
+
+template <int OFF>
+__device__ __forceinline__ void ring_store1(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF) : "memory");
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+}  // namespace
+
+__global__ __launch_bounds__(512) void gemm_q8_0_bf16_ring_kernel(const uint8_t *__restrict__ W,
+                                                                  int64_t row_bytes,
+                                                                  const uint16_t *__restrict__ X,
+                                                                  float *__restrict__ Y, int M,
+                                                                  int N, int K) {
+    constexpr int NS = kRgSlots;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kRgLds];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // Tile order: groups of up to four M tiles, N-major inside a group, so
+    // that the workgroups an XCD runs at one time (the contiguous range
+    // [j G/8, (j+1) G/8) when the grid divides by 8, workgroups being dealt
+    // to XCDs round robin) share their X rows and W rows in that XCD's L2.
+    const int m_tiles = (M + kBigBM - 1) / kBigBM;
+    const int n_tiles = N / kBigBN;
+    const int G = (int)gridDim.x;
+    const int t = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int group = t / (4 * n_tiles);
+    const int first_m = 4 * group;
+    const int gm = m_tiles - first_m < 4 ? m_tiles - first_m : 4;
+    const int local = t - group * 4 * n_tiles;
+    const int mt_idx = first_m + local % gm, nt_idx = local / gm;
+    const int m0 = mt_idx * kBigBM, n0 = nt_idx * kBigBN;
+    const int nst = K / 64;
+
+    // X rows m0.. (zeros past M), W rows n0.. (N % 64 == 0 by dispatch).
+    // Loads of stages past the last one read the following bytes of the same
+    // buffers (or zeros past their ends) into slots that are never used.
+    const __amdgpu_buffer_rsrc_t xs = wave_buffer(
+        reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2,
+        (uint32_t)((int64_t)(M - m0 < kBigBM ? M - m0 : kBigBM) * K * 2));
+    const __amdgpu_buffer_rsrc_t ws =
+        wave_buffer(W + (int64_t)n0 * row_bytes, (uint32_t)(kBigBN * row_bytes));
+
+    uint8_t *const sink = lds + NS * kRgSlot + kRgWbufs * kRgWbuf;
+    const uint32_t base0 = (uint32_t)(uintptr_t)(lds_ptr)lds;
+    const uint32_t base1 = base0 + 3u * kRgSlot;
+    const uint32_t wbase = base0 + (uint32_t)(NS * kRgSlot);
+
+    // Loads of a stage.  X: wave w moves LDS chunks 64 (2w + i) + lane of the
+    // slot, i.e. row r = chunk / 8 at swizzled position chunk % 8, which holds
+    // the row's 16-byte column chunk kc = position ^ ((r >> 1) & 7).  W: waves
+    // 0..3 move 16-byte chunks (row = chunk / 4, part chunk % 4) of dwords
+    // 0..15, wave 4 moves dword 16 of every row, waves 5..7 issue a masked
+    // load into a sink so that every wave has the same count in flight.
+    uint32_t xo[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int p = 64 * (2 * wave + i) + lane;
+        const int r = p >> 3, kc = (p & 7) ^ ((r >> 1) & 7);
+        xo[i] = (uint32_t)r * (uint32_t)(2 * K) + 16u * (uint32_t)kc;
+    }
+    const int wp = 64 * wave + lane;
+    const uint32_t wo = wave < 4 ? (uint32_t)(wp >> 2) * (uint32_t)row_bytes + 16u * (uint32_t)(wp & 3)
+                                 : (uint32_t)lane * (uint32_t)row_bytes + 64u;
+    auto issue_x = [&](int s, uint8_t *slot, int i) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (lds_ptr)(slot + 1024 * (2 * wave + i)), 16,
+                                                 xo[i] + (uint32_t)s * 128u, 0, 0, 0);
+    };
+    auto issue_w = [&](int s, uint8_t *slot) {
+        const uint32_t wk = (uint32_t)s * 68u;
+        if (wave < 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)(slot + kRgXBytes + 1024 * wave), 16,
+                                                     wo + wk, 0, 0, 0);
+        else if (wave == 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)(slot + kRgXBytes + kRgWQBytes), 4,
+                                                     wo + wk, 0, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)sink, 4, kMaskedOffset, 0, 0, 0);
+    };
+    auto issue = [&](int s, uint8_t *slot) {
+        issue_x(s, slot, 0);
+        issue_x(s, slot, 1);
+        issue_w(s, slot);
+    };
+
+    // Widening role: row cn, block cb, quants 8 cu .. 8 cu + 7 of the block,
+    // which start in raw dword i0 = 2 cu (block 0: at byte 2) or 9 + 2 cu
+    // (block 1: aligned).  Dword 16 of a row lives in the separate array.
+    // Waves 6 and 7 also widen the block-0 / block-1 scale of row `lane`.
+    const int cn = tid >> 3, cb = (tid >> 2) & 1, cu = tid & 3;
+    const int ci0 = cb ? 9 + 2 * cu : 2 * cu;
+    const uint32_t csh = cb ? 0u : 2u;
+    auto raw_at = [&](int i) {
+        return (uint32_t)(i < 16 ? kRgXBytes + 64 * cn + 4 * i : kRgXBytes + kRgWQBytes + 4 * cn);
+    };
+    const uint32_t cr0 = raw_at(ci0), cr1 = raw_at(ci0 + 1), cr2 = raw_at(ci0 + 2);
+    const uint32_t cr0_g[2] = {base0 + cr0, base1 + cr0}, cr1_g[2] = {base0 + cr1, base1 + cr1},
+                   cr2_g[2] = {base0 + cr2, base1 + cr2};
+    const uint32_t cw = wbase + swz(cn, 4 * cb + cu);
+    const int sb = wave - 6;  // scale block of waves 6 and 7
+    const uint32_t cs_g[2] = {base0 + (uint32_t)(kRgXBytes + 64 * lane + 32 * sb),
+                              base1 + (uint32_t)(kRgXBytes + 64 * lane + 32 * sb)};
+    const uint32_t cd = wbase + (uint32_t)(kRgWbBytes + 8 * lane + 4 * sb);
+    // Waves below 6 read their first quant dword again instead of a scale.
+    const uint32_t cs_g2[2] = {wave >= 6 ? cs_g[0] : cr0_g[0], wave >= 6 ? cs_g[1] : cr0_g[1]};
+    uint32_t rw[4];
+    auto widen_read = [&](auto SLOT) {
+        constexpr int so = (decltype(SLOT)::value % 3) * kRgSlot;
+        constexpr int g = decltype(SLOT)::value / 3;
+        ring_read_raw<so>(cr0_g[g], cr1_g[g], cr2_g[g], cs_g2[g], rw[0], rw[1], rw[2], rw[3]);
+    };
+    auto widen_write = [&](auto WB) {
+        constexpr int wbo = decltype(WB)::value * kRgWbuf;
+        const uint32_t q0 = __builtin_amdgcn_alignbyte(rw[1], rw[0], csh);
+        const uint32_t q1 = __builtin_amdgcn_alignbyte(rw[2], rw[1], csh);
+        uint32_t o[4];
+        i8x4_to_bf16(q0, o[0], o[1]);
+        i8x4_to_bf16(q1, o[2], o[3]);
+        ring_store4<wbo>(cw, u32x4{o[0], o[1], o[2], o[3]});
+        if (wave >= 6) ring_store1<wbo>(cd, half_bits_to_float_fast(sb ? rw[3] >> 16 : rw[3] & 0xFFFFu));
+    };
+
+    // Fragment addresses (per lane; the slot / buffer offset is an immediate).
+    const int lr = lane & 15, lk = lane >> 4;
+    const uint32_t f_xa0 = swz(32 * wm + lr, lk), f_xa1 = swz(32 * wm + lr, 4 + lk);
+    const uint32_t xa0_g[2] = {base0 + f_xa0, base1 + f_xa0}, xa1_g[2] = {base0 + f_xa1, base1 + f_xa1};
+    const uint32_t wb0 = wbase + swz(32 * wn + lr, lk), wb1 = wbase + swz(32 * wn + lr, 4 + lk);
+    const uint32_t wdd = wbase + (uint32_t)(kRgWbBytes + 8 * (32 * wn + lr));
+    auto read_frags = [&](auto SLOT, auto WB, RingFrags &f) {
+        constexpr int so = (decltype(SLOT)::value % 3) * kRgSlot;
+        constexpr int g = decltype(SLOT)::value / 3;
+        constexpr int wbo = decltype(WB)::value * kRgWbuf;
+        ring_read_frags<so, wbo>(xa0_g[g], xa1_g[g], wb0, wb1, wdd, f);
+    };
+
+    f32x4 acc[2][2];
+    f32x4 part[2][2][2][2];  // [set][kb][mt][nt]
+    float dsc[2][2][2];      // [set][kb][nt]
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            acc[a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                part[1][c][a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                dsc[1][c][a] = 0.0f;
+            }
+        }
+    RingFrags F[2];
+
+    auto mfma_one = [&](int set, const RingFrags &f, int q) {
+        const int kb = q >> 2, mt = (q >> 1) & 1, nt = q & 1;
+        const u32x4 a = kb ? (mt ? f.a11 : f.a10) : (mt ? f.a01 : f.a00);
+        const u32x4 b = kb ? (nt ? f.b11 : f.b10) : (nt ? f.b01 : f.b00);
+        part[set][kb][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(a), as_bf16x8(b), f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    };
+    auto scale_q = [&](int set, int q) {
+        const int kb = q >> 2, nt = (q >> 1) & 1, mt = q & 1;
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            acc[mt][nt][v] = fmaf(dsc[set][kb][nt], part[set][kb][mt][nt][v], acc[mt][nt][v]);
+    };
+    auto pin_acc = [&]() {
+        asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
+    };
+    auto scale = [&](int set) {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[mt][nt][v] = fmaf(dsc[set][kb][nt], part[set][kb][mt][nt][v], acc[mt][nt][v]);
+    };
+
+    // Prologue: stages 0..4 in flight; stages 0 and 1 widened; fragments of 0 read.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    issue(0, lds);
+    issue(1, lds + kRgSlot);
+    issue(2, lds + 2 * kRgSlot);
+    issue(3, lds + 3 * kRgSlot);
+    issue(4, lds + 4 * kRgSlot);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kRgDmaPerWave * (NS - 3)) : "memory");
+    widen_read(I0{});
+    ring_wait(F[1], rw[0], rw[1], rw[2], rw[3]);
+    widen_write(I0{});
+    widen_read(I1{});
+    ring_wait(F[1], rw[0], rw[1], rw[2], rw[3]);
+    widen_write(I1{});
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    read_frags(I0{}, I0{}, F[0]);
+    ring_wait(F[0], rw[0], rw[1], rw[2], rw[3]);
+
+    // Stage s = 6 c + j sits in slot j, its widened W in buffer s % 3 = j % 3.
+    auto stage = [&](auto J, int s) {
+        constexpr int j = decltype(J)::value;
+        constexpr int cur = j & 1, nxt = cur ^ 1;
+        // Stage s + 2 has landed for every wave; stage s + 1 is widened.
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier"
+                     :
+                     : "n"(kRgDmaPerWave * (NS - 4))
+                     : "memory");
+        // Eight groups, one MFMA of stage s each, with four scale FMAs of
+        // stage s - 1 and the LDS reads of stages s + 2 (raw W) and s + 1
+        // (fragments) or a load issue, so that the LDS, the matrix core, the
+        // VALU and the load path each see a steady stream.
+        constexpr int sn = (j + 1) % NS, gn = sn / 3, so_n = (sn % 3) * kRgSlot;
+        constexpr int wo_n = ((j + 1) % 3) * kRgWbuf;
+        constexpr int sd = (j + NS - 1) % NS;
+        RingFrags &f = F[cur];
+        RingFrags &fn = F[nxt];
+        dsc[cur][0][0] = __uint_as_float(f.d0.x);
+        dsc[cur][1][0] = __uint_as_float(f.d0.y);
+        dsc[cur][0][1] = __uint_as_float(f.d1.x);
+        dsc[cur][1][1] = __uint_as_float(f.d1.y);
+        widen_read(std::integral_constant<int, (j + 2) % NS>{});
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_one(cur, f, 0);
+        scale_q(nxt, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        ring_read<so_n>(xa0_g[gn], fn.a00);
+        ring_read<so_n + 2048>(xa0_g[gn], fn.a01);
+        mfma_one(cur, f, 1);
+        scale_q(nxt, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        ring_read<so_n>(xa1_g[gn], fn.a10);
+        ring_read<so_n + 2048>(xa1_g[gn], fn.a11);
+        mfma_one(cur, f, 2);
+        scale_q(nxt, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_x(s + NS - 1, lds + sd * kRgSlot, 0);
+        ring_read<wo_n>(wb0, fn.b00);
+        ring_read<wo_n + 2048>(wb0, fn.b01);
+        mfma_one(cur, f, 3);
+        scale_q(nxt, 3);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_x(s + NS - 1, lds + sd * kRgSlot, 1);
+        ring_read<wo_n>(wb1, fn.b10);
+        ring_read<wo_n + 2048>(wb1, fn.b11);
+        mfma_one(cur, f, 4);
+        scale_q(nxt, 4);
+        pin_acc();
+        __builtin_amdgcn_sched_barrier(0);
+        issue_w(s + NS - 1, lds + sd * kRgSlot);
+        __builtin_amdgcn_sched_barrier(0);
+        ring_read<wo_n>(wdd, fn.d0);
+        ring_read<wo_n + 128>(wdd, fn.d1);
+        mfma_one(cur, f, 5);
+        scale_q(nxt, 5);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_one(cur, f, 6);
+        scale_q(nxt, 6);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_one(cur, f, 7);
+        scale_q(nxt, 7);
+        pin_acc();
+        __builtin_amdgcn_sched_barrier(0);
+        ring_wait(F[nxt], rw[0], rw[1], rw[2], rw[3]);
+        widen_write(std::integral_constant<int, (j + 2) % 3>{});
+        if (s + 1 == nst) scale(cur);
+    };
+    for (int s = 0; s < nst; s += NS) {
+        stage(std::integral_constant<int, 0>{}, s);
+        if (s + 1 >= nst) break;
+        stage(std::integral_constant<int, 1>{}, s + 1);
+        if (s + 2 >= nst) break;
+        stage(std::integral_constant<int, 2>{}, s + 2);
+        if (s + 3 >= nst) break;
+        stage(std::integral_constant<int, 3>{}, s + 3);
+        if (s + 4 >= nst) break;
+        stage(std::integral_constant<int, 4>{}, s + 4);
+        if (s + 5 >= nst) break;
+        stage(std::integral_constant<int, 5>{}, s + 5);
+    }
+    // Drain the loads issued past the last stage before the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // D layout of a 16x16 tile: lane holds column lane & 15, rows 4 (lane >> 4) + v.
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + 32 * wm + 16 * mt + 4 * lk + v;
+                const int n = n0 + 32 * wn + 16 * nt + lr;
+                if (m < M) Y[(int64_t)m * N + n] = acc[mt][nt][v];
+            }
+}
+
 // Any shape: one thread per output, fp32, exact per-block scaling.
 __global__ __launch_bounds__(256) void gemm_q8_0_generic_kernel(const uint8_t *__restrict__ W,
                                                                 int64_t row_bytes,
@@ -488,14 +900,15 @@ hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint
 #define GOLLEK_BIG(P, WMW, WNW)                                                                \
     hipLaunchKernelGGL((gemm_q8_0_bf16_big_kernel<P, WMW, WNW>), dim3(grid),                \
                        dim3(64 * (WMW) * (WNW)), 0, stream, w, row_bytes, x, y, M, N, K)
-        // Measured on MI355X (4096 x 4096, M = 256 .. 1024): the eight-wave
-        // 2-deep pipeline (112 VGPRs, two workgroups per CU when the grid
-        // has them) matches the deeper ones at M = 512 and wins at M = 1024.
+        // Configs 1..4 select the register-pipelined kernel (sweeps); the
+        // default is the buffer->LDS ring.
         if (nst % 4 == 0 && cfg == 1) GOLLEK_BIG(4, 4, 2);
         else if (nst % 8 == 0 && cfg == 2) GOLLEK_BIG(8, 4, 2);
+        else if (nst % 2 == 0 && cfg == 3) GOLLEK_BIG(2, 4, 2);
         else if (nst % 4 == 0 && cfg == 4) GOLLEK_BIG(4, 2, 2);
-        else if (nst % 2 == 0) GOLLEK_BIG(2, 4, 2);
-        else GOLLEK_BIG(1, 4, 2);
+        else
+            hipLaunchKernelGGL(gemm_q8_0_bf16_ring_kernel, dim3(grid), dim3(512), 0, stream, w,
+                               row_bytes, x, y, M, N, K);
 #undef GOLLEK_BIG
         return hipGetLastError();
     }

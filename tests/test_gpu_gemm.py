@@ -83,6 +83,26 @@ def test_gemm_large_m_kernel_shapes(rows, cols, m, variant):
     t.close()
 
 
+@pytest.mark.parametrize("cfg", [0, 1, 3])
+@pytest.mark.parametrize("rows,cols,m", [(192, 4096, 300), (4096, 192, 257), (64, 64, 130)])
+def test_gemm_large_m_configs(rows, cols, m, cfg):
+    # The large-M kernels: the buffer->LDS ring (cfg 0; K from one block
+    # pair, fewer stages than ring slots, up to 64 stages) and two
+    # register-pipelined configurations.
+    print(f"[gpu] gemm large-m cfg={cfg} rows={rows} cols={cols} m={m}", flush=True)
+    data = syn.q8_0_matrix(rows, cols, seed=rows + cols + cfg)
+    t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=m + cfg)
+    y = np.full((m, rows), np.nan, np.float32)
+    ops.set_option("gemm_big_config", cfg)
+    try:
+        ops.gemm_bf16(t, x, y)
+    finally:
+        ops.set_option("gemm_big_config", 0)
+    assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
+    t.close()
+
+
 def test_gemm_rejects_other_types_and_short_buffers():
     data = syn.q4_k_matrix(16, 256, seed=1)
     t = ops.GgufTensor("w", (256, 16), syn.Q4_K, data.reshape(-1))
