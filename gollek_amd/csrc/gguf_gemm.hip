@@ -17,7 +17,9 @@
 // Kernels.  M >= 256: gemm_q8_0_bf16_ring_kernel (128 x 64 workgroup tiles
 // fed by buffer->LDS loads, described below; gemm_q8_0_bf16_big_kernel, the
 // register-pipelined version of the same tiling, remains selectable).
-// Smaller M: gemm_q8_0_bf16_kernel, where a workgroup of 4 waves owns a BM x BN tile of
+// M <= 32: gemm_q8_0_bf16_skinny_kernel (16-row column tiles, K split over
+// the waves, one buffer->LDS ring per wave).  In between:
+// gemm_q8_0_bf16_kernel, where a workgroup of 4 waves owns a BM x BN tile of
 // Y; the waves split it WM x WN and, when WK > 1, also split each K stage
 // (the partial tiles are summed through LDS at the end).  Each stage moves
 // KB = 64 * WK columns of X (bf16) and W (Q8_0 block pairs, 68 aligned bytes,
@@ -849,6 +851,214 @@ __global__ __launch_bounds__(512) void gemm_q8_0_bf16_ring_kernel(const uint8_t 
             }
 }
 
+// ---- small-M ring kernel --------------------------------------------------------
+//
+// M <= 16 TT tokens.  A workgroup of four waves owns 16 W rows and every
+// token.  Wave w contracts the Q8_0 block pairs p = w, w + 4, w + 8, ... of
+// K (64 columns each) and has a ring of NS slots of its own, so the waves
+// never wait for each other until the end: per pair it loads, by
+// buffer->LDS, the tokens' 64 bf16 columns (16-byte chunks XOR-swizzled by
+// token pair, so the fragment reads are free of bank conflicts) and the 16
+// rows' 68-byte raw pieces (dwords 0..15 as 16-byte chunks, dword 16 apart).
+// X is the MFMA A operand (rows = tokens) and W the B operand, widened from
+// the raw quants in registers: each lane's output column is one W row, so a
+// block scale is one value per lane.  The four waves' partial tiles are
+// summed through LDS in wave order at the end.
+
+namespace {
+
+constexpr int kSkRows = 16;
+
+template <int TT>
+struct SkGeom {
+    static constexpr int kXBytes = 16 * TT * 128;   // tokens x 64 bf16
+    static constexpr int kWQ = kXBytes;             // 16 rows x dwords 0..15
+    static constexpr int kW16 = kWQ + 1024;         // dword 16 of each row (64 lanes x 4 B)
+    static constexpr int kSlot = kW16 + 256;
+    static constexpr int kXDma = TT * 2;
+    static constexpr int kDma = kXDma + 2;          // + W chunks + W dword 16
+};
+
+template <int TT, int NS>
+constexpr int skinny_lds_bytes() {
+    return 4 * NS * SkGeom<TT>::kSlot + 3 * TT * 1024;
+}
+
+// 16- and 4-byte-per-lane buffer->LDS loads (__device__ functions: called
+// directly from a kernel template's body, the builtin makes hipcc's host pass
+// drop the kernel's launch stub).
+__device__ __forceinline__ void dma_lds16(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void dma_lds4(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 4, off, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (a separate template: an asm immediate that depends on
+// a kernel template's parameters also drops the stub).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// One pair's LDS reads of a wave: raw dwords 2kq, 2kq + 1, 2kq + 2, 9 + 2kq
+// (from wr0), 10 + 2kq (w10a: dword 16 lives apart), scale dwords 0 and 8
+// (from wrs), and the X fragments of both blocks and TT token tiles.
+template <int TT>
+__device__ __forceinline__ void skinny_read(uint32_t wr0, uint32_t w10a, uint32_t wrs, uint32_t xa0,
+                                            uint32_t xa1, uint2 &w01, uint2 &w29, uint32_t &w10,
+                                            uint2 &sc, u32x4 (&xf)[2][TT]) {
+    if constexpr (TT == 1) {
+        asm volatile(
+            "ds_read2_b32 %0, %6 offset0:0 offset1:1\n\t"
+            "ds_read2_b32 %1, %6 offset0:2 offset1:9\n\t"
+            "ds_read_b32 %2, %7\n\t"
+            "ds_read2_b32 %3, %8 offset0:0 offset1:8\n\t"
+            "ds_read_b128 %4, %9\n\t"
+            "ds_read_b128 %5, %10\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(w01), "=&v"(w29), "=&v"(w10), "=&v"(sc), "=&v"(xf[0][0]), "=&v"(xf[1][0])
+            : "v"(wr0), "v"(w10a), "v"(wrs), "v"(xa0), "v"(xa1)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read2_b32 %0, %8 offset0:0 offset1:1\n\t"
+            "ds_read2_b32 %1, %8 offset0:2 offset1:9\n\t"
+            "ds_read_b32 %2, %9\n\t"
+            "ds_read2_b32 %3, %10 offset0:0 offset1:8\n\t"
+            "ds_read_b128 %4, %11\n\t"
+            "ds_read_b128 %5, %11 offset:2048\n\t"
+            "ds_read_b128 %6, %12\n\t"
+            "ds_read_b128 %7, %12 offset:2048\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(w01), "=&v"(w29), "=&v"(w10), "=&v"(sc), "=&v"(xf[0][0]), "=&v"(xf[0][TT - 1]),
+              "=&v"(xf[1][0]), "=&v"(xf[1][TT - 1])
+            : "v"(wr0), "v"(w10a), "v"(wrs), "v"(xa0), "v"(xa1)
+            : "memory");
+    }
+}
+
+}  // namespace
+
+template <int TT, int NS>
+__global__ __launch_bounds__(256) void gemm_q8_0_bf16_skinny_kernel(const uint8_t *__restrict__ W,
+                                                                    int64_t row_bytes,
+                                                                    const uint16_t *__restrict__ X,
+                                                                    float *__restrict__ Y, int M,
+                                                                    int N, int K) {
+    using G = SkGeom<TT>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[skinny_lds_bytes<TT, NS>()];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = (int)blockIdx.x * kSkRows;
+    const int npairs = K / 256;  // pairs per wave
+    const int mrows = M < 16 * TT ? M : 16 * TT;
+
+    // Tokens 0 .. mrows - 1 (zeros past M), W rows n0 .. n0 + 15.  Loads of
+    // pairs past the last one read the following bytes of the same buffers
+    // (or zeros past their ends) into slots that are never used.
+    const __amdgpu_buffer_rsrc_t xs =
+        wave_buffer(reinterpret_cast<const uint8_t *>(X), (uint32_t)((int64_t)mrows * K * 2));
+    const __amdgpu_buffer_rsrc_t ws =
+        wave_buffer(W + (int64_t)n0 * row_bytes, (uint32_t)(kSkRows * row_bytes));
+    uint8_t *const ring = lds + wave * NS * G::kSlot;
+    float *const red = reinterpret_cast<float *>(lds + 4 * NS * G::kSlot);
+
+    // Load offsets of pair 0 (pair p adds 128 p to X, 68 p to W).  X: LDS
+    // chunk q = 64 i + lane is token t = q / 8 at swizzled position q % 8,
+    // which holds column chunk position ^ ((t >> 1) & 7).  W: chunk lane is
+    // row lane / 4, part lane % 4; dword 16 of row lane (lanes < 16).
+    uint32_t xo[2 * TT];
+#pragma unroll
+    for (int i = 0; i < 2 * TT; i++) {
+        const int q = 64 * i + lane;
+        const int t = q >> 3, c = (q & 7) ^ ((t >> 1) & 7);
+        xo[i] = (uint32_t)t * (uint32_t)(2 * K) + 16u * (uint32_t)c;
+    }
+    const uint32_t wo = (uint32_t)(lane >> 2) * (uint32_t)row_bytes + 16u * (uint32_t)(lane & 3);
+    const uint32_t w16o = lane < 16 ? (uint32_t)lane * (uint32_t)row_bytes + 64u : kMaskedOffset;
+    auto issue = [&](int j, uint8_t *slot) {
+        const uint32_t p = (uint32_t)(wave + 4 * j);
+#pragma unroll
+        for (int i = 0; i < 2 * TT; i++) dma_lds16(xs, slot + 1024 * i, xo[i] + 128u * p);
+        dma_lds16(ws, slot + G::kWQ, wo + 68u * p);
+        dma_lds4(ws, slot + G::kW16, lane < 16 ? w16o + 68u * p : kMaskedOffset);
+    };
+
+    // Fragment addresses relative to a slot.  A (X): token m = lane & 15 (+16
+    // per token tile), chunk 4 kb + kq at its swizzled position.  B (W): row
+    // n = lane & 15, quants 8 kq .. 8 kq + 7 of block kb (raw dwords 2kq ..
+    // 2kq + 2 with block 0 starting at byte 2; 9 + 2kq, 10 + 2kq), scales in
+    // dword 0 (low half) and dword 8 (high half).
+    const int lr = lane & 15, kq = lane >> 4;
+    const uint32_t xa0 = (uint32_t)(128 * lr + 16 * ((kq) ^ ((lr >> 1) & 7)));
+    const uint32_t xa1 = (uint32_t)(128 * lr + 16 * ((4 + kq) ^ ((lr >> 1) & 7)));
+    const uint32_t wr0 = (uint32_t)(G::kWQ + 64 * lr + 8 * kq);
+    const uint32_t w10 = kq < 3 ? wr0 + 40u : (uint32_t)(G::kW16 + 4 * lr);
+    const uint32_t wrs = (uint32_t)(G::kWQ + 64 * lr);
+    const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
+
+    f32x4 acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int j = 0; j < NS - 1; j++) issue(j, ring + j * G::kSlot);
+
+    int sl = 0;
+    for (int j = 0; j < npairs; j++) {
+        wait_vm<G::kDma * (NS - 2)>();  // pair j has landed
+        issue(j + NS - 1, ring + (sl == 0 ? NS - 1 : sl - 1) * G::kSlot);
+        const uint32_t sb = ring_base + (uint32_t)(sl * G::kSlot);
+        uint2 w01, w29, sc;
+        uint32_t w10v;
+        u32x4 xf[2][TT];
+        skinny_read<TT>(sb + wr0, sb + w10, sb + wrs, sb + xa0, sb + xa1, w01, w29, w10v, sc, xf);
+        uint32_t b0[4], b1[4];
+        i8x4_to_bf16(__builtin_amdgcn_alignbyte(w01.y, w01.x, 2), b0[0], b0[1]);
+        i8x4_to_bf16(__builtin_amdgcn_alignbyte(w29.x, w01.y, 2), b0[2], b0[3]);
+        i8x4_to_bf16(w29.y, b1[0], b1[1]);
+        i8x4_to_bf16(w10v, b1[2], b1[3]);
+        const float d0 = half_bits_to_float_fast(sc.x & 0xFFFFu);
+        const float d1 = half_bits_to_float_fast(sc.y >> 16);
+        const bf16x8 B0 = as_bf16x8(u32x4{b0[0], b0[1], b0[2], b0[3]});
+        const bf16x8 B1 = as_bf16x8(u32x4{b1[0], b1[1], b1[2], b1[3]});
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const f32x4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xf[0][t]), B0,
+                                                                     f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            const f32x4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xf[1][t]), B1,
+                                                                     f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[t][v] = fmaf(d1, p1[v], fmaf(d0, p0[v], acc[t][v]));
+        }
+        sl = sl + 1 == NS ? 0 : sl + 1;
+    }
+    // Drain the loads issued past the last pair, then sum the four waves'
+    // partial tiles in wave order.  D layout of a 16x16 tile: lane holds
+    // column lane & 15 (a W row), rows (tokens) 4 (lane >> 4) + v.
+    wait_vm<0>();
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+            *reinterpret_cast<f32x4 *>(red + (((wave - 1) * TT + t) * 64 + lane) * 4) = acc[t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        f32x4 v = acc[t];
+#pragma unroll
+        for (int w = 0; w < 3; w++) v += *reinterpret_cast<const f32x4 *>(red + ((w * TT + t) * 64 + lane) * 4);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 16 * t + 4 * kq + r;
+            if (m < M) Y[(int64_t)m * N + n0 + lr] = v[r];
+        }
+    }
+}
+
 // Any shape: one thread per output, fp32, exact per-block scaling.
 __global__ __launch_bounds__(256) void gemm_q8_0_generic_kernel(const uint8_t *__restrict__ W,
                                                                 int64_t row_bytes,
@@ -910,6 +1120,22 @@ hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint
             hipLaunchKernelGGL(gemm_q8_0_bf16_ring_kernel, dim3(grid), dim3(512), 0, stream, w,
                                row_bytes, x, y, M, N, K);
 #undef GOLLEK_BIG
+        return hipGetLastError();
+    }
+    // Small M: the buffer->LDS ring over 16-row column tiles (v == 3 keeps
+    // the register-pipelined tiles below, for sweeps).
+    if (aligned && v != 1 && v != 3 && M <= 32 && N % 16 == 0 && K % 256 == 0 &&
+        (int64_t)16 * row_bytes < ((int64_t)1 << 31) && (int64_t)M * K * 2 < ((int64_t)1 << 31)) {
+        const int cfg = tuning().gemm_big_config;
+#define GOLLEK_SKINNY(TT, NS)                                                                      \
+    hipLaunchKernelGGL((gemm_q8_0_bf16_skinny_kernel<TT, NS>), dim3(N / 16), dim3(256), 0, stream, w, \
+                       row_bytes, x, y, M, N, K)
+        // Measured on MI355X (4096 x 4096): four slots per wave beat deeper
+        // rings (which only queue more requests at the HBM).
+        if (M <= 16 && cfg == 18) GOLLEK_SKINNY(1, 8);
+        else if (M <= 16) GOLLEK_SKINNY(1, 4);
+        else GOLLEK_SKINNY(2, 4);
+#undef GOLLEK_SKINNY
         return hipGetLastError();
     }
     if (aligned && v != 1) {

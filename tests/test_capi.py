@@ -27,6 +27,14 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_library_resolves_all_of_its_own_symbols():
+    # Loading binds lazily here, so an unresolved kernel launch stub (which
+    # hipcc can leave behind for a kernel template) would only fail on first
+    # use; dlopen with RTLD_NOW resolves every symbol up front.
+    lib_path = _native.load()._name
+    ctypes.CDLL(lib_path, mode=ctypes.RTLD_GLOBAL | 0x2)  # RTLD_NOW
+
+
 def test_python_signatures_cover_header():
     assert set(declared_functions()) <= set(_native.SIGNATURES)
 

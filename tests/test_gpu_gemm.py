@@ -103,6 +103,21 @@ def test_gemm_large_m_configs(rows, cols, m, cfg):
     t.close()
 
 
+@pytest.mark.parametrize("rows,cols,m", [(16, 256, 1), (16, 256, 16), (48, 512, 17), (32, 1280, 32),
+                                          (64, 4096, 9), (4096, 768, 16), (208, 2048, 31)])
+def test_gemm_small_m_ring_shapes(rows, cols, m):
+    # The small-M ring kernel: one 16-row tile up to many, K from one stage
+    # (fewer stages than ring slots) up, one or two token tiles, partial tiles.
+    print(f"[gpu] gemm small-m rows={rows} cols={cols} m={m}", flush=True)
+    data = syn.q8_0_matrix(rows, cols, seed=rows * 3 + cols + m)
+    t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=m + 11)
+    y = np.full((m, rows), np.nan, np.float32)
+    ops.gemm_bf16(t, x, y)
+    assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
+    t.close()
+
+
 def test_gemm_rejects_other_types_and_short_buffers():
     data = syn.q4_k_matrix(16, 256, seed=1)
     t = ops.GgufTensor("w", (256, 16), syn.Q4_K, data.reshape(-1))
