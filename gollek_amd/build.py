@@ -25,6 +25,7 @@ HIP_SOURCES = (
     "gguf_gemv.hip",
     "gguf_gemv_dot4.hip",
     "gguf_gemv_mfma.hip",
+    "gguf_gemv_ring.hip",
     "gguf_gemm.hip",
     "gguf_moe.hip",
     "gguf_moe_mfma.hip",

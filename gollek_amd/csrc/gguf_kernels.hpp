@@ -29,6 +29,11 @@ hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t
                        const float *x, float *y, int64_t rows, hipStream_t stream);
 
 // Q4_K GEMV on the matrix cores (gguf_gemv_mfma.hip).
+// Q8_0 / Q4_0 GEMV through per-wave buffer->LDS rings (gguf_gemv_ring.hip).
+bool gemv_ring_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
+                         const float *x);
+hipError_t launch_gemv_ring(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
+                            const float *x, float *y, int64_t rows, hipStream_t stream);
 bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x);
 hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,

@@ -75,9 +75,10 @@ int32_t gollek_hip_last_status(void);
 
 /* Tuning knobs for benchmarks and sweeps (keys: "gemv_rows_per_wave",
  * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
- * "gemm_big_config", "moe_variant").  gemv_variant selects the Q4_K GEMV
- * kernel: 0 = the matrix-core kernel where it applies, 1 = the fp32 kernels,
- * 2 = the v_dot4 kernel (K <= 4096); moe_variant 1 selects the v_dot4 MoE
+ * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
+ * 0 = the matrix-core kernel (Q4_K) and the buffer->LDS ring kernels (Q8_0,
+ * Q4_0) where they apply, 1 = the fp32 kernels, 2 = the v_dot4 kernel (Q4_K,
+ * K <= 4096); moe_variant 1 selects the v_dot4 MoE
  * expert kernels instead of the matrix-core passes.  No reference
  * counterpart; the reference reads JVM properties instead
  * (RT/GgufParallelConfig.java:87-101). */

@@ -201,6 +201,70 @@ def test_q4k_gemv_special_headers_match_java_order():
     t.close()
 
 
+# Q8_0 / Q4_0 shapes at the edges of the ring kernel's split (16-row
+# workgroups of four 4-row waves, 512-column items): one row, ragged row
+# counts, a single item (fewer than the ring's slots), K = 16384 (all of x
+# in LDS) and past it (the fp32 kernels take over), the two configurations.
+Q80_Q40_SHAPES = [(syn.Q8_0, 1, 512), (syn.Q8_0, 15, 512), (syn.Q8_0, 17, 1536), (syn.Q8_0, 4096, 4096),
+                  (syn.Q8_0, 33, 16384), (syn.Q8_0, 6, 16896), (syn.Q4_0, 1, 512), (syn.Q4_0, 7, 1024),
+                  (syn.Q4_0, 11008, 4096), (syn.Q4_0, 35, 16384)]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", Q80_Q40_SHAPES,
+                         ids=[f"{'q8_0' if t == syn.Q8_0 else 'q4_0'}_{r}x{c}" for t, r, c in Q80_Q40_SHAPES])
+def test_q8_0_q4_0_gemv_kernels_agree_with_oracle(type_id, rows, cols):
+    print(f"[gpu] q8_0/q4_0 gemv variants type={type_id} {rows}x{cols}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=rows * 5 + cols + type_id)
+    x = syn.activation(cols, seed=rows + 6)
+    t = _tensor(type_id, data, cols)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    try:
+        for variant in (0, 1):  # buffer->LDS ring, fp32 kernels
+            ops.set_option("gemv_variant", variant)
+            y = np.zeros(rows, np.float32)
+            ops.mat_vec(t, x, y)
+            assert o.rel_err(y, ref) <= GEMV_TOL, (variant, o.rel_err(y, ref))
+            part = np.full(rows, -3.0, np.float32)
+            ops.mat_vec_rows(t, x, part, rows // 2, True)  # a row prefix
+            assert np.array_equal(part[:rows // 2], y[:rows // 2]), variant
+            assert np.all(part[rows // 2:] == -3.0), variant
+    finally:
+        ops.set_option("gemv_variant", 0)
+    t.close()
+
+
+@pytest.mark.parametrize("type_id", [syn.Q8_0, syn.Q4_0])
+def test_q8_0_q4_0_gemv_special_scales_match_java_order(type_id):
+    # NaN / infinite / zero / subnormal block scales on every block of a row:
+    # the non-finite results land in the same rows with the same sign as the
+    # oracle's Java-order mat-vec (one d_b * sum per block, as there).
+    rows, cols = 32, 4096
+    bb = 34 if type_id == syn.Q8_0 else 18
+    data = syn.matrix(type_id, rows, cols, seed=91 + type_id).copy()
+    specials = [0x0000, 0x8000, 0x7E00, 0x7C00, 0xFC00, 0x0001, 0x8001]
+    for i, hbits in enumerate(specials):
+        data[i, 0::bb] = hbits & 0xFF
+        data[i, 1::bb] = hbits >> 8
+        data[16 + i, 0:16 * bb:bb] = hbits & 0xFF   # the first 16 blocks only
+        data[16 + i, 1:16 * bb:bb] = hbits >> 8
+    x = syn.activation(cols, seed=92)
+    t = _tensor(type_id, data, cols)
+    exp = o.matvec(type_id, data, cols, x)
+    try:
+        for variant in (0, 1):
+            ops.set_option("gemv_variant", variant)
+            y = np.zeros(rows, np.float32)
+            ops.mat_vec(t, x, y)
+            assert np.array_equal(np.isnan(y), np.isnan(exp)), (variant, y, exp)
+            assert np.array_equal(np.isposinf(y), np.isposinf(exp)), variant
+            assert np.array_equal(np.isneginf(y), np.isneginf(exp)), variant
+            fin = np.isfinite(exp)
+            assert o.rel_err(y[fin], exp[fin]) <= GEMV_TOL, variant
+    finally:
+        ops.set_option("gemv_variant", 0)
+    t.close()
+
+
 def test_gemv_lm_head_full_size_sampled_rows():
     # Q4_K K=4096 x N=128256 (lm_head): full-size GPU run; fp64 oracle on every
     # 97th row, plus linearity in x over all rows.
