@@ -25,6 +25,8 @@ struct gollek_hip_weight {
     hipStream_t stream = nullptr;  // stream of the host-buffer entry points
     uint8_t *staging = nullptr;    // device staging for host x / y / dst
     size_t staging_bytes = 0;
+    float *gemm_ws = nullptr;      // split-K partial tiles of the device GEMM entry
+    size_t gemm_ws_bytes = 0;
 };
 
 namespace {
@@ -247,6 +249,7 @@ void gollek_hip_weight_free(gollek_hip_weight *w) {
     if (w->stream != nullptr) (void)hipStreamSynchronize(w->stream);
     if (w->owned && w->data != nullptr) (void)hipFree(w->data);
     if (w->staging != nullptr) (void)hipFree(w->staging);
+    if (w->gemm_ws != nullptr) (void)hipFree(w->gemm_ws);
     if (w->stream != nullptr) (void)hipStreamDestroy(w->stream);
     delete w;
 }
@@ -415,15 +418,18 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     if (rc != GOLLEK_HIP_OK) return rc;
     const size_t x_bytes = align_up((size_t)(m * w->cols) * sizeof(uint16_t), 256);
     const size_t y_bytes = (size_t)(m * w->rows) * sizeof(float);
-    rc = ensure_staging(w, x_bytes + y_bytes, err, err_len);
+    const size_t ws_bytes = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
+    const size_t ws_off = align_up(x_bytes + y_bytes, 256);
+    rc = ensure_staging(w, ws_off + ws_bytes, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     uint16_t *d_x = reinterpret_cast<uint16_t *>(w->staging);
     float *d_y = reinterpret_cast<float *>(w->staging + x_bytes);
+    float *d_ws = ws_bytes ? reinterpret_cast<float *>(w->staging + ws_off) : nullptr;
     hipError_t e = hipMemcpyAsync(d_x, x, (size_t)(m * w->cols) * sizeof(uint16_t),
                                   hipMemcpyHostToDevice, w->stream);
     if (e == hipSuccess)
         e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, d_x, d_y, (int)m, (int)w->rows,
-                                          (int)w->cols, w->stream);
+                                          (int)w->cols, w->stream, d_ws, ws_bytes);
     if (e == hipSuccess) e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "gemm", err, err_len);
@@ -435,8 +441,29 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
                                     void *stream, char *err, size_t err_len) {
     const int32_t rc = check_gemm(w, x, y, m, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
+    // The handle's split-K workspace: allocated at the first call that splits,
+    // for the largest split any m of this weight uses (at most 4 MiB on 256
+    // CUs), and kept until the handle is freed, so a launch in flight never
+    // loses it.
+    const size_t need = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
+    if (need > 0) {
+        std::lock_guard<std::mutex> lock(w->mu);
+        if (w->gemm_ws == nullptr) {
+            const size_t most = gollek::gemm_workspace_max_bytes((int)w->rows, (int)w->cols);
+            const size_t bytes = most > need ? most : need;
+            const int32_t urc = use_device(w->device, err, err_len);
+            if (urc != GOLLEK_HIP_OK) return urc;
+            const hipError_t ae = hipMalloc(reinterpret_cast<void **>(&w->gemm_ws), bytes);
+            if (ae != hipSuccess) {
+                w->gemm_ws = nullptr;
+                return hip_fail(ae, "hipMalloc(gemm workspace)", err, err_len);
+            }
+            w->gemm_ws_bytes = bytes;
+        }
+    }
     hipError_t e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
-                                                 (int)w->cols, static_cast<hipStream_t>(stream));
+                                                 (int)w->cols, static_cast<hipStream_t>(stream),
+                                                 need ? w->gemm_ws : nullptr, w->gemm_ws_bytes);
     if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;

@@ -14,14 +14,18 @@
 // fp32 result before accumulation -- the reference's own block structure.
 // Rounding q * d to bf16 instead would cost ~1e-3 relative error per weight.
 //
-// Kernels.  M >= 256: gemm_q8_0_bf16_ring_kernel (128 x 64 workgroup tiles
-// fed by buffer->LDS loads, described below; gemm_q8_0_bf16_big_kernel, the
-// register-pipelined version of the same tiling, remains selectable).
-// M <= 32: gemm_q8_0_bf16_skinny_kernel (16-row column tiles, K split over
-// the waves, one buffer->LDS ring per wave).  In between:
-// gemm_q8_0_bf16_kernel, where a workgroup of 4 waves owns a BM x BN tile of
-// Y; the waves split it WM x WN and, when WK > 1, also split each K stage
-// (the partial tiles are summed through LDS at the end).  Each stage moves
+// Kernels.  M > 32: gemm_q8_0_bf16_ring_kernel (128 x 64 workgroup tiles
+// fed by buffer->LDS loads, described below; when the tiles cover less than
+// half the CUs, as for M <= 256 at N = 4096, each tile's K range is split
+// over up to 8 workgroups whose partial tiles gemm_splitk_reduce_kernel sums
+// in split order, so the result does not depend on timing;
+// gemm_q8_0_bf16_big_kernel, the register-pipelined version of the same
+// tiling, remains selectable).  M <= 32: gemm_q8_0_bf16_skinny_kernel
+// (16-row column tiles, K split over the waves, one buffer->LDS ring per
+// wave).  Other shapes and the sweep variants: gemm_q8_0_bf16_kernel, where
+// a workgroup of 4 waves owns a BM x BN tile of Y; the waves split it WM x WN
+// and, when WK > 1, also split each K stage (the partial tiles are summed
+// through LDS at the end).  Each stage moves
 // KB = 64 * WK columns of X (bf16) and W (Q8_0 block pairs, 68 aligned bytes,
 // realigned and widened to bf16 once per workgroup) into double-buffered LDS;
 // one barrier per stage.
@@ -566,7 +570,8 @@ __global__ __launch_bounds__(512) void gemm_q8_0_bf16_ring_kernel(const uint8_t 
                                                                   int64_t row_bytes,
                                                                   const uint16_t *__restrict__ X,
                                                                   float *__restrict__ Y, int M,
-                                                                  int N, int K) {
+                                                                  int N, int K, int S,
+                                                                  float *__restrict__ partials) {
     constexpr int NS = kRgSlots;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kRgLds];
     const int tid = threadIdx.x;
@@ -578,26 +583,32 @@ __global__ __launch_bounds__(512) void gemm_q8_0_bf16_ring_kernel(const uint8_t 
     // that the workgroups an XCD runs at one time (the contiguous range
     // [j G/8, (j+1) G/8) when the grid divides by 8, workgroups being dealt
     // to XCDs round robin) share their X rows and W rows in that XCD's L2.
+    // With S > 1 (split-K) the S workgroups of a tile are adjacent in this
+    // order and split k takes stages [k nst, (k + 1) nst) of K, writing its
+    // partial tile to partials[k] (summed in split order by a second kernel).
     const int m_tiles = (M + kBigBM - 1) / kBigBM;
     const int n_tiles = N / kBigBN;
     const int G = (int)gridDim.x;
-    const int t = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int v = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int t = v / S, split = v - t * S;
     const int group = t / (4 * n_tiles);
     const int first_m = 4 * group;
     const int gm = m_tiles - first_m < 4 ? m_tiles - first_m : 4;
     const int local = t - group * 4 * n_tiles;
     const int mt_idx = first_m + local % gm, nt_idx = local / gm;
     const int m0 = mt_idx * kBigBM, n0 = nt_idx * kBigBN;
-    const int nst = K / 64;
+    const int nst = K / 64 / S;
+    const int s0 = split * nst;
 
-    // X rows m0.. (zeros past M), W rows n0.. (N % 64 == 0 by dispatch).
-    // Loads of stages past the last one read the following bytes of the same
-    // buffers (or zeros past their ends) into slots that are never used.
+    // X rows m0.. (zeros past M), W rows n0.. (N % 64 == 0 by dispatch), both
+    // from the split's first column.  Loads of stages past the last one read
+    // the following bytes of the same buffers (or zeros past their ends) into
+    // slots that are never used.
     const __amdgpu_buffer_rsrc_t xs = wave_buffer(
-        reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2,
-        (uint32_t)((int64_t)(M - m0 < kBigBM ? M - m0 : kBigBM) * K * 2));
-    const __amdgpu_buffer_rsrc_t ws =
-        wave_buffer(W + (int64_t)n0 * row_bytes, (uint32_t)(kBigBN * row_bytes));
+        reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2 + (int64_t)s0 * 128,
+        (uint32_t)((int64_t)(M - m0 < kBigBM ? M - m0 : kBigBM) * K * 2 - (int64_t)s0 * 128));
+    const __amdgpu_buffer_rsrc_t ws = wave_buffer(W + (int64_t)n0 * row_bytes + (int64_t)s0 * 68,
+                                                  (uint32_t)(kBigBN * row_bytes - (int64_t)s0 * 68));
 
     uint8_t *const sink = lds + NS * kRgSlot + kRgWbufs * kRgWbuf;
     const uint32_t base0 = (uint32_t)(uintptr_t)(lds_ptr)lds;
@@ -839,16 +850,33 @@ __global__ __launch_bounds__(512) void gemm_q8_0_bf16_ring_kernel(const uint8_t 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // D layout of a 16x16 tile: lane holds column lane & 15, rows 4 (lane >> 4) + v.
+    float *const out = partials != nullptr ? partials + (int64_t)split * M * N : Y;
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
         for (int nt = 0; nt < 2; nt++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = m0 + 32 * wm + 16 * mt + 4 * lk + v;
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 32 * wm + 16 * mt + 4 * lk + r;
                 const int n = n0 + 32 * wn + 16 * nt + lr;
-                if (m < M) Y[(int64_t)m * N + n] = acc[mt][nt][v];
+                if (m < M) out[(int64_t)m * N + n] = acc[mt][nt][r];
             }
+}
+
+// y = part[0] + part[1] + ... + part[S - 1], in that order (4 floats a thread).
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__restrict__ part, int S,
+                                                                 int64_t mn, float *__restrict__ y) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= mn) return;
+    float4 a = *reinterpret_cast<const float4 *>(part + i);
+    for (int k = 1; k < S; k++) {
+        const float4 b = *reinterpret_cast<const float4 *>(part + (int64_t)k * mn + i);
+        a.x += b.x;
+        a.y += b.y;
+        a.z += b.z;
+        a.w += b.w;
+    }
+    *reinterpret_cast<float4 *>(y + i) = a;
 }
 
 // ---- small-M ring kernel --------------------------------------------------------
@@ -1095,18 +1123,63 @@ hipError_t launch_tiled(const uint8_t *w, int64_t row_bytes, const uint16_t *x, 
 
 }  // namespace
 
+namespace {
+
+// Splits of K for the large-M ring kernel: enough that the workgroups cover
+// the CUs (up to 8), dividing the K stages evenly.
+int ring_splits(int M, int N, int K) {
+    const int tiles = (M + kBigBM - 1) / kBigBM * (N / kBigBN);
+    const int nst = K / 64;
+    int S = 1;
+    while (S < 8 && tiles * 2 * S <= tuning().cu_count && nst % (2 * S) == 0) S *= 2;
+    return S;
+}
+
+bool ring_applies(int M, int N, int K, int64_t row_bytes) {
+    return N % kBigBN == 0 && K % 64 == 0 && (int64_t)kBigBN * row_bytes < ((int64_t)1 << 31) &&
+           (int64_t)kBigBM * K * 2 < ((int64_t)1 << 31);
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int M, int N, int K) {
+    if (M <= 32 || N % kBigBN != 0 || K % 64 != 0) return 0;
+    const int S = ring_splits(M, N, K);
+    return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+}
+
+// The need of m peaks at multiples of the 128-row tile and is zero once the
+// tiles cover half the CUs; S tiles <= cu_count / 2 bounds it by
+// cu_count / 2 tiles of 128 x 64 floats.
+size_t gemm_workspace_max_bytes(int N, int K) {
+    size_t most = 0;
+    for (int mt = 1; gemm_workspace_bytes(128 * mt, N, K) > 0; mt++) {
+        const size_t b = gemm_workspace_bytes(128 * mt, N, K);
+        if (b > most) most = b;
+    }
+    return most;
+}
+
 hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
-                                 int M, int N, int K, hipStream_t stream) {
+                                 int M, int N, int K, hipStream_t stream, float *workspace,
+                                 size_t workspace_bytes) {
     if (M <= 0) return hipSuccess;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (row_bytes & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     const int v = tuning().gemm_variant;
-    // Large M: 128 x 64 tiles, register-pipelined (v == 2 forces it where the shape allows).
-    if (aligned && v != 1 && N % kBigBN == 0 && K % 64 == 0 && (M >= 256 || v == 2) &&
-        (int64_t)kBigBN * row_bytes < ((int64_t)1 << 31)) {
-        const unsigned grid = (unsigned)(((M + kBigBM - 1) / kBigBM) * (N / kBigBN));
+    // M > 32: 128 x 64 tiles (v == 2 forces them where the shape allows, v == 3
+    // keeps the register-pipelined LDS tiles below M = 256), split over K
+    // when the tiles alone leave CUs idle and a workspace is given.
+    if (aligned && v != 1 && ring_applies(M, N, K, row_bytes) && (M >= 256 || v == 2 || (M > 32 && v != 3))) {
+        const unsigned tiles = (unsigned)(((M + kBigBM - 1) / kBigBM) * (N / kBigBN));
+        const unsigned grid = tiles;
         const int nst = K / 64;
         const int cfg = tuning().gemm_big_config;
+        int S = ring_splits(M, N, K);
+        // The reduction moves 16-byte vectors of y and the workspace.
+        if (S > 1 && (workspace == nullptr || workspace_bytes < (size_t)S * M * N * sizeof(float) ||
+                      ((reinterpret_cast<uintptr_t>(workspace) | reinterpret_cast<uintptr_t>(y)) & 15u) != 0))
+            S = 1;
 #define GOLLEK_BIG(P, WMW, WNW)                                                                \
     hipLaunchKernelGGL((gemm_q8_0_bf16_big_kernel<P, WMW, WNW>), dim3(grid),                \
                        dim3(64 * (WMW) * (WNW)), 0, stream, w, row_bytes, x, y, M, N, K)
@@ -1116,9 +1189,15 @@ hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint
         else if (nst % 8 == 0 && cfg == 2) GOLLEK_BIG(8, 4, 2);
         else if (nst % 2 == 0 && cfg == 3) GOLLEK_BIG(2, 4, 2);
         else if (nst % 4 == 0 && cfg == 4) GOLLEK_BIG(4, 2, 2);
-        else
-            hipLaunchKernelGGL(gemm_q8_0_bf16_ring_kernel, dim3(grid), dim3(512), 0, stream, w,
-                               row_bytes, x, y, M, N, K);
+        else {
+            hipLaunchKernelGGL(gemm_q8_0_bf16_ring_kernel, dim3(tiles * S), dim3(512), 0, stream, w,
+                               row_bytes, x, y, M, N, K, S, S > 1 ? workspace : nullptr);
+            if (S > 1) {
+                const int64_t mn = (int64_t)M * N;
+                hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((mn / 4 + 255) / 256)),
+                                   dim3(256), 0, stream, workspace, S, mn, y);
+            }
+        }
 #undef GOLLEK_BIG
         return hipGetLastError();
     }

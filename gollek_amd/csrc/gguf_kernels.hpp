@@ -46,8 +46,15 @@ hipError_t launch_gemv_q4k_dot4(const uint8_t *w, int64_t row_bytes, int64_t col
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
 // Y[M, N] = X[M, K] (bf16 bits) . W[N, K]^T for Q8_0 W (gguf_gemm.hip).
+// Shapes whose output tiles leave CUs idle are split over K into partial
+// tiles in `workspace` (device memory of gemm_workspace_bytes(M, N, K)
+// bytes; without it they run unsplit) and summed in split order.
+size_t gemm_workspace_bytes(int M, int N, int K);
+// The largest gemm_workspace_bytes(M, N, K) over every M.
+size_t gemm_workspace_max_bytes(int N, int K);
 hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
-                                 int M, int N, int K, hipStream_t stream);
+                                 int M, int N, int K, hipStream_t stream, float *workspace = nullptr,
+                                 size_t workspace_bytes = 0);
 
 // Workspace layout of the grouped MoE FFN (byte offsets; gguf_moe.hip).
 struct MoeLayout {

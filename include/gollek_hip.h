@@ -180,6 +180,11 @@ int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *weight, int64_t row
 int32_t gollek_hip_matvec_device(gollek_hip_weight *weight, const float *x, float *y,
                                  int64_t row_count, void *stream, char *err, size_t err_len);
 
+/* Shapes whose output tiles leave CUs idle (m = 33..256 for 4096 rows) are
+ * split over K into partial tiles held in a workspace of the handle,
+ * allocated at the first such call (at most 4 MiB) and freed with the
+ * handle; splitting calls on one handle share it and must not overlap (calls
+ * on different handles may).  A y that is not 16-byte aligned runs unsplit. */
 int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t m,
                                     float *y, void *stream, char *err, size_t err_len);
 

@@ -118,6 +118,22 @@ def test_gemm_small_m_ring_shapes(rows, cols, m):
     t.close()
 
 
+@pytest.mark.parametrize("rows,cols,m", [(256, 256, 40), (512, 1024, 33), (64, 2048, 200), (64, 1024, 384),
+                                          (128, 192, 100), (1024, 4096, 256)])
+def test_gemm_split_k_shapes(rows, cols, m):
+    # The 128 x 64 tiles split over K when they leave CUs idle: one stage a
+    # split (256 x 256), eight splits (N = 64, 512), a partial M tile, an odd
+    # stage count that cannot split (K = 192), and two M tiles split in two.
+    print(f"[gpu] gemm split-k rows={rows} cols={cols} m={m}", flush=True)
+    data = syn.q8_0_matrix(rows, cols, seed=rows + 5 * cols + m)
+    t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=m + 21)
+    y = np.full((m, rows), np.nan, np.float32)
+    ops.gemm_bf16(t, x, y)
+    assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
+    t.close()
+
+
 def test_gemm_rejects_other_types_and_short_buffers():
     data = syn.q4_k_matrix(16, 256, seed=1)
     t = ops.GgufTensor("w", (256, 16), syn.Q4_K, data.reshape(-1))
@@ -146,3 +162,30 @@ def test_gemm_device_entry_matches_host(q8_4096):
     torch.cuda.synchronize()
     assert np.array_equal(y_dev.cpu().numpy(), yh)
     dw.close()
+
+
+@pytest.mark.parametrize("m", [64, 384, 40])
+def test_gemm_device_entry_split_k_workspace(m):
+    # The device entry's workspace is sized at the first call that splits for
+    # every later m of the handle (m = 384 needs more than m = 64 here); a
+    # y that is not 16-byte aligned runs unsplit.
+    import torch
+    rows, cols = 64, 1024
+    data = syn.q8_0_matrix(rows, cols, seed=31)
+    w_dev = torch.from_numpy(data.reshape(-1)).cuda()
+    dw = ops.DeviceWeight(syn.Q8_0, w_dev.data_ptr(), rows, cols)
+    try:
+        for mm in (m, 384, 64):
+            print(f"[gpu] gemm device split-k m={mm}", flush=True)
+            x = syn.activation_bf16(mm, cols, seed=mm)
+            ref = o.gemm_reference(syn.Q8_0, data, cols, x)
+            x_dev = torch.from_numpy(x.view(np.int16)).cuda()
+            y_dev = torch.full((mm * rows + 1,), float("nan"), dtype=torch.float32, device="cuda")
+            for off in (0, 1):
+                y_view = y_dev[off:off + mm * rows]
+                dw.gemm_bf16(x_dev.data_ptr(), mm, y_view.data_ptr(), torch.cuda.current_stream().cuda_stream)
+                torch.cuda.synchronize()
+                got = y_view.cpu().numpy().reshape(mm, rows)
+                assert o.rel_err(got, ref) <= GEMM_TOL
+    finally:
+        dw.close()
