@@ -357,6 +357,260 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
     }
 }
 
+// ---- K <= 4096: shared pieces of the two kernels below ----------------------
+//
+// Wave w of either kernel owns superblock w of every row it works on.  Its
+// A operands (the x digits of that superblock) are built once, in
+// registers, and each 16-row tile then costs the wave five LDS reads of the
+// 16 rows' header and quant bytes of that superblock (B lane n + 16 g:
+// bytes 8 g .. 8 g + 7 of each chunk, low nibbles then high nibbles, so A
+// row 4 h + p is zero on the other half), four MFMAs and ~90 VALU
+// instructions.
+namespace {
+
+// LDS stores through inline asm, so the compiler does not wait for every
+// buffer->LDS load in flight before them.
+__device__ __forceinline__ void lds_store_f32(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ void lds_store4(uint32_t addr, int a, int b, int c) {
+    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(i32x4{a, b, c, 0}) : "memory");
+}
+
+// The three digit planes of four elements, PLANE bytes apart.
+template <int PLANE>
+__device__ __forceinline__ void lds_store3(uint32_t addr, uint32_t w0, uint32_t w1, uint32_t w2) {
+    asm volatile(
+        "ds_write_b32 %0, %1\n\t"
+        "ds_write_b32 %0, %2 offset:%4\n\t"
+        "ds_write_b32 %0, %3 offset:%5"
+        :
+        : "v"(addr), "v"(w0), "v"(w1), "v"(w2), "n"(PLANE), "n"(2 * PLANE)
+        : "memory");
+}
+
+// LDS tables of one superblock of x: digit planes at dig + p PLANE (256
+// bytes each), the sub-block sums xs * sum X_i (8 floats), 128 x the plane
+// sums of each sub-block (8 x 16 bytes) and the scale xs.
+struct XTab {
+    uint32_t dig, sum, ps, sc;
+};
+
+// Wave-wide: turns the superblock of x whose elements 4 l .. 4 l + 3 lane l
+// holds (zeros unless `live`) into its tables.  Only this wave reads them
+// back, so no workgroup barrier is needed; the caller waits for LDS.
+template <int PLANE>
+__device__ __forceinline__ void store_x_superblock(const float4 xv, bool live, const XTab &t) {
+    const int lane = threadIdx.x & 63;
+    const float v[4] = {live ? xv.x : 0.0f, live ? xv.y : 0.0f, live ? xv.z : 0.0f, live ? xv.w : 0.0f};
+    uint32_t mb = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
+    mb = wave_max_u32(mb);  // NaN and inf order above every finite |x|
+    const bool finite = mb < 0x7F800000u;
+    int e = 0;
+    (void)frexpf(__uint_as_float(mb), &e);  // max |x| < 2^e
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+    int sx = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int X = finite ? (int)ldexpf(v[k], 22 - e) : 0;
+        const int c = (int)(int8_t)(X & 0xFF);
+        const int X1 = (X - c) >> 8;
+        const int b = (int)(int8_t)(X1 & 0xFF);
+        const int a = (X1 - b) >> 8;
+        w0 |= ((uint32_t)c & 0xFFu) << (8 * k);
+        w1 |= ((uint32_t)b & 0xFFu) << (8 * k);
+        w2 |= ((uint32_t)a & 0xFFu) << (8 * k);
+        sx += X;
+    }
+    sx = sum8_i(sx);
+    // 128 x (sum of each digit plane over the sub-block): the MFMA's C input
+    // for the high-nibble half (see the B operand in q4k_tile_parts)
+    int ps0 = 0, ps1 = 0, ps2 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        ps0 += (int)(int8_t)(w0 >> (8 * k));
+        ps1 += (int)(int8_t)(w1 >> (8 * k));
+        ps2 += (int)(int8_t)(w2 >> (8 * k));
+    }
+    ps0 = sum8_i(ps0);
+    ps1 = sum8_i(ps1);
+    ps2 = sum8_i(ps2);
+    const float scale = !live ? 0.0f : finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
+    lds_store3<PLANE>(t.dig + 4 * lane, w0, w1, w2);
+    if ((lane & 7) == 0) {
+        lds_store_f32(t.sum + 4 * (lane >> 3), (float)sx * scale);
+        lds_store4(t.ps + 16 * (lane >> 3), 128 * ps0, 128 * ps1, 128 * ps2);
+    }
+    if (lane == 0) lds_store_f32(t.sc, scale);
+}
+
+// A wave's x operands: A and C per 64-column chunk c, the sub-block sums of
+// sub-blocks 2 c + h (h = (lane >> 4) & 1) and the scale.
+struct XOps {
+    i32x4 A[4], C[4];
+    float xs4[4], xs;
+};
+
+// Reads the tables written by store_x_superblock (after the LDS wait) into
+// the operand layout; `live` zeroes A for a wave without a superblock.
+template <int PLANE>
+__device__ __forceinline__ void read_x_operands(const XTab &t, bool live, XOps &o) {
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = m >> 2;
+    const int h = (lane >> 4) & 1;
+    // Digits of elements 64 c + 8 g .. + 7 (sub-block 2 c) and + 32 (2 c + 1).
+    uint2 dl[4], dh[4];
+    i32x4 cc[4];  // 128 x plane sums of sub-blocks 2 c + 1
+    asm volatile(
+        "ds_read_b128 %0, %4 offset:16\n\t"
+        "ds_read_b128 %1, %4 offset:48\n\t"
+        "ds_read_b128 %2, %4 offset:80\n\t"
+        "ds_read_b128 %3, %4 offset:112\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(cc[0]), "=&v"(cc[1]), "=&v"(cc[2]), "=&v"(cc[3])
+        : "v"(t.ps)
+        : "memory");
+    asm volatile(
+        "ds_read_b64 %0, %13\n\t"
+        "ds_read_b64 %1, %13 offset:64\n\t"
+        "ds_read_b64 %2, %13 offset:128\n\t"
+        "ds_read_b64 %3, %13 offset:192\n\t"
+        "ds_read_b64 %4, %13 offset:32\n\t"
+        "ds_read_b64 %5, %13 offset:96\n\t"
+        "ds_read_b64 %6, %13 offset:160\n\t"
+        "ds_read_b64 %7, %13 offset:224\n\t"
+        "ds_read_b32 %8, %14\n\t"
+        "ds_read_b32 %9, %14 offset:8\n\t"
+        "ds_read_b32 %10, %14 offset:16\n\t"
+        "ds_read_b32 %11, %14 offset:24\n\t"
+        "ds_read_b32 %12, %15\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
+          "=&v"(dh[2]), "=&v"(dh[3]), "=&v"(o.xs4[0]), "=&v"(o.xs4[1]), "=&v"(o.xs4[2]),
+          "=&v"(o.xs4[3]), "=&v"(o.xs)
+        : "v"(t.dig + p * PLANE + 8 * g), "v"(t.sum + 4 * h), "v"(t.sc)
+        : "memory");
+    const bool alive = live && p < 3;
+    const bool hl = lane >= 16 && lane < 32;  // output lanes of the high-nibble half
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        o.A[c] = i32x4{alive && ha == 0 ? (int)dl[c].x : 0, alive && ha == 0 ? (int)dl[c].y : 0,
+                       alive && ha == 1 ? (int)dh[c].x : 0, alive && ha == 1 ? (int)dh[c].y : 0};
+        o.C[c] = i32x4{hl ? cc[c].x : 0, hl ? cc[c].y : 0, hl ? cc[c].z : 0, 0};
+    }
+}
+
+// Reads the 16 rows' header (a_hdr = row n's superblock) and quant bytes
+// (a_q = a_hdr + 16 + 8 g) of one tile.
+__device__ __forceinline__ void read_tile_superblock(uint32_t a_hdr, uint32_t a_q, u32x4 &hv,
+                                                     uint2 (&q)[4]) {
+    asm volatile(
+        "ds_read_b128 %0, %5\n\t"
+        "ds_read_b64 %1, %6\n\t"
+        "ds_read_b64 %2, %6 offset:32\n\t"
+        "ds_read_b64 %3, %6 offset:64\n\t"
+        "ds_read_b64 %4, %6 offset:96\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(hv), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+        : "v"(a_hdr), "v"(a_q)
+        : "memory");
+}
+
+// One superblock of a 16-row tile before its scales are applied: per chunk
+// c the exact integer sum S[c] = sum q X over sub-block 2 c + h of row n
+// (lane n + 16 h, h = 0, 1; lanes 32..63 hold values of the zero A rows,
+// which callers drop), the superblock's d and dmin, and the 6-bit scale and
+// min codes of this lane's sub-blocks h, 2 + h, 4 + h, 6 + h.
+struct TileParts {
+    int S[4];
+    float d, dmin, scf[4], mnf[4];
+};
+
+__device__ __forceinline__ void q4k_tile_parts(const u32x4 hv, const uint2 (&q)[4], const XOps &o,
+                                               TileParts &t) {
+    const int lane = threadIdx.x & 63;
+    const int h = (lane >> 4) & 1;
+    // Plane combine of output lane n + 16 h: D_p / 16^h weighted by 256^p.
+    const int sh0 = 4 * h, sh1 = 8 - 4 * h, sh2 = 16 - 4 * h;
+    // B: low nibbles q as they are; high nibbles in place as the signed
+    // byte 16 (q - 8) (one v_bitop3 each), whose -128 sum(digits) the C
+    // input cancels, so the high half's D is 16 sum q digit.  The four
+    // products are independent: all of them are issued before the first
+    // result is used.
+    i32x4 D[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const i32x4 B = {(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
+                         (int)((q[c].x ^ 0x80808080u) & 0xF0F0F0F0u),
+                         (int)((q[c].y ^ 0x80808080u) & 0xF0F0F0F0u)};
+        D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, o.C[c], 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        t.S[c] = (int)(((uint32_t)D[c][2] << sh2) + (((uint32_t)D[c][1] << sh1) + (uint32_t)(D[c][0] >> sh0)));
+    t.d = half_bits_to_float_fast(hv.x);
+    t.dmin = half_bits_to_float_fast(hv.x >> 16);
+    // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h
+    // (bytes 0 and 2 of sc03 / mn03) and 4 + h, 6 + h (of sc47 / mn47)
+    const uint32_t hy = hv.y >> (8 * h), hz = hv.z >> (8 * h), hw = hv.w >> (8 * h);
+    const uint32_t sc03 = hy & 0x003F003Fu;
+    const uint32_t mn03 = hz & 0x003F003Fu;
+    const uint32_t sc47 = (hw & 0x000F000Fu) | ((hy >> 2) & 0x00300030u);
+    const uint32_t mn47 = ((hw >> 4) & 0x000F000Fu) | ((hz >> 2) & 0x00300030u);
+    t.scf[0] = (float)(sc03 & 0xFFu);
+    t.scf[1] = (float)((sc03 >> 16) & 0xFFu);
+    t.scf[2] = (float)(sc47 & 0xFFu);
+    t.scf[3] = (float)((sc47 >> 16) & 0xFFu);
+    t.mnf[0] = (float)(mn03 & 0xFFu);
+    t.mnf[1] = (float)((mn03 >> 16) & 0xFFu);
+    t.mnf[2] = (float)(mn47 & 0xFFu);
+    t.mnf[3] = (float)((mn47 >> 16) & 0xFFu);
+}
+
+__device__ __forceinline__ bool tile_scales_finite(const TileParts &t) {
+    return __builtin_isfinite(t.d) && __builtin_isfinite(t.dmin);
+}
+
+// This lane's share of its row, for finite d and dmin: d xs sum_c sc S -
+// dmin sum_c m X_c.
+__device__ __forceinline__ float tile_value_finite(const TileParts &t, const XOps &o) {
+    float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        qs = fmaf(t.scf[c], (float)t.S[c], qs);
+        mm = fmaf(t.mnf[c], o.xs4[c], mm);
+    }
+    return fmaf(t.d * o.xs, qs, -(t.dmin * mm));
+}
+
+// The same with the reference's products, for any d and dmin: (d sc) per
+// sub-block, and zero min codes skipped even for a NaN or infinite dmin
+// (minContribution, RT/GgufKQuantLayout.java:67-69).
+__device__ __forceinline__ float tile_value_exact(const TileParts &t, const XOps &o) {
+    float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        qs = fmaf(t.d * t.scf[c], o.xs * (float)t.S[c], qs);
+        mm = fmaf(t.mnf[c] != 0.0f ? t.dmin * t.mnf[c] : 0.0f, o.xs4[c], mm);
+    }
+    return qs - mm;
+}
+
+// One superblock of a 16-row tile: lane n + 16 h (h = 0, 1) returns the
+// share of sub-blocks h, 2 + h, 4 + h, 6 + h of row n (lanes 32..63 return
+// values of the zero A rows, which callers drop).
+__device__ __forceinline__ float q4k_tile_superblock(const u32x4 hv, const uint2 (&q)[4],
+                                                     const XOps &o) {
+    TileParts t;
+    q4k_tile_parts(hv, q, o, t);
+    return tile_scales_finite(t) ? tile_value_finite(t, o) : tile_value_exact(t, o);
+}
+
+}  // namespace
+
 // ---- K <= 4096: whole 16-row tiles shared by the workgroup -------------
 //
 // A 16-row tile of a matrix with at most 16 superblocks per row is one
@@ -364,12 +618,8 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
 // tiles into a shared ring of NSLOT slots (rows at a 2320-byte pitch, so the
 // 16 rows' reads of one superblock fall on distinct banks); every wave issues
 // an equal share of a tile's 1 KB loads and one barrier per tile publishes
-// it.  Wave w owns superblock w of every tile: its A operands are built once,
-// in registers, and per tile it reads the 16 rows' header and quant bytes of
-// that superblock (B lane n + 16 g: bytes 8 g .. 8 g + 7 of each chunk, low
-// nibbles then high nibbles, so A row 4 h + p is zero on the other half).
-// Per-wave row sums meet in LDS and one wave per tile adds them in superblock
-// order.
+// it.  Per-wave row sums meet in LDS and one wave per tile adds them in
+// superblock order.
 namespace {
 
 constexpr int kT2Waves = 16;
@@ -383,28 +633,6 @@ constexpr int kT2Slot = kT2Dma * 1024;
 constexpr int kT2MaxRows = 1024;                                // rows per workgroup
 constexpr int kT2K = 16 * kQK;                                  // x elements held
 
-// LDS stores into the ring array outside the ring loads' slots, through
-// inline asm so the compiler does not wait for every buffer->LDS load first.
-__device__ __forceinline__ void lds_store_f32(uint32_t addr, float v) {
-    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-
-
-__device__ __forceinline__ void lds_store4(uint32_t addr, int a, int b, int c) {
-    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(i32x4{a, b, c, 0}) : "memory");
-}
-
-// Plane stores of the x digits through inline asm (see store_x_records).
-__device__ __forceinline__ void lds_store3(uint32_t addr, uint32_t w0, uint32_t w1, uint32_t w2) {
-    asm volatile(
-        "ds_write_b32 %0, %1\n\t"
-        "ds_write_b32 %0, %2 offset:4096\n\t"
-        "ds_write_b32 %0, %3 offset:8192"
-        :
-        : "v"(addr), "v"(w0), "v"(w1), "v"(w2)
-        : "memory");
-}
-
 }  // namespace
 
 template <int NSLOT>
@@ -417,9 +645,9 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     __shared__ float part[2][kT2Waves][32];  // [tile & 1][wave][lane]
     __shared__ float yout[kT2MaxRows];
     // The x tables (digit planes, sub-block sums [superblock][sub-block],
-    // superblock scales) live in the last ring slot, which the loop first
-    // refills after every wave has read them.  They are accessed with inline
-    // asm like the ring itself.
+    // superblock scales, plane sums) live in the last ring slot, which the
+    // loop first refills after every wave has read them.  They are accessed
+    // with inline asm like the ring itself.
     const uint32_t xdig = (uint32_t)(uintptr_t)(lds_ptr)(ring + (NSLOT - 1) * kT2Slot);
     const uint32_t xsum = xdig + 3 * kT2K;
     const uint32_t xsc = xsum + 16 * 8 * 4;
@@ -464,112 +692,20 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     load_x_parts<kT2Threads, 1>(xp, x, nsb * 8);
     __builtin_amdgcn_sched_barrier(0);
     issue(0, 0);
-    {
-        // Wave s turns superblock s of x into digits; only this wave reads
-        // them back (so no workgroup barrier here).
-        const int sb = wv;
-        const bool live = sb < nsb;
-        const float v[4] = {live ? xp.v[0].x : 0.0f, live ? xp.v[0].y : 0.0f, live ? xp.v[0].z : 0.0f,
-                            live ? xp.v[0].w : 0.0f};
-        uint32_t mb = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
-        mb = wave_max_u32(mb);
-        const bool finite = mb < 0x7F800000u;
-        int e = 0;
-        (void)frexpf(__uint_as_float(mb), &e);
-        uint32_t w0 = 0, w1 = 0, w2 = 0;
-        int sx = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int X = finite ? (int)ldexpf(v[k], 22 - e) : 0;
-            const int c = (int)(int8_t)(X & 0xFF);
-            const int X1 = (X - c) >> 8;
-            const int b = (int)(int8_t)(X1 & 0xFF);
-            const int a = (X1 - b) >> 8;
-            w0 |= ((uint32_t)c & 0xFFu) << (8 * k);
-            w1 |= ((uint32_t)b & 0xFFu) << (8 * k);
-            w2 |= ((uint32_t)a & 0xFFu) << (8 * k);
-            sx += X;
-        }
-        sx = sum8_i(sx);
-        // 128 x (sum of each digit plane over the sub-block): the MFMA's C
-        // input for the high-nibble half (see the B operand below)
-        int ps0 = 0, ps1 = 0, ps2 = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            ps0 += (int)(int8_t)(w0 >> (8 * k));
-            ps1 += (int)(int8_t)(w1 >> (8 * k));
-            ps2 += (int)(int8_t)(w2 >> (8 * k));
-        }
-        ps0 = sum8_i(ps0);
-        ps1 = sum8_i(ps1);
-        ps2 = sum8_i(ps2);
-        const float scale = !live ? 0.0f : finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
-        lds_store3(xdig + sb * kQK + 4 * lane, w0, w1, w2);
-        if ((lane & 7) == 0) {
-            lds_store_f32(xsum + 4 * (sb * 8 + (lane >> 3)), (float)sx * scale);
-            lds_store4(xps + 16 * (sb * 8 + (lane >> 3)), 128 * ps0, 128 * ps1, 128 * ps2);
-        }
-        if (lane == 0) lds_store_f32(xsc + 4 * sb, scale);
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-    // A operands of this wave's superblock (row m = 4 h + p of lane m + 16 g).
+    // Wave s owns superblock s (the tables hold all 16, so every wave writes
+    // its own, zeros past nsb).
     const int sb = wv;
     const bool active = sb < nsb;  // wave-uniform
-    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = m >> 2;
-    // Output lane n + 16 h holds sub-blocks 2 c + h of row n.
-    const int n = lane & 15, h = (lane >> 4) & 1;
-    // Digits of elements 64 c + 8 g .. + 7 (sub-block 2 c) and + 32 (2 c + 1),
-    // the sub-block sums of sub-blocks 2 c + h and the scale, in one batch.
-    uint2 dl[4], dh[4];
-    float xs4[4], xs;
-    i32x4 cc[4];  // 128 x plane sums of sub-blocks 2 c + 1
-    asm volatile(
-        "ds_read_b128 %0, %4 offset:16\n\t"
-        "ds_read_b128 %1, %4 offset:48\n\t"
-        "ds_read_b128 %2, %4 offset:80\n\t"
-        "ds_read_b128 %3, %4 offset:112\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(cc[0]), "=&v"(cc[1]), "=&v"(cc[2]), "=&v"(cc[3])
-        : "v"(xps + 128 * (active ? sb : 0))
-        : "memory");
-    asm volatile(
-        "ds_read_b64 %0, %13\n\t"
-        "ds_read_b64 %1, %13 offset:64\n\t"
-        "ds_read_b64 %2, %13 offset:128\n\t"
-        "ds_read_b64 %3, %13 offset:192\n\t"
-        "ds_read_b64 %4, %13 offset:32\n\t"
-        "ds_read_b64 %5, %13 offset:96\n\t"
-        "ds_read_b64 %6, %13 offset:160\n\t"
-        "ds_read_b64 %7, %13 offset:224\n\t"
-        "ds_read_b32 %8, %14\n\t"
-        "ds_read_b32 %9, %14 offset:8\n\t"
-        "ds_read_b32 %10, %14 offset:16\n\t"
-        "ds_read_b32 %11, %14 offset:24\n\t"
-        "ds_read_b32 %12, %15\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
-          "=&v"(dh[2]), "=&v"(dh[3]), "=&v"(xs4[0]), "=&v"(xs4[1]), "=&v"(xs4[2]), "=&v"(xs4[3]),
-          "=&v"(xs)
-        : "v"(xdig + p * kT2K + (active ? sb : 0) * kQK + 8 * g),
-          "v"(xsum + 4 * ((active ? sb : 0) * 8 + h)), "v"(xsc + 4 * (active ? sb : 0))
-        : "memory");
+    const XTab xt = {xdig + (uint32_t)(sb * kQK), xsum + (uint32_t)(32 * sb), xps + (uint32_t)(128 * sb),
+                     xsc + (uint32_t)(4 * sb)};
+    store_x_superblock<kT2K>(xp.v[0], active, xt);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    XOps xo;
+    read_x_operands<kT2K>(xt, active, xo);
 #pragma unroll
     for (int j = 1; j < NSLOT - 1; j++) issue(j, j);
-    const bool alive = active && p < 3;
-    i32x4 A[4], C[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        A[c] = i32x4{alive && ha == 0 ? (int)dl[c].x : 0, alive && ha == 0 ? (int)dl[c].y : 0,
-                     alive && ha == 1 ? (int)dh[c].x : 0, alive && ha == 1 ? (int)dh[c].y : 0};
-        const bool hl = lane >= 16 && lane < 32;  // output lanes of the high-nibble half
-        C[c] = i32x4{hl ? cc[c].x : 0, hl ? cc[c].y : 0, hl ? cc[c].z : 0, 0};
-    }
-    // Plane combine of output lane n + 16 h: D_p / 16^h weighted by 256^p.
-    const int sh0 = 4 * h, sh1 = 8 - 4 * h, sh2 = 16 - 4 * h;
 
+    const int n = lane & 15, g = lane >> 4;
     const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
     const uint32_t a_h0 = ring_base + n * kT2Pitch + sb * kQKBlockBytes;
     const uint32_t a_q0 = a_h0 + 16 + 8 * g;
@@ -591,62 +727,8 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
             u32x4 hv;
             uint2 q[4];
             const uint32_t off = (uint32_t)slot * kT2Slot;
-            asm volatile(
-                "ds_read_b128 %0, %5\n\t"
-                "ds_read_b64 %1, %6\n\t"
-                "ds_read_b64 %2, %6 offset:32\n\t"
-                "ds_read_b64 %3, %6 offset:64\n\t"
-                "ds_read_b64 %4, %6 offset:96\n\t"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(hv), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
-                : "v"(a_h0 + off), "v"(a_q0 + off)
-                : "memory");
-            // B: low nibbles q as they are; high nibbles in place as the signed
-            // byte 16 (q - 8) (one v_bitop3 each), whose -128 sum(digits) the
-            // C input cancels, so the high half's D is 16 sum q digit.
-            int S[4];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const i32x4 B = {(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
-                                 (int)((q[c].x ^ 0x80808080u) & 0xF0F0F0F0u),
-                                 (int)((q[c].y ^ 0x80808080u) & 0xF0F0F0F0u)};
-                const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[c], B, C[c], 0, 0, 0);
-                S[c] = (D[0] >> sh0) + (int)(((uint32_t)D[1] << sh1) + ((uint32_t)D[2] << sh2));
-            }
-            const float d = half_bits_to_float_fast(hv.x);
-            const float dmin = half_bits_to_float_fast(hv.x >> 16);
-            // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h
-            // (bytes 0 and 2 of sc03 / mn03) and 4 + h, 6 + h (of sc47 / mn47)
-            const uint32_t hy = hv.y >> (8 * h), hz = hv.z >> (8 * h), hw = hv.w >> (8 * h);
-            const uint32_t sc03 = hy & 0x003F003Fu;
-            const uint32_t mn03 = hz & 0x003F003Fu;
-            const uint32_t sc47 = (hw & 0x000F000Fu) | ((hy >> 2) & 0x00300030u);
-            const uint32_t mn47 = ((hw >> 4) & 0x000F000Fu) | ((hz >> 2) & 0x00300030u);
-            const float scf[4] = {(float)(sc03 & 0xFFu), (float)((sc03 >> 16) & 0xFFu),
-                                  (float)(sc47 & 0xFFu), (float)((sc47 >> 16) & 0xFFu)};
-            const float mnf[4] = {(float)(mn03 & 0xFFu), (float)((mn03 >> 16) & 0xFFu),
-                                  (float)(mn47 & 0xFFu), (float)((mn47 >> 16) & 0xFFu)};
-            float v;
-            if (__builtin_isfinite(d) && __builtin_isfinite(dmin)) {
-                float qs = 0.0f, mm = 0.0f;
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    qs = fmaf(scf[c], (float)S[c], qs);
-                    mm = fmaf(mnf[c], xs4[c], mm);
-                }
-                v = fmaf(d * xs, qs, -(dmin * mm));
-            } else {
-                // The reference's products: (d sc) per sub-block, and zero min
-                // codes skipped even for a NaN or infinite dmin
-                // (minContribution, RT/GgufKQuantLayout.java:67-69).
-                float qs = 0.0f, mm = 0.0f;
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    qs = fmaf(d * scf[c], xs * (float)S[c], qs);
-                    mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4[c], mm);
-                }
-                v = qs - mm;
-            }
+            read_tile_superblock(a_h0 + off, a_q0 + off, hv, q);
+            const float v = q4k_tile_superblock(hv, q, xo);
             if (lane < 32) part[t & 1][wv][lane] = v;
         }
         slot = slot == NSLOT - 1 ? 0 : slot + 1;
@@ -661,6 +743,133 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     }
     __syncthreads();
     for (int r = threadIdx.x; r < nr; r += kT2Threads) y[r0 + r] = yout[r];
+}
+
+// ---- K <= 4096, at most 64 rows per workgroup: one column per wave ---------
+//
+// For matrices of up to 64 rows per CU (K = 4096 and 16384 rows or fewer),
+// the workgroup's whole share of the matrix fits in LDS.  Wave w moves its
+// superblock column (the 144 bytes of superblock w of each of the
+// workgroup's rows, packed at a 144-byte pitch, so 16-row tiles are 2304
+// contiguous bytes) into its own LDS region and works through the tiles as
+// its own loads complete.  No wave waits for another's data until the row
+// sums meet at the end, so the work of a tile starts as soon as that wave's
+// part of it has arrived and little is left once the stream ends.
+namespace {
+
+constexpr int kColWaves = 16;
+constexpr int kColThreads = kColWaves * 64;
+constexpr int kColMaxRows = 64;
+constexpr int kColLoads = kColMaxRows * kQKBlockBytes / 1024;  // 9: one column, all rows
+constexpr int kColW = kColLoads * 1024;
+// x tables of the wave's superblock (digit planes 768 bytes, plane sums 128,
+// sub-block sums 32, scale 4), later the wave's row sums (64 x 2 floats).
+constexpr int kColX = 1024;
+constexpr int kColRegion = kColW + kColX;
+static_assert(kColLoads * 1024 == kColMaxRows * kQKBlockBytes, "column region holds whole rows");
+
+// Waits until at most N of this wave's loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
+    const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
+    float *__restrict__ y, int64_t rows, int rows_per_wg) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * kColRegion];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kColMaxRows
+    const uint32_t row_bytes = (uint32_t)row_bytes64;
+    const uint32_t wbase = (uint32_t)(uintptr_t)(lds_ptr)(lds + wv * kColRegion);
+    const uint32_t xbase = wbase + kColW;
+
+    // Waves past nsb own no column: they load superblock 0's x and issue
+    // only masked loads (an empty descriptor), so every wave runs the same
+    // loads and barriers.
+    const bool active = wv < nsb;  // wave-uniform
+    const int sb = active ? wv : 0;
+    // Load k of a wave moves bytes 1024 k + 16 lane of its column, i.e. row
+    // b / 144, byte b % 144 of the row's superblock; rows past nr read
+    // zeros.  The descriptor starts at the column, so the last row's
+    // superblock ends at (nr - 1) row_bytes + 144 <= nr row_bytes - 144 wv.
+    const float4 xv = reinterpret_cast<const float4 *>(x)[64 * sb + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    const __amdgpu_buffer_rsrc_t rs =
+        wave_buffer(w + r0 * row_bytes64 + kQKBlockBytes * sb,
+                    active ? (uint32_t)nr * row_bytes - kQKBlockBytes * wv : 0u);
+    // Offsets of every load, computed once (out of the tile loop).
+    uint32_t off[kColLoads];
+#pragma unroll
+    for (int k = 0; k < kColLoads; k++) {
+        const uint32_t b = 1024u * k + 16u * lane;
+        const uint32_t r = b / kQKBlockBytes, col = b - r * kQKBlockBytes;
+        off[k] = r < (uint32_t)nr ? r * row_bytes + col : kMaskedOffset;
+    }
+    auto issue = [&](int k) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + wv * kColRegion + 1024 * k), 16, off[k],
+                                                 0, 0, kStreamLoad);
+    };
+    // Tile t is rows 16 t .. 16 t + 15, bytes [2304 t, 2304 (t + 1)), i.e.
+    // complete after loads 0-2, 3-4, 5-6, 7-8.  A CU returns loads in the
+    // order its waves issued them and stalls a wave's issue once a few tens
+    // are outstanding (which also stalls its work).  So a wave issues x and
+    // tile 0, then the loads of tile t + 1 only once tile t has arrived
+    // (just before working on it): after the first round the CU's queue
+    // holds every wave's tile t before any wave's tile t + 1, each wave's
+    // tiles arrive spread over the whole stream, and the last loads to
+    // arrive are one wave's last two.
+    const int tiles = (nr + kTileRows - 1) / kTileRows;
+    issue(0);
+    issue(1);
+    issue(2);
+    __builtin_amdgcn_sched_barrier(0);  // the tile loads issued before x is waited for
+    const XTab xt = {xbase, xbase + 768, xbase + 800, xbase + 928};
+    store_x_superblock<256>(xv, active, xt);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    XOps xo;
+    read_x_operands<256>(xt, active, xo);
+
+    const int n = lane & 15, g = lane >> 4;
+    const uint32_t a_h = wbase + n * kQKBlockBytes;
+    const uint32_t a_q = a_h + 16 + 8 * g;
+    auto tile = [&](auto T) {
+        constexpr int t = decltype(T)::value;
+        wait_vm<0>();
+        if constexpr (t < 3) {
+            if (t + 1 < tiles) {
+                issue(2 * t + 3);
+                issue(2 * t + 4);
+            }
+        }
+        if (active) {
+            u32x4 hv;
+            uint2 q[4];
+            read_tile_superblock(a_h + 2304 * t, a_q + 2304 * t, hv, q);
+            const float v = q4k_tile_superblock(hv, q, xo);
+            // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until
+            // the row sums (pair h of row r at float 2 r + h)
+            if (lane < 32) lds_store_f32(xbase + 8 * (16 * t + n) + 4 * g, v);
+        }
+    };
+    tile(std::integral_constant<int, 0>{});
+    if (tiles > 1) tile(std::integral_constant<int, 1>{});
+    if (tiles > 2) tile(std::integral_constant<int, 2>{});
+    if (tiles > 3) tile(std::integral_constant<int, 3>{});
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Row sums in superblock order.
+    for (int r = threadIdx.x; r < nr; r += kColThreads) {
+        float s = 0.0f;
+        for (int k = 0; k < nsb; k++) {
+            const float2 p = *reinterpret_cast<const float2 *>(lds + k * kColRegion + kColW + 8 * r);
+            s += p.x + p.y;
+        }
+        y[r0 + r] = s;
+    }
 }
 
 namespace {
@@ -714,9 +923,18 @@ bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const voi
 hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream) {
     const int nsb = (int)(cols / kQK);
+    const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+    // Up to 64 rows per CU: every workgroup's share stays in LDS, one
+    // superblock column per wave (gemv_variant 3 keeps the shared tiles).
+    const int64_t col_rows = (rows + cus - 1) / cus;
+    if (nsb <= 16 && col_rows <= kColMaxRows && tuning().gemv_variant != 3) {
+        const int64_t grid = (rows + col_rows - 1) / col_rows;
+        hipLaunchKernelGGL(gemv_q4_k_mfma_col_kernel, dim3((unsigned)grid), dim3(kColThreads), 0, stream, w,
+                           row_bytes, nsb, x, y, rows, (int)col_rows);
+        return hipGetLastError();
+    }
     if (nsb <= 16) {
         // one workgroup per CU, at most kT2MaxRows rows each, at least one tile each
-        const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
         int64_t grid = (rows + kTileRows - 1) / kTileRows;
         if (grid > cus) grid = cus;
         int64_t per = (rows + grid - 1) / grid;

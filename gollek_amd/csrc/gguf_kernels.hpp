@@ -16,7 +16,8 @@ struct LaunchTuning {
     int gemv_waves_per_cu = 8;   // target resident waves per CU
     int gemm_variant = 0;
     int gemm_big_config = 0;     // large-M GEMM: 0 buffer->LDS ring, 1..4 register-pipelined (sweeps)
-    int gemv_variant = 0;        // Q4_K: 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring
+    int gemv_variant = 0;        // Q4_K: 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring,
+                                 // 3 matrix cores with shared tiles for K <= 4096
     int moe_variant = 0;         // 0 auto (matrix cores), 1 v_dot4 expert kernels
 };
 LaunchTuning &tuning();

@@ -78,7 +78,8 @@ int32_t gollek_hip_last_status(void);
  * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
  * 0 = the matrix-core kernel (Q4_K) and the buffer->LDS ring kernels (Q8_0,
  * Q4_0) where they apply, 1 = the fp32 kernels, 2 = the v_dot4 kernel (Q4_K,
- * K <= 4096); moe_variant 1 selects the v_dot4 MoE
+ * K <= 4096), 3 = as 0 but Q4_K with K <= 4096 always on the shared-tile
+ * matrix-core kernel; moe_variant 1 selects the v_dot4 MoE
  * expert kernels instead of the matrix-core passes.  No reference
  * counterpart; the reference reads JVM properties instead
  * (RT/GgufParallelConfig.java:87-101). */

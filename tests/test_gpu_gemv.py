@@ -135,12 +135,16 @@ def test_gemv_parity(name, type_id, rows, cols):
     t.close()
 
 
-# Q4_K shapes at the edges of the matrix-core kernel's work split: one row,
+# Q4_K shapes at the edges of the matrix-core kernels' work split: one row,
 # rows around a 16-row tile, odd superblock counts (a half-empty last ring
 # stage), K-parts summed across waves (few tiles per workgroup), K = 16384
-# (the 64-superblock tables) and an uneven share of rows per workgroup.
+# (the 64-superblock tables) and an uneven share of rows per workgroup.  For
+# K <= 4096 and at most 64 rows per CU (one superblock column per wave):
+# 1..64 rows per workgroup (a partial last tile, one row in the last tile),
+# fewer superblocks than waves, and one row past the limit (shared tiles).
 Q4K_SHAPES = [(1, 256), (15, 512), (17, 768), (33, 4096), (100, 1280), (1000, 2304),
-              (4103, 4096), (64, 16384), (40, 8448), (3000, 14336)]
+              (4103, 4096), (64, 16384), (40, 8448), (3000, 14336), (14336, 4096),
+              (16384, 4096), (16385, 4096), (4096, 2048), (9000, 3840), (257, 4096)]
 
 
 @pytest.mark.parametrize("rows,cols", Q4K_SHAPES, ids=[f"{r}x{c}" for r, c in Q4K_SHAPES])
@@ -151,7 +155,7 @@ def test_q4k_gemv_kernels_agree_with_oracle(rows, cols):
     t = _tensor(syn.Q4_K, data, cols)
     ref = o.matvec_fp64(syn.Q4_K, data, cols, x)
     try:
-        for variant in (0, 2, 1):  # matrix cores, v_dot4 ring, fp32
+        for variant in (0, 3, 2, 1):  # matrix cores, shared tiles, v_dot4 ring, fp32
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
             ops.mat_vec(t, x, y)
@@ -187,7 +191,7 @@ def test_q4k_gemv_special_headers_match_java_order():
     exp = o.matvec(syn.Q4_K, data, cols, x)
     assert np.all(np.isfinite(exp[32:39])), "zero min codes must hide dmin"
     try:
-        for variant in (0, 2):
+        for variant in (0, 3, 2):
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
             ops.mat_vec(t, x, y)
