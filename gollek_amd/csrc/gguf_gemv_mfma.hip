@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
 // registers, and each 16-row tile then costs the wave five LDS reads of the
 // 16 rows' header and quant bytes of that superblock (B lane n + 16 g:
 // bytes 8 g .. 8 g + 7 of each chunk, low nibbles then high nibbles, so A
-// row 4 h + p is zero on the other half), four MFMAs and ~90 VALU
+// row 4 h + p is zero on the other half), four MFMAs and ~65 VALU
 // instructions.
 namespace {
 
@@ -372,10 +372,6 @@ namespace {
 // buffer->LDS load in flight before them.
 __device__ __forceinline__ void lds_store_f32(uint32_t addr, float v) {
     asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-
-__device__ __forceinline__ void lds_store4(uint32_t addr, int a, int b, int c) {
-    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(i32x4{a, b, c, 0}) : "memory");
 }
 
 // The three digit planes of four elements, PLANE bytes apart.
@@ -391,10 +387,9 @@ __device__ __forceinline__ void lds_store3(uint32_t addr, uint32_t w0, uint32_t 
 }
 
 // LDS tables of one superblock of x: digit planes at dig + p PLANE (256
-// bytes each), the sub-block sums xs * sum X_i (8 floats), 128 x the plane
-// sums of each sub-block (8 x 16 bytes) and the scale xs.
+// bytes each), the sub-block sums xs * sum X_i (8 floats) and the scale xs.
 struct XTab {
-    uint32_t dig, sum, ps, sc;
+    uint32_t dig, sum, sc;
 };
 
 // Wave-wide: turns the superblock of x whose elements 4 l .. 4 l + 3 lane l
@@ -426,31 +421,16 @@ __device__ __forceinline__ void store_x_superblock(const float4 xv, bool live, c
         sx += X;
     }
     sx = sum8_i(sx);
-    // 128 x (sum of each digit plane over the sub-block): the MFMA's C input
-    // for the high-nibble half (see the B operand in q4k_tile_parts)
-    int ps0 = 0, ps1 = 0, ps2 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        ps0 += (int)(int8_t)(w0 >> (8 * k));
-        ps1 += (int)(int8_t)(w1 >> (8 * k));
-        ps2 += (int)(int8_t)(w2 >> (8 * k));
-    }
-    ps0 = sum8_i(ps0);
-    ps1 = sum8_i(ps1);
-    ps2 = sum8_i(ps2);
     const float scale = !live ? 0.0f : finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
     lds_store3<PLANE>(t.dig + 4 * lane, w0, w1, w2);
-    if ((lane & 7) == 0) {
-        lds_store_f32(t.sum + 4 * (lane >> 3), (float)sx * scale);
-        lds_store4(t.ps + 16 * (lane >> 3), 128 * ps0, 128 * ps1, 128 * ps2);
-    }
+    if ((lane & 7) == 0) lds_store_f32(t.sum + 4 * (lane >> 3), (float)sx * scale);
     if (lane == 0) lds_store_f32(t.sc, scale);
 }
 
-// A wave's x operands: A and C per 64-column chunk c, the sub-block sums of
+// A wave's x operands: A per 64-column chunk c, the sub-block sums of
 // sub-blocks 2 c + h (h = (lane >> 4) & 1) and the scale.
 struct XOps {
-    i32x4 A[4], C[4];
+    i32x4 A[4];
     float xs4[4], xs;
 };
 
@@ -463,16 +443,6 @@ __device__ __forceinline__ void read_x_operands(const XTab &t, bool live, XOps &
     const int h = (lane >> 4) & 1;
     // Digits of elements 64 c + 8 g .. + 7 (sub-block 2 c) and + 32 (2 c + 1).
     uint2 dl[4], dh[4];
-    i32x4 cc[4];  // 128 x plane sums of sub-blocks 2 c + 1
-    asm volatile(
-        "ds_read_b128 %0, %4 offset:16\n\t"
-        "ds_read_b128 %1, %4 offset:48\n\t"
-        "ds_read_b128 %2, %4 offset:80\n\t"
-        "ds_read_b128 %3, %4 offset:112\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(cc[0]), "=&v"(cc[1]), "=&v"(cc[2]), "=&v"(cc[3])
-        : "v"(t.ps)
-        : "memory");
     asm volatile(
         "ds_read_b64 %0, %13\n\t"
         "ds_read_b64 %1, %13 offset:64\n\t"
@@ -494,13 +464,10 @@ __device__ __forceinline__ void read_x_operands(const XTab &t, bool live, XOps &
         : "v"(t.dig + p * PLANE + 8 * g), "v"(t.sum + 4 * h), "v"(t.sc)
         : "memory");
     const bool alive = live && p < 3;
-    const bool hl = lane >= 16 && lane < 32;  // output lanes of the high-nibble half
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
+    for (int c = 0; c < 4; c++)
         o.A[c] = i32x4{alive && ha == 0 ? (int)dl[c].x : 0, alive && ha == 0 ? (int)dl[c].y : 0,
                        alive && ha == 1 ? (int)dh[c].x : 0, alive && ha == 1 ? (int)dh[c].y : 0};
-        o.C[c] = i32x4{hl ? cc[c].x : 0, hl ? cc[c].y : 0, hl ? cc[c].z : 0, 0};
-    }
 }
 
 // Reads the 16 rows' header (a_hdr = row n's superblock) and quant bytes
@@ -533,24 +500,21 @@ __device__ __forceinline__ void q4k_tile_parts(const u32x4 hv, const uint2 (&q)[
                                                TileParts &t) {
     const int lane = threadIdx.x & 63;
     const int h = (lane >> 4) & 1;
-    // Plane combine of output lane n + 16 h: D_p / 16^h weighted by 256^p.
-    const int sh0 = 4 * h, sh1 = 8 - 4 * h, sh2 = 16 - 4 * h;
-    // B: low nibbles q as they are; high nibbles in place as the signed
-    // byte 16 (q - 8) (one v_bitop3 each), whose -128 sum(digits) the C
-    // input cancels, so the high half's D is 16 sum q digit.  The four
-    // products are independent: all of them are issued before the first
-    // result is used.
+    // B: the low nibbles q (sub-block 2 c) and the high nibbles (2 c + 1),
+    // each as a byte 0..15.  The four products are independent: all of them
+    // are issued before the first result is used.  Plane combine: D_p
+    // weighted by 256^p.
+    const i32x4 zero = {0, 0, 0, 0};
     i32x4 D[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const i32x4 B = {(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
-                         (int)((q[c].x ^ 0x80808080u) & 0xF0F0F0F0u),
-                         (int)((q[c].y ^ 0x80808080u) & 0xF0F0F0F0u)};
-        D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, o.C[c], 0, 0, 0);
+                         (int)((q[c].x >> 4) & 0x0F0F0F0Fu), (int)((q[c].y >> 4) & 0x0F0F0F0Fu)};
+        D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, zero, 0, 0, 0);
     }
 #pragma unroll
     for (int c = 0; c < 4; c++)
-        t.S[c] = (int)(((uint32_t)D[c][2] << sh2) + (((uint32_t)D[c][1] << sh1) + (uint32_t)(D[c][0] >> sh0)));
+        t.S[c] = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
     t.d = half_bits_to_float_fast(hv.x);
     t.dmin = half_bits_to_float_fast(hv.x >> 16);
     // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h
@@ -640,18 +604,17 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int64_t rows_per_wg) {
     static_assert(kT2DmaPerWave * kT2Waves >= kT2Dma, "tile loads");
-    static_assert(3 * kT2K + 16 * 8 * 4 + 16 * 4 + 16 * 8 * 16 <= kT2Slot, "x tables fit a slot");
+    static_assert(3 * kT2K + 16 * 8 * 4 + 16 * 4 <= kT2Slot, "x tables fit a slot");
     __shared__ __attribute__((aligned(16))) uint8_t ring[NSLOT * kT2Slot + 1024];  // + sink
     __shared__ float part[2][kT2Waves][32];  // [tile & 1][wave][lane]
     __shared__ float yout[kT2MaxRows];
     // The x tables (digit planes, sub-block sums [superblock][sub-block],
-    // superblock scales, plane sums) live in the last ring slot, which the
+    // superblock scales) live in the last ring slot, which the
     // loop first refills after every wave has read them.  They are accessed
     // with inline asm like the ring itself.
     const uint32_t xdig = (uint32_t)(uintptr_t)(lds_ptr)(ring + (NSLOT - 1) * kT2Slot);
     const uint32_t xsum = xdig + 3 * kT2K;
     const uint32_t xsc = xsum + 16 * 8 * 4;
-    const uint32_t xps = xsc + 16 * 4;  // [superblock][sub-block] 4 ints
 
     const uint32_t row_bytes = (uint32_t)row_bytes64;
     const int lane = threadIdx.x & 63;
@@ -696,8 +659,7 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     // its own, zeros past nsb).
     const int sb = wv;
     const bool active = sb < nsb;  // wave-uniform
-    const XTab xt = {xdig + (uint32_t)(sb * kQK), xsum + (uint32_t)(32 * sb), xps + (uint32_t)(128 * sb),
-                     xsc + (uint32_t)(4 * sb)};
+    const XTab xt = {xdig + (uint32_t)(sb * kQK), xsum + (uint32_t)(32 * sb), xsc + (uint32_t)(4 * sb)};
     store_x_superblock<kT2K>(xp.v[0], active, xt);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     XOps xo;
@@ -759,14 +721,27 @@ namespace {
 
 constexpr int kColWaves = 16;
 constexpr int kColThreads = kColWaves * 64;
-constexpr int kColMaxRows = 64;
-constexpr int kColLoads = kColMaxRows * kQKBlockBytes / 1024;  // 9: one column, all rows
-constexpr int kColW = kColLoads * 1024;
-// x tables of the wave's superblock (digit planes 768 bytes, plane sums 128,
-// sub-block sums 32, scale 4), later the wave's row sums (64 x 2 floats).
+// x tables of the wave's superblock (digit planes 768 bytes, sub-block sums
+// 32, scale 4), later the wave's row sums (2 floats a row).
 constexpr int kColX = 1024;
-constexpr int kColRegion = kColW + kColX;
-static_assert(kColLoads * 1024 == kColMaxRows * kQKBlockBytes, "column region holds whole rows");
+
+// A wave's column: NL loads of 1 KB, 64 rows at a 144-byte pitch.
+struct ColGeom {
+    static constexpr int NL = 9;
+    static constexpr int kW = NL * 1024;                    // column bytes of a wave
+    static constexpr int kRegion = kW + kColX;              // 16 regions: 160 KB
+    static constexpr int kMaxRows = kW / kQKBlockBytes;     // 64
+    static constexpr int kMaxTiles = (kMaxRows + kTileRows - 1) / kTileRows;
+    // Last load of tile t: tile t is bytes [2304 t, 2304 (t + 1)).
+    static constexpr int last_load(int t) {
+        const int e = (kTileRows * kQKBlockBytes * (t + 1) + 1023) / 1024 - 1;
+        return e < NL - 1 ? e : NL - 1;
+    }
+    // A tile's reads end inside the wave's region (rows past kMaxRows of the
+    // last tile read the x tables, and their sums are dropped).
+    static_assert(kMaxTiles * kTileRows * kQKBlockBytes <= kRegion, "last tile inside the region");
+    static_assert(2 * 4 * kMaxTiles * kTileRows <= kColX, "row sums fit the x tables");
+};
 
 // Waits until at most N of this wave's loads are outstanding.
 template <int N>
@@ -774,19 +749,26 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// One 1 KB buffer->LDS load (16 bytes a lane).
+__device__ __forceinline__ void col_load(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, off, 0, 0, kStreamLoad);
+}
+
 }  // namespace
 
 __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int rows_per_wg) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * kColRegion];
+    using G = ColGeom;
+    constexpr int NL = G::NL;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * G::kRegion];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
-    const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kColMaxRows
+    const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kMaxRows
     const uint32_t row_bytes = (uint32_t)row_bytes64;
-    const uint32_t wbase = (uint32_t)(uintptr_t)(lds_ptr)(lds + wv * kColRegion);
-    const uint32_t xbase = wbase + kColW;
+    const uint32_t wbase = (uint32_t)(uintptr_t)(lds_ptr)(lds + wv * G::kRegion);
+    const uint32_t xbase = wbase + G::kW;
 
     // Waves past nsb own no column: they load superblock 0's x and issue
     // only masked loads (an empty descriptor), so every wave runs the same
@@ -803,32 +785,26 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
         wave_buffer(w + r0 * row_bytes64 + kQKBlockBytes * sb,
                     active ? (uint32_t)nr * row_bytes - kQKBlockBytes * wv : 0u);
     // Offsets of every load, computed once (out of the tile loop).
-    uint32_t off[kColLoads];
+    uint32_t off[NL];
 #pragma unroll
-    for (int k = 0; k < kColLoads; k++) {
+    for (int k = 0; k < NL; k++) {
         const uint32_t b = 1024u * k + 16u * lane;
         const uint32_t r = b / kQKBlockBytes, col = b - r * kQKBlockBytes;
         off[k] = r < (uint32_t)nr ? r * row_bytes + col : kMaskedOffset;
     }
-    auto issue = [&](int k) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + wv * kColRegion + 1024 * k), 16, off[k],
-                                                 0, 0, kStreamLoad);
-    };
-    // Tile t is rows 16 t .. 16 t + 15, bytes [2304 t, 2304 (t + 1)), i.e.
-    // complete after loads 0-2, 3-4, 5-6, 7-8.  A CU returns loads in the
-    // order its waves issued them and stalls a wave's issue once a few tens
-    // are outstanding (which also stalls its work).  So a wave issues x and
-    // tile 0, then the loads of tile t + 1 only once tile t has arrived
-    // (just before working on it): after the first round the CU's queue
-    // holds every wave's tile t before any wave's tile t + 1, each wave's
-    // tiles arrive spread over the whole stream, and the last loads to
-    // arrive are one wave's last two.
+    auto issue = [&](int k) { col_load(rs, lds + wv * G::kRegion + 1024 * k, off[k]); };
+    // A CU returns loads in the order its waves issued them and stalls a
+    // wave's issue once a few tens are outstanding (which also stalls its
+    // work).  So a wave issues x and tile 0, then the loads of tile t + 1
+    // only once tile t has arrived (just before working on it): after the
+    // first round the CU's queue holds every wave's tile t before any wave's
+    // tile t + 1, each wave's tiles arrive spread over the whole stream, and
+    // the last loads to arrive are one wave's last two.
     const int tiles = (nr + kTileRows - 1) / kTileRows;
-    issue(0);
-    issue(1);
-    issue(2);
+#pragma unroll
+    for (int k = 0; k <= G::last_load(0); k++) issue(k);
     __builtin_amdgcn_sched_barrier(0);  // the tile loads issued before x is waited for
-    const XTab xt = {xbase, xbase + 768, xbase + 800, xbase + 928};
+    const XTab xt = {xbase, xbase + 768, xbase + 800};
     store_x_superblock<256>(xv, active, xt);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     XOps xo;
@@ -840,10 +816,10 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
     auto tile = [&](auto T) {
         constexpr int t = decltype(T)::value;
         wait_vm<0>();
-        if constexpr (t < 3) {
+        if constexpr (t + 1 < G::kMaxTiles) {
             if (t + 1 < tiles) {
-                issue(2 * t + 3);
-                issue(2 * t + 4);
+#pragma unroll
+                for (int k = G::last_load(t) + 1; k <= G::last_load(t + 1); k++) issue(k);
             }
         }
         if (active) {
@@ -857,17 +833,20 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
         }
     };
     tile(std::integral_constant<int, 0>{});
-    if (tiles > 1) tile(std::integral_constant<int, 1>{});
-    if (tiles > 2) tile(std::integral_constant<int, 2>{});
-    if (tiles > 3) tile(std::integral_constant<int, 3>{});
+    if constexpr (G::kMaxTiles > 1) if (tiles > 1) tile(std::integral_constant<int, 1>{});
+    if constexpr (G::kMaxTiles > 2) if (tiles > 2) tile(std::integral_constant<int, 2>{});
+    if constexpr (G::kMaxTiles > 3) if (tiles > 3) tile(std::integral_constant<int, 3>{});
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // Row sums in superblock order.
     for (int r = threadIdx.x; r < nr; r += kColThreads) {
+        float2 p[kColWaves];
+#pragma unroll
+        for (int k = 0; k < kColWaves; k++)
+            p[k] = k < nsb ? *reinterpret_cast<const float2 *>(lds + k * G::kRegion + G::kW + 8 * r)
+                           : make_float2(0.0f, 0.0f);
         float s = 0.0f;
-        for (int k = 0; k < nsb; k++) {
-            const float2 p = *reinterpret_cast<const float2 *>(lds + k * kColRegion + kColW + 8 * r);
-            s += p.x + p.y;
-        }
+#pragma unroll
+        for (int k = 0; k < kColWaves; k++) s += p[k].x + p[k].y;
         y[r0 + r] = s;
     }
 }
@@ -927,10 +906,9 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
     // Up to 64 rows per CU: every workgroup's share stays in LDS, one
     // superblock column per wave (gemv_variant 3 keeps the shared tiles).
     const int64_t col_rows = (rows + cus - 1) / cus;
-    if (nsb <= 16 && col_rows <= kColMaxRows && tuning().gemv_variant != 3) {
-        const int64_t grid = (rows + col_rows - 1) / col_rows;
-        hipLaunchKernelGGL(gemv_q4_k_mfma_col_kernel, dim3((unsigned)grid), dim3(kColThreads), 0, stream, w,
-                           row_bytes, nsb, x, y, rows, (int)col_rows);
+    if (nsb <= 16 && col_rows <= ColGeom::kMaxRows && tuning().gemv_variant != 3) {
+        hipLaunchKernelGGL(gemv_q4_k_mfma_col_kernel, dim3((unsigned)((rows + col_rows - 1) / col_rows)),
+                           dim3(kColThreads), 0, stream, w, row_bytes, nsb, x, y, rows, (int)col_rows);
         return hipGetLastError();
     }
     if (nsb <= 16) {

@@ -144,7 +144,8 @@ def test_gemv_parity(name, type_id, rows, cols):
 # fewer superblocks than waves, and one row past the limit (shared tiles).
 Q4K_SHAPES = [(1, 256), (15, 512), (17, 768), (33, 4096), (100, 1280), (1000, 2304),
               (4103, 4096), (64, 16384), (40, 8448), (3000, 14336), (14336, 4096),
-              (16384, 4096), (16385, 4096), (4096, 2048), (9000, 3840), (257, 4096)]
+              (16384, 4096), (16385, 4096), (4096, 2048), (9000, 3840), (257, 4096),
+              (15000, 4096), (14500, 2048)]
 
 
 @pytest.mark.parametrize("rows,cols", Q4K_SHAPES, ids=[f"{r}x{c}" for r, c in Q4K_SHAPES])
