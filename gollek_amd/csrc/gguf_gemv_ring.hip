@@ -6,8 +6,9 @@
 // nibble - 8; RT/ = runner/gguf/gollek-gguf-core/src/main/java/tech/kayys/
 // gollek/gguf/runtime/), in fp32.
 //
-// A workgroup of four waves owns 16 consecutive rows; wave w owns rows
-// 4w .. 4w + 3 and streams them in items of 16 blocks (544 bytes of each row
+// A workgroup of W waves (4..16, chosen so that large matrices get about
+// one workgroup per CU and stage x once per CU) owns 4 W consecutive rows;
+// wave w owns rows 4w .. 4w + 3 and streams them in items of 16 blocks (544 bytes of each row
 // for Q8_0, 288 for Q4_0) through a ring of NS slots of its own, so the waves
 // never wait for each other: each row's item piece is contiguous in memory
 // and lands as 16-byte chunks (4 rows x 34 or 18 chunks: three or two load
@@ -32,7 +33,8 @@ namespace gollek {
 
 namespace {
 
-constexpr int kGrRows = 16;      // rows per workgroup
+constexpr int kGrWaveRows = 4;   // rows per wave
+constexpr int kGrMaxWaves = 16;  // waves per workgroup
 constexpr int kGrIB = 16;        // blocks per item
 constexpr int kGrMaxK = 16384;   // x floats held in LDS
 
@@ -57,13 +59,13 @@ struct GrItem {
 };
 
 // Dynamic LDS: x (144 bytes per 32-float block), per-block sums of x (K / 8
-// bytes, padded to 16), then the four waves' rings.
+// bytes, padded to 16), then the waves' rings.
 constexpr int kGrXBlock = 144;
 __host__ __device__ constexpr int gr_x_bytes(int K) { return K / 32 * kGrXBlock; }
 __host__ __device__ constexpr int gr_ring_offset(int K) { return gr_x_bytes(K) + ((K / 8 + 15) & ~15); }
 template <int TYPE>
-__host__ __device__ constexpr int gr_lds_bytes(int K, int NS) {
-    return gr_ring_offset(K) + 4 * NS * GrItem<TYPE>::kSlot;
+__host__ __device__ constexpr int gr_lds_bytes(int K, int NS, int waves) {
+    return gr_ring_offset(K) + waves * NS * GrItem<TYPE>::kSlot;
 }
 
 extern __shared__ __attribute__((aligned(16))) uint8_t gr_dyn_lds[];
@@ -172,7 +174,7 @@ __device__ __forceinline__ float gr_sbyte(uint32_t w, int k) {
 }  // namespace
 
 template <int TYPE, int NS, bool NT>
-__global__ __launch_bounds__(256) void gemv_ring_kernel(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8_t *__restrict__ w,
                                                         int64_t row_bytes, int K,
                                                         const float *__restrict__ x,
                                                         float *__restrict__ y, int64_t rows) {
@@ -186,9 +188,10 @@ __global__ __launch_bounds__(256) void gemv_ring_kernel(const uint8_t *__restric
     static_assert(PIECE % 16 == 0, "item layout");
     uint8_t *const lds = gr_dyn_lds;
     const int tid = threadIdx.x;
+    const int nt = (int)blockDim.x;  // 64 x waves
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t row0 = (int64_t)blockIdx.x * kGrRows;
+    const int64_t row0 = (int64_t)blockIdx.x * (kGrWaveRows * (nt >> 6));
     const int nitems = K / (32 * IB);
 
     uint8_t *const xl = lds;
@@ -217,7 +220,8 @@ __global__ __launch_bounds__(256) void gemv_ring_kernel(const uint8_t *__restric
             gr_dma16<NT>(ws, slot + 1024 * i, wo[i] == kMaskedOffset ? kMaskedOffset : wo[i] + jo);
     };
 
-    // x: thread t takes floats 16 t' .. 16 t' + 15 for t' = t, t + 256, ...
+    // x: thread t takes floats 16 t' .. 16 t' + 15 for t' = t, t + nt, ...
+    // (at most four, as K <= 16384 and nt >= 256)
     // (half of block t' / 2), loaded to registers before the ring prologue
     // and written to the padded layout after it.
     const __amdgpu_buffer_rsrc_t xrs = wave_buffer(reinterpret_cast<const uint8_t *>(x), (uint32_t)(4 * K));
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(256) void gemv_ring_kernel(const uint8_t *__restric
     u32x4 xr[4][4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        const int tp = tid + 256 * u;
+        const int tp = tid + nt * u;
 #pragma unroll
         for (int i = 0; i < 4; i++)
             xr[u][i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, tp < xparts ? (uint32_t)(64 * tp + 16 * i) : kMaskedOffset, 0, 0);
@@ -236,7 +240,7 @@ __global__ __launch_bounds__(256) void gemv_ring_kernel(const uint8_t *__restric
     const uint32_t xl_base = (uint32_t)(uintptr_t)(lds_ptr)xl;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        const int tp = tid + 256 * u;
+        const int tp = tid + nt * u;
         if (tp < xparts) {
             const uint32_t a = xl_base + (uint32_t)(kGrXBlock * (tp >> 1) + 64 * (tp & 1));
             asm volatile(
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(256) void gemv_ring_kernel(const uint8_t *__restric
     if constexpr (TYPE == kQ4_0) {
         // Per-block sums of x (for sum (q - 8) x = sum q x - 8 sum x).
         const uint32_t xa = (uint32_t)(uintptr_t)(lds_ptr)xl;
-        for (int b = tid; b < K / 32; b += 256) {
+        for (int b = tid; b < K / 32; b += nt) {
             float xv[32];
             gr_read_x<32>(xa + (uint32_t)(kGrXBlock * b), xv);
             float s = 0.0f;
@@ -335,14 +339,23 @@ namespace {
 template <int TYPE, int NS, bool NT = true>
 hipError_t launch_ring(const uint8_t *w, int64_t row_bytes, int64_t cols, const float *x, float *y,
                        int64_t rows, hipStream_t stream) {
-    const unsigned grid = (unsigned)((rows + kGrRows - 1) / kGrRows);
-    const int lds = gr_lds_bytes<TYPE>((int)cols, NS);
+    // Waves per workgroup: enough rows that the grid is about one workgroup
+    // per CU (each workgroup stages all of x), at least four, within LDS.
+    const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+    const int lds_cap = 160 * 1024;
+    int waves = (int)((rows + kGrWaveRows * cus - 1) / (kGrWaveRows * cus));
+    if (waves < 4) waves = 4;
+    if (waves > kGrMaxWaves) waves = kGrMaxWaves;
+    while (waves > 4 && gr_lds_bytes<TYPE>((int)cols, NS, waves) > lds_cap) waves--;
+    const int64_t wg_rows = (int64_t)kGrWaveRows * waves;
+    const unsigned grid = (unsigned)((rows + wg_rows - 1) / wg_rows);
+    const int lds = gr_lds_bytes<TYPE>((int)cols, NS, waves);
     if (lds > 65536) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_ring_kernel<TYPE, NS, NT>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((gemv_ring_kernel<TYPE, NS, NT>), dim3(grid), dim3(256), (size_t)lds, stream, w,
+    hipLaunchKernelGGL((gemv_ring_kernel<TYPE, NS, NT>), dim3(grid), dim3(64 * waves), (size_t)lds, stream, w,
                        row_bytes, (int)cols, x, y, rows);
     return hipGetLastError();
 }

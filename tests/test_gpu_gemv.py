@@ -206,13 +206,15 @@ def test_q4k_gemv_special_headers_match_java_order():
     t.close()
 
 
-# Q8_0 / Q4_0 shapes at the edges of the ring kernel's split (16-row
-# workgroups of four 4-row waves, 512-column items): one row, ragged row
-# counts, a single item (fewer than the ring's slots), K = 16384 (all of x
-# in LDS) and past it (the fp32 kernels take over), the two configurations.
+# Q8_0 / Q4_0 shapes at the edges of the ring kernel's split (workgroups of
+# 4 to 16 4-row waves, 512-column items): one row, ragged row counts, a
+# single item (fewer than the ring's slots), K = 16384 (all of x in LDS) and
+# past it (the fp32 kernels take over), 11 and 16 waves per workgroup with a
+# partial last workgroup, the two configurations.
 Q80_Q40_SHAPES = [(syn.Q8_0, 1, 512), (syn.Q8_0, 15, 512), (syn.Q8_0, 17, 1536), (syn.Q8_0, 4096, 4096),
                   (syn.Q8_0, 33, 16384), (syn.Q8_0, 6, 16896), (syn.Q4_0, 1, 512), (syn.Q4_0, 7, 1024),
-                  (syn.Q4_0, 11008, 4096), (syn.Q4_0, 35, 16384)]
+                  (syn.Q4_0, 11008, 4096), (syn.Q4_0, 35, 16384), (syn.Q4_0, 11003, 4096),
+                  (syn.Q8_0, 6000, 8192), (syn.Q4_0, 40000, 2048)]
 
 
 @pytest.mark.parametrize("type_id,rows,cols", Q80_Q40_SHAPES,
