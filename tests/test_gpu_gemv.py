@@ -314,6 +314,31 @@ def test_row_count_prefix_zero_and_long_vector():
     t.close()
 
 
+@pytest.mark.parametrize("rows,cols,prefix", [(20000, 4096, 9000), (300, 4096, 1), (2000, 8192, 17),
+                                             (700, 16384, 64), (8000, 8192, 256), (30000, 8192, 300)])
+def test_q4k_row_prefix(rows, cols, prefix):
+    # A prefix of the rows runs on a different work split (or kernel) than
+    # the full matrix.  K <= 4096: 9000 rows on the column kernel, 20000 on
+    # the shared tiles; each row's sum keeps its order, so the bits agree.
+    # K > 4096: the number of K-parts follows the tiles per workgroup, and a
+    # row's parts are added in order, so a prefix on another split agrees to
+    # rounding (within the parity bar) rather than bit for bit.
+    print(f"[gpu] q4k prefix {rows}x{cols} prefix {prefix}", flush=True)
+    data = syn.q4_k_matrix(rows, cols, seed=rows + prefix)
+    t = _tensor(syn.Q4_K, data, cols)
+    x = syn.activation(cols, seed=prefix)
+    full = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, full)
+    part = np.zeros(prefix, np.float32)
+    ops.mat_vec_rows(t, x, part, prefix, True)
+    if cols <= 4096:
+        assert np.array_equal(part, full[:prefix])
+    else:
+        assert o.rel_err(part, full[:prefix]) <= 1e-4
+        assert o.rel_err(part, o.matvec_fp64(syn.Q4_K, data[:prefix], cols, x)) <= GEMV_TOL
+    t.close()
+
+
 def test_repeated_calls_are_deterministic():
     data = syn.q8_0_matrix(1000, 4096, seed=21)
     t = _tensor(syn.Q8_0, data, 4096)
