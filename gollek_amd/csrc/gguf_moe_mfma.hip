@@ -21,11 +21,14 @@
 //
 // Every used expert's weights stream from HBM once per group of four routes
 // (routing spreads 16 tokens x top-8 over 128 experts at ~1 route per
-// expert).  The workgroups split the flattened item list evenly; a wave
-// builds its digit operands from the float vectors (x for pass 0, h for
-// pass 1) whenever the route group changes, which drains the load pipeline
-// once.  Results collect in LDS and are stored at those drains and at the
-// end: on gfx9 stores share the load counter the ring waits on.
+// expert).  When the (expert, route group) units fit the grid, each unit
+// gets its own workgroups, each an even slice of it; otherwise the
+// workgroups split the flattened item list evenly.  A wave builds its digit
+// operands from the float vectors (x for pass 0, h for pass 1) at the start
+// and whenever the route group changes, which drains the load pipeline
+// once.  Results collect in LDS and are stored at those drains, when the
+// buffer fills and at the end: on gfx9 stores share the load counter the
+// ring waits on.
 #include <type_traits>
 
 #include "gguf_dot4.hpp"
@@ -44,7 +47,7 @@ constexpr int kMoMaxDma = 38;        // 1 KB loads per item slot
 constexpr int kMoDmaPerWave = (kMoMaxDma + kMoWaves - 1) / kMoWaves;
 constexpr int kMoSlot = kMoMaxDma * 1024;
 constexpr int kMoSlots = 3;
-constexpr int kMoOutCap = 2048;      // buffered results (value, index)
+constexpr int kMoOutCap = 2560;      // buffered results (value, index)
 
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
@@ -100,8 +103,22 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const int nused = used[E];
     const int32_t *items = used + E + 1 + (MODE == 1 ? E + 1 : 0);
     const int nitems = items[nused];
-    const int i_begin = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
-    const int i_end = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+    // Work split.  Every (expert, route group) unit has G.tiles_e items, in
+    // order.  With at least as many workgroups as units, unit j gets
+    // workgroups k j .. k j + k - 1 (k = grid / units) and each takes an even
+    // slice of it, so no workgroup changes route group (which costs a
+    // pipeline drain); otherwise the items are split evenly.
+    const int nunits = nitems / G.tiles_e;
+    const int kpu = nunits > 0 ? (int)gridDim.x / nunits : 0;
+    int i_begin, i_end;
+    if (kpu >= 1) {
+        const int unit = (int)blockIdx.x / kpu, sub = (int)blockIdx.x - unit * kpu;
+        i_begin = unit < nunits ? unit * G.tiles_e + sub * G.tiles_e / kpu : 0;
+        i_end = unit < nunits ? unit * G.tiles_e + (sub + 1) * G.tiles_e / kpu : 0;
+    } else {
+        i_begin = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
+        i_end = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+    }
     if (i_begin >= i_end) return;  // uniform, before any barrier
 
     const int lane = threadIdx.x & 63;

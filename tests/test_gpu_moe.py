@@ -29,8 +29,13 @@ def _experts(E, H, I, seed):
     return gate, up, down, tg, tu, td
 
 
+# The expert passes give each (expert, route group) unit its own workgroups
+# when the units fit the grid (up to tens per unit here, 3 for the 128-expert
+# layer, one at 400 tokens x top-2 over 32 experts: 210 units) and
+# split the items evenly past the grid (600 tokens: 314 units).
 @pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
-                                       (128, 2048, 768, 16, 8)])
+                                       (128, 2048, 768, 16, 8), (32, 512, 256, 400, 2),
+                                       (32, 512, 256, 600, 2)])
 def test_moe_parity(E, H, I, T, k):
     print(f"[gpu] moe E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H)
