@@ -12,10 +12,9 @@
 //     superblock w; h = silu(g) u per route and row.
 //   pass 1 (down): item = (used expert, RT = 16 / nsb 16-row tiles of its H
 //     rows, route group); wave w = (row tile w / nsb, superblock w % nsb).
-// The Q4_K contraction is the one of gguf_gemv_mfma.hip's tile kernel
-// (v_mfma_i32_16x16x64_i8 over balanced 22-bit digits of the vector, high
-// nibbles as 16 (q - 8), corrected by 8 sum(X) after the plane combine), with two
-// routes per MFMA: A rows 8 t + 4 h + p hold route t's digits, so its
+// The Q4_K contraction is the one of gguf_gemv_mfma.hip's kernels
+// (v_mfma_i32_16x16x64_i8 over balanced 22-bit digits of the vector, low and
+// high nibbles as bytes 0..15), with two routes per MFMA: A rows 8 t + 4 h + p hold route t's digits, so its
 // results sit in output lanes 32 t + 16 h + n and the second route costs no
 // extra epilogue instructions.
 //
@@ -219,15 +218,11 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
     const uint32_t a_h0 = ring_base + mat * part_off + (rtile * 16 + n) * G.pitch + sb * kQKBlockBytes;
     const uint32_t a_q0 = a_h0 + 16 + 8 * g;
-    const int sh0 = 4 * h, sh1 = 8 - 4 * h, sh2 = 16 - 4 * h;
     const i32x4 zero4 = {0, 0, 0, 0};
 
     // Operands of the current route group: A per MFMA pair and chunk; per
-    // output lane the high-nibble correction 8 sum(X) of its sub-block (the
-    // signed 16 (q - 8) bytes yield sum X (q - 8) after the / 16), the
-    // sub-block sums and the superblock scale of its route.
+    // output lane the sub-block sums and the superblock scale of its route.
     i32x4 A[2][4];
-    int CX[2][4];
     float xs4[2][4], xs[2];
     int cur_key = -1;  // e * 65536 + group of the operands held
 
@@ -242,7 +237,6 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 A[pp][c] = i32x4{0, 0, 0, 0};
-                CX[pp][c] = 0;
                 xs4[pp][c] = 0.0f;
             }
         xs[0] = xs[1] = 0.0f;
@@ -294,7 +288,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             sx = sum8_i(sx);
             const float scale = finite ? ldexpf(1.0f, ex - 22) : __builtin_nanf("");
             // scratch: planes at 0 / 256 / 512, sub-block sums (fp32) at 768 + 4 j,
-            // 8 sum X (int) at 800 + 4 j, scale at 832
+            // scale at 832
             asm volatile(
                 "ds_write_b32 %0, %1\n\t"
                 "ds_write_b32 %0, %2 offset:256\n\t"
@@ -303,12 +297,10 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 : "v"(sbase + 4 * lane), "v"(d0), "v"(d1), "v"(d2)
                 : "memory");
             if ((lane & 7) == 0)
-                asm volatile(
-                    "ds_write_b32 %0, %1 offset:768\n\t"
-                    "ds_write_b32 %0, %2 offset:800"
-                    :
-                    : "v"(sbase + 4 * (lane >> 3)), "v"(__float_as_int((float)sx * scale)), "v"(8 * sx)
-                    : "memory");
+                asm volatile("ds_write_b32 %0, %1 offset:768"
+                             :
+                             : "v"(sbase + 4 * (lane >> 3)), "v"(__float_as_int((float)sx * scale))
+                             : "memory");
             if (lane == 0)
                 asm volatile("ds_write_b32 %0, %1 offset:832" : : "v"(sbase), "v"(__float_as_int(scale)) : "memory");
             // A rows of route j: m = 8 (j & 1) + 4 ha + p in lanes m + 16 g; this
@@ -316,29 +308,24 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             const int m = lane & 15, p = m & 3, ha = (m >> 2) & 1;
             uint2 dl[4], dh[4];
             float xsv[4], sc;
-            int cxv[4];
             asm volatile(
-                "ds_read_b64 %0, %17\n\t"
-                "ds_read_b64 %1, %17 offset:64\n\t"
-                "ds_read_b64 %2, %17 offset:128\n\t"
-                "ds_read_b64 %3, %17 offset:192\n\t"
-                "ds_read_b64 %4, %17 offset:32\n\t"
-                "ds_read_b64 %5, %17 offset:96\n\t"
-                "ds_read_b64 %6, %17 offset:160\n\t"
-                "ds_read_b64 %7, %17 offset:224\n\t"
-                "ds_read_b32 %8, %18 offset:768\n\t"
-                "ds_read_b32 %9, %18 offset:776\n\t"
-                "ds_read_b32 %10, %18 offset:784\n\t"
-                "ds_read_b32 %11, %18 offset:792\n\t"
-                "ds_read_b32 %12, %19 offset:804\n\t"
-                "ds_read_b32 %13, %19 offset:812\n\t"
-                "ds_read_b32 %14, %19 offset:820\n\t"
-                "ds_read_b32 %15, %19 offset:828\n\t"
-                "ds_read_b32 %16, %19 offset:832\n\t"
+                "ds_read_b64 %0, %13\n\t"
+                "ds_read_b64 %1, %13 offset:64\n\t"
+                "ds_read_b64 %2, %13 offset:128\n\t"
+                "ds_read_b64 %3, %13 offset:192\n\t"
+                "ds_read_b64 %4, %13 offset:32\n\t"
+                "ds_read_b64 %5, %13 offset:96\n\t"
+                "ds_read_b64 %6, %13 offset:160\n\t"
+                "ds_read_b64 %7, %13 offset:224\n\t"
+                "ds_read_b32 %8, %14 offset:768\n\t"
+                "ds_read_b32 %9, %14 offset:776\n\t"
+                "ds_read_b32 %10, %14 offset:784\n\t"
+                "ds_read_b32 %11, %14 offset:792\n\t"
+                "ds_read_b32 %12, %15 offset:832\n\t"
                 "s_waitcnt lgkmcnt(0)"
                 : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
                   "=&v"(dh[2]), "=&v"(dh[3]), "=&v"(xsv[0]), "=&v"(xsv[1]), "=&v"(xsv[2]), "=&v"(xsv[3]),
-                  "=&v"(cxv[0]), "=&v"(cxv[1]), "=&v"(cxv[2]), "=&v"(cxv[3]), "=&v"(sc)
+                  "=&v"(sc)
                 : "v"(sbase + (p < 3 ? p : 0) * 256 + 8 * g), "v"(sbase + 4 * h), "v"(sbase)
                 : "memory");
             const int pp = j >> 1, tj = j & 1;
@@ -352,10 +339,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             }
             if (tq == tj) {  // output lanes of route j
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    CX[pp][c] = h == 1 ? cxv[c] : 0;
-                    xs4[pp][c] = xsv[c];
-                }
+                for (int c = 0; c < 4; c++) xs4[pp][c] = xsv[c];
                 xs[pp] = sc;
             }
         }
@@ -462,8 +446,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 #pragma unroll
             for (int c = 0; c < 4; c++)
                 B[c] = i32x4{(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
-                             (int)((q[c].x ^ 0x80808080u) & 0xF0F0F0F0u),
-                             (int)((q[c].y ^ 0x80808080u) & 0xF0F0F0F0u)};
+                             (int)((q[c].x >> 4) & 0x0F0F0F0Fu), (int)((q[c].y >> 4) & 0x0F0F0F0Fu)};
             const float d = half_bits_to_float_fast(hv.x);
             const float dmin = half_bits_to_float_fast(hv.x >> 16);
             // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h, 4 + h, 6 + h
@@ -481,12 +464,14 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 #pragma unroll
             for (int pp = 0; pp < 2; pp++) {
                 if (pp >= npairs) break;  // uniform
+                // the pair's four products first, then their plane combines
+                i32x4 D[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[pp][c], B[c], zero4, 0, 0, 0);
                 int S[4];
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[pp][c], B[c], zero4, 0, 0, 0);
-                    S[c] = (D[0] >> sh0) + (int)(((uint32_t)D[1] << sh1) + ((uint32_t)D[2] << sh2)) + CX[pp][c];
-                }
+                for (int c = 0; c < 4; c++)
+                    S[c] = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
                 float v;
                 if (fin) {
                     float qs = 0.0f, mm = 0.0f;
@@ -507,7 +492,8 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                     }
                     v = qs - mm;
                 }
-                const float other = __shfl_down(v, 16, 64);  // h = 1 half of row n
+                // h = 1 half of row n: lane n + 16 (ds_swizzle, lanes xor 16)
+                const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
                 if (h == 0) part[i & 1][2 * pp + tq][wv][n] = v + other;
             }
         }
