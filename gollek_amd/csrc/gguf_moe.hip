@@ -63,9 +63,9 @@ MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inte
 __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restrict__ ids,
                                                         const float *__restrict__ wts, int P,
                                                         int E, int tiles0, int tiles1,
-                                                        int32_t *__restrict__ meta) {
-    extern __shared__ int32_t sh[];  // cnt[E], run[E]
-    int32_t *cnt = sh, *run = sh + E;
+                                                        int32_t *__restrict__ meta, int keys_in_lds) {
+    extern __shared__ int32_t sh[];  // cnt[E], run[E], then (keys_in_lds) key[P]
+    int32_t *cnt = sh, *run = sh + E, *keys = sh + 2 * E;
     int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
     int32_t *used = pairs + P, *nused = used + E;
     int32_t *items0 = nused + 1, *items1 = items0 + E + 1;
@@ -74,7 +74,9 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restric
     __syncthreads();
     for (int p = threadIdx.x; p < P; p += blockDim.x) {
         const int e = ids[p];
-        if (e >= 0 && e < E && wts[p] != 0.0f) atomicAdd(&cnt[e], 1);  // LDS atomic
+        const bool valid = e >= 0 && e < E && wts[p] != 0.0f;
+        if (valid) atomicAdd(&cnt[e], 1);  // LDS atomic
+        if (keys_in_lds) keys[p] = valid ? e : -1;
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -125,8 +127,12 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t *__restric
             const int p = base + lane;
             int key = -1;
             if (p < P) {
-                const int e = ids[p];
-                if (e >= 0 && e < E && wts[p] != 0.0f) key = e;
+                if (keys_in_lds) {
+                    key = keys[p];
+                } else {
+                    const int e = ids[p];
+                    if (e >= 0 && e < E && wts[p] != 0.0f) key = e;
+                }
             }
             const uint32_t k1 = (uint32_t)(key + 1);
             uint64_t same = __ballot(true);
@@ -230,6 +236,10 @@ __global__ __launch_bounds__(256) void moe_expert_kernel(
 }
 
 // out[t][c] = sum_j w[t,j] * y[t*k + j][c] over valid routes, j in order.
+// Eight routes at a time: their ids and weights, then their rows (every
+// route's row is in the workspace, so an invalid route's load is in bounds
+// and its value is dropped by a select), then the sums in route order --
+// one memory round trip per eight routes instead of two per route.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *__restrict__ ids,
                                                           const float *__restrict__ wts,
                                                           const float *__restrict__ ypair, int T,
@@ -240,13 +250,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *__restr
     if (i >= (int64_t)T * H) return;
     const int t = (int)(i / H), c = (int)(i % H);
     float acc = 0.0f;
-    for (int j = 0; j < top_k; j++) {
-        const int p = t * top_k + j;
-        const int e = ids[p];
-        const float wj = wts[p];
-        if (e < 0 || e >= E || wj == 0.0f) continue;
-        const float scaled = ypair[(int64_t)p * H + c] * wj;  // AccelOps.mulScalar
-        acc = acc + scaled;                                    // addToTokenRow
+    for (int j0 = 0; j0 < top_k; j0 += 8) {
+        bool ok[8];
+        float wj[8], yv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u < top_k ? j0 + u : top_k - 1;
+            const int p = t * top_k + j;
+            const int e = ids[p];
+            wj[u] = wts[p];
+            ok[u] = j0 + u < top_k && e >= 0 && e < E && wj[u] != 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u < top_k ? j0 + u : top_k - 1;
+            yv[u] = ypair[(int64_t)(t * top_k + j) * H + c];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float scaled = yv[u] * wj[u];  // AccelOps.mulScalar
+            acc = ok[u] ? acc + scaled : acc;    // addToTokenRow
+        }
     }
     out[i] = acc;
 }
@@ -277,8 +301,12 @@ hipError_t launch_expert(int nsb, const uint8_t *w0, const uint8_t *w1, int64_t 
 
 hipError_t launch_moe_route(const int32_t *ids, const float *wts, int P, int E, int tiles0,
                             int tiles1, int32_t *meta, hipStream_t stream) {
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 2 * (size_t)E * sizeof(int32_t), stream,
-                       ids, wts, P, E, tiles0, tiles1, meta);
+    // The routes' keys stay in LDS for the scatter when they fit the default
+    // 64 KB (the scatter otherwise reloads them, one round trip per 64).
+    const size_t base = 2 * (size_t)E * sizeof(int32_t);
+    const int keys_in_lds = base + (size_t)P * sizeof(int32_t) <= 65536 ? 1 : 0;
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), base + (keys_in_lds ? (size_t)P * sizeof(int32_t) : 0),
+                       stream, ids, wts, P, E, tiles0, tiles1, meta, keys_in_lds);
     return hipGetLastError();
 }
 
