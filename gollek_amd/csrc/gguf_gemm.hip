@@ -863,18 +863,26 @@ __global__ __launch_bounds__(512) void gemm_q8_0_bf16_ring_kernel(const uint8_t 
             }
 }
 
-// y = part[0] + part[1] + ... + part[S - 1], in that order (4 floats a thread).
+// y = part[0] + part[1] + ... + part[S - 1], in that order (4 floats a
+// thread, S <= 8): every partial is loaded before the first add, so the
+// reduction costs one memory round trip.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__restrict__ part, int S,
                                                                  int64_t mn, float *__restrict__ y) {
     const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= mn) return;
-    float4 a = *reinterpret_cast<const float4 *>(part + i);
-    for (int k = 1; k < S; k++) {
-        const float4 b = *reinterpret_cast<const float4 *>(part + (int64_t)k * mn + i);
-        a.x += b.x;
-        a.y += b.y;
-        a.z += b.z;
-        a.w += b.w;
+    float4 b[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        b[k] = *reinterpret_cast<const float4 *>(part + (int64_t)(k < S ? k : 0) * mn + i);
+    float4 a = b[0];
+#pragma unroll
+    for (int k = 1; k < 8; k++) {
+        if (k < S) {
+            a.x += b[k].x;
+            a.y += b[k].y;
+            a.z += b[k].z;
+            a.w += b[k].w;
+        }
     }
     *reinterpret_cast<float4 *>(y + i) = a;
 }
