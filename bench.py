@@ -11,7 +11,8 @@ the timed launches.
 
 Secondary lines (in "extra"): the other GEMV configurations, the Q8_0 bf16
 MFMA GEMM (M = 16 / 128 / 512; TFLOP/s at M = 512 is the metric's second
-half) and the Q4_K MoE grouped FFN, each timed the same way.
+half) and the Q4_K MoE grouped FFN, each timed the same way; the GGUF file ->
+HBM upload rate (gollek_hip_gguf_upload, wall clock).
 
 cpu_baseline: the C restatement of the reference's Java raw mat-vec (oracle/)
 on this host's cores, on the same Q4_K matrix (rank 0, N = 1 only).
@@ -268,6 +269,42 @@ def host_entry_workload(host, rows: int, cols: int, steps: int, warmup: int):
             "note": "host float[] in/out per call (PCIe + sync inclusive); weights resident"}
 
 
+def gguf_upload_workload(host, rows: int, cols: int, copies: int = 8):
+    """GGUF file -> device handles (gollek_hip_gguf_upload): a file holding
+    `copies` Q4_K rows x cols tensors is written to a temporary directory,
+    opened with the native loader and every tensor uploaded.  The file was
+    just written, so its pages are in the host page cache: this is the
+    mapped-file -> pinned staging -> HBM rate, not a disk rate.  The first
+    upload (which also allocates the pinned staging buffers) is untimed."""
+    import shutil
+    import tempfile
+
+    from gollek_amd import _native
+    from gollek_amd import tensor_ops as ops
+    from gollek_amd import gguf_writer as gw
+
+    blobs = [(f"blk.{i}.ffn_up.weight", (cols, rows), 12, host.tobytes()) for i in range(copies + 1)]
+    tmp = tempfile.mkdtemp(prefix="gguf_bench_")
+    try:
+        path = os.path.join(tmp, "model.gguf")
+        with open(path, "wb") as fh:
+            fh.write(gw.gguf_file([("general.alignment", gw.U32, 32)], blobs)[0])
+        lib = _native.load()
+        with ops.GgufFile(path) as f:
+            lib.gollek_hip_weight_free(f.upload(0))
+            t0 = time.perf_counter()
+            handles = [f.upload(i) for i in range(1, copies + 1)]
+            dt = time.perf_counter() - t0
+            for h in handles:
+                lib.gollek_hip_weight_free(h)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    nbytes = host.size * copies
+    return {"tensors": copies, "bytes": nbytes, "ms_per_tensor": dt / copies * 1e3,
+            "upload_gbs": nbytes / dt / 1e9,
+            "note": "page-cache-resident GGUF file -> pinned staging -> HBM (synchronous per tensor)"}
+
+
 # ---- CPU baseline -------------------------------------------------------------
 
 def cpu_baseline(host, cols: int):
@@ -379,6 +416,9 @@ def main() -> int:
         if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e128_top8_t16"):
             log("extra moe")
             extra["moe_q4_k_e128_top8_t16"] = moe_workload(torch, args.steps, args.warmup, seed=11)
+        if _has_symbol("gollek_hip_gguf_upload") and want("gguf_upload_q4_k_4096x14336"):
+            log("extra gguf upload")
+            extra["gguf_upload_q4_k_4096x14336"] = gguf_upload_workload(host, 14336, 4096)
 
     cpu = None
     if not args.no_cpu:

@@ -54,6 +54,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                       _CHARP, _SZ]),
     "gollek_hip_moe_grouped_device": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _P, _P,
                                              _I64, _P, _CHARP, _SZ]),
+    "gollek_hip_gguf_open": (_P, [_CHARP, _CHARP, _SZ]),
+    "gollek_hip_gguf_close": (None, [_P]),
+    "gollek_hip_gguf_info": (_I32, [_P, _P, _P, _P, _P, _P, _P]),
+    "gollek_hip_gguf_tensor": (_I32, [_P, _I64, _CHARP, _SZ, _P, _P, _P, _P, _P]),
+    "gollek_hip_gguf_find": (_I64, [_P, _CHARP]),
+    "gollek_hip_gguf_upload": (_P, [_P, _I64, _CHARP, _SZ]),
 }
 
 _lock = threading.Lock()

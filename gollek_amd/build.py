@@ -22,6 +22,7 @@ OBJ_DIR = PACKAGE_DIR / "_build"
 HIP_SOURCES = (
     "gguf_capi.hip",
     "gguf_dequant.hip",
+    "gguf_file.hip",
     "gguf_gemv.hip",
     "gguf_gemv_dot4.hip",
     "gguf_gemv_mfma.hip",

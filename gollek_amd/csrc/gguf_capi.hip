@@ -594,3 +594,31 @@ int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
 }
 
 }  // extern "C"
+
+namespace gollek {
+
+void record_status(int32_t code, const char *message) {
+    g_last_status = code;
+    g_last_error = message != nullptr ? message : "";
+}
+
+gollek_hip_weight *weight_alloc_owned(int32_t type_id, int64_t rows, int64_t cols, int64_t row_bytes,
+                                      char *err, size_t err_len) {
+    gollek_hip_weight *w = make_weight(type_id, rows, cols, row_bytes, err, err_len);
+    if (w == nullptr) return nullptr;
+    const size_t bytes = (size_t)rows * (size_t)row_bytes;
+    if (bytes > 0) {
+        const hipError_t e = hipMalloc(reinterpret_cast<void **>(&w->data), bytes);
+        if (e != hipSuccess) {
+            hip_fail(e, "hipMalloc(weight)", err, err_len);
+            gollek_hip_weight_free(w);
+            return nullptr;
+        }
+    }
+    w->owned = true;
+    return w;
+}
+
+uint8_t *weight_data(gollek_hip_weight *w) { return w->data; }
+
+}  // namespace gollek

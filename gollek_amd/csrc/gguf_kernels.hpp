@@ -84,6 +84,21 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
                                int H, int I, const float *x, const int32_t *ids, const float *wts,
                                int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);
 
+}  // namespace gollek
+
+// Pieces of the C ABI (gguf_capi.hip) the GGUF file loader (gguf_file.hip) uses.
+struct gollek_hip_weight;
+namespace gollek {
+
+// Sets what gollek_hip_last_status / gollek_hip_last_error report.
+void record_status(int32_t code, const char *message);
+// A weight handle on the current device that owns an uninitialised
+// rows * row_bytes device buffer; same validation and messages as
+// gollek_hip_weight_upload.  nullptr (with the error recorded) on failure.
+gollek_hip_weight *weight_alloc_owned(int32_t type_id, int64_t rows, int64_t cols, int64_t row_bytes,
+                                      char *err, size_t err_len);
+uint8_t *weight_data(gollek_hip_weight *w);
+
 // Name of the GEMV kernel variant launch_gemv picks (for profiling notes).
 const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, const void *w,
                               const float *x);

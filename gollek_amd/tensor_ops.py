@@ -92,6 +92,9 @@ class GgufTensor:
     type_id: int
     data: np.ndarray  # uint8, rows * row_bytes
     _handle: int | None = field(default=None, repr=False)
+    # set for tensors of a GgufFile: the handle comes from the file upload
+    _file: "GgufFile | None" = field(default=None, repr=False)
+    _index: int = field(default=-1, repr=False)
 
     @property
     def columns(self) -> int:
@@ -111,6 +114,8 @@ class GgufTensor:
 
     def handle(self) -> int:
         """Device handle, created on first use (the prepared-cache analogue)."""
+        if self._handle is None and self._file is not None:
+            self._handle = self._file.upload(self._index)
         if self._handle is None:
             lib = _native.load()
             err = _native.ErrBuf()
@@ -213,6 +218,105 @@ def mat_vec_parallel(tensor: GgufTensor, vector, output: np.ndarray) -> None:
     if tensor is None:
         raise NullPointerError("tensor")
     mat_vec_rows(tensor, vector, output, tensor.rows, True)
+
+
+# ---- GGUF files -------------------------------------------------------------
+
+@dataclass(frozen=True)
+class GgufTensorInfo:
+    """GC/loader/GGUFTensorInfo.java:8-14 (GC/ = runner/gguf/gollek-gguf-core/
+    src/main/java/tech/kayys/gollek/gguf/): name, shape (shape[0] contiguous),
+    ggml type id, offset from the data start, size in bytes."""
+
+    name: str
+    shape: tuple[int, ...]
+    type_id: int
+    offset: int
+    size_in_bytes: int
+
+
+class GgufFile:
+    """A GGUF file opened through the native parser: the facts GGUFModel holds
+    (GC/loader/GGUFParser.java:17-62: version, tensor infos, data start) and a
+    device upload per tensor (GC/runtime/GgufTensorData.java:97-104's range
+    check, then the weight upload).  Metadata values other than
+    general.alignment are not kept."""
+
+    def __init__(self, path):
+        lib = _native.load()
+        err = _native.ErrBuf()
+        self.path = str(path)
+        h = lib.gollek_hip_gguf_open(self.path.encode(), err.buf, err.size)
+        if not h:
+            raise _BY_CODE.get(lib.gollek_hip_last_status(), GgufHipError)(err.text)
+        self._h = h
+        v, nt, nkv, al, ds, fb = (ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int64(),
+                                  ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64())
+        lib.gollek_hip_gguf_info(h, *(ctypes.byref(o) for o in (v, nt, nkv, al, ds, fb)))
+        self.version, self.n_kv, self.alignment = v.value, nkv.value, al.value
+        self.data_start, self.file_bytes = ds.value, fb.value
+        self.tensors: list[GgufTensorInfo] = [self._info(i) for i in range(nt.value)]
+        self._map = None
+
+    def _info(self, index: int) -> GgufTensorInfo:
+        lib = _native.load()
+        name = ctypes.create_string_buffer(4096)
+        tid, nd = ctypes.c_int32(), ctypes.c_int32()
+        dims = (ctypes.c_int64 * 8)()
+        off, size = ctypes.c_int64(), ctypes.c_int64()
+        rc = lib.gollek_hip_gguf_tensor(self._h, index, name, 4096, ctypes.byref(tid),
+                                        ctypes.byref(nd), dims, ctypes.byref(off),
+                                        ctypes.byref(size))
+        if rc != 0:
+            raise _BY_CODE.get(rc, GgufHipError)(f"tensor index {index}")
+        return GgufTensorInfo(name.value.decode("utf-8", "replace"),
+                              tuple(int(dims[d]) for d in range(nd.value)), tid.value,
+                              off.value, size.value)
+
+    def find(self, name: str) -> int:
+        """Index of the tensor called `name`, or -1."""
+        return int(_native.load().gollek_hip_gguf_find(self._h, name.encode()))
+
+    def upload(self, index: int) -> int:
+        """A new device weight handle holding tensor `index` (caller frees it)."""
+        lib = _native.load()
+        err = _native.ErrBuf()
+        h = lib.gollek_hip_gguf_upload(self._h, index, err.buf, err.size)
+        if not h:
+            raise _BY_CODE.get(lib.gollek_hip_last_status(), GgufHipError)(err.text)
+        return h
+
+    def tensor(self, name: str) -> GgufTensor:
+        """GgufTensor for `name` whose bytes are a read-only view of the file
+        (empty where they fall outside it) and whose handle comes from
+        upload()."""
+        index = self.find(name)
+        if index < 0:
+            raise IllegalArgumentError(f"Tensor not found: {name}")
+        info = self.tensors[index]
+        if self._map is None:
+            self._map = np.memmap(self.path, dtype=np.uint8, mode="r")
+        start = self.data_start + info.offset
+        data = self._map[start:start + info.size_in_bytes] if start >= 0 else self._map[:0]
+        return GgufTensor(info.name, info.shape, info.type_id, data, _file=self, _index=index)
+
+    def close(self) -> None:
+        if self._h:
+            _native.load().gollek_hip_gguf_close(self._h)
+            self._h = None
+        self._map = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # ---- device-pointer entry points (inputs already resident in HBM) ---------

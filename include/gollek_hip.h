@@ -198,6 +198,61 @@ int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight
                                       int64_t workspace_bytes, void *stream, char *err,
                                       size_t err_len);
 
+/* ---- GGUF files --------------------------------------------------------- */
+/* GC/ = runner/gguf/gollek-gguf-core/src/main/java/tech/kayys/gollek/gguf/. */
+
+/* Opaque parsed GGUF file (a read-only mapping of it plus its tensor table). */
+typedef struct gollek_hip_gguf gollek_hip_gguf;
+
+/* Maps `path` read-only and parses the header, the metadata (skipped, except
+ * general.alignment, default 32) and the tensor infos; needs no GPU.
+ * Replaces GC/loader/GGUFReader.java:28-37 (open + mmap) with
+ * GC/loader/GGUFParser.java:17-105 (parse).  Returns NULL with the status
+ * (gollek_hip_last_status) and message set: bad magic -> ARG "Not a valid
+ * GGUF file"; a metadata type outside 0..12 -> UNSUPPORTED "Unsupported GGUF
+ * KV type: N at pos P"; a tensor type without a GGUF block layout or an
+ * element count that is not a multiple of its block -> UNSUPPORTED
+ * "Unsupported or misaligned GGUF tensor type T with N element(s)"; a
+ * truncated file, a negative or oversized length or count, more than 8
+ * dimensions, a non-numeric or non-positive general.alignment -> ARG. */
+gollek_hip_gguf *gollek_hip_gguf_open(const char *path, char *err, size_t err_len);
+
+/* Unmaps the file and frees its upload buffers.  Weight handles uploaded from
+ * it stay valid.  NULL is a no-op. */
+void gollek_hip_gguf_close(gollek_hip_gguf *file);
+
+/* Header facts: format version, tensor and metadata counts, the alignment
+ * used, the absolute offset of the tensor data (GGUFModel.dataStart,
+ * GC/loader/GGUFParser.java:57-62) and the file size.  Any pointer may be NULL. */
+int32_t gollek_hip_gguf_info(const gollek_hip_gguf *file, int32_t *version, int64_t *n_tensors,
+                             int64_t *n_kv, int64_t *alignment, int64_t *data_start,
+                             int64_t *file_bytes);
+
+/* Tensor `index` in file order (GC/loader/GGUFTensorInfo.java:8-14): name
+ * (NUL-terminated, truncated to name_len - 1), ggml type id, dimension count,
+ * dims[0..7] (dims[0] = the contiguous one; unused entries 1), offset from
+ * the data start and size in bytes.  Index out of range -> ARG.  Output
+ * pointers may be NULL. */
+int32_t gollek_hip_gguf_tensor(const gollek_hip_gguf *file, int64_t index, char *name,
+                               size_t name_len, int32_t *type_id, int32_t *n_dims, int64_t *dims,
+                               int64_t *offset, int64_t *size_bytes);
+
+/* Index of the first tensor named `name` (GGUFModel.tensors lookup by name),
+ * or -1. */
+int64_t gollek_hip_gguf_find(const gollek_hip_gguf *file, const char *name);
+
+/* Copies tensor `index` to a new device weight handle on the current device
+ * (rows = product of dims[1..], cols = dims[0]), through pinned staging
+ * buffers the file object keeps.  Replaces the byte slice of
+ * GC/runtime/GgufTensorData.java:97-104 followed by gollek_hip_weight_upload:
+ * bytes outside the file -> ARG "Tensor data range is outside model segment:
+ * NAME"; then the validation of gollek_hip_weight_upload (types other than
+ * Q4_0 / Q8_0 / Q4_K -> UNSUPPORTED).  Free the handle with
+ * gollek_hip_weight_free.  Thread-safe; uploads from one file object
+ * serialise on its staging buffers. */
+gollek_hip_weight *gollek_hip_gguf_upload(gollek_hip_gguf *file, int64_t index, char *err,
+                                          size_t err_len);
+
 #ifdef __cplusplus
 }
 #endif
