@@ -30,6 +30,7 @@ HIP_SOURCES = (
     "gguf_gemm.hip",
     "gguf_moe.hip",
     "gguf_moe_mfma.hip",
+    "gguf_moe_router.hip",
 )
 
 ARCH = "gfx950"

@@ -32,6 +32,7 @@ struct gollek_hip_weight {
 namespace {
 
 constexpr int32_t kAbiVersion = 1 * 10000 + 0 * 100 + 0;
+constexpr int64_t kRouterMaxExperts = 4096;  // router LDS: 8 B per expert + 4 B per rank
 
 thread_local std::string g_last_error;
 thread_local int32_t g_last_status = GOLLEK_HIP_OK;
@@ -589,6 +590,176 @@ int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
         e = hipMemcpyAsync(out, d_out, (size_t)(tokens * sh.H) * 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "moe", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+}  // extern "C"
+
+// ---- MoE router ---------------------------------------------------------
+
+namespace {
+
+int32_t check_router(int64_t tokens, int64_t n_experts, int64_t top_k, int32_t scoring, char *err,
+                     size_t err_len) {
+    if (scoring != GOLLEK_HIP_ROUTER_SOFTMAX && scoring != GOLLEK_HIP_ROUTER_SIGMOID)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Unknown router scoring %d", scoring);
+    if (n_experts <= 0 || n_experts > kRouterMaxExperts || top_k <= 0 || top_k > kRouterMaxExperts)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Router needs 1 <= experts, top_k <= %d (got %lld, %lld)", (int)kRouterMaxExperts,
+                    (long long)n_experts, (long long)top_k);
+    if (tokens < 0 || tokens > (1 << 24) || tokens * top_k > (1 << 24) ||
+        tokens * n_experts > (1LL << 30))
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Invalid tokens %lld / top_k %lld",
+                    (long long)tokens, (long long)top_k);
+    return GOLLEK_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t gollek_hip_moe_select_topk_device(const float *logits, int64_t tokens, int64_t n_experts,
+                                          int64_t top_k, int32_t scoring, int32_t *ids,
+                                          float *weights, void *stream, char *err,
+                                          size_t err_len) {
+    int32_t rc = check_router(tokens, n_experts, top_k, scoring, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    if (logits == nullptr || ids == nullptr || weights == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "router buffers");
+    const hipError_t e =
+        gollek::launch_moe_topk(logits, (int)tokens, (int)n_experts, (int)top_k,
+                                scoring == GOLLEK_HIP_ROUTER_SIGMOID, ids, weights,
+                                static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "router launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_moe_select_topk(const float *logits, int64_t tokens, int64_t n_experts,
+                                   int64_t top_k, int32_t scoring, int32_t *ids, float *weights,
+                                   char *err, size_t err_len) {
+    int32_t rc = check_router(tokens, n_experts, top_k, scoring, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (logits == nullptr || ids == nullptr || weights == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "router buffers");
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice", err, err_len);
+    rc = use_device(device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t lb = align_up((size_t)(tokens * n_experts) * 4, 256);
+    const size_t rb = align_up((size_t)(tokens * top_k) * 4, 256);
+    uint8_t *buf = nullptr;
+    e = hipMalloc(reinterpret_cast<void **>(&buf), lb + 2 * rb);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(router)", err, err_len);
+    float *d_l = reinterpret_cast<float *>(buf);
+    int32_t *d_ids = reinterpret_cast<int32_t *>(buf + lb);
+    float *d_w = reinterpret_cast<float *>(buf + lb + rb);
+    e = hipMemcpy(d_l, logits, (size_t)(tokens * n_experts) * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = gollek::launch_moe_topk(d_l, (int)tokens, (int)n_experts, (int)top_k,
+                                    scoring == GOLLEK_HIP_ROUTER_SIGMOID, d_ids, d_w, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(ids, d_ids, (size_t)(tokens * top_k) * 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(weights, d_w, (size_t)(tokens * top_k) * 4, hipMemcpyDeviceToHost);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return hip_fail(e, "router", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                    gollek_hip_weight *down, int64_t n_experts, const float *x,
+                                    const float *logits, int64_t tokens, int64_t top_k,
+                                    int32_t scoring, int32_t *ids, float *weights, float *out,
+                                    void *workspace, int64_t workspace_bytes, void *stream,
+                                    char *err, size_t err_len) {
+    int32_t rc = check_router(tokens, n_experts, top_k, scoring, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    MoeShape sh;
+    rc = check_moe(gate, up, down, n_experts, tokens, top_k, &sh, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    if (x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr || out == nullptr ||
+        workspace == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE block buffers");
+    const int64_t need = gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
+    if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Workspace of %lld bytes (256-byte aligned) needed, got %lld",
+                    (long long)need, (long long)workspace_bytes);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = gollek::launch_moe_topk(logits, (int)tokens, sh.E, (int)top_k,
+                                           scoring == GOLLEK_HIP_ROUTER_SIGMOID, ids, weights, s);
+    if (e == hipSuccess)
+        e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes, down->row_bytes,
+                                   sh.E, sh.H, sh.I, x, ids, weights, (int)tokens, (int)top_k, out,
+                                   static_cast<uint8_t *>(workspace), s);
+    if (e != hipSuccess) return hip_fail(e, "moe block launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
+                             gollek_hip_weight *down, int64_t n_experts, const float *x,
+                             int64_t tokens, const float *logits, int64_t top_k, int32_t scoring,
+                             float *out, int64_t out_len, char *err, size_t err_len) {
+    int32_t rc = check_router(tokens, n_experts, top_k, scoring, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    MoeShape sh;
+    rc = check_moe(gate, up, down, n_experts, tokens, top_k, &sh, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (x == nullptr || logits == nullptr || out == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE block buffers");
+    if (out_len < tokens * sh.H)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Output length %lld is smaller than %lld x %d",
+                    (long long)out_len, (long long)tokens, sh.H);
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    std::lock_guard<std::mutex> lock(gate->mu);
+    rc = use_device(gate->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t xb = align_up((size_t)(tokens * sh.H) * 4, 256);
+    const size_t lb = align_up((size_t)(tokens * sh.E) * 4, 256);
+    const size_t rb = align_up((size_t)(tokens * top_k) * 4, 256);
+    const size_t ws = (size_t)gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
+    rc = ensure_staging(gate, 2 * xb + lb + 2 * rb + ws, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    uint8_t *base = gate->staging;
+    float *d_x = reinterpret_cast<float *>(base);
+    float *d_out = reinterpret_cast<float *>(base + xb);
+    float *d_l = reinterpret_cast<float *>(base + 2 * xb);
+    int32_t *d_ids = reinterpret_cast<int32_t *>(base + 2 * xb + lb);
+    float *d_w = reinterpret_cast<float *>(base + 2 * xb + lb + rb);
+    uint8_t *d_ws = base + 2 * xb + lb + 2 * rb;
+    hipStream_t s = gate->stream;
+    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)(tokens * sh.H) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d_l, logits, (size_t)(tokens * sh.E) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = gollek::launch_moe_topk(d_l, (int)tokens, sh.E, (int)top_k,
+                                    scoring == GOLLEK_HIP_ROUTER_SIGMOID, d_ids, d_w, s);
+    if (e == hipSuccess)
+        e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
+                                   down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
+                                   (int)top_k, d_out, d_ws, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(out, d_out, (size_t)(tokens * sh.H) * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "moe block", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }

@@ -79,6 +79,11 @@ hipError_t launch_moe_route(const int32_t *ids, const float *wts, int P, int E, 
                             int tiles1, int32_t *meta, hipStream_t stream);
 hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float *ypair, int T,
                               int top_k, int H, int E, float *out, hipStream_t stream);
+// MoE router (gguf_moe_router.hip): logits [T, E] -> ids / wts [T, K] with
+// softmax (sigmoid = 0) or sigmoid scoring and renormalised top-K weights.
+size_t moe_topk_lds_bytes(int E, int K);
+hipError_t launch_moe_topk(const float *logits, int T, int E, int K, int sigmoid, int32_t *ids,
+                           float *wts, hipStream_t stream);
 bool moe_q4k_mfma_supported(int E, int H, int I, const float *x);
 hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
                                int H, int I, const float *x, const int32_t *ids, const float *wts,

@@ -429,3 +429,66 @@ def moe_grouped_device(gate: DeviceWeight, up: DeviceWeight, down: DeviceWeight,
                                            V(out_ptr), V(ws_ptr), ws_bytes, V(stream), err.buf,
                                            err.size)
     check(rc, err)
+
+
+# ---- MoE router and routed block ---------------------------------------------
+
+ROUTER_SOFTMAX = 0
+ROUTER_SIGMOID = 1
+
+
+def router_scoring(model_type: str | None) -> int:
+    """The reference's choice (MoeForwardPass.java:174-175): sigmoid when the
+    model type contains "qwen" or "moe", softmax otherwise."""
+    mt = model_type or ""
+    return ROUTER_SIGMOID if ("qwen" in mt or "moe" in mt) else ROUTER_SOFTMAX
+
+
+def moe_select_topk(logits, top_k: int, scoring: int):
+    """Router probabilities and renormalised top-k (MoeForwardPass.java:174-203
+    with selectTopK :286-306) on the GPU: logits (tokens, n_experts) float32
+    -> ids (tokens, top_k) int32, weights (tokens, top_k) float32."""
+    lv = np.ascontiguousarray(logits, dtype=np.float32)
+    if lv.ndim != 2:
+        raise IllegalArgumentError("logits must be (tokens, n_experts)")
+    tokens, n_experts = lv.shape
+    ids = np.zeros((tokens, top_k), np.int32)
+    w = np.zeros((tokens, top_k), np.float32)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_moe_select_topk(lv.ctypes.data, tokens, n_experts, top_k, scoring,
+                                         ids.ctypes.data, w.ctypes.data, err.buf, err.size), err)
+    return ids, w
+
+
+def moe_block(gate: GgufTensor, up: GgufTensor, down: GgufTensor, n_experts: int, x, logits,
+              top_k: int, scoring: int) -> np.ndarray:
+    """The routed MoE block (MoeForwardPass.java:174-240 after the router
+    linear): router on `logits`, then the grouped Q4_K expert FFN."""
+    for name, t in (("gate", gate), ("up", up), ("down", down)):
+        if t is None:
+            raise NullPointerError(name)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    lv = np.ascontiguousarray(logits, dtype=np.float32)
+    tokens = xv.shape[0]
+    out = np.zeros((tokens, gate.columns), dtype=np.float32)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    check(lib.gollek_hip_moe_block(gate.handle(), up.handle(), down.handle(), n_experts,
+                                   xv.ctypes.data, tokens, lv.ctypes.data, top_k, scoring,
+                                   out.ctypes.data, out.size, err.buf, err.size), err)
+    return out
+
+
+def moe_block_device(gate: DeviceWeight, up: DeviceWeight, down: DeviceWeight, n_experts: int,
+                     x_ptr: int, logits_ptr: int, tokens: int, top_k: int, scoring: int,
+                     ids_ptr: int, w_ptr: int, out_ptr: int, ws_ptr: int, ws_bytes: int,
+                     stream: int = 0) -> None:
+    lib = _native.load()
+    err = _native.ErrBuf()
+    V = ctypes.c_void_p
+    rc = lib.gollek_hip_moe_block_device(gate.handle, up.handle, down.handle, n_experts,
+                                         V(x_ptr), V(logits_ptr), tokens, top_k, scoring,
+                                         V(ids_ptr), V(w_ptr), V(out_ptr), V(ws_ptr), ws_bytes,
+                                         V(stream), err.buf, err.size)
+    check(rc, err)

@@ -198,6 +198,53 @@ int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight
                                       int64_t workspace_bytes, void *stream, char *err,
                                       size_t err_len);
 
+/* ---- MoE router and the routed block ------------------------------------ */
+/* SFE/ = runner/safetensor/gollek-safetensor-engine/src/main/java/tech/kayys/
+ * gollek/safetensor/engine/. */
+
+/* Router scoring (SFE/generation/moe/MoeForwardPass.java:174-197): the
+ * reference picks sigmoid when the model type contains "qwen" or "moe",
+ * softmax otherwise; the caller passes that choice. */
+#define GOLLEK_HIP_ROUTER_SOFTMAX 0
+#define GOLLEK_HIP_ROUTER_SIGMOID 1
+
+/* Per token t (logits row-major tokens x n_experts, the router linear's
+ * output): probabilities by `scoring` (sigmoid 1 / (1 + exp(-l)); softmax
+ * exp(l - max) / sum with exp in double and float sums in expert order),
+ * then the top_k experts in descending probability order, ties in index
+ * order, and their probabilities divided by their float sum when that sum
+ * is > 0 -> ids / weights (row-major tokens x top_k).  Ranks past n_experts
+ * get id 0, weight 0.  Replaces MoeForwardPass.java:174-203 with selectTopK
+ * (:286-306), bit for bit.  n_experts or top_k outside [1, 4096], an unknown
+ * scoring -> ARG.  Synchronous; allocates device memory per call (the
+ * _device variant does not). */
+int32_t gollek_hip_moe_select_topk(const float *logits, int64_t tokens, int64_t n_experts,
+                                   int64_t top_k, int32_t scoring, int32_t *ids, float *weights,
+                                   char *err, size_t err_len);
+int32_t gollek_hip_moe_select_topk_device(const float *logits, int64_t tokens, int64_t n_experts,
+                                          int64_t top_k, int32_t scoring, int32_t *ids,
+                                          float *weights, void *stream, char *err,
+                                          size_t err_len);
+
+/* The routed MoE block: gollek_hip_moe_select_topk on `logits` followed by
+ * gollek_hip_moe_grouped with the ids and weights it chose, on one stream
+ * (MoeForwardPass.java:174-240 after the router linear).  The shared expert
+ * (:235-242) is a plain SwiGLU FFN the caller adds.  Checks of both calls
+ * apply. */
+int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
+                             gollek_hip_weight *down, int64_t n_experts, const float *x,
+                             int64_t tokens, const float *logits, int64_t top_k, int32_t scoring,
+                             float *out, int64_t out_len, char *err, size_t err_len);
+/* Device variant: also writes the chosen ids / weights (device, tokens x
+ * top_k) and takes the grouped FFN's workspace from the caller
+ * (gollek_hip_moe_workspace_bytes; calls sharing it must not overlap). */
+int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                    gollek_hip_weight *down, int64_t n_experts, const float *x,
+                                    const float *logits, int64_t tokens, int64_t top_k,
+                                    int32_t scoring, int32_t *ids, float *weights, float *out,
+                                    void *workspace, int64_t workspace_bytes, void *stream,
+                                    char *err, size_t err_len);
+
 /* ---- GGUF files --------------------------------------------------------- */
 /* GC/ = runner/gguf/gollek-gguf-core/src/main/java/tech/kayys/gollek/gguf/. */
 

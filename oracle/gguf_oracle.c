@@ -537,3 +537,84 @@ int go_matvec_rows(int type_id, const uint8_t *data, int64_t rows, int64_t cols,
     free(sums);
     return GO_OK;
 }
+
+/* ---- MoE router (MoeForwardPass.java:174-203, 286-306) ------------------ */
+
+/* Float.floatToIntBits: one canonical NaN. */
+static int32_t float_to_int_bits(float v) {
+    int32_t b;
+    if (v != v) return 0x7FC00000;
+    memcpy(&b, &v, 4);
+    return b;
+}
+
+/* Float.compare(a, b). */
+static int java_float_compare(float a, float b) {
+    if (a < b) return -1;
+    if (a > b) return 1;
+    int32_t ab = float_to_int_bits(a), bb = float_to_int_bits(b);
+    return ab == bb ? 0 : (ab < bb ? -1 : 1);
+}
+
+/* Math.max(a, b) for floats. */
+static float java_max(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == 0.0f && b == 0.0f) return float_to_int_bits(a) == 0 ? a : b;
+    return a >= b ? a : b;
+}
+
+int go_moe_select_topk(const float *logits, int64_t tokens, int64_t n_experts, int64_t top_k,
+                       int sigmoid, int32_t *ids, float *weights) {
+    if (tokens < 0 || n_experts <= 0 || top_k <= 0) return GO_ERR_ARG;
+    float *p = malloc((size_t)n_experts * sizeof(float));
+    int32_t *idx = malloc((size_t)n_experts * sizeof(int32_t));
+    if (p == NULL || idx == NULL) {
+        free(p);
+        free(idx);
+        return GO_ERR_ARG;
+    }
+    for (int64_t t = 0; t < tokens; t++) {
+        const float *l = logits + t * n_experts;
+        if (sigmoid) { /* :178-181 */
+            for (int64_t e = 0; e < n_experts; e++) p[e] = 1.0f / (1.0f + (float)exp((double)(-l[e])));
+        } else {       /* :183-196 */
+            float max = -INFINITY;
+            for (int64_t e = 0; e < n_experts; e++) max = java_max(max, l[e]);
+            float sum = 0.0f;
+            for (int64_t e = 0; e < n_experts; e++) {
+                p[e] = (float)exp((double)(l[e] - max));
+                sum += p[e];
+            }
+            for (int64_t e = 0; e < n_experts; e++) p[e] /= sum;
+        }
+        /* :288-293: stable sort of the indices, descending Float.compare
+         * (insertion sort keeps equal keys in index order, as TimSort does). */
+        for (int64_t e = 0; e < n_experts; e++) {
+            int64_t j = e;
+            while (j > 0 && java_float_compare(p[e], p[idx[j - 1]]) > 0) {
+                idx[j] = idx[j - 1];
+                j--;
+            }
+            idx[j] = (int32_t)e;
+        }
+        /* :295-304 (the arrays start zeroed: ranks past n_experts stay 0). */
+        int32_t *oi = ids + t * top_k;
+        float *ow = weights + t * top_k;
+        for (int64_t k = 0; k < top_k; k++) {
+            oi[k] = 0;
+            ow[k] = 0.0f;
+        }
+        float wsum = 0.0f;
+        for (int64_t k = 0; k < top_k && k < n_experts; k++) {
+            oi[k] = idx[k];
+            ow[k] = p[idx[k]];
+            wsum += p[idx[k]];
+        }
+        if (wsum > 0.0f)
+            for (int64_t k = 0; k < top_k; k++) ow[k] /= wsum;
+    }
+    free(p);
+    free(idx);
+    return GO_OK;
+}

@@ -21,6 +21,13 @@
  *   go_dot_row /         reference closed-form dots (384, 128, 16/48, 32/64,
  *   go_matvec_rows       +-2464, -264, lane-order dots) and an fp64 dot over
  *                        the bit-exact dequantized rows at 1e-3.
+ *   go_moe_select_topk   closed forms (uniform logits: ids 0..k-1 by the
+ *                        stable tie order, weights 1/k; distinct logits:
+ *                        numpy's stable descending argsort and fp64
+ *                        probabilities; a NaN probability ranks first and
+ *                        skips the renormalisation; k past the expert count
+ *                        pads id 0 / weight 0; all-zero sigmoid weights stay
+ *                        0) in tests/test_oracle.py.
  * The fp32 rounding order of the Java Vector-API kernels (FloatVector lane
  * reductions) cannot be reproduced without a JVM; the scalar Java loops are
  * restated instead, so GEMV parity is tolerance-based (1e-3), as specified.
@@ -82,6 +89,15 @@ void go_group_sums32(const float *x, int64_t cols, float *sums);
  * (RT/GgufKMeta.java:115-181). */
 int go_q4k_rows_have_mins(const uint8_t *data, int64_t row_bytes, int64_t cols,
                           int64_t row_count);
+
+/* MoE router (runner/safetensor/gollek-safetensor-engine/src/main/java/tech/
+ * kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:174-203,
+ * 286-306): logits [tokens, n_experts] -> sigmoid (sigmoid != 0) or softmax
+ * probabilities, top_k by a stable descending Float.compare sort, weights
+ * renormalised by their float sum when it is > 0 -> ids / weights
+ * [tokens, top_k] (ranks past n_experts: id 0, weight 0). */
+int go_moe_select_topk(const float *logits, int64_t tokens, int64_t n_experts, int64_t top_k,
+                       int sigmoid, int32_t *ids, float *weights);
 
 #ifdef __cplusplus
 }

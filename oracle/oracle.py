@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
         L.go_matvec_rows.argtypes = [I, P, I64, I64, I64, P, P, I64, I]
         L.go_default_threads.restype = I
         L.go_group_sums32.argtypes = [P, I64, P]
+        L.go_moe_select_topk.restype = I
+        L.go_moe_select_topk.argtypes = [P, I64, I64, I64, I, P, P]
         L.go_q4k_rows_have_mins.restype = I
         L.go_q4k_rows_have_mins.argtypes = [P, I64, I64, I64]
         _lib = L
@@ -157,6 +159,20 @@ def gemm_reference(type_id: int, data, cols: int, x_bf16_bits) -> np.ndarray:
     w = dequantize(type_id, data, cols).astype(np.float64)
     x = (np.asarray(x_bf16_bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
     return x.astype(np.float64) @ w.T
+
+
+def moe_select_topk(logits, top_k: int, sigmoid: bool):
+    """MoE router (go_moe_select_topk): logits (T, E) fp32 -> ids (T, k)
+    int32, weights (T, k) fp32, as MoeForwardPass.java:174-203,286-306."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = lg.shape
+    ids = np.zeros((T, top_k), np.int32)
+    w = np.zeros((T, top_k), np.float32)
+    rc = lib().go_moe_select_topk(lg.ctypes.data, T, E, top_k, int(bool(sigmoid)),
+                                  ids.ctypes.data, w.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"go_moe_select_topk: status {rc}")
+    return ids, w
 
 
 def silu(v: np.ndarray) -> np.ndarray:

@@ -105,3 +105,110 @@ def test_moe_device_entry_matches_host():
         d.close()
     for t in (tg, tu, td):
         t.close()
+
+
+# ---- router and routed block -------------------------------------------------
+
+def _same_bits(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return np.array_equal(np.isnan(a), np.isnan(b)) and \
+        np.array_equal(a[~np.isnan(b)].view(np.uint32), b[~np.isnan(b)].view(np.uint32))
+
+
+def _router_cases():
+    rng = np.random.default_rng(31)
+    cases = [("normal", rng.standard_normal((16, 128)).astype(np.float32), 8),
+             ("e60", rng.standard_normal((7, 60)).astype(np.float32), 4),
+             ("e300", (3 * rng.standard_normal((5, 300))).astype(np.float32), 16),
+             ("e4096", rng.standard_normal((2, 4096)).astype(np.float32), 32),
+             ("k_past_e", rng.standard_normal((3, 5)).astype(np.float32), 8),
+             ("ties", np.round(rng.standard_normal((9, 64)) * 2).astype(np.float32), 8),
+             ("wide", (rng.standard_normal((4, 128)) * 40).astype(np.float32), 8),
+             ("single", rng.standard_normal((1, 1)).astype(np.float32), 1)]
+    sp = rng.standard_normal((6, 32)).astype(np.float32)
+    sp[0, 3] = np.nan
+    sp[1, 5] = np.inf
+    sp[2, :] = -np.inf
+    sp[3, 7] = -np.inf
+    sp[4, :] = 0.0
+    sp[5, ::2] = -0.0
+    cases.append(("specials", sp, 4))
+    return cases
+
+
+@pytest.mark.parametrize("scoring", [ops.ROUTER_SOFTMAX, ops.ROUTER_SIGMOID])
+def test_router_matches_oracle_bit_for_bit(scoring):
+    for name, lg, k in _router_cases():
+        print(f"[gpu] router {name} scoring={scoring} shape={lg.shape} k={k}", flush=True)
+        ids, w = ops.moe_select_topk(lg, k, scoring)
+        rids, rw = o.moe_select_topk(lg, k, scoring == ops.ROUTER_SIGMOID)
+        assert np.array_equal(ids, rids), name
+        assert _same_bits(w, rw), name
+    ids, w = ops.moe_select_topk(np.zeros((0, 8), np.float32), 2, scoring)
+    assert ids.shape == (0, 2)
+
+
+def test_router_rejects_bad_arguments():
+    lg = np.zeros((2, 8), np.float32)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.moe_select_topk(lg, 2, 7)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.moe_select_topk(lg, 0, ops.ROUTER_SOFTMAX)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.moe_select_topk(np.zeros((1, 5000), np.float32), 2, ops.ROUTER_SOFTMAX)
+    assert ops.router_scoring("qwen3_moe") == ops.ROUTER_SIGMOID
+    assert ops.router_scoring("mixtral") == ops.ROUTER_SOFTMAX
+
+
+@pytest.mark.parametrize("E,H,I,T,k,scoring", [(128, 2048, 768, 16, 8, ops.ROUTER_SIGMOID),
+                                               (16, 1024, 512, 9, 4, ops.ROUTER_SOFTMAX)])
+def test_moe_block_routes_then_runs_the_grouped_ffn(E, H, I, T, k, scoring):
+    print(f"[gpu] moe block E={E} H={H} I={I} T={T} k={k} scoring={scoring}", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + 5)
+    x = syn.activation(T * H, seed=41).reshape(T, H)
+    logits = (2 * np.random.default_rng(42).standard_normal((T, E))).astype(np.float32)
+    out = ops.moe_block(tg, tu, td, E, x, logits, k, scoring)
+    ids, w = o.moe_select_topk(logits, k, scoring == ops.ROUTER_SIGMOID)
+    grouped = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    assert np.array_equal(out.view(np.uint32), grouped.view(np.uint32))
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w)
+    assert o.rel_err(out, ref) <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+def test_moe_block_device_entry_matches_host():
+    import torch
+    E, H, I, T, k = 16, 1024, 512, 9, 4
+    print("[gpu] moe block device entry", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=77)
+    x = syn.activation(T * H, seed=78).reshape(T, H)
+    logits = np.random.default_rng(79).standard_normal((T, E)).astype(np.float32)
+    host = ops.moe_block(tg, tu, td, E, x, logits, k, ops.ROUTER_SOFTMAX)
+    dev = {n: torch.from_numpy(a.reshape(-1)).cuda() for n, a in
+           (("g", gate), ("u", up), ("d", down))}
+    dw = [ops.DeviceWeight(syn.Q4_K, dev["g"].data_ptr(), E * I, H),
+          ops.DeviceWeight(syn.Q4_K, dev["u"].data_ptr(), E * I, H),
+          ops.DeviceWeight(syn.Q4_K, dev["d"].data_ptr(), E * H, I)]
+    dx = torch.from_numpy(x).cuda()
+    dl = torch.from_numpy(logits).cuda()
+    ids = torch.zeros((T, k), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, k), dtype=torch.float32, device="cuda")
+    out = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    nbytes = ops.moe_workspace_bytes(T, k, H, I, E)
+    ws = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda")
+    base = (ws.data_ptr() + 255) // 256 * 256
+    stream = torch.cuda.current_stream().cuda_stream
+    ops.moe_block_device(dw[0], dw[1], dw[2], E, dx.data_ptr(), dl.data_ptr(), T, k,
+                         ops.ROUTER_SOFTMAX, ids.data_ptr(), w.data_ptr(), out.data_ptr(), base,
+                         nbytes, stream)
+    torch.cuda.synchronize()
+    rids, rw = o.moe_select_topk(logits, k, False)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert _same_bits(w.cpu().numpy(), rw)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), host.view(np.uint32))
+    for d in dw:
+        d.close()
+    for t in (tg, tu, td):
+        t.close()

@@ -182,3 +182,64 @@ def test_moe_reference_paths_agree_and_properties():
     wz[0, 0] = 0.0
     assert np.allclose(o.moe_reference_q4k(gate, up, down, E, x, bad, w),
                        o.moe_reference_q4k(gate, up, down, E, x, ids, wz), rtol=1e-12, atol=1e-12)
+
+
+# ---- MoE router oracle (MoeForwardPass.java:174-203, 286-306) ----------------
+
+def _sig64(v):
+    return 1.0 / (1.0 + np.exp(-np.asarray(v, np.float64)))
+
+
+@pytest.mark.parametrize("sigmoid", [False, True])
+def test_router_uniform_logits_take_the_first_k_with_equal_weights(sigmoid):
+    # Equal probabilities: a stable sort keeps index order, and k equal
+    # weights renormalise to 1/k (exact for k = 8: 16 x 1/16 and 8 x 0.5).
+    lg = np.zeros((3, 16), np.float32)
+    ids, w = o.moe_select_topk(lg, 8, sigmoid)
+    assert np.array_equal(ids, np.tile(np.arange(8, dtype=np.int32), (3, 1)))
+    assert np.array_equal(w, np.full((3, 8), 0.125, np.float32))
+
+
+@pytest.mark.parametrize("sigmoid", [False, True])
+def test_router_distinct_logits_follow_a_descending_sort(sigmoid):
+    rng = np.random.default_rng(8)
+    T, E, k = 5, 64, 6
+    lg = np.stack([rng.permutation(np.linspace(-4, 4, E)) for _ in range(T)]).astype(np.float32)
+    ids, w = o.moe_select_topk(lg, k, sigmoid)
+    for t in range(T):
+        exp_ids = np.argsort(-lg[t].astype(np.float64), kind="stable")[:k]
+        assert np.array_equal(ids[t], exp_ids)
+        s = _sig64(lg[t, exp_ids]) if sigmoid else np.exp(lg[t, exp_ids].astype(np.float64))
+        assert np.allclose(w[t], s / s.sum(), rtol=2e-6, atol=0)
+        assert abs(float(w[t].astype(np.float64).sum()) - 1.0) < 2e-6
+
+
+def test_router_ties_keep_index_order():
+    lg = np.array([[1, 3, 3, 2, 3]], np.float32)
+    for sigmoid in (False, True):
+        ids, w = o.moe_select_topk(lg, 2, sigmoid)
+        assert ids.tolist() == [[1, 2]]
+        assert w.tolist() == [[0.5, 0.5]]
+
+
+def test_router_nan_ranks_first_and_skips_renormalisation():
+    ids, w = o.moe_select_topk(np.array([[0, 1, np.nan, 2]], np.float32), 2, True)
+    assert ids.tolist() == [[2, 3]]
+    assert np.isnan(w[0, 0])
+    assert abs(float(w[0, 1]) - _sig64(2.0)) <= 1e-7  # the raw sigmoid, not renormalised
+    # softmax: a NaN max makes every probability NaN; all tie, index order.
+    ids, w = o.moe_select_topk(np.array([[0, 1, np.nan, 2]], np.float32), 3, False)
+    assert ids.tolist() == [[0, 1, 2]] and np.all(np.isnan(w))
+    # +inf logit: inf - inf = NaN at that expert, exp(-inf) = 0 elsewhere, sum NaN.
+    ids, w = o.moe_select_topk(np.array([[0, np.inf, 1]], np.float32), 2, False)
+    assert ids.tolist() == [[0, 1]] and np.all(np.isnan(w))
+
+
+def test_router_pads_past_the_expert_count_and_keeps_zero_sums():
+    ids, w = o.moe_select_topk(np.array([[0.0, 2.0, 1.0]], np.float32), 5, False)
+    assert ids.tolist() == [[1, 2, 0, 0, 0]]
+    assert w[0, 3] == 0 and w[0, 4] == 0
+    assert abs(float(w[0, :3].astype(np.float64).sum()) - 1.0) < 2e-7
+    assert w[0, 0] > w[0, 1] > w[0, 2] > 0
+    ids, w = o.moe_select_topk(np.full((1, 4), -np.inf, np.float32), 2, True)
+    assert ids.tolist() == [[0, 1]] and w.tolist() == [[0.0, 0.0]]
