@@ -234,6 +234,27 @@ def moe_workload(torch, steps: int, warmup: int, seed: int):
     res = {"ms_per_step": ms, "steps": n, "experts_touched": int(used),
            "algo_bytes": int(bytes_used), "algo_gbs": bytes_used / (ms * 1e-3) / 1e9,
            "hbm_frac": bytes_used / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+    # The routed block: router logits (seeded N(0, 2^2)) -> sigmoid top-8 on the
+    # GPU -> the same grouped FFN (gollek_hip_moe_block_device).
+    logits = torch.from_numpy(
+        (2.0 * np.random.default_rng(seed + 5).standard_normal((T, E))).astype(np.float32)).cuda()
+    bids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    bw = torch.empty((T, k), dtype=torch.float32, device="cuda")
+
+    def launch_block(i, stream):
+        g, u, d = layers[i][1]
+        ops.moe_block_device(g, u, d, E, xd.data_ptr(), logits.data_ptr(), T, k,
+                             ops.ROUTER_SIGMOID, bids.data_ptr(), bw.data_ptr(), out.data_ptr(),
+                             ws.data_ptr(), ws_bytes, stream)
+
+    bms, bn = graph_time(torch, launch_block, copies, steps, warmup)
+    bused = len(np.unique(bids.cpu().numpy()))
+    bbytes = bused * (gate.shape[1] * I + up.shape[1] * I + down.shape[1] * H) + 2 * T * H * 4 \
+        + T * E * 4
+    res["routed_block"] = {"ms_per_step": bms, "steps": bn, "experts_touched": int(bused),
+                           "scoring": "sigmoid", "algo_bytes": int(bbytes),
+                           "algo_gbs": bbytes / (bms * 1e-3) / 1e9}
     for _, handles in layers:
         for h in handles:
             h.close()

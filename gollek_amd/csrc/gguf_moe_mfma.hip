@@ -103,14 +103,15 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const int32_t *items = used + E + 1 + (MODE == 1 ? E + 1 : 0);
     const int nitems = items[nused];
     // Work split.  Every (expert, route group) unit has G.tiles_e items, in
-    // order.  With at least as many workgroups as units, unit j gets
-    // workgroups k j .. k j + k - 1 (k = grid / units) and each takes an even
-    // slice of it, so no workgroup changes route group (which costs a
-    // pipeline drain); otherwise the items are split evenly.
+    // order.  When k = grid / units workgroups per unit leave at most 1/8 of
+    // the grid idle, unit j gets workgroups k j .. k j + k - 1 and each takes
+    // an even slice of it, so no workgroup changes route group (which costs a
+    // pipeline drain); otherwise the items are split evenly over the grid.
     const int nunits = nitems / G.tiles_e;
     const int kpu = nunits > 0 ? (int)gridDim.x / nunits : 0;
+    const bool unit_split = kpu >= 1 && 8 * ((int)gridDim.x - kpu * nunits) <= (int)gridDim.x;
     int i_begin, i_end;
-    if (kpu >= 1) {
+    if (unit_split) {
         const int unit = (int)blockIdx.x / kpu, sub = (int)blockIdx.x - unit * kpu;
         i_begin = unit < nunits ? unit * G.tiles_e + sub * G.tiles_e / kpu : 0;
         i_end = unit < nunits ? unit * G.tiles_e + (sub + 1) * G.tiles_e / kpu : 0;

@@ -30,9 +30,9 @@ def _experts(E, H, I, seed):
 
 
 # The expert passes give each (expert, route group) unit its own workgroups
-# when the units fit the grid (up to tens per unit here, 3 for the 128-expert
-# layer, one at 400 tokens x top-2 over 32 experts: 210 units) and
-# split the items evenly past the grid (600 tokens: 314 units).
+# when that leaves at most 1/8 of the grid idle (8 and 16 experts: tens of
+# workgroups per unit) and split the items evenly otherwise (the 128-expert
+# layer's 87 units; 210 and 314 units at 400 / 600 tokens x top-2).
 @pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
                                        (128, 2048, 768, 16, 8), (32, 512, 256, 400, 2),
                                        (32, 512, 256, 600, 2)])
