@@ -229,7 +229,7 @@ int32_t gollek_hip_moe_select_topk_device(const float *logits, int64_t tokens, i
 /* The routed MoE block: gollek_hip_moe_select_topk on `logits` followed by
  * gollek_hip_moe_grouped with the ids and weights it chose, on one stream
  * (MoeForwardPass.java:174-240 after the router linear).  The shared expert
- * (:235-242) is a plain SwiGLU FFN the caller adds.  Checks of both calls
+ * (:240-247) is a plain SwiGLU FFN the caller adds.  Checks of both calls
  * apply. */
 int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
                              gollek_hip_weight *down, int64_t n_experts, const float *x,
