@@ -23,6 +23,8 @@ ERR_NOMEM = -5
 Q4_0 = 2
 Q8_0 = 8
 Q4_K = 12
+Q5_K = 13
+Q6_K = 14
 
 _c = ctypes
 _P = _c.c_void_p

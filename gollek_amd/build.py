@@ -24,6 +24,7 @@ HIP_SOURCES = (
     "gguf_dequant.hip",
     "gguf_file.hip",
     "gguf_gemv.hip",
+    "gguf_k56.hip",
     "gguf_gemv_dot4.hip",
     "gguf_gemv_mfma.hip",
     "gguf_gemv_ring.hip",

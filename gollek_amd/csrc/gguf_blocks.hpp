@@ -18,7 +18,7 @@
 
 namespace gollek {
 
-enum TypeId : int { kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12 };
+enum TypeId : int { kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
 
 constexpr int kQ8BlockBytes = 34;
 constexpr int kQ4BlockBytes = 18;

@@ -70,18 +70,28 @@ const char *type_label(int32_t type_id) {
     case GOLLEK_HIP_Q4_0: return "Q4_0";
     case GOLLEK_HIP_Q8_0: return "Q8_0";
     case GOLLEK_HIP_Q4_K: return "Q4_K";
+    case GOLLEK_HIP_Q5_K: return "Q5_K";
+    case GOLLEK_HIP_Q6_K: return "Q6_K";
     default: return "?";
     }
 }
 
-int block_size(int32_t type_id) { return type_id == GOLLEK_HIP_Q4_K ? 256 : 32; }
+// Elements and bytes per block (GC/core/GgmlType.java:11-24).
+int block_size(int32_t type_id) { return type_id >= GOLLEK_HIP_Q4_K ? 256 : 32; }
 
 int block_bytes(int32_t type_id) {
-    return type_id == GOLLEK_HIP_Q4_K ? 144 : (type_id == GOLLEK_HIP_Q8_0 ? 34 : 18);
+    switch (type_id) {
+    case GOLLEK_HIP_Q4_0: return 18;
+    case GOLLEK_HIP_Q8_0: return 34;
+    case GOLLEK_HIP_Q4_K: return 144;
+    case GOLLEK_HIP_Q5_K: return 176;
+    default: return 210;  // Q6_K
+    }
 }
 
 bool supported(int32_t type_id) {
-    return type_id == GOLLEK_HIP_Q4_0 || type_id == GOLLEK_HIP_Q8_0 || type_id == GOLLEK_HIP_Q4_K;
+    return type_id == GOLLEK_HIP_Q4_0 || type_id == GOLLEK_HIP_Q8_0 || type_id == GOLLEK_HIP_Q4_K ||
+           type_id == GOLLEK_HIP_Q5_K || type_id == GOLLEK_HIP_Q6_K;
 }
 
 std::mutex g_init_mu;

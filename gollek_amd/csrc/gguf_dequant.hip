@@ -94,6 +94,7 @@ __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__rest
 hipError_t launch_dequant(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                           int64_t row0, int64_t nrows, float *out, hipStream_t stream) {
     if (nrows <= 0) return hipSuccess;
+    if (is_k56(type_id)) return launch_dequant_k56(type_id, w, row_bytes, cols, row0, nrows, out, stream);
     const int threads = 256;
     if (type_id == kQ8_0 || type_id == kQ4_0) {
         const int nb = (int)(cols / 32);

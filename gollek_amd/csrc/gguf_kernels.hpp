@@ -40,6 +40,15 @@ bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const voi
 hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
+// Q5_K / Q6_K (gguf_k56.hip): dequantization and the GEMV; the GEMV needs
+// gemv_k56_supported (x 16-byte aligned, weights 2-byte aligned).
+bool is_k56(int type_id);
+hipError_t launch_dequant_k56(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
+                              int64_t row0, int64_t nrows, float *out, hipStream_t stream);
+bool gemv_k56_supported(int type_id, int64_t row_bytes, const void *w, const float *x);
+hipError_t launch_gemv_k56(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
+                           const float *x, float *y, int64_t rows, hipStream_t stream);
+
 // Q4_K GEMV with integer dot products (gguf_gemv_dot4.hip).
 bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x);

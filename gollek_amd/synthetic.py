@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import numpy as np
 
-Q4_0, Q8_0, Q4_K = 2, 8, 12
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -98,7 +98,38 @@ def q4_k_matrix(rows: int, cols: int, seed: int) -> np.ndarray:
     return out.reshape(rows, ns * 144)
 
 
+def q5_k_matrix(rows: int, cols: int, seed: int) -> np.ndarray:
+    """(rows, cols/256*176) uint8: d, dmin = fp16(|N| * 0.01), 6-bit scale and
+    min codes ~ U{0..63}, qh and qs bytes ~ U{0..255}."""
+    g = rng(seed)
+    ns = cols // 256
+    out = np.empty((rows, ns, 176), dtype=np.uint8)
+    _put_u16(out, 0, f16_bits(np.abs(g.standard_normal((rows, ns), dtype=np.float32)) * 0.01))
+    _put_u16(out, 2, f16_bits(np.abs(g.standard_normal((rows, ns), dtype=np.float32)) * 0.01))
+    sc = g.integers(0, 64, size=(rows, ns, 8), dtype=np.uint16)
+    mn = g.integers(0, 64, size=(rows, ns, 8), dtype=np.uint16)
+    out[..., 4:16] = pack_q4k_scales(sc, mn)
+    out[..., 16:] = g.integers(0, 256, size=(rows, ns, 160), dtype=np.uint8)
+    return out.reshape(rows, ns * 176)
+
+
+def q6_k_matrix(rows: int, cols: int, seed: int) -> np.ndarray:
+    """(rows, cols/256*210) uint8: ql, qh bytes ~ U{0..255}, int8 scales
+    ~ U{-64..63}, d = fp16(|N| * 0.002)."""
+    g = rng(seed)
+    ns = cols // 256
+    out = np.empty((rows, ns, 210), dtype=np.uint8)
+    out[..., :192] = g.integers(0, 256, size=(rows, ns, 192), dtype=np.uint8)
+    out[..., 192:208] = g.integers(-64, 64, size=(rows, ns, 16)).astype(np.int8).view(np.uint8)
+    _put_u16(out, 208, f16_bits(np.abs(g.standard_normal((rows, ns), dtype=np.float32)) * 0.002))
+    return out.reshape(rows, ns * 210)
+
+
 def matrix(type_id: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    if type_id == Q5_K:
+        return q5_k_matrix(rows, cols, seed)
+    if type_id == Q6_K:
+        return q6_k_matrix(rows, cols, seed)
     if type_id == Q8_0:
         return q8_0_matrix(rows, cols, seed)
     if type_id == Q4_0:

@@ -25,8 +25,10 @@ import numpy as np
 
 from . import _native
 
-BLOCK = {_native.Q4_0: (32, 18), _native.Q8_0: (32, 34), _native.Q4_K: (256, 144)}
-TYPE_NAMES = {_native.Q4_0: "Q4_0", _native.Q8_0: "Q8_0", _native.Q4_K: "Q4_K"}
+BLOCK = {_native.Q4_0: (32, 18), _native.Q8_0: (32, 34), _native.Q4_K: (256, 144),
+         _native.Q5_K: (256, 176), _native.Q6_K: (256, 210)}
+TYPE_NAMES = {_native.Q4_0: "Q4_0", _native.Q8_0: "Q8_0", _native.Q4_K: "Q4_K",
+              _native.Q5_K: "Q5_K", _native.Q6_K: "Q6_K"}
 
 
 class GgufHipError(RuntimeError):

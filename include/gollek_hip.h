@@ -49,10 +49,14 @@ extern "C" {
 #define GOLLEK_HIP_ERR_DEVICE (-4)
 #define GOLLEK_HIP_ERR_NOMEM (-5)
 
-/* ggml type ids accepted by this library (GC/core/GgmlType.java:11,16,21). */
+/* ggml type ids accepted by this library (GC/core/GgmlType.java:11,16,21).  The
+ * *_device mat-vec of Q5_K / Q6_K needs x 16-byte aligned and Q5_K weights
+ * 4-byte aligned (else DEVICE). */
 #define GOLLEK_HIP_Q4_0 2
 #define GOLLEK_HIP_Q8_0 8
 #define GOLLEK_HIP_Q4_K 12
+#define GOLLEK_HIP_Q5_K 13 /* GC/core/GgmlType.java:22; dequantize, dot and mat-vec only */
+#define GOLLEK_HIP_Q6_K 14 /* GC/core/GgmlType.java:23; dequantize, dot and mat-vec only */
 
 /* Opaque device-resident weight matrix. */
 typedef struct gollek_hip_weight gollek_hip_weight;

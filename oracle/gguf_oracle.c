@@ -27,6 +27,8 @@ int go_block_size(int type_id) {
     case GO_Q4_0: return 32;
     case GO_Q8_0: return 32;
     case GO_Q4_K: return QK_K;
+    case GO_Q5_K: return QK_K;
+    case GO_Q6_K: return QK_K;
     default: return 0;
     }
 }
@@ -36,6 +38,8 @@ int go_block_bytes(int type_id) {
     case GO_Q4_0: return 18;
     case GO_Q8_0: return 34;
     case GO_Q4_K: return 144;
+    case GO_Q5_K: return 176;
+    case GO_Q6_K: return 210;
     default: return 0;
     }
 }
@@ -141,6 +145,56 @@ static void dequant_q4_k_block(const uint8_t *blk, float *y) {
 
 /* RT/GgufRowDequantizer.java:29-276 (Q4_0 :97-107, Q8_0 :141-152,
  * Q4_K :242-252, unsupported :275) */
+/* RT/GgufKBlockDequantizer.java:91-170: Q5_K.  Chunk c (64 elements) uses
+ * sub-blocks 2c, 2c+1, quants 48 + 32c.., and high-bit masks 1 << 2c,
+ * 2 << 2c over qh[0..32); values fl(fl(d1 * q) - m1), the min rules of Q4_K. */
+static void dequant_q5_k_block(const uint8_t *blk, float *y) {
+    const float d = go_f16_to_f32(rd16(blk));
+    const float dmin = go_f16_to_f32(rd16(blk + 2));
+    const uint8_t *qh = blk + 16;
+    for (int c = 0; c < 4; c++) {
+        int sc1, m1c, sc2, m2c;
+        go_k4_scale_min(blk + 4, 2 * c, &sc1, &m1c);
+        go_k4_scale_min(blk + 4, 2 * c + 1, &sc2, &m2c);
+        const float d1 = d * (float)sc1, d2 = d * (float)sc2;
+        float m1 = 0.0f, m2 = 0.0f;
+        if (dmin != 0.0f) {
+            m1 = min_contribution(dmin, m1c);
+            m2 = min_contribution(dmin, m2c);
+        }
+        const uint8_t *qs = blk + 48 + 32 * c;
+        const int mlo = 1 << (2 * c), mhi = 2 << (2 * c);
+        for (int i = 0; i < 32; i++) {
+            const int lo = (qs[i] & 0x0F) + ((qh[i] & mlo) != 0 ? 16 : 0);
+            const int hi = (qs[i] >> 4) + ((qh[i] & mhi) != 0 ? 16 : 0);
+            y[64 * c + i] = d1 * (float)lo - m1;
+            y[64 * c + 32 + i] = d2 * (float)hi - m2;
+        }
+    }
+}
+
+/* RT/GgufKBlockDequantizer.java:319-432: Q6_K, d at byte 208; per 128-element
+ * half: ql 64 bytes, qh 32 bytes, 8 int8 scales; values fl(fl(d * sc) * (q - 32)). */
+static void dequant_q6_k_block(const uint8_t *blk, float *y) {
+    const float d = go_f16_to_f32(rd16(blk + 208));
+    for (int h = 0; h < 2; h++) {
+        const uint8_t *ql = blk + 64 * h, *qh = blk + 128 + 32 * h;
+        const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+        float *o = y + 128 * h;
+        for (int half = 0; half < 2; half++) {
+            const float s1 = d * (float)sc[half], s2 = d * (float)sc[half + 2];
+            const float s3 = d * (float)sc[half + 4], s4 = d * (float)sc[half + 6];
+            for (int i = 16 * half; i < 16 * half + 16; i++) {
+                const int a = ql[i], b = ql[32 + i], hb = qh[i];
+                o[i] = s1 * (float)(((a & 0x0F) | ((hb & 0x03) << 4)) - 32);
+                o[32 + i] = s2 * (float)(((b & 0x0F) | (((hb >> 2) & 0x03) << 4)) - 32);
+                o[64 + i] = s3 * (float)(((a >> 4) | (((hb >> 4) & 0x03) << 4)) - 32);
+                o[96 + i] = s4 * (float)(((b >> 4) | (((hb >> 6) & 0x03) << 4)) - 32);
+            }
+        }
+    }
+}
+
 int go_dequantize_row(int type_id, const uint8_t *row, int64_t cols, float *dst) {
     int bs = go_block_size(type_id);
     if (bs == 0) return GO_ERR_UNSUPPORTED;
@@ -152,6 +206,8 @@ int go_dequantize_row(int type_id, const uint8_t *row, int64_t cols, float *dst)
         float *y = dst + b * bs;
         if (type_id == GO_Q8_0) dequant_q8_0_block(blk, y);
         else if (type_id == GO_Q4_0) dequant_q4_0_block(blk, y);
+        else if (type_id == GO_Q5_K) dequant_q5_k_block(blk, y);
+        else if (type_id == GO_Q6_K) dequant_q6_k_block(blk, y);
         else dequant_q4_k_block(blk, y);
     }
     return GO_OK;
@@ -403,7 +459,7 @@ void go_group_sums32(const float *x, int64_t cols, float *sums) {
 int go_dot_row(int type_id, const uint8_t *row, int64_t cols, const float *x,
                float *out) {
     int bs = go_block_size(type_id);
-    if (bs == 0) return GO_ERR_UNSUPPORTED;
+    if (bs == 0 || type_id == GO_Q5_K || type_id == GO_Q6_K) return GO_ERR_UNSUPPORTED;
     if (cols % bs != 0) return GO_ERR_ARG;
     if (type_id == GO_Q8_0) *out = dot_q8_0(row, cols, x);
     else if (type_id == GO_Q4_0) *out = dot_q4_0(row, cols, x);
@@ -466,7 +522,7 @@ int go_matvec_rows(int type_id, const uint8_t *data, int64_t rows, int64_t cols,
                    int64_t row_bytes, const float *x, float *y,
                    int64_t row_count, int threads) {
     int bs = go_block_size(type_id);
-    if (bs == 0) return GO_ERR_UNSUPPORTED;
+    if (bs == 0 || type_id == GO_Q5_K || type_id == GO_Q6_K) return GO_ERR_UNSUPPORTED;
     if (cols % bs != 0) return GO_ERR_ARG;
     if (row_count < 0 || row_count > rows) return GO_ERR_ARG;
     if (row_count == 0) return GO_OK;

@@ -21,6 +21,11 @@
  *   go_dot_row /         reference closed-form dots (384, 128, 16/48, 32/64,
  *   go_matvec_rows       +-2464, -264, lane-order dots) and an fp64 dot over
  *                        the bit-exact dequantized rows at 1e-3.
+ *   go_dequantize_row    Q5_K / Q6_K: the reference's lane-order fixtures
+ *   (Q5_K, Q6_K)         (TST/GgufQ5LaneFx, GgufQ5CalcFx, GgufQ6LaneFx,
+ *                        GgufQ5KOffTest) and the numpy restatement of the
+ *                        ggml block formulas (tests/npref.py).  go_dot_row
+ *                        and go_matvec_rows do not take these types.
  *   go_moe_select_topk   closed forms (uniform logits: ids 0..k-1 by the
  *                        stable tie order, weights 1/k; distinct logits:
  *                        numpy's stable descending argsort and fp64
@@ -43,7 +48,7 @@ extern "C" {
 #endif
 
 /* ggml type ids (GC/core/GgmlType.java:11,16,21). */
-enum { GO_Q4_0 = 2, GO_Q8_0 = 8, GO_Q4_K = 12 };
+enum { GO_Q4_0 = 2, GO_Q8_0 = 8, GO_Q4_K = 12, GO_Q5_K = 13, GO_Q6_K = 14 };
 
 /* Status codes shared with the oracle's Python wrapper. */
 enum {

@@ -85,6 +85,70 @@ def q8_pattern_block(scale: int, seed: int) -> list[int]:
     return le16(scale) + [(seed + 41 * i) & 0xFF for i in range(32)]
 
 
+def q5k_lane_block(has_mins: bool) -> list[int]:
+    """GgufQ5LaneFx.writeNoMinBlock / writeMinBlock (TST/GgufQ5LaneFx.java:13-24,
+    TST/GgufQ5Fx.java:13-55, TST/GgufQ5CalcFx.java:10-17)."""
+    b = [0] * 176
+    if has_mins:  # writeBlockWithMin(scale 2, min 1): d = dmin = 1.0
+        b[0:2], b[2:4] = le16(0x3C00), le16(0x3C00)
+        for i in range(4):
+            b[4 + i], b[8 + i], b[12 + i] = 2, 1, (1 << 4) | 2
+    else:         # writeBlock: d = 1.0, dmin = 0, scale codes 1
+        b[0:2], b[2:4] = le16(0x3C00), le16(0)
+        b[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    for i in range(32):
+        b[16 + i] = (i * 73 + 0x5A) & 0xFF
+    for i in range(128):
+        lo = i & 0x0F
+        b[48 + i] = lo | ((15 - lo) << 4)
+    return b
+
+
+def q5k_lane_row(has_mins: bool) -> list[float]:
+    """GgufQ5CalcFx.expectedRow (:27-66)."""
+    row = [0.0] * 256
+    for sb in range(0, 256, 64):
+        qb = (sb // 64) * 32
+        sl, shh = sb // 32, sb // 32 + 1
+        for i in range(32):
+            hb = (i * 73 + 0x5A) & 0xFF
+            lo = ((qb + i) & 0x0F) + (((hb >> sl) & 1) << 4)
+            hi = (15 - ((qb + i) & 0x0F)) + (((hb >> shh) & 1) << 4)
+            row[sb + i] = 2.0 * lo - 1.0 if has_mins else float(lo)
+            row[sb + 32 + i] = 2.0 * hi - 1.0 if has_mins else float(hi)
+    return row
+
+
+def q6k_lane_block() -> list[int]:
+    """GgufQ6Fx.writeLaneOrderBlock (TST/GgufQ6Fx.java:26-38)."""
+    b = [0] * 210
+    for i in range(128):
+        lo = i & 0x0F
+        b[i] = lo | ((15 - lo) << 4)
+    for i in range(64):
+        b[128 + i] = (i * 53 + 0xA7) & 0xFF
+    for i in range(16):
+        b[192 + i] = 1
+    b[208:210] = le16(0x3C00)
+    return b
+
+
+def q6k_lane_row() -> list[float]:
+    """GgufQ6LaneFx.expectedRow (TST/GgufQ6LaneFx.java:30-48)."""
+    row = [0.0] * 256
+    for sb in range(0, 256, 128):
+        lb, hbase = (sb // 128) * 64, (sb // 128) * 32
+        for i in range(32):
+            a = q6k_lane_block()[lb + i]
+            bb = q6k_lane_block()[lb + 32 + i]
+            hb = q6k_lane_block()[128 + hbase + i]
+            row[sb + i] = float(((a & 0x0F) | ((hb & 3) << 4)) - 32)
+            row[sb + 32 + i] = float(((bb & 0x0F) | (((hb >> 2) & 3) << 4)) - 32)
+            row[sb + 64 + i] = float(((a >> 4) | (((hb >> 4) & 3) << 4)) - 32)
+            row[sb + 96 + i] = float(((bb >> 4) | (((hb >> 6) & 3) << 4)) - 32)
+    return row
+
+
 def ones(n: int) -> list[float]:
     return [1.0] * n
 
@@ -196,6 +260,28 @@ def fixtures() -> list[dict]:
     nan_bits = struct.unpack("<f", struct.pack("<I", 0x7FC00000))[0]
     add("f16_special_scales", "TST/GgufF16SpecialTest.java:18-44 (RT/GgufQuantTables.java:142-164)",
         Q8_0, 32, 6, data, expected_dequant=[[v if v == v else nan_bits] * 32 for v in vals])
+    for has_mins in (False, True):
+        row = q5k_lane_row(has_mins)
+        dot = float(sum(np.float64(a) * b for a, b in zip(row, ramp(256))))
+        assert abs(dot) < 2 ** 24 and dot == int(dot)
+        add(f"q5k_lane_order_{'min' if has_mins else 'nomin'}",
+            "TST/GgufQ5LaneFx.java:13-24 (TST/GgufQ5CalcFx.java:10-66, TST/GgufQ5Fx.java:13-55)",
+            13, 256, 1, q5k_lane_block(has_mins), vector=ramp(256), expected_dequant=[row],
+            expected_matvec=[dot])
+    q5_off = [0] * 176
+    q5_off[0:2] = le16(0x3C00)
+    q5_off[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    q5_off[16:48] = [0xFF] * 32
+    q5_off[48:176] = [0x11] * 128
+    add("q5k_offset_second_block", "TST/GgufQ5KOffTest.java:19-33 (the tensor's block at offset 176)",
+        13, 256, 1, q5_off, vector=ones(256), expected_dequant=[[17.0] * 256],
+        expected_matvec=[4352.0])
+    row = q6k_lane_row()
+    dot = float(sum(np.float64(a) * b for a, b in zip(row, ramp(256))))
+    assert abs(dot) < 2 ** 24 and dot == int(dot)
+    add("q6k_lane_order", "TST/GgufQ6LaneTest.java:20-41 (TST/GgufQ6LaneFx.java:10-48, TST/GgufQ6Fx.java:26-43)",
+        14, 256, 1, q6k_lane_block(), vector=ramp(256), expected_dequant=[row],
+        expected_matvec=[dot])
     return fx
 
 

@@ -248,10 +248,10 @@ def test_upload_checks_the_tensor_range_before_the_device(tmp_path):
 
 def test_upload_rejects_types_without_a_kernel_before_the_device(tmp_path):
     blobs = [("norm", (64,), F32, bytes(256)), ("h", (64, 2), F16, bytes(256)),
-             ("q6", (256, 2), 14, bytes(420))]
+             ("q2", (256, 2), 10, bytes(168))]
     data = gw.gguf_file([], blobs)[0]
     with ops.GgufFile(_write(tmp_path, data)) as f:
-        for name, tid in (("norm", 0), ("h", 1), ("q6", 14)):
+        for name, tid in (("norm", 0), ("h", 1), ("q2", 10)):
             with pytest.raises(ops.UnsupportedOperationError, match=f"type id: {tid}$"):
                 f.upload(f.find(name))
 

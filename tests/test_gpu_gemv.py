@@ -373,3 +373,35 @@ def test_device_pointer_entry_points_match_host():
         assert_same_bits(deq.cpu().numpy(), exp)
         dw.close()
         host_t.close()
+
+
+# ---- Q5_K / Q6_K -----------------------------------------------------------
+
+K56_SHAPES = [(syn.Q5_K, 1, 256), (syn.Q5_K, 7, 768), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 33, 16384),
+              (syn.Q5_K, 1003, 2304), (syn.Q6_K, 1, 256), (syn.Q6_K, 5, 768), (syn.Q6_K, 4096, 4096),
+              (syn.Q6_K, 37, 16384), (syn.Q6_K, 1001, 2304), (syn.Q6_K, 14336, 4096)]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", K56_SHAPES,
+                         ids=[f"{'q5_k' if t == syn.Q5_K else 'q6_k'}_{r}x{c}" for t, r, c in K56_SHAPES])
+def test_q5_k_q6_k_dequant_and_gemv(type_id, rows, cols):
+    # Odd superblock counts (3, 9) put every other Q6_K superblock at a 2-byte
+    # aligned offset; the last row exercises the realigned reads at the end.
+    print(f"[gpu] k56 type={type_id} {rows}x{cols}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=rows * 3 + cols + type_id)
+    x = syn.activation(cols, seed=rows + 9)
+    t = _tensor(type_id, data, cols)
+    for r0, n in {(0, min(rows, 64)), (max(0, rows - 3), min(rows, 3))}:
+        assert_same_bits(ops.dequantize_rows(t, r0, n), o.dequantize(type_id, data, cols, r0, n),
+                         (type_id, r0))
+    y = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    assert o.rel_err(y, ref) <= GEMV_TOL, o.rel_err(y, ref)
+    part = np.full(rows, -3.0, np.float32)
+    ops.mat_vec_rows(t, x, part, rows // 2, True)
+    assert np.array_equal(part[:rows // 2], y[:rows // 2])
+    assert np.all(part[rows // 2:] == -3.0)
+    r = rows - 1
+    assert ops.dot_row(t, r, x) == pytest.approx(float(y[r]), rel=1e-6, abs=1e-6)
+    t.close()

@@ -37,7 +37,10 @@ def test_golden_matvec(golden):
     for fx in golden:
         if fx["expected_matvec"] is None:
             continue
-        y = o.matvec(fx["type_id"], _data(fx), fx["cols"], _vec(fx), fx["row_count"])
+        if fx["type_id"] in (syn.Q5_K, syn.Q6_K):  # no Java-order dot in the oracle: fp64 dot
+            y = o.matvec_fp64(fx["type_id"], _data(fx), fx["cols"], _vec(fx))[:fx["row_count"]]
+        else:
+            y = o.matvec(fx["type_id"], _data(fx), fx["cols"], _vec(fx), fx["row_count"])
         exp = np.asarray(fx["expected_matvec"], dtype=np.float64)
         # JUnit assertEquals(expected, actual, delta): absolute difference.
         assert np.all(np.abs(y - exp) <= fx["tolerance"]), (fx["name"], y, exp)
@@ -46,7 +49,7 @@ def test_golden_matvec(golden):
 def test_golden_single_row_dot_matches_matvec(golden):
     # TST/GgufFx.java:26-35: single-row matVecRows equals dotRow exactly.
     for fx in golden:
-        if fx["vector"] is None:
+        if fx["vector"] is None or fx["type_id"] in (syn.Q5_K, syn.Q6_K):
             continue
         data, cols = _data(fx), fx["cols"]
         rb = o.row_bytes(fx["type_id"], cols)
@@ -74,7 +77,7 @@ def test_k4_scale_min_round_trip():
             assert o.k4_scale_min(packed, j) == (sc[j], mn[j])
 
 
-@pytest.mark.parametrize("type_id", [syn.Q8_0, syn.Q4_0, syn.Q4_K])
+@pytest.mark.parametrize("type_id", [syn.Q8_0, syn.Q4_0, syn.Q4_K, syn.Q5_K, syn.Q6_K])
 def test_dequant_matches_numpy_restatement(type_id):
     cols = 512
     data = syn.matrix(type_id, 33, cols, seed=11 + type_id)
