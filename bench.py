@@ -417,7 +417,9 @@ def main() -> int:
     if not args.no_extra:
         for name, t, rows, cols in (("q8_0_gemv_4096x4096", syn.Q8_0, 4096, 4096),
                                     ("q4_0_gemv_4096x11008", syn.Q4_0, 11008, 4096),
-                                    ("q4_k_gemv_4096x128256", syn.Q4_K, 128256, 4096)):
+                                    ("q4_k_gemv_4096x128256", syn.Q4_K, 128256, 4096),
+                                    ("q6_k_gemv_14336x4096", syn.Q6_K, 4096, 14336),
+                                    ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, 4096)):
             if not want(name):
                 continue
             log(f"extra {name}")

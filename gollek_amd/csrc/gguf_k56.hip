@@ -265,20 +265,30 @@ bool gemv_k56_supported(int type_id, int64_t row_bytes, const void *w, const flo
 hipError_t launch_gemv_k56(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                            const float *x, float *y, int64_t rows, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    constexpr int R = 4;
+    // Rows per batch R: 4 (x reused over 4 rows) when that still gives the
+    // target wave count, else fewer, so small matrices keep enough waves in
+    // flight to cover the load latency.
     const LaunchTuning &t = tuning();
     const int64_t target_waves = (int64_t)t.cu_count * t.gemv_waves_per_cu;
+    const int R = rows >= 4 * target_waves ? 4 : (rows >= 2 * target_waves ? 2 : 1);
     int64_t rpw = (rows + target_waves - 1) / target_waves;
     rpw = (rpw + R - 1) / R * R;
     const int64_t waves = (rows + rpw - 1) / rpw;
     const unsigned grid = (unsigned)((waves + 3) / 4);
     const int nsb = (int)(cols / kQK);
-    if (type_id == kQ5_K)
-        hipLaunchKernelGGL((gemv_k56_kernel<kQ5_K, R>), dim3(grid), dim3(256), 0, stream, w,
-                           row_bytes, nsb, x, y, rows, rpw);
-    else
-        hipLaunchKernelGGL((gemv_k56_kernel<kQ6_K, R>), dim3(grid), dim3(256), 0, stream, w,
-                           row_bytes, nsb, x, y, rows, rpw);
+#define GOLLEK_K56_LAUNCH(TY, RR)                                                                \
+    hipLaunchKernelGGL((gemv_k56_kernel<TY, RR>), dim3(grid), dim3(256), 0, stream, w, row_bytes, \
+                       nsb, x, y, rows, rpw)
+    if (type_id == kQ5_K) {
+        if (R == 4) GOLLEK_K56_LAUNCH(kQ5_K, 4);
+        else if (R == 2) GOLLEK_K56_LAUNCH(kQ5_K, 2);
+        else GOLLEK_K56_LAUNCH(kQ5_K, 1);
+    } else {
+        if (R == 4) GOLLEK_K56_LAUNCH(kQ6_K, 4);
+        else if (R == 2) GOLLEK_K56_LAUNCH(kQ6_K, 2);
+        else GOLLEK_K56_LAUNCH(kQ6_K, 1);
+    }
+#undef GOLLEK_K56_LAUNCH
     return hipGetLastError();
 }
 
