@@ -7,7 +7,8 @@
  * gguf/runtime/).  The Java facade RT/GgufTensorOps keeps its signatures; an
  * FFM (java.lang.foreign) binding calls these functions from inside
  * RT/GgufMatVec.rows (RT/GgufMatVec.java:55-96) for ggml type ids 2 (Q4_0),
- * 8 (Q8_0) and 12 (Q4_K), ahead of the prepared and raw Java routes.
+ * 8 (Q8_0), 12 (Q4_K), 13 (Q5_K) and 14 (Q6_K), ahead of the prepared and raw
+ * Java routes.
  *
  * Conventions (those of the reference's own native bridge,
  * runner/gguf/gguf-fast-bridge/gollek_gguf_fast.cpp:672-800):
