@@ -135,21 +135,24 @@ __device__ __forceinline__ int unit_x_offset(int part, int k) {
     return 128 * h + 32 * (k >> 4) + 16 * p + (k & 15);   // groups of 16
 }
 
-// Sum over the unit's 64 elements of dequantized weight * x.
+// Sum over the unit's 64 elements of dequantized weight * x; xl / xh are
+// the sums of the unit's low / high 32 x values (Q5_K min terms).
 template <int TYPE>
-__device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const float *xv) {
+__device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const float *xv, float xl,
+                                          float xh) {
     if (TYPE == kQ5_K) {
         const int c = part;
-        const float d = half_bits_to_float_fast(ld_u16(blk));
-        const float dmin = half_bits_to_float_fast(ld_u16(blk + 2));
-        int sc1, mc1, sc2, mc2;
-        q4k_code(blk + 4, 2 * c, &sc1, &mc1);
-        q4k_code(blk + 4, 2 * c + 1, &sc2, &mc2);
+        const uint4 hd = load16_even(blk);  // d | dmin | 12 scale bytes
+        const float d = half_bits_to_float_fast(hd.x & 0xFFFFu);
+        const float dmin = half_bits_to_float_fast(hd.x >> 16);
+        uint32_t scp, mnp;
+        q4k_pair_codes(hd.y, hd.z, hd.w, c, &scp, &mnp);
+        const uint32_t sc1 = scp & 0xFFu, sc2 = scp >> 8, mc1 = mnp & 0xFFu, mc2 = mnp >> 8;
         const uint4 h0 = load16_even(blk + 16);
         const uint4 h1 = load16_even(blk + 32);
         const uint4 q0 = load16_even(blk + 48 + 32 * c);
         const uint4 q1 = load16_even(blk + 64 + 32 * c);
-        float al = 0.0f, ah = 0.0f, xl = 0.0f, xh = 0.0f;
+        float al = 0.0f, ah = 0.0f;
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const int v = byte_of(i < 16 ? q0 : q1, i & 15);
@@ -158,8 +161,6 @@ __device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const fl
             const int hi = (v >> 4) + (((hb >> (2 * c + 1)) & 1) << 4);
             al = fmaf((float)lo, xv[i], al);
             ah = fmaf((float)hi, xv[32 + i], ah);
-            xl += xv[i];
-            xh += xv[32 + i];
         }
         const bool mins = !(dmin == 0.0f);
         const float m1 = (mins && mc1) ? dmin * (float)mc1 : 0.0f;
@@ -215,11 +216,19 @@ __global__ __launch_bounds__(256) void gemv_k56_kernel(const uint8_t *__restrict
                 xv[k + 2] = v.z;
                 xv[k + 3] = v.w;
             }
+            float xl = 0.0f, xh = 0.0f;
+            if (TYPE == kQ5_K) {
+#pragma unroll
+                for (int k = 0; k < 32; k++) {
+                    xl += xv[k];
+                    xh += xv[32 + k];
+                }
+            }
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const int64_t r = r0 + i;
                 if (r < row_end)
-                    acc[i] += unit_dot<TYPE>(w + r * row_bytes + (int64_t)sb * BB, part, xv);
+                    acc[i] += unit_dot<TYPE>(w + r * row_bytes + (int64_t)sb * BB, part, xv, xl, xh);
             }
         }
 #pragma unroll
