@@ -52,6 +52,18 @@ __device__ __forceinline__ uint4 load16_even(const uint8_t *p) {
                       __builtin_amdgcn_alignbyte(v3, v2, 2), __builtin_amdgcn_alignbyte(v4, v3, 2));
 }
 
+// load16_even without a branch, for waves whose lanes mix both alignments:
+// always five dword loads, the fifth re-reading the fourth when p is 4-byte
+// aligned (so it never leaves the piece), then a shift by p & 3 bytes.
+__device__ __forceinline__ uint4 load16_even_uniform(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~static_cast<uintptr_t>(3));
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint32_t v0 = q[0], v1 = q[1], v2 = q[2], v3 = q[3], v4 = q[3 + (sh >> 1)];
+    return make_uint4(__builtin_amdgcn_alignbyte(v1, v0, sh), __builtin_amdgcn_alignbyte(v2, v1, sh),
+                      __builtin_amdgcn_alignbyte(v3, v2, sh), __builtin_amdgcn_alignbyte(v4, v3, sh));
+}
+
 __device__ __forceinline__ int byte_of(const uint4 v, int j) {
     const uint32_t w = j < 4 ? v.x : (j < 8 ? v.y : (j < 12 ? v.z : v.w));
     return (int)((w >> (8 * (j & 3))) & 0xFFu);
@@ -168,10 +180,10 @@ __device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const fl
         return d * (float)sc1 * al + d * (float)sc2 * ah - (m1 * xl + m2 * xh);
     } else {
         const int h = part >> 1, p = part & 1;
-        const uint4 la = load16_even(blk + 64 * h + 16 * p);
-        const uint4 lb = load16_even(blk + 64 * h + 32 + 16 * p);
-        const uint4 hq = load16_even(blk + 128 + 32 * h + 16 * p);
-        const uint4 sv = load16_even(blk + 192);
+        const uint4 la = load16_even_uniform(blk + 64 * h + 16 * p);
+        const uint4 lb = load16_even_uniform(blk + 64 * h + 32 + 16 * p);
+        const uint4 hq = load16_even_uniform(blk + 128 + 32 * h + 16 * p);
+        const uint4 sv = load16_even_uniform(blk + 192);
         const float d = half_bits_to_float_fast(ld_u16(blk + 208));
         const uint32_t sw0 = h ? sv.z : sv.x, sw1 = h ? sv.w : sv.y;
         const float s1 = (float)(int8_t)(sw0 >> (8 * p)), s2 = (float)(int8_t)(sw0 >> (8 * (2 + p)));
