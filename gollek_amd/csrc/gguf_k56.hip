@@ -64,11 +64,6 @@ __device__ __forceinline__ uint4 load16_even_uniform(const uint8_t *p) {
                       __builtin_amdgcn_alignbyte(v3, v2, sh), __builtin_amdgcn_alignbyte(v4, v3, sh));
 }
 
-__device__ __forceinline__ int byte_of(const uint4 v, int j) {
-    const uint32_t w = j < 4 ? v.x : (j < 8 ? v.y : (j < 12 ? v.z : v.w));
-    return (int)((w >> (8 * (j & 3))) & 0xFFu);
-}
-
 // ---- dequantization ----------------------------------------------------------
 
 // One thread per (row, superblock, chunk c): 64 outputs.
@@ -147,11 +142,15 @@ __device__ __forceinline__ int unit_x_offset(int part, int k) {
     return 128 * h + 32 * (k >> 4) + 16 * p + (k & 15);   // groups of 16
 }
 
-// Sum over the unit's 64 elements of dequantized weight * x; xl / xh are
-// the sums of the unit's low / high 32 x values (Q5_K min terms).
+// Sum over the unit's 64 elements of dequantized weight * x.  xs[g] is the
+// sum of the unit's x values of group g (Q5_K: 2 groups of 32, for the min
+// terms; Q6_K: 4 groups of 16, for the -32 offset).  Codes are formed four
+// at a time in 32-bit words (nibble masks and the high bits shifted into
+// bit 4 / bits 4-5 of each byte; no carries cross a byte) and converted with
+// v_cvt_f32_ubyteN.
 template <int TYPE>
-__device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const float *xv, float xl,
-                                          float xh) {
+__device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const float *xv,
+                                          const float *xs) {
     if (TYPE == kQ5_K) {
         const int c = part;
         const uint4 hd = load16_even(blk);  // d | dmin | 12 scale bytes
@@ -164,20 +163,24 @@ __device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const fl
         const uint4 h1 = load16_even(blk + 32);
         const uint4 q0 = load16_even(blk + 48 + 32 * c);
         const uint4 q1 = load16_even(blk + 64 + 32 * c);
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         float al = 0.0f, ah = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const int v = byte_of(i < 16 ? q0 : q1, i & 15);
-            const int hb = byte_of(i < 16 ? h0 : h1, i & 15);
-            const int lo = (v & 0x0F) + (((hb >> (2 * c)) & 1) << 4);
-            const int hi = (v >> 4) + (((hb >> (2 * c + 1)) & 1) << 4);
-            al = fmaf((float)lo, xv[i], al);
-            ah = fmaf((float)hi, xv[32 + i], ah);
+        for (int wi = 0; wi < 8; wi++) {
+            const uint32_t lo = opaque((qw[wi] & 0x0F0F0F0Fu) | (((hw[wi] >> (2 * c)) & 0x01010101u) << 4));
+            const uint32_t hi =
+                opaque(((qw[wi] >> 4) & 0x0F0F0F0Fu) | (((hw[wi] >> (2 * c + 1)) & 0x01010101u) << 4));
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                al = fmaf(byte_f(lo, b), xv[4 * wi + b], al);
+                ah = fmaf(byte_f(hi, b), xv[32 + 4 * wi + b], ah);
+            }
         }
         const bool mins = !(dmin == 0.0f);
         const float m1 = (mins && mc1) ? dmin * (float)mc1 : 0.0f;
         const float m2 = (mins && mc2) ? dmin * (float)mc2 : 0.0f;
-        return d * (float)sc1 * al + d * (float)sc2 * ah - (m1 * xl + m2 * xh);
+        return d * (float)sc1 * al + d * (float)sc2 * ah - (m1 * xs[0] + m2 * xs[1]);
     } else {
         const int h = part >> 1, p = part & 1;
         const uint4 la = load16_even_uniform(blk + 64 * h + 16 * p);
@@ -188,16 +191,27 @@ __device__ __forceinline__ float unit_dot(const uint8_t *blk, int part, const fl
         const uint32_t sw0 = h ? sv.z : sv.x, sw1 = h ? sv.w : sv.y;
         const float s1 = (float)(int8_t)(sw0 >> (8 * p)), s2 = (float)(int8_t)(sw0 >> (8 * (2 + p)));
         const float s3 = (float)(int8_t)(sw1 >> (8 * p)), s4 = (float)(int8_t)(sw1 >> (8 * (2 + p)));
+        const uint32_t aw[4] = {la.x, la.y, la.z, la.w}, bw[4] = {lb.x, lb.y, lb.z, lb.w};
+        const uint32_t hw[4] = {hq.x, hq.y, hq.z, hq.w};
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int a = byte_of(la, j), b = byte_of(lb, j), hb = byte_of(hq, j);
-            a0 = fmaf((float)(((a & 0x0F) | ((hb & 3) << 4)) - 32), xv[j], a0);
-            a1 = fmaf((float)(((b & 0x0F) | (((hb >> 2) & 3) << 4)) - 32), xv[16 + j], a1);
-            a2 = fmaf((float)(((a >> 4) | (((hb >> 4) & 3) << 4)) - 32), xv[32 + j], a2);
-            a3 = fmaf((float)(((b >> 4) | (((hb >> 6) & 3) << 4)) - 32), xv[48 + j], a3);
+        for (int wi = 0; wi < 4; wi++) {
+            const uint32_t A = aw[wi], B = bw[wi], H = hw[wi];
+            const uint32_t g0 = opaque((A & 0x0F0F0F0Fu) | ((H & 0x03030303u) << 4));
+            const uint32_t g1 = opaque((B & 0x0F0F0F0Fu) | (((H >> 2) & 0x03030303u) << 4));
+            const uint32_t g2 = opaque(((A >> 4) & 0x0F0F0F0Fu) | (((H >> 4) & 0x03030303u) << 4));
+            const uint32_t g3 = opaque(((B >> 4) & 0x0F0F0F0Fu) | (((H >> 6) & 0x03030303u) << 4));
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                a0 = fmaf(byte_f(g0, b), xv[4 * wi + b], a0);
+                a1 = fmaf(byte_f(g1, b), xv[16 + 4 * wi + b], a1);
+                a2 = fmaf(byte_f(g2, b), xv[32 + 4 * wi + b], a2);
+                a3 = fmaf(byte_f(g3, b), xv[48 + 4 * wi + b], a3);
+            }
         }
-        return d * (s1 * a0 + s2 * a1 + s3 * a2 + s4 * a3);
+        // sum (q - 32) x = sum q x - 32 sum x per group
+        return d * (s1 * (a0 - 32.0f * xs[0]) + s2 * (a1 - 32.0f * xs[1]) +
+                    s3 * (a2 - 32.0f * xs[2]) + s4 * (a3 - 32.0f * xs[3]));
     }
 }
 
@@ -228,19 +242,20 @@ __global__ __launch_bounds__(256) void gemv_k56_kernel(const uint8_t *__restrict
                 xv[k + 2] = v.z;
                 xv[k + 3] = v.w;
             }
-            float xl = 0.0f, xh = 0.0f;
-            if (TYPE == kQ5_K) {
+            // group sums of x: Q5_K 2 x 32 (slots 0-31, 32-63), Q6_K 4 x 16
+            constexpr int NG = TYPE == kQ5_K ? 2 : 4;
+            float xs[NG];
 #pragma unroll
-                for (int k = 0; k < 32; k++) {
-                    xl += xv[k];
-                    xh += xv[32 + k];
-                }
+            for (int g = 0; g < NG; g++) {
+                xs[g] = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 64 / NG; k++) xs[g] += xv[g * (64 / NG) + k];
             }
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const int64_t r = r0 + i;
                 if (r < row_end)
-                    acc[i] += unit_dot<TYPE>(w + r * row_bytes + (int64_t)sb * BB, part, xv, xl, xh);
+                    acc[i] += unit_dot<TYPE>(w + r * row_bytes + (int64_t)sb * BB, part, xv, xs);
             }
         }
 #pragma unroll
