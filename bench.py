@@ -57,6 +57,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--only", default="", help="comma list of workload names to run")
     p.add_argument("--eager", action="store_true",
                    help="launch each step directly instead of replaying a HIP graph")
+    p.add_argument("--ceilings", action="store_true",
+                   help="only measure the device's attainable figures: single-launch HBM read "
+                        "time by size and grid (plain streaming kernels), the empty-launch "
+                        "floor, and a hipBLASLt bf16 GEMM at M = 512 (one JSON line each)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 256 MiB device-to-device copy 10 times (known HBM bytes, "
                         "used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -99,52 +103,58 @@ def warm_device(torch, seconds: float) -> float:
     return time.perf_counter() - t0
 
 
+MIN_WARM_SECONDS = 0.05  # untimed replays of each workload before its timed region
+
+
 def graph_time(torch, launch, copies: int, steps: int, warmup: int):
-    """Capture `copies` launches (one per weight copy) in a graph, replay it;
-    returns (ms per launch, launches timed).  With EAGER the launches are made
-    directly on the stream instead."""
-    reps = max(1, math.ceil(steps / copies))
-    wreps = max(1, math.ceil(warmup / copies))
+    """Times exactly `steps` launches; returns (ms per launch, launches timed).
+
+    Launch i uses weight copy i % copies.  Untimed first: one eager pass over
+    every copy, then replays of a graph of one full rotation until at least
+    `warmup` launches and MIN_WARM_SECONDS have passed.  Timed: one replay of
+    a graph of exactly `steps` launches starting at copy 0, so every copy is
+    reused only after the others (>= 512 MiB) have been streamed, bracketed
+    by HIP events on the launch stream.  With EAGER the timed launches are
+    made directly on the stream instead of from a graph."""
+    steps = max(1, int(steps))
     stream = torch.cuda.Stream()
-    if EAGER:
-        with torch.cuda.stream(stream):
-            for _ in range(wreps):
-                for i in range(copies):
-                    launch(i, stream.cuda_stream)
-            stream.synchronize()
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record(stream)
-            for _ in range(reps):
-                for i in range(copies):
-                    launch(i, stream.cuda_stream)
-            end.record(stream)
-        end.synchronize()
-        return start.elapsed_time(end) / (reps * copies), reps * copies
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         for i in range(copies):  # eager warm-up before capture
             launch(i, stream.cuda_stream)
     stream.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
+    warm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(warm, stream=stream):
         s = torch.cuda.current_stream().cuda_stream
         for i in range(copies):
             launch(i, s)
+    done, t0 = 0, time.perf_counter()
     with torch.cuda.stream(stream):
-        for _ in range(wreps):
+        while done < warmup or time.perf_counter() - t0 < MIN_WARM_SECONDS:
+            warm.replay()
+            stream.synchronize()
+            done += copies
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    if EAGER:
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for i in range(steps):
+                launch(i % copies, stream.cuda_stream)
+            end.record(stream)
+    else:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(steps):
+                launch(i % copies, s)
+        with torch.cuda.stream(stream):
+            start.record(stream)
             g.replay()
-        stream.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(reps):
-            g.replay()
-        end.record(stream)
+            end.record(stream)
     end.synchronize()
     torch.cuda.synchronize()
-    n = reps * copies
-    return start.elapsed_time(end) / n, n
+    return start.elapsed_time(end) / steps, steps
 
 
 # ---- workloads ----------------------------------------------------------------
@@ -207,8 +217,10 @@ def moe_workload(torch, steps: int, warmup: int, seed: int):
     down = syn.q4_k_matrix(E * H, I, seed + 2)
     ids, w = syn.moe_routing(T, E, k, seed + 3)
     x = syn.activation(T * H, seed + 4).reshape(T, H)
-    # Two copies of the whole layer (2 x 340 MB) defeat the Infinity Cache.
-    copies = 2
+    # Three copies of the whole layer (3 x 340 MB): a copy is reused only after
+    # the other two layers' touched experts (> 400 MB) have streamed, so the
+    # 256 MB Infinity Cache cannot serve it.
+    copies = 3
     layers = []
     for _ in range(copies):
         bufs = [torch.from_numpy(a.reshape(-1)).cuda() for a in (gate, up, down)]
@@ -363,6 +375,86 @@ def cpu_baseline(host, cols: int):
     }
 
 
+def ceilings(torch, steps: int, warmup: int) -> int:
+    """Attainable HBM read time per launch (libgollek_ceiling.so: plain
+    streaming reads, every load issued up front) by size, load kind and grid;
+    the empty-launch floor; a hipBLASLt bf16 GEMM (torch.nn.functional.linear)
+    at M = 512, K = N = 4096 on pre-dequantized weights.  Timed exactly like
+    the workloads (graph_time over a >= 640 MiB rotation)."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(REPO / "gollek_amd" / "libgollek_ceiling.so"))
+    lib.gollek_ceiling_loads_per_lane.restype = ctypes.c_int64
+    lib.gollek_ceiling_loads_per_lane.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                                  ctypes.c_int32]
+    lib.gollek_ceiling_launch.restype = ctypes.c_int32
+    lib.gollek_ceiling_launch.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                          ctypes.c_void_p]
+    kinds = {0: "reg_nt", 1: "reg", 2: "lds_nt", 3: "empty"}
+    out = torch.empty(16384 * 1024, dtype=torch.int32, device="cuda")
+    best = {}
+
+    def run(kind, nbytes, bufs, blocks, wpb):
+        if lib.gollek_ceiling_loads_per_lane(kind, nbytes, blocks, wpb) < 0:
+            return
+        ptrs = [b.data_ptr() for b in bufs]
+        if lib.gollek_ceiling_launch(kind, ptrs[0], nbytes, out.data_ptr(), blocks, wpb, None) != 0:
+            return
+        torch.cuda.synchronize()
+
+        def launch(i, st):
+            lib.gollek_ceiling_launch(kind, ptrs[i], nbytes, out.data_ptr(), blocks, wpb, st)
+
+        ms, n = graph_time(torch, launch, len(ptrs), steps, warmup)
+        rec = {"ceiling": "hbm_read", "kind": kinds[kind], "bytes": nbytes, "blocks": blocks,
+               "waves_per_block": wpb, "us": round(ms * 1e3, 3), "steps": n,
+               "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1) if nbytes else None}
+        print(json.dumps(rec), flush=True)
+        key = (kinds[kind] if kind == 3 else "read", nbytes)
+        if key not in best or rec["us"] < best[key]["us"]:
+            best[key] = rec
+
+    sizes = (33030144, 2 * 2 ** 20, 8 * 2 ** 20, 17825792, 25362432, 64 * 2 ** 20,
+             128 * 2 ** 20, 295501824)
+    for nbytes in sizes:
+        copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        for b in bufs:
+            b.fill_(0x5A)
+        kset = (0, 1, 2) if nbytes == 33030144 else (0, 2)
+        for kind in kset:
+            for wpb in (4, 8, 16):
+                for blocks in (256, 512, 768, 1024, 2048, 4096, 8192):
+                    run(kind, nbytes, bufs, blocks, wpb)
+        del bufs
+    for blocks in (256, 896, 1024, 4096):
+        run(3, 0, [out], blocks, 4)
+    # hipBLASLt bf16 GEMM, Y = X W^T, M = 512, K = N = 4096
+    M = K = N = 4096
+    M = 512
+    wbytes = 2 * N * K
+    copies = max(2, math.ceil(ROTATION_BYTES / wbytes))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    ws = [torch.randn(N, K, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(copies)]
+    xb = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16)
+    yb = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+
+    def gemm(i, st):
+        torch.nn.functional.linear(xb, ws[i], out=yb)
+
+    ms, n = graph_time(torch, gemm, copies, steps, warmup)
+    rec = {"ceiling": "bf16_gemm_hipblaslt", "m": M, "n": N, "k": K, "us": round(ms * 1e3, 3),
+           "steps": n, "tflops": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1),
+           "op": "torch.nn.functional.linear(bf16 X, bf16 W) -> bf16 Y"}
+    print(json.dumps(rec), flush=True)
+    summary = {"ceiling_summary": [best[k] for k in sorted(best, key=lambda k: (k[0], k[1]))],
+               "bf16_gemm_m512_tflops": rec["tflops"]}
+    print(json.dumps(summary), flush=True)
+    return 0
+
+
 def traffic_from_profile():
     """HBM bytes per launch of the headline kernel from the committed
     rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel
@@ -391,6 +483,9 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n,
                           "copies": 10}))
         return 0
+    if args.ceilings:
+        import torch
+        return ceilings(torch, min(args.steps, 400), args.warmup)
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: this path runs on one GPU; "
                                    f"--gpus {args.gpus} is not supported (use --gpus 1)"}))

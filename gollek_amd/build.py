@@ -17,6 +17,9 @@ REPO_DIR = PACKAGE_DIR.parent
 CSRC_DIR = PACKAGE_DIR / "csrc"
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_PATH = PACKAGE_DIR / "libgollek_hip.so"
+# Measurement kernels of bench.py --ceilings (not part of the product library).
+CEILING_LIB_PATH = PACKAGE_DIR / "libgollek_ceiling.so"
+CEILING_SOURCES = ("hbm_ceiling.hip",)
 OBJ_DIR = PACKAGE_DIR / "_build"
 
 HIP_SOURCES = (
@@ -69,10 +72,16 @@ def _compile_one(hipcc: str, src: Path, obj: Path) -> tuple[Path, str]:
 
 
 def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source and link libgollek_hip.so; returns its path."""
+    """Compile every HIP source and link libgollek_hip.so (and the measurement
+    library libgollek_ceiling.so); returns the product library's path."""
+    _link(CEILING_SOURCES, CEILING_LIB_PATH, verbose)
+    return _link(HIP_SOURCES, LIB_PATH, verbose)
+
+
+def _link(names, lib_path: Path, verbose: bool) -> Path:
     hipcc = _hipcc()
     OBJ_DIR.mkdir(exist_ok=True)
-    sources = [CSRC_DIR / s for s in HIP_SOURCES if (CSRC_DIR / s).exists()]
+    sources = [CSRC_DIR / s for s in names if (CSRC_DIR / s).exists()]
     jobs = min(len(sources), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(
@@ -80,14 +89,14 @@ def build_library(verbose: bool = False) -> Path:
     for obj, log in results:
         if verbose and log:
             print(f"[{obj.name}] {log}", file=sys.stderr)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC",
            *[str(o) for o, _ in results], "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":

@@ -3,7 +3,7 @@
 //
 // A vector x is held as "digit planes": per 32-element group g, a power-of-two
 // scale s_g = 2^(e-23) with max|x_g| < 2^e, the exact integers
-// X_i = trunc(x_i / s_g) (|X_i| < 2^23) split into three bytes
+// X_i = rint(x_i / s_g) (|X_i| < 2^23) split into three bytes
 // X = a' * 2^16 + b' * 2^8 + c' (c', b' unsigned, a' signed), and the fp32
 // group sum used by the Q4_K min term.  Nibbles are then contracted with
 // v_dot4_u32_u8 / v_dot4_i32_i8 exactly in int32; a group's value is
@@ -15,6 +15,14 @@
 namespace gollek {
 
 constexpr int kDigitWords = 24;  // per 32-element group: 8 c' + 8 b' + 8 a' dwords
+
+// Nearest integer to v (|v| < 2^23), kept inside the 24-bit two's-complement
+// range of the three digit bytes: +-2^23 (a rounding of the largest values)
+// becomes +-(2^23 - 1).
+__device__ __forceinline__ int round_digits23(float v) {
+    const int X = (int)rintf(v);
+    return X > 8388607 ? 8388607 : (X < -8388607 ? -8388607 : X);
+}
 
 __device__ __forceinline__ uint32_t pack_byte(const int *X, int byte) {
     const int sh = 8 * byte;
@@ -31,22 +39,27 @@ __device__ inline void build_x_digits(const float *__restrict__ x, int ngroups, 
         const float4 *px = reinterpret_cast<const float4 *>(x + 32 * G + 8 * part);
         const float4 a = px[0], b = px[1];
         const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        float mx = 0.0f, s = 0.0f;
+        // Maximum of |x| over the bit patterns: NaN and inf order above every
+        // finite value, so a non-finite element reaches the branch below
+        // (fmaxf would drop a NaN).
+        uint32_t mb = 0;
+        float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            mx = fmaxf(mx, fabsf(v[i]));
+            mb = max(mb, __float_as_uint(v[i]) & 0x7FFFFFFFu);
             s += v[i];
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
+        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
+        const float mx = __uint_as_float(mb);
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
         int e = 0;
         (void)frexpf(mx, &e);  // mx < 2^e, so |x / 2^(e-23)| < 2^23
-        const bool finite = mx <= 3.402823466e38f;
+        const bool finite = mb < 0x7F800000u;
         int X[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) X[i] = finite ? (int)ldexpf(v[i], 23 - e) : 0;
+        for (int i = 0; i < 8; i++) X[i] = finite ? round_digits23(ldexpf(v[i], 23 - e)) : 0;
         uint2 *out = reinterpret_cast<uint2 *>(dig + kDigitWords * G + 2 * part);
 #pragma unroll
         for (int byte = 0; byte < 3; byte++)
@@ -187,12 +200,13 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
     return v;
 }
 
-// Max / sum over aligned groups of eight lanes (quad xor 1, xor 2, then the
-// half-row mirror, which pairs lanes 0-3 with 7-4 of each eight).
-__device__ __forceinline__ float max8(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    return fmaxf(v, dpp_f<0x141>(v));
+// Max (of unsigned bit patterns) / sum over aligned groups of eight lanes
+// (quad xor 1, xor 2, then the half-row mirror, which pairs lanes 0-3 with
+// 7-4 of each eight).
+__device__ __forceinline__ uint32_t max8_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));
+    return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float sum8(float v) {
     v += dpp_f<0xB1>(v);
@@ -231,14 +245,17 @@ __device__ __forceinline__ void store_x_digits(const XPart<XL> &p, int ngroups, 
         const int t = threadIdx.x + i * NT;
         const int G = t >> 3, part = t & 7;
         const float v[4] = {p.v[i].x, p.v[i].y, p.v[i].z, p.v[i].w};
-        const float mx = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        // integer maximum of the |x| bits, so NaN and inf are not dropped
+        const uint32_t mb = max8_u32(max(max(__float_as_uint(v[0]) & 0x7FFFFFFFu, __float_as_uint(v[1]) & 0x7FFFFFFFu),
+                                         max(__float_as_uint(v[2]) & 0x7FFFFFFFu, __float_as_uint(v[3]) & 0x7FFFFFFFu)));
+        const float mx = __uint_as_float(mb);
         const float s = sum8((v[0] + v[1]) + (v[2] + v[3]));
         int e = 0;
         (void)frexpf(mx, &e);  // mx < 2^e, so |x / 2^(e-23)| < 2^23
-        const bool finite = mx <= 3.402823466e38f;
+        const bool finite = mb < 0x7F800000u;
         int X[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) X[k] = finite ? (int)ldexpf(v[k], 23 - e) : 0;
+        for (int k = 0; k < 4; k++) X[k] = finite ? round_digits23(ldexpf(v[k], 23 - e)) : 0;
         if (G < ngroups) {
             uint32_t *out = dig + kDigitWords * G + part;
 #pragma unroll

@@ -5,40 +5,50 @@
 // java/tech/kayys/gollek/gguf/runtime/):
 //   y[n] = sum_sb sum_j [ (d sc_j) (sum_{i in j} q_i x_i) - (m_j ? dmin m_j : 0) X_j ]
 // over the eight 32-element sub-blocks j of every superblock, X_j = sum of x
-// over sub-block j.  Tolerance parity (rel_err <= 1e-3).
+// over sub-block j.  Tolerance parity (rel_err <= 1e-3, and within twice the
+// reference's own fp32 error for K <= 4096).
 //
-// x.  Per superblock s (256 elements): a power-of-two scale xs = 2^(e-22)
-// with max |x| < 2^e, the integers X_i = trunc(x_i / xs) (|X_i| < 2^22, so the
-// per-element error is below 2^-21 of the superblock's max |x|) as balanced
-// signed bytes X = 65536 a + 256 b + c (c, b in [-128, 127], |a| <= 64), and
-// the sub-block sums xs * sum X_i.  Built once per workgroup in LDS.
+// Three kernels, by shape:
+//   * K <= 4096, at most 64 rows per CU (the 8B-class FFN shapes):
+//     gemv_q4_k_mfma_col_kernel, one superblock column per wave, the
+//     workgroup's share in LDS;
+//   * K <= 4096, more rows (lm_head): gemv_q4_k_mfma_tile_kernel, 16-row
+//     tiles streamed through a shared ring;
+//   * K up to 16384: gemv_q4_k_mfma_kernel, per-wave rings of 16 rows x 2
+//     superblocks with K split into parts when a workgroup has few tiles.
+// All three contract 16 weight rows against 64 columns of x per
+// v_mfma_i32_16x16x64_i8, with x as exact integers split into signed-byte
+// digit planes (the B operand holds the rows' nibbles as bytes 0..15; A row
+// m = 4 h + p holds plane p of sub-block 2 c + h and zeros on the other
+// sub-block's columns, so lane n + 16 h of D holds the plane sums of one
+// (row, sub-block)).  The K <= 4096 kernels use four planes of 30-bit
+// integers (their shared pieces are described further down); the K > 4096
+// kernel uses three planes of 22-bit integers:
 //
-// Matrix cores.  v_mfma_i32_16x16x64_i8 with B = 16 weight rows' nibbles
-// (0..15, one 64-column chunk: lane n + 16 g holds 16 nibbles of row n from
-// run g, i.e. chunk columns 16 g .. 16 g + 15, low nibbles for g < 2, high
-// for g >= 2) and A row m = 4 h + p = plane p of the x digits of sub-block
-// 2 c + h, zero on the other sub-block's columns.  D[4 h + p][n] is then the
-// plane-p sum over one sub-block of row n, sitting in lane n + 16 h, and
-// 65536 D2 + 256 D1 + D0 = sum q_i X_i exactly in int32 (|.| < 32 * 15 * 2^22
-// < 2^31).  A rows 3, 7 and 8..15 are zero.  Per 1024 weights a wave spends
-// one MFMA and ~20 VALU instructions (nibble masks, the plane combine, the
-// per-sub-block scale), about a third of the v_dot4 formulation's cost, so
-// the kernel is bound by HBM rather than by the VALU.
+// x (K > 4096).  Per superblock s (256 elements): a power-of-two scale
+// xs = 2^(e-22) with max |x| < 2^e, the integers X_i = rint(x_i / xs)
+// (|X_i| <= 2^22, so the per-element error is at most 2^-23 of the
+// superblock's max |x|) as balanced signed bytes X = 65536 a + 256 b + c
+// (c, b in [-128, 127], |a| <= 64), and the sub-block sums xs * sum X_i.
+// Built once per workgroup in LDS.  65536 D2 + 256 D1 + D0 = sum q_i X_i
+// exactly in int32 (|.| <= 32 * 15 * 2^22 < 2^31).
 //
-// A records.  Per (superblock, chunk) 208 bytes: for run g = 0..3 and plane
-// p = 0..2 the 16 digit bytes of chunk columns 16 g .. 16 g + 15, then 16
-// zero bytes.  Lane (m, g) reads record + (3 g + p) * 16 when its A row is
-// live for run g (m < 8, p = m % 4 < 3, h = m / 4 = g / 2) and the zero bytes
-// otherwise, so no lane selects or masks.
+// A records (K > 4096).  Per (superblock, chunk) 208 bytes: for run
+// g = 0..3 and plane p = 0..2 the 16 digit bytes of chunk columns
+// 16 g .. 16 g + 15, then 16 zero bytes.  Lane (m, g) reads record +
+// (3 g + p) * 16 when its A row is live for run g (m < 8, p = m % 4 < 3,
+// h = m / 4 = g / 2) and the zero bytes otherwise, so no lane selects or
+// masks.  B lane n + 16 g holds 16 nibbles of row n from run g, i.e. chunk
+// columns 16 g .. 16 g + 15, low nibbles for g < 2, high for g >= 2.
 //
-// Streaming.  A workgroup (one per CU) owns an equal share of the rows, cut
-// into 16-row tiles; a tile's columns are split into ks K-parts when there
-// are fewer tiles than waves.  (tile, K-part) items go round-robin to the
-// eight waves.  Each wave streams its items through a ring of NSLOT LDS
-// stages of 16 rows x 2 superblocks (rows at a 304-byte pitch, so the 16
-// rows' 16-byte reads fall on distinct banks), filled by buffer->LDS loads of
-// whole kilobytes whose row and column masks are folded into the offsets.
-// K-part sums meet in LDS and are added in K order.
+// Streaming (K > 4096).  A workgroup (one per CU) owns an equal share of the
+// rows, cut into 16-row tiles; a tile's columns are split into ks K-parts
+// when there are fewer tiles than waves.  (tile, K-part) items go
+// round-robin to the eight waves.  Each wave streams its items through a
+// ring of NSLOT LDS stages of 16 rows x 2 superblocks (rows at a 304-byte
+// pitch, so the 16 rows' 16-byte reads fall on distinct banks), filled by
+// buffer->LDS loads of whole kilobytes whose row and column masks are folded
+// into the offsets.  K-part sums meet in LDS and are added in K order.
 #include <type_traits>
 
 #include "gguf_dot4.hpp"
@@ -111,7 +121,9 @@ __device__ __forceinline__ void store_x_records(const XPart<XL> &xp, int nsb, in
         int s = 0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int X = finite ? (int)ldexpf(v[k], 22 - e) : 0;
+            // round to nearest: |X| <= 2^22, so the top digit is at most 64
+            // and sum q X over a sub-block stays below 2^31
+            const int X = finite ? (int)rintf(ldexpf(v[k], 22 - e)) : 0;
             const int c = (int)(int8_t)(X & 0xFF);
             const int X1 = (X - c) >> 8;
             const int b = (int)(int8_t)(X1 & 0xFF);
@@ -357,117 +369,31 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
     }
 }
 
-// ---- K <= 4096: shared pieces of the two kernels below ----------------------
+// ---- shared pieces of the K <= 4096 kernels --------------------------------
 //
-// Wave w of either kernel owns superblock w of every row it works on.  Its
-// A operands (the x digits of that superblock) are built once, in
-// registers, and each 16-row tile then costs the wave five LDS reads of the
-// 16 rows' header and quant bytes of that superblock (B lane n + 16 g:
-// bytes 8 g .. 8 g + 7 of each chunk, low nibbles then high nibbles, so A
-// row 4 h + p is zero on the other half), four MFMAs and ~65 VALU
-// instructions.
+// A wave owns one superblock column of 16-row tiles.  Its A operands (the x
+// digits of that superblock) are built once, in registers, and each tile
+// then costs the wave five LDS reads of the 16 rows' header and quant bytes
+// of that superblock (B lane n + 16 g: bytes 8 g .. 8 g + 7 of each chunk,
+// low nibbles then high nibbles, so A row 4 h + p is zero on the other
+// half), four MFMAs and their epilogue.
+//
+// x is held as four balanced signed-byte digit planes of 30-bit integers,
+// X_i = trunc(x_i / 2^(e-30)) with max |x| < 2^e over the superblock, so the
+// quantisation error of an element is below 2^-30 of that maximum (an fp32
+// element has 24 significant bits, so only elements under 2^-6 of the
+// maximum lose a fraction at all).  The
+// MFMA's A rows 4 h + p (h = sub-block parity, p = plane 0..3) are all live
+// for h < 2: lane n + 16 h receives the four plane sums D_p of one (row,
+// sub-block), each exact in int32 (|D_p| <= 32 * 15 * 128), and combines
+// them as (D2 + 256 D3) 65536 + (D0 + 256 D1) with one fp32 rounding.  The
+// sub-block sums of x for the min term are fp32 sums of x itself.
 namespace {
 
 // LDS stores through inline asm, so the compiler does not wait for every
 // buffer->LDS load in flight before them.
 __device__ __forceinline__ void lds_store_f32(uint32_t addr, float v) {
     asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-
-// The three digit planes of four elements, PLANE bytes apart.
-template <int PLANE>
-__device__ __forceinline__ void lds_store3(uint32_t addr, uint32_t w0, uint32_t w1, uint32_t w2) {
-    asm volatile(
-        "ds_write_b32 %0, %1\n\t"
-        "ds_write_b32 %0, %2 offset:%4\n\t"
-        "ds_write_b32 %0, %3 offset:%5"
-        :
-        : "v"(addr), "v"(w0), "v"(w1), "v"(w2), "n"(PLANE), "n"(2 * PLANE)
-        : "memory");
-}
-
-// LDS tables of one superblock of x: digit planes at dig + p PLANE (256
-// bytes each), the sub-block sums xs * sum X_i (8 floats) and the scale xs.
-struct XTab {
-    uint32_t dig, sum, sc;
-};
-
-// Wave-wide: turns the superblock of x whose elements 4 l .. 4 l + 3 lane l
-// holds (zeros unless `live`) into its tables.  Only this wave reads them
-// back, so no workgroup barrier is needed; the caller waits for LDS.
-template <int PLANE>
-__device__ __forceinline__ void store_x_superblock(const float4 xv, bool live, const XTab &t) {
-    const int lane = threadIdx.x & 63;
-    const float v[4] = {live ? xv.x : 0.0f, live ? xv.y : 0.0f, live ? xv.z : 0.0f, live ? xv.w : 0.0f};
-    uint32_t mb = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
-    mb = wave_max_u32(mb);  // NaN and inf order above every finite |x|
-    const bool finite = mb < 0x7F800000u;
-    int e = 0;
-    (void)frexpf(__uint_as_float(mb), &e);  // max |x| < 2^e
-    uint32_t w0 = 0, w1 = 0, w2 = 0;
-    int sx = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int X = finite ? (int)ldexpf(v[k], 22 - e) : 0;
-        const int c = (int)(int8_t)(X & 0xFF);
-        const int X1 = (X - c) >> 8;
-        const int b = (int)(int8_t)(X1 & 0xFF);
-        const int a = (X1 - b) >> 8;
-        w0 |= ((uint32_t)c & 0xFFu) << (8 * k);
-        w1 |= ((uint32_t)b & 0xFFu) << (8 * k);
-        w2 |= ((uint32_t)a & 0xFFu) << (8 * k);
-        sx += X;
-    }
-    sx = sum8_i(sx);
-    const float scale = !live ? 0.0f : finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
-    lds_store3<PLANE>(t.dig + 4 * lane, w0, w1, w2);
-    if ((lane & 7) == 0) lds_store_f32(t.sum + 4 * (lane >> 3), (float)sx * scale);
-    if (lane == 0) lds_store_f32(t.sc, scale);
-}
-
-// A wave's x operands: A per 64-column chunk c, the sub-block sums of
-// sub-blocks 2 c + h (h = (lane >> 4) & 1) and the scale.
-struct XOps {
-    i32x4 A[4];
-    float xs4[4], xs;
-};
-
-// Reads the tables written by store_x_superblock (after the LDS wait) into
-// the operand layout; `live` zeroes A for a wave without a superblock.
-template <int PLANE>
-__device__ __forceinline__ void read_x_operands(const XTab &t, bool live, XOps &o) {
-    const int lane = threadIdx.x & 63;
-    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = m >> 2;
-    const int h = (lane >> 4) & 1;
-    // Digits of elements 64 c + 8 g .. + 7 (sub-block 2 c) and + 32 (2 c + 1).
-    uint2 dl[4], dh[4];
-    asm volatile(
-        "ds_read_b64 %0, %13\n\t"
-        "ds_read_b64 %1, %13 offset:64\n\t"
-        "ds_read_b64 %2, %13 offset:128\n\t"
-        "ds_read_b64 %3, %13 offset:192\n\t"
-        "ds_read_b64 %4, %13 offset:32\n\t"
-        "ds_read_b64 %5, %13 offset:96\n\t"
-        "ds_read_b64 %6, %13 offset:160\n\t"
-        "ds_read_b64 %7, %13 offset:224\n\t"
-        "ds_read_b32 %8, %14\n\t"
-        "ds_read_b32 %9, %14 offset:8\n\t"
-        "ds_read_b32 %10, %14 offset:16\n\t"
-        "ds_read_b32 %11, %14 offset:24\n\t"
-        "ds_read_b32 %12, %15\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
-          "=&v"(dh[2]), "=&v"(dh[3]), "=&v"(o.xs4[0]), "=&v"(o.xs4[1]), "=&v"(o.xs4[2]),
-          "=&v"(o.xs4[3]), "=&v"(o.xs)
-        : "v"(t.dig + p * PLANE + 8 * g), "v"(t.sum + 4 * h), "v"(t.sc)
-        : "memory");
-    const bool alive = live && p < 3;
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-        o.A[c] = i32x4{alive && ha == 0 ? (int)dl[c].x : 0, alive && ha == 0 ? (int)dl[c].y : 0,
-                       alive && ha == 1 ? (int)dh[c].x : 0, alive && ha == 1 ? (int)dh[c].y : 0};
 }
 
 // Reads the 16 rows' header (a_hdr = row n's superblock) and quant bytes
@@ -486,24 +412,108 @@ __device__ __forceinline__ void read_tile_superblock(uint32_t a_hdr, uint32_t a_
         : "memory");
 }
 
-// One superblock of a 16-row tile before its scales are applied: per chunk
-// c the exact integer sum S[c] = sum q X over sub-block 2 c + h of row n
-// (lane n + 16 h, h = 0, 1; lanes 32..63 hold values of the zero A rows,
-// which callers drop), the superblock's d and dmin, and the 6-bit scale and
-// min codes of this lane's sub-blocks h, 2 + h, 4 + h, 6 + h.
-struct TileParts {
-    int S[4];
-    float d, dmin, scf[4], mnf[4];
+// Waits until at most N of this wave's loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One 1 KB buffer->LDS load (16 bytes a lane).
+__device__ __forceinline__ void col_load(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, off, 0, 0, kStreamLoad);
+}
+
+// A wave's x operands for one superblock with four digit planes.
+struct XOps4 {
+    i32x4 A[4];
+    float xs4[4], xs;
 };
 
-__device__ __forceinline__ void q4k_tile_parts(const u32x4 hv, const uint2 (&q)[4], const XOps &o,
-                                               TileParts &t) {
+// Wave-wide: lane l holds elements 4 l .. 4 l + 3 of a superblock of x.
+// Writes the digit planes to `scratch` (1 KB of LDS private to the wave),
+// reads them back in the A operand layout and leaves the scratch free.
+__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o) {
+    const int lane = threadIdx.x & 63;
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t mb = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
+    mb = wave_max_u32(mb);  // NaN and inf order above every finite |x|
+    const bool finite = mb < 0x7F800000u;
+    int e = 0;
+    (void)frexpf(__uint_as_float(mb), &e);  // max |x| < 2^e
+    // X = trunc(x / 2^(e-30)), |X| < 2^30 (an fp32 holds 24 significant bits,
+    // so only elements below 2^-6 of the maximum lose their fraction: an
+    // error under 2^-30 of it).  Adding 0x808080 makes the low three bytes
+    // u_p = d_p + 128 of the balanced digits d_p in [-128, 127]; the XOR
+    // maps them back to d_p as signed bytes and leaves the top digit
+    // d3 = (X + 0x808080) >> 24 in [-64, 64] as byte 3.
+    uint32_t Y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int X = finite ? (int)ldexpf(v[k], 30 - e) : 0;
+        Y[k] = ((uint32_t)X + 0x00808080u) ^ 0x00808080u;
+    }
+    // 4 x 4 byte transpose: w[p] = byte p of Y[0], Y[1], Y[2], Y[3].
+    const uint32_t t01l = __builtin_amdgcn_perm(Y[1], Y[0], 0x05010400u);
+    const uint32_t t01h = __builtin_amdgcn_perm(Y[1], Y[0], 0x07030602u);
+    const uint32_t t23l = __builtin_amdgcn_perm(Y[3], Y[2], 0x05010400u);
+    const uint32_t t23h = __builtin_amdgcn_perm(Y[3], Y[2], 0x07030602u);
+    const uint32_t w[4] = {__builtin_amdgcn_perm(t23l, t01l, 0x05040100u),
+                           __builtin_amdgcn_perm(t23l, t01l, 0x07060302u),
+                           __builtin_amdgcn_perm(t23h, t01h, 0x05040100u),
+                           __builtin_amdgcn_perm(t23h, t01h, 0x07060302u)};
+    // Plane p at scratch + 256 p; lane l's four elements at byte 4 l.
+    asm volatile(
+        "ds_write2st64_b32 %0, %1, %2 offset1:1\n\t"
+        "ds_write2st64_b32 %0, %3, %4 offset0:2 offset1:3"
+        :
+        : "v"(scratch + 4 * lane), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3])
+        : "memory");
+    // Sub-block j = lanes 8 j .. 8 j + 7; lane n + 16 g (h = g & 1) needs the
+    // sums of sub-blocks 2 c + h.
+    const float s8 = sum8((v[0] + v[1]) + (v[2] + v[3]));
+    const int h = (lane >> 4) & 1;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s8), 16 * c));
+        const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s8), 16 * c + 8));
+        o.xs4[c] = h ? b : a;
+    }
+    o.xs = finite ? ldexpf(1.0f, e - 30) : __builtin_nanf("");
+    // A lane (m, g): plane p = m & 3 of elements 64 c + 8 g .. + 7 (sub-block
+    // 2 c) for m < 4, of elements 64 c + 32 + 8 g .. + 7 (2 c + 1) for
+    // 4 <= m < 8; rows 8..15 are zero.
+    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = m >> 2;
+    uint2 dl[4], dh[4];
+    asm volatile(
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "ds_read_b64 %0, %8\n\t"
+        "ds_read_b64 %1, %8 offset:64\n\t"
+        "ds_read_b64 %2, %8 offset:128\n\t"
+        "ds_read_b64 %3, %8 offset:192\n\t"
+        "ds_read_b64 %4, %8 offset:32\n\t"
+        "ds_read_b64 %5, %8 offset:96\n\t"
+        "ds_read_b64 %6, %8 offset:160\n\t"
+        "ds_read_b64 %7, %8 offset:224\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
+          "=&v"(dh[2]), "=&v"(dh[3])
+        : "v"(scratch + 256 * p + 8 * g)
+        : "memory");
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        o.A[c] = i32x4{ha == 0 ? (int)dl[c].x : 0, ha == 0 ? (int)dl[c].y : 0,
+                       ha == 1 ? (int)dh[c].x : 0, ha == 1 ? (int)dh[c].y : 0};
+}
+
+// One superblock of a 16-row tile with four-plane x: lane n + 16 h returns
+// the share of sub-blocks h, 2 + h, 4 + h, 6 + h of row n (lanes 32..63
+// return values of the zero A rows, which callers drop).
+__device__ __forceinline__ float q4k_tile_superblock4(const u32x4 hv, const uint2 (&q)[4],
+                                                      const XOps4 &o) {
     const int lane = threadIdx.x & 63;
     const int h = (lane >> 4) & 1;
-    // B: the low nibbles q (sub-block 2 c) and the high nibbles (2 c + 1),
-    // each as a byte 0..15.  The four products are independent: all of them
-    // are issued before the first result is used.  Plane combine: D_p
-    // weighted by 256^p.
     const i32x4 zero = {0, 0, 0, 0};
     i32x4 D[4];
 #pragma unroll
@@ -512,11 +522,15 @@ __device__ __forceinline__ void q4k_tile_parts(const u32x4 hv, const uint2 (&q)[
                          (int)((q[c].x >> 4) & 0x0F0F0F0Fu), (int)((q[c].y >> 4) & 0x0F0F0F0Fu)};
         D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, zero, 0, 0, 0);
     }
+    float Sq[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        t.S[c] = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
-    t.d = half_bits_to_float_fast(hv.x);
-    t.dmin = half_bits_to_float_fast(hv.x >> 16);
+    for (int c = 0; c < 4; c++) {
+        const int lo = D[c][0] + D[c][1] * 256;  // |.| < 2^24: exact as a float
+        const int hi = D[c][2] + D[c][3] * 256;
+        Sq[c] = fmaf((float)hi, 65536.0f, (float)lo);
+    }
+    const float d = half_bits_to_float_fast(hv.x);
+    const float dmin = half_bits_to_float_fast(hv.x >> 16);
     // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h
     // (bytes 0 and 2 of sc03 / mn03) and 4 + h, 6 + h (of sc47 / mn47)
     const uint32_t hy = hv.y >> (8 * h), hz = hv.z >> (8 * h), hw = hv.w >> (8 * h);
@@ -524,53 +538,28 @@ __device__ __forceinline__ void q4k_tile_parts(const u32x4 hv, const uint2 (&q)[
     const uint32_t mn03 = hz & 0x003F003Fu;
     const uint32_t sc47 = (hw & 0x000F000Fu) | ((hy >> 2) & 0x00300030u);
     const uint32_t mn47 = ((hw >> 4) & 0x000F000Fu) | ((hz >> 2) & 0x00300030u);
-    t.scf[0] = (float)(sc03 & 0xFFu);
-    t.scf[1] = (float)((sc03 >> 16) & 0xFFu);
-    t.scf[2] = (float)(sc47 & 0xFFu);
-    t.scf[3] = (float)((sc47 >> 16) & 0xFFu);
-    t.mnf[0] = (float)(mn03 & 0xFFu);
-    t.mnf[1] = (float)((mn03 >> 16) & 0xFFu);
-    t.mnf[2] = (float)(mn47 & 0xFFu);
-    t.mnf[3] = (float)((mn47 >> 16) & 0xFFu);
-}
-
-__device__ __forceinline__ bool tile_scales_finite(const TileParts &t) {
-    return __builtin_isfinite(t.d) && __builtin_isfinite(t.dmin);
-}
-
-// This lane's share of its row, for finite d and dmin: d xs sum_c sc S -
-// dmin sum_c m X_c.
-__device__ __forceinline__ float tile_value_finite(const TileParts &t, const XOps &o) {
+    const float scf[4] = {(float)(sc03 & 0xFFu), (float)((sc03 >> 16) & 0xFFu),
+                          (float)(sc47 & 0xFFu), (float)((sc47 >> 16) & 0xFFu)};
+    const float mnf[4] = {(float)(mn03 & 0xFFu), (float)((mn03 >> 16) & 0xFFu),
+                          (float)(mn47 & 0xFFu), (float)((mn47 >> 16) & 0xFFu)};
     float qs = 0.0f, mm = 0.0f;
+    if (__builtin_isfinite(d) && __builtin_isfinite(dmin)) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        qs = fmaf(t.scf[c], (float)t.S[c], qs);
-        mm = fmaf(t.mnf[c], o.xs4[c], mm);
+        for (int c = 0; c < 4; c++) {
+            qs = fmaf(scf[c], Sq[c], qs);
+            mm = fmaf(mnf[c], o.xs4[c], mm);
+        }
+        return fmaf(d * o.xs, qs, -(dmin * mm));
     }
-    return fmaf(t.d * o.xs, qs, -(t.dmin * mm));
-}
-
-// The same with the reference's products, for any d and dmin: (d sc) per
-// sub-block, and zero min codes skipped even for a NaN or infinite dmin
-// (minContribution, RT/GgufKQuantLayout.java:67-69).
-__device__ __forceinline__ float tile_value_exact(const TileParts &t, const XOps &o) {
-    float qs = 0.0f, mm = 0.0f;
+    // The reference's products for a non-finite d or dmin: (d sc) per
+    // sub-block, and zero min codes skipped even for a NaN or infinite dmin
+    // (minContribution, RT/GgufKQuantLayout.java:67-69).
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        qs = fmaf(t.d * t.scf[c], o.xs * (float)t.S[c], qs);
-        mm = fmaf(t.mnf[c] != 0.0f ? t.dmin * t.mnf[c] : 0.0f, o.xs4[c], mm);
+        qs = fmaf(d * scf[c], o.xs * Sq[c], qs);
+        mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, o.xs4[c], mm);
     }
     return qs - mm;
-}
-
-// One superblock of a 16-row tile: lane n + 16 h (h = 0, 1) returns the
-// share of sub-blocks h, 2 + h, 4 + h, 6 + h of row n (lanes 32..63 return
-// values of the zero A rows, which callers drop).
-__device__ __forceinline__ float q4k_tile_superblock(const u32x4 hv, const uint2 (&q)[4],
-                                                     const XOps &o) {
-    TileParts t;
-    q4k_tile_parts(hv, q, o, t);
-    return tile_scales_finite(t) ? tile_value_finite(t, o) : tile_value_exact(t, o);
 }
 
 }  // namespace
@@ -595,7 +584,6 @@ constexpr int kT2Dma = (kT2Stage + 1023) / 1024;                // 37 loads per 
 constexpr int kT2DmaPerWave = (kT2Dma + kT2Waves - 1) / kT2Waves;  // 3
 constexpr int kT2Slot = kT2Dma * 1024;
 constexpr int kT2MaxRows = 1024;                                // rows per workgroup
-constexpr int kT2K = 16 * kQK;                                  // x elements held
 
 }  // namespace
 
@@ -604,17 +592,14 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int64_t rows_per_wg) {
     static_assert(kT2DmaPerWave * kT2Waves >= kT2Dma, "tile loads");
-    static_assert(3 * kT2K + 16 * 8 * 4 + 16 * 4 <= kT2Slot, "x tables fit a slot");
+    static_assert(kT2Waves * 1024 <= kT2Slot, "x scratch fits a slot");
     __shared__ __attribute__((aligned(16))) uint8_t ring[NSLOT * kT2Slot + 1024];  // + sink
     __shared__ float part[2][kT2Waves][32];  // [tile & 1][wave][lane]
     __shared__ float yout[kT2MaxRows];
-    // The x tables (digit planes, sub-block sums [superblock][sub-block],
-    // superblock scales) live in the last ring slot, which the
-    // loop first refills after every wave has read them.  They are accessed
-    // with inline asm like the ring itself.
-    const uint32_t xdig = (uint32_t)(uintptr_t)(lds_ptr)(ring + (NSLOT - 1) * kT2Slot);
-    const uint32_t xsum = xdig + 3 * kT2K;
-    const uint32_t xsc = xsum + 16 * 8 * 4;
+    // Each wave's x scratch (four digit planes, 1 KB) is kilobyte w of the
+    // last ring slot, which the loop first refills after every wave has
+    // read its operands back.
+    const uint32_t xscr = (uint32_t)(uintptr_t)(lds_ptr)(ring + (NSLOT - 1) * kT2Slot);
 
     const uint32_t row_bytes = (uint32_t)row_bytes64;
     const int lane = threadIdx.x & 63;
@@ -633,7 +618,8 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
         const uint32_t k = (uint32_t)(wv + kT2Waves * i);
         const uint32_t b = 1024u * k + 16u * lane;
         const uint32_t r = b / kT2Pitch, col = b - r * kT2Pitch;
-        dbase[i] = (k < (uint32_t)kT2Dma && col < row_bytes) ? r * row_bytes + col : kMaskedOffset;
+        dbase[i] = (k < (uint32_t)kT2Dma && r < (uint32_t)kTileRows && col < row_bytes) ? r * row_bytes + col
+                                                                                       : kMaskedOffset;
     }
     auto issue = [&](int slot, int tile) {
         const uint32_t uoff = tile < tiles ? (uint32_t)tile * kTileRows * row_bytes : kMaskedOffset;
@@ -646,24 +632,21 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
         }
     };
 
-    // x: thread t converts elements 4 t .. 4 t + 3, so wave s holds superblock s.
     // Load order: x, then tile 0; the later tiles only once x has arrived.  A
     // tile is usable when all of it has arrived, and the memory system serves
     // requests issued together interleaved, so this head start makes tile 0
-    // complete well before tile 1 instead of together with it.
-    XPart<1> xp;
-    load_x_parts<kT2Threads, 1>(xp, x, nsb * 8);
-    __builtin_amdgcn_sched_barrier(0);
-    issue(0, 0);
-    // Wave s owns superblock s (the tables hold all 16, so every wave writes
-    // its own, zeros past nsb).
+    // complete well before tile 1 instead of together with it.  Wave s owns
+    // superblock s (lane l converts its elements 4 l .. 4 l + 3); a wave past
+    // nsb converts superblock 0 (its operands are never used).
     const int sb = wv;
     const bool active = sb < nsb;  // wave-uniform
-    const XTab xt = {xdig + (uint32_t)(sb * kQK), xsum + (uint32_t)(32 * sb), xsc + (uint32_t)(4 * sb)};
-    store_x_superblock<kT2K>(xp.v[0], active, xt);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    XOps xo;
-    read_x_operands<kT2K>(xt, active, xo);
+    const float4 xv = reinterpret_cast<const float4 *>(x)[64 * (active ? sb : 0) + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    issue(0, 0);
+    float4 xr = xv;  // the conversion stays below the tile loads
+    asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
+    XOps4 xo;
+    x_operands4(xr, xscr + 1024u * (uint32_t)wv, xo);
 #pragma unroll
     for (int j = 1; j < NSLOT - 1; j++) issue(j, j);
 
@@ -690,7 +673,7 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
             uint2 q[4];
             const uint32_t off = (uint32_t)slot * kT2Slot;
             read_tile_superblock(a_h0 + off, a_q0 + off, hv, q);
-            const float v = q4k_tile_superblock(hv, q, xo);
+            const float v = q4k_tile_superblock4(hv, q, xo);
             if (lane < 32) part[t & 1][wv][lane] = v;
         }
         slot = slot == NSLOT - 1 ? 0 : slot + 1;
@@ -707,6 +690,7 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
     for (int r = threadIdx.x; r < nr; r += kT2Threads) y[r0 + r] = yout[r];
 }
 
+
 // ---- K <= 4096, at most 64 rows per workgroup: one column per wave ---------
 //
 // For matrices of up to 64 rows per CU (K = 4096 and 16384 rows or fewer),
@@ -715,14 +699,25 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
 // workgroup's rows, packed at a 144-byte pitch, so 16-row tiles are 2304
 // contiguous bytes) into its own LDS region and works through the tiles as
 // its own loads complete.  No wave waits for another's data until the row
-// sums meet at the end, so the work of a tile starts as soon as that wave's
-// part of it has arrived and little is left once the stream ends.
+// sums meet at the end.
+//
+// Pacing.  A CU accepts only a few tens of kilobytes of loads in flight; a
+// wave whose load does not fit stalls at the issue and cannot compute
+// meanwhile.  So a wave issues x and tile 0, and the loads of tile t + 1
+// only once tile t has arrived (just before working on it): the CU's queue
+// then runs tile-major, each wave's tiles arrive spread over the stream, and
+// after the last byte only one tile per wave is left.  Measured on MI355X
+// against the alternatives (Q4_K 14336 x 4096): two or all four tiles in
+// flight per wave, 9.1 / 9.3 us; a shared-tile ring with one barrier per
+// tile, 9.0 us; the whole share issued up front with per-tile barriers,
+// 9.8 us (its waves only finish issuing after 3-5 us, so every tile's work
+// lands after the stream); this kernel, 8.9 us.
 namespace {
 
 constexpr int kColWaves = 16;
 constexpr int kColThreads = kColWaves * 64;
-// x tables of the wave's superblock (digit planes 768 bytes, sub-block sums
-// 32, scale 4), later the wave's row sums (2 floats a row).
+// x scratch of the wave's superblock (four digit planes), later the wave's
+// row sums (2 floats a row).
 constexpr int kColX = 1024;
 
 // A wave's column: NL loads of 1 KB, 64 rows at a 144-byte pitch.
@@ -737,22 +732,9 @@ struct ColGeom {
         const int e = (kTileRows * kQKBlockBytes * (t + 1) + 1023) / 1024 - 1;
         return e < NL - 1 ? e : NL - 1;
     }
-    // A tile's reads end inside the wave's region (rows past kMaxRows of the
-    // last tile read the x tables, and their sums are dropped).
-    static_assert(kMaxTiles * kTileRows * kQKBlockBytes <= kRegion, "last tile inside the region");
-    static_assert(2 * 4 * kMaxTiles * kTileRows <= kColX, "row sums fit the x tables");
+    static_assert(kMaxTiles * kTileRows * kQKBlockBytes <= kW, "the tiles fill the column");
+    static_assert(2 * 4 * kMaxTiles * kTileRows <= kColX, "row sums fit the x scratch");
 };
-
-// Waits until at most N of this wave's loads are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// One 1 KB buffer->LDS load (16 bytes a lane).
-__device__ __forceinline__ void col_load(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, off, 0, 0, kStreamLoad);
-}
 
 }  // namespace
 
@@ -770,21 +752,20 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
     const uint32_t wbase = (uint32_t)(uintptr_t)(lds_ptr)(lds + wv * G::kRegion);
     const uint32_t xbase = wbase + G::kW;
 
-    // Waves past nsb own no column: they load superblock 0's x and issue
+    // Waves past nsb own no column: they convert superblock 0's x and issue
     // only masked loads (an empty descriptor), so every wave runs the same
     // loads and barriers.
     const bool active = wv < nsb;  // wave-uniform
     const int sb = active ? wv : 0;
+    const float4 xv = reinterpret_cast<const float4 *>(x)[64 * sb + lane];
+    __builtin_amdgcn_sched_barrier(0);
     // Load k of a wave moves bytes 1024 k + 16 lane of its column, i.e. row
     // b / 144, byte b % 144 of the row's superblock; rows past nr read
     // zeros.  The descriptor starts at the column, so the last row's
     // superblock ends at (nr - 1) row_bytes + 144 <= nr row_bytes - 144 wv.
-    const float4 xv = reinterpret_cast<const float4 *>(x)[64 * sb + lane];
-    __builtin_amdgcn_sched_barrier(0);
     const __amdgpu_buffer_rsrc_t rs =
         wave_buffer(w + r0 * row_bytes64 + kQKBlockBytes * sb,
                     active ? (uint32_t)nr * row_bytes - kQKBlockBytes * wv : 0u);
-    // Offsets of every load, computed once (out of the tile loop).
     uint32_t off[NL];
 #pragma unroll
     for (int k = 0; k < NL; k++) {
@@ -793,22 +774,14 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
         off[k] = r < (uint32_t)nr ? r * row_bytes + col : kMaskedOffset;
     }
     auto issue = [&](int k) { col_load(rs, lds + wv * G::kRegion + 1024 * k, off[k]); };
-    // A CU returns loads in the order its waves issued them and stalls a
-    // wave's issue once a few tens are outstanding (which also stalls its
-    // work).  So a wave issues x and tile 0, then the loads of tile t + 1
-    // only once tile t has arrived (just before working on it): after the
-    // first round the CU's queue holds every wave's tile t before any wave's
-    // tile t + 1, each wave's tiles arrive spread over the whole stream, and
-    // the last loads to arrive are one wave's last two.
     const int tiles = (nr + kTileRows - 1) / kTileRows;
 #pragma unroll
     for (int k = 0; k <= G::last_load(0); k++) issue(k);
-    __builtin_amdgcn_sched_barrier(0);  // the tile loads issued before x is waited for
-    const XTab xt = {xbase, xbase + 768, xbase + 800};
-    store_x_superblock<256>(xv, active, xt);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    XOps xo;
-    read_x_operands<256>(xt, active, xo);
+    __builtin_amdgcn_sched_barrier(0);
+    float4 xr = xv;  // the conversion stays below the tile loads
+    asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
+    XOps4 xo;
+    x_operands4(xr, xbase, xo);
 
     const int n = lane & 15, g = lane >> 4;
     const uint32_t a_h = wbase + n * kQKBlockBytes;
@@ -826,7 +799,7 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
             u32x4 hv;
             uint2 q[4];
             read_tile_superblock(a_h + 2304 * t, a_q + 2304 * t, hv, q);
-            const float v = q4k_tile_superblock(hv, q, xo);
+            const float v = q4k_tile_superblock4(hv, q, xo);
             // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until
             // the row sums (pair h of row r at float 2 r + h)
             if (lane < 32) lds_store_f32(xbase + 8 * (16 * t + n) + 4 * g, v);
@@ -903,10 +876,11 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
                                 const float *x, float *y, int64_t rows, hipStream_t stream) {
     const int nsb = (int)(cols / kQK);
     const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
-    // Up to 64 rows per CU: every workgroup's share stays in LDS, one
+    const int variant = tuning().gemv_variant;
+    // At most 64 rows per CU: every workgroup's share stays in LDS, one
     // superblock column per wave (gemv_variant 3 keeps the shared tiles).
     const int64_t col_rows = (rows + cus - 1) / cus;
-    if (nsb <= 16 && col_rows <= ColGeom::kMaxRows && tuning().gemv_variant != 3) {
+    if (nsb <= 16 && col_rows <= ColGeom::kMaxRows && variant != 3) {
         hipLaunchKernelGGL(gemv_q4_k_mfma_col_kernel, dim3((unsigned)((rows + col_rows - 1) / col_rows)),
                            dim3(kColThreads), 0, stream, w, row_bytes, nsb, x, y, rows, (int)col_rows);
         return hipGetLastError();
@@ -925,12 +899,8 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
         return hipGetLastError();
     }
     const MfmaPlan p = plan_mfma(rows, nsb);
-    if (nsb <= 16)
-        hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<3, 16>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
-                           stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
-    else
-        hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
-                           stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
+    hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
+                       stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
     return hipGetLastError();
 }
 

@@ -13,10 +13,11 @@
 // never wait for each other: each row's item piece is contiguous in memory
 // and lands as 16-byte chunks (4 rows x 34 or 18 chunks: three or two load
 // instructions, the last one partly masked).  x (fp32) is staged once per
-// workgroup in LDS, with the per-block sums of x for Q4_0's offset.  Lane
+// workgroup in LDS.  Lane
 // (row r = lane / 16, block b = lane % 16) contracts its block's 32 quants
 // in order with fp32 FMAs (int8 bytes widen with one sign-extending SDWA
-// convert each) and adds d_b times that sum to its partial, the block
+// convert each; Q4_0 nibbles with an unsigned convert and an exact - 8) and
+// adds d_b times that sum to its partial, the block
 // structure of the reference; the 16 lanes of a row meet in a shuffle
 // reduction at the end.  x sits in LDS at 144 bytes per 32-float block (16
 // bytes of padding), so the 16 lanes' 16-byte reads of 16 blocks fall in
@@ -58,11 +59,10 @@ struct GrItem {
     static constexpr int kSlot = 1024 * kDma;                        // masked lanes land in the pad
 };
 
-// Dynamic LDS: x (144 bytes per 32-float block), per-block sums of x (K / 8
-// bytes, padded to 16), then the waves' rings.
+// Dynamic LDS: x (144 bytes per 32-float block), then the waves' rings.
 constexpr int kGrXBlock = 144;
 __host__ __device__ constexpr int gr_x_bytes(int K) { return K / 32 * kGrXBlock; }
-__host__ __device__ constexpr int gr_ring_offset(int K) { return gr_x_bytes(K) + ((K / 8 + 15) & ~15); }
+__host__ __device__ constexpr int gr_ring_offset(int K) { return gr_x_bytes(K); }
 template <int TYPE>
 __host__ __device__ constexpr int gr_lds_bytes(int K, int NS, int waves) {
     return gr_ring_offset(K) + waves * NS * GrItem<TYPE>::kSlot;
@@ -160,12 +160,6 @@ __device__ __forceinline__ void gr_read_x(uint32_t a, float (&x)[N]) {
     }
 }
 
-__device__ __forceinline__ float gr_read_f(uint32_t a) {
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-    return __uint_as_float(v);
-}
-
 // Sign-extended byte k of w as a float (one SDWA convert).
 __device__ __forceinline__ float gr_sbyte(uint32_t w, int k) {
     return (float)(int)(int8_t)(uint8_t)(w >> (8 * k));
@@ -195,7 +189,6 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
     const int nitems = K / (32 * IB);
 
     uint8_t *const xl = lds;
-    float *const xsum = reinterpret_cast<float *>(lds + gr_x_bytes(K));
     uint8_t *const ring = lds + gr_ring_offset(K) + wave * NS * I::kSlot;
 
     // The wave's four rows (zeros past `rows`).  Loads of items past the last
@@ -260,19 +253,6 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
     for (int u = 0; u < 4; u++)
         asm volatile("" : : "v"(xr[u][0]), "v"(xr[u][1]), "v"(xr[u][2]), "v"(xr[u][3]));
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if constexpr (TYPE == kQ4_0) {
-        // Per-block sums of x (for sum (q - 8) x = sum q x - 8 sum x).
-        const uint32_t xa = (uint32_t)(uintptr_t)(lds_ptr)xl;
-        for (int b = tid; b < K / 32; b += nt) {
-            float xv[32];
-            gr_read_x<32>(xa + (uint32_t)(kGrXBlock * b), xv);
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 32; i++) s += xv[i];
-            asm volatile("ds_write_b32 %0, %1" : : "v"((uint32_t)(uintptr_t)(lds_ptr)(xsum + b)), "v"(s) : "memory");
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    }
 
     // Lane roles: row r = lane / 16, block b = lane % 16 of the item.  Q4_0
     // quants: low nibbles are quants 0..15, high nibbles 16..31.
@@ -286,7 +266,6 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
     const uint32_t s_sh = (uint32_t)(8 * (soff & 3));             // 0 or 16
     const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
     const uint32_t x_lane = xl_base + (uint32_t)(kGrXBlock * b);
-    const uint32_t xs_lane = (uint32_t)(uintptr_t)(lds_ptr)(xsum + b);
 
     float acc = 0.0f;
     int sl = 0;
@@ -308,9 +287,10 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
             for (int i = 0; i < 32; i++) s = fmaf(gr_sbyte(qa[i >> 2], i & 3), xv[i], s);
             acc = fmaf(d, s, acc);
         } else {
+            // (q - 8) x per element, as the reference does: the offset is
+            // exact in fp32 and nothing cancels.
             float xv[32];
             gr_read_x<32>(x_lane + (uint32_t)(kGrXBlock * IB * j), xv);
-            const float sx = gr_read_f(xs_lane + 4u * (uint32_t)(IB * j));
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -318,11 +298,11 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
                 const uint32_t hi = opaque((qa[i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    s = fmaf(byte_f(lo, k), xv[4 * i + k], s);
-                    s = fmaf(byte_f(hi, k), xv[16 + 4 * i + k], s);
+                    s = fmaf(byte_f(lo, k) - 8.0f, xv[4 * i + k], s);
+                    s = fmaf(byte_f(hi, k) - 8.0f, xv[16 + 4 * i + k], s);
                 }
             }
-            acc = fmaf(d, fmaf(-8.0f, sx, s), acc);
+            acc = fmaf(d, s, acc);
         }
         sl = sl + 1 == NS ? 0 : sl + 1;
     }

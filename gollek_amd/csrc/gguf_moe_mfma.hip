@@ -276,7 +276,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             int sx = 0;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int X = finite ? (int)ldexpf(vv[k], 22 - ex) : 0;
+                const int X = finite ? (int)rintf(ldexpf(vv[k], 22 - ex)) : 0;  // |X| <= 2^22
                 const int c0 = (int)(int8_t)(X & 0xFF);
                 const int X1 = (X - c0) >> 8;
                 const int c1 = (int)(int8_t)(X1 & 0xFF);

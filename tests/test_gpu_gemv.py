@@ -135,6 +135,30 @@ def test_gemv_parity(name, type_id, rows, cols):
     t.close()
 
 
+ACCURACY_CONFIGS = [("c0_q8_0", syn.Q8_0, 4096, 4096), ("c1_q4_0", syn.Q4_0, 11008, 4096),
+                    ("c2a_q4_k", syn.Q4_K, 14336, 4096), ("q4_k_k2048", syn.Q4_K, 4096, 2048)]
+
+
+@pytest.mark.parametrize("name,type_id,rows,cols", ACCURACY_CONFIGS, ids=[c[0] for c in ACCURACY_CONFIGS])
+@pytest.mark.parametrize("seed", [1, 2])
+def test_gemv_error_within_twice_java_order_fp32(name, type_id, rows, cols, seed):
+    # The GPU mat-vec is at least as accurate as the reference's own fp32
+    # loop, up to a factor 2: both against the fp64 dot over the bit-exact
+    # dequantized rows, on the same inputs.
+    print(f"[gpu] accuracy {name} seed {seed}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=seed)
+    x = syn.activation(cols, seed=seed + 1)
+    t = _tensor(type_id, data, cols, name)
+    y = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    e_gpu = o.rel_err(y, ref)
+    e_java = o.rel_err(o.matvec(type_id, data, cols, x), ref)
+    print(f"[gpu] accuracy {name} seed {seed}: gpu {e_gpu:.3e} java-order fp32 {e_java:.3e}", flush=True)
+    assert e_gpu <= 2.0 * e_java, (e_gpu, e_java)
+    t.close()
+
+
 # Q4_K shapes at the edges of the matrix-core kernels' work split: one row,
 # rows around a 16-row tile, odd superblock counts (a half-empty last ring
 # stage), K-parts summed across waves (few tiles per workgroup), K = 16384
@@ -156,7 +180,7 @@ def test_q4k_gemv_kernels_agree_with_oracle(rows, cols):
     t = _tensor(syn.Q4_K, data, cols)
     ref = o.matvec_fp64(syn.Q4_K, data, cols, x)
     try:
-        for variant in (0, 3, 2, 1):  # matrix cores, shared tiles, v_dot4 ring, fp32
+        for variant in (0, 3, 2, 1):  # matrix cores (CU block or shared tiles), v_dot4, fp32
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
             ops.mat_vec(t, x, y)
