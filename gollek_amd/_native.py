@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gollek_hip_matvec_device": (_I32, [_P, _P, _P, _I64, _P, _CHARP, _SZ]),
     "gollek_hip_gemm_bf16": (_I32, [_P, _P, _I64, _I64, _P, _I64, _CHARP, _SZ]),
     "gollek_hip_gemm_bf16_device": (_I32, [_P, _P, _I64, _P, _P, _CHARP, _SZ]),
+    "gollek_hip_gemm_bf16_device_noalloc": (_I32, [_P, _P, _I64, _P, _P, _CHARP, _SZ]),
     "gollek_hip_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "gollek_hip_moe_grouped": (_I32, [_P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64,
                                       _CHARP, _SZ]),

@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -97,7 +98,18 @@ bool supported(int32_t type_id) {
 std::mutex g_init_mu;
 int g_initialised_device = -1;
 
-// Makes `device` current on this thread and records its CU count once.
+// Split-K scratch of gollek_hip_gemm_bf16_device_noalloc: a file-scope
+// device array, so each GPU holds its own copy from module load until the
+// process ends.  On the host, `scratch` only names that array; kernels get
+// the per-device address hipGetSymbolAddress returns, resolved once per
+// device (with the device current) when the library first sets it up.
+constexpr size_t kGemmScratchBytes = (size_t)8 << 20;  // gemm_workspace_bytes <= 8 MiB on 256 CUs
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kGemmScratchBytes / sizeof(float)];
+std::atomic<float *> g_scratch_ptr[kMaxDevices];
+
+// Makes `device` current on this thread, records its CU count and resolves
+// its copy of the static GEMM scratch, once.
 int32_t use_device(int device, char *err, size_t err_len) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice", err, err_len);
@@ -108,6 +120,12 @@ int32_t use_device(int device, char *err, size_t err_len) {
         if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute", err, err_len);
         if (cus > 0) gollek::tuning().cu_count = cus;
         g_initialised_device = device;
+    }
+    if (device >= 0 && device < kMaxDevices && g_scratch_ptr[device].load() == nullptr) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)", err, err_len);
+        g_scratch_ptr[device].store(static_cast<float *>(ptr));
     }
     return GOLLEK_HIP_OK;
 }
@@ -453,7 +471,7 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
     const int32_t rc = check_gemm(w, x, y, m, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     // The handle's split-K workspace: allocated at the first call that splits,
-    // for the largest split any m of this weight uses (at most 4 MiB on 256
+    // for the largest split any m of this weight uses (at most 8 MiB on 256
     // CUs), and kept until the handle is freed, so a launch in flight never
     // loses it.
     const size_t need = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
@@ -475,6 +493,35 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
     hipError_t e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
                                                  (int)w->cols, static_cast<hipStream_t>(stream),
                                                  need ? w->gemm_ws : nullptr, w->gemm_ws_bytes);
+    if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *w, const uint16_t *x, int64_t m,
+                                            float *y, void *stream, char *err, size_t err_len) {
+    const int32_t rc = check_gemm(w, x, y, m, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    // The split-K partials go to this GPU's static scratch: no allocation,
+    // and every call on the GPU shares it (each split writes its whole
+    // partial tile before the in-order reduction reads it, so nothing needs
+    // clearing; overlapping calls race).
+    const size_t need = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
+    float *ws = nullptr;
+    if (need > 0) {
+        if (need > kGemmScratchBytes)
+            return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                        "GEMM %lld x %lld x %lld needs %zu bytes of split-K scratch, more than the "
+                        "static %zu", (long long)m, (long long)w->rows, (long long)w->cols, need,
+                        kGemmScratchBytes);
+        ws = (w->device >= 0 && w->device < kMaxDevices) ? g_scratch_ptr[w->device].load() : nullptr;
+        if (ws == nullptr)
+            return fail(GOLLEK_HIP_ERR_DEVICE, err, err_len,
+                        "the static GEMM scratch of device %d is not set up", w->device);
+    }
+    hipError_t e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
+                                                 (int)w->cols, static_cast<hipStream_t>(stream), ws,
+                                                 ws != nullptr ? kGemmScratchBytes : 0);
     if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;

@@ -1157,8 +1157,8 @@ size_t gemm_workspace_bytes(int M, int N, int K) {
 }
 
 // The need of m peaks at multiples of the 128-row tile and is zero once the
-// tiles cover half the CUs; S tiles <= cu_count / 2 bounds it by
-// cu_count / 2 tiles of 128 x 64 floats.
+// tiles cover half the CUs; S tiles <= cu_count (ring_splits) bounds it by
+// cu_count tiles of 128 x 64 floats (8 MiB on 256 CUs, at m = 128).
 size_t gemm_workspace_max_bytes(int N, int K) {
     size_t most = 0;
     for (int mt = 1; gemm_workspace_bytes(128 * mt, N, K) > 0; mt++) {

@@ -188,11 +188,23 @@ int32_t gollek_hip_matvec_device(gollek_hip_weight *weight, const float *x, floa
 
 /* Shapes whose output tiles leave CUs idle (m = 33..256 for 4096 rows) are
  * split over K into partial tiles held in a workspace of the handle,
- * allocated at the first such call (at most 4 MiB) and freed with the
- * handle; splitting calls on one handle share it and must not overlap (calls
+ * allocated at the first such call (at most 8 MiB on 256 CUs) and freed with
+ * the handle; splitting calls on one handle share it and must not overlap (calls
  * on different handles may).  A y that is not 16-byte aligned runs unsplit. */
 int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t m,
                                     float *y, void *stream, char *err, size_t err_len);
+
+/* gollek_hip_gemm_bf16_device without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops).  The split-K partial tiles
+ * go to a static per-GPU scratch of 8 MiB (held from library load until the
+ * process ends; enough for every m on a 256-CU MI355X) instead of the
+ * handle's lazily allocated workspace.  All calls on one GPU share that
+ * scratch, so calls that overlap on a GPU race; shapes needing more than
+ * 8 MiB -> ARG.  Same checks and results as gollek_hip_gemm_bf16_device. */
+int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *weight, const uint16_t *x_bf16,
+                                            int64_t m, float *y, void *stream, char *err,
+                                            size_t err_len);
 
 /* `workspace` (device, workspace_bytes >= gollek_hip_moe_workspace_bytes) is
  * scratch owned by the caller; calls sharing one workspace must not overlap. */
