@@ -9,6 +9,7 @@ import pytest
 from gollek_amd import synthetic as syn
 from gollek_amd import tensor_ops as ops
 from oracle import oracle as o
+from tests.test_oracle import MOE_CF_E, moe_closed_form_case, moe_closed_form_expected
 
 pytestmark = pytest.mark.gpu
 MOE_TOL = 1e-3
@@ -33,9 +34,11 @@ def _experts(E, H, I, seed):
 # when that leaves at most 1/8 of the grid idle (8 and 16 experts: tens of
 # workgroups per unit) and split the items evenly otherwise (the 128-expert
 # layer's 87 units; 210 and 314 units at 400 / 600 tokens x top-2).
+# Hidden 4096 is past the matrix-core passes (H <= 2048) and runs the v_dot4
+# expert kernels.
 @pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
                                        (128, 2048, 768, 16, 8), (32, 512, 256, 400, 2),
-                                       (32, 512, 256, 600, 2)])
+                                       (32, 512, 256, 600, 2), (8, 4096, 1536, 9, 2)])
 def test_moe_parity(E, H, I, T, k):
     print(f"[gpu] moe E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H)
@@ -46,6 +49,63 @@ def test_moe_parity(E, H, I, T, k):
     err = o.rel_err(out, ref)
     print(f"[gpu] moe rel_err={err:.3e}", flush=True)
     assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+@pytest.fixture
+def moe_variant():
+    def set_variant(v):
+        ops.set_option("moe_variant", v)
+    yield set_variant
+    ops.set_option("moe_variant", 0)
+
+
+def test_moe_v_dot4_variant_parity(moe_variant):
+    # moe_variant 1: the v_dot4 expert kernels at a shape the matrix-core
+    # passes also take.
+    E, H, I, T, k = 16, 1024, 512, 9, 4
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H)
+    ids, w = syn.moe_routing(T, E, k, seed=3)
+    x = syn.activation(T * H, seed=4).reshape(T, H)
+    moe_variant(1)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    assert o.rel_err(out, o.moe_reference_q4k(gate, up, down, E, x, ids, w)) <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_moe_closed_form(variant, moe_variant):
+    # Constant experts and tokens: every output element is
+    # sum_j w_j d_e I silu(g_e S_t) u_e S_t (see tests/test_oracle.py).
+    gate, up, down, x, ids, w = moe_closed_form_case()
+    E, H, I = MOE_CF_E, x.shape[1], gate.shape[0] // MOE_CF_E
+    tg = ops.GgufTensor("g", (H, I, E), syn.Q4_K, gate.reshape(-1))
+    tu = ops.GgufTensor("u", (H, I, E), syn.Q4_K, up.reshape(-1))
+    td = ops.GgufTensor("d", (I, H, E), syn.Q4_K, down.reshape(-1))
+    moe_variant(variant)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    assert o.rel_err(out, moe_closed_form_expected()) <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_moe_nan_activation_poisons_only_its_token(variant, moe_variant):
+    # A NaN in x makes every output of that token NaN, as in the reference's
+    # loop (gate . x is NaN), and leaves the other tokens untouched.
+    E, H, I, T, k = 8, 512, 256, 4, 2
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=31)
+    ids, w = syn.moe_routing(T, E, k, seed=32)
+    x = syn.activation(T * H, seed=33).reshape(T, H)
+    x[1, 300] = np.nan
+    moe_variant(variant)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    assert np.all(np.isnan(out[1]))
+    keep = [0, 2, 3]
+    ref = o.moe_reference_q4k(gate, up, down, E, x[keep], ids[keep], w[keep])
+    assert o.rel_err(out[keep], ref) <= MOE_TOL
     for t in (tg, tu, td):
         t.close()
 

@@ -8,6 +8,8 @@
   * mat-vec against an fp64 dot over the dequantized rows;
   * planted mistakes in a copy of the restatement are caught by the fixtures.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -185,6 +187,121 @@ def test_moe_reference_paths_agree_and_properties():
     wz[0, 0] = 0.0
     assert np.allclose(o.moe_reference_q4k(gate, up, down, E, x, bad, w),
                        o.moe_reference_q4k(gate, up, down, E, x, ids, wz), rtol=1e-12, atol=1e-12)
+
+
+# ---- MoE expert FFN in closed form ------------------------------------------
+#
+# Experts whose every gate / up / down element is one constant (Q4_K blocks
+# with equal codes; a negative d gives a negative constant, a nonzero dmin
+# with equal min codes shifts it) and tokens whose x is one constant make
+# every dot product a closed form: gate_e . x_t = g_e S_t, up_e . x_t = u_e S_t
+# (S_t = sum of x_t), every element of h = silu(g_e S_t) u_e S_t, and every
+# output element sum_j w_tj d_e I silu(g_e S_t) u_e S_t.  The constants put
+# silu in its curved range with a != b, so a gate <-> up swap, a missing
+# silu, a sigmoid in its place and a route weight applied twice each change
+# the result far beyond rounding (the planted-mistake check below).
+
+MOE_CF_E, MOE_CF_H, MOE_CF_I = 3, 256, 512
+# (d, dmin, scale code, min code, nibble): value d * sc * q - dmin * m
+MOE_CF_GATE = [(0.5, 0.25, 2, 4, 3), (-0.25, 0.0, 2, 9, 1), (0.125, 0.0, 2, 0, 1)]   # 2.0, -0.5, 0.25
+MOE_CF_UP = [(-0.25, 0.0, 1, 0, 3), (0.25, 0.0, 1, 0, 5), (0.5, 0.5, 1, 1, 2)]       # -0.75, 1.25, 0.5
+MOE_CF_DOWN = [(0.125, 0.0, 1, 0, 1), (0.0625, 0.0, 1, 3, 1), (-0.25, 0.125, 1, 2, 1)]  # 0.125, 0.0625, -0.5
+MOE_CF_IDS = np.array([[0, 1], [2, 0]], np.int32)
+MOE_CF_W = np.array([[0.75, 0.25], [0.625, 0.375]], np.float32)
+MOE_CF_XV = (1.0 / 256, -1.0 / 512)  # per-token constant x: S_t = 1.0, -0.5
+
+
+def _const_q4k(rows, cols, d, dmin, sc, m, q):
+    nsb = cols // 256
+    blk = np.zeros((rows, nsb, 144), np.uint8)
+    dd = syn.f16_bits(np.array([d, dmin], np.float32))
+    blk[..., 0], blk[..., 1] = dd[0] & 0xFF, dd[0] >> 8
+    blk[..., 2], blk[..., 3] = dd[1] & 0xFF, dd[1] >> 8
+    blk[..., 4:16] = syn.pack_q4k_scales(np.full(8, sc), np.full(8, m))
+    blk[..., 16:] = q | (q << 4)
+    return blk.reshape(rows, nsb * 144)
+
+
+def moe_closed_form_case():
+    E, H, I = MOE_CF_E, MOE_CF_H, MOE_CF_I
+    gate = np.concatenate([_const_q4k(I, H, *p) for p in MOE_CF_GATE])
+    up = np.concatenate([_const_q4k(I, H, *p) for p in MOE_CF_UP])
+    down = np.concatenate([_const_q4k(H, I, *p) for p in MOE_CF_DOWN])
+    x = np.stack([np.full(H, v, np.float32) for v in MOE_CF_XV])
+    return gate, up, down, x, MOE_CF_IDS, MOE_CF_W
+
+
+def _value(p):
+    d, dmin, sc, m, q = p
+    return d * sc * q - (dmin * m if m else 0.0)
+
+
+def moe_closed_form_expected(act=None, swap=False, weight_power=1):
+    act = act or (lambda v: v / (1.0 + math.exp(-v)))
+    out = np.zeros((len(MOE_CF_XV), MOE_CF_H))
+    for t, xv in enumerate(MOE_CF_XV):
+        S = xv * MOE_CF_H
+        for j in range(MOE_CF_IDS.shape[1]):
+            e, wj = int(MOE_CF_IDS[t, j]), float(MOE_CF_W[t, j])
+            a, b = _value(MOE_CF_GATE[e]) * S, _value(MOE_CF_UP[e]) * S
+            if swap:
+                a, b = b, a
+            out[t] += wj ** weight_power * _value(MOE_CF_DOWN[e]) * MOE_CF_I * act(a) * b
+    return out
+
+
+def test_moe_reference_closed_form():
+    gate, up, down, x, ids, w = moe_closed_form_case()
+    # the constructed blocks dequantize to the intended constants
+    for blocks, params, cols in ((gate, MOE_CF_GATE, MOE_CF_H), (up, MOE_CF_UP, MOE_CF_H),
+                                 (down, MOE_CF_DOWN, MOE_CF_I)):
+        rows = blocks.shape[0] // MOE_CF_E
+        for e, p in enumerate(params):
+            deq = o.dequantize(12, blocks[e * rows:(e + 1) * rows], cols)
+            assert np.all(deq == np.float32(_value(p))), (e, p)
+    got = o.moe_reference_q4k(gate, up, down, MOE_CF_E, x, ids, w)
+    exp = moe_closed_form_expected()
+    assert np.allclose(got, exp, rtol=1e-12, atol=1e-12)
+    # Each plausible mistake moves the answer by at least 5 %.
+    mutants = {
+        "gate/up swapped": moe_closed_form_expected(swap=True),
+        "no silu": moe_closed_form_expected(act=lambda v: v),
+        "sigmoid for silu": moe_closed_form_expected(act=lambda v: 1.0 / (1.0 + math.exp(-v))),
+        "relu for silu": moe_closed_form_expected(act=lambda v: max(v, 0.0)),
+        "route weight twice": moe_closed_form_expected(weight_power=2),
+    }
+    for name, mut in mutants.items():
+        assert np.max(np.abs(mut - exp)) > 0.05 * np.max(np.abs(exp)), name
+
+
+def _moe_reference_mutant(kind, gate, up, down, E, x, ids, w):
+    """moe_reference_q4k with one planted mistake (CPU only)."""
+    H = gate.shape[1] // 144 * 256
+    I = gate.shape[0] // E
+    out = np.zeros((ids.shape[0], H))
+    for t in range(ids.shape[0]):
+        xt = x[t].astype(np.float64)
+        for j in range(ids.shape[1]):
+            e, wj = int(ids[t, j]), float(w[t, j])
+            g = o.dequantize(12, gate[e * I:(e + 1) * I], H).astype(np.float64)
+            u = o.dequantize(12, up[e * I:(e + 1) * I], H).astype(np.float64)
+            d = o.dequantize(12, down[e * H:(e + 1) * H], I).astype(np.float64)
+            if kind == "swap":
+                h = o.silu(u @ xt) * (g @ xt)
+            elif kind == "nosilu":
+                h = (g @ xt) * (u @ xt)
+            else:  # weight applied inside the activation
+                h = o.silu(wj * (g @ xt)) * (u @ xt)
+                wj = 1.0
+            out[t] += wj * (d @ h)
+    return out
+
+
+@pytest.mark.parametrize("kind", ["swap", "nosilu", "weight_inside"])
+def test_moe_closed_form_catches_planted_mistakes(kind):
+    gate, up, down, x, ids, w = moe_closed_form_case()
+    mut = _moe_reference_mutant(kind, gate, up, down, MOE_CF_E, x, ids, w)
+    assert not np.allclose(mut, moe_closed_form_expected(), rtol=1e-3, atol=1e-6), kind
 
 
 # ---- MoE router oracle (MoeForwardPass.java:174-203, 286-306) ----------------
