@@ -11,6 +11,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <new>
 #include <string>
 
 #include "gguf_kernels.hpp"
@@ -44,7 +45,11 @@ int32_t fail(int32_t code, char *err, size_t err_len, const char *fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
-    g_last_error = buf;
+    try {
+        g_last_error = buf;
+    } catch (const std::bad_alloc &) {  // keep the status; the message is in err
+        g_last_error.clear();
+    }
     g_last_status = code;
     if (err != nullptr && err_len > 0) {
         size_t n = strlen(buf);
@@ -827,7 +832,11 @@ namespace gollek {
 
 void record_status(int32_t code, const char *message) {
     g_last_status = code;
-    g_last_error = message != nullptr ? message : "";
+    try {
+        g_last_error = message != nullptr ? message : "";
+    } catch (const std::bad_alloc &) {
+        g_last_error.clear();
+    }
 }
 
 gollek_hip_weight *weight_alloc_owned(int32_t type_id, int64_t rows, int64_t cols, int64_t row_bytes,

@@ -126,13 +126,22 @@ struct gollek_hip_gguf {
 
 namespace {
 
-void release(gollek_hip_gguf *f) {
+// Frees the upload stream, staging buffers and events (whichever exist)
+// and clears their handles.
+void release_staging(gollek_hip_gguf *f) {
     if (f->stream != nullptr) (void)hipStreamSynchronize(f->stream);
     for (int i = 0; i < 2; i++) {
         if (f->done[i] != nullptr) (void)hipEventDestroy(f->done[i]);
         if (f->stage[i] != nullptr) (void)hipHostFree(f->stage[i]);
+        f->done[i] = nullptr;
+        f->stage[i] = nullptr;
     }
     if (f->stream != nullptr) (void)hipStreamDestroy(f->stream);
+    f->stream = nullptr;
+}
+
+void release(gollek_hip_gguf *f) {
+    release_staging(f);
     if (f->map != nullptr) munmap(f->map, f->size);
     if (f->fd >= 0) close(f->fd);
     delete f;
@@ -206,7 +215,13 @@ int32_t parse(gollek_hip_gguf *f, char *err, size_t err_len) {
     f->version = c.get<int32_t>();
     const int64_t n_tensors = c.get<int64_t>();
     f->n_kv = c.get<int64_t>();
-    if (c.ok && (n_tensors < 0 || f->n_kv < 0 || (uint64_t)n_tensors > f->size || (uint64_t)f->n_kv > f->size))
+    // Every metadata entry takes at least 12 bytes (key length, type, a value
+    // of at least one byte less one) and every tensor info at least 24 (name
+    // length, dimension count, type, offset), so counts the bytes left cannot
+    // hold are rejected before anything is sized by them.
+    const uint64_t left = c.ok ? c.size - c.pos : 0;
+    if (c.ok && (n_tensors < 0 || f->n_kv < 0 || (uint64_t)f->n_kv > left / 12 ||
+                 (uint64_t)n_tensors > (left - (uint64_t)f->n_kv * 12) / 24))
         return file_fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Invalid GGUF counts: %lld tensors, %lld keys",
                          (long long)n_tensors, (long long)f->n_kv);
     for (int64_t i = 0; i < f->n_kv && c.ok; i++) {
@@ -224,7 +239,6 @@ int32_t parse(gollek_hip_gguf *f, char *err, size_t err_len) {
         const int32_t rc = skip_value(c, type, is_alignment, &f->alignment, 0, err, err_len);
         if (rc != GOLLEK_HIP_OK) return rc;
     }
-    f->tensors.reserve(c.ok ? (size_t)n_tensors : 0);
     for (int64_t i = 0; i < n_tensors && c.ok; i++) {
         TensorInfo t;
         const int64_t nlen = c.get<int64_t>();
@@ -304,7 +318,13 @@ gollek_hip_gguf *gollek_hip_gguf_open(const char *path, char *err, size_t err_le
         }
         f->map = static_cast<uint8_t *>(m);
     }
-    if (parse(f, err, err_len) != GOLLEK_HIP_OK) {
+    int32_t rc;
+    try {
+        rc = parse(f, err, err_len);
+    } catch (const std::bad_alloc &) {  // the tensor table outgrew host memory
+        rc = file_fail(GOLLEK_HIP_ERR_NOMEM, err, err_len, "Out of host memory parsing %s", path);
+    }
+    if (rc != GOLLEK_HIP_OK) {
         release(f);
         return nullptr;
     }
@@ -351,8 +371,12 @@ int32_t gollek_hip_gguf_tensor(const gollek_hip_gguf *f, int64_t index, char *na
 
 int64_t gollek_hip_gguf_find(const gollek_hip_gguf *f, const char *name) {
     if (f == nullptr || name == nullptr) return -1;
-    const auto it = f->by_name.find(name);
-    return it == f->by_name.end() ? -1 : it->second;
+    try {
+        const auto it = f->by_name.find(name);
+        return it == f->by_name.end() ? -1 : it->second;
+    } catch (const std::bad_alloc &) {  // the key string could not be built
+        return -1;
+    }
 }
 
 gollek_hip_weight *gollek_hip_gguf_upload(gollek_hip_gguf *f, int64_t index, char *err, size_t err_len) {
@@ -385,10 +409,16 @@ gollek_hip_weight *gollek_hip_gguf_upload(gollek_hip_gguf *f, int64_t index, cha
     uint8_t *dst = gollek::weight_data(w);
     std::lock_guard<std::mutex> lock(f->mu);
     hipError_t e = hipSuccess;
-    if (f->stream == nullptr) {
+    // The stream, the two pinned staging buffers and their events are set up
+    // together at the first upload: if any of them fails, all are released,
+    // so a later call sets them up again instead of using a partial set.
+    if (f->stream == nullptr || f->stage[0] == nullptr || f->stage[1] == nullptr ||
+        f->done[0] == nullptr || f->done[1] == nullptr) {
+        release_staging(f);
         e = hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking);
         for (int i = 0; i < 2 && e == hipSuccess; i++) e = hipHostMalloc(reinterpret_cast<void **>(&f->stage[i]), kStageBytes, hipHostMallocDefault);
         for (int i = 0; i < 2 && e == hipSuccess; i++) e = hipEventCreateWithFlags(&f->done[i], hipEventDisableTiming);
+        if (e != hipSuccess) release_staging(f);
     }
     // Chunk k: mapped bytes -> staging buffer k % 2 (once the copy that last
     // read that buffer has finished) -> device.

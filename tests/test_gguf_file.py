@@ -224,6 +224,22 @@ def test_malformed_fields_are_rejected(tmp_path, patch, match):
         ops.GgufFile(_write(tmp_path, data))
 
 
+@pytest.mark.parametrize("n_tensors,n_kv", [(2 ** 33, 0), (0, 2 ** 33), (2 ** 31, 2 ** 31)])
+def test_counts_beyond_what_the_file_can_hold_are_rejected(tmp_path, n_tensors, n_kv):
+    # A 64 GiB sparse file whose header claims more tensor infos (>= 24 bytes
+    # each) or metadata entries (>= 12 bytes each) than its bytes can hold is
+    # rejected before anything is sized by the counts (this used to reserve
+    # a tensor table for 2^33 entries and abort the process).
+    p = tmp_path / "sparse.gguf"
+    with open(p, "wb") as fh:
+        fh.write(b"GGUF" + struct.pack("<iqq", 3, n_tensors, n_kv))
+        fh.truncate(64 << 30)
+    if p.stat().st_blocks * 512 > (1 << 30):
+        pytest.skip("the filesystem does not keep sparse files sparse")
+    with pytest.raises(ops.IllegalArgumentError, match="counts"):
+        ops.GgufFile(p)
+
+
 def test_upload_checks_the_tensor_range_before_the_device(tmp_path):
     # GgufTensorData.checkedSlice (RT/GgufTensorData.java:97-104): the bytes
     # must lie inside the file.  Each case fails ahead of any device call.
