@@ -203,7 +203,7 @@ def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int):
         "algo_gbs": algo_bytes / (ms * 1e-3) / 1e9,
     }
     rot.close()
-    return res
+    return res, host
 
 
 def moe_workload(torch, steps: int, warmup: int, seed: int):
@@ -270,7 +270,7 @@ def moe_workload(torch, steps: int, warmup: int, seed: int):
     for _, handles in layers:
         for h in handles:
             h.close()
-    return res
+    return res, (gate, up, down, E, H, I, x, ids, w)
 
 
 def host_entry_workload(host, rows: int, cols: int, steps: int, warmup: int):
@@ -340,39 +340,102 @@ def gguf_upload_workload(host, rows: int, cols: int, copies: int = 8):
 
 # ---- CPU baseline -------------------------------------------------------------
 
-def cpu_baseline(host, cols: int):
-    """Oracle (C restatement of the reference's Java raw route) on all host
-    cores over the full Q4_K matrix: median of >= 10 reps after 2 warm-ups;
-    plus a single-thread rate on the first 1024 rows."""
+def _cpu_median(fn, min_reps: int = 10, budget_s: float = 3.0, max_reps: int = 200):
+    """Median seconds of fn() over >= min_reps runs after 2 warm-ups (more
+    runs while the budget lasts); returns (median, runs)."""
+    for _ in range(2):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_gemv(type_id: int, host, cols: int, label: str, budget_s: float = 3.0):
+    """The oracle (C restatement of the reference's Java raw mat-vec route,
+    scheduled like RT/GgufParallelConfig: all host cores, 2T row chunks) over
+    the whole matrix, plus a single-thread rate on its first 1024 rows."""
     from gollek_amd import synthetic as syn
     from oracle import oracle as o
     x = syn.activation(cols, 99)
     threads = o.default_threads()
-    for _ in range(2):
-        o.matvec(syn.Q4_K, host, cols, x, threads=threads)
-    times = []
-    t_end = time.perf_counter() + 10.0
-    while len(times) < 10 or (time.perf_counter() < t_end and len(times) < 200):
-        t0 = time.perf_counter()
-        o.matvec(syn.Q4_K, host, cols, x, threads=threads)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    sample_rows = 1024
-    sub = host[:sample_rows]
-    st = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        o.matvec(syn.Q4_K, sub, cols, x, threads=1)
-        st.append(time.perf_counter() - t0)
-    st_med = statistics.median(st)
+    med, n = _cpu_median(lambda: o.matvec(type_id, host, cols, x, threads=threads), budget_s=budget_s)
+    sub = host[:1024]
+    st, _ = _cpu_median(lambda: o.matvec(type_id, sub, cols, x, threads=1), min_reps=5, budget_s=1.0,
+                        max_reps=20)
     return {
         "value": host.size / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"full Q4_K 14336x4096 matrix ({host.size} packed bytes), median of "
-                   f"{len(times)} reps after 2 warm-ups, {threads} threads; C restatement of "
-                   f"the reference Java raw route (oracle/gguf_oracle.c)"),
+        "sample": (f"full {label} matrix ({host.size} packed bytes), median of {n} reps after 2 "
+                   f"warm-ups, {threads} threads; C restatement of the reference Java raw route "
+                   f"(oracle/gguf_oracle.c)"),
         "ms_per_matvec": med * 1e3,
-        "single_thread_gbs": sub.size / st_med / 1e9,
+        "single_thread_gbs": sub.size / st / 1e9,
     }
+
+
+def cpu_baseline(host, cols: int):
+    """cpu_baseline of the headline Q4_K 14336 x 4096 matrix."""
+    from gollek_amd import synthetic as syn
+    return cpu_gemv(syn.Q4_K, host, cols, "Q4_K 14336x4096", budget_s=5.0)
+
+
+def cpu_gemm(host, m: int, seed: int):
+    """The reference's prefill for one Q8_0 Linear: m independent matVecRows
+    (RT/GgufTensorOps.java:666-674) over the rows of X (bf16 -> fp32
+    exactly), each on all host cores.  Bounded: >= 3 reps."""
+    from gollek_amd import synthetic as syn
+    from oracle import oracle as o
+    cols = 4096
+    xb = syn.activation_bf16(m, cols, seed)
+    x = syn.bf16_to_f32(xb).reshape(m, cols)
+    threads = o.default_threads()
+
+    def run():
+        for r in range(m):
+            o.matvec(syn.Q8_0, host, cols, x[r], threads=threads)
+
+    med, n = _cpu_median(run, min_reps=3, budget_s=2.0, max_reps=50)
+    flops = 2.0 * m * host.shape[0] * cols
+    return {"value": flops / med / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "ms_per_gemm": med * 1e3, "weight_gbs_per_row_pass": host.size * m / med / 1e9,
+            "sample": (f"{m} mat-vecs of the Q8_0 4096x4096 matrix (one per row of X), median of "
+                       f"{n} reps after 2 warm-ups, {threads} threads per mat-vec; oracle")}
+
+
+def cpu_moe(gate, up, down, E: int, H: int, I: int, x, ids, wts):
+    """The reference's MoE expert loop (MoeForwardPass.java:217-240 with
+    swigluFfn): per token and route, gate and up mat-vecs of the expert's
+    Q4_K rows, silu(g) * u in fp32, the down mat-vec and the weighted add,
+    each mat-vec on all host cores (oracle)."""
+    import numpy as np
+
+    from gollek_amd import synthetic as syn
+    from oracle import oracle as o
+    threads = o.default_threads()
+    T, k = ids.shape
+
+    def run():
+        out = np.zeros((T, H), np.float32)
+        for t in range(T):
+            for j in range(k):
+                e, wj = int(ids[t, j]), np.float32(wts[t, j])
+                g = o.matvec(syn.Q4_K, gate[e * I:(e + 1) * I], H, x[t], threads=threads)
+                u = o.matvec(syn.Q4_K, up[e * I:(e + 1) * I], H, x[t], threads=threads)
+                with np.errstate(over="ignore"):  # exp(-g) = inf: silu -> -0
+                    h = (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
+                out[t] += wj * o.matvec(syn.Q4_K, down[e * H:(e + 1) * H], I, h, threads=threads)
+        return out
+
+    med, n = _cpu_median(run, min_reps=5, budget_s=3.0, max_reps=50)
+    pair_bytes = gate.shape[1] * I * 2 + down.shape[1] * H
+    return {"value": T * k * pair_bytes / med / 1e9, "unit": "GB/s (weights streamed per route)",
+            "cores": threads, "kind": "port", "ms_per_layer": med * 1e3,
+            "sample": (f"{T} tokens x top-{k} of {E} Q4_K experts (H {H}, I {I}), every route's "
+                       f"expert read per route as the reference does; median of {n} reps after 2 "
+                       f"warm-ups, {threads} threads per mat-vec; oracle")}
 
 
 def ceilings(torch, steps: int, warmup: int) -> int:
@@ -509,6 +572,8 @@ def main() -> int:
     log(f"headline {head['weight_gbs']:.1f} GB/s, {head['ms_per_step'] * 1e3:.2f} us/launch")
 
     extra = {}
+    hosts = {}  # workload -> host copy of its weights (for the CPU baselines)
+    moe_inputs = gemm_host = None
     if not args.no_extra:
         for name, t, rows, cols in (("q8_0_gemv_4096x4096", syn.Q8_0, 4096, 4096),
                                     ("q4_0_gemv_4096x11008", syn.Q4_0, 11008, 4096),
@@ -518,7 +583,7 @@ def main() -> int:
             if not want(name):
                 continue
             log(f"extra {name}")
-            r, _ = gemv_workload(torch, t, rows, cols, args.steps, args.warmup, seed=5)
+            r, hosts[name] = gemv_workload(torch, t, rows, cols, args.steps, args.warmup, seed=5)
             r["hbm_frac"] = r["weight_gbs"] / HBM_PEAK_GBS
             extra[name] = r
         have_gemm = hasattr(ops.DeviceWeight, "gemm_bf16") and _has_symbol("gollek_hip_gemm_bf16_device")
@@ -526,14 +591,15 @@ def main() -> int:
             name = f"q8_0_gemm_bf16_m{m}_4096x4096"
             if have_gemm and want(name):
                 log(f"extra {name}")
-                extra[name] = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
+                extra[name], gemm_host = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
         if want("q4_k_gemv_host_entry_4096x14336"):
             log("extra host-buffer entry point")
             extra["q4_k_gemv_host_entry_4096x14336"] = host_entry_workload(
                 host, 14336, 4096, args.steps, args.warmup)
         if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e128_top8_t16"):
             log("extra moe")
-            extra["moe_q4_k_e128_top8_t16"] = moe_workload(torch, args.steps, args.warmup, seed=11)
+            extra["moe_q4_k_e128_top8_t16"], moe_inputs = moe_workload(torch, args.steps, args.warmup,
+                                                                      seed=11)
         if _has_symbol("gollek_hip_gguf_upload") and want("gguf_upload_q4_k_4096x14336"):
             log("extra gguf upload")
             extra["gguf_upload_q4_k_4096x14336"] = gguf_upload_workload(host, 14336, 4096)
@@ -542,6 +608,22 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline (oracle restatement of the reference raw route)")
         cpu = cpu_baseline(host, 4096)
+        # The other configurations, each on a bounded sample (a few seconds).
+        cpus = {}
+        for name, t, cols, label in (("q8_0_gemv_4096x4096", syn.Q8_0, 4096, "Q8_0 4096x4096"),
+                                     ("q4_0_gemv_4096x11008", syn.Q4_0, 4096, "Q4_0 11008x4096"),
+                                     ("q4_k_gemv_4096x128256", syn.Q4_K, 4096, "Q4_K 128256x4096")):
+            if name in hosts:
+                log(f"cpu baseline {name}")
+                cpus[name] = cpu_gemv(t, hosts[name], cols, label, budget_s=2.0)
+        if gemm_host is not None:
+            for m in (16, 128, 512):
+                log(f"cpu baseline gemm m={m}")
+                cpus[f"q8_0_gemm_bf16_m{m}_4096x4096"] = cpu_gemm(gemm_host, m, seed=8)
+        if moe_inputs is not None:
+            log("cpu baseline moe")
+            cpus["moe_q4_k_e128_top8_t16"] = cpu_moe(*moe_inputs)
+        extra["cpu_baselines"] = cpus
 
     ms = head["ms_per_step"]
     value = head["weight_gbs"]
