@@ -1,0 +1,355 @@
+package tech.kayys.gollek.gguf.runtime;
+
+import tech.kayys.gollek.gguf.loader.GGUFModel;
+import tech.kayys.gollek.gguf.loader.GGUFTensorInfo;
+
+import java.lang.foreign.Arena;
+import java.lang.foreign.FunctionDescriptor;
+import java.lang.foreign.Linker;
+import java.lang.foreign.MemorySegment;
+import java.lang.foreign.SymbolLookup;
+import java.lang.foreign.ValueLayout;
+import java.lang.invoke.MethodHandle;
+import java.nio.charset.StandardCharsets;
+import java.nio.file.Files;
+import java.nio.file.Path;
+import java.util.IdentityHashMap;
+import java.util.Map;
+import java.util.WeakHashMap;
+
+/**
+ * MI355X (gfx950) route of the GGUF mat-vec, dot and row dequantization
+ * through libgollek_hip.so, the C ABI of include/gollek_hip.h, bound with the
+ * FFM API the way the CLI binds its native bridge
+ * (ui/gollek-cli/src/main/java/tech/kayys/gollek/cli/commands/GgufFastRun.java:1915-1990:
+ * System.load, SymbolLookup.libraryLookup, Linker.downcallHandle).
+ *
+ * <p>Hooks (this class is package-private in the runtime package, next to
+ * GgufMatVec and GgufTensorData):</p>
+ * <ul>
+ * <li>GgufMatVec.rows (RT/GgufMatVec.java:55-96), after the row-count and
+ * output-length checks and before the prepared and raw routes:
+ * <pre>
+ * if (GgufHipMatVec.tryRows(model, tensor, rows, columns, layout.rowBytes(), vector, output, rowCount)) {
+ *     return;
+ * }
+ * </pre></li>
+ * <li>GgufTensorOps.dotRow and dequantizeRow (RT/GgufTensorOps.java:636-650),
+ * after checkLayoutRow: {@code tryDotRow} / {@code tryDequantizeRow}, falling
+ * through to the Java code when they return false.</li>
+ * <li>GgufTensorOps.clearPreparedMatrixCaches, which JavaNativeGgufBackend.close
+ * calls (core/plugin/gollek-plugin-runner-gguf/.../JavaNativeGgufBackend.java:139-143):
+ * {@code GgufHipMatVec.release(model)}.</li>
+ * </ul>
+ *
+ * <p>The route is taken when the system property gollek.hip.enabled is not
+ * "false", the library (gollek.hip.library, default libgollek_hip.so on the
+ * library path) loads with ABI major 1, gollek_hip_init accepts device
+ * gollek.hip.device (default 0), and the tensor's ggml type is one the
+ * library multiplies (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K).  Otherwise the try
+ * methods return false and the Java routes run unchanged.  A tensor's bytes
+ * (GgufTensorData.tensorData, a slice of the model's mapped segment) are
+ * copied to the device once, at its first use, and the device handle lives
+ * until release(model).</p>
+ *
+ * <p>Status codes map back to the exceptions the Java route throws
+ * (RT/GgufMatVec.java:32-35, 65-71, 196-200; RT/GgufRowDot.java:77-82;
+ * GC/core/GgmlType.java:70-81): NULL to NullPointerException, ARG to
+ * IllegalArgumentException, UNSUPPORTED to UnsupportedOperationException;
+ * DEVICE and NOMEM, which have no Java counterpart, to
+ * IllegalStateException.  The library's message is the exception's.</p>
+ */
+final class GgufHipMatVec {
+    static final int OK = 0;
+    static final int ERR_NULL = -1;
+    static final int ERR_ARG = -2;
+    static final int ERR_UNSUPPORTED = -3;
+    static final int ERR_DEVICE = -4;
+    static final int ERR_NOMEM = -5;
+
+    private static final int ABI_MAJOR = 1;
+    private static final int ERR_LEN = 512;
+
+    /** Device handles per model and tensor (GGUFTensorInfo is a record over an array: identity keys). */
+    private static final Map<GGUFModel, Map<GGUFTensorInfo, MemorySegment>> HANDLES = new WeakHashMap<>();
+
+    private GgufHipMatVec() {
+    }
+
+    static boolean supportsType(int typeId) {
+        return typeId == 2 || typeId == 8 || typeId == 12 || typeId == 13 || typeId == 14;
+    }
+
+    /** output[r] = row r of the tensor . vector for r < rowCount; false when the route is not taken. */
+    static boolean tryRows(GGUFModel model, GGUFTensorInfo tensor, long rows, int columns, long rowBytes,
+                           float[] vector, float[] output, int rowCount) {
+        Binding b = Binding.get();
+        if (b == null || !supportsType(tensor.typeId())) {
+            return false;
+        }
+        MemorySegment w = handle(b, model, tensor, rows, columns, rowBytes);
+        try (Arena arena = Arena.ofConfined()) {
+            MemorySegment err = arena.allocate(ERR_LEN);
+            int rc = b.matvecRows(w, MemorySegment.ofArray(vector), (long) vector.length,
+                    MemorySegment.ofArray(output), (long) output.length, (long) rowCount, err, (long) ERR_LEN);
+            check(rc, err);
+        }
+        return true;
+    }
+
+    /** Row {@code row} of the tensor . vector into out[0]; false when the route is not taken. */
+    static boolean tryDotRow(GGUFModel model, GGUFTensorInfo tensor, long rows, int columns, long rowBytes,
+                             long row, float[] vector, float[] out) {
+        Binding b = Binding.get();
+        if (b == null || !supportsType(tensor.typeId())) {
+            return false;
+        }
+        MemorySegment w = handle(b, model, tensor, rows, columns, rowBytes);
+        try (Arena arena = Arena.ofConfined()) {
+            MemorySegment err = arena.allocate(ERR_LEN);
+            int rc = b.dotRow(w, row, MemorySegment.ofArray(vector), (long) vector.length,
+                    MemorySegment.ofArray(out), err, (long) ERR_LEN);
+            check(rc, err);
+        }
+        return true;
+    }
+
+    /** Row {@code row} dequantized into dst[0, columns), bit-exact with GgufRowDequantizer. */
+    static boolean tryDequantizeRow(GGUFModel model, GGUFTensorInfo tensor, long rows, int columns, long rowBytes,
+                                    long row, float[] dst) {
+        Binding b = Binding.get();
+        if (b == null || !supportsType(tensor.typeId())) {
+            return false;
+        }
+        MemorySegment w = handle(b, model, tensor, rows, columns, rowBytes);
+        try (Arena arena = Arena.ofConfined()) {
+            MemorySegment err = arena.allocate(ERR_LEN);
+            int rc = b.dequantizeRows(w, row, 1L, MemorySegment.ofArray(dst), (long) dst.length, err,
+                    (long) ERR_LEN);
+            check(rc, err);
+        }
+        return true;
+    }
+
+    /** Frees every device handle of the model (the prepared-cache clear). */
+    static void release(GGUFModel model) {
+        Binding b = Binding.get();
+        Map<GGUFTensorInfo, MemorySegment> handles;
+        synchronized (HANDLES) {
+            handles = HANDLES.remove(model);
+        }
+        if (b == null || handles == null) {
+            return;
+        }
+        for (MemorySegment w : handles.values()) {
+            b.weightFree(w);
+        }
+    }
+
+    private static MemorySegment handle(Binding b, GGUFModel model, GGUFTensorInfo tensor, long rows, int columns,
+                                        long rowBytes) {
+        synchronized (HANDLES) {
+            Map<GGUFTensorInfo, MemorySegment> perModel = HANDLES.computeIfAbsent(model, m -> new IdentityHashMap<>());
+            MemorySegment w = perModel.get(tensor);
+            if (w != null) {
+                return w;
+            }
+            MemorySegment bytes = GgufTensorData.tensorData(model, tensor);
+            try (Arena arena = Arena.ofConfined()) {
+                MemorySegment err = arena.allocate(ERR_LEN);
+                w = b.weightUpload(tensor.typeId(), bytes, rows, (long) columns, rowBytes, err, (long) ERR_LEN);
+                if (w.address() == 0L) {
+                    check(b.lastStatus(), err);
+                    throw new IllegalStateException("gollek_hip_weight_upload returned no handle");
+                }
+            }
+            perModel.put(tensor, w);
+            return w;
+        }
+    }
+
+    private static void check(int rc, MemorySegment err) {
+        if (rc == OK) {
+            return;
+        }
+        String message = err.getString(0L, StandardCharsets.UTF_8);
+        switch (rc) {
+            case ERR_NULL -> throw new NullPointerException(message);
+            case ERR_ARG -> throw new IllegalArgumentException(message);
+            case ERR_UNSUPPORTED -> throw new UnsupportedOperationException(message);
+            default -> throw new IllegalStateException(message);
+        }
+    }
+
+    /** The library's downcall handles, one per exported function this class uses. */
+    static final class Binding {
+        private static final Object LOCK = new Object();
+        private static volatile Binding instance;
+        private static volatile boolean unavailable;
+
+        private final MethodHandle version;
+        private final MethodHandle init;
+        private final MethodHandle lastStatus;
+        private final MethodHandle weightUpload;
+        private final MethodHandle weightFree;
+        private final MethodHandle matvecRows;
+        private final MethodHandle dotRow;
+        private final MethodHandle dequantizeRows;
+
+        /** The binding, or null when the route is disabled or the library cannot be used here. */
+        static Binding get() {
+            Binding b = instance;
+            if (b != null || unavailable) {
+                return b;
+            }
+            synchronized (LOCK) {
+                if (instance == null && !unavailable) {
+                    try {
+                        if ("false".equals(System.getProperty("gollek.hip.enabled", "true"))) {
+                            unavailable = true;
+                        } else {
+                            instance = new Binding(libraryPath(), Integer.getInteger("gollek.hip.device", 0).intValue());
+                        }
+                    } catch (Throwable t) {
+                        unavailable = true;  // no library, no device or a mismatched ABI: stay on the Java routes
+                    }
+                }
+                return instance;
+            }
+        }
+
+        private static Path libraryPath() {
+            String configured = System.getProperty("gollek.hip.library");
+            if (configured != null && !configured.isBlank()) {
+                return Path.of(configured);
+            }
+            for (String dir : System.getProperty("java.library.path", "").split(java.io.File.pathSeparator)) {
+                if (!dir.isBlank()) {
+                    Path candidate = Path.of(dir, System.mapLibraryName("gollek_hip"));
+                    if (Files.isRegularFile(candidate)) {
+                        return candidate;
+                    }
+                }
+            }
+            return Path.of(System.mapLibraryName("gollek_hip"));
+        }
+
+        private Binding(Path library, int device) throws Throwable {
+            System.load(library.toAbsolutePath().toString());
+            Linker linker = Linker.nativeLinker();
+            SymbolLookup lookup = SymbolLookup.libraryLookup(library, Arena.global());
+            this.version = downcall(linker, lookup, "gollek_hip_version",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT), false);
+            this.init = downcall(linker, lookup, "gollek_hip_init",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.JAVA_INT, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
+            this.lastStatus = downcall(linker, lookup, "gollek_hip_last_status",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT), false);
+            this.weightUpload = downcall(linker, lookup, "gollek_hip_weight_upload",
+                    FunctionDescriptor.of(ValueLayout.ADDRESS,
+                            ValueLayout.JAVA_INT, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.JAVA_LONG,
+                            ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
+            this.weightFree = downcall(linker, lookup, "gollek_hip_weight_free",
+                    FunctionDescriptor.ofVoid(ValueLayout.ADDRESS), false);
+            // The float[] arguments are passed as heap segments: critical downcalls with heap access.
+            this.matvecRows = downcall(linker, lookup, "gollek_hip_matvec_rows",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS,
+                            ValueLayout.JAVA_LONG, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG),
+                    true);
+            this.dotRow = downcall(linker, lookup, "gollek_hip_dot_row",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), true);
+            this.dequantizeRows = downcall(linker, lookup, "gollek_hip_dequantize_rows",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS,
+                            ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), true);
+            int abi = (int) version.invokeExact();
+            if (abi / 10000 != ABI_MAJOR) {
+                throw new IllegalStateException("libgollek_hip ABI " + abi + " is not major " + ABI_MAJOR);
+            }
+            try (Arena arena = Arena.ofConfined()) {
+                MemorySegment err = arena.allocate(ERR_LEN);
+                int rc = (int) init.invokeExact(device, err, (long) ERR_LEN);
+                if (rc != OK) {
+                    throw new IllegalStateException(err.getString(0L, StandardCharsets.UTF_8));
+                }
+            }
+        }
+
+        private static MethodHandle downcall(Linker linker, SymbolLookup lookup, String name,
+                                             FunctionDescriptor descriptor, boolean heapArguments) {
+            MemorySegment symbol = lookup.find(name).orElseThrow(
+                    () -> new IllegalStateException("libgollek_hip does not export " + name));
+            return heapArguments
+                    ? linker.downcallHandle(symbol, descriptor, Linker.Option.critical(true))
+                    : linker.downcallHandle(symbol, descriptor);
+        }
+
+        // Typed entry points: their primitive parameters match the descriptors
+        // exactly, as invokeExact requires (no boxing, no widening).
+
+        int lastStatus() {
+            try {
+                return (int) lastStatus.invokeExact();
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        MemorySegment weightUpload(int typeId, MemorySegment hostBytes, long rows, long cols, long rowBytes,
+                                   MemorySegment err, long errLen) {
+            try {
+                return (MemorySegment) weightUpload.invokeExact(typeId, hostBytes, rows, cols, rowBytes, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        void weightFree(MemorySegment weight) {
+            try {
+                weightFree.invokeExact(weight);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int matvecRows(MemorySegment weight, MemorySegment x, long xLen, MemorySegment y, long yLen, long rowCount,
+                       MemorySegment err, long errLen) {
+            try {
+                return (int) matvecRows.invokeExact(weight, x, xLen, y, yLen, rowCount, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int dotRow(MemorySegment weight, long row, MemorySegment x, long xLen, MemorySegment out, MemorySegment err,
+                   long errLen) {
+            try {
+                return (int) dotRow.invokeExact(weight, row, x, xLen, out, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int dequantizeRows(MemorySegment weight, long row0, long nrows, MemorySegment dst, long dstLen,
+                           MemorySegment err, long errLen) {
+            try {
+                return (int) dequantizeRows.invokeExact(weight, row0, nrows, dst, dstLen, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        private static RuntimeException propagate(Throwable t) {
+            if (t instanceof RuntimeException r) {
+                return r;
+            }
+            if (t instanceof Error e) {
+                throw e;
+            }
+            return new IllegalStateException(t);
+        }
+    }
+}
