@@ -1139,7 +1139,7 @@ int ring_splits(int M, int N, int K) {
     const int tiles = (M + kBigBM - 1) / kBigBM * (N / kBigBN);
     const int nst = K / 64;
     int S = 1;
-    while (S < 8 && tiles * 2 * S <= tuning().cu_count && nst % (2 * S) == 0) S *= 2;
+    while (S < 8 && tiles * 2 * S <= device_cus() && nst % (2 * S) == 0) S *= 2;
     return S;
 }
 

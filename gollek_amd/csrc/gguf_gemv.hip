@@ -440,7 +440,7 @@ hipError_t launch_fixed(int type_id, const uint8_t *w, int64_t row_bytes, int64_
     const LaunchTuning &t = tuning();
     int64_t rpw = t.gemv_rows_per_wave;
     if (rpw <= 0) {
-        const int64_t target_waves = (int64_t)t.cu_count * t.gemv_waves_per_cu;
+        const int64_t target_waves = (int64_t)device_cus() * t.gemv_waves_per_cu;
         rpw = (rows + target_waves - 1) / target_waves;
     }
     rpw = ((rpw + RG - 1) / RG) * RG;  // whole row groups

@@ -833,7 +833,7 @@ struct MfmaPlan {
 
 MfmaPlan plan_mfma(int64_t rows, int nsb) {
     MfmaPlan p;
-    const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+    const int64_t cus = device_cus();
     int64_t grid = (rows + kTileRows - 1) / kTileRows;  // at least a tile per workgroup
     if (grid > cus) grid = cus;
     int64_t per = (rows + grid - 1) / grid;
@@ -875,7 +875,7 @@ bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const voi
 hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream) {
     const int nsb = (int)(cols / kQK);
-    const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+    const int64_t cus = device_cus();
     const int variant = tuning().gemv_variant;
     // At most 64 rows per CU: every workgroup's share stays in LDS, one
     // superblock column per wave (gemv_variant 3 keeps the shared tiles).

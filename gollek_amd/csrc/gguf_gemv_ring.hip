@@ -321,7 +321,7 @@ hipError_t launch_ring(const uint8_t *w, int64_t row_bytes, int64_t cols, const 
                        int64_t rows, hipStream_t stream) {
     // Waves per workgroup: enough rows that the grid is about one workgroup
     // per CU (each workgroup stages all of x), at least four, within LDS.
-    const int64_t cus = tuning().cu_count > 0 ? tuning().cu_count : 256;
+    const int64_t cus = device_cus();
     const int lds_cap = 160 * 1024;
     int waves = (int)((rows + kGrWaveRows * cus - 1) / (kGrWaveRows * cus));
     if (waves < 4) waves = 4;

@@ -4,23 +4,34 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stdint.h>
 
 namespace gollek {
 
-// Tunables read by the launchers.  Zero means "pick automatically".
+// Kernel selection knobs read by the launchers (gollek_hip_set_option).
+// Process-wide and atomic: a set_option call on one thread and launches on
+// others do not race, and a launch sees either the old or the new value.
+// Zero means "pick automatically".
 struct LaunchTuning {
-    int cu_count = 256;          // compute units of the current device
-    int64_t gemv_rows_per_wave = 0;
-    int gemv_row_batch = 0;      // rows per load batch (1, 2, 4, 8)
-    int gemv_waves_per_cu = 8;   // target resident waves per CU
-    int gemm_variant = 0;
-    int gemm_big_config = 0;     // large-M GEMM: 0 buffer->LDS ring, 1..4 register-pipelined (sweeps)
-    int gemv_variant = 0;        // Q4_K: 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring,
-                                 // 3 matrix cores with shared tiles for K <= 4096
-    int moe_variant = 0;         // 0 auto (matrix cores), 1 v_dot4 expert kernels
+    std::atomic<int> cu_count{256};          // compute units of the current device
+    std::atomic<int64_t> gemv_rows_per_wave{0};
+    std::atomic<int> gemv_row_batch{0};      // rows per load batch (1, 2, 4, 8)
+    std::atomic<int> gemv_waves_per_cu{8};   // target resident waves per CU
+    std::atomic<int> gemm_variant{0};
+    std::atomic<int> gemm_big_config{0};     // large-M GEMM: 0 buffer->LDS ring, 1..4 register-pipelined
+    std::atomic<int> gemv_variant{0};        // Q4_K: 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring,
+                                             // 3 matrix cores with shared tiles for K <= 4096
+    std::atomic<int> moe_variant{0};         // 0 auto (matrix cores), 1 v_dot4 expert kernels
 };
 LaunchTuning &tuning();
+
+// Compute units of the current device (256 until a device is initialised).
+inline int device_cus() {
+    const int c = tuning().cu_count.load(std::memory_order_relaxed);
+    return c > 0 ? c : 256;
+}
 
 hipError_t launch_dequant(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                           int64_t row0, int64_t nrows, float *out, hipStream_t stream);

@@ -552,7 +552,7 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
     const MoeTileGeom g0 = make_geom(0, E, H, I), g1 = make_geom(1, E, H, I);
     hipError_t e = launch_moe_route(ids, wts, P, E, g0.tiles_e, g1.tiles_e, meta, stream);
     if (e != hipSuccess) return e;
-    const unsigned grid = (unsigned)(tuning().cu_count > 0 ? tuning().cu_count : 256);
+    const unsigned grid = (unsigned)device_cus();
     float *hbuf = reinterpret_cast<float *>(ws + L.h);
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
     hipLaunchKernelGGL(moe_expert_tile_kernel<0>, dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0, x,

@@ -78,7 +78,10 @@ const char *gollek_hip_last_error(void);
  * success).  Lets a caller map a NULL handle back to the exception type. */
 int32_t gollek_hip_last_status(void);
 
-/* Tuning knobs for benchmarks and sweeps (keys: "gemv_rows_per_wave",
+/* Kernel selection for tests, benchmarks and sweeps; the Java adapter never
+ * calls it, and the defaults are the measured choices.  The setting is
+ * process-wide (every device and thread) and atomic: launches on other
+ * threads see the old or the new value, never a torn one.  Keys: "gemv_rows_per_wave",
  * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
  * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
  * 0 = the matrix-core kernel (Q4_K) and the buffer->LDS ring kernels (Q8_0,
@@ -311,7 +314,7 @@ int64_t gollek_hip_gguf_find(const gollek_hip_gguf *file, const char *name);
  * GC/runtime/GgufTensorData.java:97-104 followed by gollek_hip_weight_upload:
  * bytes outside the file -> ARG "Tensor data range is outside model segment:
  * NAME"; then the validation of gollek_hip_weight_upload (types other than
- * Q4_0 / Q8_0 / Q4_K -> UNSUPPORTED).  Free the handle with
+ * Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K -> UNSUPPORTED).  Free the handle with
  * gollek_hip_weight_free.  Thread-safe; uploads from one file object
  * serialise on its staging buffers. */
 gollek_hip_weight *gollek_hip_gguf_upload(gollek_hip_gguf *file, int64_t index, char *err,
