@@ -579,6 +579,7 @@ def main() -> int:
                                     ("q4_0_gemv_4096x11008", syn.Q4_0, 11008, 4096),
                                     ("q4_k_gemv_4096x128256", syn.Q4_K, 128256, 4096),
                                     ("q6_k_gemv_14336x4096", syn.Q6_K, 4096, 14336),
+                                    ("q6_k_gemv_4096x128256", syn.Q6_K, 128256, 4096),
                                     ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, 4096)):
             if not want(name):
                 continue
@@ -612,7 +613,10 @@ def main() -> int:
         cpus = {}
         for name, t, cols, label in (("q8_0_gemv_4096x4096", syn.Q8_0, 4096, "Q8_0 4096x4096"),
                                      ("q4_0_gemv_4096x11008", syn.Q4_0, 4096, "Q4_0 11008x4096"),
-                                     ("q4_k_gemv_4096x128256", syn.Q4_K, 4096, "Q4_K 128256x4096")):
+                                     ("q4_k_gemv_4096x128256", syn.Q4_K, 4096, "Q4_K 128256x4096"),
+                                     ("q6_k_gemv_14336x4096", syn.Q6_K, 14336, "Q6_K 4096x14336"),
+                                     ("q6_k_gemv_4096x128256", syn.Q6_K, 4096, "Q6_K 128256x4096"),
+                                     ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, "Q5_K 4096x4096")):
             if name in hosts:
                 log(f"cpu baseline {name}")
                 cpus[name] = cpu_gemv(t, hosts[name], cols, label, budget_s=2.0)

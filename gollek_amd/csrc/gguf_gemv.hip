@@ -344,7 +344,8 @@ __global__ __launch_bounds__(256) void gemv_q4_0_kernel(const uint8_t *__restric
 
 // Any row length and alignment: one wave per row, one lane per block, byte
 // loads.  Used for shapes the fast kernels do not cover (odd block counts,
-// very long rows, unaligned borrowed buffers).
+// very long rows, unaligned borrowed buffers: x not 16-byte aligned, or
+// weights off the alignment a fast kernel reads them at).
 __device__ float generic_block_dot(int type_id, const uint8_t *blk, const float *xb) {
     if (type_id == kQ8_0) {
         const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
@@ -362,6 +363,24 @@ __device__ float generic_block_dot(int type_id, const uint8_t *blk, const float 
         }
         return d * s;
     }
+    if (type_id == kQ6_K) {  // element e: scale e / 16, code - 32
+        const float d = half_bits_to_float_fast((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+        float total = 0.0f;
+        for (int g = 0; g < 16; g++) {
+            float s = 0.0f;
+            for (int k = 0; k < 16; k++) {
+                const int e = 16 * g + k, h = e >> 7, j = (e >> 5) & 3, l = e & 31;
+                const int ql = blk[64 * h + 32 * (j & 1) + l];
+                const int q = ((j < 2 ? ql : ql >> 4) & 0x0F) | (((blk[128 + 32 * h + l] >> (2 * j)) & 3) << 4);
+                s = fmaf((float)(q - 32), xb[e], s);
+            }
+            total = fmaf(d * (float)(int8_t)blk[192 + g], s, total);
+        }
+        return total;
+    }
+    // Q4_K, or Q5_K (qh[32] at 16, quants at 48; bit 2c / 2c+1 of qh[i] adds 16)
+    const bool q5 = type_id == kQ5_K;
+    const int qs = q5 ? 48 : 16;
     const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
     const float dmin = half_bits_to_float_fast((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
     float total = 0.0f;
@@ -371,10 +390,11 @@ __device__ float generic_block_dot(int type_id, const uint8_t *blk, const float 
         q4k_code(blk + 4, 2 * c + 1, &sc2, &mc2);
         float a1 = 0.0f, a2 = 0.0f, v1 = 0.0f, v2 = 0.0f;
         for (int i = 0; i < 32; i++) {
-            const int q = blk[16 + 32 * c + i];
+            const int q = blk[qs + 32 * c + i];
+            const int hb = q5 ? blk[16 + i] : 0;
             const float x1 = xb[64 * c + i], x2 = xb[64 * c + 32 + i];
-            a1 = fmaf((float)(q & 0x0F), x1, a1);
-            a2 = fmaf((float)(q >> 4), x2, a2);
+            a1 = fmaf((float)((q & 0x0F) + (((hb >> (2 * c)) & 1) << 4)), x1, a1);
+            a2 = fmaf((float)((q >> 4) + (((hb >> (2 * c + 1)) & 1) << 4)), x2, a2);
             v1 += x1;
             v2 += x2;
         }
@@ -474,7 +494,8 @@ hipError_t launch_rb(int type_id, const uint8_t *w, int64_t row_bytes, int64_t c
 
 const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, const void *w,
                               const float *x) {
-    if (is_k56(type_id)) return "gemv_k56_kernel";
+    if (is_k56(type_id))
+        return gemv_k56_supported(type_id, row_bytes, w, x) ? "gemv_k56_kernel" : "gemv_generic_kernel";
     const GemvPlan p = plan_for(type_id, row_bytes, cols, w, x);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_mfma_kernel";
     if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_dot4_kernel";
@@ -488,17 +509,15 @@ const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, cons
 hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                        const float *x, float *y, int64_t rows, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    if (is_k56(type_id))
-        return gemv_k56_supported(type_id, row_bytes, w, x)
-                   ? launch_gemv_k56(type_id, w, row_bytes, cols, x, y, rows, stream)
-                   : hipErrorInvalidValue;
+    if (is_k56(type_id) && gemv_k56_supported(type_id, row_bytes, w, x))
+        return launch_gemv_k56(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q4k_mfma(w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q4k_dot4(w, row_bytes, cols, x, y, rows, stream);
     if (gemv_ring_supported(type_id, row_bytes, cols, rows, w, x))
         return launch_gemv_ring(type_id, w, row_bytes, cols, x, y, rows, stream);
-    const GemvPlan p = plan_for(type_id, row_bytes, cols, w, x);
+    const GemvPlan p = is_k56(type_id) ? GemvPlan() : plan_for(type_id, row_bytes, cols, w, x);
 #define GOLLEK_GEMV_CASE(L, R)                                                                \
     if (p.lpr == L && p.rounds == R)                                                          \
         return launch_rb<L, R>(type_id, w, row_bytes, cols, x, y, rows, stream);
@@ -511,8 +530,12 @@ hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t
     GOLLEK_GEMV_CASE(8, 1)
     GOLLEK_GEMV_CASE(8, 3)
 #undef GOLLEK_GEMV_CASE
-    const int bs = type_id == kQ4_K ? kQK : 32;
-    const int bb = type_id == kQ4_K ? kQKBlockBytes : (type_id == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes);
+    const int bs = (type_id == kQ4_K || is_k56(type_id)) ? kQK : 32;
+    const int bb = type_id == kQ4_K   ? kQKBlockBytes
+                   : type_id == kQ5_K ? 176
+                   : type_id == kQ6_K ? 210
+                   : type_id == kQ8_0 ? kQ8BlockBytes
+                                      : kQ4BlockBytes;
     const int nb = (int)(cols / bs);
     const unsigned grid = (unsigned)((rows + 3) / 4);
     hipLaunchKernelGGL(gemv_generic_kernel, dim3(grid), dim3(256), 0, stream, type_id, w, row_bytes,

@@ -52,7 +52,9 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
 // Q5_K / Q6_K (gguf_k56.hip): dequantization and the GEMV; the GEMV needs
-// gemv_k56_supported (x 16-byte aligned, weights 2-byte aligned).
+// gemv_k56_supported (x 16-byte aligned, Q6_K weights 2-byte and Q5_K
+// weights 4-byte aligned); launch_gemv runs other buffers on the generic
+// kernel.
 bool is_k56(int type_id);
 hipError_t launch_dequant_k56(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                               int64_t row0, int64_t nrows, float *out, hipStream_t stream);

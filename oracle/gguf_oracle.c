@@ -20,6 +20,17 @@
 
 #define QK_K 256
 
+/* GO_PLANT n (n > 0) builds a copy with one planted mistake, for the tests
+ * that show the oracle's checks catch it (never set in the built oracle):
+ *   1  Q5_K low codes take their high bit from the high codes' plane
+ *   2  Q6_K direct dots drop the -32 offset
+ *   3  Q6_K second-half groups use the first half's scales
+ *   4  Q6_K group-sum dots subtract the wrong 16-element x sum
+ *   5  Q4_K / Q5_K second sub-block of a chunk uses the first one's min */
+#ifndef GO_PLANT
+#define GO_PLANT 0
+#endif
+
 /* ---- format geometry (GC/core/GgmlType.java:11,16,21,70-81) ------------ */
 
 int go_block_size(int type_id) {
@@ -295,24 +306,47 @@ static float dot_q4_0(const uint8_t *row, int64_t cols, const float *x) {
     return sum;
 }
 
-/* ---- Q4_K raw dots (RT/GgufQ4RawDot.java) -------------------------------- */
+/* ---- Q4_K / Q5_K raw dots (RT/GgufQ4RawDot.java, RT/GgufQ5RawDot.java) ---
+ * Q5_K is Q4_K's block with 32 bytes of high bits placed before the quants
+ * (176 bytes: d, dmin, 12 scale bytes, qh[32], qs[128]).  Its code for
+ * element i of chunk c is the Q4_K nibble plus 16 x bit 2c (low nibbles) or
+ * bit 2c+1 (high nibbles) of qh[i]; every loop, accumulator and branch of the
+ * Java Q5_K dots is otherwise that of the Q4_K ones (RT/GgufQ5RawDot.java:
+ * 37-172 beside RT/GgufQ4RawDot.java:37-146, :174-329 beside :148-329,
+ * :393-795 beside :331-674), so one set of functions serves both. */
 
-/* Partial dots of one 64-element chunk: the low nibbles of the 32 bytes pair
- * with x[0..32), the high nibbles with x[32..64).  Accumulated in groups of 8
- * exactly as the Java loops do (RT/GgufQ4RawDot.java:83-131, :642-668). */
-static void q4k_chunk_dots(const uint8_t *q, const float *x, float *qd1, float *qd2,
-                           float *vs1, float *vs2) {
+typedef struct {
+    int bytes; /* block bytes */
+    int qs;    /* offset of the 128 quant bytes */
+    int qh;    /* offset of the 32 high-bit bytes, -1 without */
+} kfmt;
+
+static const kfmt KF_Q4 = {144, 16, -1};
+static const kfmt KF_Q5 = {176, 48, 16};
+
+/* Partial dots of one 64-element chunk c: the low codes of the 32 bytes pair
+ * with x[0..32), the high codes with x[32..64).  Accumulated in groups of 8
+ * exactly as the Java loops do (RT/GgufQ4RawDot.java:83-131, :642-668;
+ * RT/GgufQ5RawDot.java:87-153, :740-790: eight products summed left to
+ * right, then added to the chunk's accumulator). */
+static void k_chunk_dots(const uint8_t *blk, const kfmt *f, int c, const float *x,
+                         float *qd1, float *qd2, float *vs1, float *vs2) {
+    const uint8_t *q = blk + f->qs + 32 * c;
+    const uint8_t *qh = f->qh >= 0 ? blk + f->qh : NULL;
     float a1 = 0.0f, a2 = 0.0f, v1 = 0.0f, v2 = 0.0f;
     for (int i = 0; i < 32; i += 8) {
-        float t1 = (float)(q[i] & 0x0F) * x[i];
-        float t2 = (float)(q[i] >> 4) * x[32 + i];
-        float u1 = x[i];
-        float u2 = x[32 + i];
-        for (int k = 1; k < 8; k++) {
-            t1 += (float)(q[i + k] & 0x0F) * x[i + k];
-            t2 += (float)(q[i + k] >> 4) * x[32 + i + k];
-            u1 += x[i + k];
-            u2 += x[32 + i + k];
+        float t1 = 0.0f, t2 = 0.0f, u1 = 0.0f, u2 = 0.0f;
+        for (int k = 0; k < 8; k++) {
+            int lo = q[i + k] & 0x0F, hi = q[i + k] >> 4;
+            if (qh) {
+                lo += ((qh[i + k] >> (GO_PLANT == 1 ? 2 * c + 1 : 2 * c)) & 1) << 4;
+                hi += ((qh[i + k] >> (2 * c + 1)) & 1) << 4;
+            }
+            float p1 = (float)lo * x[i + k], p2 = (float)hi * x[32 + i + k];
+            t1 = k ? t1 + p1 : p1;
+            t2 = k ? t2 + p2 : p2;
+            u1 = k ? u1 + x[i + k] : x[i + k];
+            u2 = k ? u2 + x[32 + i + k] : x[32 + i + k];
         }
         a1 += t1;
         a2 += t2;
@@ -325,12 +359,13 @@ static void q4k_chunk_dots(const uint8_t *q, const float *x, float *qd1, float *
     if (vs2) *vs2 = v2;
 }
 
-/* dotRowQ4K: single row, inline vector sums (RT/GgufQ4RawDot.java:37-146). */
-static float dot_q4_k_inline(const uint8_t *row, int64_t cols, const float *x) {
+/* dotRowQ4K / dotRowQ5K: single row, inline vector sums
+ * (RT/GgufQ4RawDot.java:37-146, RT/GgufQ5RawDot.java:37-172). */
+static float dot_k_inline(const kfmt *f, const uint8_t *row, int64_t cols, const float *x) {
     float sum = 0.0f;
     int64_t blocks = cols / QK_K;
     for (int64_t b = 0; b < blocks; b++) {
-        const uint8_t *blk = row + b * 144;
+        const uint8_t *blk = row + b * f->bytes;
         const float *v = x + b * QK_K;
         float d = go_f16_to_f32(rd16(blk));
         float dmin = go_f16_to_f32(rd16(blk + 2));
@@ -342,9 +377,9 @@ static float dot_q4_k_inline(const uint8_t *row, int64_t cols, const float *x) {
             float d1 = d * (float)sc1;
             float d2 = d * (float)sc2;
             int min1 = has_block_mins ? mc1 : 0;
-            int min2 = has_block_mins ? mc2 : 0;
+            int min2 = has_block_mins ? (GO_PLANT == 5 ? mc1 : mc2) : 0;
             float qd1, qd2, vs1, vs2;
-            q4k_chunk_dots(blk + 16 + 32 * c, v + 64 * c, &qd1, &qd2, &vs1, &vs2);
+            k_chunk_dots(blk, f, c, v + 64 * c, &qd1, &qd2, &vs1, &vs2);
             sum += d1 * qd1 + d2 * qd2;
             if (min1 != 0) sum -= dmin * (float)min1 * vs1;
             if (min2 != 0) sum -= dmin * (float)min2 * vs2;
@@ -353,8 +388,9 @@ static float dot_q4_k_inline(const uint8_t *row, int64_t cols, const float *x) {
     return sum;
 }
 
-/* dotRowQ4KNoMinBlock (RT/GgufQ4RawDot.java:255-329) */
-static float q4k_nomin_block(const uint8_t *blk, const float *v) {
+/* dotRowQ4KNoMinBlock (RT/GgufQ4RawDot.java:255-329) /
+ * dotRowQ5KNoMinBlock (RT/GgufQ5RawDot.java:276-391) */
+static float k_nomin_block(const kfmt *f, const uint8_t *blk, const float *v) {
     float d = go_f16_to_f32(rd16(blk));
     float part[4];
     for (int c = 0; c < 4; c++) {
@@ -364,14 +400,16 @@ static float q4k_nomin_block(const uint8_t *blk, const float *v) {
         float d1 = d * (float)sc1;
         float d2 = d * (float)sc2;
         float qd1, qd2;
-        q4k_chunk_dots(blk + 16 + 32 * c, v + 64 * c, &qd1, &qd2, NULL, NULL);
+        k_chunk_dots(blk, f, c, v + 64 * c, &qd1, &qd2, NULL, NULL);
         part[c] = d1 * qd1 + d2 * qd2;
     }
     return part[0] + part[1] + part[2] + part[3];
 }
 
-/* dotRowQ4KGroupSumBlock / ...SuperBlock (RT/GgufQ4RawDot.java:531-674) */
-static float q4k_groupsum_block(const uint8_t *blk, const float *v, const float *gs) {
+/* dotRowQ4KGroupSumBlock / ...SuperBlock (RT/GgufQ4RawDot.java:531-674),
+ * dotRowQ5KGroupSumBlock / ...SuperBlock (RT/GgufQ5RawDot.java:604-795) */
+static float k_groupsum_block(const kfmt *f, const uint8_t *blk, const float *v,
+                              const float *gs) {
     float d = go_f16_to_f32(rd16(blk));
     float dmin = go_f16_to_f32(rd16(blk + 2));
     int has_block_mins = !(dmin == 0.0f);
@@ -386,10 +424,10 @@ static float q4k_groupsum_block(const uint8_t *blk, const float *v, const float 
         float m1 = 0.0f, m2 = 0.0f;
         if (has_pair_mins) {
             m1 = min_contribution(dmin, mc1);
-            m2 = min_contribution(dmin, mc2);
+            m2 = min_contribution(dmin, GO_PLANT == 5 ? mc1 : mc2);
         }
         float qd1, qd2;
-        q4k_chunk_dots(blk + 16 + 32 * c, v + 64 * c, &qd1, &qd2, NULL, NULL);
+        k_chunk_dots(blk, f, c, v + 64 * c, &qd1, &qd2, NULL, NULL);
         float contribution = d1 * qd1 + d2 * qd2;
         if (has_pair_mins) contribution -= m1 * gs[2 * c] + m2 * gs[2 * c + 1];
         part[c] = contribution;
@@ -398,30 +436,33 @@ static float q4k_groupsum_block(const uint8_t *blk, const float *v, const float 
 }
 
 /* Four-way block unrolled row sums shared by dotRowQ4KNoMins
- * (RT/GgufQ4RawDot.java:148-175) and dotRowQ4KWithGroupSums (:331-382). */
-static float dot_q4_k_unrolled(const uint8_t *row, int64_t cols, const float *x,
-                               const float *gs) {
+ * (RT/GgufQ4RawDot.java:148-175), dotRowQ4KWithGroupSums (:331-382),
+ * dotRowQ5KNoMins (RT/GgufQ5RawDot.java:167-196) and
+ * dotRowQ5KWithGroupSums (:393-451). */
+static float dot_k_unrolled(const kfmt *f, const uint8_t *row, int64_t cols, const float *x,
+                            const float *gs) {
     float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int64_t blocks = cols / QK_K, b = 0;
     for (; b + 4 <= blocks; b += 4) {
         for (int u = 0; u < 4; u++) {
-            const uint8_t *blk = row + (b + u) * 144;
+            const uint8_t *blk = row + (b + u) * f->bytes;
             const float *v = x + (b + u) * QK_K;
-            s[u] += gs ? q4k_groupsum_block(blk, v, gs + (b + u) * 8) : q4k_nomin_block(blk, v);
+            s[u] += gs ? k_groupsum_block(f, blk, v, gs + (b + u) * 8) : k_nomin_block(f, blk, v);
         }
     }
     float sum = s[0] + s[1] + s[2] + s[3];
     for (; b < blocks; b++) {
-        const uint8_t *blk = row + b * 144;
+        const uint8_t *blk = row + b * f->bytes;
         const float *v = x + b * QK_K;
-        sum += gs ? q4k_groupsum_block(blk, v, gs + b * 8) : q4k_nomin_block(blk, v);
+        sum += gs ? k_groupsum_block(f, blk, v, gs + b * 8) : k_nomin_block(f, blk, v);
     }
     return sum;
 }
 
-/* RT/GgufKMeta.java:171-181 (K4_LOW_MIN_MASK / K4_HIGH_MIN_MASK cover every
- * bit that contributes to a 6-bit min code). */
-static int q4k_block_has_mins(const uint8_t *blk) {
+/* RT/GgufKMeta.java:115-181 (K4_LOW_MIN_MASK / K4_HIGH_MIN_MASK cover every
+ * bit that contributes to a 6-bit min code; Q4_K and Q5_K keep dmin and the
+ * scale bytes at the same offsets). */
+static int k_block_has_mins(const uint8_t *blk) {
     float dmin = go_f16_to_f32(rd16(blk + 2));
     if (dmin == 0.0f) return 0;
     for (int j = 0; j < 8; j++) {
@@ -432,24 +473,107 @@ static int q4k_block_has_mins(const uint8_t *blk) {
     return 0;
 }
 
-static int q4k_row_has_mins(const uint8_t *row, int64_t cols) {
+static int k_row_has_mins(const kfmt *f, const uint8_t *row, int64_t cols) {
     for (int64_t b = 0; b < cols / QK_K; b++)
-        if (q4k_block_has_mins(row + b * 144)) return 1;
+        if (k_block_has_mins(row + b * f->bytes)) return 1;
     return 0;
+}
+
+static int k_rows_have_mins(const kfmt *f, const uint8_t *data, int64_t row_bytes, int64_t cols,
+                            int64_t row_count) {
+    for (int64_t r = 0; r < row_count; r++)
+        if (k_row_has_mins(f, data + r * row_bytes, cols)) return 1;
+    return 0;
+}
+
+int go_k_rows_have_mins(int type_id, const uint8_t *data, int64_t row_bytes, int64_t cols,
+                        int64_t row_count) {
+    if (type_id != GO_Q4_K && type_id != GO_Q5_K) return GO_ERR_UNSUPPORTED;
+    return k_rows_have_mins(type_id == GO_Q5_K ? &KF_Q5 : &KF_Q4, data, row_bytes, cols, row_count);
 }
 
 int go_q4k_rows_have_mins(const uint8_t *data, int64_t row_bytes, int64_t cols,
                           int64_t row_count) {
-    for (int64_t r = 0; r < row_count; r++)
-        if (q4k_row_has_mins(data + r * row_bytes, cols)) return 1;
-    return 0;
+    return k_rows_have_mins(&KF_Q4, data, row_bytes, cols, row_count);
 }
 
-/* RT/GgufSum.java:30-47: per-32 sums of x, restated sequentially. */
+/* ---- Q6_K raw dots (RT/GgufQ6RawDot.java) -------------------------------- */
+
+/* dotRowQ6KHalf (RT/GgufQ6RawDot.java:402-512) and
+ * dotRowQ6KHalfWithGroupSums (:514-629).  lo = ql of this 128-element half,
+ * hi = its qh, v = its x, off in {0, 16} picks the 16-element groups
+ * off..off+16 of each 32-element quarter.  Without group sums each code
+ * enters as (q - 32); with them the codes enter raw and each quarter
+ * subtracts 32 x its 16-element x sum, gs[0], gs[2], gs[4], gs[6]. */
+static float q6k_half(const uint8_t *lo, const uint8_t *hi, const float *v, int off,
+                      float s1, float s2, float s3, float s4, const float *gs) {
+    const int bias = gs || GO_PLANT == 2 ? 0 : 32;
+    float qd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = off; i < off + 16; i += 8) {
+        float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < 8; k++) {
+            const int a = lo[i + k], b = lo[32 + i + k], h = hi[i + k];
+            const int code[4] = {(a & 0x0F) | ((h & 0x03) << 4),
+                                 (b & 0x0F) | (((h >> 2) & 0x03) << 4),
+                                 (a >> 4) | (((h >> 4) & 0x03) << 4),
+                                 (b >> 4) | (((h >> 6) & 0x03) << 4)};
+            for (int j = 0; j < 4; j++) {
+                float p = (float)(code[j] - bias) * v[32 * j + i + k];
+                t[j] = k ? t[j] + p : p;
+            }
+        }
+        for (int j = 0; j < 4; j++) qd[j] += t[j];
+    }
+    if (!gs) return s1 * qd[0] + s2 * qd[1] + s3 * qd[2] + s4 * qd[3];
+    return s1 * (qd[0] - 32.0f * gs[0]) + s2 * (qd[1] - 32.0f * gs[GO_PLANT == 4 ? 1 : 2]) +
+           s3 * (qd[2] - 32.0f * gs[4]) + s4 * (qd[3] - 32.0f * gs[6]);
+}
+
+/* dotRowQ6KBlock (RT/GgufQ6RawDot.java:76-132) and dotRowQ6KGroupSumBlock
+ * (:334-400): d at byte 208, int8 scales at 192..207; gs (16-element x
+ * sums of this block, or NULL) as q6k_half takes them. */
+static float q6k_block(const uint8_t *blk, const float *v, const float *gs) {
+    const float d = go_f16_to_f32(rd16(blk + 208));
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    float part[4];
+    for (int p = 0; p < 4; p++) {
+        const int h = p >> 1, off = 16 * (p & 1);
+        const int8_t *s = sc + (GO_PLANT == 3 ? 0 : 8 * h) + (p & 1);
+        part[p] = q6k_half(blk + 64 * h, blk + 128 + 32 * h, v + 128 * h, off,
+                           d * (float)s[0], d * (float)s[2], d * (float)s[4], d * (float)s[6],
+                           gs ? gs + 8 * h + (p & 1) : NULL);
+    }
+    return part[0] + part[1] + part[2] + part[3];
+}
+
+/* dotRowQ6K (RT/GgufQ6RawDot.java:32-74) and dotRowQ6KWithGroupSums
+ * (:134-185): four block accumulators, then the tail blocks. */
+static float dot_q6_k(const uint8_t *row, int64_t cols, const float *x, const float *gs) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t blocks = cols / QK_K, b = 0;
+    for (; b + 4 <= blocks; b += 4)
+        for (int u = 0; u < 4; u++)
+            s[u] += q6k_block(row + (b + u) * 210, x + (b + u) * QK_K, gs ? gs + (b + u) * 16 : NULL);
+    float sum = s[0] + s[1] + s[2] + s[3];
+    for (; b < blocks; b++)
+        sum += q6k_block(row + b * 210, x + b * QK_K, gs ? gs + b * 16 : NULL);
+    return sum;
+}
+
+/* RT/GgufSum.java:30-47, :49-66: per-32 and per-16 sums of x, restated
+ * sequentially. */
 void go_group_sums32(const float *x, int64_t cols, float *sums) {
     for (int64_t g = 0; g < cols / 32; g++) {
         float s = 0.0f;
         for (int i = 0; i < 32; i++) s += x[32 * g + i];
+        sums[g] = s;
+    }
+}
+
+void go_group_sums16(const float *x, int64_t cols, float *sums) {
+    for (int64_t g = 0; g < cols / 16; g++) {
+        float s = 0.0f;
+        for (int i = 0; i < 16; i++) s += x[16 * g + i];
         sums[g] = s;
     }
 }
@@ -459,20 +583,29 @@ void go_group_sums32(const float *x, int64_t cols, float *sums) {
 int go_dot_row(int type_id, const uint8_t *row, int64_t cols, const float *x,
                float *out) {
     int bs = go_block_size(type_id);
-    if (bs == 0 || type_id == GO_Q5_K || type_id == GO_Q6_K) return GO_ERR_UNSUPPORTED;
+    if (bs == 0) return GO_ERR_UNSUPPORTED;
     if (cols % bs != 0) return GO_ERR_ARG;
-    if (type_id == GO_Q8_0) *out = dot_q8_0(row, cols, x);
-    else if (type_id == GO_Q4_0) *out = dot_q4_0(row, cols, x);
-    else if (q4k_row_has_mins(row, cols)) *out = dot_q4_k_inline(row, cols, x);
-    else *out = dot_q4_k_unrolled(row, cols, x, NULL);
+    if (type_id == GO_Q8_0) {
+        *out = dot_q8_0(row, cols, x);
+    } else if (type_id == GO_Q4_0) {
+        *out = dot_q4_0(row, cols, x);
+    } else if (type_id == GO_Q6_K) {
+        *out = dot_q6_k(row, cols, x, NULL); /* RT/GgufRawDot.java:146-148 */
+    } else {
+        /* RT/GgufRawDot.java:78-91 (Q4_K), :120-133 (Q5_K): the row's own
+         * min scan picks the inline or the no-min dot. */
+        const kfmt *f = type_id == GO_Q5_K ? &KF_Q5 : &KF_Q4;
+        *out = k_row_has_mins(f, row, cols) ? dot_k_inline(f, row, cols, x)
+                                            : dot_k_unrolled(f, row, cols, x, NULL);
+    }
     return GO_OK;
 }
 
 /* ---- multi-row mat-vec: RT/GgufRawRoute.java:56-105 and the walkers in
  * RT/GgufQ8RawRows.java:18-41, RT/GgufQ32RawRows.java:18-37,
- * RT/GgufKRawRows.java:122-201, scheduled like RT/GgufParallelConfig.java. */
+ * RT/GgufKRawRows.java:122-320, scheduled like RT/GgufParallelConfig.java. */
 
-enum { Q4K_NOMIN = 0, Q4K_DIRECT = 1, Q4K_GROUPSUM = 2 };
+enum { K_NOMIN = 0, K_DIRECT = 1, K_GROUPSUM = 2 };
 
 typedef struct {
     int type_id;
@@ -480,7 +613,7 @@ typedef struct {
     int64_t cols, row_bytes;
     const float *x;
     const float *group_sums;
-    int q4k_mode;
+    int k_mode;
     float *y;
     int64_t row_begin, row_end;
 } go_task;
@@ -491,9 +624,14 @@ static void run_rows(const go_task *t) {
         float v;
         if (t->type_id == GO_Q8_0) v = dot_q8_0(row, t->cols, t->x);
         else if (t->type_id == GO_Q4_0) v = dot_q4_0(row, t->cols, t->x);
-        else if (t->q4k_mode == Q4K_DIRECT) v = dot_q4_k_inline(row, t->cols, t->x);
-        else v = dot_q4_k_unrolled(row, t->cols, t->x,
-                                   t->q4k_mode == Q4K_GROUPSUM ? t->group_sums : NULL);
+        else if (t->type_id == GO_Q6_K)
+            v = dot_q6_k(row, t->cols, t->x, t->k_mode == K_GROUPSUM ? t->group_sums : NULL);
+        else {
+            const kfmt *f = t->type_id == GO_Q5_K ? &KF_Q5 : &KF_Q4;
+            if (t->k_mode == K_DIRECT) v = dot_k_inline(f, row, t->cols, t->x);
+            else v = dot_k_unrolled(f, row, t->cols, t->x,
+                                    t->k_mode == K_GROUPSUM ? t->group_sums : NULL);
+        }
         t->y[r] = v;
     }
 }
@@ -522,7 +660,7 @@ int go_matvec_rows(int type_id, const uint8_t *data, int64_t rows, int64_t cols,
                    int64_t row_bytes, const float *x, float *y,
                    int64_t row_count, int threads) {
     int bs = go_block_size(type_id);
-    if (bs == 0 || type_id == GO_Q5_K || type_id == GO_Q6_K) return GO_ERR_UNSUPPORTED;
+    if (bs == 0) return GO_ERR_UNSUPPORTED;
     if (cols % bs != 0) return GO_ERR_ARG;
     if (row_count < 0 || row_count > rows) return GO_ERR_ARG;
     if (row_count == 0) return GO_OK;
@@ -537,18 +675,31 @@ int go_matvec_rows(int type_id, const uint8_t *data, int64_t rows, int64_t cols,
     base.x = x;
     base.y = y;
     float *sums = NULL;
-    if (type_id == GO_Q4_K) {
-        /* RT/GgufRawMatVec.java:47-79: tensor-level min scan, then the no-min,
-         * direct (2..4 rows) or group-sum walker. */
-        if (!go_q4k_rows_have_mins(data, row_bytes, cols, row_count)) {
-            base.q4k_mode = Q4K_NOMIN;
+    if (type_id == GO_Q4_K || type_id == GO_Q5_K) {
+        /* RT/GgufRawMatVec.java:47-79 (Q4_K), :195-267 (Q5_K): tensor-level
+         * min scan, then the no-min, direct (2..4 rows) or group-sum walker. */
+        const kfmt *f = type_id == GO_Q5_K ? &KF_Q5 : &KF_Q4;
+        if (!k_rows_have_mins(f, data, row_bytes, cols, row_count)) {
+            base.k_mode = K_NOMIN;
         } else if (row_count <= 4) {
-            base.q4k_mode = Q4K_DIRECT;
+            base.k_mode = K_DIRECT;
         } else {
-            base.q4k_mode = Q4K_GROUPSUM;
+            base.k_mode = K_GROUPSUM;
             sums = (float *)malloc(sizeof(float) * (size_t)(cols / 32));
             if (!sums) return GO_ERR_ARG;
             go_group_sums32(x, cols, sums);
+            base.group_sums = sums;
+        }
+    } else if (type_id == GO_Q6_K) {
+        /* RT/GgufRawMatVec.java:270-296: direct rows for 2..4, else the
+         * per-16 x sums and the group-sum walker. */
+        if (row_count <= 4) {
+            base.k_mode = K_DIRECT;
+        } else {
+            base.k_mode = K_GROUPSUM;
+            sums = (float *)malloc(sizeof(float) * (size_t)(cols / 16));
+            if (!sums) return GO_ERR_ARG;
+            go_group_sums16(x, cols, sums);
             base.group_sums = sums;
         }
     }

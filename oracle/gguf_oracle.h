@@ -24,8 +24,16 @@
  *   go_dequantize_row    Q5_K / Q6_K: the reference's lane-order fixtures
  *   (Q5_K, Q6_K)         (TST/GgufQ5LaneFx, GgufQ5CalcFx, GgufQ6LaneFx,
  *                        GgufQ5KOffTest) and the numpy restatement of the
- *                        ggml block formulas (tests/npref.py).  go_dot_row
- *                        and go_matvec_rows do not take these types.
+ *                        ggml block formulas (tests/npref.py).
+ *   go_dot_row /         Q5_K / Q6_K: the same lane-order fixtures' dots at
+ *   go_matvec_rows       0.0; closed forms of constant blocks (every code and
+ *   (Q5_K, Q6_K)         x equal: the row sum is a product of exact
+ *                        integers, met by every walker); the no-min,
+ *                        inline, direct and group-sum walkers against each
+ *                        other and against an fp64 dot at 1e-4; and planted
+ *                        mistakes (a high bit from the wrong plane, a lost
+ *                        -32, a scale from the wrong half) that those checks
+ *                        catch (tests/test_oracle.py).
  *   go_moe_select_topk   closed forms (uniform logits: ids 0..k-1 by the
  *                        stable tie order, weights 1/k; distinct logits:
  *                        numpy's stable descending argsort and fp64
@@ -87,13 +95,18 @@ int go_matvec_rows(int type_id, const uint8_t *data, int64_t rows, int64_t cols,
 /* Number of host threads go_matvec_rows uses when threads <= 0. */
 int go_default_threads(void);
 
-/* Per-32 group sums of x (RT/GgufSum.java:30-47), sequential order. */
+/* Per-32 and per-16 group sums of x (RT/GgufSum.java:30-66), sequential
+ * order. */
 void go_group_sums32(const float *x, int64_t cols, float *sums);
+void go_group_sums16(const float *x, int64_t cols, float *sums);
 
 /* Whether any of the first row_count rows of a Q4_K matrix has an active min
  * (RT/GgufKMeta.java:115-181). */
 int go_q4k_rows_have_mins(const uint8_t *data, int64_t row_bytes, int64_t cols,
                           int64_t row_count);
+/* The same for Q4_K or Q5_K (type_id 12 or 13); GO_ERR_UNSUPPORTED else. */
+int go_k_rows_have_mins(int type_id, const uint8_t *data, int64_t row_bytes, int64_t cols,
+                        int64_t row_count);
 
 /* MoE router (runner/safetensor/gollek-safetensor-engine/src/main/java/tech/
  * kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:174-203,

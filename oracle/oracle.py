@@ -29,8 +29,8 @@ import numpy as np
 ORACLE_DIR = Path(__file__).resolve().parent
 LIB_PATH = ORACLE_DIR / "build" / "libgguf_oracle.so"
 
-Q4_0, Q8_0, Q4_K = 2, 8, 12
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 _lib = None
 
@@ -45,28 +45,46 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        L = ctypes.CDLL(str(LIB_PATH))
-        P, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
-        L.go_f16_to_f32.restype = F
-        L.go_f16_to_f32.argtypes = [ctypes.c_uint16]
-        L.go_f16_to_f32_n.argtypes = [P, I64, P]
-        L.go_k4_scale_min.argtypes = [P, I, P, P]
-        L.go_row_bytes.restype = I64
-        L.go_row_bytes.argtypes = [I, I64]
-        L.go_dequantize_rows.restype = I
-        L.go_dequantize_rows.argtypes = [I, P, I64, I64, I64, I64, P]
-        L.go_dot_row.restype = I
-        L.go_dot_row.argtypes = [I, P, I64, P, P]
-        L.go_matvec_rows.restype = I
-        L.go_matvec_rows.argtypes = [I, P, I64, I64, I64, P, P, I64, I]
-        L.go_default_threads.restype = I
-        L.go_group_sums32.argtypes = [P, I64, P]
-        L.go_moe_select_topk.restype = I
-        L.go_moe_select_topk.argtypes = [P, I64, I64, I64, I, P, P]
-        L.go_q4k_rows_have_mins.restype = I
-        L.go_q4k_rows_have_mins.argtypes = [P, I64, I64, I64]
-        _lib = L
+        _lib = load(LIB_PATH)
     return _lib
+
+
+def build_planted(n: int, out_dir) -> Path:
+    """Build a copy of the oracle with planted mistake n (gguf_oracle.c's
+    GO_PLANT list) into out_dir, for tests that show the checks catch it."""
+    out = Path(out_dir) / f"libgguf_oracle_plant{n}.so"
+    subprocess.run(["gcc", "-O1", "-ffp-contract=off", "-fno-fast-math", "-std=c11", "-fPIC", "-shared",
+                    f"-DGO_PLANT={int(n)}", str(ORACLE_DIR / "gguf_oracle.c"), "-o", str(out),
+                    "-lpthread", "-lm"], check=True)
+    return out
+
+
+def load(path) -> ctypes.CDLL:
+    """Load an oracle build (the default one, or a planted copy)."""
+    L = ctypes.CDLL(str(path))
+    P, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    L.go_f16_to_f32.restype = F
+    L.go_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.go_f16_to_f32_n.argtypes = [P, I64, P]
+    L.go_k4_scale_min.argtypes = [P, I, P, P]
+    L.go_row_bytes.restype = I64
+    L.go_row_bytes.argtypes = [I, I64]
+    L.go_dequantize_rows.restype = I
+    L.go_dequantize_rows.argtypes = [I, P, I64, I64, I64, I64, P]
+    L.go_dot_row.restype = I
+    L.go_dot_row.argtypes = [I, P, I64, P, P]
+    L.go_matvec_rows.restype = I
+    L.go_matvec_rows.argtypes = [I, P, I64, I64, I64, P, P, I64, I]
+    L.go_default_threads.restype = I
+    L.go_group_sums32.argtypes = [P, I64, P]
+    L.go_group_sums16.argtypes = [P, I64, P]
+    L.go_k_rows_have_mins.restype = I
+    L.go_k_rows_have_mins.argtypes = [I, P, I64, I64, I64]
+    L.go_moe_select_topk.restype = I
+    L.go_moe_select_topk.argtypes = [P, I64, I64, I64, I, P, P]
+    L.go_q4k_rows_have_mins.restype = I
+    L.go_q4k_rows_have_mins.argtypes = [P, I64, I64, I64]
+    return L
 
 
 def _u8(data) -> np.ndarray:
@@ -104,18 +122,18 @@ def dequantize(type_id: int, data, cols: int, row0: int = 0, nrows: int | None =
     return out
 
 
-def dot_row(type_id: int, row_data, cols: int, x) -> float:
+def dot_row(type_id: int, row_data, cols: int, x, _lib=None) -> float:
     d = _u8(row_data)
     xv = np.ascontiguousarray(x, dtype=np.float32)
     out = ctypes.c_float()
-    rc = lib().go_dot_row(type_id, d.ctypes.data, cols, xv.ctypes.data, ctypes.byref(out))
+    rc = (_lib or lib()).go_dot_row(type_id, d.ctypes.data, cols, xv.ctypes.data, ctypes.byref(out))
     if rc != 0:
         raise ValueError(f"oracle dot failed: {rc}")
     return out.value
 
 
 def matvec(type_id: int, data, cols: int, x, row_count: int | None = None,
-           threads: int = 0) -> np.ndarray:
+           threads: int = 0, _lib=None) -> np.ndarray:
     d = _u8(data)
     rb = row_bytes(type_id, cols)
     rows = d.size // rb
@@ -123,7 +141,7 @@ def matvec(type_id: int, data, cols: int, x, row_count: int | None = None,
         row_count = rows
     xv = np.ascontiguousarray(x, dtype=np.float32)
     y = np.zeros(max(row_count, 1), dtype=np.float32)
-    rc = lib().go_matvec_rows(type_id, d.ctypes.data, rows, cols, rb, xv.ctypes.data,
+    rc = (_lib or lib()).go_matvec_rows(type_id, d.ctypes.data, rows, cols, rb, xv.ctypes.data,
                               y.ctypes.data, row_count, threads)
     if rc != 0:
         raise ValueError(f"oracle matvec failed: {rc}")
@@ -141,9 +159,25 @@ def group_sums32(x) -> np.ndarray:
     return out
 
 
+def group_sums16(x) -> np.ndarray:
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(xv.size // 16, dtype=np.float32)
+    lib().go_group_sums16(xv.ctypes.data, xv.size, out.ctypes.data)
+    return out
+
+
 def q4k_rows_have_mins(data, cols: int, row_count: int) -> bool:
     d = _u8(data)
     return bool(lib().go_q4k_rows_have_mins(d.ctypes.data, row_bytes(Q4_K, cols), cols, row_count))
+
+
+def k_rows_have_mins(type_id: int, data, cols: int, row_count: int) -> bool:
+    """Q4_K / Q5_K: whether any of the first row_count rows has an active min."""
+    d = _u8(data)
+    rc = lib().go_k_rows_have_mins(type_id, d.ctypes.data, row_bytes(type_id, cols), cols, row_count)
+    if rc < 0:
+        raise ValueError(f"oracle min scan failed: {rc}")
+    return bool(rc)
 
 
 # ---- fp64 references -----------------------------------------------------

@@ -136,7 +136,8 @@ def test_gemv_parity(name, type_id, rows, cols):
 
 
 ACCURACY_CONFIGS = [("c0_q8_0", syn.Q8_0, 4096, 4096), ("c1_q4_0", syn.Q4_0, 11008, 4096),
-                    ("c2a_q4_k", syn.Q4_K, 14336, 4096), ("q4_k_k2048", syn.Q4_K, 4096, 2048)]
+                    ("c2a_q4_k", syn.Q4_K, 14336, 4096), ("q4_k_k2048", syn.Q4_K, 4096, 2048),
+                    ("q5_k_4096", syn.Q5_K, 4096, 4096), ("q6_k_14336x4096", syn.Q6_K, 14336, 4096)]
 
 
 @pytest.mark.parametrize("name,type_id,rows,cols", ACCURACY_CONFIGS, ids=[c[0] for c in ACCURACY_CONFIGS])
@@ -422,6 +423,8 @@ def test_q5_k_q6_k_dequant_and_gemv(type_id, rows, cols):
     ops.mat_vec(t, x, y)
     ref = o.matvec_fp64(type_id, data, cols, x)
     assert o.rel_err(y, ref) <= GEMV_TOL, o.rel_err(y, ref)
+    java = o.matvec(type_id, data, cols, x)
+    assert o.rel_err(y, java) <= GEMV_TOL, o.rel_err(y, java)
     part = np.full(rows, -3.0, np.float32)
     ops.mat_vec_rows(t, x, part, rows // 2, True)
     assert np.array_equal(part[:rows // 2], y[:rows // 2])
@@ -429,3 +432,62 @@ def test_q5_k_q6_k_dequant_and_gemv(type_id, rows, cols):
     r = rows - 1
     assert ops.dot_row(t, r, x) == pytest.approx(float(y[r]), rel=1e-6, abs=1e-6)
     t.close()
+
+
+def test_q6_k_lm_head_full_size_sampled_rows():
+    # Q6_K K=4096 x N=128256 (the lm_head type of Q4_K_M files): full-size
+    # GPU run; the oracle's Java-order rows and the fp64 dot on every 61st
+    # row, plus linearity in x over all rows.
+    rows, cols = 128256, 4096
+    print("[gpu] q6_k gemv lm_head 128256x4096", flush=True)
+    data = syn.q6_k_matrix(rows, cols, seed=2025)
+    t = _tensor(syn.Q6_K, data, cols, "output.weight")
+    x1, x2 = syn.activation(cols, 3), syn.activation(cols, 4)
+    y1, y2, y12 = (np.zeros(rows, np.float32) for _ in range(3))
+    ops.mat_vec(t, x1, y1)
+    ops.mat_vec(t, x2, y2)
+    ops.mat_vec(t, (x1 + x2).astype(np.float32), y12)
+    sel = np.arange(0, rows, 61)
+    assert o.rel_err(y1[sel], o.matvec_fp64(syn.Q6_K, data[sel], cols, x1)) <= GEMV_TOL
+    assert o.rel_err(y1[sel], o.matvec(syn.Q6_K, data[sel], cols, x1)) <= GEMV_TOL
+    assert o.normwise_err(y12, y1.astype(np.float64) + y2) <= 1e-5
+    t.close()
+
+
+UNALIGNED = [(t, off) for t in (syn.Q8_0, syn.Q4_0, syn.Q4_K, syn.Q5_K, syn.Q6_K) for off in (1, 2)]
+
+
+@pytest.mark.parametrize("type_id,w_off", UNALIGNED, ids=[f"type{t}_w+{o_}" for t, o_ in UNALIGNED])
+def test_unaligned_device_buffers(type_id, w_off):
+    # Borrowed device buffers at any byte offset: weights 1 or 2 bytes past
+    # an aligned address and x 4 bytes past a 16-byte boundary go to the
+    # generic kernel (byte loads of the weights, scalar loads of x), which
+    # meets the same bar as the fast kernels; an aligned x with the same
+    # misaligned weights as well.
+    import torch
+    rows, cols = 300, 2304
+    print(f"[gpu] unaligned type={type_id} w+{w_off}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=40 + type_id + w_off)
+    x = syn.activation(cols, seed=41)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    java = o.matvec(type_id, data, cols, x)
+    flat = torch.from_numpy(np.ascontiguousarray(data).reshape(-1))
+    wbuf = torch.zeros(flat.numel() + 64, dtype=torch.uint8, device="cuda")
+    wbuf[w_off:w_off + flat.numel()].copy_(flat.cuda())
+    xbuf = torch.zeros(cols + 8, dtype=torch.float32, device="cuda")
+    y_dev = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    dw = ops.DeviceWeight(type_id, wbuf.data_ptr() + w_off, rows, cols)
+    for x_off in (1, 0):
+        xbuf[x_off:x_off + cols].copy_(torch.from_numpy(x).cuda())
+        y_dev.fill_(-5.0)
+        dw.matvec(xbuf.data_ptr() + 4 * x_off, y_dev.data_ptr(), rows, stream)
+        torch.cuda.synchronize()
+        y = y_dev.cpu().numpy()
+        assert o.rel_err(y, ref) <= GEMV_TOL, (x_off, o.rel_err(y, ref))
+        assert o.rel_err(y, java) <= GEMV_TOL, (x_off, o.rel_err(y, java))
+    deq = torch.empty((3, cols), dtype=torch.float32, device="cuda")
+    dw.dequantize(7, 3, deq.data_ptr(), stream)
+    torch.cuda.synchronize()
+    assert_same_bits(deq.cpu().numpy(), o.dequantize(type_id, data, cols, 7, 3))
+    dw.close()

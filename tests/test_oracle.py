@@ -6,7 +6,10 @@
   * 6-bit scale/min unpack against the generator's inverse packer;
   * dequantization bit-exact against an independent numpy restatement;
   * mat-vec against an fp64 dot over the dequantized rows;
-  * planted mistakes in a copy of the restatement are caught by the fixtures.
+  * planted mistakes in a copy of the restatement are caught by the fixtures;
+  * Q5_K / Q6_K dots: exact-arithmetic cases (every walker must return the
+    fp64 dot of the independently dequantized rows bit for bit) and planted
+    mistakes built into copies of the C oracle (GO_PLANT) that they catch.
 """
 import math
 
@@ -39,10 +42,7 @@ def test_golden_matvec(golden):
     for fx in golden:
         if fx["expected_matvec"] is None:
             continue
-        if fx["type_id"] in (syn.Q5_K, syn.Q6_K):  # no Java-order dot in the oracle: fp64 dot
-            y = o.matvec_fp64(fx["type_id"], _data(fx), fx["cols"], _vec(fx))[:fx["row_count"]]
-        else:
-            y = o.matvec(fx["type_id"], _data(fx), fx["cols"], _vec(fx), fx["row_count"])
+        y = o.matvec(fx["type_id"], _data(fx), fx["cols"], _vec(fx), fx["row_count"])
         exp = np.asarray(fx["expected_matvec"], dtype=np.float64)
         # JUnit assertEquals(expected, actual, delta): absolute difference.
         assert np.all(np.abs(y - exp) <= fx["tolerance"]), (fx["name"], y, exp)
@@ -51,7 +51,7 @@ def test_golden_matvec(golden):
 def test_golden_single_row_dot_matches_matvec(golden):
     # TST/GgufFx.java:26-35: single-row matVecRows equals dotRow exactly.
     for fx in golden:
-        if fx["vector"] is None or fx["type_id"] in (syn.Q5_K, syn.Q6_K):
+        if fx["vector"] is None:
             continue
         data, cols = _data(fx), fx["cols"]
         rb = o.row_bytes(fx["type_id"], cols)
@@ -363,3 +363,113 @@ def test_router_pads_past_the_expert_count_and_keeps_zero_sums():
     assert w[0, 0] > w[0, 1] > w[0, 2] > 0
     ids, w = o.moe_select_topk(np.full((1, 4), -np.inf, np.float32), 2, True)
     assert ids.tolist() == [[0, 1]] and w.tolist() == [[0.0, 0.0]]
+
+
+# ---- Q5_K / Q6_K dots ------------------------------------------------------
+#
+# Blocks whose scales are powers of two times small integers and x values
+# that are multiples of 1/4 in [-1, 1] make every product and every partial
+# sum of the Java loops exactly representable in fp32 (below 2^24 units of
+# the smallest step), so each walker -- the single-row dot, the no-min
+# unrolled dot, the inline-min direct rows (2..4) and the group-sum rows --
+# must equal the fp64 dot over tests/npref.py's dequantized rows exactly,
+# whatever its summation order.  That pins which code, which high-bit plane,
+# which scale, min and x sum each element pairs with.
+
+def _exact_q5_k(rows, cols, seed, mins=True):
+    g = np.random.default_rng(seed)
+    ns = cols // 256
+    out = np.zeros((rows, ns, 176), np.uint8)
+    out[..., 0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    out[..., 2:4] = np.frombuffer(np.float16(0.125 if mins else 0.0).tobytes(), np.uint8)
+    out[..., 4:16] = syn.pack_q4k_scales(g.integers(0, 8, (rows, ns, 8)), g.integers(0, 8, (rows, ns, 8)))
+    out[..., 16:] = g.integers(0, 256, (rows, ns, 160), dtype=np.uint8)
+    return out.reshape(rows, ns * 176)
+
+
+def _exact_q6_k(rows, cols, seed):
+    g = np.random.default_rng(seed)
+    ns = cols // 256
+    out = np.zeros((rows, ns, 210), np.uint8)
+    out[..., :192] = g.integers(0, 256, (rows, ns, 192), dtype=np.uint8)
+    out[..., 192:208] = g.integers(-8, 8, (rows, ns, 16)).astype(np.int8).view(np.uint8)
+    out[..., 208:210] = np.frombuffer(np.float16(0.125).tobytes(), np.uint8)
+    return out.reshape(rows, ns * 210)
+
+
+def _exact_x(cols, seed):
+    return (np.random.default_rng(seed).integers(-4, 5, cols) / 4.0).astype(np.float32)
+
+
+EXACT_CASES = [("q5_k_mins", syn.Q5_K, True), ("q5_k_nomins", syn.Q5_K, False), ("q6_k", syn.Q6_K, None)]
+
+
+def _exact_case(type_id, mins, rows, cols, seed):
+    data = _exact_q5_k(rows, cols, seed, mins) if type_id == syn.Q5_K else _exact_q6_k(rows, cols, seed)
+    return data, _exact_x(cols, seed + 1)
+
+
+def _exact_mismatches(type_id, data, cols, x, lib=None):
+    """Rows (over every walker) where the oracle differs from the exact dot."""
+    exact = npref.dequant(type_id, data, cols).astype(np.float64) @ x.astype(np.float64)
+    rows = exact.size
+    bad = []
+    rb = o.row_bytes(type_id, cols)
+    flat = np.ascontiguousarray(data).reshape(-1)
+    for r in range(rows):  # single-row dots
+        if o.dot_row(type_id, flat[r * rb:(r + 1) * rb], cols, x, _lib=lib) != exact[r]:
+            bad.append(("dot", r))
+    for n in (2, 4, rows):  # direct rows, group-sum / no-min rows
+        y = o.matvec(type_id, data, cols, x, row_count=n, threads=1, _lib=lib)
+        bad += [("rows%d" % n, r) for r in np.nonzero(y != exact[:n])[0]]
+    return bad
+
+
+@pytest.mark.parametrize("name,type_id,mins", EXACT_CASES, ids=[c[0] for c in EXACT_CASES])
+@pytest.mark.parametrize("cols", [256, 1280, 2048])
+def test_k56_dots_exact_cases(name, type_id, mins, cols):
+    data, x = _exact_case(type_id, mins, 9, cols, cols + type_id)
+    if type_id == syn.Q5_K:
+        assert o.k_rows_have_mins(type_id, data, cols, 9) == mins
+    assert _exact_mismatches(type_id, data, cols, x) == []
+
+
+@pytest.mark.parametrize("type_id", [syn.Q5_K, syn.Q6_K])
+@pytest.mark.parametrize("cols", [256, 768, 4096])
+def test_k56_walkers_agree_with_fp64(type_id, cols):
+    # Random fp16 scales and Gaussian x: every walker within rounding of the
+    # fp64 dot over the bit-exact dequantized rows, and threads do not change
+    # the bits.  1e-4: the Q6_K group-sum rows subtract 32 x the x sums from
+    # raw-code dots, which cancels about two decimal digits on these rows.
+    rows = 23
+    data = syn.matrix(type_id, rows, cols, seed=cols + 3 * type_id)
+    x = syn.activation(cols, seed=cols + 1)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    y = o.matvec(type_id, data, cols, x, threads=1)
+    assert o.rel_err(y, ref) <= 1e-4
+    assert np.array_equal(y, o.matvec(type_id, data, cols, x, threads=5))
+    for n in (1, 2, 4):
+        assert o.rel_err(o.matvec(type_id, data, cols, x, row_count=n), ref[:n]) <= 1e-4
+
+
+def test_group_sums16_exact():
+    x = _exact_x(512, 3)
+    assert np.array_equal(o.group_sums16(x), x.reshape(-1, 16).astype(np.float64).sum(1))
+
+
+PLANTS = {1: EXACT_CASES[0], 2: EXACT_CASES[2], 3: EXACT_CASES[2], 4: EXACT_CASES[2], 5: EXACT_CASES[0]}
+
+
+@pytest.mark.parametrize("plant", sorted(PLANTS))
+def test_k56_exact_cases_catch_planted_mistakes(plant, tmp_path):
+    # A copy of the oracle with one planted mistake (gguf_oracle.c GO_PLANT)
+    # fails the exact-arithmetic check on the walkers the mistake touches.
+    lib = o.load(o.build_planted(plant, tmp_path))
+    _, type_id, mins = PLANTS[plant]
+    data, x = _exact_case(type_id, mins, 9, 1280, 77)
+    assert _exact_mismatches(type_id, data, cols=1280, x=x) == []
+    bad = _exact_mismatches(type_id, data, 1280, x, lib=lib)
+    assert bad, plant
+    walkers = {w for w, _ in bad}
+    if plant == 4:  # only the group-sum rows subtract the per-16 x sums
+        assert walkers == {"rows9"}, walkers
