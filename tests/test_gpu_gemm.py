@@ -83,12 +83,12 @@ def test_gemm_large_m_kernel_shapes(rows, cols, m, variant):
     t.close()
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 3])
+@pytest.mark.parametrize("cfg", [0, 5, 1, 3])
 @pytest.mark.parametrize("rows,cols,m", [(192, 4096, 300), (4096, 192, 257), (64, 64, 130)])
 def test_gemm_large_m_configs(rows, cols, m, cfg):
-    # The large-M kernels: the buffer->LDS ring (cfg 0; K from one block
-    # pair, fewer stages than ring slots, up to 64 stages) and two
-    # register-pipelined configurations.
+    # The large-M kernels: the buffer->LDS ring fed by loader waves (cfg 0)
+    # or by every wave (cfg 5), K from one block pair, fewer stages than ring
+    # slots, up to 64 stages; and two register-pipelined configurations.
     print(f"[gpu] gemm large-m cfg={cfg} rows={rows} cols={cols} m={m}", flush=True)
     data = syn.q8_0_matrix(rows, cols, seed=rows + cols + cfg)
     t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
