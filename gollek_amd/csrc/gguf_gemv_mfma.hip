@@ -432,7 +432,11 @@ struct XOps4 {
 // Wave-wide: lane l holds elements 4 l .. 4 l + 3 of a superblock of x.
 // Writes the digit planes to `scratch` (1 KB of LDS private to the wave),
 // reads them back in the A operand layout and leaves the scratch free.
-__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o) {
+// With PS, ps[c][p] = the integer sum of plane p's digits over sub-block
+// 2 c + h (h = (lane >> 4) & 1), for codes stored with an offset.
+template <bool PS = false>
+__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o,
+                                            int (*ps)[4] = nullptr) {
     const int lane = threadIdx.x & 63;
     const float v[4] = {xv.x, xv.y, xv.z, xv.w};
     uint32_t mb = 0;
@@ -481,6 +485,18 @@ __device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, X
         o.xs4[c] = h ? b : a;
     }
     o.xs = finite ? ldexpf(1.0f, e - 30) : __builtin_nanf("");
+    if constexpr (PS) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int sp = sum8_i(__builtin_amdgcn_sdot4((int)w[p], 0x01010101, 0, false));
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int a = __builtin_amdgcn_readlane(sp, 16 * c);
+                const int b = __builtin_amdgcn_readlane(sp, 16 * c + 8);
+                ps[c][p] = h ? b : a;
+            }
+        }
+    }
     // A lane (m, g): plane p = m & 3 of elements 64 c + 8 g .. + 7 (sub-block
     // 2 c) for m < 4, of elements 64 c + 32 + 8 g .. + 7 (2 c + 1) for
     // 4 <= m < 8; rows 8..15 are zero.
@@ -560,6 +576,100 @@ __device__ __forceinline__ float q4k_tile_superblock4(const u32x4 hv, const uint
         mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, o.xs4[c], mm);
     }
     return qs - mm;
+}
+
+// Q4_0 / Q8_0 on the K <= 4096 kernels: a 256-element piece of a row is
+// eight blocks of 32 (block j at BB j: fp16 d, then 16 bytes of nibbles --
+// byte i holds element i low and element 16 + i high -- or 32 int8), and
+// sub-block j of the Q4_K layout is block j.  B lane n + 16 g of chunk c
+// holds the codes of elements 8 g .. 8 g + 7 of blocks 2 c and 2 c + 1
+// (Q4_0: the low nibbles of quant bytes 8 (g & 1) .. + 7 for g < 2, their
+// high nibbles for g >= 2; Q8_0: quant bytes 8 g .. 8 g + 7), which pair
+// with the A rows of x_operands4.  The quant bytes of the even block start
+// 2 bytes past a dword, so a lane reads the three dwords covering them and
+// realigns; those of the odd block are dword aligned.
+//
+// Reads one tile's piece of row n (a_q = the row's piece + 8 (g & 1) for
+// Q4_0, + 8 g for Q8_0; a_d = the row's piece + BB h): raw[5 c .. 5 c + 2]
+// = dwords 2 c BB + {0, 4, 8}, raw[5 c + 3, 5 c + 4] = dwords (2 c + 1) BB +
+// 2 + {0, 4} past a_q; dh[c] = the fp16 d of block 2 c + h.
+template <int BB>
+__device__ __forceinline__ void read_tile_piece32(uint32_t a_q, uint32_t a_d, uint32_t (&raw)[20],
+                                                  uint32_t (&dh)[4]) {
+#define GOLLEK_OFFS(c) (2 * (c) * BB) / 4, (2 * (c) * BB) / 4 + 1, (2 * (c) * BB) / 4 + 2, \
+                       ((2 * (c) + 1) * BB + 2) / 4, ((2 * (c) + 1) * BB + 2) / 4 + 1
+    constexpr int o[20] = {GOLLEK_OFFS(0), GOLLEK_OFFS(1), GOLLEK_OFFS(2), GOLLEK_OFFS(3)};
+#undef GOLLEK_OFFS
+    static_assert(o[19] < 256, "ds_read2 dword offsets");
+    uint2 v[10];
+    asm volatile(
+        "ds_read2_b32 %0, %14 offset0:%16 offset1:%17\n\t"
+        "ds_read2_b32 %1, %14 offset0:%18 offset1:%19\n\t"
+        "ds_read2_b32 %2, %14 offset0:%20 offset1:%21\n\t"
+        "ds_read2_b32 %3, %14 offset0:%22 offset1:%23\n\t"
+        "ds_read2_b32 %4, %14 offset0:%24 offset1:%25\n\t"
+        "ds_read2_b32 %5, %14 offset0:%26 offset1:%27\n\t"
+        "ds_read2_b32 %6, %14 offset0:%28 offset1:%29\n\t"
+        "ds_read2_b32 %7, %14 offset0:%30 offset1:%31\n\t"
+        "ds_read2_b32 %8, %14 offset0:%32 offset1:%33\n\t"
+        "ds_read2_b32 %9, %14 offset0:%34 offset1:%35\n\t"
+        "ds_read_u16 %10, %15\n\t"
+        "ds_read_u16 %11, %15 offset:%36\n\t"
+        "ds_read_u16 %12, %15 offset:%37\n\t"
+        "ds_read_u16 %13, %15 offset:%38\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+          "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(dh[0]), "=&v"(dh[1]), "=&v"(dh[2]), "=&v"(dh[3])
+        : "v"(a_q), "v"(a_d), "n"(o[0]), "n"(o[1]), "n"(o[2]), "n"(o[3]), "n"(o[4]), "n"(o[5]), "n"(o[6]),
+          "n"(o[7]), "n"(o[8]), "n"(o[9]), "n"(o[10]), "n"(o[11]), "n"(o[12]), "n"(o[13]), "n"(o[14]),
+          "n"(o[15]), "n"(o[16]), "n"(o[17]), "n"(o[18]), "n"(o[19]), "n"(2 * BB), "n"(4 * BB), "n"(6 * BB)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 10; i++) {
+        raw[2 * i] = v[i].x;
+        raw[2 * i + 1] = v[i].y;
+    }
+}
+
+// The piece's share of row n from blocks 2 c + h (lane n + 16 h, h < 2;
+// lanes 32..63 return values of the zero A rows).  Q4_0 codes are stored
+// as q + 8: each plane sum drops 8 x the plane's digit sum (ps) first, so
+// sum (q - 8) X stays exact in int32 up to the plane combine.
+template <int TYPE>
+__device__ __forceinline__ float q32_tile_piece(const uint32_t (&raw)[20], const uint32_t (&dh)[4],
+                                                const XOps4 &o, const int (&ps)[4][4]) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t sh = TYPE == kQ4_0 ? 4u * (uint32_t)(lane >> 5) : 0u;
+    const i32x4 zero = {0, 0, 0, 0};
+    i32x4 D[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t *r = raw + 5 * c;
+        const uint32_t l0 = __builtin_amdgcn_alignbyte(r[1], r[0], 2);
+        const uint32_t l1 = __builtin_amdgcn_alignbyte(r[2], r[1], 2);
+        i32x4 B;
+        if constexpr (TYPE == kQ4_0)
+            B = i32x4{(int)((l0 >> sh) & 0x0F0F0F0Fu), (int)((l1 >> sh) & 0x0F0F0F0Fu),
+                      (int)((r[3] >> sh) & 0x0F0F0F0Fu), (int)((r[4] >> sh) & 0x0F0F0F0Fu)};
+        else
+            B = i32x4{(int)l0, (int)l1, (int)r[3], (int)r[4]};
+        D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, zero, 0, 0, 0);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        int d0 = D[c][0], d1 = D[c][1], d2 = D[c][2], d3 = D[c][3];
+        if constexpr (TYPE == kQ4_0) {
+            d0 -= 8 * ps[c][0];
+            d1 -= 8 * ps[c][1];
+            d2 -= 8 * ps[c][2];
+            d3 -= 8 * ps[c][3];
+        }
+        // |d0 + 256 d1| < 2^28 (Q8_0) or 2^24 (Q4_0): at most one rounding each
+        const float S = fmaf((float)(d2 + 256 * d3), 65536.0f, (float)(d0 + 256 * d1));
+        acc = fmaf(half_bits_to_float_fast(dh[c]), S, acc);
+    }
+    return acc * o.xs;
 }
 
 }  // namespace
@@ -720,29 +830,38 @@ constexpr int kColThreads = kColWaves * 64;
 // row sums (2 floats a row).
 constexpr int kColX = 1024;
 
-// A wave's column: NL loads of 1 KB, 64 rows at a 144-byte pitch.
+// A wave's column: NL loads of 1 KB, the rows' PB-byte pieces (Q4_K, Q4_0:
+// a 144-byte superblock or eight blocks; Q8_0: eight 34-byte blocks, 272
+// bytes) packed at a PB-byte pitch.
+template <int TYPE>
 struct ColGeom {
+    static constexpr int PB = TYPE == kQ8_0 ? 8 * kQ8BlockBytes : kQKBlockBytes;
     static constexpr int NL = 9;
     static constexpr int kW = NL * 1024;                    // column bytes of a wave
     static constexpr int kRegion = kW + kColX;              // 16 regions: 160 KB
-    static constexpr int kMaxRows = kW / kQKBlockBytes;     // 64
-    static constexpr int kMaxTiles = (kMaxRows + kTileRows - 1) / kTileRows;
-    // Last load of tile t: tile t is bytes [2304 t, 2304 (t + 1)).
+    static constexpr int kMaxTiles = kW / (kTileRows * PB);  // whole tiles only
+    static constexpr int kMaxRows = kMaxTiles * kTileRows;   // 64 (Q8_0: 32)
+    static constexpr int kTileBytes = kTileRows * PB;
+    // Last load of tile t: tile t is bytes [16 PB t, 16 PB (t + 1)).
     static constexpr int last_load(int t) {
-        const int e = (kTileRows * kQKBlockBytes * (t + 1) + 1023) / 1024 - 1;
+        const int e = (kTileBytes * (t + 1) + 1023) / 1024 - 1;
         return e < NL - 1 ? e : NL - 1;
     }
-    static_assert(kMaxTiles * kTileRows * kQKBlockBytes <= kW, "the tiles fill the column");
+    static_assert(kMaxTiles >= 2 && kMaxTiles <= 4, "the kernel unrolls up to four tiles");
     static_assert(2 * 4 * kMaxTiles * kTileRows <= kColX, "row sums fit the x scratch");
 };
 
 }  // namespace
 
-__global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
+// TYPE: Q4_K, Q4_0 or Q8_0; a piece is the 256 elements of one superblock
+// column.
+template <int TYPE>
+__global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int rows_per_wg) {
-    using G = ColGeom;
+    using G = ColGeom<TYPE>;
     constexpr int NL = G::NL;
+    constexpr int PB = G::PB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * G::kRegion];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -760,17 +879,16 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
     const float4 xv = reinterpret_cast<const float4 *>(x)[64 * sb + lane];
     __builtin_amdgcn_sched_barrier(0);
     // Load k of a wave moves bytes 1024 k + 16 lane of its column, i.e. row
-    // b / 144, byte b % 144 of the row's superblock; rows past nr read
-    // zeros.  The descriptor starts at the column, so the last row's
-    // superblock ends at (nr - 1) row_bytes + 144 <= nr row_bytes - 144 wv.
+    // b / PB, byte b % PB of the row's piece; rows past nr read zeros.  The
+    // descriptor starts at the column, so the last row's piece ends at
+    // (nr - 1) row_bytes + PB <= nr row_bytes - PB wv.
     const __amdgpu_buffer_rsrc_t rs =
-        wave_buffer(w + r0 * row_bytes64 + kQKBlockBytes * sb,
-                    active ? (uint32_t)nr * row_bytes - kQKBlockBytes * wv : 0u);
+        wave_buffer(w + r0 * row_bytes64 + PB * sb, active ? (uint32_t)nr * row_bytes - PB * wv : 0u);
     uint32_t off[NL];
 #pragma unroll
     for (int k = 0; k < NL; k++) {
         const uint32_t b = 1024u * k + 16u * lane;
-        const uint32_t r = b / kQKBlockBytes, col = b - r * kQKBlockBytes;
+        const uint32_t r = b / PB, col = b - r * PB;
         off[k] = r < (uint32_t)nr ? r * row_bytes + col : kMaskedOffset;
     }
     auto issue = [&](int k) { col_load(rs, lds + wv * G::kRegion + 1024 * k, off[k]); };
@@ -781,11 +899,18 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
     float4 xr = xv;  // the conversion stays below the tile loads
     asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
     XOps4 xo;
-    x_operands4(xr, xbase, xo);
+    int ps[4][4];
+    if constexpr (TYPE == kQ4_0)
+        x_operands4<true>(xr, xbase, xo, ps);
+    else
+        x_operands4(xr, xbase, xo);
 
     const int n = lane & 15, g = lane >> 4;
-    const uint32_t a_h = wbase + n * kQKBlockBytes;
-    const uint32_t a_q = a_h + 16 + 8 * g;
+    // Q4_K: header and quant addresses of row n; Q4_0 / Q8_0: quant and
+    // scale addresses of row n's piece (see read_tile_piece32).
+    const uint32_t a_h = wbase + n * PB;
+    const uint32_t a_q = TYPE == kQ4_K ? a_h + 16 + 8 * g : a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
+    const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
     auto tile = [&](auto T) {
         constexpr int t = decltype(T)::value;
         wait_vm<0>();
@@ -796,10 +921,18 @@ __global__ __launch_bounds__(kColThreads) void gemv_q4_k_mfma_col_kernel(
             }
         }
         if (active) {
-            u32x4 hv;
-            uint2 q[4];
-            read_tile_superblock(a_h + 2304 * t, a_q + 2304 * t, hv, q);
-            const float v = q4k_tile_superblock4(hv, q, xo);
+            float v;
+            if constexpr (TYPE == kQ4_K) {
+                u32x4 hv;
+                uint2 q[4];
+                read_tile_superblock(a_h + G::kTileBytes * t, a_q + G::kTileBytes * t, hv, q);
+                v = q4k_tile_superblock4(hv, q, xo);
+            } else {
+                uint32_t raw[20], dh[4];
+                read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(
+                    a_q + G::kTileBytes * t, a_d + G::kTileBytes * t, raw, dh);
+                v = q32_tile_piece<TYPE>(raw, dh, xo, ps);
+            }
             // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until
             // the row sums (pair h of row r at float 2 r + h)
             if (lane < 32) lds_store_f32(xbase + 8 * (16 * t + n) + 4 * g, v);
@@ -880,8 +1013,8 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
     // At most 64 rows per CU: every workgroup's share stays in LDS, one
     // superblock column per wave (gemv_variant 3 keeps the shared tiles).
     const int64_t col_rows = (rows + cus - 1) / cus;
-    if (nsb <= 16 && col_rows <= ColGeom::kMaxRows && variant != 3) {
-        hipLaunchKernelGGL(gemv_q4_k_mfma_col_kernel, dim3((unsigned)((rows + col_rows - 1) / col_rows)),
+    if (nsb <= 16 && col_rows <= ColGeom<kQ4_K>::kMaxRows && variant != 3) {
+        hipLaunchKernelGGL(gemv_mfma_col_kernel<kQ4_K>, dim3((unsigned)((rows + col_rows - 1) / col_rows)),
                            dim3(kColThreads), 0, stream, w, row_bytes, nsb, x, y, rows, (int)col_rows);
         return hipGetLastError();
     }
@@ -901,6 +1034,39 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
     const MfmaPlan p = plan_mfma(rows, nsb);
     hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
                        stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
+    return hipGetLastError();
+}
+
+// Q4_0 / Q8_0 on the matrix cores (the column kernel): K a multiple of 256
+// up to 4096, 16-byte aligned weights, rows and x.  Every row count runs on
+// it (workgroups of at most ColGeom<TYPE>::kMaxRows rows, more workgroups
+// than CUs when needed), so a row's sum has the same bits whatever the row
+// count of the call.
+bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
+                        const float *x) {
+    if (type_id != kQ4_0 && type_id != kQ8_0) return false;
+    const int v = tuning().gemv_variant;
+    if (v == 1 || v == 2 || v == 4) return false;  // fp32 / ring paths kept selectable
+    if (cols <= 0 || cols % kQK != 0 || cols / kQK > 16 || rows <= 0) return false;
+    const int bb = type_id == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes;
+    if (row_bytes != cols / 32 * bb || (row_bytes & 15) != 0) return false;
+    return ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+}
+
+hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
+                                const float *x, float *y, int64_t rows, hipStream_t stream) {
+    const int nsb = (int)(cols / kQK);
+    const int64_t cus = device_cus();
+    const int64_t most = type_id == kQ8_0 ? ColGeom<kQ8_0>::kMaxRows : ColGeom<kQ4_0>::kMaxRows;
+    int64_t col_rows = (rows + cus - 1) / cus;
+    if (col_rows > most) col_rows = most;
+    const dim3 grid((unsigned)((rows + col_rows - 1) / col_rows));
+    if (type_id == kQ8_0)
+        hipLaunchKernelGGL(gemv_mfma_col_kernel<kQ8_0>, grid, dim3(kColThreads), 0, stream, w, row_bytes, nsb,
+                           x, y, rows, (int)col_rows);
+    else
+        hipLaunchKernelGGL(gemv_mfma_col_kernel<kQ4_0>, grid, dim3(kColThreads), 0, stream, w, row_bytes, nsb,
+                           x, y, rows, (int)col_rows);
     return hipGetLastError();
 }
 

@@ -239,7 +239,13 @@ def test_q4k_gemv_special_headers_match_java_order():
 Q80_Q40_SHAPES = [(syn.Q8_0, 1, 512), (syn.Q8_0, 15, 512), (syn.Q8_0, 17, 1536), (syn.Q8_0, 4096, 4096),
                   (syn.Q8_0, 33, 16384), (syn.Q8_0, 6, 16896), (syn.Q4_0, 1, 512), (syn.Q4_0, 7, 1024),
                   (syn.Q4_0, 11008, 4096), (syn.Q4_0, 35, 16384), (syn.Q4_0, 11003, 4096),
-                  (syn.Q8_0, 6000, 8192), (syn.Q4_0, 40000, 2048)]
+                  (syn.Q8_0, 6000, 8192), (syn.Q4_0, 40000, 2048),
+                  # the matrix-core column kernel's edges: the most rows per CU
+                  # (Q8_0 32, Q4_0 64) and one past them, one superblock
+                  # column, an odd number of them, a partial last tile
+                  (syn.Q8_0, 8192, 4096), (syn.Q8_0, 8193, 4096), (syn.Q4_0, 16384, 4096),
+                  (syn.Q4_0, 16385, 4096), (syn.Q8_0, 4000, 256), (syn.Q4_0, 3000, 2304),
+                  (syn.Q8_0, 5000, 2304), (syn.Q4_0, 300, 768)]
 
 
 @pytest.mark.parametrize("type_id,rows,cols", Q80_Q40_SHAPES,
@@ -251,7 +257,7 @@ def test_q8_0_q4_0_gemv_kernels_agree_with_oracle(type_id, rows, cols):
     t = _tensor(type_id, data, cols)
     ref = o.matvec_fp64(type_id, data, cols, x)
     try:
-        for variant in (0, 1):  # buffer->LDS ring, fp32 kernels
+        for variant in (0, 4, 1):  # matrix-core column kernel where it applies, buffer->LDS ring, fp32
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
             ops.mat_vec(t, x, y)
@@ -283,7 +289,7 @@ def test_q8_0_q4_0_gemv_special_scales_match_java_order(type_id):
     t = _tensor(type_id, data, cols)
     exp = o.matvec(type_id, data, cols, x)
     try:
-        for variant in (0, 1):
+        for variant in (0, 4, 1):
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
             ops.mat_vec(t, x, y)
