@@ -23,6 +23,7 @@ enum TypeId : int { kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
 constexpr int kQ8BlockBytes = 34;
 constexpr int kQ4BlockBytes = 18;
 constexpr int kQKBlockBytes = 144;
+constexpr int kQ5KBlockBytes = 176;
 constexpr int kQK = 256;
 
 // Exact IEEE half -> float, with NaN mapped to the canonical quiet NaN the

@@ -494,12 +494,12 @@ hipError_t launch_rb(int type_id, const uint8_t *w, int64_t row_bytes, int64_t c
 
 const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, const void *w,
                               const float *x) {
+    if (q32_mfma_supported(type_id, row_bytes, cols, 1, w, x)) return "gemv_mfma_col_kernel";
     if (is_k56(type_id))
         return gemv_k56_supported(type_id, row_bytes, w, x) ? "gemv_k56_kernel" : "gemv_generic_kernel";
     const GemvPlan p = plan_for(type_id, row_bytes, cols, w, x);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_mfma_kernel";
     if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_dot4_kernel";
-    if (q32_mfma_supported(type_id, row_bytes, cols, 1, w, x)) return "gemv_mfma_col_kernel";
     if (gemv_ring_supported(type_id, row_bytes, cols, 1, w, x)) return "gemv_ring_kernel";
     if (p.lpr == 0) return "gemv_generic_kernel";
     if (type_id == kQ4_K) return "gemv_q4_k_kernel";
@@ -510,14 +510,14 @@ const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, cons
 hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                        const float *x, float *y, int64_t rows, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
+    if (q32_mfma_supported(type_id, row_bytes, cols, rows, w, x))
+        return launch_gemv_q32_mfma(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (is_k56(type_id) && gemv_k56_supported(type_id, row_bytes, w, x))
         return launch_gemv_k56(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q4k_mfma(w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q4k_dot4(w, row_bytes, cols, x, y, rows, stream);
-    if (q32_mfma_supported(type_id, row_bytes, cols, rows, w, x))
-        return launch_gemv_q32_mfma(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (gemv_ring_supported(type_id, row_bytes, cols, rows, w, x))
         return launch_gemv_ring(type_id, w, row_bytes, cols, x, y, rows, stream);
     const GemvPlan p = is_k56(type_id) ? GemvPlan() : plan_for(type_id, row_bytes, cols, w, x);

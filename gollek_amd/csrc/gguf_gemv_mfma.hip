@@ -412,6 +412,23 @@ __device__ __forceinline__ void read_tile_superblock(uint32_t a_hdr, uint32_t a_
         : "memory");
 }
 
+// Q5_K: header (a_hdr = row n's superblock), high-bit bytes 8 g .. 8 g + 7
+// (a_qh = a_hdr + 16 + 8 g) and quant bytes (a_q = a_hdr + 48 + 8 g) of one tile.
+__device__ __forceinline__ void read_tile_superblock5(uint32_t a_hdr, uint32_t a_qh, uint32_t a_q,
+                                                      u32x4 &hv, uint2 &qh, uint2 (&q)[4]) {
+    asm volatile(
+        "ds_read_b128 %0, %6\n\t"
+        "ds_read_b64 %1, %7\n\t"
+        "ds_read_b64 %2, %8\n\t"
+        "ds_read_b64 %3, %8 offset:32\n\t"
+        "ds_read_b64 %4, %8 offset:64\n\t"
+        "ds_read_b64 %5, %8 offset:96\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(hv), "=&v"(qh), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+        : "v"(a_hdr), "v"(a_qh), "v"(a_q)
+        : "memory");
+}
+
 // Waits until at most N of this wave's loads are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -525,23 +542,34 @@ __device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, X
 
 // One superblock of a 16-row tile with four-plane x: lane n + 16 h returns
 // the share of sub-blocks h, 2 + h, 4 + h, 6 + h of row n (lanes 32..63
-// return values of the zero A rows, which callers drop).
+// return values of the zero A rows, which callers drop).  Q5_K (Q5): qh holds
+// the high-bit bytes 8 g .. 8 g + 7 of the lane's elements; bit 2 c (low
+// nibbles) or 2 c + 1 (high nibbles) of each becomes bit 4 of the code.
+template <bool Q5 = false>
 __device__ __forceinline__ float q4k_tile_superblock4(const u32x4 hv, const uint2 (&q)[4],
-                                                      const XOps4 &o) {
+                                                      const XOps4 &o, const uint2 qh = uint2{0u, 0u}) {
     const int lane = threadIdx.x & 63;
     const int h = (lane >> 4) & 1;
     const i32x4 zero = {0, 0, 0, 0};
     i32x4 D[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const i32x4 B = {(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
-                         (int)((q[c].x >> 4) & 0x0F0F0F0Fu), (int)((q[c].y >> 4) & 0x0F0F0F0Fu)};
+        uint32_t b[4] = {q[c].x & 0x0F0F0F0Fu, q[c].y & 0x0F0F0F0Fu, (q[c].x >> 4) & 0x0F0F0F0Fu,
+                         (q[c].y >> 4) & 0x0F0F0F0Fu};
+        if constexpr (Q5) {
+            b[0] |= ((qh.x >> (2 * c)) & 0x01010101u) << 4;
+            b[1] |= ((qh.y >> (2 * c)) & 0x01010101u) << 4;
+            b[2] |= ((qh.x >> (2 * c + 1)) & 0x01010101u) << 4;
+            b[3] |= ((qh.y >> (2 * c + 1)) & 0x01010101u) << 4;
+        }
+        const i32x4 B = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
         D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, zero, 0, 0, 0);
     }
     float Sq[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const int lo = D[c][0] + D[c][1] * 256;  // |.| < 2^24: exact as a float
+        // |.| < 2^24 for 4-bit codes: exact as a float (one rounding for Q5_K)
+        const int lo = D[c][0] + D[c][1] * 256;
         const int hi = D[c][2] + D[c][3] * 256;
         Sq[c] = fmaf((float)hi, 65536.0f, (float)lo);
     }
@@ -835,12 +863,12 @@ constexpr int kColX = 1024;
 // bytes) packed at a PB-byte pitch.
 template <int TYPE>
 struct ColGeom {
-    static constexpr int PB = TYPE == kQ8_0 ? 8 * kQ8BlockBytes : kQKBlockBytes;
+    static constexpr int PB = TYPE == kQ8_0 ? 8 * kQ8BlockBytes : TYPE == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     static constexpr int NL = 9;
     static constexpr int kW = NL * 1024;                    // column bytes of a wave
     static constexpr int kRegion = kW + kColX;              // 16 regions: 160 KB
     static constexpr int kMaxTiles = kW / (kTileRows * PB);  // whole tiles only
-    static constexpr int kMaxRows = kMaxTiles * kTileRows;   // 64 (Q8_0: 32)
+    static constexpr int kMaxRows = kMaxTiles * kTileRows;   // 64 (Q5_K: 48, Q8_0: 32)
     static constexpr int kTileBytes = kTileRows * PB;
     // Last load of tile t: tile t is bytes [16 PB t, 16 PB (t + 1)).
     static constexpr int last_load(int t) {
@@ -853,8 +881,8 @@ struct ColGeom {
 
 }  // namespace
 
-// TYPE: Q4_K, Q4_0 or Q8_0; a piece is the 256 elements of one superblock
-// column.
+// TYPE: Q4_K, Q5_K, Q4_0 or Q8_0; a piece is the 256 elements of one
+// superblock column.
 template <int TYPE>
 __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
@@ -927,6 +955,12 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
                 uint2 q[4];
                 read_tile_superblock(a_h + G::kTileBytes * t, a_q + G::kTileBytes * t, hv, q);
                 v = q4k_tile_superblock4(hv, q, xo);
+            } else if constexpr (TYPE == kQ5_K) {
+                u32x4 hv;
+                uint2 qh, q[4];
+                read_tile_superblock5(a_h + G::kTileBytes * t, a_h + 16 + 8 * g + G::kTileBytes * t,
+                                      a_h + 48 + 8 * g + G::kTileBytes * t, hv, qh, q);
+                v = q4k_tile_superblock4<true>(hv, q, xo, qh);
             } else {
                 uint32_t raw[20], dh[4];
                 read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(
@@ -1037,19 +1071,19 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
     return hipGetLastError();
 }
 
-// Q4_0 / Q8_0 on the matrix cores (the column kernel): K a multiple of 256
-// up to 4096, 16-byte aligned weights, rows and x.  Every row count runs on
+// Q4_0 / Q8_0 / Q5_K on the matrix cores (the column kernel): K a multiple
+// of 256 up to 4096, 16-byte aligned weights, rows and x.  Every row count runs on
 // it (workgroups of at most ColGeom<TYPE>::kMaxRows rows, more workgroups
 // than CUs when needed), so a row's sum has the same bits whatever the row
 // count of the call.
 bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x) {
-    if (type_id != kQ4_0 && type_id != kQ8_0) return false;
+    if (type_id != kQ4_0 && type_id != kQ8_0 && type_id != kQ5_K) return false;
     const int v = tuning().gemv_variant;
-    if (v == 1 || v == 2 || v == 4) return false;  // fp32 / ring paths kept selectable
+    if (v == 1 || v == 2 || v == 4) return false;  // fp32 / ring / Q5_K fp32 paths kept selectable
     if (cols <= 0 || cols % kQK != 0 || cols / kQK > 16 || rows <= 0) return false;
-    const int bb = type_id == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes;
-    if (row_bytes != cols / 32 * bb || (row_bytes & 15) != 0) return false;
+    const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+    if (row_bytes != cols / kQK * piece || (row_bytes & 15) != 0) return false;
     return ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
 }
 
@@ -1057,12 +1091,17 @@ hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes
                                 const float *x, float *y, int64_t rows, hipStream_t stream) {
     const int nsb = (int)(cols / kQK);
     const int64_t cus = device_cus();
-    const int64_t most = type_id == kQ8_0 ? ColGeom<kQ8_0>::kMaxRows : ColGeom<kQ4_0>::kMaxRows;
+    const int64_t most = type_id == kQ8_0   ? ColGeom<kQ8_0>::kMaxRows
+                         : type_id == kQ5_K ? ColGeom<kQ5_K>::kMaxRows
+                                            : ColGeom<kQ4_0>::kMaxRows;
     int64_t col_rows = (rows + cus - 1) / cus;
     if (col_rows > most) col_rows = most;
     const dim3 grid((unsigned)((rows + col_rows - 1) / col_rows));
     if (type_id == kQ8_0)
         hipLaunchKernelGGL(gemv_mfma_col_kernel<kQ8_0>, grid, dim3(kColThreads), 0, stream, w, row_bytes, nsb,
+                           x, y, rows, (int)col_rows);
+    else if (type_id == kQ5_K)
+        hipLaunchKernelGGL(gemv_mfma_col_kernel<kQ5_K>, grid, dim3(kColThreads), 0, stream, w, row_bytes, nsb,
                            x, y, rows, (int)col_rows);
     else
         hipLaunchKernelGGL(gemv_mfma_col_kernel<kQ4_0>, grid, dim3(kColThreads), 0, stream, w, row_bytes, nsb,

@@ -31,7 +31,7 @@ namespace gollek {
 
 namespace {
 
-constexpr int kQ5KBytes = 176;
+constexpr int kQ5KBytes = kQ5KBlockBytes;
 constexpr int kQ6KBytes = 210;
 
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {

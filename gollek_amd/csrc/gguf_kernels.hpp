@@ -22,7 +22,8 @@ struct LaunchTuning {
     std::atomic<int> gemm_variant{0};
     std::atomic<int> gemm_big_config{0};     // large-M GEMM: 0 buffer->LDS ring, 1..4 register-pipelined
     std::atomic<int> gemv_variant{0};        // 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring (Q4_K),
-                                             // 3 Q4_K on shared tiles for K <= 4096, 4 Q8_0 / Q4_0 rings
+                                             // 3 Q4_K on shared tiles for K <= 4096, 4 Q8_0 / Q4_0
+                                             // rings and Q5_K fp32
     std::atomic<int> moe_variant{0};         // 0 auto (matrix cores), 1 v_dot4 expert kernels
 };
 LaunchTuning &tuning();
@@ -50,8 +51,8 @@ bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const voi
                         const float *x);
 hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
-// Q4_0 / Q8_0 on the matrix cores (gguf_gemv_mfma.hip, the column kernel):
-// K a multiple of 256 up to 4096, any row count.
+// Q4_0 / Q8_0 / Q5_K on the matrix cores (gguf_gemv_mfma.hip, the column
+// kernel): K a multiple of 256 up to 4096, any row count.
 bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x);
 hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,

@@ -409,7 +409,7 @@ def test_device_pointer_entry_points_match_host():
 # ---- Q5_K / Q6_K -----------------------------------------------------------
 
 K56_SHAPES = [(syn.Q5_K, 1, 256), (syn.Q5_K, 7, 768), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 33, 16384),
-              (syn.Q5_K, 1003, 2304), (syn.Q6_K, 1, 256), (syn.Q6_K, 5, 768), (syn.Q6_K, 4096, 4096),
+              (syn.Q5_K, 1003, 2304), (syn.Q5_K, 12289, 4096), (syn.Q5_K, 20000, 1024), (syn.Q6_K, 1, 256), (syn.Q6_K, 5, 768), (syn.Q6_K, 4096, 4096),
               (syn.Q6_K, 37, 16384), (syn.Q6_K, 1001, 2304), (syn.Q6_K, 14336, 4096)]
 
 
@@ -425,18 +425,25 @@ def test_q5_k_q6_k_dequant_and_gemv(type_id, rows, cols):
     for r0, n in {(0, min(rows, 64)), (max(0, rows - 3), min(rows, 3))}:
         assert_same_bits(ops.dequantize_rows(t, r0, n), o.dequantize(type_id, data, cols, r0, n),
                          (type_id, r0))
-    y = np.zeros(rows, np.float32)
-    ops.mat_vec(t, x, y)
     ref = o.matvec_fp64(type_id, data, cols, x)
-    assert o.rel_err(y, ref) <= GEMV_TOL, o.rel_err(y, ref)
     java = o.matvec(type_id, data, cols, x)
-    assert o.rel_err(y, java) <= GEMV_TOL, o.rel_err(y, java)
-    part = np.full(rows, -3.0, np.float32)
-    ops.mat_vec_rows(t, x, part, rows // 2, True)
-    assert np.array_equal(part[:rows // 2], y[:rows // 2])
-    assert np.all(part[rows // 2:] == -3.0)
-    r = rows - 1
-    assert ops.dot_row(t, r, x) == pytest.approx(float(y[r]), rel=1e-6, abs=1e-6)
+    try:
+        # Q5_K with K <= 4096: the matrix-core column kernel (0) and the fp32
+        # kernel (4); the others run the fp32 kernel either way.
+        for variant in (0, 4):
+            ops.set_option("gemv_variant", variant)
+            y = np.zeros(rows, np.float32)
+            ops.mat_vec(t, x, y)
+            assert o.rel_err(y, ref) <= GEMV_TOL, (variant, o.rel_err(y, ref))
+            assert o.rel_err(y, java) <= GEMV_TOL, (variant, o.rel_err(y, java))
+            part = np.full(rows, -3.0, np.float32)
+            ops.mat_vec_rows(t, x, part, rows // 2, True)
+            assert np.array_equal(part[:rows // 2], y[:rows // 2]), variant
+            assert np.all(part[rows // 2:] == -3.0)
+            r = rows - 1
+            assert ops.dot_row(t, r, x) == pytest.approx(float(y[r]), rel=1e-6, abs=1e-6)
+    finally:
+        ops.set_option("gemv_variant", 0)
     t.close()
 
 
