@@ -32,12 +32,13 @@
 
 #include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"
+#include "gguf_mfma_q4k.hpp"
 
 namespace gollek {
 
-namespace {
+using namespace mfq;
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
+namespace {
 
 constexpr int kMoWaves = 16;
 constexpr int kMoThreads = kMoWaves * 64;
@@ -47,25 +48,6 @@ constexpr int kMoDmaPerWave = (kMoMaxDma + kMoWaves - 1) / kMoWaves;
 constexpr int kMoSlot = kMoMaxDma * 1024;
 constexpr int kMoSlots = 3;
 constexpr int kMoOutCap = 2560;      // buffered results (value, index)
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
-    v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
-    v = max(v, (uint32_t)dpp_i<0x124>((int)v));
-    v = max(v, (uint32_t)dpp_i<0x128>((int)v));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-__device__ __forceinline__ int sum8_i(int v) {
-    v += dpp_i<0xB1>(v);
-    v += dpp_i<0x4E>(v);
-    return v + dpp_i<0x141>(v);
-}
 
 }  // namespace
 
