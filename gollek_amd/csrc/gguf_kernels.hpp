@@ -113,7 +113,7 @@ hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float 
 size_t moe_topk_lds_bytes(int E, int K);
 hipError_t launch_moe_topk(const float *logits, int T, int E, int K, int sigmoid, int32_t *ids,
                            float *wts, hipStream_t stream);
-bool moe_q4k_mfma_supported(int E, int H, int I, const float *x);
+bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x);
 hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
                                int H, int I, const float *x, const int32_t *ids, const float *wts,
                                int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);

@@ -322,7 +322,7 @@ hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t 
                           int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                           const float *x, const int32_t *ids, const float *wts, int T, int top_k,
                           float *out, uint8_t *ws, hipStream_t stream) {
-    if (tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, x))
+    if (tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, T * top_k, x))
         return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream);
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;

@@ -4,8 +4,10 @@
 // DirectForwardFfnService.java:40-61): h_pair = silu(gate_e x_t) * (up_e x_t),
 // y_pair = down_e h_pair, out[t] = sum_j w[t,j] y_pair[t,j] in route order.
 //
-// Two passes of one tile kernel, after the routing kernel has sorted the
-// valid routes by expert and laid out work items:
+// Two passes of one tile kernel.  Each workgroup first sorts the valid
+// routes by expert and lays out the work items itself, in LDS (routing is a
+// few microseconds of latency as a launch of its own, and tables in global
+// memory would put dependent reads in front of the first weight load):
 //   pass 0 (gate/up): item = (used expert, 16-row tile of its I rows, group of
 //     up to 4 of its routes).  A slot holds the tile's 16 gate rows and 16 up
 //     rows; wave w < nsb contracts gate superblock w, wave nsb + w up
@@ -47,7 +49,97 @@ constexpr int kMoMaxDma = 38;        // 1 KB loads per item slot
 constexpr int kMoDmaPerWave = (kMoMaxDma + kMoWaves - 1) / kMoWaves;
 constexpr int kMoSlot = kMoMaxDma * 1024;
 constexpr int kMoSlots = 3;
-constexpr int kMoOutCap = 2560;      // buffered results (value, index)
+constexpr int kMoOutCap = 1536;      // buffered results (value, index)
+constexpr int kMoMaxExperts = 256;   // routing tables held in LDS
+constexpr int kMoMaxRoutes = 2048;
+
+// Routing tables of one pass, built in LDS by every workgroup: the valid
+// routes (expert id in range, weight != 0; MoeForwardPass.java:222) stably
+// sorted by expert (pairs), each expert's first slot in that order
+// (offsets[e], offsets[E] = valid routes), the used experts in expert order
+// and per used expert u the first work item items[u] (items[nused] = all).
+struct MoeRouteLds {
+    int32_t offsets[kMoMaxExperts + 1];
+    int32_t used[kMoMaxExperts];
+    int32_t items[kMoMaxExperts + 1];
+    int32_t nused;
+    uint16_t pairs[kMoMaxRoutes];
+};
+
+// Builds R for work units of tiles_e items per (expert, group of kMoGroup
+// routes).  tmp: P + E ints of LDS that nothing else uses meanwhile.  Every
+// thread of the workgroup calls this; it ends with a barrier.  Counts by LDS
+// atomics, then wave 0 scans the experts in chunks of 64 and scatters the
+// routes 64 at a time in route order: a route's slot is its expert's running
+// offset plus its rank among the chunk's equal keys (found by ballots over
+// the key bits).
+__device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__restrict__ wts, int P,
+                              int E, int tiles_e, MoeRouteLds &R, int32_t *tmp) {
+    int32_t *keys = tmp, *run = tmp + P;
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    for (int e = tid; e < E; e += (int)blockDim.x) run[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += (int)blockDim.x) {
+        const int e = ids[p];
+        const bool valid = e >= 0 && e < E && wts[p] != 0.0f;
+        if (valid) atomicAdd(&run[e], 1);  // LDS atomic
+        keys[p] = valid ? e : -1;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        int carry = 0, ucount = 0, icarry = 0;
+        for (int base = 0; base < E; base += 64) {
+            const int e = base + lane;
+            const int c = e < E ? run[e] : 0;
+            const int units = tiles_e * ((c + kMoGroup - 1) / kMoGroup);
+            int a = c, b = units;  // inclusive scans over the 64 lanes
+            for (int d = 1; d < 64; d <<= 1) {
+                const int ta = __shfl_up(a, d, 64), tb = __shfl_up(b, d, 64);
+                if (lane >= d) {
+                    a += ta;
+                    b += tb;
+                }
+            }
+            const uint64_t ub = __ballot(c > 0);
+            if (e < E) {
+                R.offsets[e] = carry + a - c;
+                run[e] = carry + a - c;
+            }
+            if (c > 0) {
+                const int u = ucount + __popcll(ub & below);
+                R.used[u] = e;
+                R.items[u] = icarry + b - units;
+            }
+            carry += __shfl(a, 63, 64);
+            icarry += __shfl(b, 63, 64);
+            ucount += __popcll(ub);
+        }
+        if (lane == 0) {
+            R.offsets[E] = carry;
+            R.nused = ucount;
+            R.items[ucount] = icarry;
+        }
+        int bits = 1;
+        while ((1 << bits) <= E) bits++;
+        for (int base = 0; base < P; base += 64) {
+            const int p = base + lane;
+            const int key = p < P ? keys[p] : -1;
+            const uint32_t k1 = (uint32_t)(key + 1);
+            uint64_t same = __ballot(true);
+            for (int bt = 0; bt < bits; bt++) {
+                const uint64_t v = __ballot((k1 >> bt) & 1u);
+                same &= ((k1 >> bt) & 1u) ? v : ~v;
+            }
+            const int rank = __popcll(same & below);
+            const int r0 = key >= 0 ? run[key] : 0;  // read by all lanes before any update
+            if (key >= 0) R.pairs[r0 + rank] = (uint16_t)p;
+            const bool last = (same >> lane) == 1ull;  // highest lane of its key
+            if (key >= 0 && last) run[key] = r0 + __popcll(same);
+        }
+    }
+    __syncthreads();
+}
 
 }  // namespace
 
@@ -65,24 +157,71 @@ struct MoeTileGeom {
     int64_t w_bytes;  // bytes of one stacked weight matrix (< 2^31)
 };
 
+// One route's 16 h values as a digit record (every lane of the wave calls
+// this; lanes 16 k .. 16 k + 15 hold one route's elements r = lane & 15):
+// three balanced signed-byte planes of the 22-bit integers
+// X_r = trunc(h_r / 2^(e-22)), max |h| < 2^e over the 16 (so an element's
+// error is below 2^-22 of that maximum), plane-major: lane r returns dword
+// 4 (r & 3) + (r >> 2) = plane r & 3 of elements 4 (r >> 2) .. + 3 (plane 3
+// is zero and not stored); `scale` = 2^(e-22) (NaN when an h is not finite)
+// and `sum` = the fp32 sum of the 16 h, in every lane.
+__device__ __forceinline__ uint32_t h_record16(float hval, float &scale, float &sum) {
+    uint32_t mb = __float_as_uint(hval) & 0x7FFFFFFFu;
+    mb = max(mb, (uint32_t)dpp_i<0xB1>((int)mb));   // quad_perm [1,0,3,2]
+    mb = max(mb, (uint32_t)dpp_i<0x4E>((int)mb));   // quad_perm [2,3,0,1]
+    mb = max(mb, (uint32_t)dpp_i<0x124>((int)mb));  // row_ror:4
+    mb = max(mb, (uint32_t)dpp_i<0x128>((int)mb));  // row_ror:8
+    const bool finite = mb < 0x7F800000u;
+    int e = 0;
+    (void)frexpf(__uint_as_float(mb), &e);
+    const int X = finite ? (int)ldexpf(hval, 22 - e) : 0;  // |X| < 2^22
+    // Adding 0x8080 makes bytes 0, 1 the digits + 128; the XOR maps them back
+    // to signed bytes and leaves the top digit (X + 0x8080) >> 16 in
+    // [-64, 64] as byte 2.
+    const uint32_t Y = ((uint32_t)X + 0x00008080u) ^ 0x00008080u;
+    float s = hval;
+    s += __int_as_float(dpp_i<0xB1>(__float_as_int(s)));
+    s += __int_as_float(dpp_i<0x4E>(__float_as_int(s)));
+    s += __int_as_float(dpp_i<0x124>(__float_as_int(s)));
+    s += __int_as_float(dpp_i<0x128>(__float_as_int(s)));
+    sum = s;
+    scale = finite ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
+    // lane 4 j + p: byte p of the quad's four Y (quad_perm broadcasts)
+    const uint32_t y0 = (uint32_t)dpp_i<0x00>((int)Y), y1 = (uint32_t)dpp_i<0x55>((int)Y);
+    const uint32_t y2 = (uint32_t)dpp_i<0xAA>((int)Y), y3 = (uint32_t)dpp_i<0xFF>((int)Y);
+    const uint32_t pb = (uint32_t)(threadIdx.x & 3);
+    const uint32_t sel = pb | ((pb + 4u) << 8) | 0x0C0C0000u;
+    return __builtin_amdgcn_perm(y1, y0, sel) | (__builtin_amdgcn_perm(y3, y2, sel) << 16);
+}
+
+// h record of route p and 16-element group G (groups = I / 16 per route):
+// 14 dwords at 14 (p groups + G): the 12 plane dwords of h_record16, then
+// scale and sum, so one route's records are one contiguous run.
+constexpr int kRecDwords = 14;
+
 // MODE 0: gate/up (w0 = gate, w1 = up); MODE 1: down (w0 = down).
+// REC (MODE 0): h leaves as records (kRecDwords) for moe_down_combine_kernel;
+// otherwise as fp32 (out + p I + row).
 // vec: pass 0 x[T][H] (route p -> token p / top_k); pass 1 h[P][I] (route p).
-template <int MODE>
+template <int MODE, bool REC>
 __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, MoeTileGeom G,
-    const float *__restrict__ vec, int top_k, const int32_t *__restrict__ meta, int E, int P,
-    float *__restrict__ out) {
+    const float *__restrict__ vec, int top_k, const int32_t *__restrict__ ids,
+    const float *__restrict__ wts, int E, int P, float *__restrict__ out) {
+    static_assert(MODE == 0 || !REC, "records are pass 0's output");
     __shared__ __attribute__((aligned(16))) uint8_t ring[kMoSlots * kMoSlot + 1024];  // + sink
     __shared__ __attribute__((aligned(16))) uint8_t scratch[kMoWaves][1024];  // digit build
     __shared__ float part[2][kMoGroup][kMoWaves][16];
     __shared__ float outv[kMoOutCap];
     __shared__ int outi[kMoOutCap];
     __shared__ int gid[kMoGroup];  // route ids of the current group
+    __shared__ MoeRouteLds R;
 
-    const int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
-    const int32_t *used = pairs + P;
-    const int nused = used[E];
-    const int32_t *items = used + E + 1 + (MODE == 1 ? E + 1 : 0);
+    // Routing (the ring is free until the first loads below).
+    moe_route_lds(ids, wts, P, E, G.tiles_e, R, reinterpret_cast<int32_t *>(ring));
+    const int32_t *offsets = R.offsets, *used = R.used, *items = R.items;
+    const uint16_t *pairs = R.pairs;
+    const int nused = R.nused;
     const int nitems = items[nused];
     // Work split.  Every (expert, route group) unit has G.tiles_e items, in
     // order.  When k = grid / units workgroups per unit leave at most 1/8 of
@@ -129,7 +268,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         }
         c.u = lo;
         c.e = used[c.u];
-        c.cnt = counts[c.e];
+        c.cnt = offsets[c.e + 1] - offsets[c.e];
         c.groups = (c.cnt + kMoGroup - 1) / kMoGroup;
         const int j = i - items[c.u];
         c.group = j / G.tiles_e;
@@ -143,7 +282,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         c.group = 0;
         if (++c.u < nused) {
             c.e = used[c.u];
-            c.cnt = counts[c.e];
+            c.cnt = offsets[c.e + 1] - offsets[c.e];
             c.groups = (c.cnt + kMoGroup - 1) / kMoGroup;
         }
     };
@@ -368,7 +507,20 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     };
     auto flush = [&]() {
         __syncthreads();
-        for (int q = threadIdx.x; q < nout; q += kMoThreads) out[outi[q]] = outv[q];
+        if constexpr (REC) {
+            // Buffered h come in runs of 16 (one route's 16-row group), each
+            // a row of 16 lanes: converted to records here.
+            for (int q = threadIdx.x; q < nout; q += kMoThreads) {
+                const int r = q & 15, rg = outi[q] >> 4;
+                float scale, sum;
+                const uint32_t rec = h_record16(outv[q], scale, sum);
+                float *o = out + kRecDwords * rg;
+                if ((r & 3) < 3) o[4 * (r & 3) + (r >> 2)] = __uint_as_float(rec);
+                if (r < 2) o[12 + r] = r == 0 ? scale : sum;
+            }
+        } else {
+            for (int q = threadIdx.x; q < nout; q += kMoThreads) out[outi[q]] = outv[q];
+        }
         nout = 0;
         __syncthreads();
     };
@@ -489,6 +641,406 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     flush();
 }
 
+// ---- Down projection and combine, token-major --------------------------
+//
+// Workgroup = (16 rows of H, group of tg tokens): wave 0 groups the
+// workgroup's tg * top_k <= 64 routes by expert (items); wave w takes items
+// w, w + waves, ... and works through their routes one unit (item, route)
+// at a time.  A unit's loads are the item's 16-row down tile (16 x I/256
+// superblocks, into one of the wave's three tile slots; a later unit of the
+// same item loads nothing there) and the route's h records (into one of
+// three route slots); the loads of unit k + 2 go out before unit k is
+// computed, so two units are in flight per wave and no wave waits on
+// another until the combine.  A route's 16 results go to LDS; then every
+// token's rows are combined in route order, fp32 multiply then add
+// (MoeForwardPass.java:217-240, :461-472), skipping the routes
+// moe_combine_kernel skips.
+//
+// Contraction (v_mfma_i32_16x16x64_i8, B = the tile's nibbles as in the
+// GEMV): h records carry one power-of-two scale per 16 elements, so A row
+// m = 4 q + p holds plane p < 3 of quarter q of the chunk (16 elements:
+// half q & 1 of sub-block 2 c + (q >> 1)), live on the lanes g with
+// g >> 1 == q & 1, in bytes 0..7 (q < 2, low nibbles) or 8..15; output lane
+// n + 16 g holds the plane sums of row n and quarter g,
+// D0 + 256 D1 + 65536 D2 = sum q X exactly (|.| < 16 * 15 * 2^22), which it
+// scales by the quarter's scale before the sub-block's d sc.
+namespace {
+
+constexpr int kMdMaxWaves = 8;
+constexpr int kMdRoutes = 64;  // routes per workgroup
+constexpr int kMdSlots = 2;    // tile and route slots per wave (units in flight + 1)
+
+constexpr uint32_t md_pitch(int nsb) {  // odd 16-byte units: the 16 rows' reads spread over the banks
+    return ((nsb * kQKBlockBytes / 16) % 2 == 1) ? nsb * kQKBlockBytes : nsb * kQKBlockBytes + 16;
+}
+// A slot's bytes move as whole kilobytes (16 bytes a lane) plus a tail of
+// 256-byte loads (4 bytes a lane), so slots take no more LDS than they hold.
+constexpr int md_tile_bytes(int nsb) { return 16 * (int)md_pitch(nsb); }
+constexpr int md_route_bytes(int nsb) { return nsb * 16 * kRecDwords * 4; }
+constexpr int md_full(int bytes) { return bytes / 1024; }
+constexpr int md_tail(int bytes) { return (bytes % 1024 + 255) / 256; }
+constexpr int md_slot(int bytes) { return 1024 * md_full(bytes) + 256 * md_tail(bytes); }
+
+}  // namespace
+
+// One unit's LDS operands of superblock s: the 16 rows' header and quant
+// bytes (B), the A halves (records or the zero sink) and (scale, sum).
+struct MdSb {
+    u32x4 hv;
+    uint2 qb[4], xl[4], xh[4];
+    float2 xp[4];
+};
+// Reads of superblock s for one asm statement (named operands, so one
+// statement can read every superblock of a unit and wait once).
+#define MD_SB_READS(s)                                                                            \
+    "ds_read_b128 %[hv" #s "], %[th" #s "]\n\t"                                                   \
+    "ds_read_b64 %[qa" #s "], %[tq" #s "]\n\t"                                                    \
+    "ds_read_b64 %[qb" #s "], %[tq" #s "] offset:32\n\t"                                          \
+    "ds_read_b64 %[qc" #s "], %[tq" #s "] offset:64\n\t"                                          \
+    "ds_read_b64 %[qd" #s "], %[tq" #s "] offset:96\n\t"                                          \
+    "ds_read_b64 %[la" #s "], %[rl" #s "]\n\t"                                                    \
+    "ds_read_b64 %[lb" #s "], %[rl" #s "] offset:224\n\t"                                         \
+    "ds_read_b64 %[lc" #s "], %[rl" #s "] offset:448\n\t"                                         \
+    "ds_read_b64 %[ld" #s "], %[rl" #s "] offset:672\n\t"                                         \
+    "ds_read_b64 %[ha" #s "], %[rh" #s "]\n\t"                                                    \
+    "ds_read_b64 %[hb" #s "], %[rh" #s "] offset:224\n\t"                                         \
+    "ds_read_b64 %[hc" #s "], %[rh" #s "] offset:448\n\t"                                         \
+    "ds_read_b64 %[hd" #s "], %[rh" #s "] offset:672\n\t"                                         \
+    "ds_read_b64 %[pa" #s "], %[rp" #s "]\n\t"                                                    \
+    "ds_read_b64 %[pb" #s "], %[rp" #s "] offset:224\n\t"                                         \
+    "ds_read_b64 %[pc" #s "], %[rp" #s "] offset:448\n\t"                                         \
+    "ds_read_b64 %[pd" #s "], %[rp" #s "] offset:672\n\t"
+#define MD_SB_OUTS(s)                                                                             \
+    [hv##s] "=&v"(o[s].hv), [qa##s] "=&v"(o[s].qb[0]), [qb##s] "=&v"(o[s].qb[1]),                  \
+        [qc##s] "=&v"(o[s].qb[2]), [qd##s] "=&v"(o[s].qb[3]), [la##s] "=&v"(o[s].xl[0]),            \
+        [lb##s] "=&v"(o[s].xl[1]), [lc##s] "=&v"(o[s].xl[2]), [ld##s] "=&v"(o[s].xl[3]),            \
+        [ha##s] "=&v"(o[s].xh[0]), [hb##s] "=&v"(o[s].xh[1]), [hc##s] "=&v"(o[s].xh[2]),            \
+        [hd##s] "=&v"(o[s].xh[3]), [pa##s] "=&v"(o[s].xp[0]), [pb##s] "=&v"(o[s].xp[1]),            \
+        [pc##s] "=&v"(o[s].xp[2]), [pd##s] "=&v"(o[s].xp[3])
+#define MD_SB_INS(s)                                                                              \
+    [th##s] "v"(a_h + s * kQKBlockBytes), [tq##s] "v"(a_q + s * kQKBlockBytes),                     \
+        [rl##s] "v"(a_lo + s * lo_step), [rh##s] "v"(a_hi + s * hi_step), [rp##s] "v"(a_p + s * 896u)
+
+// Every LDS operand of a unit (nsb superblocks), then one wait.
+template <int NSB>
+__device__ __forceinline__ void md_read_unit(MdSb (&o)[NSB], uint32_t a_h, uint32_t a_q, uint32_t a_lo,
+                                             uint32_t lo_step, uint32_t a_hi, uint32_t hi_step, uint32_t a_p) {
+    static_assert(16 * 4 * kRecDwords == 896 && 4 * 4 * kRecDwords == 224, "record strides");
+    if constexpr (NSB == 1)
+        asm volatile(MD_SB_READS(0) "s_waitcnt lgkmcnt(0)" : MD_SB_OUTS(0) : MD_SB_INS(0) : "memory");
+    else if constexpr (NSB == 2)
+        asm volatile(MD_SB_READS(0) MD_SB_READS(1) "s_waitcnt lgkmcnt(0)"
+                     : MD_SB_OUTS(0), MD_SB_OUTS(1)
+                     : MD_SB_INS(0), MD_SB_INS(1)
+                     : "memory");
+    else if constexpr (NSB == 3)
+        asm volatile(MD_SB_READS(0) MD_SB_READS(1) MD_SB_READS(2) "s_waitcnt lgkmcnt(0)"
+                     : MD_SB_OUTS(0), MD_SB_OUTS(1), MD_SB_OUTS(2)
+                     : MD_SB_INS(0), MD_SB_INS(1), MD_SB_INS(2)
+                     : "memory");
+    else
+        asm volatile(MD_SB_READS(0) MD_SB_READS(1) MD_SB_READS(2) MD_SB_READS(3) "s_waitcnt lgkmcnt(0)"
+                     : MD_SB_OUTS(0), MD_SB_OUTS(1), MD_SB_OUTS(2), MD_SB_OUTS(3)
+                     : MD_SB_INS(0), MD_SB_INS(1), MD_SB_INS(2), MD_SB_INS(3)
+                     : "memory");
+}
+#undef MD_SB_READS
+#undef MD_SB_OUTS
+#undef MD_SB_INS
+
+// Lane 0 takes the next index from an LDS counter for the wave.
+__device__ __forceinline__ int wave_grab(int *counter) {
+    int v = 0;
+    if ((threadIdx.x & 63) == 0) v = atomicAdd(counter, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+struct MoeDownGeom {
+    uint32_t wave_bytes;         // LDS per wave
+    int tg;                      // tokens per workgroup
+    uint32_t w_bytes, h_bytes;   // ranges: stacked down weights; h records
+};
+
+template <int NSB>
+__global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
+    const uint8_t *__restrict__ down, MoeDownGeom G, const uint8_t *__restrict__ hrec,
+    const int32_t *__restrict__ ids, const float *__restrict__ wts, int T, int top_k, int H, int E,
+    float *__restrict__ out) {
+    constexpr uint32_t kRowBytes = NSB * kQKBlockBytes, kPitch = md_pitch(NSB);
+    constexpr uint32_t kRecBytes = md_route_bytes(NSB);  // one route's records
+    constexpr int kTF = md_full(md_tile_bytes(NSB)), kTT = md_tail(md_tile_bytes(NSB));
+    constexpr int kRF = md_full(md_route_bytes(NSB)), kRT = md_tail(md_route_bytes(NSB));
+    constexpr int kUnitLoads = kTF + kTT + kRF + kRT;  // every unit issues exactly this many
+    constexpr uint32_t kTileSlot = md_slot(md_tile_bytes(NSB)), kRouteSlot = md_slot(md_route_bytes(NSB));
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // sink, then waves x wave_bytes
+    __shared__ float ys[kMdRoutes][16];
+    __shared__ float rw[kMdRoutes];
+    __shared__ int rok[kMdRoutes];
+    __shared__ int it_e[kMdRoutes];
+    __shared__ unsigned long long it_mask[kMdRoutes];
+    __shared__ int n_items, next_item;
+
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = (int)blockIdx.x * 16;
+    const int t0 = (int)blockIdx.y * G.tg;
+    const int nt = min(G.tg, T - t0);
+    const int p0 = t0 * top_k;
+
+    // Routing: route slot j = route p0 + j; an item is an expert with the
+    // mask of its route slots.
+    if (wv == 0) {
+        int key = -1;
+        float w = 0.0f;
+        if (lane < nt * top_k) {
+            const int e = ids[p0 + lane];
+            w = wts[p0 + lane];
+            if (e >= 0 && e < E && w != 0.0f) key = e;
+        }
+        rw[lane] = w;
+        rok[lane] = key >= 0 ? 1 : 0;
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        int bits = 1;
+        while ((1 << bits) <= E) bits++;
+        const uint32_t k1 = (uint32_t)(key + 1);
+        uint64_t same = __ballot(true);
+        for (int bt = 0; bt < bits; bt++) {
+            const uint64_t v = __ballot((k1 >> bt) & 1u);
+            same &= ((k1 >> bt) & 1u) ? v : ~v;
+        }
+        const bool leader = key >= 0 && (same & below) == 0ull;
+        const uint64_t lb = __ballot(leader);
+        if (leader) {
+            const int idx = __popcll(lb & below);
+            it_e[idx] = key;
+            it_mask[idx] = same;
+        }
+        if (lane == 0) {
+            n_items = __popcll(lb);
+            next_item = 0;
+        }
+    }
+    if (threadIdx.x < 256) reinterpret_cast<uint32_t *>(lds)[threadIdx.x] = 0u;  // the sink
+    __syncthreads();
+    const int nitems = n_items;
+
+    uint8_t *const sink = lds;  // always zero: reads of dead A lanes, writes of loads that move nothing
+    uint8_t *const wbase = lds + 1024u + (uint32_t)wv * G.wave_bytes;
+    const __amdgpu_buffer_rsrc_t rsw = wave_buffer(down, G.w_bytes);
+    const __amdgpu_buffer_rsrc_t rsh = wave_buffer(hrec, G.h_bytes);
+    const __amdgpu_buffer_rsrc_t rs0 = wave_buffer(hrec, 0);  // every load out of range
+    // Per-lane offsets of the tile loads (row b / pitch, column b % pitch of
+    // staged byte b: 1024 k + 16 lane for the full loads, then
+    // 1024 kTF + 256 k + 4 lane for the tail) and of the record loads.
+    uint32_t toff[kTF + kTT], roff[kRF + kRT];
+#pragma unroll
+    for (int k = 0; k < kTF + kTT; k++) {
+        const uint32_t b = k < kTF ? 1024u * k + 16u * lane : 1024u * kTF + 256u * (k - kTF) + 4u * lane;
+        const uint32_t r = b / kPitch, col = b - r * kPitch;
+        toff[k] = (r < 16u && col < kRowBytes) ? r * kRowBytes + col : kMaskedOffset;
+    }
+#pragma unroll
+    for (int k = 0; k < kRF + kRT; k++) {
+        const uint32_t o = k < kRF ? 1024u * k + 16u * lane : 1024u * kRF + 256u * (k - kRF) + 4u * lane;
+        roff[k] = o < kRecBytes ? o : kMaskedOffset;
+    }
+    auto mask_of = [&](int item) -> uint64_t {
+        if (item >= nitems) return 0ull;
+        const uint64_t m = it_mask[item];
+        return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(m >> 32)) << 32) |
+               (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)m);
+    };
+    // Items go to the waves as they ask (a wave sharing its SIMD takes fewer).
+    auto grab = [&]() -> int { return wave_grab(&next_item); };
+    // Issue cursor: the item whose units go out next and its routes left.
+    int ii = grab();
+    uint64_t im = mask_of(ii);
+    bool ifirst = true;
+    int its = kMdSlots - 1, irs = 0;  // last tile slot used; next route slot
+    // Issues the next unit's loads (exactly kUnitLoads, all out of range when
+    // no unit is left) and returns it as j | tile slot << 8 | route slot << 12,
+    // or -1.
+    auto issue_next = [&]() -> int {
+        const bool have = __builtin_amdgcn_readfirstlane(ii < nitems ? 1 : 0) != 0;
+        const bool tile = __builtin_amdgcn_readfirstlane(have && ifirst ? 1 : 0) != 0;
+        if (tile) its = its == kMdSlots - 1 ? 0 : its + 1;
+        const int e = have ? __builtin_amdgcn_readfirstlane(it_e[ii]) : 0;
+        const uint32_t base = ((uint32_t)e * (uint32_t)H + (uint32_t)row0) * kRowBytes;
+        // (one descriptor per branch: a selected one would be taken for divergent)
+        // (Offsets go through named locals: an array element written in the
+        // builtin's argument list breaks the kernel's host stub.)
+        if (tile) {
+            uint8_t *tdst = wbase + (uint32_t)its * kTileSlot;
+#pragma unroll
+            for (int k = 0; k < kTF; k++) {
+                const uint32_t o = toff[k] + base;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_ptr)(tdst + 1024 * k), 16, o, 0, 0, kStreamLoad);
+            }
+#pragma unroll
+            for (int k = kTF; k < kTF + kTT; k++) {
+                const uint32_t o = toff[k] + base;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_ptr)(tdst + 1024 * kTF + 256 * (k - kTF)), 4, o, 0,
+                                                         0, kStreamLoad);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kTF; k++) {
+                const uint32_t o = toff[k];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs0, (lds_ptr)sink, 16, o, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = kTF; k < kTF + kTT; k++) {
+                const uint32_t o = toff[k];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs0, (lds_ptr)sink, 4, o, 0, 0, 0);
+            }
+        }
+        const int j = have ? __builtin_ctzll(im) : 0;
+        const uint32_t rb = (uint32_t)(p0 + j) * kRecBytes;
+        if (have) {
+            uint8_t *rdst = wbase + kMdSlots * kTileSlot + (uint32_t)irs * kRouteSlot;
+#pragma unroll
+            for (int k = 0; k < kRF; k++) {
+                const uint32_t o = roff[k] + rb;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsh, (lds_ptr)(rdst + 1024 * k), 16, o, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = kRF; k < kRF + kRT; k++) {
+                const uint32_t o = roff[k] + rb;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsh, (lds_ptr)(rdst + 1024 * kRF + 256 * (k - kRF)), 4, o, 0,
+                                                         0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kRF; k++) {
+                const uint32_t o = roff[k];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs0, (lds_ptr)sink, 16, o, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = kRF; k < kRF + kRT; k++) {
+                const uint32_t o = roff[k];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs0, (lds_ptr)sink, 4, o, 0, 0, 0);
+            }
+        }
+        const int unit = have ? (j | its << 8 | irs << 12) : -1;
+        irs = irs == kMdSlots - 1 ? 0 : irs + 1;
+        if (have) {
+            im &= im - 1;
+            ifirst = im == 0ull;
+            if (ifirst) {
+                ii = grab();
+                im = mask_of(ii);
+            }
+        }
+        return unit;
+    };
+
+    const int n = lane & 15, g = lane >> 4, q = n >> 2, pl = n & 3;
+    const bool live = (g >> 1) == (q & 1) && pl < 3;
+    const int hs = g >> 1;  // sub-block parity of this output lane's quarter
+    const i32x4 zero4 = {0, 0, 0, 0};
+    const uint32_t zero_lds = (uint32_t)(uintptr_t)(lds_ptr)sink;
+    // A bytes 0..7 (q < 2) or 8..15 come from the records; the other half,
+    // and every byte of a dead lane, from the zero sink.
+    const bool lo_live = live && q < 2, hi_live = live && q >= 2;
+    // y of the unit's route from its tile slot and route slot.
+    auto compute = [&](int unit) {
+        const int j = unit & 255, ts = (unit >> 8) & 15, rs = unit >> 12;
+        const uint32_t tb = (uint32_t)(uintptr_t)(lds_ptr)(wbase + (uint32_t)ts * kTileSlot);
+        const uint32_t rb = (uint32_t)(uintptr_t)(lds_ptr)(wbase + kMdSlots * kTileSlot + (uint32_t)rs * kRouteSlot);
+        const uint32_t a_h0 = tb + n * kPitch, a_q0 = a_h0 + 16 + 8 * g;
+        // records of groups 16 s + 4 c + q (A) and 16 s + 4 c + g (scale, sum)
+        const uint32_t a_x = rb + 4 * kRecDwords * q + 16 * (pl < 3 ? pl : 0) + 8 * (g & 1);
+        const uint32_t a_lo0 = lo_live ? a_x : zero_lds, a_hi0 = hi_live ? a_x : zero_lds;
+        const uint32_t lo_step = lo_live ? 16u * 4 * kRecDwords : 0u, hi_step = hi_live ? 16u * 4 * kRecDwords : 0u;
+        const uint32_t a_p0 = rb + 4 * kRecDwords * g + 48;
+        MdSb o[NSB];
+        md_read_unit<NSB>(o, a_h0, a_q0, a_lo0, lo_step, a_hi0, hi_step, a_p0);
+        // every superblock's products first, then their epilogues
+        i32x4 Dall[NSB][4];
+#pragma unroll
+        for (int s = 0; s < NSB; s++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint2 qv = o[s].qb[c];
+                const i32x4 B = {(int)(qv.x & 0x0F0F0F0Fu), (int)(qv.y & 0x0F0F0F0Fu),
+                                 (int)((qv.x >> 4) & 0x0F0F0F0Fu), (int)((qv.y >> 4) & 0x0F0F0F0Fu)};
+                const i32x4 A = {(int)o[s].xl[c].x, (int)o[s].xl[c].y, (int)o[s].xh[c].x, (int)o[s].xh[c].y};
+                Dall[s][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero4, 0, 0, 0);
+            }
+        float v = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NSB; s++) {
+            const u32x4 hv = o[s].hv;
+            const float2 *xp = o[s].xp;
+            const i32x4 *D = Dall[s];
+            const float d = half_bits_to_float_fast(hv.x);
+            const float dmin = half_bits_to_float_fast(hv.x >> 16);
+            // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks hs, 2 + hs, 4 + hs, 6 + hs
+            const uint32_t hy = hv.y >> (8 * hs), hz = hv.z >> (8 * hs), hw = hv.w >> (8 * hs);
+            const uint32_t sc03 = hy & 0x003F003Fu;
+            const uint32_t mn03 = hz & 0x003F003Fu;
+            const uint32_t sc47 = (hw & 0x000F000Fu) | ((hy >> 2) & 0x00300030u);
+            const uint32_t mn47 = ((hw >> 4) & 0x000F000Fu) | ((hz >> 2) & 0x00300030u);
+            const float scf[4] = {(float)(sc03 & 0xFFu), (float)((sc03 >> 16) & 0xFFu),
+                                  (float)(sc47 & 0xFFu), (float)((sc47 >> 16) & 0xFFu)};
+            const float mnf[4] = {(float)(mn03 & 0xFFu), (float)((mn03 >> 16) & 0xFFu),
+                                  (float)(mn47 & 0xFFu), (float)((mn47 >> 16) & 0xFFu)};
+            float S[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                S[c] = (float)(int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0])) *
+                       xp[c].x;
+            if (__builtin_isfinite(d) && __builtin_isfinite(dmin)) {
+                float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    qs = fmaf(scf[c], S[c], qs);
+                    mm = fmaf(mnf[c], xp[c].y, mm);
+                }
+                v += fmaf(d, qs, -(dmin * mm));
+            } else {
+                // the reference's (d sc) products; zero min codes skip a
+                // non-finite dmin (minContribution, RT/GgufKQuantLayout.java:67-69)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    v += (d * scf[c]) * S[c] - (mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f) * xp[c].y;
+            }
+        }
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (lane < 16) lds_store_f32((uint32_t)(uintptr_t)(lds_ptr)&ys[j][lane], v);
+    };
+
+    // Unit k's loads go out before unit k - (kMdSlots - 1) is computed.
+    int u0 = issue_next(), u1 = kMdSlots > 2 ? issue_next() : -1;
+    while (u0 >= 0) {  // uniform
+        wait_vm<kUnitLoads * (kMdSlots - 2)>();  // unit u0's loads are done (later units' may not be)
+        const int un = issue_next();
+        compute(u0);
+        if constexpr (kMdSlots > 2) {
+            u0 = u1;
+            u1 = un;
+        } else {
+            u0 = un;
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    {
+#pragma clang fp contract(off)
+        for (int o = (int)threadIdx.x; o < nt * 16; o += (int)blockDim.x) {
+            const int t = o >> 4, r = o & 15;
+            float acc = 0.0f;
+            for (int j = 0; j < top_k; j++) {
+                const int slot = t * top_k + j;
+                const float scaled = ys[slot][r] * rw[slot];  // AccelOps.mulScalar
+                acc = rok[slot] ? acc + scaled : acc;         // addToTokenRow
+            }
+            out[(int64_t)(t0 + t) * H + row0 + r] = acc;
+        }
+    }
+}
+
 namespace {
 
 MoeTileGeom make_geom(int mode, int E, int H, int I) {
@@ -496,7 +1048,7 @@ MoeTileGeom make_geom(int mode, int E, int H, int I) {
     const int K = mode == 0 ? H : I;
     g.nsb = K / kQK;
     g.rows_e = mode == 0 ? I : H;
-    g.rt = mode == 0 ? 1 : (16 / g.nsb);
+    g.rt = mode == 0 ? 1 : min(16 / g.nsb, 8);
     g.tiles_e = (g.rows_e + 16 * g.rt - 1) / (16 * g.rt);
     g.row_bytes = (uint32_t)(g.nsb * kQKBlockBytes);
     // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all banks
@@ -510,10 +1062,30 @@ MoeTileGeom make_geom(int mode, int E, int H, int I) {
     return g;
 }
 
+// The token-major down pass: I up to 1024 (a wave's slots fit at least one
+// wave), top_k <= 64 and 32-bit buffer offsets.
+constexpr int kMdStaticLds = kMdRoutes * (16 * 4 + 4 + 4 + 4 + 8) + 16;  // ys, rw, rok, it_e, it_mask, counters
+constexpr int kLdsBytes = 163840;
+
+bool make_down_geom(int E, int H, int I, int T, int top_k, MoeDownGeom &g, int &waves) {
+    const int nsb = I / kQK;
+    if (nsb < 1 || nsb > 4 || top_k < 1 || top_k > kMdRoutes || H % 16 != 0) return false;
+    g.wave_bytes = (uint32_t)(kMdSlots * (md_slot(md_tile_bytes(nsb)) + md_slot(md_route_bytes(nsb))));
+    g.tg = kMdRoutes / top_k;
+    const int64_t w_bytes = (int64_t)E * H * nsb * kQKBlockBytes;
+    const int64_t h_bytes = (int64_t)T * top_k * (I / 16) * kRecDwords * 4;
+    if (w_bytes >= (int64_t)kMaskedOffset || h_bytes >= (int64_t)kMaskedOffset) return false;
+    g.w_bytes = (uint32_t)w_bytes;
+    g.h_bytes = (uint32_t)h_bytes;
+    waves = min(kMdMaxWaves, (int)((kLdsBytes - kMdStaticLds - 1024) / (int)g.wave_bytes));
+    return waves >= 1;
+}
+
 }  // namespace
 
-bool moe_q4k_mfma_supported(int E, int H, int I, const float *x) {
+bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x) {
     if (H % kQK != 0 || I % kQK != 0 || H > 8 * kQK || I > 16 * kQK) return false;
+    if (E > kMoMaxExperts || P > kMoMaxRoutes) return false;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return false;
     for (int mode = 0; mode < 2; mode++) {
         const MoeTileGeom g = make_geom(mode, E, H, I);
@@ -523,25 +1095,50 @@ bool moe_q4k_mfma_supported(int E, int H, int I, const float *x) {
     return true;
 }
 
-// Routing, gate/up, down and combine (4 launches); the caller has checked
-// moe_q4k_mfma_supported.
+// Gate/up then down: with the token-major down pass (I <= 1024) two
+// launches, h as digit records; otherwise gate/up, the expert-major down
+// pass and the combine.  Each pass routes in LDS first.  The caller has
+// checked moe_q4k_mfma_supported.
 hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
                                int H, int I, const float *x, const int32_t *ids, const float *wts,
                                int T, int top_k, float *out, uint8_t *ws, hipStream_t stream) {
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
-    int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
     const MoeTileGeom g0 = make_geom(0, E, H, I), g1 = make_geom(1, E, H, I);
-    hipError_t e = launch_moe_route(ids, wts, P, E, g0.tiles_e, g1.tiles_e, meta, stream);
-    if (e != hipSuccess) return e;
     const unsigned grid = (unsigned)device_cus();
     float *hbuf = reinterpret_cast<float *>(ws + L.h);
+    // h records (P I 3.5 bytes) fit the fp32 h region.
+    MoeDownGeom gd;
+    int waves = 0;
+    if (make_down_geom(E, H, I, T, top_k, gd, waves)) {
+        hipLaunchKernelGGL((moe_expert_tile_kernel<0, true>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
+                           g0, x, top_k, ids, wts, E, P, hbuf);
+        const dim3 dgrid((unsigned)(H / 16), (unsigned)((T + gd.tg - 1) / gd.tg));
+        const size_t lds = 1024 + (size_t)waves * gd.wave_bytes;
+        const uint8_t *hrec = ws + L.h;
+        auto run = [&](auto kernel) {
+            if (lds > 65536) {
+                const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return e;
+            }
+            hipLaunchKernelGGL(kernel, dgrid, dim3(64 * waves), lds, stream, down, gd, hrec, ids, wts, T, top_k,
+                               H, E, out);
+            return hipGetLastError();
+        };
+        switch (I / kQK) {
+        case 1: return run(&moe_down_combine_kernel<1>);
+        case 2: return run(&moe_down_combine_kernel<2>);
+        case 3: return run(&moe_down_combine_kernel<3>);
+        default: return run(&moe_down_combine_kernel<4>);
+        }
+    }
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
-    hipLaunchKernelGGL(moe_expert_tile_kernel<0>, dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0, x,
-                       top_k, meta, E, P, hbuf);
-    hipLaunchKernelGGL(moe_expert_tile_kernel<1>, dim3(grid), dim3(kMoThreads), 0, stream, down,
-                       (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, meta, E, P, ypair);
-    e = hipGetLastError();
+    hipLaunchKernelGGL((moe_expert_tile_kernel<0, false>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0,
+                       x, top_k, ids, wts, E, P, hbuf);
+    hipLaunchKernelGGL((moe_expert_tile_kernel<1, false>), dim3(grid), dim3(kMoThreads), 0, stream, down,
+                       (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_moe_combine(ids, wts, ypair, T, top_k, H, E, out, stream);
 }
