@@ -66,13 +66,25 @@ struct MoeRouteLds {
     uint16_t pairs[kMoMaxRoutes];
 };
 
+// Inclusive prefix sum over the wave (DPP: shifts within rows of 16, then
+// the row totals broadcast to the rows above).
+__device__ __forceinline__ int wave_scan_incl(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
 // Builds R for work units of tiles_e items per (expert, group of kMoGroup
 // routes).  tmp: P + E ints of LDS that nothing else uses meanwhile.  Every
 // thread of the workgroup calls this; it ends with a barrier.  Counts by LDS
-// atomics, then wave 0 scans the experts in chunks of 64 and scatters the
-// routes 64 at a time in route order: a route's slot is its expert's running
-// offset plus its rank among the chunk's equal keys (found by ballots over
-// the key bits).
+// atomics, then wave 0 scans the experts in chunks of 64 (wave_scan_incl)
+// and scatters the routes 64 at a time in route order: a route's slot is its
+// expert's running offset plus its rank among the chunk's equal keys (found
+// by ballots over the key bits).
 __device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__restrict__ wts, int P,
                               int E, int tiles_e, MoeRouteLds &R, int32_t *tmp) {
     int32_t *keys = tmp, *run = tmp + P;
@@ -93,14 +105,7 @@ __device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__re
             const int e = base + lane;
             const int c = e < E ? run[e] : 0;
             const int units = tiles_e * ((c + kMoGroup - 1) / kMoGroup);
-            int a = c, b = units;  // inclusive scans over the 64 lanes
-            for (int d = 1; d < 64; d <<= 1) {
-                const int ta = __shfl_up(a, d, 64), tb = __shfl_up(b, d, 64);
-                if (lane >= d) {
-                    a += ta;
-                    b += tb;
-                }
-            }
+            const int a = wave_scan_incl(c), b = wave_scan_incl(units);
             const uint64_t ub = __ballot(c > 0);
             if (e < E) {
                 R.offsets[e] = carry + a - c;
@@ -111,8 +116,8 @@ __device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__re
                 R.used[u] = e;
                 R.items[u] = icarry + b - units;
             }
-            carry += __shfl(a, 63, 64);
-            icarry += __shfl(b, 63, 64);
+            carry += __builtin_amdgcn_readlane(a, 63);
+            icarry += __builtin_amdgcn_readlane(b, 63);
             ucount += __popcll(ub);
         }
         if (lane == 0) {
@@ -525,13 +530,17 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         __syncthreads();
     };
 
-    // Prologue: the first group's vectors, the first items' loads, then the
-    // group's operands.
+    // Prologue: the first item's loads, the first group's vectors, the next
+    // items' loads, then the group's operands.  Every workgroup starts at
+    // once, and the memory system serves requests issued together
+    // interleaved: issued first, item 0 lands well before the items after it
+    // instead of together with them.
     Cursor c_cur = c_first;
     Item cur = item_of(c_cur);
+    issue(0, i_begin);
     build(cur, false, [&]() {
 #pragma unroll
-        for (int j = 0; j < kMoSlots - 1; j++) issue(j, i_begin + j);
+        for (int j = 1; j < kMoSlots - 1; j++) issue(j, i_begin + j);
     });
     cur_key = cur.e * 65536 + cur.group;
 
