@@ -164,12 +164,13 @@ struct MoeTileGeom {
 
 // One route's 16 h values as a digit record (every lane of the wave calls
 // this; lanes 16 k .. 16 k + 15 hold one route's elements r = lane & 15):
-// three balanced signed-byte planes of the 22-bit integers
-// X_r = trunc(h_r / 2^(e-22)), max |h| < 2^e over the 16 (so an element's
-// error is below 2^-22 of that maximum), plane-major: lane r returns dword
-// 4 (r & 3) + (r >> 2) = plane r & 3 of elements 4 (r >> 2) .. + 3 (plane 3
-// is zero and not stored); `scale` = 2^(e-22) (NaN when an h is not finite)
-// and `sum` = the fp32 sum of the 16 h, in every lane.
+// three balanced signed-byte planes of the integers
+// X_r = rint(h_r / 2^(e-22)), max |h| < 2^e over the 16, so |X_r| <= 2^22
+// and an element's error is at most 2^-23 of that maximum; plane-major:
+// lane r returns dword 4 (r & 3) + (r >> 2) = plane r & 3 of elements
+// 4 (r >> 2) .. + 3 (plane 3 is zero and not stored); `scale` = 2^(e-22)
+// (NaN when an h is not finite) and `sum` = the fp32 sum of the 16 h, in
+// every lane.
 __device__ __forceinline__ uint32_t h_record16(float hval, float &scale, float &sum) {
     uint32_t mb = __float_as_uint(hval) & 0x7FFFFFFFu;
     mb = max(mb, (uint32_t)dpp_i<0xB1>((int)mb));   // quad_perm [1,0,3,2]
@@ -179,7 +180,7 @@ __device__ __forceinline__ uint32_t h_record16(float hval, float &scale, float &
     const bool finite = mb < 0x7F800000u;
     int e = 0;
     (void)frexpf(__uint_as_float(mb), &e);
-    const int X = finite ? (int)ldexpf(hval, 22 - e) : 0;  // |X| < 2^22
+    const int X = finite ? (int)rintf(ldexpf(hval, 22 - e)) : 0;  // |X| <= 2^22
     // Adding 0x8080 makes bytes 0, 1 the digits + 128; the XOR maps them back
     // to signed bytes and leaves the top digit (X + 0x8080) >> 16 in
     // [-64, 64] as byte 2.
@@ -671,7 +672,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 // half q & 1 of sub-block 2 c + (q >> 1)), live on the lanes g with
 // g >> 1 == q & 1, in bytes 0..7 (q < 2, low nibbles) or 8..15; output lane
 // n + 16 g holds the plane sums of row n and quarter g,
-// D0 + 256 D1 + 65536 D2 = sum q X exactly (|.| < 16 * 15 * 2^22), which it
+// D0 + 256 D1 + 65536 D2 = sum q X exactly (|.| <= 16 * 15 * 2^22), which it
 // scales by the quarter's scale before the sub-block's d sc.
 namespace {
 
