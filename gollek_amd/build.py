@@ -30,6 +30,7 @@ HIP_SOURCES = (
     "gguf_k56.hip",
     "gguf_gemv_dot4.hip",
     "gguf_gemv_mfma.hip",
+    "gguf_gemv_q6k_mfma.hip",
     "gguf_gemv_ring.hip",
     "gguf_gemm.hip",
     "gguf_moe.hip",

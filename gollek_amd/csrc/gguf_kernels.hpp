@@ -23,7 +23,7 @@ struct LaunchTuning {
     std::atomic<int> gemm_big_config{0};     // large-M GEMM: 0 buffer->LDS ring, 1..4 register-pipelined
     std::atomic<int> gemv_variant{0};        // 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring (Q4_K),
                                              // 3 Q4_K on shared tiles for K <= 4096, 4 Q8_0 / Q4_0
-                                             // rings and Q5_K fp32
+                                             // rings and Q5_K / Q6_K fp32
     std::atomic<int> moe_variant{0};         // 0 auto (matrix cores), 1 v_dot4 expert kernels
 };
 LaunchTuning &tuning();
@@ -57,6 +57,12 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
                         const float *x);
 hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
+
+// Q6_K on the matrix cores (gguf_gemv_q6k_mfma.hip): K = 2048 or 4096, row
+// bytes K / 256 * 210, weights and x 16-byte aligned.
+bool q6k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x);
+hipError_t launch_gemv_q6k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols, const float *x, float *y,
+                                int64_t rows, hipStream_t stream);
 
 // Q5_K / Q6_K (gguf_k56.hip): dequantization and the GEMV; the GEMV needs
 // gemv_k56_supported (x 16-byte aligned, Q6_K weights 2-byte and Q5_K

@@ -89,22 +89,14 @@ __device__ __forceinline__ void col_load(__amdgpu_buffer_rsrc_t rs, uint8_t *dst
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, off, 0, 0, kStreamLoad);
 }
 
-// A wave's x operands for one superblock with four digit planes.
-struct XOps4 {
-    i32x4 A[4];
-    float xs4[4], xs;
-};
-
 // Wave-wide: lane l holds elements 4 l .. 4 l + 3 of a superblock of x.
-// Writes the digit planes to `scratch` (1 KB of LDS private to the wave),
-// reads them back in the A operand layout and leaves the scratch free.
-// With PS, ps[c][p] = the integer sum of plane p's digits over sub-block
-// 2 c + h (h = (lane >> 4) & 1), for codes stored with an offset.
-template <bool PS = false>
-__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o,
-                                            int (*ps)[4] = nullptr) {
+// Writes the four balanced signed-byte digit planes of X = trunc(x /
+// 2^(e-30)), max |x| < 2^e, to `scratch` (1 KB of LDS private to the wave:
+// plane p at + 256 p, element i at byte i), leaves this lane's four
+// digits of plane p in w[p] and returns the scale 2^(e-30) (NaN when an x
+// is not finite).
+__device__ __forceinline__ float x_planes4(const float (&v)[4], uint32_t scratch, uint32_t (&w)[4]) {
     const int lane = threadIdx.x & 63;
-    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
     uint32_t mb = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) mb = max(mb, __float_as_uint(v[k]) & 0x7FFFFFFFu);
@@ -129,10 +121,10 @@ __device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, X
     const uint32_t t01h = __builtin_amdgcn_perm(Y[1], Y[0], 0x07030602u);
     const uint32_t t23l = __builtin_amdgcn_perm(Y[3], Y[2], 0x05010400u);
     const uint32_t t23h = __builtin_amdgcn_perm(Y[3], Y[2], 0x07030602u);
-    const uint32_t w[4] = {__builtin_amdgcn_perm(t23l, t01l, 0x05040100u),
-                           __builtin_amdgcn_perm(t23l, t01l, 0x07060302u),
-                           __builtin_amdgcn_perm(t23h, t01h, 0x05040100u),
-                           __builtin_amdgcn_perm(t23h, t01h, 0x07060302u)};
+    w[0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+    w[1] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+    w[2] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+    w[3] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
     // Plane p at scratch + 256 p; lane l's four elements at byte 4 l.
     asm volatile(
         "ds_write2st64_b32 %0, %1, %2 offset1:1\n\t"
@@ -140,6 +132,27 @@ __device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, X
         :
         : "v"(scratch + 4 * lane), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3])
         : "memory");
+    return finite ? ldexpf(1.0f, e - 30) : __builtin_nanf("");
+}
+
+// A wave's x operands for one superblock with four digit planes.
+struct XOps4 {
+    i32x4 A[4];
+    float xs4[4], xs;
+};
+
+// Wave-wide: lane l holds elements 4 l .. 4 l + 3 of a superblock of x.
+// Writes the digit planes to `scratch` (1 KB of LDS private to the wave),
+// reads them back in the A operand layout and leaves the scratch free.
+// With PS, ps[c][p] = the integer sum of plane p's digits over sub-block
+// 2 c + h (h = (lane >> 4) & 1), for codes stored with an offset.
+template <bool PS = false>
+__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o,
+                                            int (*ps)[4] = nullptr) {
+    const int lane = threadIdx.x & 63;
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t w[4];
+    o.xs = x_planes4(v, scratch, w);
     // Sub-block j = lanes 8 j .. 8 j + 7; lane n + 16 g (h = g & 1) needs the
     // sums of sub-blocks 2 c + h.
     const float s8 = sum8((v[0] + v[1]) + (v[2] + v[3]));
@@ -150,7 +163,6 @@ __device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, X
         const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s8), 16 * c + 8));
         o.xs4[c] = h ? b : a;
     }
-    o.xs = finite ? ldexpf(1.0f, e - 30) : __builtin_nanf("");
     if constexpr (PS) {
 #pragma unroll
         for (int p = 0; p < 4; p++) {

@@ -17,8 +17,8 @@ import pytest
 
 from gollek_amd import build
 
-RING_SOURCES = ["gguf_gemm.hip", "gguf_gemv_dot4.hip", "gguf_gemv_mfma.hip", "gguf_gemv_ring.hip",
-                "gguf_moe_mfma.hip"]
+RING_SOURCES = ["gguf_gemm.hip", "gguf_gemv_dot4.hip", "gguf_gemv_mfma.hip", "gguf_gemv_q6k_mfma.hip",
+                "gguf_gemv_ring.hip", "gguf_moe_mfma.hip"]
 
 
 def _assembly(src: str, tmp_path: Path) -> str:
