@@ -1,5 +1,6 @@
 // gguf_gemv_q6k_mfma.hip -- Q6_K GEMV (decode, M = 1) on the gfx950 matrix
-// cores, K = 2048 or 4096 (the lm_head of Q4_K_M files is Q6_K).
+// cores, K a multiple of 2048 up to 14336 (Q4_K_M files store the lm_head
+// and part of the FFN down projections as Q6_K).
 //
 // Same value as the reference raw Q6_K mat-vec (RT/GgufQ6RawDot.java:32-134;
 // block layout RT/GgufKBlockDequantizer.java:319-432): per 256-element
@@ -27,12 +28,19 @@
 // fp32, then scale by sc_q and, per superblock, by d and x's scale.
 //
 // Streaming.  One workgroup (16 waves) per CU takes an equal share of the
-// rows in 16-row tiles.  An item is a tile's 16 rows x 8 superblocks (one
-// half of K = 4096: 1680 bytes of each row, 26,880 bytes), so a 5-slot
-// ring keeps four items (107 KB) in flight per CU; every wave issues two of
-// an item's 27 buffer->LDS loads of 1 KB, one barrier per item publishes
-// it, and wave w (superblock w) works on the items of its half.  Partial
-// row sums meet in LDS and one wave per tile adds them.  Superblocks are
+// rows in 16-row tiles.  An item is a tile's 16 rows x 8 superblocks (an
+// eighth of a row per 2048 columns: 1680 bytes of each row, 26,880 bytes);
+// every wave issues two of an item's 27 buffer->LDS loads of 1 KB, one
+// barrier per item publishes it, and wave w works on position w & 7 of the
+// items j with j & 1 == w >> 3.  K <= 4096: wave w owns superblock w, builds
+// its x operands once, and a 5-slot ring keeps four items (107 KB) in
+// flight per CU.  Wider K: x's digit planes for every superblock are built
+// once into LDS (1 KB each), a wave reads its operands per item, and the
+// ring has 3 slots (carrying x in the items instead, converted per item,
+// with a 4-slot ring measured 19.8 us against 17.4 us at 4096 x 14336: the
+// conversion sits on every item's critical path).  A wave sums its items
+// of a tile in registers; the waves' row sums meet in LDS and one wave per
+// tile adds them.  Superblocks are
 // 210 bytes, so every other one starts 2 bytes off a dword in LDS: a lane
 // reads aligned dwords and v_alignbyte_b32 realigns them (the shift is 0 or
 // 2, uniform per wave).
@@ -54,22 +62,86 @@ constexpr int kQ6Item = kQ6TileRows * kQ6Pitch;                    // 26880
 constexpr int kQ6Dma = (kQ6Item + 1023) / 1024;                  // 27 loads of 1 KB
 constexpr int kQ6DmaPerWave = (kQ6Dma + kQ6Waves - 1) / kQ6Waves;  // 2
 constexpr int kQ6Slot = kQ6Dma * 1024;
-constexpr int kQ6Slots = 5;
 constexpr int kQ6MaxRows = 1024;                                 // rows per workgroup
+constexpr int kQ6MaxSbLds = 56;                                  // superblocks of x in LDS (K <= 14336)
+
+// One superblock's x operands from its four digit planes (1 KB of LDS,
+// plane p at + 256 p, element i at byte i).  A lane (m, g): plane p = m & 3
+// of quarter q = m >> 2 of chunk c, i.e. elements 128 (c >> 1) + 32 (c & 1)
+// + 64 (q >> 1) + 8 g .. + 7, live when g >> 1 == q & 1 (bytes 0..7 for
+// q < 2, 8..15 otherwise); corr[c][p] = 32 x the digit sum of plane p over
+// this output lane's quarter g of chunk c.
+__device__ __forceinline__ void q6_x_operands(uint32_t planes, i32x4 (&A)[4], int (&corr)[4][4]) {
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15, g = lane >> 4, q = n >> 2, pl = n & 3;
+    const bool live = (g >> 1) == (q & 1);
+    uint2 xa[4];
+    uint4 qs[4][4];  // [c][p]: the 16 digits of this lane's quarter
+    const uint32_t a_x = planes + 256u * pl + 64u * (q >> 1) + 8u * g;
+    const uint32_t a_s = planes + 64u * (g >> 1) + 16u * (g & 1);
+    asm volatile(
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "ds_read_b64 %0, %20\n\t"
+        "ds_read_b64 %1, %20 offset:32\n\t"
+        "ds_read_b64 %2, %20 offset:128\n\t"
+        "ds_read_b64 %3, %20 offset:160\n\t"
+        "ds_read_b128 %4, %21\n\t"
+        "ds_read_b128 %5, %21 offset:256\n\t"
+        "ds_read_b128 %6, %21 offset:512\n\t"
+        "ds_read_b128 %7, %21 offset:768\n\t"
+        "ds_read_b128 %8, %21 offset:32\n\t"
+        "ds_read_b128 %9, %21 offset:288\n\t"
+        "ds_read_b128 %10, %21 offset:544\n\t"
+        "ds_read_b128 %11, %21 offset:800\n\t"
+        "ds_read_b128 %12, %21 offset:128\n\t"
+        "ds_read_b128 %13, %21 offset:384\n\t"
+        "ds_read_b128 %14, %21 offset:640\n\t"
+        "ds_read_b128 %15, %21 offset:896\n\t"
+        "ds_read_b128 %16, %21 offset:160\n\t"
+        "ds_read_b128 %17, %21 offset:416\n\t"
+        "ds_read_b128 %18, %21 offset:672\n\t"
+        "ds_read_b128 %19, %21 offset:928\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]), "=&v"(qs[0][0]), "=&v"(qs[0][1]),
+          "=&v"(qs[0][2]), "=&v"(qs[0][3]), "=&v"(qs[1][0]), "=&v"(qs[1][1]), "=&v"(qs[1][2]),
+          "=&v"(qs[1][3]), "=&v"(qs[2][0]), "=&v"(qs[2][1]), "=&v"(qs[2][2]), "=&v"(qs[2][3]),
+          "=&v"(qs[3][0]), "=&v"(qs[3][1]), "=&v"(qs[3][2]), "=&v"(qs[3][3])
+        : "v"(a_x), "v"(a_s)
+        : "memory");
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int lo = live ? (int)xa[c].x : 0, hi = live ? (int)xa[c].y : 0;
+        A[c] = q < 2 ? i32x4{lo, hi, 0, 0} : i32x4{0, 0, lo, hi};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint4 d = qs[c][p];
+            int sum = __builtin_amdgcn_sdot4((int)d.x, 0x01010101, 0, false);
+            sum = __builtin_amdgcn_sdot4((int)d.y, 0x01010101, sum, false);
+            sum = __builtin_amdgcn_sdot4((int)d.z, 0x01010101, sum, false);
+            sum = __builtin_amdgcn_sdot4((int)d.w, 0x01010101, sum, false);
+            corr[c][p] = 32 * sum;
+        }
+    }
+}
 
 }  // namespace
 
+// XLDS: K > 4096, x's planes for every superblock in LDS.
+template <bool XLDS>
 __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int64_t rows_per_wg) {
+    constexpr int kQ6Slots = XLDS ? 3 : 5;
     static_assert(kQ6DmaPerWave * kQ6Waves >= kQ6Dma, "item loads");
     static_assert(kQ6Waves * 1024 <= kQ6Slot, "x scratch fits a slot");
     __shared__ __attribute__((aligned(16))) uint8_t ring[kQ6Slots * kQ6Slot + 1024];  // + sink
     __shared__ float part[2][kQ6Waves][2][16];  // [tile & 1][wave][quarter pair][row]
     __shared__ float yout[kQ6MaxRows];
-    // Each wave's x scratch (four digit planes, 1 KB) is kilobyte w of the
-    // last ring slot, which the loop first refills after every wave has
-    // read its operands back.
+    __shared__ __attribute__((aligned(16))) uint8_t xpl[XLDS ? kQ6MaxSbLds : 1][1024];  // XLDS: x's planes
+    __shared__ float xst[XLDS ? kQ6MaxSbLds : 1];                                      // XLDS: x's scales
+    // K <= 4096: each wave's x scratch (four digit planes, 1 KB) is kilobyte
+    // w of the last ring slot, which the loop first refills after every wave
+    // has read its operands back.
     const uint32_t xscr = (uint32_t)(uintptr_t)(lds_ptr)(ring + (kQ6Slots - 1) * kQ6Slot);
 
     const uint32_t row_bytes = (uint32_t)row_bytes64;
@@ -78,8 +150,8 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
     const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kQ6MaxRows
     const int tiles = (nr + kQ6TileRows - 1) / kQ6TileRows;
-    const int halves = nsb / kQ6HalfSb;  // 1 or 2
-    const int items = tiles * halves;
+    const int chunks = nsb / kQ6HalfSb;  // items per tile
+    const int items = tiles * chunks;
     // Rows past the workgroup's share are out of the descriptor's range.
     const __amdgpu_buffer_rsrc_t rs = wave_buffer(w + r0 * row_bytes64, (uint32_t)nr * row_bytes);
 
@@ -95,7 +167,7 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         dbase[i] = (k < (uint32_t)kQ6Dma && r < (uint32_t)kQ6TileRows) ? r * row_bytes + col : kMaskedOffset;
     }
     auto issue = [&](int slot, int item) {
-        const int t = item / halves, hf = item - t * halves;
+        const int t = item / chunks, hf = item - t * chunks;
         const uint32_t uoff =
             item < items ? (uint32_t)t * kQ6TileRows * row_bytes + (uint32_t)hf * kQ6Pitch : kMaskedOffset;
 #pragma unroll
@@ -107,83 +179,47 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         }
     };
 
-    // Wave w owns superblock w (half w >> 3, position w & 7 in the item); a
-    // wave past nsb converts superblock 0 (its operands are never used).
     const int sb = wv;
-    const bool active = sb < nsb;  // wave-uniform
-    const int my_half = sb >> 3;
-    const float4 xv = reinterpret_cast<const float4 *>(x)[64 * (active ? sb : 0) + lane];
-    __builtin_amdgcn_sched_barrier(0);
-    issue(0, 0);
-    float4 xr = xv;  // the conversion stays below the first item's loads
-    asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
+    const bool active = XLDS || sb < nsb;  // wave-uniform
+    const int my_par = sb >> 3;
+    float4 xr = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (!XLDS) {
+        const float4 xv = reinterpret_cast<const float4 *>(x)[64 * (active ? sb : 0) + lane];
+        __builtin_amdgcn_sched_barrier(0);
+        issue(0, 0);
+        xr = xv;  // the conversion stays below the first item's loads
+        asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
+    } else {
+        issue(0, 0);
+    }
 
-    // x operands.  A lane (m, g): plane p = m & 3 of quarter q = m >> 2 of
-    // chunk c, i.e. elements 128 (c >> 1) + 32 (c & 1) + 64 (q >> 1) + 8 g
-    // .. + 7, live when g >> 1 == q & 1 (bytes 0..7 for q < 2, 8..15
-    // otherwise).  corr[c][p] = 32 x the digit sum of plane p over this
-    // output lane's quarter g of chunk c.
-    const int n = lane & 15, g = lane >> 4, q = n >> 2, pl = n & 3;
-    const uint32_t myscr = xscr + 1024u * (uint32_t)wv;
+    // K <= 4096: wave w owns superblock w (item parity w >> 3, position
+    // w & 7 in the item); a wave past nsb converts superblock 0 (its
+    // operands are never used).  Wider K: wave w converts superblocks
+    // w, w + 16, ... into xpl.
+    const int n = lane & 15, g = lane >> 4;
     i32x4 A[4];
     int corr[4][4];
-    float xs;
-    {
+    float xs = 0.0f;
+    if constexpr (!XLDS) {
         const float v[4] = {xr.x, xr.y, xr.z, xr.w};
         uint32_t wd[4];
+        const uint32_t myscr = xscr + 1024u * (uint32_t)wv;
         xs = x_planes4(v, myscr, wd);
-        const bool live = (g >> 1) == (q & 1);
-        uint2 xa[4];
-        uint4 qs[4][4];  // [c][p]: the 16 digits of this lane's quarter
-        const uint32_t a_x = myscr + 256u * pl + 64u * (q >> 1) + 8u * g;
-        const uint32_t a_s = myscr + 64u * (g >> 1) + 16u * (g & 1);
-        asm volatile(
-            "s_waitcnt lgkmcnt(0)\n\t"
-            "ds_read_b64 %0, %20\n\t"
-            "ds_read_b64 %1, %20 offset:32\n\t"
-            "ds_read_b64 %2, %20 offset:128\n\t"
-            "ds_read_b64 %3, %20 offset:160\n\t"
-            "ds_read_b128 %4, %21\n\t"
-            "ds_read_b128 %5, %21 offset:256\n\t"
-            "ds_read_b128 %6, %21 offset:512\n\t"
-            "ds_read_b128 %7, %21 offset:768\n\t"
-            "ds_read_b128 %8, %21 offset:32\n\t"
-            "ds_read_b128 %9, %21 offset:288\n\t"
-            "ds_read_b128 %10, %21 offset:544\n\t"
-            "ds_read_b128 %11, %21 offset:800\n\t"
-            "ds_read_b128 %12, %21 offset:128\n\t"
-            "ds_read_b128 %13, %21 offset:384\n\t"
-            "ds_read_b128 %14, %21 offset:640\n\t"
-            "ds_read_b128 %15, %21 offset:896\n\t"
-            "ds_read_b128 %16, %21 offset:160\n\t"
-            "ds_read_b128 %17, %21 offset:416\n\t"
-            "ds_read_b128 %18, %21 offset:672\n\t"
-            "ds_read_b128 %19, %21 offset:928\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]), "=&v"(qs[0][0]), "=&v"(qs[0][1]),
-              "=&v"(qs[0][2]), "=&v"(qs[0][3]), "=&v"(qs[1][0]), "=&v"(qs[1][1]), "=&v"(qs[1][2]),
-              "=&v"(qs[1][3]), "=&v"(qs[2][0]), "=&v"(qs[2][1]), "=&v"(qs[2][2]), "=&v"(qs[2][3]),
-              "=&v"(qs[3][0]), "=&v"(qs[3][1]), "=&v"(qs[3][2]), "=&v"(qs[3][3])
-            : "v"(a_x), "v"(a_s)
-            : "memory");
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int lo = live ? (int)xa[c].x : 0, hi = live ? (int)xa[c].y : 0;
-            A[c] = q < 2 ? i32x4{lo, hi, 0, 0} : i32x4{0, 0, lo, hi};
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const uint4 d = qs[c][p];
-                int sum = __builtin_amdgcn_sdot4((int)d.x, 0x01010101, 0, false);
-                sum = __builtin_amdgcn_sdot4((int)d.y, 0x01010101, sum, false);
-                sum = __builtin_amdgcn_sdot4((int)d.z, 0x01010101, sum, false);
-                sum = __builtin_amdgcn_sdot4((int)d.w, 0x01010101, sum, false);
-                corr[c][p] = 32 * sum;
-            }
+        q6_x_operands(myscr, A, corr);
+    } else {
+        for (int s2 = wv; s2 < nsb; s2 += kQ6Waves) {  // uniform
+            const float4 xv2 = reinterpret_cast<const float4 *>(x)[64 * s2 + lane];
+            const float v[4] = {xv2.x, xv2.y, xv2.z, xv2.w};
+            uint32_t wd[4];
+            const float sc = x_planes4(v, (uint32_t)(uintptr_t)(lds_ptr)xpl[s2], wd);
+            if (lane == 0) xst[s2] = sc;
         }
     }
 #pragma unroll
     for (int j = 1; j < kQ6Slots - 1; j++) issue(j, j);
 
+    float acc = 0.0f;  // this wave's sum over its items of the current tile
     const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
     // This wave's superblock within a row of an item, and its dword misalignment.
     const uint32_t sb_off = (uint32_t)(sb & 7) * kQ6SbBytes;
@@ -197,16 +233,22 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         // are the only ones outstanding; the barrier makes every wave's
         // visible and ends every wave's reads of the slot refilled below.
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kQ6DmaPerWave * (kQ6Slots - 2)) : "memory");
-        const int t = it / halves, hf = it - t * halves;
-        // the previous tile's rows, once its last half is in part[]
+        const int t = it / chunks, hf = it - t * chunks;
+        // the previous tile's rows, once every wave's share is in part[]
         if (hf == 0 && t >= 1 && wv == (t - 1) % kQ6Waves && lane < 16) {
             float s = 0.0f;
-            for (int k = 0; k < nsb; k++) s += part[(t - 1) & 1][k][0][lane] + part[(t - 1) & 1][k][1][lane];
+            for (int k = 0; k < min(nsb, kQ6Waves); k++)
+                s += part[(t - 1) & 1][k][0][lane] + part[(t - 1) & 1][k][1][lane];
             const int row = (t - 1) * kQ6TileRows + lane;
             if (row < nr) yout[row] = s;
         }
         issue(slot == 0 ? kQ6Slots - 1 : slot - 1, it + kQ6Slots - 1);
-        if (active && my_half == hf) {
+        if (active && (hf & 1) == my_par) {
+            if constexpr (XLDS) {
+                const int s2 = kQ6HalfSb * hf + (sb & 7);
+                q6_x_operands((uint32_t)(uintptr_t)(lds_ptr)xpl[s2], A, corr);
+                xs = xst[s2];
+            }
             const uint32_t ab = row_al + (uint32_t)slot * kQ6Slot;
             const uint32_t aq = ab + 8u * g;
             // ql pieces (c = 0..3 at 0, 32, 64, 96), qh pieces (ip = 0, 1 at
@@ -281,17 +323,21 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
                 const float S = fmaf((float)(d2 + 256 * d3), 65536.0f, (float)(d0 + 256 * d1));
                 v = fmaf((float)scv, S, v);
             }
-            v *= d * xs;
-            // quarters g, g ^ 1 (lanes n + 16 g, xor 16): lanes 0..15 and 32..47 keep the pair sums
-            v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
-            if ((lane & 16) == 0) part[t & 1][sb][lane >> 5][n] = v;
+            acc = fmaf(v, d * xs, acc);
+            if (hf + 2 >= chunks) {  // this wave's last item of the tile
+                // quarters g, g ^ 1 (lanes n + 16 g, xor 16): lanes 0..15 and 32..47 keep the pair sums
+                acc += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(acc), 0x401F));
+                if ((lane & 16) == 0) part[t & 1][sb][lane >> 5][n] = acc;
+                acc = 0.0f;
+            }
         }
         slot = slot == kQ6Slots - 1 ? 0 : slot + 1;
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (tiles >= 1 && wv == (tiles - 1) % kQ6Waves && lane < 16) {
         float s = 0.0f;
-        for (int k = 0; k < nsb; k++) s += part[(tiles - 1) & 1][k][0][lane] + part[(tiles - 1) & 1][k][1][lane];
+        for (int k = 0; k < min(nsb, kQ6Waves); k++)
+            s += part[(tiles - 1) & 1][k][0][lane] + part[(tiles - 1) & 1][k][1][lane];
         const int row = (tiles - 1) * kQ6TileRows + lane;
         if (row < nr) yout[row] = s;
     }
@@ -304,7 +350,7 @@ bool q6k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const voi
     if (v == 1 || v == 2 || v == 4) return false;  // the fp32 kernel stays selectable
     if (cols <= 0 || cols % kQK != 0) return false;
     const int64_t nsb = cols / kQK;
-    if (nsb != 8 && nsb != 16) return false;  // one or two 8-superblock halves
+    if (nsb % kQ6HalfSb != 0 || nsb > kQ6MaxSbLds) return false;  // whole items; x fits LDS
     if (row_bytes != nsb * kQ6SbBytes || rows < 1) return false;
     if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) != 0) return false;
     return (int64_t)kQ6MaxRows * row_bytes < ((int64_t)1 << 31);
@@ -321,8 +367,13 @@ hipError_t launch_gemv_q6k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
     grid = (rows + per - 1) / per;
     per = (rows + grid - 1) / grid;
     grid = (rows + per - 1) / per;
-    hipLaunchKernelGGL(gemv_q6_k_mfma_tile_kernel, dim3((unsigned)grid), dim3(kQ6Threads), 0, stream, w, row_bytes,
-                       (int)(cols / kQK), x, y, rows, per);
+    const int nsb = (int)(cols / kQK);
+    if (nsb <= 2 * kQ6HalfSb)
+        hipLaunchKernelGGL(gemv_q6_k_mfma_tile_kernel<false>, dim3((unsigned)grid), dim3(kQ6Threads), 0, stream, w,
+                           row_bytes, nsb, x, y, rows, per);
+    else
+        hipLaunchKernelGGL(gemv_q6_k_mfma_tile_kernel<true>, dim3((unsigned)grid), dim3(kQ6Threads), 0, stream, w,
+                           row_bytes, nsb, x, y, rows, per);
     return hipGetLastError();
 }
 

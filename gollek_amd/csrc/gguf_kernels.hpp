@@ -58,8 +58,8 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
 hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
-// Q6_K on the matrix cores (gguf_gemv_q6k_mfma.hip): K = 2048 or 4096, row
-// bytes K / 256 * 210, weights and x 16-byte aligned.
+// Q6_K on the matrix cores (gguf_gemv_q6k_mfma.hip): K a multiple of 2048 up
+// to 14336, row bytes K / 256 * 210, weights and x 16-byte aligned.
 bool q6k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x);
 hipError_t launch_gemv_q6k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols, const float *x, float *y,
                                 int64_t rows, hipStream_t stream);

@@ -85,7 +85,7 @@ int32_t gollek_hip_last_status(void);
  * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
  * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
  * 0 = the matrix-core kernels (Q4_K; Q8_0, Q4_0 and Q5_K with K <= 4096;
- * Q6_K with K = 2048 or 4096), the buffer->LDS ring kernels (Q8_0, Q4_0
+ * Q6_K with K a multiple of 2048 up to 14336), the buffer->LDS ring kernels (Q8_0, Q4_0
  * otherwise) and the fp32 Q5_K / Q6_K kernel where they apply, 1 = the
  * fp32 kernels, 2 = the v_dot4 kernel (Q4_K, K <= 4096), 3 = as 0 but Q4_K
  * with K <= 4096 always on the shared-tile matrix-core kernel, 4 = as 0 but

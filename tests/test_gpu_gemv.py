@@ -137,7 +137,8 @@ def test_gemv_parity(name, type_id, rows, cols):
 
 ACCURACY_CONFIGS = [("c0_q8_0", syn.Q8_0, 4096, 4096), ("c1_q4_0", syn.Q4_0, 11008, 4096),
                     ("c2a_q4_k", syn.Q4_K, 14336, 4096), ("q4_k_k2048", syn.Q4_K, 4096, 2048),
-                    ("q5_k_4096", syn.Q5_K, 4096, 4096), ("q6_k_14336x4096", syn.Q6_K, 14336, 4096)]
+                    ("q5_k_4096", syn.Q5_K, 4096, 4096), ("q6_k_14336x4096", syn.Q6_K, 14336, 4096),
+                    ("q6_k_k14336", syn.Q6_K, 4096, 14336)]
 
 
 @pytest.mark.parametrize("name,type_id,rows,cols", ACCURACY_CONFIGS, ids=[c[0] for c in ACCURACY_CONFIGS])
@@ -411,7 +412,8 @@ def test_device_pointer_entry_points_match_host():
 K56_SHAPES = [(syn.Q5_K, 1, 256), (syn.Q5_K, 7, 768), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 33, 16384),
               (syn.Q5_K, 1003, 2304), (syn.Q5_K, 12289, 4096), (syn.Q5_K, 20000, 1024), (syn.Q6_K, 1, 256), (syn.Q6_K, 5, 768), (syn.Q6_K, 4096, 4096),
               (syn.Q6_K, 37, 16384), (syn.Q6_K, 1001, 2304), (syn.Q6_K, 14336, 4096), (syn.Q6_K, 17, 4096),
-              (syn.Q6_K, 300, 2048), (syn.Q6_K, 4113, 2048)]
+              (syn.Q6_K, 300, 2048), (syn.Q6_K, 4113, 2048), (syn.Q6_K, 4096, 14336), (syn.Q6_K, 100, 6144),
+              (syn.Q6_K, 33, 8192)]
 
 
 @pytest.mark.parametrize("type_id,rows,cols", K56_SHAPES,
@@ -429,9 +431,9 @@ def test_q5_k_q6_k_dequant_and_gemv(type_id, rows, cols):
     ref = o.matvec_fp64(type_id, data, cols, x)
     java = o.matvec(type_id, data, cols, x)
     try:
-        # Q5_K with K <= 4096 and Q6_K with K = 2048 / 4096: the matrix-core
-        # kernels (0) and the fp32 kernel (4); the others run the fp32 kernel
-        # either way.
+        # Q5_K with K <= 4096 and Q6_K with K a multiple of 2048 up to 14336:
+        # the matrix-core kernels (0) and the fp32 kernel (4); the others run
+        # the fp32 kernel either way.
         for variant in (0, 4):
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
