@@ -534,6 +534,7 @@ int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *w, const uint16_t
 
 struct MoeShape {
     int E, H, I;
+    int down_type;
 };
 
 static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_hip_weight *down,
@@ -542,10 +543,10 @@ static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_
     if (gate == nullptr || up == nullptr || down == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "expert weights");
     if (gate->type_id != GOLLEK_HIP_Q4_K || up->type_id != GOLLEK_HIP_Q4_K ||
-        down->type_id != GOLLEK_HIP_Q4_K)
+        (down->type_id != GOLLEK_HIP_Q4_K && down->type_id != GOLLEK_HIP_Q6_K))
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "Unsupported MoE expert weight types %d/%d/%d (Q4_K only)", gate->type_id,
-                    up->type_id, down->type_id);
+                    "Unsupported MoE expert weight types %d/%d/%d (Q4_K gate/up, Q4_K or Q6_K down)",
+                    gate->type_id, up->type_id, down->type_id);
     if (n_experts <= 0 || gate->rows % n_experts != 0)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Gate rows %lld are not a multiple of %lld experts",
                     (long long)gate->rows, (long long)n_experts);
@@ -562,12 +563,18 @@ static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_
     if (tokens < 0 || top_k <= 0 || tokens * top_k > (1 << 24))
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Invalid tokens %lld / top_k %lld",
                     (long long)tokens, (long long)top_k);
+    if (down->type_id == GOLLEK_HIP_Q6_K &&
+        !gollek::moe_q6k_down_supported((int)n_experts, (int)H, (int)I, (int)tokens, (int)top_k))
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "Q6_K down experts need hidden <= 2048, inter <= 1024 (multiples of 256), <= 256 "
+                    "experts, top_k <= 64 and tokens * top_k <= 2048");
     for (gollek_hip_weight *w : {gate, up, down})
         if ((reinterpret_cast<uintptr_t>(w->data) & 15u) != 0)
             return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Expert weights must be 16-byte aligned");
     shape->E = (int)n_experts;
     shape->H = (int)H;
     shape->I = (int)I;
+    shape->down_type = down->type_id;
     return GOLLEK_HIP_OK;
 }
 
@@ -592,6 +599,8 @@ int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight
     }
     if (x == nullptr || ids == nullptr || weights == nullptr || out == nullptr || workspace == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE buffers");
+    if (sh.down_type == GOLLEK_HIP_Q6_K && (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "x must be 16-byte aligned with Q6_K down experts");
     const int64_t need = gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
     if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
@@ -601,7 +610,7 @@ int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight
                                           down->row_bytes, sh.E, sh.H, sh.I, x, ids, weights,
                                           (int)tokens, (int)top_k, out,
                                           static_cast<uint8_t *>(workspace),
-                                          static_cast<hipStream_t>(stream));
+                                          static_cast<hipStream_t>(stream), sh.down_type);
     if (e != hipSuccess) return hip_fail(e, "moe launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -647,7 +656,7 @@ int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
     if (e == hipSuccess)
         e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
                                    down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
-                                   (int)top_k, d_out, d_ws, s);
+                                   (int)top_k, d_out, d_ws, s, sh.down_type);
     if (e == hipSuccess)
         e = hipMemcpyAsync(out, d_out, (size_t)(tokens * sh.H) * 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -756,6 +765,8 @@ int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *
     if (x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr || out == nullptr ||
         workspace == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE block buffers");
+    if (sh.down_type == GOLLEK_HIP_Q6_K && (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "x must be 16-byte aligned with Q6_K down experts");
     const int64_t need = gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
     if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
@@ -767,7 +778,7 @@ int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *
     if (e == hipSuccess)
         e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes, down->row_bytes,
                                    sh.E, sh.H, sh.I, x, ids, weights, (int)tokens, (int)top_k, out,
-                                   static_cast<uint8_t *>(workspace), s);
+                                   static_cast<uint8_t *>(workspace), s, sh.down_type);
     if (e != hipSuccess) return hip_fail(e, "moe block launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -817,7 +828,7 @@ int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
     if (e == hipSuccess)
         e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
                                    down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
-                                   (int)top_k, d_out, d_ws, s);
+                                   (int)top_k, d_out, d_ws, s, sh.down_type);
     if (e == hipSuccess)
         e = hipMemcpyAsync(out, d_out, (size_t)(tokens * sh.H) * 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);

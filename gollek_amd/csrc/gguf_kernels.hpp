@@ -100,11 +100,16 @@ struct MoeLayout {
 MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inter, int64_t experts);
 
 // out[T, H] = sum_j w[t,j] down_e(silu(gate_e x_t) * up_e x_t) for Q4_K stacked
-// experts; ws must hold moe_layout(...).total bytes.
+// gate / up experts and Q4_K or (down_type kQ6_K, where
+// moe_q6k_down_supported) Q6_K down experts; ws must hold
+// moe_layout(...).total bytes.
 hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                           int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                           const float *x, const int32_t *ids, const float *wts, int T, int top_k,
-                          float *out, uint8_t *ws, hipStream_t stream);
+                          float *out, uint8_t *ws, hipStream_t stream, int down_type = 12);
+// Whether the matrix-core passes can take Q6_K down experts of this shape
+// (the token-major down pass; x must also be 16-byte aligned).
+bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k);
 
 // Pieces of the MoE pipeline shared by its two implementations (gguf_moe.hip,
 // gguf_moe_mfma.hip): routing (meta layout of moe_layout; tiles0 / tiles1 =
@@ -122,7 +127,8 @@ hipError_t launch_moe_topk(const float *logits, int T, int E, int K, int sigmoid
 bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x);
 hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
                                int H, int I, const float *x, const int32_t *ids, const float *wts,
-                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);
+                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream,
+                               int down_type);
 
 }  // namespace gollek
 

@@ -321,9 +321,14 @@ hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float 
 hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                           int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                           const float *x, const int32_t *ids, const float *wts, int T, int top_k,
-                          float *out, uint8_t *ws, hipStream_t stream) {
+                          float *out, uint8_t *ws, hipStream_t stream, int down_type) {
+    if (down_type == kQ6_K) {  // the matrix-core passes only
+        if (!moe_q4k_mfma_supported(E, H, I, T * top_k, x) || !moe_q6k_down_supported(E, H, I, T, top_k))
+            return hipErrorInvalidValue;
+        return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream, down_type);
+    }
     if (tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, T * top_k, x))
-        return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream);
+        return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream, down_type);
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);

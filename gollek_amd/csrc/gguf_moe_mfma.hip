@@ -680,12 +680,17 @@ constexpr int kMdMaxWaves = 8;
 constexpr int kMdRoutes = 64;  // routes per workgroup
 constexpr int kMdSlots = 2;    // tile and route slots per wave (units in flight + 1)
 
-constexpr uint32_t md_pitch(int nsb) {  // odd 16-byte units: the 16 rows' reads spread over the banks
-    return ((nsb * kQKBlockBytes / 16) % 2 == 1) ? nsb * kQKBlockBytes : nsb * kQKBlockBytes + 16;
+constexpr int kQ6KBlockBytes = 210;
+// Down rows: Q4_K at a pitch of odd 16-byte units (the 16 rows' reads spread
+// over the banks); Q6_K (Q6) packed as stored: a 16-row tile of 210-byte
+// superblocks is one contiguous, 16-byte aligned run (16 x 210 = 3360).
+constexpr uint32_t md_row_bytes(int nsb, bool q6) { return nsb * (q6 ? kQ6KBlockBytes : kQKBlockBytes); }
+constexpr uint32_t md_pitch(int nsb, bool q6) {
+    return q6 || (md_row_bytes(nsb, false) / 16) % 2 == 1 ? md_row_bytes(nsb, q6) : md_row_bytes(nsb, q6) + 16;
 }
 // A slot's bytes move as whole kilobytes (16 bytes a lane) plus a tail of
 // 256-byte loads (4 bytes a lane), so slots take no more LDS than they hold.
-constexpr int md_tile_bytes(int nsb) { return 16 * (int)md_pitch(nsb); }
+constexpr int md_tile_bytes(int nsb, bool q6) { return 16 * (int)md_pitch(nsb, q6); }
 constexpr int md_route_bytes(int nsb) { return nsb * 16 * kRecDwords * 4; }
 constexpr int md_full(int bytes) { return bytes / 1024; }
 constexpr int md_tail(int bytes) { return (bytes % 1024 + 255) / 256; }
@@ -771,17 +776,17 @@ struct MoeDownGeom {
     uint32_t w_bytes, h_bytes;   // ranges: stacked down weights; h records
 };
 
-template <int NSB>
+template <int NSB, bool Q6>
 __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
     const uint8_t *__restrict__ down, MoeDownGeom G, const uint8_t *__restrict__ hrec,
     const int32_t *__restrict__ ids, const float *__restrict__ wts, int T, int top_k, int H, int E,
     float *__restrict__ out) {
-    constexpr uint32_t kRowBytes = NSB * kQKBlockBytes, kPitch = md_pitch(NSB);
+    constexpr uint32_t kRowBytes = md_row_bytes(NSB, Q6), kPitch = md_pitch(NSB, Q6);
     constexpr uint32_t kRecBytes = md_route_bytes(NSB);  // one route's records
-    constexpr int kTF = md_full(md_tile_bytes(NSB)), kTT = md_tail(md_tile_bytes(NSB));
+    constexpr int kTF = md_full(md_tile_bytes(NSB, Q6)), kTT = md_tail(md_tile_bytes(NSB, Q6));
     constexpr int kRF = md_full(md_route_bytes(NSB)), kRT = md_tail(md_route_bytes(NSB));
     constexpr int kUnitLoads = kTF + kTT + kRF + kRT;  // every unit issues exactly this many
-    constexpr uint32_t kTileSlot = md_slot(md_tile_bytes(NSB)), kRouteSlot = md_slot(md_route_bytes(NSB));
+    constexpr uint32_t kTileSlot = md_slot(md_tile_bytes(NSB, Q6)), kRouteSlot = md_slot(md_route_bytes(NSB));
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // sink, then waves x wave_bytes
     __shared__ float ys[kMdRoutes][16];
     __shared__ float rw[kMdRoutes];
@@ -1021,12 +1026,124 @@ __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
         if (lane < 16) lds_store_f32((uint32_t)(uintptr_t)(lds_ptr)&ys[j][lane], v);
     };
 
+    // Q6_K down rows: chunk c of a superblock (half c >> 1, part c & 1)
+    // covers elements 128 (c >> 1) + 32 (c & 1) + l and + 64 (l < 32), so A
+    // row 4 q + p reads record group 8 (c >> 1) + 2 (c & 1) + 4 (q >> 1) +
+    // (q & 1) (16 elements: the second run for q >= 2, half q & 1), and the
+    // quarter's scale is byte 8 (c >> 1) + 2 (c & 1) + 4 (g >> 1) + (g & 1)
+    // of the superblock's int8 scales.  Rows are 210 s + 16-row-aligned
+    // bytes apart, so a lane's superblock starts 0 or 2 bytes off a dword:
+    // it reads aligned dwords and realigns them (v_alignbyte_b32).  The -32
+    // offset enters as -32 times the quarter's fp32 sum of h.
+    auto compute_q6 = [&](int unit) {
+        const int j = unit & 255, ts = (unit >> 8) & 15, rs = unit >> 12;
+        const uint32_t tb = (uint32_t)(uintptr_t)(lds_ptr)(wbase + (uint32_t)ts * kTileSlot);
+        const uint32_t rb = (uint32_t)(uintptr_t)(lds_ptr)(wbase + kMdSlots * kTileSlot + (uint32_t)rs * kRouteSlot);
+        const uint32_t a_x = rb + 4 * kRecDwords * (4 * (q >> 1) + (q & 1)) + 16 * (pl < 3 ? pl : 0) + 8 * (g & 1);
+        const uint32_t a_lo0 = lo_live ? a_x : zero_lds, a_hi0 = hi_live ? a_x : zero_lds;
+        const uint32_t lo_step = lo_live ? 16u * 4 * kRecDwords : 0u, hi_step = hi_live ? 16u * 4 * kRecDwords : 0u;
+        const uint32_t a_p0 = rb + 4 * kRecDwords * (4 * hs + (g & 1)) + 48;
+        float v = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NSB; s++) {
+            const uint32_t sa = tb + (uint32_t)n * kRowBytes + (uint32_t)s * kQ6KBlockBytes;
+            const uint32_t sh = sa & 3u, ab = sa - sh, aq = ab + 8u * (uint32_t)g;
+            uint2 p01[6], s01, s23, xl[4], xh[4];
+            uint32_t p2[6], s4;
+            float2 xp[4];
+            static_assert(4 * kRecDwords * 2 == 112 && 4 * kRecDwords * 8 == 448 && 4 * kRecDwords * 10 == 560,
+                          "record offsets of chunks 1..3");
+            asm volatile(
+                "ds_read2_b32 %0, %27 offset1:1\n\t"
+                "ds_read_b32 %6, %27 offset:8\n\t"
+                "ds_read2_b32 %1, %27 offset0:8 offset1:9\n\t"
+                "ds_read_b32 %7, %27 offset:40\n\t"
+                "ds_read2_b32 %2, %27 offset0:16 offset1:17\n\t"
+                "ds_read_b32 %8, %27 offset:72\n\t"
+                "ds_read2_b32 %3, %27 offset0:24 offset1:25\n\t"
+                "ds_read_b32 %9, %27 offset:104\n\t"
+                "ds_read2_b32 %4, %27 offset0:32 offset1:33\n\t"
+                "ds_read_b32 %10, %27 offset:136\n\t"
+                "ds_read2_b32 %5, %27 offset0:40 offset1:41\n\t"
+                "ds_read_b32 %11, %27 offset:168\n\t"
+                "ds_read2_b32 %12, %28 offset0:48 offset1:49\n\t"
+                "ds_read2_b32 %13, %28 offset0:50 offset1:51\n\t"
+                "ds_read_b32 %14, %28 offset:208\n\t"
+                "ds_read_b64 %15, %29\n\t"
+                "ds_read_b64 %16, %29 offset:112\n\t"
+                "ds_read_b64 %17, %29 offset:448\n\t"
+                "ds_read_b64 %18, %29 offset:560\n\t"
+                "ds_read_b64 %19, %30\n\t"
+                "ds_read_b64 %20, %30 offset:112\n\t"
+                "ds_read_b64 %21, %30 offset:448\n\t"
+                "ds_read_b64 %22, %30 offset:560\n\t"
+                "ds_read_b64 %23, %31\n\t"
+                "ds_read_b64 %24, %31 offset:112\n\t"
+                "ds_read_b64 %25, %31 offset:448\n\t"
+                "ds_read_b64 %26, %31 offset:560\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(p01[0]), "=&v"(p01[1]), "=&v"(p01[2]), "=&v"(p01[3]), "=&v"(p01[4]), "=&v"(p01[5]),
+                  "=&v"(p2[0]), "=&v"(p2[1]), "=&v"(p2[2]), "=&v"(p2[3]), "=&v"(p2[4]), "=&v"(p2[5]), "=&v"(s01),
+                  "=&v"(s23), "=&v"(s4), "=&v"(xl[0]), "=&v"(xl[1]), "=&v"(xl[2]), "=&v"(xl[3]), "=&v"(xh[0]),
+                  "=&v"(xh[1]), "=&v"(xh[2]), "=&v"(xh[3]), "=&v"(xp[0]), "=&v"(xp[1]), "=&v"(xp[2]), "=&v"(xp[3])
+                : "v"(aq), "v"(ab), "v"(a_lo0 + s * lo_step), "v"(a_hi0 + s * hi_step),
+                  "v"(a_p0 + 16u * 4 * kRecDwords * s)
+                : "memory");
+            uint32_t ql[4][2], qh[2][2];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                ql[c][0] = __builtin_amdgcn_alignbyte(p01[c].y, p01[c].x, sh);
+                ql[c][1] = __builtin_amdgcn_alignbyte(p2[c], p01[c].y, sh);
+            }
+#pragma unroll
+            for (int ip = 0; ip < 2; ip++) {
+                qh[ip][0] = __builtin_amdgcn_alignbyte(p01[4 + ip].y, p01[4 + ip].x, sh);
+                qh[ip][1] = __builtin_amdgcn_alignbyte(p2[4 + ip], p01[4 + ip].y, sh);
+            }
+            const uint32_t s0 = __builtin_amdgcn_alignbyte(s01.y, s01.x, sh);
+            const uint32_t s1 = __builtin_amdgcn_alignbyte(s23.x, s01.y, sh);
+            const uint32_t s2 = __builtin_amdgcn_alignbyte(s23.y, s23.x, sh);
+            const uint32_t s3 = __builtin_amdgcn_alignbyte(s4, s23.y, sh);
+            const float d = half_bits_to_float_fast(s4 >> (8 * sh));
+            i32x4 D[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int ip = c >> 1, pt = c & 1;
+                uint32_t b[4];
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const uint32_t hq = qh[ip][k];
+                    b[k] = (ql[c][k] & 0x0F0F0F0Fu) | ((pt == 0 ? hq << 4 : hq << 2) & 0x30303030u);
+                    b[2 + k] = ((ql[c][k] >> 4) & 0x0F0F0F0Fu) | ((pt == 0 ? hq : hq >> 2) & 0x30303030u);
+                }
+                const i32x4 B = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+                const i32x4 A = {(int)xl[c].x, (int)xl[c].y, (int)xh[c].x, (int)xh[c].y};
+                D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero4, 0, 0, 0);
+            }
+            const uint32_t slo = hs ? s1 : s0, shi = hs ? s3 : s2;
+            float vs = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t sw = (c >> 1) ? shi : slo;
+                const float scv = (float)(int)(int8_t)((sw >> (8 * ((g & 1) + 2 * (c & 1)))) & 0xFFu);
+                const float S =
+                    (float)(int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
+                vs = fmaf(scv, fmaf(S, xp[c].x, -32.0f * xp[c].y), vs);
+            }
+            v = fmaf(d, vs, v);
+        }
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (lane < 16) lds_store_f32((uint32_t)(uintptr_t)(lds_ptr)&ys[j][lane], v);
+    };
+
     // Unit k's loads go out before unit k - (kMdSlots - 1) is computed.
     int u0 = issue_next(), u1 = kMdSlots > 2 ? issue_next() : -1;
     while (u0 >= 0) {  // uniform
         wait_vm<kUnitLoads * (kMdSlots - 2)>();  // unit u0's loads are done (later units' may not be)
         const int un = issue_next();
-        compute(u0);
+        if constexpr (Q6) compute_q6(u0);
+        else compute(u0);
         if constexpr (kMdSlots > 2) {
             u0 = u1;
             u1 = un;
@@ -1077,12 +1194,12 @@ MoeTileGeom make_geom(int mode, int E, int H, int I) {
 constexpr int kMdStaticLds = kMdRoutes * (16 * 4 + 4 + 4 + 4 + 8) + 16;  // ys, rw, rok, it_e, it_mask, counters
 constexpr int kLdsBytes = 163840;
 
-bool make_down_geom(int E, int H, int I, int T, int top_k, MoeDownGeom &g, int &waves) {
+bool make_down_geom(int E, int H, int I, int T, int top_k, bool q6, MoeDownGeom &g, int &waves) {
     const int nsb = I / kQK;
     if (nsb < 1 || nsb > 4 || top_k < 1 || top_k > kMdRoutes || H % 16 != 0) return false;
-    g.wave_bytes = (uint32_t)(kMdSlots * (md_slot(md_tile_bytes(nsb)) + md_slot(md_route_bytes(nsb))));
+    g.wave_bytes = (uint32_t)(kMdSlots * (md_slot(md_tile_bytes(nsb, q6)) + md_slot(md_route_bytes(nsb))));
     g.tg = kMdRoutes / top_k;
-    const int64_t w_bytes = (int64_t)E * H * nsb * kQKBlockBytes;
+    const int64_t w_bytes = (int64_t)E * H * md_row_bytes(nsb, q6);
     const int64_t h_bytes = (int64_t)T * top_k * (I / 16) * kRecDwords * 4;
     if (w_bytes >= (int64_t)kMaskedOffset || h_bytes >= (int64_t)kMaskedOffset) return false;
     g.w_bytes = (uint32_t)w_bytes;
@@ -1096,7 +1213,7 @@ bool make_down_geom(int E, int H, int I, int T, int top_k, MoeDownGeom &g, int &
 bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x) {
     if (H % kQK != 0 || I % kQK != 0 || H > 8 * kQK || I > 16 * kQK) return false;
     if (E > kMoMaxExperts || P > kMoMaxRoutes) return false;
-    if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return false;
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return false;  // (nullptr: shape only)
     for (int mode = 0; mode < 2; mode++) {
         const MoeTileGeom g = make_geom(mode, E, H, I);
         if (g.ndma > kMoMaxDma || g.w_bytes >= (int64_t)kMaskedOffset) return false;
@@ -1105,13 +1222,22 @@ bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x) {
     return true;
 }
 
+bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k) {
+    MoeDownGeom g;
+    int waves = 0;
+    return moe_q4k_mfma_supported(E, H, I, T * top_k, nullptr) && make_down_geom(E, H, I, T, top_k, true, g, waves);
+}
+
 // Gate/up then down: with the token-major down pass (I <= 1024) two
 // launches, h as digit records; otherwise gate/up, the expert-major down
 // pass and the combine.  Each pass routes in LDS first.  The caller has
-// checked moe_q4k_mfma_supported.
+// checked moe_q4k_mfma_supported (and, for Q6_K down rows,
+// moe_q6k_down_supported).
 hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
                                int H, int I, const float *x, const int32_t *ids, const float *wts,
-                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream) {
+                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream,
+                               int down_type) {
+    const bool q6 = down_type == kQ6_K;
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
     const MoeTileGeom g0 = make_geom(0, E, H, I), g1 = make_geom(1, E, H, I);
@@ -1120,7 +1246,7 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
     // h records (P I 3.5 bytes) fit the fp32 h region.
     MoeDownGeom gd;
     int waves = 0;
-    if (make_down_geom(E, H, I, T, top_k, gd, waves)) {
+    if (make_down_geom(E, H, I, T, top_k, q6, gd, waves)) {
         hipLaunchKernelGGL((moe_expert_tile_kernel<0, true>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
                            g0, x, top_k, ids, wts, E, P, hbuf);
         const dim3 dgrid((unsigned)(H / 16), (unsigned)((T + gd.tg - 1) / gd.tg));
@@ -1136,13 +1262,18 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
                                H, E, out);
             return hipGetLastError();
         };
-        switch (I / kQK) {
-        case 1: return run(&moe_down_combine_kernel<1>);
-        case 2: return run(&moe_down_combine_kernel<2>);
-        case 3: return run(&moe_down_combine_kernel<3>);
-        default: return run(&moe_down_combine_kernel<4>);
+        switch (I / kQK + (q6 ? 4 : 0)) {
+        case 1: return run(&moe_down_combine_kernel<1, false>);
+        case 2: return run(&moe_down_combine_kernel<2, false>);
+        case 3: return run(&moe_down_combine_kernel<3, false>);
+        case 4: return run(&moe_down_combine_kernel<4, false>);
+        case 5: return run(&moe_down_combine_kernel<1, true>);
+        case 6: return run(&moe_down_combine_kernel<2, true>);
+        case 7: return run(&moe_down_combine_kernel<3, true>);
+        default: return run(&moe_down_combine_kernel<4, true>);
         }
     }
+    if (q6) return hipErrorNotSupported;  // only the token-major down pass reads Q6_K rows
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
     hipLaunchKernelGGL((moe_expert_tile_kernel<0, false>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0,
                        x, top_k, ids, wts, E, P, hbuf);

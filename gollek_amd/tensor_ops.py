@@ -394,7 +394,8 @@ def gemm_bf16(tensor: GgufTensor, x_bf16: np.ndarray, output: np.ndarray) -> Non
 
 def moe_grouped(gate: GgufTensor, up: GgufTensor, down: GgufTensor, n_experts: int, x, ids,
                 weights) -> np.ndarray:
-    """Grouped Q4_K MoE expert FFN (the expert loop of MoeForwardPass.computeAccel,
+    """Grouped MoE expert FFN over Q4_K gate / up and Q4_K or Q6_K down experts
+    (the expert loop of MoeForwardPass.computeAccel,
     runner/safetensor/gollek-safetensor-engine/src/main/java/tech/kayys/gollek/
     safetensor/engine/generation/moe/MoeForwardPass.java:217-240): x (tokens,
     hidden) float32, ids (tokens, top_k) int32, weights (tokens, top_k) float32
@@ -466,7 +467,8 @@ def moe_select_topk(logits, top_k: int, scoring: int):
 def moe_block(gate: GgufTensor, up: GgufTensor, down: GgufTensor, n_experts: int, x, logits,
               top_k: int, scoring: int) -> np.ndarray:
     """The routed MoE block (MoeForwardPass.java:174-240 after the router
-    linear): router on `logits`, then the grouped Q4_K expert FFN."""
+    linear): router on `logits`, then the grouped expert FFN (Q4_K gate / up,
+    Q4_K or Q6_K down)."""
     for name, t in (("gate", gate), ("up", up), ("down", down)):
         if t is None:
             raise NullPointerError(name)

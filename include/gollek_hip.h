@@ -159,7 +159,9 @@ int32_t gollek_hip_matvec_rows(gollek_hip_weight *weight, const float *x, int64_
 int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t x_len,
                              int64_t m, float *y, int64_t y_len, char *err, size_t err_len);
 
-/* Grouped MoE expert FFN over Q4_K expert weights stacked as GGUF stores them:
+/* Grouped MoE expert FFN over Q4_K gate / up and Q4_K or Q6_K down expert
+ * weights (Q4_K_M files store some layers' ffn_down_exps as Q6_K), stacked
+ * as GGUF stores them:
  * gate and up have n_experts * inter rows of `hidden` columns, down has
  * n_experts * hidden rows of `inter` columns.  For each token t (x row-major
  * tokens x hidden) and route j < top_k (ids / weights row-major tokens x
@@ -169,8 +171,10 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, 
  * route) expert loop of runner/safetensor/gollek-safetensor-engine/src/main/
  * java/tech/kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:
  * 217-240 with :461-472 (swigluFfn: .../engine/forward/
- * DirectForwardFfnService.java:40-61), reading each used expert once.  Weight
- * types other than Q4_K, or hidden / inter above 4096 -> UNSUPPORTED. */
+ * DirectForwardFfnService.java:40-61), reading each used expert once.  Other
+ * weight types, hidden / inter above 4096, or Q6_K down experts beyond
+ * hidden 2048 / inter 1024 / 256 experts / top_k 64 / 2048 routes ->
+ * UNSUPPORTED. */
 int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
                                gollek_hip_weight *down, int64_t n_experts, const float *x,
                                int64_t tokens, const int32_t *ids, const float *weights,

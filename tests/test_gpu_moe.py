@@ -20,13 +20,13 @@ def _init():
     ops.init(0)
 
 
-def _experts(E, H, I, seed):
+def _experts(E, H, I, seed, down_type=syn.Q4_K):
     gate = syn.q4_k_matrix(E * I, H, seed)
     up = syn.q4_k_matrix(E * I, H, seed + 1)
-    down = syn.q4_k_matrix(E * H, I, seed + 2)
+    down = syn.matrix(down_type, E * H, I, seed + 2)
     tg = ops.GgufTensor("blk.0.ffn_gate_exps.weight", (H, I, E), syn.Q4_K, gate.reshape(-1))
     tu = ops.GgufTensor("blk.0.ffn_up_exps.weight", (H, I, E), syn.Q4_K, up.reshape(-1))
-    td = ops.GgufTensor("blk.0.ffn_down_exps.weight", (I, H, E), syn.Q4_K, down.reshape(-1))
+    td = ops.GgufTensor("blk.0.ffn_down_exps.weight", (I, H, E), down_type, down.reshape(-1))
     return gate, up, down, tg, tu, td
 
 
@@ -51,6 +51,38 @@ def test_moe_parity(E, H, I, T, k):
     assert err <= MOE_TOL
     for t in (tg, tu, td):
         t.close()
+
+
+# Q4_K_M files store some layers' ffn_down_exps as Q6_K: the token-major
+# down pass reads them (inter 256 .. 1024; odd rows start 2 bytes off a
+# dword, so every tile takes the realigned reads).
+@pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
+                                       (128, 2048, 768, 16, 8), (32, 512, 1024, 40, 2)])
+def test_moe_q6_k_down_parity(E, H, I, T, k):
+    print(f"[gpu] moe q6_k down E={E} H={H} I={I} T={T} k={k}", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + 1, down_type=syn.Q6_K)
+    ids, w = syn.moe_routing(T, E, k, seed=5)
+    x = syn.activation(T * H, seed=6).reshape(T, H)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=syn.Q6_K)
+    err = o.rel_err(out, ref)
+    print(f"[gpu] moe q6_k down rel_err={err:.3e}", flush=True)
+    assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+def test_moe_q6_k_down_rejects_unsupported_shapes():
+    # Q6_K down experts run only on the token-major down pass: inter above
+    # 1024 or hidden above 2048 -> UNSUPPORTED; Q5_K down is not taken.
+    for (E, H, I, dt) in [(4, 512, 1280, syn.Q6_K), (4, 4096, 256, syn.Q6_K), (4, 512, 256, syn.Q5_K)]:
+        gate, up, down, tg, tu, td = _experts(E, H, I, seed=1, down_type=dt)
+        x = syn.activation(2 * H, seed=2).reshape(2, H)
+        ids, w = syn.moe_routing(2, E, 2, seed=3)
+        with pytest.raises(ops.UnsupportedOperationError):
+            ops.moe_grouped(tg, tu, td, E, x, ids, w)
+        for t in (tg, tu, td):
+            t.close()
 
 
 @pytest.fixture

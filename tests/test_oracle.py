@@ -161,6 +161,24 @@ def test_planted_mistakes_fail_the_fixtures(golden, kind):
     assert caught, kind
 
 
+def test_moe_reference_q6_k_down_matches_dense():
+    # Q6_K down experts: the packed reference dequantizes them as Q6_K (the
+    # dequantization is pinned by the reference's Q6_K fixtures) and equals
+    # the dense reference on those rows; read as Q4_K bytes they would not.
+    E, H, I, T, k = 3, 256, 512, 2, 2
+    gate = syn.q4_k_matrix(E * I, H, 11)
+    up = syn.q4_k_matrix(E * I, H, 12)
+    down = syn.q6_k_matrix(E * H, I, 13)
+    ids, w = syn.moe_routing(T, E, k, 14)
+    x = syn.activation(T * H, 15).reshape(T, H)
+    packed = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=syn.Q6_K)
+    dense = o.moe_reference(o.dequantize(12, gate, H).reshape(E, I, H).astype(np.float64),
+                            o.dequantize(12, up, H).reshape(E, I, H).astype(np.float64),
+                            o.dequantize(syn.Q6_K, down, I).reshape(E, H, I).astype(np.float64),
+                            x, ids, w)
+    assert np.allclose(packed, dense, rtol=1e-12, atol=1e-12)
+
+
 def test_moe_reference_paths_agree_and_properties():
     # The packed-expert reference equals the dense one on the same dequantized
     # weights; the output is linear in the route weights; route order within a
