@@ -7,7 +7,9 @@ Weights rotate over enough copies (>= 512 MiB) that the 256 MB Infinity Cache
 cannot hold them, so every step streams its matrix from HBM.  Inputs are
 resident in HBM before the timed region; launches are replayed from a captured
 HIP graph on the launch stream, and HIP events on that stream bracket exactly
-the timed launches.
+the timed launches.  GEMV weights carry their prepared mat-vec layout
+(gollek_hip_weight_prepare, built once before timing, the same byte count);
+the headline matrix is also timed on the GGUF bytes in place.
 
 Secondary lines (in "extra"): the other GEMV configurations, the Q8_0 bf16
 MFMA GEMM (M = 16 / 128 / 512; TFLOP/s at M = 512 is the metric's second
@@ -72,13 +74,21 @@ def parse() -> argparse.Namespace:
 class Rotation:
     """Device copies of one packed weight matrix, launched round robin."""
 
-    def __init__(self, torch, host_bytes, type_id: int, rows: int, cols: int):
+    def __init__(self, torch, host_bytes, type_id: int, rows: int, cols: int, prepared: bool = False):
         from gollek_amd import tensor_ops as ops
         nbytes = host_bytes.size
         self.copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
         base = torch.from_numpy(host_bytes.reshape(-1)).cuda()
         self.buffers = [base] + [base.clone() for _ in range(self.copies - 1)]
         self.weights = [ops.DeviceWeight(type_id, b.data_ptr(), rows, cols) for b in self.buffers]
+        if prepared:
+            # Each copy's prepared mat-vec layout (gollek_hip_weight_prepare,
+            # built once like a model-load step, outside any timed region; a
+            # no-op for shapes without one): launches then stream the copy's
+            # prepared bytes, as many as the GGUF bytes.
+            for w in self.weights:
+                w.prepare()
+            torch.cuda.synchronize()
         self.nbytes = nbytes
 
     def close(self):
@@ -159,10 +169,11 @@ def graph_time(torch, launch, copies: int, steps: int, warmup: int):
 
 # ---- workloads ----------------------------------------------------------------
 
-def gemv_workload(torch, type_id: int, rows: int, cols: int, steps: int, warmup: int, seed: int):
+def gemv_workload(torch, type_id: int, rows: int, cols: int, steps: int, warmup: int, seed: int,
+                  prepared: bool = True):
     from gollek_amd import synthetic as syn
     host = syn.matrix(type_id, rows, cols, seed)
-    rot = Rotation(torch, host, type_id, rows, cols)
+    rot = Rotation(torch, host, type_id, rows, cols, prepared)
     x = torch.from_numpy(syn.activation(cols, seed + 1)).cuda()
     y = torch.empty(rows, dtype=torch.float32, device="cuda")
 
@@ -172,7 +183,7 @@ def gemv_workload(torch, type_id: int, rows: int, cols: int, steps: int, warmup:
     ms, n = graph_time(torch, launch, rot.copies, steps, warmup)
     algo_bytes = rot.nbytes + 4 * cols + 4 * rows
     res = {
-        "ms_per_step": ms, "steps": n, "weight_copies": rot.copies,
+        "ms_per_step": ms, "steps": n, "weight_copies": rot.copies, "prepared_layout": prepared,
         "weight_bytes": int(rot.nbytes), "algo_bytes": int(algo_bytes),
         "weight_gbs": rot.nbytes / (ms * 1e-3) / 1e9,
         "algo_gbs": algo_bytes / (ms * 1e-3) / 1e9,
@@ -587,6 +598,13 @@ def main() -> int:
             r, hosts[name] = gemv_workload(torch, t, rows, cols, args.steps, args.warmup, seed=5)
             r["hbm_frac"] = r["weight_gbs"] / HBM_PEAK_GBS
             extra[name] = r
+        if want("q4_k_gemv_4096x14336_gguf_layout"):
+            # The headline matrix without its prepared layout: the column
+            # kernel reading the GGUF rows in place.
+            log("extra headline on the GGUF layout")
+            r, _ = gemv_workload(torch, syn.Q4_K, 14336, 4096, args.steps, args.warmup, seed=2, prepared=False)
+            r["hbm_frac"] = r["weight_gbs"] / HBM_PEAK_GBS
+            extra["q4_k_gemv_4096x14336_gguf_layout"] = r
         have_gemm = hasattr(ops.DeviceWeight, "gemm_bf16") and _has_symbol("gollek_hip_gemm_bf16_device")
         for m in (16, 128, 512):
             name = f"q8_0_gemm_bf16_m{m}_4096x4096"
@@ -650,6 +668,7 @@ def main() -> int:
             "workload": "q4_k_gemv_m1_k4096_n14336",
             "type": "Q4_K", "m": 1, "k": 4096, "n": 14336,
             "weight_bytes": head["weight_bytes"], "weight_copies": head["weight_copies"],
+            "prepared_layout": head["prepared_layout"],
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         },
         "roofline": {

@@ -29,6 +29,8 @@ struct gollek_hip_weight {
     size_t staging_bytes = 0;
     float *gemm_ws = nullptr;      // split-K partial tiles of the device GEMM entry
     size_t gemm_ws_bytes = 0;
+    uint8_t *prep = nullptr;       // prepared column layout (gollek_hip_weight_prepare)
+    int64_t prep_rows = 0;         // its rows per workgroup
 };
 
 namespace {
@@ -284,8 +286,49 @@ void gollek_hip_weight_free(gollek_hip_weight *w) {
     if (w->owned && w->data != nullptr) (void)hipFree(w->data);
     if (w->staging != nullptr) (void)hipFree(w->staging);
     if (w->gemm_ws != nullptr) (void)hipFree(w->gemm_ws);
+    if (w->prep != nullptr) (void)hipFree(w->prep);
     if (w->stream != nullptr) (void)hipStreamDestroy(w->stream);
     delete w;
+}
+
+int32_t gollek_hip_weight_prepare(gollek_hip_weight *w, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    std::lock_guard<std::mutex> lock(w->mu);
+    int32_t rc = use_device(w->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    // Only shapes the column kernel takes for a full mat-vec have a layout.
+    const int64_t per = gollek::col_layout_rows(w->type_id, w->rows, w->cols);
+    const bool takes = per > 0 && (gollek::q32_mfma_supported(w->type_id, w->row_bytes, w->cols, w->rows, w->data,
+                                                              nullptr) ||
+                                   (w->type_id == GOLLEK_HIP_Q4_K &&
+                                    gollek::q4k_mfma_supported(w->row_bytes, w->cols, w->rows, w->data, nullptr)));
+    if (!takes || (w->prep != nullptr && w->prep_rows == per)) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    if (w->prep != nullptr) {
+        (void)hipStreamSynchronize(w->stream);
+        (void)hipFree(w->prep);
+        w->prep = nullptr;
+        w->prep_rows = 0;
+    }
+    uint8_t *p = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&p), (size_t)(w->rows * w->row_bytes));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(GOLLEK_HIP_ERR_NOMEM, err, err_len, "prepared layout of %lld bytes",
+                    (long long)(w->rows * w->row_bytes));
+    }
+    e = gollek::launch_prepare_col_layout(w->type_id, w->data, p, w->rows, w->row_bytes, per, w->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return hip_fail(e, "prepare", err, err_len);
+    }
+    w->prep = p;
+    w->prep_rows = per;
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
 }
 
 int32_t gollek_hip_weight_info(const gollek_hip_weight *w, int32_t *type_id, int64_t *rows,
@@ -343,9 +386,11 @@ static int32_t matvec_host(gollek_hip_weight *w, const uint8_t *rows_base, int64
     float *d_y = reinterpret_cast<float *>(w->staging + x_bytes);
     hipError_t e = hipMemcpyAsync(d_x, x, (size_t)w->cols * sizeof(float), hipMemcpyHostToDevice,
                                   w->stream);
+    // the prepared layout covers full mat-vecs only (its partition depends on the row count)
+    const bool full = rows_base == w->data && nrows == w->rows;
     if (e == hipSuccess)
         e = gollek::launch_gemv(w->type_id, rows_base, w->row_bytes, w->cols, d_x, d_y, nrows,
-                                w->stream);
+                                w->stream, full ? w->prep : nullptr, full ? w->prep_rows : 0);
     if (e == hipSuccess) e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "matvec", err, err_len);
@@ -412,8 +457,10 @@ int32_t gollek_hip_matvec_device(gollek_hip_weight *w, const float *x, float *y,
     if (row_count < 0 || row_count > w->rows)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Requested row count %lld is outside tensor rows %lld",
                     (long long)row_count, (long long)w->rows);
+    const bool full = row_count == w->rows;  // the prepared layout covers full mat-vecs only
     hipError_t e = gollek::launch_gemv(w->type_id, w->data, w->row_bytes, w->cols, x, y, row_count,
-                                       static_cast<hipStream_t>(stream));
+                                       static_cast<hipStream_t>(stream), full ? w->prep : nullptr,
+                                       full ? w->prep_rows : 0);
     if (e != hipSuccess) return hip_fail(e, "matvec launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;

@@ -509,16 +509,17 @@ const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, cons
 }
 
 hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
-                       const float *x, float *y, int64_t rows, hipStream_t stream) {
+                       const float *x, float *y, int64_t rows, hipStream_t stream,
+                       const uint8_t *prep, int64_t prep_rows) {
     if (rows <= 0) return hipSuccess;
     if (q32_mfma_supported(type_id, row_bytes, cols, rows, w, x))
-        return launch_gemv_q32_mfma(type_id, w, row_bytes, cols, x, y, rows, stream);
+        return launch_gemv_q32_mfma(type_id, w, row_bytes, cols, x, y, rows, stream, prep, prep_rows);
     if (type_id == kQ6_K && q6k_mfma_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q6k_mfma(w, row_bytes, cols, x, y, rows, stream);
     if (is_k56(type_id) && gemv_k56_supported(type_id, row_bytes, w, x))
         return launch_gemv_k56(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, rows, w, x))
-        return launch_gemv_q4k_mfma(w, row_bytes, cols, x, y, rows, stream);
+        return launch_gemv_q4k_mfma(w, row_bytes, cols, x, y, rows, stream, prep, prep_rows);
     if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q4k_dot4(w, row_bytes, cols, x, y, rows, stream);
     if (gemv_ring_supported(type_id, row_bytes, cols, rows, w, x))

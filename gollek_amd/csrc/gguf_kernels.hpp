@@ -37,9 +37,20 @@ inline int device_cus() {
 hipError_t launch_dequant(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                           int64_t row0, int64_t nrows, float *out, hipStream_t stream);
 
-// y[r] = sum_k W[r, k] * x[k] for r < rows.
+// y[r] = sum_k W[r, k] * x[k] for r < rows.  prep: the matrix's prepared
+// column layout for prep_rows rows per workgroup (launch_prepare_col_layout),
+// used when the column kernel takes the shape with that partition.
 hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
-                       const float *x, float *y, int64_t rows, hipStream_t stream);
+                       const float *x, float *y, int64_t rows, hipStream_t stream,
+                       const uint8_t *prep = nullptr, int64_t prep_rows = 0);
+
+// The column kernel's partition of a full mat-vec (rows per workgroup; 0
+// when the column kernel does not take the shape) and the prepared layout
+// for it: every workgroup's block of rows stored superblock column by
+// column (same bytes; gguf_gemv_mfma.hip).
+int64_t col_layout_rows(int type_id, int64_t rows, int64_t cols);
+hipError_t launch_prepare_col_layout(int type_id, const uint8_t *raw, uint8_t *prep, int64_t rows,
+                                     int64_t row_bytes, int64_t per, hipStream_t stream);
 
 // Q4_K GEMV on the matrix cores (gguf_gemv_mfma.hip).
 // Q8_0 / Q4_0 GEMV through per-wave buffer->LDS rings (gguf_gemv_ring.hip).
@@ -50,13 +61,15 @@ hipError_t launch_gemv_ring(int type_id, const uint8_t *w, int64_t row_bytes, in
 bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x);
 hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols,
-                                const float *x, float *y, int64_t rows, hipStream_t stream);
+                                const float *x, float *y, int64_t rows, hipStream_t stream,
+                                const uint8_t *prep = nullptr, int64_t prep_rows = 0);
 // Q4_0 / Q8_0 / Q5_K on the matrix cores (gguf_gemv_mfma.hip, the column
 // kernel): K a multiple of 256 up to 4096, any row count.
 bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x);
 hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
-                                const float *x, float *y, int64_t rows, hipStream_t stream);
+                                const float *x, float *y, int64_t rows, hipStream_t stream,
+                                const uint8_t *prep = nullptr, int64_t prep_rows = 0);
 
 // Q6_K on the matrix cores (gguf_gemv_q6k_mfma.hip): K a multiple of 2048 up
 // to 14336, row bytes K / 256 * 210, weights and x 16-byte aligned.

@@ -49,8 +49,11 @@ import java.util.WeakHashMap;
  * library multiplies (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K).  Otherwise the try
  * methods return false and the Java routes run unchanged.  A tensor's bytes
  * (GgufTensorData.tensorData, a slice of the model's mapped segment) are
- * copied to the device once, at its first use, and the device handle lives
- * until release(model).</p>
+ * copied to the device once, at its first use, its prepared mat-vec layout
+ * is built then unless gollek.hip.prepare is "false" (the reference's
+ * auto_prepare at model load, core/plugin/gollek-plugin-runner-gguf/.../
+ * JavaNativeGgufBackend.java:157-180), and
+ * the device handle lives until release(model).</p>
  *
  * <p>Status codes map back to the exceptions the Java route throws
  * (RT/GgufMatVec.java:32-35, 65-71, 196-200; RT/GgufRowDot.java:77-82;
@@ -162,6 +165,16 @@ final class GgufHipMatVec {
                     check(b.lastStatus(), err);
                     throw new IllegalStateException("gollek_hip_weight_upload returned no handle");
                 }
+                // The prepared mat-vec layout, built once like the reference's prepared
+                // matrices (gollek.gguf.java_native.auto_prepare); without device memory
+                // for it the handle keeps reading the GGUF bytes.
+                if (!"false".equals(System.getProperty("gollek.hip.prepare", "true"))) {
+                    int rc = b.weightPrepare(w, err, (long) ERR_LEN);
+                    if (rc != OK && rc != ERR_NOMEM) {
+                        b.weightFree(w);
+                        check(rc, err);
+                    }
+                }
             }
             perModel.put(tensor, w);
             return w;
@@ -192,6 +205,7 @@ final class GgufHipMatVec {
         private final MethodHandle lastStatus;
         private final MethodHandle weightUpload;
         private final MethodHandle weightFree;
+        private final MethodHandle weightPrepare;
         private final MethodHandle matvecRows;
         private final MethodHandle dotRow;
         private final MethodHandle dequantizeRows;
@@ -251,6 +265,9 @@ final class GgufHipMatVec {
                             ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
             this.weightFree = downcall(linker, lookup, "gollek_hip_weight_free",
                     FunctionDescriptor.ofVoid(ValueLayout.ADDRESS), false);
+            this.weightPrepare = downcall(linker, lookup, "gollek_hip_weight_prepare",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
             // The float[] arguments are passed as heap segments: critical downcalls with heap access.
             this.matvecRows = downcall(linker, lookup, "gollek_hip_matvec_rows",
                     FunctionDescriptor.of(ValueLayout.JAVA_INT,
@@ -310,6 +327,14 @@ final class GgufHipMatVec {
         void weightFree(MemorySegment weight) {
             try {
                 weightFree.invokeExact(weight);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int weightPrepare(MemorySegment weight, MemorySegment err, long errLen) {
+            try {
+                return (int) weightPrepare.invokeExact(weight, err, errLen);
             } catch (Throwable t) {
                 throw propagate(t);
             }

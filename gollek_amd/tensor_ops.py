@@ -129,6 +129,12 @@ class GgufTensor:
             self._handle = h
         return self._handle
 
+    def prepare(self) -> None:
+        """Build the handle's prepared mat-vec layout (gollek_hip_weight_prepare;
+        the reference builds its prepared matrices at model load)."""
+        err = _native.ErrBuf()
+        check(_native.load().gollek_hip_weight_prepare(self.handle(), err.buf, err.size), err)
+
     def close(self) -> None:
         if self._handle is not None:
             _native.load().gollek_hip_weight_free(self._handle)
@@ -336,6 +342,11 @@ class DeviceWeight:
         if not h:
             raise _BY_CODE.get(lib.gollek_hip_last_status(), GgufHipError)(err.text)
         self.handle = h
+
+    def prepare(self) -> None:
+        """Build the handle's prepared mat-vec layout (gollek_hip_weight_prepare)."""
+        err = _native.ErrBuf()
+        check(_native.load().gollek_hip_weight_prepare(self.handle, err.buf, err.size), err)
 
     def close(self) -> None:
         if self.handle:

@@ -114,6 +114,20 @@ gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *de
                                                  int64_t row_bytes, char *err,
                                                  size_t err_len);
 
+/* Build the handle's prepared mat-vec layout: a second device copy of the
+ * matrix in which every workgroup's block of rows is stored superblock
+ * column by column, the order the matrix-core column kernel reads (Q4_K,
+ * Q8_0, Q4_0 and Q5_K with K <= 4096 and at most 64 rows per CU; measured
+ * 7.8 us against 8.8 us for Q4_K 14336 x 4096).  Later full mat-vecs
+ * (row_count == rows) on the handle read it; every other entry point keeps
+ * reading the GGUF bytes.  The layout follows the device's CU count and
+ * gemv_variant at the time of the call; a no-op (OK) for other shapes.
+ * Replaces the reference's prepared-matrix build at model load
+ * (RT/GgufPreparedMatrixStore.java:120-127 via PRG/JavaNativeGgufBackend
+ * .java:157-180), which likewise keeps a prepared copy beside the raw
+ * bytes.  Freed with the handle.  Device memory exhausted -> NOMEM. */
+int32_t gollek_hip_weight_prepare(gollek_hip_weight *weight, char *err, size_t err_len);
+
 /* Release a handle (device memory it owns, its stream and staging buffers).
  * Replaces clearPreparedMatrixCaches on backend close
  * (PRG/JavaNativeGgufBackend.java:139-143).  NULL is ignored. */

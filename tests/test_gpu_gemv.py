@@ -407,6 +407,69 @@ def test_device_pointer_entry_points_match_host():
         host_t.close()
 
 
+# Column-kernel shapes (K <= 4096, at most 64 / 48 / 32 rows per CU for
+# Q4_K and Q4_0 / Q5_K / Q8_0, the last two capped by more workgroups), a
+# ragged one, and shapes with no prepared layout (too many rows per CU, Q6_K,
+# K > 4096) where prepare() is a no-op.
+PREP_SHAPES = [(syn.Q4_K, 14336, 4096), (syn.Q4_K, 1001, 2304), (syn.Q4_K, 4000, 256),
+               (syn.Q8_0, 4096, 4096), (syn.Q8_0, 9000, 1024), (syn.Q4_0, 11008, 4096),
+               (syn.Q5_K, 4096, 4096), (syn.Q5_K, 12289, 4096), (syn.Q4_K, 16385, 4096),
+               (syn.Q6_K, 4096, 4096), (syn.Q4_K, 33, 8192)]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", PREP_SHAPES,
+                         ids=[f"type{t}_{r}x{c}" for t, r, c in PREP_SHAPES])
+def test_prepared_layout_matches_gguf_bytes(type_id, rows, cols):
+    # The prepared copy holds the same pieces in the column kernel's read
+    # order, so a full mat-vec reading it is bit-identical to one reading the
+    # GGUF bytes; row prefixes keep reading the GGUF bytes.
+    import torch
+    print(f"[gpu] prepared layout type={type_id} {rows}x{cols}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=50 + rows + type_id)
+    x = syn.activation(cols, seed=51)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    t = _tensor(type_id, data, cols)
+    y_raw = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y_raw)
+    assert o.rel_err(y_raw, ref) <= GEMV_TOL
+    t.prepare()
+    t.prepare()  # idempotent
+    y_prep = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y_prep)
+    assert np.array_equal(y_prep, y_raw)
+    part = np.full(rows, -3.0, np.float32)
+    ops.mat_vec_rows(t, x, part, rows - 1, True)
+    assert np.array_equal(part[:rows - 1], y_raw[:rows - 1]) and part[-1] == -3.0
+    try:
+        # Q4_K variant 3 (shared tiles) and the fp32 / ring variants do not
+        # read the layout; back at 0 the layout is used again.
+        for variant in (3, 4, 0):
+            ops.set_option("gemv_variant", variant)
+            y = np.zeros(rows, np.float32)
+            ops.mat_vec(t, x, y)
+            assert o.rel_err(y, ref) <= GEMV_TOL, variant
+        assert np.array_equal(y, y_raw)
+    finally:
+        ops.set_option("gemv_variant", 0)
+    t.close()
+
+    w_dev = torch.from_numpy(data.reshape(-1)).cuda()
+    x_dev = torch.from_numpy(x).cuda()
+    y_dev = torch.full((rows,), -7.0, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    dw = ops.DeviceWeight(type_id, w_dev.data_ptr(), rows, cols)
+    dw.prepare()
+    dw.matvec(x_dev.data_ptr(), y_dev.data_ptr(), rows, stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(y_dev.cpu().numpy(), y_raw)
+    y_dev.fill_(-7.0)
+    dw.matvec(x_dev.data_ptr(), y_dev.data_ptr(), rows // 2, stream)
+    torch.cuda.synchronize()
+    got = y_dev.cpu().numpy()
+    assert np.array_equal(got[:rows // 2], y_raw[:rows // 2]) and np.all(got[rows // 2:] == -7.0)
+    dw.close()
+
+
 # ---- Q5_K / Q6_K -----------------------------------------------------------
 
 K56_SHAPES = [(syn.Q5_K, 1, 256), (syn.Q5_K, 7, 768), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 33, 16384),

@@ -91,6 +91,7 @@ WRAPPERS = {  # typed wrapper -> the symbol whose handle it invokes
     "lastStatus": "gollek_hip_last_status",
     "weightUpload": "gollek_hip_weight_upload",
     "weightFree": "gollek_hip_weight_free",
+    "weightPrepare": "gollek_hip_weight_prepare",
     "matvecRows": "gollek_hip_matvec_rows",
     "dotRow": "gollek_hip_dot_row",
     "dequantizeRows": "gollek_hip_dequantize_rows",
