@@ -609,7 +609,14 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
 // flight per wave, 9.1 / 9.3 us; a shared-tile ring with one barrier per
 // tile, 9.0 us; the whole share issued up front with per-tile barriers,
 // 9.8 us (its waves only finish issuing after 3-5 us, so every tile's work
-// lands after the stream); this kernel, 8.9 us.
+// lands after the stream); this kernel, 8.9 us.  Again on the prepared
+// layout (this kernel 7.9 us): every load up front 8.2 us, two tiles ahead
+// 8.2 us, waves 8..15 (or 12..15) issuing their whole column at once
+// 8.5 (8.2) us, two or four columns per wave (8 or 4 waves) 8.2 / 10.5 us.
+// A timestamp trace shows why the tail is what it is: a workgroup's waves
+// start in groups of four (one per SIMD) about 0.1, 0.5, 1.1 and 2.1 us
+// after its first, also with no load in flight (a barrier before the first
+// load), so the last group's four paced round trips end the stream.
 namespace {
 
 constexpr int kColWaves = 16;
