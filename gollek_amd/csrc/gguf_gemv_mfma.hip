@@ -10,7 +10,7 @@
 //
 // Three kernels, by shape:
 //   * K <= 4096, at most 64 rows per CU (the 8B-class FFN shapes):
-//     gemv_q4_k_mfma_col_kernel, one superblock column per wave, the
+//     gemv_mfma_col_kernel, one superblock column per wave, the
 //     workgroup's share in LDS;
 //   * K <= 4096, more rows (lm_head): gemv_q4_k_mfma_tile_kernel, 16-row
 //     tiles streamed through a shared ring;
@@ -621,13 +621,12 @@ namespace {
 
 constexpr int kColWaves = 16;
 constexpr int kColThreads = kColWaves * 64;
-// x scratch of the wave's superblock (four digit planes), later the wave's
-// row sums (2 floats a row).
+// x scratch of the wave (four digit planes of a superblock).
 constexpr int kColX = 1024;
 
-// A wave's column: NL loads of 1 KB, the rows' PB-byte pieces (Q4_K, Q4_0:
-// a 144-byte superblock or eight blocks; Q8_0: eight 34-byte blocks, 272
-// bytes) packed at a PB-byte pitch.
+// A column's region: the rows' PB-byte pieces (Q4_K, Q4_0: a 144-byte
+// superblock or eight blocks; Q5_K: 176 bytes; Q8_0: eight 34-byte blocks,
+// 272 bytes) packed at a PB-byte pitch in up to 9 KB, then kColX.
 template <int TYPE>
 struct ColGeom {
     static constexpr int PB = TYPE == kQ8_0 ? 8 * kQ8BlockBytes : TYPE == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
@@ -637,13 +636,7 @@ struct ColGeom {
     static constexpr int kMaxTiles = kW / (kTileRows * PB);  // whole tiles only
     static constexpr int kMaxRows = kMaxTiles * kTileRows;   // 64 (Q5_K: 48, Q8_0: 32)
     static constexpr int kTileBytes = kTileRows * PB;
-    // Last load of tile t: tile t is bytes [16 PB t, 16 PB (t + 1)).
-    static constexpr int last_load(int t) {
-        const int e = (kTileBytes * (t + 1) + 1023) / 1024 - 1;
-        return e < NL - 1 ? e : NL - 1;
-    }
-    static_assert(kMaxTiles >= 2 && kMaxTiles <= 4, "the kernel unrolls up to four tiles");
-    static_assert(2 * 4 * kMaxTiles * kTileRows <= kColX, "row sums fit the x scratch");
+    static_assert(kMaxTiles >= 2 && kMaxTiles <= 4, "up to four tiles");
 };
 
 }  // namespace
@@ -654,109 +647,124 @@ struct ColGeom {
 // is one contiguous run of its rows' pieces; the same bytes otherwise.
 // Measured on MI355X (Q4_K 14336 x 4096): 7.8 us against 8.8 us reading the
 // GGUF rows, whose columns are 144-byte pieces 2304 bytes apart.
+//
+// Tiles.  Each 16-row tile of a column is moved by its own loads (1 KB
+// loads, then 256-byte tails of 4 bytes a lane: 2304 = 2 KB + 256, 2816 =
+// 2 KB + 3 x 256, 4352 = 4 KB + 256), so a tile's wait covers exactly its
+// bytes, and its row sums go to the first 128 bytes of the tile in LDS once
+// it has been read (pair h of row n at float 2 n + h).  Measured against
+// 1 KB loads spanning tile boundaries with the row sums in the x scratch:
+// Q4_K 14336 x 4096 7.7 against 7.9 us, Q4_0 11008 x 4096 7.4 against
+// 7.9 us, Q8_0 4096 x 4096 5.33 against 5.40 us (Q5_K 4.98 against
+// 4.92 us: its 768-byte tail takes three loads).
+// Also measured and dropped: the first four waves taking the last tile of
+// columns 12..15 (whose waves start ~2 us later), 8.2 us.
 template <int TYPE, bool PREP>
 __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int rows_per_wg) {
     using G = ColGeom<TYPE>;
-    constexpr int NL = G::NL;
     constexpr int PB = G::PB;
+    constexpr int TB = G::kTileBytes;
+    constexpr int kFull = TB / 1024;          // 1 KB loads per tile
+    constexpr int kTail = (TB % 1024) / 256;  // 256-byte tail loads per tile
+    static_assert(TB % 256 == 0 && PB % 16 == 0, "tiles are whole loads");
     __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * G::kRegion];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
     const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kMaxRows
     const uint32_t row_bytes = (uint32_t)row_bytes64;
-    const uint32_t wbase = (uint32_t)(uintptr_t)(lds_ptr)(lds + wv * G::kRegion);
-    const uint32_t xbase = wbase + G::kW;
-
-    // Waves past nsb own no column: they convert superblock 0's x and issue
-    // only masked loads (an empty descriptor), so every wave runs the same
-    // loads and barriers.
-    const bool active = wv < nsb;  // wave-uniform
-    const int sb = active ? wv : 0;
-    const float4 xv = reinterpret_cast<const float4 *>(x)[64 * sb + lane];
-    __builtin_amdgcn_sched_barrier(0);
-    // Load k of a wave moves bytes 1024 k + 16 lane of its column, i.e. row
-    // b / PB, byte b % PB of the row's piece; rows past nr read zeros.  The
-    // descriptor starts at the column, so the last row's piece ends at
-    // (nr - 1) row_bytes + PB <= nr row_bytes - PB wv.
-    // PREP: the column is nr PB-byte pieces from w + r0 row_bytes + nr PB sb.
-    const __amdgpu_buffer_rsrc_t rs =
-        PREP ? wave_buffer(w + r0 * row_bytes64 + (int64_t)nr * PB * sb, active ? (uint32_t)(nr * PB) : 0u)
-             : wave_buffer(w + r0 * row_bytes64 + PB * sb, active ? (uint32_t)nr * row_bytes - PB * wv : 0u);
-    uint32_t off[NL];
-#pragma unroll
-    for (int k = 0; k < NL; k++) {
-        const uint32_t b = 1024u * k + 16u * lane;
-        const uint32_t r = b / PB, col = b - r * PB;
-        off[k] = r < (uint32_t)nr ? (PREP ? b : r * row_bytes + col) : kMaskedOffset;
-    }
-    auto issue = [&](int k) { col_load(rs, lds + wv * G::kRegion + 1024 * k, off[k]); };
     const int tiles = (nr + kTileRows - 1) / kTileRows;
-#pragma unroll
-    for (int k = 0; k <= G::last_load(0); k++) issue(k);
-    __builtin_amdgcn_sched_barrier(0);
-    float4 xr = xv;  // the conversion stays below the tile loads
-    asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
-    XOps4 xo;
-    int ps[4][4];
-    if constexpr (TYPE == kQ4_0)
-        x_operands4<true>(xr, xbase, xo, ps);
-    else
-        x_operands4(xr, xbase, xo);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)lds;
 
-    const int n = lane & 15, g = lane >> 4;
-    // Q4_K: header and quant addresses of row n; Q4_0 / Q8_0: quant and
-    // scale addresses of row n's piece (see read_tile_piece32).
-    const uint32_t a_h = wbase + n * PB;
-    const uint32_t a_q = TYPE == kQ4_K ? a_h + 16 + 8 * g : a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
-    const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
-    auto tile = [&](auto T) {
-        constexpr int t = decltype(T)::value;
-        wait_vm<0>();
-        if constexpr (t + 1 < G::kMaxTiles) {
-            if (t + 1 < tiles) {
+    if (wv < nsb) {  // wave-uniform; waves past nsb own no column
+        // The column's rows: nr PB-byte pieces (PREP: contiguous from
+        // w + r0 row_bytes + nr PB wv; otherwise row r's piece at r row_bytes
+        // from w + r0 row_bytes + PB wv, the descriptor ending at the last
+        // row's piece: (nr - 1) row_bytes + PB <= nr row_bytes - PB wv).
+        const __amdgpu_buffer_rsrc_t rs =
+            PREP ? wave_buffer(w + r0 * row_bytes64 + (int64_t)nr * PB * wv, (uint32_t)(nr * PB))
+                 : wave_buffer(w + r0 * row_bytes64 + PB * wv, (uint32_t)nr * row_bytes - PB * wv);
+        // Byte b of a column: row b / PB, byte b % PB of the row's piece;
+        // rows past nr read as zeros.
+        auto offset = [&](uint32_t b) {
+            const uint32_t r = b / PB, col = b - r * PB;
+            return r < (uint32_t)nr ? (PREP ? b : r * row_bytes + col) : kMaskedOffset;
+        };
+        uint8_t *const region = lds + wv * G::kRegion;
+        auto issue = [&](int t) {
+            const uint32_t tb = (uint32_t)(TB * t);
 #pragma unroll
-                for (int k = G::last_load(t) + 1; k <= G::last_load(t + 1); k++) issue(k);
+            for (int j = 0; j < kFull; j++) {
+                const uint32_t o = offset(tb + 1024u * j + 16u * lane);  // a named local for the builtin
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(region + tb + 1024 * j), 16, o, 0, 0,
+                                                         kStreamLoad);
             }
-        }
-        if (active) {
+#pragma unroll
+            for (int j = 0; j < kTail; j++) {
+                const uint32_t o = offset(tb + 1024u * kFull + 256u * j + 4u * lane);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(region + tb + 1024 * kFull + 256 * j), 4, o,
+                                                         0, 0, kStreamLoad);
+            }
+        };
+
+        // x first, then tile 0, then the digit planes while it flies.  Pacing:
+        // each next tile is issued once the previous one has arrived (see
+        // above).
+        const float4 xv = reinterpret_cast<const float4 *>(x)[64 * wv + lane];
+        __builtin_amdgcn_sched_barrier(0);
+        issue(0);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t rbase = lds0 + wv * G::kRegion;
+        XOps4 xo;
+        int ps[4][4];
+        float4 xr = xv;  // the conversion stays below the tile's loads
+        asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
+        if constexpr (TYPE == kQ4_0)
+            x_operands4<true>(xr, rbase + G::kW, xo, ps);
+        else
+            x_operands4(xr, rbase + G::kW, xo);
+
+        const int n = lane & 15, g = lane >> 4;
+        for (int t = 0; t < tiles; t++) {
+            wait_vm<0>();
+            if (t + 1 < tiles) issue(t + 1);
+            // Row n's piece of the tile: Q4_K header and quants; Q4_0 / Q8_0
+            // quants and scales (see read_tile_piece32).
+            const uint32_t a_t = rbase + TB * t;
+            const uint32_t a_h = a_t + n * PB;
             float v;
             if constexpr (TYPE == kQ4_K) {
                 u32x4 hv;
                 uint2 q[4];
-                read_tile_superblock(a_h + G::kTileBytes * t, a_q + G::kTileBytes * t, hv, q);
+                read_tile_superblock(a_h, a_h + 16 + 8 * g, hv, q);
                 v = q4k_tile_superblock4(hv, q, xo);
             } else if constexpr (TYPE == kQ5_K) {
                 u32x4 hv;
                 uint2 qh, q[4];
-                read_tile_superblock5(a_h + G::kTileBytes * t, a_h + 16 + 8 * g + G::kTileBytes * t,
-                                      a_h + 48 + 8 * g + G::kTileBytes * t, hv, qh, q);
+                read_tile_superblock5(a_h, a_h + 16 + 8 * g, a_h + 48 + 8 * g, hv, qh, q);
                 v = q4k_tile_superblock4<true>(hv, q, xo, qh);
             } else {
                 uint32_t raw[20], dh[4];
-                read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(
-                    a_q + G::kTileBytes * t, a_d + G::kTileBytes * t, raw, dh);
+                const uint32_t a_q = a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
+                const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
+                read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(a_q, a_d, raw, dh);
                 v = q32_tile_piece<TYPE>(raw, dh, xo, ps);
             }
-            // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until
-            // the row sums (pair h of row r at float 2 r + h)
-            if (lane < 32) lds_store_f32(xbase + 8 * (16 * t + n) + 4 * g, v);
+            // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until the
+            // row sums; the tile has been read (read_* wait for their reads)
+            if (lane < 32) lds_store_f32(a_t + 8 * n + 4 * g, v);
         }
-    };
-    tile(std::integral_constant<int, 0>{});
-    if constexpr (G::kMaxTiles > 1) if (tiles > 1) tile(std::integral_constant<int, 1>{});
-    if constexpr (G::kMaxTiles > 2) if (tiles > 2) tile(std::integral_constant<int, 2>{});
-    if constexpr (G::kMaxTiles > 3) if (tiles > 3) tile(std::integral_constant<int, 3>{});
+    }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // Row sums in superblock order.
     for (int r = threadIdx.x; r < nr; r += kColThreads) {
+        const int off = TB * (r >> 4) + 8 * (r & 15);
         float2 p[kColWaves];
 #pragma unroll
         for (int k = 0; k < kColWaves; k++)
-            p[k] = k < nsb ? *reinterpret_cast<const float2 *>(lds + k * G::kRegion + G::kW + 8 * r)
-                           : make_float2(0.0f, 0.0f);
+            p[k] = k < nsb ? *reinterpret_cast<const float2 *>(lds + k * G::kRegion + off) : make_float2(0.0f, 0.0f);
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < kColWaves; k++) s += p[k].x + p[k].y;
