@@ -124,9 +124,66 @@ __device__ __forceinline__ void q6_x_operands(uint32_t planes, i32x4 (&A)[4], in
     }
 }
 
+// K > 4096: the digit sums of one superblock, for q6_x_operands_sums.  wd[p]
+// = this lane's four digits of plane p (x_planes4; lane l holds elements
+// 4 l .. 4 l + 3), so group G = l >> 2 of 16 elements is a quad: quarter g
+// of chunk c with G = 8 (c >> 1) + 2 (c & 1) + 4 (g >> 1) + (g & 1).  The
+// sums (|.| <= 16 x 128) go to sums + 2 (16 g + 4 c + p) as int16.
+__device__ __forceinline__ void q6_digit_sums(const uint32_t (&wd)[4], uint32_t sums) {
+    const int lane = threadIdx.x & 63;
+    int gs[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        int t = __builtin_amdgcn_sdot4((int)wd[p], 0x01010101, 0, false);
+        t += dpp_i<0xB1>(t);  // quad_perm [1,0,3,2]
+        t += dpp_i<0x4E>(t);  // quad_perm [2,3,0,1]
+        gs[p] = t;
+    }
+    const int G = lane >> 2;
+    const int c = 2 * (G >> 3) + ((G >> 1) & 1), g = 2 * ((G >> 2) & 1) + (G & 1);
+    const uint32_t lo = ((uint32_t)gs[0] & 0xFFFFu) | ((uint32_t)gs[1] << 16);
+    const uint32_t hi = ((uint32_t)gs[2] & 0xFFFFu) | ((uint32_t)gs[3] << 16);
+    if ((lane & 3) == 0)
+        asm volatile("ds_write_b64 %0, %1" : : "v"(sums + 8u * (uint32_t)(4 * g + c)), "v"(uint2{lo, hi}) : "memory");
+}
+
+// K > 4096: q6_x_operands with the digit sums read from q6_digit_sums'
+// table instead of summed from the planes.
+__device__ __forceinline__ void q6_x_operands_sums(uint32_t planes, uint32_t sums, i32x4 (&A)[4],
+                                                   int (&corr)[4][4]) {
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15, g = lane >> 4, q = n >> 2, pl = n & 3;
+    const bool live = (g >> 1) == (q & 1);
+    uint2 xa[4];
+    uint4 sv[2];  // int16 sums [c][p] of this lane's quarter g
+    asm volatile(
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "ds_read_b64 %0, %6\n\t"
+        "ds_read_b64 %1, %6 offset:32\n\t"
+        "ds_read_b64 %2, %6 offset:128\n\t"
+        "ds_read_b64 %3, %6 offset:160\n\t"
+        "ds_read_b128 %4, %7\n\t"
+        "ds_read_b128 %5, %7 offset:16\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]), "=&v"(sv[0]), "=&v"(sv[1])
+        : "v"(planes + 256u * pl + 64u * (q >> 1) + 8u * g), "v"(sums + 32u * g)
+        : "memory");
+    const uint32_t sw[8] = {sv[0].x, sv[0].y, sv[0].z, sv[0].w, sv[1].x, sv[1].y, sv[1].z, sv[1].w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int lo = live ? (int)xa[c].x : 0, hi = live ? (int)xa[c].y : 0;
+        A[c] = q < 2 ? i32x4{lo, hi, 0, 0} : i32x4{0, 0, lo, hi};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t w2 = sw[2 * c + (p >> 1)];
+            corr[c][p] = 32 * (int)(int16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xFFFFu));
+        }
+    }
+}
+
 }  // namespace
 
-// XLDS: K > 4096, x's planes for every superblock in LDS.
+// XLDS: K > 4096, x's planes and digit sums for every superblock in LDS.
 template <bool XLDS>
 __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
@@ -139,6 +196,7 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     __shared__ float yout[kQ6MaxRows];
     __shared__ __attribute__((aligned(16))) uint8_t xpl[XLDS ? kQ6MaxSbLds : 1][1024];  // XLDS: x's planes
     __shared__ float xst[XLDS ? kQ6MaxSbLds : 1];                                      // XLDS: x's scales
+    __shared__ __attribute__((aligned(16))) int16_t xds[XLDS ? kQ6MaxSbLds : 1][64];   // XLDS: digit sums
     // K <= 4096: each wave's x scratch (four digit planes, 1 KB) is kilobyte
     // w of the last ring slot, which the loop first refills after every wave
     // has read its operands back.
@@ -183,6 +241,8 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     const bool active = XLDS || sb < nsb;  // wave-uniform
     const int my_par = sb >> 3;
     float4 xr = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int kXl = (kQ6MaxSbLds + kQ6Waves - 1) / kQ6Waves;  // x superblocks per wave (XLDS)
+    float4 xq[XLDS ? kXl : 1];
     if constexpr (!XLDS) {
         const float4 xv = reinterpret_cast<const float4 *>(x)[64 * (active ? sb : 0) + lane];
         __builtin_amdgcn_sched_barrier(0);
@@ -190,7 +250,18 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         xr = xv;  // the conversion stays below the first item's loads
         asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
     } else {
-        issue(0, 0);
+        // Every x superblock of the wave first (w, w + 16, ...; past nsb the
+        // last one again, unused), then the ring's first items: one round
+        // trip for all of them instead of one per superblock.
+#pragma unroll
+        for (int i = 0; i < kXl; i++) {
+            const int s2 = wv + kQ6Waves * i;
+            xq[i] = reinterpret_cast<const float4 *>(x)[64 * (s2 < nsb ? s2 : nsb - 1) + lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < kQ6Slots - 1; j++) issue(j, j);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // K <= 4096: wave w owns superblock w (item parity w >> 3, position
@@ -208,16 +279,22 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         xs = x_planes4(v, myscr, wd);
         q6_x_operands(myscr, A, corr);
     } else {
-        for (int s2 = wv; s2 < nsb; s2 += kQ6Waves) {  // uniform
-            const float4 xv2 = reinterpret_cast<const float4 *>(x)[64 * s2 + lane];
-            const float v[4] = {xv2.x, xv2.y, xv2.z, xv2.w};
-            uint32_t wd[4];
-            const float sc = x_planes4(v, (uint32_t)(uintptr_t)(lds_ptr)xpl[s2], wd);
-            if (lane == 0) xst[s2] = sc;
+#pragma unroll
+        for (int i = 0; i < kXl; i++) {
+            const int s2 = wv + kQ6Waves * i;
+            if (s2 < nsb) {  // uniform
+                const float v[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
+                uint32_t wd[4];
+                const float sc = x_planes4(v, (uint32_t)(uintptr_t)(lds_ptr)xpl[s2], wd);
+                if (lane == 0) xst[s2] = sc;
+                q6_digit_sums(wd, (uint32_t)(uintptr_t)(lds_ptr)xds[s2]);
+            }
         }
     }
+    if constexpr (!XLDS) {
 #pragma unroll
-    for (int j = 1; j < kQ6Slots - 1; j++) issue(j, j);
+        for (int j = 1; j < kQ6Slots - 1; j++) issue(j, j);
+    }
 
     float acc = 0.0f;  // this wave's sum over its items of the current tile
     const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
@@ -246,7 +323,8 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         if (active && (hf & 1) == my_par) {
             if constexpr (XLDS) {
                 const int s2 = kQ6HalfSb * hf + (sb & 7);
-                q6_x_operands((uint32_t)(uintptr_t)(lds_ptr)xpl[s2], A, corr);
+                q6_x_operands_sums((uint32_t)(uintptr_t)(lds_ptr)xpl[s2], (uint32_t)(uintptr_t)(lds_ptr)xds[s2],
+                                   A, corr);
                 xs = xst[s2];
             }
             const uint32_t ab = row_al + (uint32_t)slot * kQ6Slot;
