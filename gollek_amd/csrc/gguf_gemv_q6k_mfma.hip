@@ -124,11 +124,14 @@ __device__ __forceinline__ void q6_x_operands(uint32_t planes, i32x4 (&A)[4], in
     }
 }
 
-// K > 4096: the digit sums of one superblock, for q6_x_operands_sums.  wd[p]
-// = this lane's four digits of plane p (x_planes4; lane l holds elements
-// 4 l .. 4 l + 3), so group G = l >> 2 of 16 elements is a quad: quarter g
-// of chunk c with G = 8 (c >> 1) + 2 (c & 1) + 4 (g >> 1) + (g & 1).  The
-// sums (|.| <= 16 x 128) go to sums + 2 (16 g + 4 c + p) as int16.
+// K > 4096: the -32 corrections of one superblock, for q6_x_operands_sums.
+// wd[p] = this lane's four digits of plane p (x_planes4; lane l holds
+// elements 4 l .. 4 l + 3), so group G = l >> 2 of 16 elements is a quad:
+// quarter g of chunk c with G = 8 (c >> 1) + 2 (c & 1) + 4 (g >> 1) + (g &
+// 1).  With s_p its digit sum of plane p (|s_p| <= 16 x 128), the pair
+// {32 (s0 + 256 s1), 32 (s2 + 256 s3)} (|.| < 2^24) goes to sums + 8 (4 g
+// + c): what the plane pairs (D0 + 256 D1, D2 + 256 D3) of a chunk lose to
+// the -32 offset.
 __device__ __forceinline__ void q6_digit_sums(const uint32_t (&wd)[4], uint32_t sums) {
     const int lane = threadIdx.x & 63;
     int gs[4];
@@ -141,44 +144,49 @@ __device__ __forceinline__ void q6_digit_sums(const uint32_t (&wd)[4], uint32_t 
     }
     const int G = lane >> 2;
     const int c = 2 * (G >> 3) + ((G >> 1) & 1), g = 2 * ((G >> 2) & 1) + (G & 1);
-    const uint32_t lo = ((uint32_t)gs[0] & 0xFFFFu) | ((uint32_t)gs[1] << 16);
-    const uint32_t hi = ((uint32_t)gs[2] & 0xFFFFu) | ((uint32_t)gs[3] << 16);
+    const uint32_t lo = (uint32_t)(32 * (gs[0] + 256 * gs[1]));
+    const uint32_t hi = (uint32_t)(32 * (gs[2] + 256 * gs[3]));
     if ((lane & 3) == 0)
         asm volatile("ds_write_b64 %0, %1" : : "v"(sums + 8u * (uint32_t)(4 * g + c)), "v"(uint2{lo, hi}) : "memory");
 }
 
-// K > 4096: q6_x_operands with the digit sums read from q6_digit_sums'
-// table instead of summed from the planes.
-__device__ __forceinline__ void q6_x_operands_sums(uint32_t planes, uint32_t sums, i32x4 (&A)[4],
-                                                   int (&corr)[4][4]) {
-    const int lane = threadIdx.x & 63;
-    const int n = lane & 15, g = lane >> 4, q = n >> 2, pl = n & 3;
-    const bool live = (g >> 1) == (q & 1);
-    uint2 xa[4];
-    uint4 sv[2];  // int16 sums [c][p] of this lane's quarter g
+// K > 4096: one superblock's operands from its planes and q6_digit_sums'
+// table.  a01 / a23: this lane's A bytes in the planes (plane base +
+// 256 p + 64 (q >> 1) + 8 g) for the lanes whose A row is live in dwords
+// 0, 1 (q < 2) / 2, 3 (q >= 2), a zeroed block otherwise, so the halves of A
+// need no selects; cc[c] = the chunk's two corrections for quarter g.
+__device__ __forceinline__ void q6_x_operands_sums(uint32_t a01, uint32_t a23, uint32_t sums, i32x4 (&A)[4],
+                                                   int (&cc)[4][2]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    uint2 x01[4], x23[4];
+    uint4 sv[2];
     asm volatile(
         "s_waitcnt lgkmcnt(0)\n\t"
-        "ds_read_b64 %0, %6\n\t"
-        "ds_read_b64 %1, %6 offset:32\n\t"
-        "ds_read_b64 %2, %6 offset:128\n\t"
-        "ds_read_b64 %3, %6 offset:160\n\t"
-        "ds_read_b128 %4, %7\n\t"
-        "ds_read_b128 %5, %7 offset:16\n\t"
+        "ds_read_b64 %0, %10\n\t"
+        "ds_read_b64 %1, %10 offset:32\n\t"
+        "ds_read_b64 %2, %10 offset:128\n\t"
+        "ds_read_b64 %3, %10 offset:160\n\t"
+        "ds_read_b64 %4, %11\n\t"
+        "ds_read_b64 %5, %11 offset:32\n\t"
+        "ds_read_b64 %6, %11 offset:128\n\t"
+        "ds_read_b64 %7, %11 offset:160\n\t"
+        "ds_read_b128 %8, %12\n\t"
+        "ds_read_b128 %9, %12 offset:16\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]), "=&v"(sv[0]), "=&v"(sv[1])
-        : "v"(planes + 256u * pl + 64u * (q >> 1) + 8u * g), "v"(sums + 32u * g)
+        : "=&v"(x01[0]), "=&v"(x01[1]), "=&v"(x01[2]), "=&v"(x01[3]), "=&v"(x23[0]), "=&v"(x23[1]),
+          "=&v"(x23[2]), "=&v"(x23[3]), "=&v"(sv[0]), "=&v"(sv[1])
+        : "v"(a01), "v"(a23), "v"(sums + 32u * g)
         : "memory");
-    const uint32_t sw[8] = {sv[0].x, sv[0].y, sv[0].z, sv[0].w, sv[1].x, sv[1].y, sv[1].z, sv[1].w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int lo = live ? (int)xa[c].x : 0, hi = live ? (int)xa[c].y : 0;
-        A[c] = q < 2 ? i32x4{lo, hi, 0, 0} : i32x4{0, 0, lo, hi};
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const uint32_t w2 = sw[2 * c + (p >> 1)];
-            corr[c][p] = 32 * (int)(int16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xFFFFu));
-        }
-    }
+    for (int c = 0; c < 4; c++) A[c] = i32x4{(int)x01[c].x, (int)x01[c].y, (int)x23[c].x, (int)x23[c].y};
+    cc[0][0] = (int)sv[0].x;
+    cc[0][1] = (int)sv[0].y;
+    cc[1][0] = (int)sv[0].z;
+    cc[1][1] = (int)sv[0].w;
+    cc[2][0] = (int)sv[1].x;
+    cc[2][1] = (int)sv[1].y;
+    cc[3][0] = (int)sv[1].z;
+    cc[3][1] = (int)sv[1].w;
 }
 
 }  // namespace
@@ -196,7 +204,8 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     __shared__ float yout[kQ6MaxRows];
     __shared__ __attribute__((aligned(16))) uint8_t xpl[XLDS ? kQ6MaxSbLds : 1][1024];  // XLDS: x's planes
     __shared__ float xst[XLDS ? kQ6MaxSbLds : 1];                                      // XLDS: x's scales
-    __shared__ __attribute__((aligned(16))) int16_t xds[XLDS ? kQ6MaxSbLds : 1][64];   // XLDS: digit sums
+    __shared__ __attribute__((aligned(16))) int32_t xds[XLDS ? kQ6MaxSbLds : 1][32];   // XLDS: corrections
+    __shared__ __attribute__((aligned(16))) uint32_t zpad[XLDS ? 64 : 1];              // XLDS: zeros for A
     // K <= 4096: each wave's x scratch (four digit planes, 1 KB) is kilobyte
     // w of the last ring slot, which the loop first refills after every wave
     // has read its operands back.
@@ -270,15 +279,22 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     // w, w + 16, ... into xpl.
     const int n = lane & 15, g = lane >> 4;
     i32x4 A[4];
-    int corr[4][4];
+    int cc[4][2];  // per chunk: the corrections of (D0 + 256 D1, D2 + 256 D3)
     float xs = 0.0f;
     if constexpr (!XLDS) {
         const float v[4] = {xr.x, xr.y, xr.z, xr.w};
         uint32_t wd[4];
         const uint32_t myscr = xscr + 1024u * (uint32_t)wv;
         xs = x_planes4(v, myscr, wd);
+        int corr[4][4];
         q6_x_operands(myscr, A, corr);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            cc[c][0] = corr[c][0] + 256 * corr[c][1];
+            cc[c][1] = corr[c][2] + 256 * corr[c][3];
+        }
     } else {
+        if (wv == 0) zpad[lane] = 0u;  // published by the first item's barrier
 #pragma unroll
         for (int i = 0; i < kXl; i++) {
             const int s2 = wv + kQ6Waves * i;
@@ -303,6 +319,12 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
     const uint32_t sh = sb_off & 3u;  // 0 or 2
     const uint32_t row_al = ring_base + (uint32_t)n * kQ6Pitch + (sb_off & ~3u);
     const int hs = g >> 1, hh = g & 1;  // output quarter: run hs, half hh
+    // XLDS: this lane's A bytes within a superblock's planes, and which half
+    // of A they fill (none for the lanes whose row is dead in its run)
+    const int aq = n >> 2;
+    const bool live_a = (g >> 1) == (aq & 1);
+    const uint32_t a_off = 256u * (uint32_t)(n & 3) + 64u * (uint32_t)(aq >> 1) + 8u * (uint32_t)g;
+    const uint32_t zaddr = (uint32_t)(uintptr_t)(lds_ptr)zpad;
     const i32x4 zero4 = {0, 0, 0, 0};
     int slot = 0;
     for (int it = 0; it < items; it++) {
@@ -323,8 +345,9 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
         if (active && (hf & 1) == my_par) {
             if constexpr (XLDS) {
                 const int s2 = kQ6HalfSb * hf + (sb & 7);
-                q6_x_operands_sums((uint32_t)(uintptr_t)(lds_ptr)xpl[s2], (uint32_t)(uintptr_t)(lds_ptr)xds[s2],
-                                   A, corr);
+                const uint32_t pa = (uint32_t)(uintptr_t)(lds_ptr)xpl[s2] + a_off;
+                q6_x_operands_sums(live_a && aq < 2 ? pa : zaddr, live_a && aq >= 2 ? pa : zaddr,
+                                   (uint32_t)(uintptr_t)(lds_ptr)xds[s2], A, cc);
                 xs = xst[s2];
             }
             const uint32_t ab = row_al + (uint32_t)slot * kQ6Slot;
@@ -396,9 +419,10 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
             for (int c = 0; c < 4; c++) {
                 const uint32_t sw = (c >> 1) ? shi : slo;
                 const int scv = (int)(int8_t)((sw >> (8 * (hh + 2 * (c & 1)))) & 0xFFu);
-                const int d0 = D[c][0] - corr[c][0], d1 = D[c][1] - corr[c][1];
-                const int d2 = D[c][2] - corr[c][2], d3 = D[c][3] - corr[c][3];
-                const float S = fmaf((float)(d2 + 256 * d3), 65536.0f, (float)(d0 + 256 * d1));
+                // exact in int32: |D_p| <= 64 x 63 x 128, |cc| < 2^24
+                const int lo = D[c][0] + 256 * D[c][1] - cc[c][0];
+                const int hi = D[c][2] + 256 * D[c][3] - cc[c][1];
+                const float S = fmaf((float)hi, 65536.0f, (float)lo);
                 v = fmaf((float)scv, S, v);
             }
             acc = fmaf(v, d * xs, acc);
