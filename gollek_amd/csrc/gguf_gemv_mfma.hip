@@ -613,10 +613,11 @@ __global__ __launch_bounds__(kT2Threads) void gemv_q4_k_mfma_tile_kernel(
 // layout (this kernel 7.9 us): every load up front 8.2 us, two tiles ahead
 // 8.2 us, waves 8..15 (or 12..15) issuing their whole column at once
 // 8.5 (8.2) us, two or four columns per wave (8 or 4 waves) 8.2 / 10.5 us.
-// A timestamp trace shows why the tail is what it is: a workgroup's waves
-// start in groups of four (one per SIMD) about 0.1, 0.5, 1.1 and 2.1 us
-// after its first, also with no load in flight (a barrier before the first
-// load), so the last group's four paced round trips end the stream.
+// A realtime-stamped copy (tile-aligned loads, 7.7 us) shows the waves all
+// starting within 0.5 us and their tiles returning in groups of four (one
+// wave per SIMD at a time, the order their loads were accepted): median
+// last-tile arrival 4.3, 4.8, 5.3 and 6.2 us for waves 0..3, 4..7, 8..11,
+// 12..15; the CU takes in ~22 B/ns meanwhile.
 namespace {
 
 constexpr int kColWaves = 16;
@@ -658,7 +659,7 @@ struct ColGeom {
 // 7.9 us, Q8_0 4096 x 4096 5.33 against 5.40 us (Q5_K 4.98 against
 // 4.92 us: its 768-byte tail takes three loads).
 // Also measured and dropped: the first four waves taking the last tile of
-// columns 12..15 (whose waves start ~2 us later), 8.2 us.
+// columns 12..15 (whose tiles arrive last), 8.2 us.
 template <int TYPE, bool PREP>
 __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
