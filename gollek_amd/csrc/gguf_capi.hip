@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <cstring>
 #include <mutex>
 #include <new>
 #include <string>
@@ -31,6 +32,8 @@ struct gollek_hip_weight {
     size_t gemm_ws_bytes = 0;
     uint8_t *prep = nullptr;       // prepared column layout (gollek_hip_weight_prepare)
     int64_t prep_rows = 0;         // its rows per workgroup
+    uint8_t *hstage = nullptr;     // pinned host staging for host x / y / dst
+    size_t hstage_bytes = 0;
 };
 
 namespace {
@@ -160,6 +163,30 @@ int32_t check_shape(int32_t type_id, int64_t rows, int64_t cols, int64_t row_byt
     return GOLLEK_HIP_OK;
 }
 
+// Host buffers (a Java float[], a numpy array) are pageable; copies through
+// page-locked staging run as plain DMA.  Up to kHostStageMax bytes per
+// handle (grown on demand, freed with the handle); larger transfers copy
+// from the caller's memory directly.  Every host entry point synchronizes
+// its stream before returning, so a buffer is never regrown under a copy.
+constexpr size_t kHostStageMax = (size_t)16 << 20;
+
+uint8_t *host_staging(gollek_hip_weight *w, size_t bytes) {
+    if (bytes > kHostStageMax) return nullptr;
+    if (w->hstage_bytes >= bytes) return w->hstage;
+    if (w->hstage != nullptr) (void)hipHostFree(w->hstage);
+    w->hstage = nullptr;
+    w->hstage_bytes = 0;
+    const size_t want = bytes < ((size_t)64 << 10) ? ((size_t)64 << 10) : bytes;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;  // the direct copies still work
+    }
+    w->hstage = static_cast<uint8_t *>(p);
+    w->hstage_bytes = want;
+    return w->hstage;
+}
+
 int32_t ensure_staging(gollek_hip_weight *w, size_t bytes, char *err, size_t err_len) {
     if (w->staging_bytes >= bytes) return GOLLEK_HIP_OK;
     if (w->staging != nullptr) {
@@ -287,6 +314,7 @@ void gollek_hip_weight_free(gollek_hip_weight *w) {
     if (w->staging != nullptr) (void)hipFree(w->staging);
     if (w->gemm_ws != nullptr) (void)hipFree(w->gemm_ws);
     if (w->prep != nullptr) (void)hipFree(w->prep);
+    if (w->hstage != nullptr) (void)hipHostFree(w->hstage);
     if (w->stream != nullptr) (void)hipStreamDestroy(w->stream);
     delete w;
 }
@@ -364,11 +392,14 @@ int32_t gollek_hip_dequantize_rows(gollek_hip_weight *w, int64_t row0, int64_t n
     rc = ensure_staging(w, bytes, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     float *d_out = reinterpret_cast<float *>(w->staging);
+    uint8_t *hs = host_staging(w, bytes);
     hipError_t e = gollek::launch_dequant(w->type_id, w->data, w->row_bytes, w->cols, row0, nrows,
                                           d_out, w->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(dst, d_out, bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(hs ? (void *)hs : (void *)dst, d_out, bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "dequantize", err, err_len);
+    if (hs != nullptr) std::memcpy(dst, hs, bytes);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }
@@ -384,16 +415,22 @@ static int32_t matvec_host(gollek_hip_weight *w, const uint8_t *rows_base, int64
     if (rc != GOLLEK_HIP_OK) return rc;
     float *d_x = reinterpret_cast<float *>(w->staging);
     float *d_y = reinterpret_cast<float *>(w->staging + x_bytes);
-    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)w->cols * sizeof(float), hipMemcpyHostToDevice,
-                                  w->stream);
+    const size_t xn = (size_t)w->cols * sizeof(float);
+    uint8_t *hs = host_staging(w, x_bytes + y_bytes);
+    if (hs != nullptr) std::memcpy(hs, x, xn);
+    hipError_t e =
+        hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
     // the prepared layout covers full mat-vecs only (its partition depends on the row count)
     const bool full = rows_base == w->data && nrows == w->rows;
     if (e == hipSuccess)
         e = gollek::launch_gemv(w->type_id, rows_base, w->row_bytes, w->cols, d_x, d_y, nrows,
                                 w->stream, full ? w->prep : nullptr, full ? w->prep_rows : 0);
-    if (e == hipSuccess) e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(hs ? (void *)(hs + x_bytes) : (void *)y, d_y, y_bytes, hipMemcpyDeviceToHost,
+                           w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "matvec", err, err_len);
+    if (hs != nullptr) std::memcpy(y, hs + x_bytes, y_bytes);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }
@@ -506,14 +543,20 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     uint16_t *d_x = reinterpret_cast<uint16_t *>(w->staging);
     float *d_y = reinterpret_cast<float *>(w->staging + x_bytes);
     float *d_ws = ws_bytes ? reinterpret_cast<float *>(w->staging + ws_off) : nullptr;
-    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)(m * w->cols) * sizeof(uint16_t),
-                                  hipMemcpyHostToDevice, w->stream);
+    const size_t xn = (size_t)(m * w->cols) * sizeof(uint16_t);
+    uint8_t *hs = host_staging(w, x_bytes + y_bytes);
+    if (hs != nullptr) std::memcpy(hs, x, xn);
+    hipError_t e =
+        hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
     if (e == hipSuccess)
         e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, d_x, d_y, (int)m, (int)w->rows,
                                           (int)w->cols, w->stream, d_ws, ws_bytes);
-    if (e == hipSuccess) e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(hs ? (void *)(hs + x_bytes) : (void *)y, d_y, y_bytes, hipMemcpyDeviceToHost,
+                           w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "gemm", err, err_len);
+    if (hs != nullptr) std::memcpy(y, hs + x_bytes, y_bytes);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }
