@@ -591,7 +591,8 @@ def main() -> int:
                                     ("q4_k_gemv_4096x128256", syn.Q4_K, 128256, 4096),
                                     ("q6_k_gemv_14336x4096", syn.Q6_K, 4096, 14336),
                                     ("q6_k_gemv_4096x128256", syn.Q6_K, 128256, 4096),
-                                    ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, 4096)):
+                                    ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, 4096),
+                                    ("q5_k_gemv_14336x4096", syn.Q5_K, 4096, 14336)):
             if not want(name):
                 continue
             log(f"extra {name}")
@@ -634,7 +635,8 @@ def main() -> int:
                                      ("q4_k_gemv_4096x128256", syn.Q4_K, 4096, "Q4_K 128256x4096"),
                                      ("q6_k_gemv_14336x4096", syn.Q6_K, 14336, "Q6_K 4096x14336"),
                                      ("q6_k_gemv_4096x128256", syn.Q6_K, 4096, "Q6_K 128256x4096"),
-                                     ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, "Q5_K 4096x4096")):
+                                     ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, "Q5_K 4096x4096"),
+                                     ("q5_k_gemv_14336x4096", syn.Q5_K, 14336, "Q5_K 4096x14336")):
             if name in hosts:
                 log(f"cpu baseline {name}")
                 cpus[name] = cpu_gemv(t, hosts[name], cols, label, budget_s=2.0)

@@ -496,6 +496,7 @@ const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, cons
                               const float *x) {
     if (q32_mfma_supported(type_id, row_bytes, cols, 1, w, x)) return "gemv_mfma_col_kernel";
     if (type_id == kQ6_K && q6k_mfma_supported(row_bytes, cols, 1, w, x)) return "gemv_q6_k_mfma_tile_kernel";
+    if (type_id == kQ5_K && q5k_wide_mfma_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_mfma_kernel";
     if (is_k56(type_id))
         return gemv_k56_supported(type_id, row_bytes, w, x) ? "gemv_k56_kernel" : "gemv_generic_kernel";
     const GemvPlan p = plan_for(type_id, row_bytes, cols, w, x);
@@ -516,6 +517,8 @@ hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t
         return launch_gemv_q32_mfma(type_id, w, row_bytes, cols, x, y, rows, stream, prep, prep_rows);
     if (type_id == kQ6_K && q6k_mfma_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q6k_mfma(w, row_bytes, cols, x, y, rows, stream);
+    if (type_id == kQ5_K && q5k_wide_mfma_supported(row_bytes, cols, rows, w, x))
+        return launch_gemv_q5k_wide_mfma(w, row_bytes, cols, x, y, rows, stream);
     if (is_k56(type_id) && gemv_k56_supported(type_id, row_bytes, w, x))
         return launch_gemv_k56(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, rows, w, x))

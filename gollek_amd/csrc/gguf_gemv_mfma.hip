@@ -65,10 +65,20 @@ constexpr int kMfWaves = 8;                       // waves per workgroup
 constexpr int kMfThreads = kMfWaves * 64;
 constexpr int kTileRows = 16;                     // weight rows per MFMA tile
 constexpr int kSps = 2;                           // superblocks per ring stage
-constexpr int kStageCols = kSps * kQKBlockBytes;  // 288 bytes of a row per stage
-constexpr int kRowPitch = kStageCols + 16;        // LDS pitch of a staged row
-constexpr int kStageDma = (kTileRows * kRowPitch + 1023) / 1024;  // 1 KB loads per stage
-constexpr int kSlotBytes = kStageDma * 1024;
+// K > 4096 ring stages of Q4_K (144-byte superblocks, quants at 16) or
+// Q5_K (176 bytes: qh[32] at 16, quants at 48): kSps superblocks of 16 rows
+// at a pitch of an odd number of 16-byte units (304 / 368 bytes), so the 16
+// rows' 16-byte reads of one superblock fall on distinct banks.
+template <int TYPE>
+struct WkGeom {
+    static constexpr int PB = TYPE == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+    static constexpr int kQOff = TYPE == kQ5_K ? 48 : 16;
+    static constexpr int kStageCols = kSps * PB;                          // bytes of a row per stage
+    static constexpr int kRowPitch = kStageCols + 16;                     // LDS pitch of a staged row
+    static constexpr int kStageDma = (kTileRows * kRowPitch + 1023) / 1024;  // 1 KB loads per stage
+    static constexpr int kSlotBytes = kStageDma * 1024;
+    static_assert((kRowPitch / 16) % 2 == 1, "odd pitch in 16-byte units");
+};
 constexpr int kRecBytes = 208;                    // A record of one 64-column chunk
 constexpr int kRecZero = 192;                     // offset of its zero bytes
 constexpr int kSbRecBytes = 4 * kRecBytes;        // A records of one superblock
@@ -143,7 +153,7 @@ __device__ __forceinline__ void store_x_records(const XPart<XL> &xp, int nsb, in
 // wait for all of them; the stage is complete once the VM loads issued after
 // it are the only ones outstanding, and the LDS reads finish before the slot
 // is refilled.
-template <int OFF, int VM>
+template <int OFF, int VM, int PB = kQKBlockBytes>
 __device__ __forceinline__ void read_stage(uint32_t a_hdr, uint32_t a_qs, u32x4 (&hd)[2],
                                            u32x4 (&q)[2][4]) {
     asm volatile(
@@ -161,9 +171,36 @@ __device__ __forceinline__ void read_stage(uint32_t a_hdr, uint32_t a_qs, u32x4 
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(hd[0]), "=&v"(hd[1]), "=&v"(q[0][0]), "=&v"(q[0][1]), "=&v"(q[0][2]),
           "=&v"(q[0][3]), "=&v"(q[1][0]), "=&v"(q[1][1]), "=&v"(q[1][2]), "=&v"(q[1][3])
-        : "v"(a_hdr), "v"(a_qs), "n"(VM), "n"(OFF), "n"(OFF + kQKBlockBytes), "n"(OFF + 32),
-          "n"(OFF + 64), "n"(OFF + 96), "n"(OFF + kQKBlockBytes + 32),
-          "n"(OFF + kQKBlockBytes + 64), "n"(OFF + kQKBlockBytes + 96)
+        : "v"(a_hdr), "v"(a_qs), "n"(VM), "n"(OFF), "n"(OFF + PB), "n"(OFF + 32),
+          "n"(OFF + 64), "n"(OFF + 96), "n"(OFF + PB + 32),
+          "n"(OFF + PB + 64), "n"(OFF + PB + 96)
+        : "memory");
+}
+
+// Q5_K: read_stage plus this lane's 16 qh bytes of both superblocks (a_qh =
+// row n's qh + 16 (g & 1)), under the same wait.
+template <int OFF, int VM, int PB>
+__device__ __forceinline__ void read_stage5(uint32_t a_hdr, uint32_t a_qs, uint32_t a_qh, u32x4 (&hd)[2],
+                                            u32x4 (&q)[2][4], u32x4 (&qh)[2]) {
+    asm volatile(
+        "s_waitcnt vmcnt(%15)\n\t"
+        "ds_read_b128 %0, %12 offset:%16\n\t"
+        "ds_read_b128 %1, %12 offset:%17\n\t"
+        "ds_read_b128 %2, %13 offset:%16\n\t"
+        "ds_read_b128 %3, %13 offset:%18\n\t"
+        "ds_read_b128 %4, %13 offset:%19\n\t"
+        "ds_read_b128 %5, %13 offset:%20\n\t"
+        "ds_read_b128 %6, %13 offset:%17\n\t"
+        "ds_read_b128 %7, %13 offset:%21\n\t"
+        "ds_read_b128 %8, %13 offset:%22\n\t"
+        "ds_read_b128 %9, %13 offset:%23\n\t"
+        "ds_read_b128 %10, %14 offset:%16\n\t"
+        "ds_read_b128 %11, %14 offset:%17\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(hd[0]), "=&v"(hd[1]), "=&v"(q[0][0]), "=&v"(q[0][1]), "=&v"(q[0][2]), "=&v"(q[0][3]),
+          "=&v"(q[1][0]), "=&v"(q[1][1]), "=&v"(q[1][2]), "=&v"(q[1][3]), "=&v"(qh[0]), "=&v"(qh[1])
+        : "v"(a_hdr), "v"(a_qs), "v"(a_qh), "n"(VM), "n"(OFF), "n"(OFF + PB), "n"(OFF + 32), "n"(OFF + 64),
+          "n"(OFF + 96), "n"(OFF + PB + 32), "n"(OFF + PB + 64), "n"(OFF + PB + 96)
         : "memory");
 }
 
@@ -181,11 +218,16 @@ struct StagePos {
 
 }  // namespace
 
-// NSLOT ring stages per wave; MAXSB = superblocks per row the LDS tables hold.
-template <int NSLOT, int MAXSB>
+// TYPE: Q4_K or Q5_K; NSLOT ring stages per wave; MAXSB = superblocks per
+// row the LDS tables hold.
+template <int TYPE, int NSLOT, int MAXSB>
 __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int64_t rows_per_wg, int ks) {
+    using WG = WkGeom<TYPE>;
+    constexpr int kStageCols = WG::kStageCols, kRowPitch = WG::kRowPitch, kStageDma = WG::kStageDma;
+    constexpr int kSlotBytes = WG::kSlotBytes;
+    constexpr bool Q5 = TYPE == kQ5_K;
     constexpr int XL = (64 * MAXSB + kMfThreads - 1) / kMfThreads;
     // x tables and row sums in one LDS array, the ring in another (the ring's
     // buffer->LDS loads then provably touch none of the tables).
@@ -235,7 +277,7 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
             const int sg = kp * L + p.st;
             uoff = (uint32_t)tile * kTileRows * row_bytes + (uint32_t)sg * kStageCols;
             const int left = nsb - sg * kSps;
-            lim = (uint32_t)(left < kSps ? left : kSps) * kQKBlockBytes;
+            lim = (uint32_t)(left < kSps ? left : kSps) * WG::PB;
         }
         uoff = __builtin_amdgcn_readfirstlane(uoff);
         lim = __builtin_amdgcn_readfirstlane(lim);
@@ -265,7 +307,8 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
     const int a_off = (n < 8 && (n & 3) < 3 && (n >> 2) == (g >> 1)) ? (3 * g + (n & 3)) * 16 : kRecZero;
     const int sh = 4 * (g >> 1);
     const uint32_t a_hdr = (uint32_t)(uintptr_t)(lds_ptr)myring + n * kRowPitch;
-    const uint32_t a_qs = a_hdr + 16 + 16 * (g & 1);
+    const uint32_t a_qs = a_hdr + WG::kQOff + 16 * (g & 1);
+    const uint32_t a_qh = a_hdr + 16 + 16 * (g & 1);  // Q5_K's high bits
     const i32x4 zero = {0, 0, 0, 0};
 
     StagePos cp;
@@ -274,8 +317,11 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
     // instruction immediates).
     auto stage = [&](int q, auto slot_tag) {
         constexpr int J = decltype(slot_tag)::value;
-        u32x4 hd[2], qv[2][4];
-        read_stage<J * kSlotBytes, kStageDma * (NSLOT - 1)>(a_hdr, a_qs, hd, qv);
+        u32x4 hd[2], qv[2][4], qh[2];
+        if constexpr (Q5)
+            read_stage5<J * kSlotBytes, kStageDma * (NSLOT - 1), WG::PB>(a_hdr, a_qs, a_qh, hd, qv, qh);
+        else
+            read_stage<J * kSlotBytes, kStageDma * (NSLOT - 1)>(a_hdr, a_qs, hd, qv);
         issue(myring + J * kSlotBytes, pf);
         pf.advance(L);
         if (q >= total) return;
@@ -309,11 +355,29 @@ __global__ __launch_bounds__(kMfThreads) void gemv_q4_k_mfma_kernel(
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const u32x4 wq = qv[s2][c];
-                const i32x4 B = {(int)((wq.x >> sh) & 0x0F0F0F0Fu), (int)((wq.y >> sh) & 0x0F0F0F0Fu),
-                                 (int)((wq.z >> sh) & 0x0F0F0F0Fu), (int)((wq.w >> sh) & 0x0F0F0F0Fu)};
+                i32x4 B = {(int)((wq.x >> sh) & 0x0F0F0F0Fu), (int)((wq.y >> sh) & 0x0F0F0F0Fu),
+                           (int)((wq.z >> sh) & 0x0F0F0F0Fu), (int)((wq.w >> sh) & 0x0F0F0F0Fu)};
+                if constexpr (Q5) {
+                    // element e's fifth bit: qh byte e % 32 (this lane's 16), bit e / 32
+                    // = 2 c for the low nibbles (g < 2), 2 c + 1 for the high ones
+                    const int hb = 2 * c + (g >> 1);
+                    const u32x4 hq = qh[s2];
+                    B[0] |= (int)(((hq.x >> hb) & 0x01010101u) << 4);
+                    B[1] |= (int)(((hq.y >> hb) & 0x01010101u) << 4);
+                    B[2] |= (int)(((hq.z >> hb) & 0x01010101u) << 4);
+                    B[3] |= (int)(((hq.w >> hb) & 0x01010101u) << 4);
+                }
                 const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[c], B, zero, 0, 0, 0);
-                const int S = (int)((uint32_t)D[0] + ((uint32_t)D[1] << 8) + ((uint32_t)D[2] << 16));
-                acc_sb = fmaf(d * scf[c], (float)S, acc_sb);
+                float Sf;
+                if constexpr (Q5) {
+                    // |sum q X| <= 32 x 31 x 2^22 does not fit int32: the planes
+                    // 0, 1 combine exactly, plane 2 joins in one fp32 rounding
+                    Sf = fmaf((float)D[2], 65536.0f, (float)(D[0] + 256 * D[1]));
+                } else {
+                    // |.| <= 32 x 15 x 2^22 < 2^31: exact in int32
+                    Sf = (float)(int)((uint32_t)D[0] + ((uint32_t)D[1] << 8) + ((uint32_t)D[2] << 16));
+                }
+                acc_sb = fmaf(d * scf[c], Sf, acc_sb);
             }
             // min term: zero codes contribute nothing even for a NaN or
             // infinite dmin (minContribution, RT/GgufKQuantLayout.java:67-69)
@@ -853,8 +917,28 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
         return hipGetLastError();
     }
     const MfmaPlan p = plan_mfma(rows, nsb);
-    hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
+    hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<kQ4_K, 2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
                        stream, w, row_bytes, nsb, x, y, rows, p.rows_per_wg, p.ks);
+    return hipGetLastError();
+}
+
+// Q5_K past K = 4096 (the column kernel takes K <= 4096): the K > 4096
+// Q4_K kernel with the fifth bit from qh.
+bool q5k_wide_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x) {
+    (void)rows;
+    const int v = tuning().gemv_variant;
+    if (v == 1 || v == 2 || v == 4) return false;  // the fp32 kernel stays selectable
+    if (cols <= 0 || cols % kQK != 0) return false;
+    const int64_t nsb = cols / kQK;
+    return nsb > 16 && nsb <= 64 && row_bytes == nsb * kQ5KBlockBytes &&
+           ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+}
+
+hipError_t launch_gemv_q5k_wide_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols, const float *x, float *y,
+                                     int64_t rows, hipStream_t stream) {
+    const MfmaPlan p = plan_mfma(rows, (int)(cols / kQK));
+    hipLaunchKernelGGL((gemv_q4_k_mfma_kernel<kQ5_K, 2, 64>), dim3((unsigned)p.grid), dim3(kMfThreads), 0,
+                       stream, w, row_bytes, (int)(cols / kQK), x, y, rows, p.rows_per_wg, p.ks);
     return hipGetLastError();
 }
 

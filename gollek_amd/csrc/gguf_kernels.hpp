@@ -73,6 +73,11 @@ hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes
 
 // Q6_K on the matrix cores (gguf_gemv_q6k_mfma.hip): K a multiple of 2048 up
 // to 14336, row bytes K / 256 * 210, weights and x 16-byte aligned.
+// Q5_K past K = 4096 on the matrix cores (gguf_gemv_mfma.hip, the K > 4096
+// Q4_K kernel with the fifth bit): K a multiple of 256 up to 16384.
+bool q5k_wide_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x);
+hipError_t launch_gemv_q5k_wide_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols, const float *x, float *y,
+                                     int64_t rows, hipStream_t stream);
 bool q6k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x);
 hipError_t launch_gemv_q6k_mfma(const uint8_t *w, int64_t row_bytes, int64_t cols, const float *x, float *y,
                                 int64_t rows, hipStream_t stream);

@@ -84,8 +84,8 @@ int32_t gollek_hip_last_status(void);
  * threads see the old or the new value, never a torn one.  Keys: "gemv_rows_per_wave",
  * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
  * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
- * 0 = the matrix-core kernels (Q4_K; Q8_0, Q4_0 and Q5_K with K <= 4096;
- * Q6_K with K a multiple of 2048 up to 14336), the buffer->LDS ring kernels (Q8_0, Q4_0
+ * 0 = the matrix-core kernels (Q4_K; Q8_0 and Q4_0 with K <= 4096; Q5_K with
+ * K up to 16384; Q6_K with K a multiple of 2048 up to 14336), the buffer->LDS ring kernels (Q8_0, Q4_0
  * otherwise) and the fp32 Q5_K / Q6_K kernel where they apply, 1 = the
  * fp32 kernels, 2 = the v_dot4 kernel (Q4_K, K <= 4096), 3 = as 0 but Q4_K
  * with K <= 4096 always on the shared-tile matrix-core kernel, 4 = as 0 but

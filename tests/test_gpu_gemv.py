@@ -473,6 +473,7 @@ def test_prepared_layout_matches_gguf_bytes(type_id, rows, cols):
 # ---- Q5_K / Q6_K -----------------------------------------------------------
 
 K56_SHAPES = [(syn.Q5_K, 1, 256), (syn.Q5_K, 7, 768), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 33, 16384),
+              (syn.Q5_K, 4096, 14336), (syn.Q5_K, 1001, 6144), (syn.Q5_K, 100, 8192), (syn.Q5_K, 17, 4352),
               (syn.Q5_K, 1003, 2304), (syn.Q5_K, 12289, 4096), (syn.Q5_K, 20000, 1024), (syn.Q6_K, 1, 256), (syn.Q6_K, 5, 768), (syn.Q6_K, 4096, 4096),
               (syn.Q6_K, 37, 16384), (syn.Q6_K, 1001, 2304), (syn.Q6_K, 14336, 4096), (syn.Q6_K, 17, 4096),
               (syn.Q6_K, 300, 2048), (syn.Q6_K, 4113, 2048), (syn.Q6_K, 4096, 14336), (syn.Q6_K, 100, 6144),
@@ -494,9 +495,9 @@ def test_q5_k_q6_k_dequant_and_gemv(type_id, rows, cols):
     ref = o.matvec_fp64(type_id, data, cols, x)
     java = o.matvec(type_id, data, cols, x)
     try:
-        # Q5_K with K <= 4096 and Q6_K with K a multiple of 2048 up to 14336:
-        # the matrix-core kernels (0) and the fp32 kernel (4); the others run
-        # the fp32 kernel either way.
+        # Q5_K with K up to 16384 and Q6_K with K a multiple of 2048 up to
+        # 14336: the matrix-core kernels (0) and the fp32 kernel (4); the
+        # others run the fp32 kernel either way.
         for variant in (0, 4):
             ops.set_option("gemv_variant", variant)
             y = np.zeros(rows, np.float32)
