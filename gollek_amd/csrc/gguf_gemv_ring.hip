@@ -186,7 +186,11 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t row0 = (int64_t)blockIdx.x * (kGrWaveRows * (nt >> 6));
-    const int nitems = K / (32 * IB);
+    // K a multiple of 32: the last item may hold fewer than IB blocks; its
+    // lanes past the row's last block read bytes of the next row (or zeros
+    // past the wave's rows) and x past K (LDS of the ring), and add nothing.
+    const int nblocks = K / 32;
+    const int nitems = (nblocks + IB - 1) / IB;
 
     uint8_t *const xl = lds;
     uint8_t *const ring = lds + gr_ring_offset(K) + wave * NS * I::kSlot;
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 32; i++) s = fmaf(gr_sbyte(qa[i >> 2], i & 3), xv[i], s);
-            acc = fmaf(d, s, acc);
+            acc = IB * j + b < nblocks ? fmaf(d, s, acc) : acc;
         } else {
             // (q - 8) x per element, as the reference does: the offset is
             // exact in fp32 and nothing cancels.
@@ -302,7 +306,7 @@ __global__ __launch_bounds__(64 * kGrMaxWaves) void gemv_ring_kernel(const uint8
                     s = fmaf(byte_f(hi, k) - 8.0f, xv[16 + 4 * i + k], s);
                 }
             }
-            acc = fmaf(d, s, acc);
+            acc = IB * j + b < nblocks ? fmaf(d, s, acc) : acc;
         }
         sl = sl + 1 == NS ? 0 : sl + 1;
     }
@@ -347,7 +351,7 @@ bool gemv_ring_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t r
     if (type_id != kQ8_0 && type_id != kQ4_0) return false;
     if (tuning().gemv_variant == 1) return false;
     const int bb = type_id == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes;
-    return cols > 0 && cols % (32 * kGrIB) == 0 && cols <= kGrMaxK && row_bytes == cols / 32 * bb &&
+    return cols > 0 && cols % 32 == 0 && cols <= kGrMaxK && row_bytes == cols / 32 * bb &&
            (row_bytes & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 3u) == 0 &&
            (reinterpret_cast<uintptr_t>(x) & 3u) == 0 && 4 * row_bytes < ((int64_t)1 << 31) &&
            rows > 0;

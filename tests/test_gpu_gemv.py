@@ -246,7 +246,12 @@ Q80_Q40_SHAPES = [(syn.Q8_0, 1, 512), (syn.Q8_0, 15, 512), (syn.Q8_0, 17, 1536),
                   # column, an odd number of them, a partial last tile
                   (syn.Q8_0, 8192, 4096), (syn.Q8_0, 8193, 4096), (syn.Q4_0, 16384, 4096),
                   (syn.Q4_0, 16385, 4096), (syn.Q8_0, 4000, 256), (syn.Q4_0, 3000, 2304),
-                  (syn.Q8_0, 5000, 2304), (syn.Q4_0, 300, 768)]
+                  (syn.Q8_0, 5000, 2304), (syn.Q4_0, 300, 768),
+                  # K a multiple of 32 but not of 512 (the ring's last item
+                  # holds fewer than 16 blocks): the 7B FFN down projection,
+                  # one block past whole items, fewer blocks than one item
+                  (syn.Q4_0, 4096, 11008), (syn.Q8_0, 100, 11008), (syn.Q8_0, 33, 4128),
+                  (syn.Q4_0, 17, 160), (syn.Q8_0, 9, 1312)]
 
 
 @pytest.mark.parametrize("type_id,rows,cols", Q80_Q40_SHAPES,
