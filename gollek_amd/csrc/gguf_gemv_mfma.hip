@@ -837,6 +837,143 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     }
 }
 
+// ---- 4096 < K <= 16384, few rows per CU: several columns per wave ----------
+//
+// The column kernel for wide rows (e.g. Q4_K 4096 x 14336, the FFN down
+// projection): a workgroup per CU, its block of at most kMaxRows rows read
+// from the same prepared layout (or the GGUF rows), wave w taking the
+// superblock columns w, w + 16, ... (up to four).  Its units are (column,
+// 16-row tile), column by column, each moved by its own loads (as the column
+// kernel's tiles) into two slots of the wave's LDS region with the same
+// pacing: unit k + 1 is issued once unit k has arrived.  x: every column's
+// superblock is loaded up front, and a column's digit planes are built while
+// the next unit's loads fly.  Row sums accumulate per wave in LDS (pair h of
+// row r at part[w][r][h]) and meet at the end in wave order.
+constexpr int kWideMaxCols = 4;  // columns per wave (K <= 16384)
+
+template <int TYPE, bool PREP>
+__global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
+    const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
+    float *__restrict__ y, int64_t rows, int rows_per_wg) {
+    using G = ColGeom<TYPE>;
+    constexpr int PB = G::PB;
+    constexpr int TB = G::kTileBytes;
+    constexpr int kFull = TB / 1024;
+    constexpr int kTail = (TB % 1024) / 256;
+    constexpr int kRegionW = 2 * TB + kColX;  // two unit slots, then the x scratch
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * kRegionW];
+    __shared__ float part[kColWaves][G::kMaxRows][2];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int nr = (int)(rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg);  // 1..kMaxRows
+    const uint32_t row_bytes = (uint32_t)row_bytes64;
+    const int tiles = (nr + kTileRows - 1) / kTileRows;
+    const int ncol = wv < nsb ? (nsb - wv + kColWaves - 1) / kColWaves : 0;  // wave-uniform
+
+    if (ncol > 0) {
+        // The workgroup's block: nr rows (PREP: column c is nr PB-byte pieces
+        // at nr PB c; otherwise row r's piece of column c at r row_bytes + PB c).
+        const __amdgpu_buffer_rsrc_t rs = wave_buffer(w + r0 * row_bytes64, (uint32_t)nr * row_bytes);
+        auto offset = [&](int c, uint32_t b) {  // byte b of column c
+            const uint32_t r = b / PB, col = b - r * PB;
+            return r < (uint32_t)nr ? (PREP ? (uint32_t)(nr * PB * c) + b : r * row_bytes + PB * c + col)
+                                    : kMaskedOffset;
+        };
+        uint8_t *const region = lds + wv * kRegionW;
+        const uint32_t rbase = (uint32_t)(uintptr_t)(lds_ptr)region;
+        const int nunits = ncol * tiles;
+        auto issue = [&](int k) {
+            const int i = k / tiles, t = k - i * tiles;
+            const int c = wv + kColWaves * i;
+            const uint32_t tb = (uint32_t)(TB * t);
+            uint8_t *const dst = region + TB * (k & 1);
+#pragma unroll
+            for (int j = 0; j < kFull; j++) {
+                const uint32_t o = offset(c, tb + 1024u * j + 16u * lane);  // a named local for the builtin
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * j), 16, o, 0, 0, kStreamLoad);
+            }
+#pragma unroll
+            for (int j = 0; j < kTail; j++) {
+                const uint32_t o = offset(c, tb + 1024u * kFull + 256u * j + 4u * lane);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + 1024 * kFull + 256 * j), 4, o, 0, 0,
+                                                         kStreamLoad);
+            }
+        };
+        // x of every column (past nsb the wave's first again, unused), then unit 0.
+        float4 xq[kWideMaxCols];
+#pragma unroll
+        for (int i = 0; i < kWideMaxCols; i++) {
+            const int c = wv + kColWaves * i;
+            xq[i] = reinterpret_cast<const float4 *>(x)[64 * (c < nsb ? c : wv) + lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(0);
+        __builtin_amdgcn_sched_barrier(0);
+        XOps4 xo;
+        int ps[4][4];
+        auto build = [&](const float4 xv) {
+            if constexpr (TYPE == kQ4_0)
+                x_operands4<true>(xv, rbase + 2 * TB, xo, ps);
+            else
+                x_operands4(xv, rbase + 2 * TB, xo);
+        };
+        build(xq[0]);
+        // every x load is complete here (they precede unit 0's loads), so
+        // later builds wait for nothing
+        asm volatile("" : "+v"(xq[1].x), "+v"(xq[1].y), "+v"(xq[1].z), "+v"(xq[1].w), "+v"(xq[2].x),
+                     "+v"(xq[2].y), "+v"(xq[2].z), "+v"(xq[2].w), "+v"(xq[3].x), "+v"(xq[3].y), "+v"(xq[3].z),
+                     "+v"(xq[3].w));
+
+        const int n = lane & 15, g = lane >> 4;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per tile, summed over the wave's columns in order
+        static_assert(G::kMaxTiles <= 4, "four tile sums");
+        for (int k = 0; k < nunits; k++) {
+            wait_vm<0>();
+            if (k + 1 < nunits) issue(k + 1);
+            const int t = k % tiles;
+            const uint32_t a_h = rbase + TB * (k & 1) + n * PB;
+            float v;
+            if constexpr (TYPE == kQ4_K) {
+                u32x4 hv;
+                uint2 q[4];
+                read_tile_superblock(a_h, a_h + 16 + 8 * g, hv, q);
+                v = q4k_tile_superblock4(hv, q, xo);
+            } else if constexpr (TYPE == kQ5_K) {
+                u32x4 hv;
+                uint2 qh, q[4];
+                read_tile_superblock5(a_h, a_h + 16 + 8 * g, a_h + 48 + 8 * g, hv, qh, q);
+                v = q4k_tile_superblock4<true>(hv, q, xo, qh);
+            } else {
+                uint32_t raw[20], dh[4];
+                const uint32_t a_q = a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
+                const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
+                read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(a_q, a_d, raw, dh);
+                v = q32_tile_piece<TYPE>(raw, dh, xo, ps);
+            }
+            // lane n + 16 h: sub-blocks 2 c + h of row n
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += t == i ? v : 0.0f;
+            if (k + 1 < nunits && (k + 1) % tiles == 0) {  // the next unit starts a column
+                // component selects (an indexed pick of xq goes to scratch)
+                const int i = (k + 1) / tiles;
+                auto pick = [&](float a1, float a2, float a3) { return i == 1 ? a1 : i == 2 ? a2 : a3; };
+                build(float4{pick(xq[1].x, xq[2].x, xq[3].x), pick(xq[1].y, xq[2].y, xq[3].y),
+                             pick(xq[1].z, xq[2].z, xq[3].z), pick(xq[1].w, xq[2].w, xq[3].w)});
+            }
+        }
+        if (lane < 32)
+            for (int t = 0; t < tiles; t++) part[wv][16 * t + n][g] = t == 0 ? acc[0] : t == 1 ? acc[1] : t == 2 ? acc[2] : acc[3];
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int nw = nsb < kColWaves ? nsb : kColWaves;
+    for (int r = threadIdx.x; r < nr; r += kColThreads) {
+        float s = 0.0f;
+        for (int k = 0; k < nw; k++) s += part[k][r][0] + part[k][r][1];
+        y[r0 + r] = s;
+    }
+}
+
 namespace {
 
 struct MfmaPlan {
@@ -890,17 +1027,29 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
                                 const uint8_t *prep, int64_t prep_rows) {
     const int nsb = (int)(cols / kQK);
     const int64_t cus = device_cus();
-    // At most 64 rows per CU: every workgroup's share stays in LDS, one
-    // superblock column per wave (gemv_variant 3 keeps the shared tiles).
+    // At most 64 rows per CU: one workgroup per CU's block of rows, one
+    // superblock column per wave (K <= 4096) or several (the wide kernel,
+    // K <= 16384); gemv_variant 3 keeps the shared tiles.
     const int64_t col_rows = col_layout_rows(kQ4_K, rows, cols);
     if (col_rows > 0) {
         const dim3 grid((unsigned)((rows + col_rows - 1) / col_rows));
-        if (prep != nullptr && prep_rows == col_rows)
-            hipLaunchKernelGGL((gemv_mfma_col_kernel<kQ4_K, true>), grid, dim3(kColThreads), 0, stream, prep,
-                               row_bytes, nsb, x, y, rows, (int)col_rows);
-        else
-            hipLaunchKernelGGL((gemv_mfma_col_kernel<kQ4_K, false>), grid, dim3(kColThreads), 0, stream, w,
-                               row_bytes, nsb, x, y, rows, (int)col_rows);
+        const bool use_prep = prep != nullptr && prep_rows == col_rows;
+        const uint8_t *src = use_prep ? prep : w;
+        if (nsb <= kColWaves) {
+            if (use_prep)
+                hipLaunchKernelGGL((gemv_mfma_col_kernel<kQ4_K, true>), grid, dim3(kColThreads), 0, stream, src,
+                                   row_bytes, nsb, x, y, rows, (int)col_rows);
+            else
+                hipLaunchKernelGGL((gemv_mfma_col_kernel<kQ4_K, false>), grid, dim3(kColThreads), 0, stream, src,
+                                   row_bytes, nsb, x, y, rows, (int)col_rows);
+        } else {
+            if (use_prep)
+                hipLaunchKernelGGL((gemv_mfma_wide_kernel<kQ4_K, true>), grid, dim3(kColThreads), 0, stream, src,
+                                   row_bytes, nsb, x, y, rows, (int)col_rows);
+            else
+                hipLaunchKernelGGL((gemv_mfma_wide_kernel<kQ4_K, false>), grid, dim3(kColThreads), 0, stream, src,
+                                   row_bytes, nsb, x, y, rows, (int)col_rows);
+        }
         return hipGetLastError();
     }
     if (nsb <= 16) {
@@ -952,7 +1101,7 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
     if (type_id != kQ4_0 && type_id != kQ8_0 && type_id != kQ5_K) return false;
     const int v = tuning().gemv_variant;
     if (v == 1 || v == 2 || v == 4) return false;  // fp32 / ring / Q5_K fp32 paths kept selectable
-    if (cols <= 0 || cols % kQK != 0 || cols / kQK > 16 || rows <= 0) return false;
+    if (cols <= 0 || cols % kQK != 0 || cols / kQK > 16 * kWideMaxCols || rows <= 0) return false;
     const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     if (row_bytes != cols / kQK * piece || (row_bytes & 15) != 0) return false;
     return ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
@@ -967,14 +1116,20 @@ hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes
     const dim3 grid((unsigned)((rows + col_rows - 1) / col_rows));
     const bool use_prep = prep != nullptr && prep_rows == col_rows;
     const uint8_t *src = use_prep ? prep : w;
-#define GOLLEK_COL(T)                                                                                     \
-    do {                                                                                                  \
-        if (use_prep)                                                                                     \
-            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, true>), grid, dim3(kColThreads), 0, stream, src,  \
-                               row_bytes, nsb, x, y, rows, (int)col_rows);                               \
-        else                                                                                              \
-            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false>), grid, dim3(kColThreads), 0, stream, src, \
-                               row_bytes, nsb, x, y, rows, (int)col_rows);                               \
+#define GOLLEK_COL(T)                                                                                      \
+    do {                                                                                                   \
+        if (nsb <= kColWaves && use_prep)                                                                  \
+            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, true>), grid, dim3(kColThreads), 0, stream, src,   \
+                               row_bytes, nsb, x, y, rows, (int)col_rows);                                \
+        else if (nsb <= kColWaves)                                                                         \
+            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false>), grid, dim3(kColThreads), 0, stream, src,  \
+                               row_bytes, nsb, x, y, rows, (int)col_rows);                                \
+        else if (use_prep)                                                                                 \
+            hipLaunchKernelGGL((gemv_mfma_wide_kernel<T, true>), grid, dim3(kColThreads), 0, stream, src,  \
+                               row_bytes, nsb, x, y, rows, (int)col_rows);                                \
+        else                                                                                               \
+            hipLaunchKernelGGL((gemv_mfma_wide_kernel<T, false>), grid, dim3(kColThreads), 0, stream, src, \
+                               row_bytes, nsb, x, y, rows, (int)col_rows);                                \
     } while (0)
     if (type_id == kQ8_0) GOLLEK_COL(kQ8_0);
     else if (type_id == kQ5_K) GOLLEK_COL(kQ5_K);
@@ -990,14 +1145,15 @@ int64_t col_layout_rows(int type_id, int64_t rows, int64_t cols) {
     if (rows <= 0 || cols <= 0 || cols % kQK != 0) return 0;
     const int64_t nsb = cols / kQK, cus = device_cus();
     const int64_t per = (rows + cus - 1) / cus;
+    if (nsb > 16 * kWideMaxCols) return 0;
     if (type_id == kQ4_K) {
         const int v = tuning().gemv_variant;
         if (v == 1 || v == 2 || v == 3) return 0;
-        return nsb <= 16 && per <= ColGeom<kQ4_K>::kMaxRows ? per : 0;
+        return per <= ColGeom<kQ4_K>::kMaxRows ? per : 0;
     }
     if (type_id != kQ4_0 && type_id != kQ8_0 && type_id != kQ5_K) return 0;
     const int v = tuning().gemv_variant;
-    if (v == 1 || v == 2 || v == 4 || nsb > 16) return 0;
+    if (v == 1 || v == 2 || v == 4) return 0;
     const int64_t most = type_id == kQ8_0   ? ColGeom<kQ8_0>::kMaxRows
                          : type_id == kQ5_K ? ColGeom<kQ5_K>::kMaxRows
                                             : ColGeom<kQ4_0>::kMaxRows;

@@ -84,8 +84,9 @@ int32_t gollek_hip_last_status(void);
  * threads see the old or the new value, never a torn one.  Keys: "gemv_rows_per_wave",
  * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
  * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
- * 0 = the matrix-core kernels (Q4_K; Q8_0 and Q4_0 with K <= 4096; Q5_K with
- * K up to 16384; Q6_K with K a multiple of 2048 up to 14336), the buffer->LDS ring kernels (Q8_0, Q4_0
+ * 0 = the matrix-core kernels (Q4_K; Q8_0 and Q4_0 with K up to 16384 and at most
+ * 32 / 64 rows per CU; Q5_K with K up to 16384; Q6_K with K a multiple of 2048 up
+ * to 14336), the buffer->LDS ring kernels (Q8_0, Q4_0
  * otherwise) and the fp32 Q5_K / Q6_K kernel where they apply, 1 = the
  * fp32 kernels, 2 = the v_dot4 kernel (Q4_K, K <= 4096), 3 = as 0 but Q4_K
  * with K <= 4096 always on the shared-tile matrix-core kernel, 4 = as 0 but
@@ -116,9 +117,9 @@ gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *de
 
 /* Build the handle's prepared mat-vec layout: a second device copy of the
  * matrix in which every workgroup's block of rows is stored superblock
- * column by column, the order the matrix-core column kernel reads (Q4_K,
- * Q8_0, Q4_0 and Q5_K with K <= 4096 and at most 64 rows per CU; measured
- * 7.8 us against 8.8 us for Q4_K 14336 x 4096).  Later full mat-vecs
+ * column by column, the order the matrix-core column kernels read (Q4_K,
+ * Q8_0, Q4_0 and Q5_K with K up to 16384 and at most 64 / 32 / 64 / 48 rows
+ * per CU; measured 7.8 us against 8.8 us for Q4_K 14336 x 4096).  Later full mat-vecs
  * (row_count == rows) on the handle read it; every other entry point keeps
  * reading the GGUF bytes.  The layout follows the device's CU count and
  * gemv_variant at the time of the call; a no-op (OK) for other shapes.
