@@ -592,7 +592,9 @@ def main() -> int:
                                     ("q6_k_gemv_14336x4096", syn.Q6_K, 4096, 14336),
                                     ("q6_k_gemv_4096x128256", syn.Q6_K, 128256, 4096),
                                     ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, 4096),
-                                    ("q5_k_gemv_14336x4096", syn.Q5_K, 4096, 14336)):
+                                    ("q5_k_gemv_14336x4096", syn.Q5_K, 4096, 14336),
+                                    ("q4_k_gemv_14336x4096", syn.Q4_K, 4096, 14336),
+                                    ("q4_0_gemv_11008x4096", syn.Q4_0, 4096, 11008)):
             if not want(name):
                 continue
             log(f"extra {name}")
@@ -636,7 +638,9 @@ def main() -> int:
                                      ("q6_k_gemv_14336x4096", syn.Q6_K, 14336, "Q6_K 4096x14336"),
                                      ("q6_k_gemv_4096x128256", syn.Q6_K, 4096, "Q6_K 128256x4096"),
                                      ("q5_k_gemv_4096x4096", syn.Q5_K, 4096, "Q5_K 4096x4096"),
-                                     ("q5_k_gemv_14336x4096", syn.Q5_K, 14336, "Q5_K 4096x14336")):
+                                     ("q5_k_gemv_14336x4096", syn.Q5_K, 14336, "Q5_K 4096x14336"),
+                                     ("q4_k_gemv_14336x4096", syn.Q4_K, 14336, "Q4_K 4096x14336"),
+                                     ("q4_0_gemv_11008x4096", syn.Q4_0, 11008, "Q4_0 4096x11008")):
             if name in hosts:
                 log(f"cpu baseline {name}")
                 cpus[name] = cpu_gemv(t, hosts[name], cols, label, budget_s=2.0)
