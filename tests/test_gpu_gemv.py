@@ -550,6 +550,42 @@ def test_q6_k_lm_head_full_size_sampled_rows():
     t.close()
 
 
+# One shape per kernel family: the column kernel (K = 4096), the wide-row
+# kernel (K = 14336 / 11008), the shared-tile and ring kernels (many rows per
+# CU, K not a multiple of 256), the K > 4096 Q4_K kernel, Q6_K both paths.
+NONFINITE_X = [(syn.Q4_K, 4096, 4096), (syn.Q4_K, 4096, 14336), (syn.Q4_K, 20000, 4096),
+               (syn.Q4_K, 20000, 6144), (syn.Q8_0, 4096, 4096), (syn.Q8_0, 300, 4128),
+               (syn.Q4_0, 4096, 11008), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 1000, 8192),
+               (syn.Q6_K, 4096, 4096), (syn.Q6_K, 1000, 14336)]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", NONFINITE_X, ids=[f"type{t}_{r}x{c}" for t, r, c in NONFINITE_X])
+def test_non_finite_x_poisons_every_row(type_id, rows, cols):
+    # A NaN in x makes every row NaN, as in the reference's fp32 loop (every
+    # row multiplies it, 0 x NaN included).  An infinity makes every row
+    # non-finite in both: the loop gives +-inf or NaN per row (0 x inf,
+    # +inf - inf), these kernels NaN (x's scale for that superblock is NaN).
+    print(f"[gpu] non-finite x type={type_id} {rows}x{cols}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=rows + cols + type_id)
+    t = _tensor(type_id, data, cols)
+    try:
+        for variant in (0, 4):
+            ops.set_option("gemv_variant", variant)
+            for bad in (np.nan, np.inf, -np.inf):
+                x = syn.activation(cols, seed=7).copy()
+                x[(cols * 2) // 3 + 5] = bad
+                y = np.zeros(rows, np.float32)
+                ops.mat_vec(t, x, y)
+                java = o.matvec(type_id, data, cols, x)
+                if np.isnan(bad):
+                    assert np.all(np.isnan(y)) and np.all(np.isnan(java)), (variant, bad)
+                else:
+                    assert not np.any(np.isfinite(y)) and not np.any(np.isfinite(java)), (variant, bad)
+    finally:
+        ops.set_option("gemv_variant", 0)
+    t.close()
+
+
 UNALIGNED = [(t, off) for t in (syn.Q8_0, syn.Q4_0, syn.Q4_K, syn.Q5_K, syn.Q6_K) for off in (1, 2)]
 
 
