@@ -123,6 +123,10 @@ gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *de
  * (row_count == rows) on the handle read it; every other entry point keeps
  * reading the GGUF bytes.  The layout follows the device's CU count and
  * gemv_variant at the time of the call; a no-op (OK) for other shapes.
+ * Call it before the handle's device mat-vecs start, or with none in
+ * flight: a call that finds a copy for another partition frees it, and the
+ * _device entry points read the copy on the caller's stream without the
+ * handle's lock.
  * Replaces the reference's prepared-matrix build at model load
  * (RT/GgufPreparedMatrixStore.java:120-127 via PRG/JavaNativeGgufBackend
  * .java:157-180), which likewise keeps a prepared copy beside the raw
