@@ -26,8 +26,11 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <mutex>
 #include <new>
+#include <thread>
+#include <vector>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -54,7 +57,12 @@ constexpr TypeGeom kTypes[] = {
 constexpr int kNumTypes = sizeof(kTypes) / sizeof(kTypes[0]);
 
 constexpr int kMaxDims = 8;
-constexpr size_t kStageBytes = 32u << 20;  // per pinned staging buffer (two of them)
+// Upload staging: up to kLanes host threads each copy every kLanes-th chunk
+// of kSlotBytes from the mapped file into one of their two pinned slots and
+// queue its DMA, so host copies run in parallel with each other and with the
+// DMAs (one thread's copy alone moves ~10-20 GB/s).  64 MiB pinned in all.
+constexpr int kLanes = 8;
+constexpr size_t kSlotBytes = 4u << 20;
 
 struct TensorInfo {
     std::string name;
@@ -119,9 +127,9 @@ struct gollek_hip_gguf {
     std::unordered_map<std::string, int64_t> by_name;
     // upload resources, created at the first upload; uploads serialise on mu
     std::mutex mu;
-    uint8_t *stage[2] = {nullptr, nullptr};
+    uint8_t *stage[kLanes][2] = {};
     hipStream_t stream = nullptr;
-    hipEvent_t done[2] = {nullptr, nullptr};
+    hipEvent_t done[kLanes][2] = {};
 };
 
 namespace {
@@ -130,11 +138,13 @@ namespace {
 // and clears their handles.
 void release_staging(gollek_hip_gguf *f) {
     if (f->stream != nullptr) (void)hipStreamSynchronize(f->stream);
-    for (int i = 0; i < 2; i++) {
-        if (f->done[i] != nullptr) (void)hipEventDestroy(f->done[i]);
-        if (f->stage[i] != nullptr) (void)hipHostFree(f->stage[i]);
-        f->done[i] = nullptr;
-        f->stage[i] = nullptr;
+    for (int l = 0; l < kLanes; l++) {
+        for (int i = 0; i < 2; i++) {
+            if (f->done[l][i] != nullptr) (void)hipEventDestroy(f->done[l][i]);
+            if (f->stage[l][i] != nullptr) (void)hipHostFree(f->stage[l][i]);
+            f->done[l][i] = nullptr;
+            f->stage[l][i] = nullptr;
+        }
     }
     if (f->stream != nullptr) (void)hipStreamDestroy(f->stream);
     f->stream = nullptr;
@@ -409,32 +419,65 @@ gollek_hip_weight *gollek_hip_gguf_upload(gollek_hip_gguf *f, int64_t index, cha
     uint8_t *dst = gollek::weight_data(w);
     std::lock_guard<std::mutex> lock(f->mu);
     hipError_t e = hipSuccess;
-    // The stream, the two pinned staging buffers and their events are set up
-    // together at the first upload: if any of them fails, all are released,
-    // so a later call sets them up again instead of using a partial set.
-    if (f->stream == nullptr || f->stage[0] == nullptr || f->stage[1] == nullptr ||
-        f->done[0] == nullptr || f->done[1] == nullptr) {
+    // The stream, the pinned slots and their events are set up together at
+    // the first upload: if any of them fails, all are released, so a later
+    // call sets them up again instead of using a partial set.
+    if (f->stream == nullptr || f->stage[kLanes - 1][1] == nullptr || f->done[kLanes - 1][1] == nullptr) {
         release_staging(f);
         e = hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking);
-        for (int i = 0; i < 2 && e == hipSuccess; i++) e = hipHostMalloc(reinterpret_cast<void **>(&f->stage[i]), kStageBytes, hipHostMallocDefault);
-        for (int i = 0; i < 2 && e == hipSuccess; i++) e = hipEventCreateWithFlags(&f->done[i], hipEventDisableTiming);
+        for (int l = 0; l < kLanes; l++) {
+            for (int i = 0; i < 2 && e == hipSuccess; i++) {
+                e = hipHostMalloc(reinterpret_cast<void **>(&f->stage[l][i]), kSlotBytes, hipHostMallocDefault);
+                if (e == hipSuccess) e = hipEventCreateWithFlags(&f->done[l][i], hipEventDisableTiming);
+            }
+        }
         if (e != hipSuccess) release_staging(f);
     }
-    // Chunk k: mapped bytes -> staging buffer k % 2 (once the copy that last
-    // read that buffer has finished) -> device.
+    // Chunk k (kSlotBytes from offset k * kSlotBytes) belongs to lane
+    // k % lanes and goes through that lane's slot (k / lanes) % 2, once the
+    // DMA that last read the slot has finished.  All DMAs share f->stream;
+    // an event recorded after a lane's DMA may also cover other lanes' DMAs
+    // queued before it, which only makes the wait longer.
     const uint8_t *src = f->map + f->data_start + t.offset;
-    bool used[2] = {false, false};
-    for (int64_t off = 0, k = 0; off < t.size && e == hipSuccess; off += (int64_t)kStageBytes, k++) {
-        const int b = (int)(k & 1);
-        const size_t n = (size_t)(t.size - off < (int64_t)kStageBytes ? t.size - off : (int64_t)kStageBytes);
-        if (used[b]) e = hipEventSynchronize(f->done[b]);
-        if (e != hipSuccess) break;
-        memcpy(f->stage[b], src + off, n);
-        e = hipMemcpyAsync(dst + off, f->stage[b], n, hipMemcpyHostToDevice, f->stream);
-        if (e == hipSuccess) e = hipEventRecord(f->done[b], f->stream);
-        used[b] = true;
+    const int64_t chunks = (t.size + (int64_t)kSlotBytes - 1) / (int64_t)kSlotBytes;
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int lanes = (int)std::min<int64_t>(std::min<int64_t>(kLanes, hw == 0 ? 1 : hw), std::max<int64_t>(chunks, 1));
+    hipError_t lane_err[kLanes];
+    auto lane = [&](int l) {
+        hipError_t le = hipSuccess;
+        for (int64_t k = l, j = 0; k < chunks && le == hipSuccess; k += lanes, j++) {
+            const int b = (int)(j & 1);
+            const int64_t off = k * (int64_t)kSlotBytes;
+            const size_t n = (size_t)std::min<int64_t>((int64_t)kSlotBytes, t.size - off);
+            if (j >= 2) le = hipEventSynchronize(f->done[l][b]);
+            if (le != hipSuccess) break;
+            memcpy(f->stage[l][b], src + off, n);
+            le = hipMemcpyAsync(dst + off, f->stage[l][b], n, hipMemcpyHostToDevice, f->stream);
+            if (le == hipSuccess) le = hipEventRecord(f->done[l][b], f->stream);
+        }
+        lane_err[l] = le;
+    };
+    if (e == hipSuccess) {
+        // Lanes 1.. on their own threads; the calling thread runs lane 0 and
+        // then any lane whose thread could not be started.
+        std::vector<std::thread> th;
+        std::vector<int> inline_lanes;
+        th.reserve((size_t)lanes);
+        for (int l = 1; l < lanes; l++) {
+            try {
+                th.emplace_back(lane, l);
+            } catch (...) {
+                inline_lanes.push_back(l);
+            }
+        }
+        lane(0);
+        for (int l : inline_lanes) lane(l);
+        for (std::thread &x : th) x.join();
+        for (int l = 0; l < lanes && e == hipSuccess; l++) e = lane_err[l];
+        // Wait for every queued DMA, also after an error in one lane.
+        const hipError_t es = hipStreamSynchronize(f->stream);
+        if (e == hipSuccess) e = es;
     }
-    if (e == hipSuccess) e = hipStreamSynchronize(f->stream);
     if (e != hipSuccess) {
         file_fail(e == hipErrorOutOfMemory ? GOLLEK_HIP_ERR_NOMEM : GOLLEK_HIP_ERR_DEVICE, err, err_len,
                   "GGUF upload of %s failed: %s", t.name.c_str(), hipGetErrorString(e));

@@ -138,7 +138,6 @@ namespace {
 template <int NDMA>
 hipError_t launch_ring(const uint8_t *w, int64_t row_bytes, int nsb, const float *x, float *y,
                        int64_t rows, hipStream_t stream) {
-    const LaunchTuning &t = tuning();
     const int64_t cus = device_cus();
     // One workgroup per CU when that keeps every wave at <= kMaxWaveRows rows;
     // fewer when there are fewer rows than waves; more (run in turn) for

@@ -1,7 +1,8 @@
 """GPU parity of tensors uploaded from a GGUF file (MI355X).
 
-A file holding Q4_0, Q8_0 and Q4_K matrices (some larger than one or two
-32 MiB staging chunks) is opened with the native loader; each tensor is
+A file holding Q4_0, Q8_0 and Q4_K matrices (from under one 4 MiB staging
+chunk to 17 of them, so that one copy lane reuses its slots) is opened with
+the native loader; each tensor is
 uploaded from the file and checked against the oracle: dequantized rows at
 the start, at every chunk boundary and at the end bit-exact, the full GEMV
 within GEMV_TOL, and bit-identical to the same bytes uploaded from host
@@ -18,11 +19,12 @@ from tests.test_gpu_gemv import GEMV_TOL, assert_same_bits
 
 pytestmark = pytest.mark.gpu
 
-CHUNK = 32 << 20  # staging chunk of the loader
+CHUNK = 4 << 20  # staging chunk of the loader (8 copy lanes, 2 slots each)
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 
-# (name, type, rows, cols): 1.6 MB, 33 MB (two chunks), 71 MB (three chunks,
-# the first staging buffer reused), 0.2 MB.
+# (name, type, rows, cols): 1.6 MB, 33 MB (eight full chunks and a part),
+# 71 MB (17 chunks: lane 0 takes chunks 0, 8 and 16, reusing its first
+# slot), 0.2 MB (one part chunk).
 TENSORS = [("blk.0.attn_q.weight", Q4_0, 300, 4096),
            ("blk.0.ffn_up.weight", Q4_K, 14336, 4096),
            ("blk.0.ffn_down.weight", Q8_0, 8192, 8192),
