@@ -485,11 +485,12 @@ __device__ __forceinline__ void read_tile_piece32(uint32_t a_q, uint32_t a_d, ui
 
 // The piece's share of row n from blocks 2 c + h (lane n + 16 h, h < 2;
 // lanes 32..63 return values of the zero A rows).  Q4_0 codes are stored
-// as q + 8: each plane sum drops 8 x the plane's digit sum (ps) first, so
-// sum (q - 8) X stays exact in int32 up to the plane combine.
+// as q + 8 (RT/GgufQ4RawDot.java): the B bytes are q - 8 as signed bytes,
+// ((q + 0x78) ^ 0x80) per byte (q + 0x78 <= 0x87, so nothing carries into
+// the next byte), and each plane sum is sum (q - 8) X exactly in int32.
 template <int TYPE>
 __device__ __forceinline__ float q32_tile_piece(const uint32_t (&raw)[20], const uint32_t (&dh)[4],
-                                                const XOps4 &o, const int (&ps)[4][4]) {
+                                                const XOps4 &o) {
     const int lane = threadIdx.x & 63;
     const uint32_t sh = TYPE == kQ4_0 ? 4u * (uint32_t)(lane >> 5) : 0u;
     const i32x4 zero = {0, 0, 0, 0};
@@ -500,23 +501,17 @@ __device__ __forceinline__ float q32_tile_piece(const uint32_t (&raw)[20], const
         const uint32_t l0 = __builtin_amdgcn_alignbyte(r[1], r[0], 2);
         const uint32_t l1 = __builtin_amdgcn_alignbyte(r[2], r[1], 2);
         i32x4 B;
-        if constexpr (TYPE == kQ4_0)
-            B = i32x4{(int)((l0 >> sh) & 0x0F0F0F0Fu), (int)((l1 >> sh) & 0x0F0F0F0Fu),
-                      (int)((r[3] >> sh) & 0x0F0F0F0Fu), (int)((r[4] >> sh) & 0x0F0F0F0Fu)};
-        else
+        if constexpr (TYPE == kQ4_0) {
+            auto sq = [&](uint32_t v) { return (int)((((v >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u); };
+            B = i32x4{sq(l0), sq(l1), sq(r[3]), sq(r[4])};
+        } else
             B = i32x4{(int)l0, (int)l1, (int)r[3], (int)r[4]};
         D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[c], B, zero, 0, 0, 0);
     }
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        int d0 = D[c][0], d1 = D[c][1], d2 = D[c][2], d3 = D[c][3];
-        if constexpr (TYPE == kQ4_0) {
-            d0 -= 8 * ps[c][0];
-            d1 -= 8 * ps[c][1];
-            d2 -= 8 * ps[c][2];
-            d3 -= 8 * ps[c][3];
-        }
+        const int d0 = D[c][0], d1 = D[c][1], d2 = D[c][2], d3 = D[c][3];
         // |d0 + 256 d1| < 2^28 (Q8_0) or 2^24 (Q4_0): at most one rounding each
         const float S = fmaf((float)(d2 + 256 * d3), 65536.0f, (float)(d0 + 256 * d1));
         acc = fmaf(half_bits_to_float_fast(dh[c]), S, acc);
@@ -783,13 +778,9 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t rbase = lds0 + wv * G::kRegion;
         XOps4 xo;
-        int ps[4][4];
         float4 xr = xv;  // the conversion stays below the tile's loads
         asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
-        if constexpr (TYPE == kQ4_0)
-            x_operands4<true>(xr, rbase + G::kW, xo, ps);
-        else
-            x_operands4(xr, rbase + G::kW, xo);
+        x_operands4(xr, rbase + G::kW, xo);
 
         const int n = lane & 15, g = lane >> 4;
         for (int t = 0; t < tiles; t++) {
@@ -815,7 +806,7 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
                 const uint32_t a_q = a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
                 const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
                 read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(a_q, a_d, raw, dh);
-                v = q32_tile_piece<TYPE>(raw, dh, xo, ps);
+                v = q32_tile_piece<TYPE>(raw, dh, xo);
             }
             // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until the
             // row sums; the tile has been read (read_* wait for their reads)
@@ -846,8 +837,8 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
 // 16-row tile), column by column, each moved by its own loads (as the column
 // kernel's tiles) into two slots of the wave's LDS region with the same
 // pacing: unit k + 1 is issued once unit k has arrived.  x: every column's
-// superblock is loaded up front, and a column's digit planes are built while
-// the next unit's loads fly.  Row sums accumulate per wave in LDS (pair h of
+// superblock is loaded up front and its digit planes built while unit 0's
+// loads fly, kept compactly (XOpsC) until the column's units.  Row sums accumulate per wave in LDS (pair h of
 // row r at part[w][r][h]) and meet at the end in wave order.
 constexpr int kWideMaxCols = 4;  // columns per wave (K <= 16384)
 
@@ -900,7 +891,10 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
                                                          kStreamLoad);
             }
         };
-        // x of every column (past nsb the wave's first again, unused), then unit 0.
+        // x of every column (past nsb the wave's first again, unused), then
+        // unit 0, then every column's operands while unit 0 flies (built
+        // between units instead, they held up the units: 9.3 against 8.0 us
+        // for Q4_K 4096 x 14336).
         float4 xq[kWideMaxCols];
 #pragma unroll
         for (int i = 0; i < kWideMaxCols; i++) {
@@ -910,56 +904,44 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
         __builtin_amdgcn_sched_barrier(0);
         issue(0);
         __builtin_amdgcn_sched_barrier(0);
-        XOps4 xo;
-        int ps[4][4];
-        auto build = [&](const float4 xv) {
-            if constexpr (TYPE == kQ4_0)
-                x_operands4<true>(xv, rbase + 2 * TB, xo, ps);
-            else
-                x_operands4(xv, rbase + 2 * TB, xo);
-        };
-        build(xq[0]);
-        // every x load is complete here (they precede unit 0's loads), so
-        // later builds wait for nothing
-        asm volatile("" : "+v"(xq[1].x), "+v"(xq[1].y), "+v"(xq[1].z), "+v"(xq[1].w), "+v"(xq[2].x),
-                     "+v"(xq[2].y), "+v"(xq[2].z), "+v"(xq[2].w), "+v"(xq[3].x), "+v"(xq[3].y), "+v"(xq[3].z),
-                     "+v"(xq[3].w));
+        XOpsC xc[kWideMaxCols];
+#pragma unroll
+        for (int i = 0; i < kWideMaxCols; i++)
+            if (i < ncol) x_operands4c(xq[i], rbase + 2 * TB, xc[i]);
 
         const int n = lane & 15, g = lane >> 4;
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per tile, summed over the wave's columns in order
         static_assert(G::kMaxTiles <= 4, "four tile sums");
-        for (int k = 0; k < nunits; k++) {
-            wait_vm<0>();
-            if (k + 1 < nunits) issue(k + 1);
-            const int t = k % tiles;
-            const uint32_t a_h = rbase + TB * (k & 1) + n * PB;
-            float v;
-            if constexpr (TYPE == kQ4_K) {
-                u32x4 hv;
-                uint2 q[4];
-                read_tile_superblock(a_h, a_h + 16 + 8 * g, hv, q);
-                v = q4k_tile_superblock4(hv, q, xo);
-            } else if constexpr (TYPE == kQ5_K) {
-                u32x4 hv;
-                uint2 qh, q[4];
-                read_tile_superblock5(a_h, a_h + 16 + 8 * g, a_h + 48 + 8 * g, hv, qh, q);
-                v = q4k_tile_superblock4<true>(hv, q, xo, qh);
-            } else {
-                uint32_t raw[20], dh[4];
-                const uint32_t a_q = a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
-                const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
-                read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(a_q, a_d, raw, dh);
-                v = q32_tile_piece<TYPE>(raw, dh, xo, ps);
-            }
-            // lane n + 16 h: sub-blocks 2 c + h of row n
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] += t == i ? v : 0.0f;
-            if (k + 1 < nunits && (k + 1) % tiles == 0) {  // the next unit starts a column
-                // component selects (an indexed pick of xq goes to scratch)
-                const int i = (k + 1) / tiles;
-                auto pick = [&](float a1, float a2, float a3) { return i == 1 ? a1 : i == 2 ? a2 : a3; };
-                build(float4{pick(xq[1].x, xq[2].x, xq[3].x), pick(xq[1].y, xq[2].y, xq[3].y),
-                             pick(xq[1].z, xq[2].z, xq[3].z), pick(xq[1].w, xq[2].w, xq[3].w)});
+        for (int i = 0; i < kWideMaxCols; i++) {  // unrolled: xc[i] stays in registers
+            if (i >= ncol) break;
+            const XOps4 xo = x_expand(xc[i]);
+            for (int t = 0; t < tiles; t++) {
+                const int k = i * tiles + t;
+                wait_vm<0>();
+                if (k + 1 < nunits) issue(k + 1);
+                const uint32_t a_h = rbase + TB * (k & 1) + n * PB;
+                float v;
+                if constexpr (TYPE == kQ4_K) {
+                    u32x4 hv;
+                    uint2 q[4];
+                    read_tile_superblock(a_h, a_h + 16 + 8 * g, hv, q);
+                    v = q4k_tile_superblock4(hv, q, xo);
+                } else if constexpr (TYPE == kQ5_K) {
+                    u32x4 hv;
+                    uint2 qh, q[4];
+                    read_tile_superblock5(a_h, a_h + 16 + 8 * g, a_h + 48 + 8 * g, hv, qh, q);
+                    v = q4k_tile_superblock4<true>(hv, q, xo, qh);
+                } else {
+                    uint32_t raw[20], dh[4];
+                    const uint32_t a_q = a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
+                    const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
+                    read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(a_q, a_d, raw, dh);
+                    v = q32_tile_piece<TYPE>(raw, dh, xo);
+                }
+                // lane n + 16 h: sub-blocks 2 c + h of row n
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[j] += t == j ? v : 0.0f;
             }
         }
         if (lane < 32)

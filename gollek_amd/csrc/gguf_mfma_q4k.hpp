@@ -141,14 +141,19 @@ struct XOps4 {
     float xs4[4], xs;
 };
 
+// The same operands held compactly (13 registers instead of 21) by kernels
+// that keep several superblocks' operands at once: d[c] = the eight bytes
+// of A[c] this lane holds, which x_expand places at A[c] bytes 0..7 (A rows
+// m < 4) or 8..15 (4 <= m < 8); rows m >= 8 hold zeros.
+struct XOpsC {
+    uint2 d[4];
+    float xs4[4], xs;
+};
+
 // Wave-wide: lane l holds elements 4 l .. 4 l + 3 of a superblock of x.
 // Writes the digit planes to `scratch` (1 KB of LDS private to the wave),
 // reads them back in the A operand layout and leaves the scratch free.
-// With PS, ps[c][p] = the integer sum of plane p's digits over sub-block
-// 2 c + h (h = (lane >> 4) & 1), for codes stored with an offset.
-template <bool PS = false>
-__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o,
-                                            int (*ps)[4] = nullptr) {
+__device__ __forceinline__ void x_operands4c(const float4 xv, uint32_t scratch, XOpsC &o) {
     const int lane = threadIdx.x & 63;
     const float v[4] = {xv.x, xv.y, xv.z, xv.w};
     uint32_t w[4];
@@ -163,42 +168,42 @@ __device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, X
         const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s8), 16 * c + 8));
         o.xs4[c] = h ? b : a;
     }
-    if constexpr (PS) {
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const int sp = sum8_i(__builtin_amdgcn_sdot4((int)w[p], 0x01010101, 0, false));
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int a = __builtin_amdgcn_readlane(sp, 16 * c);
-                const int b = __builtin_amdgcn_readlane(sp, 16 * c + 8);
-                ps[c][p] = h ? b : a;
-            }
-        }
-    }
     // A lane (m, g): plane p = m & 3 of elements 64 c + 8 g .. + 7 (sub-block
     // 2 c) for m < 4, of elements 64 c + 32 + 8 g .. + 7 (2 c + 1) for
-    // 4 <= m < 8; rows 8..15 are zero.
-    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = m >> 2;
-    uint2 dl[4], dh[4];
+    // 4 <= m < 8 (rows m >= 8 read the 4 <= m < 8 bytes and drop them).
+    const int m = lane & 15, g = lane >> 4, p = m & 3, ha = (m >> 2) & 1;
+    uint2 d[4];
     asm volatile(
         "s_waitcnt lgkmcnt(0)\n\t"
-        "ds_read_b64 %0, %8\n\t"
-        "ds_read_b64 %1, %8 offset:64\n\t"
-        "ds_read_b64 %2, %8 offset:128\n\t"
-        "ds_read_b64 %3, %8 offset:192\n\t"
-        "ds_read_b64 %4, %8 offset:32\n\t"
-        "ds_read_b64 %5, %8 offset:96\n\t"
-        "ds_read_b64 %6, %8 offset:160\n\t"
-        "ds_read_b64 %7, %8 offset:224\n\t"
+        "ds_read_b64 %0, %4\n\t"
+        "ds_read_b64 %1, %4 offset:64\n\t"
+        "ds_read_b64 %2, %4 offset:128\n\t"
+        "ds_read_b64 %3, %4 offset:192\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(dl[0]), "=&v"(dl[1]), "=&v"(dl[2]), "=&v"(dl[3]), "=&v"(dh[0]), "=&v"(dh[1]),
-          "=&v"(dh[2]), "=&v"(dh[3])
-        : "v"(scratch + 256 * p + 8 * g)
+        : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3])
+        : "v"(scratch + 256 * p + 8 * g + 32 * ha)
         : "memory");
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        o.A[c] = i32x4{ha == 0 ? (int)dl[c].x : 0, ha == 0 ? (int)dl[c].y : 0,
-                       ha == 1 ? (int)dh[c].x : 0, ha == 1 ? (int)dh[c].y : 0};
+    for (int c = 0; c < 4; c++) o.d[c] = m < 8 ? d[c] : uint2{0u, 0u};
+}
+
+__device__ __forceinline__ XOps4 x_expand(const XOpsC &c) {
+    const bool lo = (threadIdx.x & 15) < 4;
+    XOps4 o;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int a = (int)c.d[k].x, b = (int)c.d[k].y;
+        o.A[k] = i32x4{lo ? a : 0, lo ? b : 0, lo ? 0 : a, lo ? 0 : b};
+        o.xs4[k] = c.xs4[k];
+    }
+    o.xs = c.xs;
+    return o;
+}
+
+__device__ __forceinline__ void x_operands4(const float4 xv, uint32_t scratch, XOps4 &o) {
+    XOpsC c;
+    x_operands4c(xv, scratch, c);
+    o = x_expand(c);
 }
 
 // One superblock of a 16-row tile with four-plane x: lane n + 16 h returns
