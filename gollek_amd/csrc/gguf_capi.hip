@@ -656,8 +656,8 @@ static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_
     if (down->type_id == GOLLEK_HIP_Q6_K &&
         !gollek::moe_q6k_down_supported((int)n_experts, (int)H, (int)I, (int)tokens, (int)top_k))
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "Q6_K down experts need hidden <= 2048, inter <= 1024 (multiples of 256), <= 256 "
-                    "experts, top_k <= 64 and tokens * top_k <= 2048");
+                    "Q6_K down experts need hidden <= 4096 (past 2048 an even multiple of 256), "
+                    "inter <= 1024 (multiples of 256), <= 256 experts, top_k <= 64 and tokens * top_k <= 2048");
     for (gollek_hip_weight *w : {gate, up, down})
         if ((reinterpret_cast<uintptr_t>(w->data) & 15u) != 0)
             return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Expert weights must be 16-byte aligned");

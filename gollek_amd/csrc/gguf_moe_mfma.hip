@@ -150,11 +150,13 @@ __device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__re
 
 // Host-computed geometry of one pass.
 struct MoeTileGeom {
-    int nsb;          // superblocks per weight row (K / 256)
+    int nsb;          // superblocks per item row (K / 256, over halves)
+    int halves;       // K-halves per tile (pass 0 with K > 2048: 2; else 1)
     int rows_e;       // weight rows per expert
     int rt;           // 16-row tiles per item (pass 0: 1)
-    int tiles_e;      // items per expert and route group
-    uint32_t row_bytes, pitch;
+    int tiles_e;      // items per expert and route group (tiles x halves)
+    uint32_t row_bytes, pitch;  // bytes of an item's row, its LDS pitch
+    uint32_t stride;  // bytes of a weight row (halves x row_bytes)
     int part_dma;     // loads per matrix part (pass 0) or per item (pass 1)
     int ndma;         // loads per item
     int vec_len;      // vector length (K)
@@ -209,18 +211,25 @@ constexpr int kRecDwords = 14;
 // REC (MODE 0): h leaves as records (kRecDwords) for moe_down_combine_kernel;
 // otherwise as fp32 (out + p I + row).
 // vec: pass 0 x[T][H] (route p -> token p / top_k); pass 1 h[P][I] (route p).
-template <int MODE, bool REC>
+// HV (MODE 0): K-halves per tile.  With HV = 2 (hidden sizes past 2048) a
+// tile's two halves are consecutive items, each wave keeps both halves' x
+// operands, and the first half's gate / up row sums wait in LDS (hsave)
+// for the second's, so h = silu(gate) * up is formed once per row.
+template <int MODE, bool REC, int HV = 1>
 __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, MoeTileGeom G,
     const float *__restrict__ vec, int top_k, const int32_t *__restrict__ ids,
     const float *__restrict__ wts, int E, int P, float *__restrict__ out) {
     static_assert(MODE == 0 || !REC, "records are pass 0's output");
+    static_assert(HV == 1 || (HV == 2 && MODE == 0), "K-halves in pass 0 only");
     __shared__ __attribute__((aligned(16))) uint8_t ring[kMoSlots * kMoSlot + 1024];  // + sink
-    __shared__ __attribute__((aligned(16))) uint8_t scratch[kMoWaves][1024];  // digit build
+    // digit build; HV = 2: + the (half, route) x sums and scales from 768
+    __shared__ __attribute__((aligned(16))) uint8_t scratch[kMoWaves][HV == 2 ? 1088 : 1024];
     __shared__ float part[2][kMoGroup][kMoWaves][16];
     __shared__ float outv[kMoOutCap];
     __shared__ int outi[kMoOutCap];
     __shared__ int gid[kMoGroup];  // route ids of the current group
+    __shared__ float hsave[HV == 2 ? kMoGroup * 16 : 1][2];  // first-half gate / up sums
     __shared__ MoeRouteLds R;
 
     // Routing (the ring is free until the first loads below).
@@ -238,13 +247,16 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const int kpu = nunits > 0 ? (int)gridDim.x / nunits : 0;
     const bool unit_split = kpu >= 1 && 8 * ((int)gridDim.x - kpu * nunits) <= (int)gridDim.x;
     int i_begin, i_end;
+    // Slices are whole tiles (HV items each), so a tile's halves stay in
+    // one workgroup.
+    const int tpu = G.tiles_e / HV, ntiles = nitems / HV;
     if (unit_split) {
         const int unit = (int)blockIdx.x / kpu, sub = (int)blockIdx.x - unit * kpu;
-        i_begin = unit < nunits ? unit * G.tiles_e + sub * G.tiles_e / kpu : 0;
-        i_end = unit < nunits ? unit * G.tiles_e + (sub + 1) * G.tiles_e / kpu : 0;
+        i_begin = unit < nunits ? unit * G.tiles_e + HV * (sub * tpu / kpu) : 0;
+        i_end = unit < nunits ? unit * G.tiles_e + HV * ((sub + 1) * tpu / kpu) : 0;
     } else {
-        i_begin = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
-        i_end = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+        i_begin = HV * (int)((int64_t)blockIdx.x * ntiles / gridDim.x);
+        i_end = HV * (int)((int64_t)(blockIdx.x + 1) * ntiles / gridDim.x);
     }
     if (i_begin >= i_end) return;  // uniform, before any barrier
 
@@ -259,7 +271,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     // the next expert (dependent table reads per item would sit on the
     // critical path after every barrier).
     struct Item {
-        int u, e, group, tile, ntok, row0, nrows;
+        int u, e, group, tile, half, ntok, row0, nrows;
     };
     struct Cursor {
         int u, e, cnt, groups, group, tile;
@@ -297,9 +309,10 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         it.u = c.u;
         it.e = c.e;
         it.group = c.group;
-        it.tile = c.tile;
+        it.tile = c.tile / HV;
+        it.half = c.tile - HV * it.tile;
         it.ntok = min(kMoGroup, c.cnt - kMoGroup * c.group);
-        it.row0 = c.tile * rows_item;
+        it.row0 = it.tile * rows_item;
         it.nrows = min(rows_item, G.rows_e - it.row0);
         return it;
     };
@@ -316,7 +329,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         if (i < i_end) {
             for (; i_issue < i; i_issue++) step(c_issue);
             const Item it = item_of(c_issue);
-            base = (uint32_t)(((int64_t)it.e * G.rows_e + it.row0) * G.row_bytes);
+            base = (uint32_t)(((int64_t)it.e * G.rows_e + it.row0) * G.stride + (int64_t)it.half * G.row_bytes);
             nrows = it.nrows;
         }
         base = __builtin_amdgcn_readfirstlane(base);
@@ -330,7 +343,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             const bool ok = k < G.ndma && r < (uint32_t)nrows && col < G.row_bytes && base != kMaskedOffset;
             uint8_t *dst = k < G.ndma ? ring + slot * kMoSlot + 1024 * k : ring + kMoSlots * kMoSlot;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(second ? rs1 : rs0, (lds_ptr)dst, 16,
-                                                     ok ? base + r * G.row_bytes + col : kMaskedOffset,
+                                                     ok ? base + r * G.stride + col : kMaskedOffset,
                                                      0, 0, kStreamLoad);
         }
     };
@@ -350,8 +363,14 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 
     // Operands of the current route group: A per MFMA pair and chunk; per
     // output lane the sub-block sums and the superblock scale of its route.
-    i32x4 A[2][4];
-    float xs4[2][4], xs[2];
+    // HV = 2: [0] for the first half's superblock sb, [1] for sb + nsb; A is
+    // kept as the lane's two live dwords (Ac; rows m hold them in dwords
+    // 0, 1 when (m >> 2) & 1 == 0, else in 2, 3), expanded at the MFMA, and
+    // the sub-block sums and scales stay in the wave's scratch (9 floats at
+    // 768 + 36 (4 half + route)), read per pair.
+    i32x4 A[2][4];       // HV = 1
+    uint2 Ac[HV][2][4];  // HV = 2
+    float xs4[2][4], xs[2];  // HV = 1
     int cur_key = -1;  // e * 65536 + group of the operands held
 
     // Digits of route group `it` for this wave's superblock.
@@ -361,29 +380,45 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     // (drain = true) the vectors queue behind the ring's loads anyway.
     auto build = [&](const Item &it, bool drain, auto &&between) {
 #pragma unroll
-        for (int pp = 0; pp < 2; pp++)
+        for (int hf = 0; hf < HV; hf++) {
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                A[pp][c] = i32x4{0, 0, 0, 0};
-                xs4[pp][c] = 0.0f;
+            for (int pp = 0; pp < 2; pp++) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if constexpr (HV == 1) {
+                        A[pp][c] = i32x4{0, 0, 0, 0};
+                        xs4[pp][c] = 0.0f;
+                    } else {
+                        Ac[hf][pp][c] = uint2{0u, 0u};
+                    }
+                }
+                if constexpr (HV == 1) xs[pp] = 0.0f;
             }
-        xs[0] = xs[1] = 0.0f;
+        }
         if (!active) {
             between();
             return;
         }
         const uint32_t sbase = (uint32_t)(uintptr_t)(lds_ptr)scratch[wv];
-        float4 v[kMoGroup];
-        // loads first, then one wait (this also drains the ring's loads)
+        int vrow[kMoGroup];  // vector row of each route
 #pragma unroll
         for (int j = 0; j < kMoGroup; j++) {
             const int p = pairs[offsets[it.e] + kMoGroup * it.group + min(j, it.ntok - 1)];
             if (wv == 0 && lane == 0) gid[j] = p;  // route ids for the reductions
-            const int vi = MODE == 0 ? p / top_k : p;
-            v[j] = reinterpret_cast<const float4 *>(vec + (int64_t)vi * G.vec_len + sb * kQK)[lane];
+            vrow[j] = MODE == 0 ? p / top_k : p;
         }
-        between();
-        if (drain) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // A half at a time (HV = 2: the second half's vectors are loaded once
+        // the first half's digits are built, which keeps the registers in
+        // bounds; their wait also covers the ring loads issued before them).
+#pragma unroll
+        for (int hf = 0; hf < HV; hf++) {
+        float4 v[kMoGroup];
+        // loads first, then one wait (this also drains the ring's loads)
+#pragma unroll
+        for (int j = 0; j < kMoGroup; j++)
+            v[j] = reinterpret_cast<const float4 *>(vec + (int64_t)vrow[j] * G.vec_len + (sb + hf * G.nsb) * kQK)[lane];
+        if (hf == 0) between();
+        if (drain || hf > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         // Consume every loaded vector so the compiler's own wait comes here
         // (it cannot see the one above): a load it still thought outstanding
         // would make it wait for all loads before the next write of its registers.
@@ -424,13 +459,28 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 :
                 : "v"(sbase + 4 * lane), "v"(d0), "v"(d1), "v"(d2)
                 : "memory");
-            if ((lane & 7) == 0)
-                asm volatile("ds_write_b32 %0, %1 offset:768"
-                             :
-                             : "v"(sbase + 4 * (lane >> 3)), "v"(__float_as_int((float)sx * scale))
-                             : "memory");
-            if (lane == 0)
-                asm volatile("ds_write_b32 %0, %1 offset:832" : : "v"(sbase), "v"(__float_as_int(scale)) : "memory");
+            if constexpr (HV == 1) {
+                if ((lane & 7) == 0)
+                    asm volatile("ds_write_b32 %0, %1 offset:768"
+                                 :
+                                 : "v"(sbase + 4 * (lane >> 3)), "v"(__float_as_int((float)sx * scale))
+                                 : "memory");
+                if (lane == 0)
+                    asm volatile("ds_write_b32 %0, %1 offset:832" : : "v"(sbase), "v"(__float_as_int(scale)) : "memory");
+            } else {  // kept for the items: sums at + 4 sub-block, scale at + 32
+                // the slot offset enters through an asm so its address is
+                // formed here, not kept in a register across the item loop
+                uint32_t so = 768u + 36u * (uint32_t)(4 * hf + j);
+                asm volatile("" : "+v"(so));
+                const uint32_t slot = sbase + so;
+                if ((lane & 7) == 0)
+                    asm volatile("ds_write_b32 %0, %1"
+                                 :
+                                 : "v"(slot + 4 * (lane >> 3)), "v"(__float_as_int((float)sx * scale))
+                                 : "memory");
+                if (lane == 0)
+                    asm volatile("ds_write_b32 %0, %1 offset:32" : : "v"(slot), "v"(__float_as_int(scale)) : "memory");
+            }
             // A rows of route j: m = 8 (j & 1) + 4 ha + p in lanes m + 16 g; this
             // output lane's sub-blocks 2 c + h.
             const int m = lane & 15, p = m & 3, ha = (m >> 2) & 1;
@@ -461,16 +511,20 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 if (mine_in) {
-                    A[pp][c] = i32x4{ha == 0 ? (int)dl[c].x : 0, ha == 0 ? (int)dl[c].y : 0,
-                                     ha == 1 ? (int)dh[c].x : 0, ha == 1 ? (int)dh[c].y : 0};
+                    if constexpr (HV == 1)
+                        A[pp][c] = i32x4{ha == 0 ? (int)dl[c].x : 0, ha == 0 ? (int)dl[c].y : 0,
+                                         ha == 1 ? (int)dh[c].x : 0, ha == 1 ? (int)dh[c].y : 0};
+                    else
+                        Ac[hf][pp][c] = ha == 0 ? dl[c] : dh[c];
                 }
             }
-            if (tq == tj) {  // output lanes of route j
+            if (HV == 1 && tq == tj) {  // output lanes of route j
 #pragma unroll
                 for (int c = 0; c < 4; c++) xs4[pp][c] = xsv[c];
                 xs[pp] = sc;
             }
         }
+        }  // halves
     };
 
     // Results of item `it` from the partial sums in part[buf]: one wave per item.
@@ -480,10 +534,17 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             if (lane < it.ntok * 16) {
                 const int tk = lane >> 4, r = lane & 15;
                 if (r < it.nrows) {
-                    float gs = 0.0f, us = 0.0f;
+                    // the second half continues the first half's sums
+                    float gs = HV == 2 && it.half == 1 ? hsave[lane][0] : 0.0f;
+                    float us = HV == 2 && it.half == 1 ? hsave[lane][1] : 0.0f;
                     for (int s = 0; s < G.nsb; s++) {
                         gs += part[buf][tk][s][r];
                         us += part[buf][tk][G.nsb + s][r];
+                    }
+                    if (HV == 2 && it.half == 0) {  // uniform: no result yet
+                        hsave[lane][0] = gs;
+                        hsave[lane][1] = us;
+                        return;
                     }
                     const int p = gid[tk];
                     const int slot = base + tk * it.nrows + r;
@@ -509,7 +570,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     // The reduction of the previous item by its wave; every wave advances nout.
     auto reduce_prev = [&](const Item &it, int i_prev) {
         if (wv == i_prev % kMoWaves) reduce(it, i_prev & 1, nout);
-        nout += it.ntok * it.nrows;
+        if (HV == 1 || it.half == HV - 1) nout += it.ntok * it.nrows;
     };
     auto flush = [&]() {
         __syncthreads();
@@ -606,13 +667,50 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                                   (float)(mn47 & 0xFFu), (float)((mn47 >> 16) & 0xFFu)};
             const bool fin = __builtin_isfinite(d) && __builtin_isfinite(dmin);
             const int npairs = (cur.ntok + 1) >> 1;
+            // the half's operands by a compile-time index (a runtime pick of a
+            // register array would go through scratch)
+            const bool lo_dw = ((n >> 2) & 1) == 0;  // this lane's A row holds dwords 0, 1
+            // HV = 2: this lane's slot bases (route tq + 2 pp at + 72 pp + 144 half)
+            const uint32_t xl_s = (uint32_t)(uintptr_t)(lds_ptr)scratch[wv] + 36u * (uint32_t)tq;
+            const uint32_t xl_h = xl_s + 4u * (uint32_t)h;
+            // (half, pair) by compile-time indices: register arrays and LDS
+            // offsets stay fixed (a runtime index would go through scratch)
+            auto pairs_of = [&](auto hfc, auto ppc) {
+            constexpr int hf = decltype(hfc)::value, pp = decltype(ppc)::value;
+            {
+                if (pp >= npairs) return;  // uniform
+                // route 2 pp + tq's sums of sub-blocks 2 c + h and its scale
+                float xs4h[4], xsh;
+                if constexpr (HV == 1) {
 #pragma unroll
-            for (int pp = 0; pp < 2; pp++) {
-                if (pp >= npairs) break;  // uniform
+                    for (int c = 0; c < 4; c++) xs4h[c] = xs4[pp][c];
+                    xsh = xs[pp];
+                } else {
+                    constexpr int so = 768 + 36 * (4 * hf + 2 * pp);
+                    asm volatile(
+                        "ds_read_b32 %0, %5 offset:%7\n\t"
+                        "ds_read_b32 %1, %5 offset:%8\n\t"
+                        "ds_read_b32 %2, %5 offset:%9\n\t"
+                        "ds_read_b32 %3, %5 offset:%10\n\t"
+                        "ds_read_b32 %4, %6 offset:%11\n\t"
+                        "s_waitcnt lgkmcnt(0)"
+                        : "=&v"(xs4h[0]), "=&v"(xs4h[1]), "=&v"(xs4h[2]), "=&v"(xs4h[3]), "=&v"(xsh)
+                        : "v"(xl_h), "v"(xl_s), "n"(so), "n"(so + 8), "n"(so + 16), "n"(so + 24), "n"(so + 32)
+                        : "memory");
+                }
                 // the pair's four products first, then their plane combines
                 i32x4 D[4];
 #pragma unroll
-                for (int c = 0; c < 4; c++) D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[pp][c], B[c], zero4, 0, 0, 0);
+                for (int c = 0; c < 4; c++) {
+                    i32x4 a;
+                    if constexpr (HV == 1) {
+                        a = A[pp][c];
+                    } else {
+                        const int u0 = (int)Ac[hf][pp][c].x, u1 = (int)Ac[hf][pp][c].y;
+                        a = lo_dw ? i32x4{u0, u1, 0, 0} : i32x4{0, 0, u0, u1};
+                    }
+                    D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[c], zero4, 0, 0, 0);
+                }
                 int S[4];
 #pragma unroll
                 for (int c = 0; c < 4; c++)
@@ -623,23 +721,31 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
                         qs = fmaf(scf[c], (float)S[c], qs);
-                        mm = fmaf(mnf[c], xs4[pp][c], mm);
+                        mm = fmaf(mnf[c], xs4h[c], mm);
                     }
-                    v = fmaf(d * xs[pp], qs, -(dmin * mm));
+                    v = fmaf(d * xsh, qs, -(dmin * mm));
                 } else {
                     // the reference's (d sc) products; zero min codes skip a
                     // non-finite dmin (minContribution, RT/GgufKQuantLayout.java:67-69)
                     float qs = 0.0f, mm = 0.0f;
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        qs = fmaf(d * scf[c], xs[pp] * (float)S[c], qs);
-                        mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4[pp][c], mm);
+                        qs = fmaf(d * scf[c], xsh * (float)S[c], qs);
+                        mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4h[c], mm);
                     }
                     v = qs - mm;
                 }
                 // h = 1 half of row n: lane n + 16 (ds_swizzle, lanes xor 16)
                 const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
                 if (h == 0) part[i & 1][2 * pp + tq][wv][n] = v + other;
+            }
+            };
+            if (HV == 2 && cur.half == 1) {  // uniform
+                pairs_of(std::integral_constant<int, HV - 1>{}, std::integral_constant<int, 0>{});
+                pairs_of(std::integral_constant<int, HV - 1>{}, std::integral_constant<int, 1>{});
+            } else {
+                pairs_of(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+                pairs_of(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
             }
         }
         prev = cur;
@@ -1173,11 +1279,15 @@ namespace {
 MoeTileGeom make_geom(int mode, int E, int H, int I) {
     MoeTileGeom g{};
     const int K = mode == 0 ? H : I;
-    g.nsb = K / kQK;
+    // Gate/up items hold 16 rows of both matrices over at most 8
+    // superblocks: longer rows (an even count up to 16) are cut in halves.
+    g.halves = mode == 0 && K / kQK > 8 ? 2 : 1;
+    g.nsb = K / kQK / g.halves;
     g.rows_e = mode == 0 ? I : H;
     g.rt = mode == 0 ? 1 : min(16 / g.nsb, 8);
-    g.tiles_e = (g.rows_e + 16 * g.rt - 1) / (16 * g.rt);
+    g.tiles_e = g.halves * ((g.rows_e + 16 * g.rt - 1) / (16 * g.rt));
     g.row_bytes = (uint32_t)(g.nsb * kQKBlockBytes);
+    g.stride = (uint32_t)(g.halves * g.row_bytes);
     // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all banks
     g.pitch = ((g.row_bytes / 16) % 2 == 1) ? g.row_bytes : g.row_bytes + 16;
     const int part_bytes = 16 * g.rt * (int)g.pitch;
@@ -1185,7 +1295,7 @@ MoeTileGeom make_geom(int mode, int E, int H, int I) {
     g.ndma = mode == 0 ? 2 * g.part_dma : g.part_dma;
     g.vec_len = K;
     g.out_len = g.rows_e;
-    g.w_bytes = (int64_t)E * g.rows_e * g.row_bytes;
+    g.w_bytes = (int64_t)E * g.rows_e * g.stride;
     return g;
 }
 
@@ -1211,7 +1321,8 @@ bool make_down_geom(int E, int H, int I, int T, int top_k, bool q6, MoeDownGeom 
 }  // namespace
 
 bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x) {
-    if (H % kQK != 0 || I % kQK != 0 || H > 8 * kQK || I > 16 * kQK) return false;
+    if (H % kQK != 0 || I % kQK != 0 || H > 16 * kQK || I > 16 * kQK) return false;
+    if (H > 8 * kQK && (H / kQK) % 2 != 0) return false;  // halves of equal length
     if (E > kMoMaxExperts || P > kMoMaxRoutes) return false;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return false;  // (nullptr: shape only)
     for (int mode = 0; mode < 2; mode++) {
@@ -1247,8 +1358,12 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
     MoeDownGeom gd;
     int waves = 0;
     if (make_down_geom(E, H, I, T, top_k, q6, gd, waves)) {
-        hipLaunchKernelGGL((moe_expert_tile_kernel<0, true>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
-                           g0, x, top_k, ids, wts, E, P, hbuf);
+        if (g0.halves == 2)
+            hipLaunchKernelGGL((moe_expert_tile_kernel<0, true, 2>), dim3(grid), dim3(kMoThreads), 0, stream, gate,
+                               up, g0, x, top_k, ids, wts, E, P, hbuf);
+        else
+            hipLaunchKernelGGL((moe_expert_tile_kernel<0, true>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
+                               g0, x, top_k, ids, wts, E, P, hbuf);
         const dim3 dgrid((unsigned)(H / 16), (unsigned)((T + gd.tg - 1) / gd.tg));
         const size_t lds = 1024 + (size_t)waves * gd.wave_bytes;
         const uint8_t *hrec = ws + L.h;
@@ -1275,8 +1390,12 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
     }
     if (q6) return hipErrorNotSupported;  // only the token-major down pass reads Q6_K rows
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
-    hipLaunchKernelGGL((moe_expert_tile_kernel<0, false>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0,
-                       x, top_k, ids, wts, E, P, hbuf);
+    if (g0.halves == 2)
+        hipLaunchKernelGGL((moe_expert_tile_kernel<0, false, 2>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
+                           g0, x, top_k, ids, wts, E, P, hbuf);
+    else
+        hipLaunchKernelGGL((moe_expert_tile_kernel<0, false>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0,
+                           x, top_k, ids, wts, E, P, hbuf);
     hipLaunchKernelGGL((moe_expert_tile_kernel<1, false>), dim3(grid), dim3(kMoThreads), 0, stream, down,
                        (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
     hipError_t e = hipGetLastError();

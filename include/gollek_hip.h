@@ -192,8 +192,8 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, 
  * 217-240 with :461-472 (swigluFfn: .../engine/forward/
  * DirectForwardFfnService.java:40-61), reading each used expert once.  Other
  * weight types, hidden / inter above 4096, or Q6_K down experts beyond
- * hidden 2048 / inter 1024 / 256 experts / top_k 64 / 2048 routes ->
- * UNSUPPORTED. */
+ * hidden 4096 (past 2048: an even multiple of 256) / inter 1024 / 256
+ * experts / top_k 64 / 2048 routes -> UNSUPPORTED. */
 int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
                                gollek_hip_weight *down, int64_t n_experts, const float *x,
                                int64_t tokens, const int32_t *ids, const float *weights,

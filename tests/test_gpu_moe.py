@@ -34,11 +34,13 @@ def _experts(E, H, I, seed, down_type=syn.Q4_K):
 # when that leaves at most 1/8 of the grid idle (8 and 16 experts: tens of
 # workgroups per unit) and split the items evenly otherwise (the 128-expert
 # layer's 87 units; 210 and 314 units at 400 / 600 tokens x top-2).
-# Hidden 4096 is past the matrix-core passes (H <= 2048) and runs the v_dot4
-# expert kernels.
+# Hidden sizes past 2048 (an even number of superblocks up to 16) cut each
+# gate/up tile into two K-halves: 2560 (halves of 5), 3072 (of 6), 4096 (of
+# 8, with inter 1536 on the expert-major down pass).
 @pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
                                        (128, 2048, 768, 16, 8), (32, 512, 256, 400, 2),
-                                       (32, 512, 256, 600, 2), (8, 4096, 1536, 9, 2)])
+                                       (32, 512, 256, 600, 2), (8, 4096, 1536, 9, 2),
+                                       (8, 3072, 512, 5, 2), (16, 2560, 256, 12, 4)])
 def test_moe_parity(E, H, I, T, k):
     print(f"[gpu] moe E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H)
@@ -57,7 +59,8 @@ def test_moe_parity(E, H, I, T, k):
 # down pass reads them (inter 256 .. 1024; odd rows start 2 bytes off a
 # dword, so every tile takes the realigned reads).
 @pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
-                                       (128, 2048, 768, 16, 8), (32, 512, 1024, 40, 2)])
+                                       (128, 2048, 768, 16, 8), (32, 512, 1024, 40, 2),
+                                       (8, 4096, 512, 9, 2)])
 def test_moe_q6_k_down_parity(E, H, I, T, k):
     print(f"[gpu] moe q6_k down E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + 1, down_type=syn.Q6_K)
@@ -73,9 +76,10 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
 
 
 def test_moe_q6_k_down_rejects_unsupported_shapes():
-    # Q6_K down experts run only on the token-major down pass: inter above
-    # 1024 or hidden above 2048 -> UNSUPPORTED; Q5_K down is not taken.
-    for (E, H, I, dt) in [(4, 512, 1280, syn.Q6_K), (4, 4096, 256, syn.Q6_K), (4, 512, 256, syn.Q5_K)]:
+    # Q6_K down experts run only on the matrix-core passes' token-major down
+    # pass: inter above 1024, or hidden past 2048 with an odd number of
+    # superblocks (no equal K-halves) -> UNSUPPORTED; Q5_K down is not taken.
+    for (E, H, I, dt) in [(4, 512, 1280, syn.Q6_K), (4, 2304, 256, syn.Q6_K), (4, 512, 256, syn.Q5_K)]:
         gate, up, down, tg, tu, td = _experts(E, H, I, seed=1, down_type=dt)
         x = syn.activation(2 * H, seed=2).reshape(2, H)
         ids, w = syn.moe_routing(2, E, 2, seed=3)
