@@ -13,8 +13,9 @@ the headline matrix is also timed on the GGUF bytes in place.
 
 Secondary lines (in "extra"): the other GEMV configurations, the Q8_0 bf16
 MFMA GEMM (M = 16 / 128 / 512; TFLOP/s at M = 512 is the metric's second
-half) and the Q4_K MoE grouped FFN, each timed the same way; the GGUF file ->
-HBM upload rate (gollek_hip_gguf_upload, wall clock).
+half) and the Q4_K MoE grouped FFN (hidden 2048 with the routed block, and
+hidden 4096), each timed the same way; the GGUF file -> HBM upload rate
+(gollek_hip_gguf_upload, wall clock).
 
 cpu_baseline: the C restatement of the reference's Java raw mat-vec (oracle/)
 on this host's cores, on the same Q4_K matrix (rank 0, N = 1 only).
@@ -217,21 +218,24 @@ def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int):
     return res, host
 
 
-def moe_workload(torch, steps: int, warmup: int, seed: int):
+def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048, 768, 16),
+                 copies: int = 3, routed: bool = True):
+    """Grouped expert FFN over Q4_K experts, shape (experts, top_k, hidden,
+    inter, tokens); with `routed`, also the routed block (router -> top-k ->
+    the same FFN).  Weights rotate over `copies` whole layers."""
     import numpy as np
 
     from gollek_amd import synthetic as syn
     from gollek_amd import tensor_ops as ops
-    E, k, H, I, T = 128, 8, 2048, 768, 16
+    E, k, H, I, T = shape
     gate = syn.q4_k_matrix(E * I, H, seed)
     up = syn.q4_k_matrix(E * I, H, seed + 1)
     down = syn.q4_k_matrix(E * H, I, seed + 2)
     ids, w = syn.moe_routing(T, E, k, seed + 3)
     x = syn.activation(T * H, seed + 4).reshape(T, H)
-    # Three copies of the whole layer (3 x 340 MB): a copy is reused only after
-    # the other two layers' touched experts (> 400 MB) have streamed, so the
-    # 256 MB Infinity Cache cannot serve it.
-    copies = 3
+    # At 128 x 2048 x 768, three copies of the whole layer (3 x 340 MB): a copy
+    # is reused only after the other two layers' touched experts (> 400 MB)
+    # have streamed, so the 256 MB Infinity Cache cannot serve it.
     layers = []
     for _ in range(copies):
         bufs = [torch.from_numpy(a.reshape(-1)).cuda() for a in (gate, up, down)]
@@ -256,7 +260,13 @@ def moe_workload(torch, steps: int, warmup: int, seed: int):
     bytes_used = used * (gate.shape[1] * I + up.shape[1] * I + down.shape[1] * H) + 2 * T * H * 4
     res = {"ms_per_step": ms, "steps": n, "experts_touched": int(used),
            "algo_bytes": int(bytes_used), "algo_gbs": bytes_used / (ms * 1e-3) / 1e9,
-           "hbm_frac": bytes_used / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+           "hbm_frac": bytes_used / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "shape": {"experts": E, "top_k": k, "hidden": H, "inter": I, "tokens": T}}
+    if not routed:
+        for _, handles in layers:
+            for h in handles:
+                h.close()
+        return res, (gate, up, down, E, H, I, x, ids, w)
 
     # The routed block: router logits (seeded N(0, 2^2)) -> sigmoid top-8 on the
     # GPU -> the same grouped FFN (gollek_hip_moe_block_device).
@@ -622,6 +632,13 @@ def main() -> int:
             log("extra moe")
             extra["moe_q4_k_e128_top8_t16"], moe_inputs = moe_workload(torch, args.steps, args.warmup,
                                                                       seed=11)
+        if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e128_top8_t16_h4096"):
+            log("extra moe hidden 4096")
+            # 128 experts, top-8, hidden 4096, inter 1536 (two 1.36 GB layers
+            # of which 860 MB are touched: past the Infinity Cache)
+            extra["moe_q4_k_e128_top8_t16_h4096"] = moe_workload(
+                torch, args.steps, args.warmup, seed=13, shape=(128, 8, 4096, 1536, 16), copies=2,
+                routed=False)[0]
         if _has_symbol("gollek_hip_gguf_upload") and want("gguf_upload_q4_k_4096x14336"):
             log("extra gguf upload")
             extra["gguf_upload_q4_k_4096x14336"] = gguf_upload_workload(host, 14336, 4096)
