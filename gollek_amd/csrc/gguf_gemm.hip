@@ -938,10 +938,11 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__
                                                                  int64_t mn, float *__restrict__ y) {
     const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= mn) return;
+    // only the S partials are read (S is uniform); the sum runs in split order
     float4 b[8];
 #pragma unroll
     for (int k = 0; k < 8; k++)
-        b[k] = *reinterpret_cast<const float4 *>(part + (int64_t)(k < S ? k : 0) * mn + i);
+        if (k < S) b[k] = *reinterpret_cast<const float4 *>(part + (int64_t)k * mn + i);
     float4 a = b[0];
 #pragma unroll
     for (int k = 1; k < 8; k++) {
