@@ -740,12 +740,50 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 if (h == 0) part[i & 1][2 * pp + tq][wv][n] = v + other;
             }
             };
-            if (HV == 2 && cur.half == 1) {  // uniform
-                pairs_of(std::integral_constant<int, HV - 1>{}, std::integral_constant<int, 0>{});
-                pairs_of(std::integral_constant<int, HV - 1>{}, std::integral_constant<int, 1>{});
-            } else {
-                pairs_of(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-                pairs_of(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+            if constexpr (HV == 2) {
+                if (cur.half == 1) {  // uniform
+                    pairs_of(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+                    pairs_of(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+                } else {
+                    pairs_of(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+                    pairs_of(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+                }
+            } else {  // one half: the pairs in a loop (the form the hidden <= 2048 passes were tuned in)
+#pragma unroll
+            for (int pp = 0; pp < 2; pp++) {
+                if (pp >= npairs) break;  // uniform
+                // the pair's four products first, then their plane combines
+                i32x4 D[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[pp][c], B[c], zero4, 0, 0, 0);
+                int S[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    S[c] = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
+                float v;
+                if (fin) {
+                    float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        qs = fmaf(scf[c], (float)S[c], qs);
+                        mm = fmaf(mnf[c], xs4[pp][c], mm);
+                    }
+                    v = fmaf(d * xs[pp], qs, -(dmin * mm));
+                } else {
+                    // the reference's (d sc) products; zero min codes skip a
+                    // non-finite dmin (minContribution, RT/GgufKQuantLayout.java:67-69)
+                    float qs = 0.0f, mm = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        qs = fmaf(d * scf[c], xs[pp] * (float)S[c], qs);
+                        mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4[pp][c], mm);
+                    }
+                    v = qs - mm;
+                }
+                // h = 1 half of row n: lane n + 16 (ds_swizzle, lanes xor 16)
+                const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+                if (h == 0) part[i & 1][2 * pp + tq][wv][n] = v + other;
+            }
             }
         }
         prev = cur;
