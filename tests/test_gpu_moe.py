@@ -36,11 +36,16 @@ def _experts(E, H, I, seed, down_type=syn.Q4_K):
 # layer's 87 units; 210 and 314 units at 400 / 600 tokens x top-2).
 # Hidden sizes past 2048 (an even number of superblocks up to 16) cut each
 # gate/up tile into two K-halves: 2560 (halves of 5), 3072 (of 6), 4096 (of
-# 8, with inter 1536 on the expert-major down pass).
+# 8, with inter 1536 on the expert-major down pass).  The few-route cases
+# give every route group its own workgroups; 300 and 280 tokens x top-2
+# (~150 route groups on 256 workgroups) take the even split, whose slices
+# start on whole tiles so a tile's two halves stay in one workgroup (with
+# the token-major and the expert-major down pass respectively).
 @pytest.mark.parametrize("E,H,I,T,k", [(8, 512, 256, 4, 2), (16, 1024, 512, 9, 4),
                                        (128, 2048, 768, 16, 8), (32, 512, 256, 400, 2),
                                        (32, 512, 256, 600, 2), (8, 4096, 1536, 9, 2),
-                                       (8, 3072, 512, 5, 2), (16, 2560, 256, 12, 4)])
+                                       (8, 3072, 512, 5, 2), (16, 2560, 256, 12, 4),
+                                       (32, 4096, 256, 300, 2), (16, 3072, 1280, 280, 2)])
 def test_moe_parity(E, H, I, T, k):
     print(f"[gpu] moe E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H)
