@@ -30,7 +30,6 @@
 #include <mutex>
 #include <new>
 #include <thread>
-#include <vector>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -459,20 +458,22 @@ gollek_hip_weight *gollek_hip_gguf_upload(gollek_hip_gguf *f, int64_t index, cha
     };
     if (e == hipSuccess) {
         // Lanes 1.. on their own threads; the calling thread runs lane 0 and
-        // then any lane whose thread could not be started.
-        std::vector<std::thread> th;
-        std::vector<int> inline_lanes;
-        th.reserve((size_t)lanes);
+        // then any lane whose thread could not be started (fixed arrays: no
+        // allocation that could throw out of this entry point).
+        std::thread th[kLanes];
+        bool started[kLanes] = {};
         for (int l = 1; l < lanes; l++) {
             try {
-                th.emplace_back(lane, l);
+                th[l] = std::thread(lane, l);
+                started[l] = true;
             } catch (...) {
-                inline_lanes.push_back(l);
             }
         }
         lane(0);
-        for (int l : inline_lanes) lane(l);
-        for (std::thread &x : th) x.join();
+        for (int l = 1; l < lanes; l++)
+            if (!started[l]) lane(l);
+        for (int l = 1; l < lanes; l++)
+            if (started[l]) th[l].join();
         for (int l = 0; l < lanes && e == hipSuccess; l++) e = lane_err[l];
         // Wait for every queued DMA, also after an error in one lane.
         const hipError_t es = hipStreamSynchronize(f->stream);
