@@ -422,12 +422,15 @@ static int32_t matvec_host(gollek_hip_weight *w, const uint8_t *rows_base, int64
         hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
     // the prepared layout covers full mat-vecs only (its partition depends on the row count)
     const bool full = rows_base == w->data && nrows == w->rows;
+    // With the pinned staging the kernel stores y there itself (the buffer is
+    // mapped for the device; the stream synchronisation below makes the
+    // stores visible to the host), which saves the device-to-host copy.
+    float *k_y = hs != nullptr ? reinterpret_cast<float *>(hs + x_bytes) : d_y;
     if (e == hipSuccess)
-        e = gollek::launch_gemv(w->type_id, rows_base, w->row_bytes, w->cols, d_x, d_y, nrows,
+        e = gollek::launch_gemv(w->type_id, rows_base, w->row_bytes, w->cols, d_x, k_y, nrows,
                                 w->stream, full ? w->prep : nullptr, full ? w->prep_rows : 0);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(hs ? (void *)(hs + x_bytes) : (void *)y, d_y, y_bytes, hipMemcpyDeviceToHost,
-                           w->stream);
+    if (e == hipSuccess && hs == nullptr)
+        e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "matvec", err, err_len);
     if (hs != nullptr) std::memcpy(y, hs + x_bytes, y_bytes);
