@@ -389,14 +389,20 @@ int32_t gollek_hip_dequantize_rows(gollek_hip_weight *w, int64_t row0, int64_t n
     int32_t rc = use_device(w->device, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     const size_t bytes = (size_t)nrows * (size_t)w->cols * sizeof(float);
-    rc = ensure_staging(w, bytes, err, err_len);
-    if (rc != GOLLEK_HIP_OK) return rc;
-    float *d_out = reinterpret_cast<float *>(w->staging);
+    // With the pinned staging the kernel stores the rows there itself (the
+    // buffer is mapped for the device); otherwise through device staging and
+    // a device-to-host copy.
     uint8_t *hs = host_staging(w, bytes);
+    float *d_out = reinterpret_cast<float *>(hs);
+    if (hs == nullptr) {
+        rc = ensure_staging(w, bytes, err, err_len);
+        if (rc != GOLLEK_HIP_OK) return rc;
+        d_out = reinterpret_cast<float *>(w->staging);
+    }
     hipError_t e = gollek::launch_dequant(w->type_id, w->data, w->row_bytes, w->cols, row0, nrows,
                                           d_out, w->stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(hs ? (void *)hs : (void *)dst, d_out, bytes, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess && hs == nullptr)
+        e = hipMemcpyAsync(dst, d_out, bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "dequantize", err, err_len);
     if (hs != nullptr) std::memcpy(dst, hs, bytes);
