@@ -557,12 +557,15 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     if (hs != nullptr) std::memcpy(hs, x, xn);
     hipError_t e =
         hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
+    // With the pinned staging the kernels store Y there themselves (mapped
+    // for the device; x_bytes keeps it 256-byte aligned, so the split-K
+    // path stays available), which saves the device-to-host copy.
+    float *k_y = hs != nullptr ? reinterpret_cast<float *>(hs + x_bytes) : d_y;
     if (e == hipSuccess)
-        e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, d_x, d_y, (int)m, (int)w->rows,
+        e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, d_x, k_y, (int)m, (int)w->rows,
                                           (int)w->cols, w->stream, d_ws, ws_bytes);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(hs ? (void *)(hs + x_bytes) : (void *)y, d_y, y_bytes, hipMemcpyDeviceToHost,
-                           w->stream);
+    if (e == hipSuccess && hs == nullptr)
+        e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "gemm", err, err_len);
     if (hs != nullptr) std::memcpy(y, hs + x_bytes, y_bytes);
