@@ -932,20 +932,31 @@ int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
     float *d_w = reinterpret_cast<float *>(base + 2 * xb + lb + rb);
     uint8_t *d_ws = base + 2 * xb + lb + 2 * rb;
     hipStream_t s = gate->stream;
-    hipError_t e = hipMemcpyAsync(d_x, x, (size_t)(tokens * sh.H) * 4, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(d_l, logits, (size_t)(tokens * sh.E) * 4, hipMemcpyHostToDevice, s);
+    const size_t xn = (size_t)(tokens * sh.H) * 4, ln = (size_t)(tokens * sh.E) * 4;
+    // Pinned staging laid out as the device buffer (x | out | logits): the
+    // inputs go up in one copy and the expert passes store `out` into it.
+    uint8_t *hs = host_staging(gate, 2 * xb + lb);
+    hipError_t e = hipSuccess;
+    if (hs != nullptr) {
+        std::memcpy(hs, x, xn);
+        std::memcpy(hs + 2 * xb, logits, ln);
+        e = hipMemcpyAsync(d_x, hs, 2 * xb + lb, hipMemcpyHostToDevice, s);
+    } else {
+        e = hipMemcpyAsync(d_x, x, xn, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(d_l, logits, ln, hipMemcpyHostToDevice, s);
+    }
+    float *k_out = hs != nullptr ? reinterpret_cast<float *>(hs + xb) : d_out;
     if (e == hipSuccess)
         e = gollek::launch_moe_topk(d_l, (int)tokens, sh.E, (int)top_k,
                                     scoring == GOLLEK_HIP_ROUTER_SIGMOID, d_ids, d_w, s);
     if (e == hipSuccess)
         e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
                                    down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
-                                   (int)top_k, d_out, d_ws, s, sh.down_type);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(out, d_out, (size_t)(tokens * sh.H) * 4, hipMemcpyDeviceToHost, s);
+                                   (int)top_k, k_out, d_ws, s, sh.down_type);
+    if (e == hipSuccess && hs == nullptr) e = hipMemcpyAsync(out, d_out, xn, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "moe block", err, err_len);
+    if (hs != nullptr) std::memcpy(out, hs + xb, xn);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }
