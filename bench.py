@@ -194,11 +194,11 @@ def gemv_workload(torch, type_id: int, rows: int, cols: int, steps: int, warmup:
     return res, host
 
 
-def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int):
+def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int, type_id: int = 8,
+                  rows: int = 4096, cols: int = 4096):
     from gollek_amd import synthetic as syn
-    rows = cols = 4096
-    host = syn.q8_0_matrix(rows, cols, seed)
-    rot = Rotation(torch, host, syn.Q8_0, rows, cols)
+    host = syn.matrix(type_id, rows, cols, seed)
+    rot = Rotation(torch, host, type_id, rows, cols)
     xb = torch.from_numpy(syn.activation_bf16(m, cols, seed + 1).view("int16")).cuda()
     y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
 
@@ -403,27 +403,26 @@ def cpu_baseline(host, cols: int):
     return cpu_gemv(syn.Q4_K, host, cols, "Q4_K 14336x4096", budget_s=5.0)
 
 
-def cpu_gemm(host, m: int, seed: int):
-    """The reference's prefill for one Q8_0 Linear: m independent matVecRows
+def cpu_gemm(host, m: int, seed: int, type_id: int = 8, cols: int = 4096):
+    """The reference's prefill for one Linear: m independent matVecRows
     (RT/GgufTensorOps.java:666-674) over the rows of X (bf16 -> fp32
     exactly), each on all host cores.  Bounded: >= 3 reps."""
     from gollek_amd import synthetic as syn
     from oracle import oracle as o
-    cols = 4096
     xb = syn.activation_bf16(m, cols, seed)
     x = syn.bf16_to_f32(xb).reshape(m, cols)
     threads = o.default_threads()
 
     def run():
         for r in range(m):
-            o.matvec(syn.Q8_0, host, cols, x[r], threads=threads)
+            o.matvec(type_id, host, cols, x[r], threads=threads)
 
     med, n = _cpu_median(run, min_reps=3, budget_s=2.0, max_reps=50)
     flops = 2.0 * m * host.shape[0] * cols
     return {"value": flops / med / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
             "ms_per_gemm": med * 1e3, "weight_gbs_per_row_pass": host.size * m / med / 1e9,
-            "sample": (f"{m} mat-vecs of the Q8_0 4096x4096 matrix (one per row of X), median of "
-                       f"{n} reps after 2 warm-ups, {threads} threads per mat-vec; oracle")}
+            "sample": (f"{m} mat-vecs of the {host.shape[0]}x{cols} matrix (one per row of X), median "
+                       f"of {n} reps after 2 warm-ups, {threads} threads per mat-vec; oracle")}
 
 
 def cpu_moe(gate, up, down, E: int, H: int, I: int, x, ids, wts):
@@ -624,6 +623,14 @@ def main() -> int:
             if have_gemm and want(name):
                 log(f"extra {name}")
                 extra[name], gemm_host = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
+        # Q4_K / Q4_0 weights at the FFN shape (K 4096, N 14336).
+        for tname, t, ms in (("q4_k", syn.Q4_K, (16, 128, 512)), ("q4_0", syn.Q4_0, (128, 512))):
+            for m in ms:
+                name = f"{tname}_gemm_bf16_m{m}_4096x14336"
+                if have_gemm and want(name):
+                    log(f"extra {name}")
+                    extra[name], hosts[name] = gemm_workload(torch, m, args.steps, args.warmup, seed=9,
+                                                             type_id=t, rows=14336, cols=4096)
         if want("q4_k_gemv_host_entry_4096x14336"):
             log("extra host-buffer entry point")
             extra["q4_k_gemv_host_entry_4096x14336"] = host_entry_workload(
@@ -665,9 +672,23 @@ def main() -> int:
             for m in (16, 128, 512):
                 log(f"cpu baseline gemm m={m}")
                 cpus[f"q8_0_gemm_bf16_m{m}_4096x4096"] = cpu_gemm(gemm_host, m, seed=8)
+        for name in [k for k in hosts if "_gemm_" in k]:
+            m = int(name.split("_m")[1].split("_")[0])
+            if m > 128:
+                continue  # the m = 128 line's rate stands for it (m mat-vecs each)
+            log(f"cpu baseline {name}")
+            cpus[name] = cpu_gemm(hosts[name], m, seed=8, type_id=syn.Q4_K if name.startswith("q4_k") else syn.Q4_0)
         if moe_inputs is not None:
             log("cpu baseline moe")
             cpus["moe_q4_k_e128_top8_t16"] = cpu_moe(*moe_inputs)
+        # One shared description instead of a sample text per entry.
+        for c in cpus.values():
+            c.pop("sample", None)
+        extra["cpu_baselines_note"] = (
+            "oracle (C restatement of the reference Java raw route) on all host cores with the "
+            "reference's row chunking; GEMV: the full matrix, median of >= 10 reps after 2 "
+            "warm-ups; GEMM: m mat-vecs (the reference's prefill); MoE: every route's expert "
+            "mat-vecs per route, as the reference runs them")
         extra["cpu_baselines"] = cpus
 
     ms = head["ms_per_step"]
@@ -704,8 +725,60 @@ def main() -> int:
     g512 = extra.get("q8_0_gemm_bf16_m512_4096x4096")
     if g512:
         line["gemm_tflops_m512"] = round(g512["tflops"], 2)
-    print(json.dumps(line))
+    # Last key: one short entry per configuration, so that the end of the
+    # line (what a log tail keeps) carries every configuration's figure.
+    line["configs"] = config_summary(head, extra, cpu)
+    print(json.dumps(_rounded(line)))
     return 0
+
+
+# (summary name, extra key, roofline) for the configurations the metric and
+# its five configurations name, in that order.
+SUMMARY = (
+    ("C0_q8_0_gemv_4096x4096", "q8_0_gemv_4096x4096", "hbm"),
+    ("C1_q4_0_gemv_4096x11008", "q4_0_gemv_4096x11008", "hbm"),
+    ("C2a_q4_k_gemv_4096x14336", None, "hbm"),
+    ("C2b_q4_k_gemv_4096x128256", "q4_k_gemv_4096x128256", "hbm"),
+    ("C3_gemm_m16", "q8_0_gemm_bf16_m16_4096x4096", "hbm"),
+    ("C3_gemm_m128", "q8_0_gemm_bf16_m128_4096x4096", "both"),
+    ("C3_gemm_m512", "q8_0_gemm_bf16_m512_4096x4096", "mfma"),
+    ("C4_moe_e128_top8_t16", "moe_q4_k_e128_top8_t16", "hbm"),
+)
+
+
+def config_summary(head, extra, head_cpu=None):
+    """Per configuration: microseconds per launch, the fraction of the
+    roofline that bounds it (HBM 8 TB/s on algorithmic bytes, or dense bf16
+    MFMA 2.5 PFLOP/s) and the CPU baseline's rate where one was measured."""
+    cpus = extra.get("cpu_baselines", {})
+    out = {}
+    for name, key, bound in SUMMARY:
+        r = head if key is None else extra.get(key)
+        if not r:
+            continue
+        e = {"us": round(r["ms_per_step"] * 1e3, 2)}
+        if bound in ("hbm", "both"):
+            e["hbm_frac"] = round(r["algo_gbs"] / HBM_PEAK_GBS, 3)
+        if bound in ("mfma", "both"):
+            e["mfma_frac"] = round(r["mfma_frac"], 3)
+            e["tflops"] = round(r["tflops"], 1)
+        c = cpus.get(key) if key is not None else head_cpu
+        if c:
+            e["cpu"] = f"{c['value']:.1f} {c['unit'].split(' ')[0]}"
+        out[name] = e
+    return out
+
+
+def _rounded(obj):
+    """Floats to 4 significant digits (the timing noise is larger), so that
+    the one JSON line stays short."""
+    if isinstance(obj, float):
+        return float(f"{obj:.4g}") if math.isfinite(obj) else obj
+    if isinstance(obj, dict):
+        return {k: _rounded(v) for k, v in obj.items()}
+    if isinstance(obj, (list, tuple)):
+        return [_rounded(v) for v in obj]
+    return obj
 
 
 def _has_symbol(name: str) -> bool:

@@ -33,6 +33,7 @@ HIP_SOURCES = (
     "gguf_gemv_q6k_mfma.hip",
     "gguf_gemv_ring.hip",
     "gguf_gemm.hip",
+    "gguf_gemm_tile.hip",
     "gguf_moe.hip",
     "gguf_moe_mfma.hip",
     "gguf_moe_router.hip",

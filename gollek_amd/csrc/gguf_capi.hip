@@ -113,7 +113,7 @@ int g_initialised_device = -1;
 // process ends.  On the host, `scratch` only names that array; kernels get
 // the per-device address hipGetSymbolAddress returns, resolved once per
 // device (with the device current) when the library first sets it up.
-constexpr size_t kGemmScratchBytes = (size_t)8 << 20;  // gemm_workspace_bytes <= 8 MiB on 256 CUs
+constexpr size_t kGemmScratchBytes = (size_t)16 << 20;  // gemm_workspace_bytes < 16 MiB on 256 CUs
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) float scratch[kGemmScratchBytes / sizeof(float)];
 std::atomic<float *> g_scratch_ptr[kMaxDevices];
@@ -258,8 +258,6 @@ int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t 
     if (strcmp(key, "gemv_rows_per_wave") == 0) t.gemv_rows_per_wave = value;
     else if (strcmp(key, "gemv_row_batch") == 0) t.gemv_row_batch = (int)value;
     else if (strcmp(key, "gemv_waves_per_cu") == 0) t.gemv_waves_per_cu = value > 0 ? (int)value : 8;
-    else if (strcmp(key, "gemm_variant") == 0) t.gemm_variant = (int)value;
-    else if (strcmp(key, "gemm_big_config") == 0) t.gemm_big_config = (int)value;
     else if (strcmp(key, "gemv_variant") == 0) t.gemv_variant = (int)value;
     else if (strcmp(key, "moe_variant") == 0) t.moe_variant = (int)value;
     else return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Unknown option %s", key);
@@ -517,9 +515,9 @@ static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, in
     if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
     if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "input");
     if (y == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "output");
-    if (w->type_id != GOLLEK_HIP_Q8_0)
+    if (w->type_id != GOLLEK_HIP_Q8_0 && w->type_id != GOLLEK_HIP_Q4_0 && w->type_id != GOLLEK_HIP_Q4_K)
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "Unsupported GGUF bf16 GEMM type id: %d (Q8_0 only)", w->type_id);
+                    "Unsupported GGUF bf16 GEMM type id: %d (Q8_0, Q4_0 or Q4_K)", w->type_id);
     if (m < 0 || m > (int64_t)0x7FFFFFFF || w->rows > 0x7FFFFFFF || w->cols > 0x7FFFFFFF)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "GEMM shape %lld x %lld x %lld is out of range",
                     (long long)m, (long long)w->rows, (long long)w->cols);
@@ -545,7 +543,7 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     if (rc != GOLLEK_HIP_OK) return rc;
     const size_t x_bytes = align_up((size_t)(m * w->cols) * sizeof(uint16_t), 256);
     const size_t y_bytes = (size_t)(m * w->rows) * sizeof(float);
-    const size_t ws_bytes = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
+    const size_t ws_bytes = gollek::gemm_workspace_bytes(w->type_id, (int)m, (int)w->rows, (int)w->cols);
     const size_t ws_off = align_up(x_bytes + y_bytes, 256);
     rc = ensure_staging(w, ws_off + ws_bytes, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
@@ -562,8 +560,8 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     // path stays available), which saves the device-to-host copy.
     float *k_y = hs != nullptr ? reinterpret_cast<float *>(hs + x_bytes) : d_y;
     if (e == hipSuccess)
-        e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, d_x, k_y, (int)m, (int)w->rows,
-                                          (int)w->cols, w->stream, d_ws, ws_bytes);
+        e = gollek::launch_gemm_bf16(w->type_id, w->data, w->row_bytes, d_x, k_y, (int)m, (int)w->rows,
+                                     (int)w->cols, w->stream, d_ws, ws_bytes);
     if (e == hipSuccess && hs == nullptr)
         e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
@@ -578,14 +576,14 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
     const int32_t rc = check_gemm(w, x, y, m, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     // The handle's split-K workspace: allocated at the first call that splits,
-    // for the largest split any m of this weight uses (at most 8 MiB on 256
+    // for the largest split any m of this weight uses (below 16 MiB on 256
     // CUs), and kept until the handle is freed, so a launch in flight never
     // loses it.
-    const size_t need = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
+    const size_t need = gollek::gemm_workspace_bytes(w->type_id, (int)m, (int)w->rows, (int)w->cols);
     if (need > 0) {
         std::lock_guard<std::mutex> lock(w->mu);
         if (w->gemm_ws == nullptr) {
-            const size_t most = gollek::gemm_workspace_max_bytes((int)w->rows, (int)w->cols);
+            const size_t most = gollek::gemm_workspace_max_bytes(w->type_id, (int)w->rows, (int)w->cols);
             const size_t bytes = most > need ? most : need;
             const int32_t urc = use_device(w->device, err, err_len);
             if (urc != GOLLEK_HIP_OK) return urc;
@@ -597,9 +595,9 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
             w->gemm_ws_bytes = bytes;
         }
     }
-    hipError_t e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
-                                                 (int)w->cols, static_cast<hipStream_t>(stream),
-                                                 need ? w->gemm_ws : nullptr, w->gemm_ws_bytes);
+    hipError_t e = gollek::launch_gemm_bf16(w->type_id, w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
+                                            (int)w->cols, static_cast<hipStream_t>(stream),
+                                            need ? w->gemm_ws : nullptr, w->gemm_ws_bytes);
     if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -612,23 +610,20 @@ int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *w, const uint16_t
     // The split-K partials go to this GPU's static scratch: no allocation,
     // and every call on the GPU shares it (each split writes its whole
     // partial tile before the in-order reduction reads it, so nothing needs
-    // clearing; overlapping calls race).
-    const size_t need = gollek::gemm_workspace_bytes((int)m, (int)w->rows, (int)w->cols);
+    // clearing; overlapping calls race).  A shape whose splits would need more
+    // than the scratch holds is split less (the launcher picks the splits
+    // that fit), down to none.
+    const size_t need = gollek::gemm_workspace_bytes(w->type_id, (int)m, (int)w->rows, (int)w->cols);
     float *ws = nullptr;
     if (need > 0) {
-        if (need > kGemmScratchBytes)
-            return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
-                        "GEMM %lld x %lld x %lld needs %zu bytes of split-K scratch, more than the "
-                        "static %zu", (long long)m, (long long)w->rows, (long long)w->cols, need,
-                        kGemmScratchBytes);
         ws = (w->device >= 0 && w->device < kMaxDevices) ? g_scratch_ptr[w->device].load() : nullptr;
         if (ws == nullptr)
             return fail(GOLLEK_HIP_ERR_DEVICE, err, err_len,
                         "the static GEMM scratch of device %d is not set up", w->device);
     }
-    hipError_t e = gollek::launch_gemm_q8_0_bf16(w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
-                                                 (int)w->cols, static_cast<hipStream_t>(stream), ws,
-                                                 ws != nullptr ? kGemmScratchBytes : 0);
+    hipError_t e = gollek::launch_gemm_bf16(w->type_id, w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
+                                            (int)w->cols, static_cast<hipStream_t>(stream), ws,
+                                            ws != nullptr ? kGemmScratchBytes : 0);
     if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;

@@ -1,8 +1,8 @@
-// gguf_gemm.hip -- Q8_0 x bf16 small-M GEMM (prefill / batched decode) on
-// gfx950 bf16 MFMA, fp32 accumulate.
+// gguf_gemm.hip -- small-M GEMM (prefill / batched decode) dispatch, the
+// Q8_0 kernels for M <= 32 and the fallbacks for other shapes, on gfx950.
 //
-// Y[M, N] = X[M, K] . W[N, K]^T with X bf16 and W the GGUF Q8_0 matrix (the
-// Linear convention of runner/safetensor/gollek-safetensor-core/src/main/java/
+// Y[M, N] = X[M, K] . W[N, K]^T with X bf16 and W a GGUF matrix (the Linear
+// convention of runner/safetensor/gollek-safetensor-core/src/main/java/
 // tech/kayys/gollek/safetensor/core/tensor/AccelOps.java:370-376).  The
 // reference has no GGUF GEMM: its prefill runs M independent raw mat-vecs
 // (RT/GgufQ8RawDot.java:137-184, RT/ = runner/gguf/gollek-gguf-core/src/main/
@@ -14,21 +14,17 @@
 // fp32 result before accumulation -- the reference's own block structure.
 // Rounding q * d to bf16 instead would cost ~1e-3 relative error per weight.
 //
-// Kernels.  M > 32: gemm_q8_0_bf16_ring_kernel (128 x 64 workgroup tiles
-// fed by buffer->LDS loads, described below; when the tiles cover less than
-// half the CUs, as for M <= 256 at N = 4096, each tile's K range is split
-// over up to 8 workgroups whose partial tiles gemm_splitk_reduce_kernel sums
-// in split order, so the result does not depend on timing;
-// gemm_q8_0_bf16_big_kernel, the register-pipelined version of the same
-// tiling, remains selectable).  M <= 32: gemm_q8_0_bf16_skinny_kernel
-// (16-row column tiles, K split over the waves, one buffer->LDS ring per
-// wave).  Other shapes and the sweep variants: gemm_q8_0_bf16_kernel, where
-// a workgroup of 4 waves owns a BM x BN tile of Y; the waves split it WM x WN
+// Kernels.  Q8_0 with M <= 32: gemm_q8_0_bf16_skinny_kernel (16-row column
+// tiles, K split over the waves, one buffer->LDS ring per wave).  Q8_0, Q4_0
+// and Q4_K with K a multiple of 256 otherwise: the 128 x 128 tile kernel of
+// gguf_gemm_tile.hip.  Other shapes: gemm_q8_0_bf16_kernel, where a
+// workgroup of 4 waves owns a BM x BN tile of Y; the waves split it WM x WN
 // and, when WK > 1, also split each K stage (the partial tiles are summed
-// through LDS at the end).  Each stage moves
-// KB = 64 * WK columns of X (bf16) and W (Q8_0 block pairs, 68 aligned bytes,
-// realigned and widened to bf16 once per workgroup) into double-buffered LDS;
-// one barrier per stage.
+// through LDS at the end).  Each stage moves KB = 64 * WK columns of X (bf16)
+// and W (Q8_0 block pairs, 68 aligned bytes, realigned and widened to bf16
+// once per workgroup) into double-buffered LDS; one barrier per stage.  Any
+// remaining shape or alignment: one thread per output (gemm_q8_0_generic_kernel,
+// gemm_generic_kernel).
 #include <type_traits>
 
 #include "gguf_blocks.hpp"
@@ -247,714 +243,11 @@ __global__ __launch_bounds__(256) void gemm_q8_0_bf16_kernel(const uint8_t *__re
             }
 }
 
-// ---- large-M kernel -----------------------------------------------------------
-//
-// Workgroup tile 128 (M) x 64 (N), four waves of 64 x 32 (2 x 2), K in stages
-// of one Q8_0 block pair (64 columns).  Operands are staged in LDS as bf16
-// (X as stored, W converted once per workgroup: each int8 quant becomes an
-// exact bf16, each fp16 block scale an fp32), in 128-byte rows whose 16-byte
-// chunks are XOR-swizzled by row so the MFMA fragment reads are free of bank
-// conflicts.  Global loads run kPipe stages ahead in registers (raw buffer
-// loads: rows past M read zeros); one barrier per stage with two LDS buffers.
-// Per Q8_0 block every 16 x 16 output tile takes one v_mfma_f32_16x16x32_bf16
-// with a zero accumulator and the fp32 scale is applied with four FMAs.
-// Workgroups map to tiles so that each XCD's workgroups share M tiles: X,
-// re-read by every N tile, then comes from that XCD's L2.
-
 namespace {
-
-constexpr int kBigBM = 128, kBigBN = 64;
-
-// Byte offset of bf16 chunk kc (8 elements) of row r in a tile of 128-byte
-// rows whose 16-byte chunks are XOR-swizzled by row pair, so the 16-byte
-// fragment reads of 16 consecutive rows fall in distinct banks.
-constexpr int kRowStride = 128;
-__device__ __forceinline__ uint32_t swz(int r, int kc) {
-    return (uint32_t)(r * kRowStride + 16 * (kc ^ ((r >> 1) & 7)));
-}
-
-template <int XCH>
-struct BigRegs {
-    u32x4 x[XCH];  // 16-byte chunks of X
-    u32x4 q;       // W quant dwords
-    uint32_t q5;   // fifth quant dword (even block) or the scale dword (odd block)
-};
-
-struct BigStage {
-    uint8_t x[kBigBM * kRowStride];
-    uint8_t w[kBigBN * kRowStride];
-    float d[kBigBN][4];  // [.][b] block scales; [.][2 + b] unused (see stash)
-};
-
-}  // namespace
-
-template <int kPipe, int WAVES_M, int WAVES_N>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_q8_0_bf16_big_kernel(
-    const uint8_t *__restrict__ W, int64_t row_bytes, const uint16_t *__restrict__ X,
-    float *__restrict__ Y, int M, int N, int K) {
-    constexpr int NTH = 64 * WAVES_M * WAVES_N;
-    constexpr int WM = kBigBM / WAVES_M, WN = kBigBN / WAVES_N;
-    constexpr int MT = WM / 16, NT = WN / 16;
-    constexpr int XCH = kBigBM * 8 / NTH;   // X chunks per thread per stage
-    constexpr int WIT = kBigBN * 4;          // W (row, block, half) items per stage
-    static_assert(XCH * NTH == kBigBM * 8 && WIT <= NTH && NTH % WIT == 0, "staging split");
-    __shared__ __attribute__((aligned(16))) BigStage st[2];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int n_tiles = N / kBigBN;
-    // Tiles in M-major order t = m * n_tiles + n.  Workgroups are dealt to the
-    // eight XCDs round robin (blockIdx % 8), so when the grid divides by 8,
-    // XCD j takes the contiguous tiles [j G/8, (j+1) G/8): its workgroups share
-    // one or two M tiles and the X rows they read stay in that XCD's L2.
-    const int G = (int)gridDim.x;
-    const int t = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
-    const int mt_idx = t / n_tiles, nt_idx = t % n_tiles;
-    const int m0 = mt_idx * kBigBM, n0 = nt_idx * kBigBN;
-    const int nst = K / 64;
-
-    // X rows m0.. (zeros past M), W rows n0.. (N % 64 == 0 by dispatch).
-    const __amdgpu_buffer_rsrc_t xs = wave_buffer(
-        reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2,
-        (uint32_t)((int64_t)(M - m0 < kBigBM ? M - m0 : kBigBM) * K * 2));
-    const __amdgpu_buffer_rsrc_t ws =
-        wave_buffer(W + (int64_t)n0 * row_bytes, (uint32_t)(kBigBN * row_bytes));
-
-    // Staging roles.  X: chunks c = tid + NTH i (row c / 8, chunk c % 8).
-    // W: item tid % WIT: row, block (0/1) and 16-quant half of the pair; with
-    // more threads than items the spares repeat an item (same loads, same
-    // values to the same LDS bytes), which keeps the code free of branches.
-    const int wit = tid % WIT;
-    const int wr = wit >> 2, wb = (wit >> 1) & 1, wu = wit & 1;
-    const uint32_t w_q = (uint32_t)(wr * row_bytes) + (wb ? 36u + 16u * wu : 16u * wu);
-    const uint32_t w_5 = (uint32_t)(wr * row_bytes) + (wb ? 32u : 16u * wu + 16u);
-
-    // Loads of stage s; stages past the end read zeros (masked offsets), so
-    // every pipeline step issues the same loads and the load counters stay
-    // exact (a conditional load would make the compiler wait for all of them).
-    auto load = [&](BigRegs<XCH> &R, int s) {
-        const bool live = s < nst;
-        const uint32_t k0b = (uint32_t)s * 128u;  // bf16 bytes
-#pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const int c = tid + NTH * i;
-            const uint32_t o = (uint32_t)((c >> 3) * K * 2) + k0b + 16u * (c & 7);
-            R.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xs, live ? o : kMaskedOffset, 0, 0);
-        }
-        const uint32_t pb = (uint32_t)s * 68u;
-        R.q = __builtin_amdgcn_raw_buffer_load_b128(ws, live ? w_q + pb : kMaskedOffset, 0, 0);
-        R.q5 = __builtin_amdgcn_raw_buffer_load_b32(ws, live ? w_5 + pb : kMaskedOffset, 0, 0);
-    };
-    auto stash = [&](const BigRegs<XCH> &R, BigStage &S) {
-#pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const int c = tid + NTH * i;
-            *reinterpret_cast<u32x4 *>(S.x + swz(c >> 3, c & 7)) = R.x[i];
-        }
-        // Even blocks: the quants start 2 bytes into the first dword.
-        const int sh = wb ? 0 : 2;
-        uint32_t qd[4];
-        qd[0] = __builtin_amdgcn_alignbyte(R.q.y, R.q.x, sh);
-        qd[1] = __builtin_amdgcn_alignbyte(R.q.z, R.q.y, sh);
-        qd[2] = __builtin_amdgcn_alignbyte(R.q.w, R.q.z, sh);
-        qd[3] = __builtin_amdgcn_alignbyte(R.q5, R.q.w, sh);
-        uint32_t o[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) i8x4_to_bf16(qd[j], o[2 * j], o[2 * j + 1]);
-        const int kc = 4 * wb + 2 * wu;
-        *reinterpret_cast<u32x4 *>(S.w + swz(wr, kc)) = u32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<u32x4 *>(S.w + swz(wr, kc + 1)) = u32x4{o[4], o[5], o[6], o[7]};
-        // Only the first half of an even block holds its scale; the second half
-        // stores into a slot nobody reads (d[.][2 + b]) instead of branching.
-        S.d[wr][wb + 2 * wu] = half_bits_to_float_fast(wb ? (R.q5 >> 16) : R.q.x);
-    };
-
-    f32x4 acc[MT][NT];
-#pragma unroll
-    for (int a = 0; a < MT; a++)
-#pragma unroll
-        for (int b = 0; b < NT; b++) acc[a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // Pipeline: registers hold stages s + 1 .. s + kPipe; LDS buffer s & 1
-    // holds stage s.  In stage s a wave issues its MFMAs, then converts and
-    // writes stage s + 1 into the other buffer while they run, applies the
-    // scales, and meets the others at the one barrier of the stage.
-    // The host guarantees nst % kPipe == 0 and nst >= kPipe, so the steady
-    // state below has no branches around loads.
-    BigRegs<XCH> R[kPipe];
-#pragma unroll
-    for (int j = 0; j < kPipe; j++) load(R[j], j);
-    stash(R[0], st[0]);
-    load(R[0], kPipe);
-    __syncthreads();
-
-    const int lr = lane & 15, lk = lane >> 4;
-    for (int s0 = 0; s0 < nst; s0 += kPipe) {
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) {
-            const int s = s0 + j;
-            const BigStage &S = st[s & 1];
-            f32x4 part[2][MT][NT];
-            float dsc[2][NT];
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                bf16x8 A[MT], B[NT];
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                    A[mt] = *reinterpret_cast<const bf16x8 *>(S.x + swz(wm * WM + mt * 16 + lr, 4 * kb + lk));
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    B[nt] = *reinterpret_cast<const bf16x8 *>(S.w + swz(wn * WN + nt * 16 + lr, 4 * kb + lk));
-                    dsc[kb][nt] = S.d[wn * WN + nt * 16 + lr][kb];
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                    for (int nt = 0; nt < NT; nt++)
-                        part[kb][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            A[mt], B[nt], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            }
-            // Stage s + 1 sits in R[(j + 1) % kPipe]: write it to the other
-            // buffer while the MFMAs run (past the last stage this writes
-            // zeros nobody reads), then refill the slot with s + 1 + kPipe.
-            BigRegs<XCH> &Rn = R[(j + 1) % kPipe];
-            stash(Rn, st[(s + 1) & 1]);
-            load(Rn, s + 1 + kPipe);
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                        for (int v = 0; v < 4; v++)
-                            acc[mt][nt][v] = fmaf(dsc[kb][nt], part[kb][mt][nt][v], acc[mt][nt][v]);
-            __syncthreads();
-        }
-    }
-
-    // D layout of a 16x16 tile: lane holds column lane & 15, rows 4 (lane >> 4) + v.
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = m0 + wm * WM + mt * 16 + 4 * lk + v;
-                const int n = n0 + wn * WN + nt * 16 + lr;
-                if (m < M) Y[(int64_t)m * N + n] = acc[mt][nt][v];
-            }
-}
-
-// ---- large-M ring kernel --------------------------------------------------------
-//
-// Same 128 x 64 workgroup tile, eight waves of 32 x 32 and the same MFMA /
-// scale arithmetic as gemm_q8_0_bf16_big_kernel, with the operands moved by
-// buffer->LDS loads into a ring of six stage slots:
-//   - X: the stage's 128 rows x 64 columns of bf16 land directly in the
-//     XOR-swizzled layout of swz() (each lane loads the global chunk that
-//     belongs at its LDS position);
-//   - W: each row's 68-byte stage piece (a Q8_0 block pair) lands raw, its
-//     dwords 0..15 as four 16-byte chunks and dword 16 in a separate array.
-// The workgroup widens W to bf16 (and the block scales to fp32) two stages
-// ahead into one of three converted-W buffers.  The work of stage s is spread
-// so that the units overlap: right after the stage's one barrier each wave
-// issues the MFMAs of stage s from fragments it read during stage s - 1,
-// then the loads of stage s + 5, reads the fragments of stage s + 1, widens
-// stage s + 2, and applies the block scales to the MFMA results of stage
-// s - 1.  The loop is unrolled by the six slots so that every LDS address is
-// a per-lane register plus an immediate.  The LDS reads of ring data and all
-// LDS writes in the loop are inline asm: the compiler cannot tell which
-// buffer->LDS load wrote which bytes and would otherwise wait for every load
-// in flight.
-//
-// Default (LOADERS): two more waves issue every load of the ring and wait for
-// them before each barrier, so the eight compute waves never stall at a load
-// issue when the CU's queue of outstanding requests is full (measured on
-// MI355X at M = 512: 36-37 us against 38-39 us with every wave loading).
-
-namespace {
-
-constexpr int kRgSlots = 6;
-constexpr int kRgXBytes = kBigBM * kRowStride;                  // X stage (bf16, swizzled)
-constexpr int kRgWQBytes = kBigBN * 64;                         // W dwords 0..15 per row
-constexpr int kRgW16Bytes = kBigBN * 4;                         // W dword 16 per row
-constexpr int kRgSlot = kRgXBytes + kRgWQBytes + kRgW16Bytes;   // 20736 bytes
-constexpr int kRgWbBytes = kBigBN * kRowStride;                 // converted W (bf16, swizzled)
-constexpr int kRgWbuf = kRgWbBytes + kBigBN * 8;                // + fp32 scales [row][2]
-constexpr int kRgWbufs = 3;
-constexpr int kRgDmaPerWave = 3;                                // 2 X + 1 W (or sink) per stage
-constexpr int kRgLds = kRgSlots * kRgSlot + kRgWbufs * kRgWbuf + 256;
-static_assert(kRgLds <= 160 * 1024, "LDS budget");
-// Slots 0..2 and 3..5 are addressed from two base registers so that every
-// offset fits the 16-bit immediate of the DS instructions.
-static_assert(2 * kRgSlot + kRgSlot <= 65536, "slot group offsets");
-
-// The stage's MFMA operands of one wave: A for blocks (kb) x rows (mt), B for
-// blocks x columns (nt), and the fp32 scale pairs of its two 16-column groups.
-struct RingFrags {
-    u32x4 a00, a01, a10, a11;  // a[kb][mt]
-    u32x4 b00, b01, b10, b11;  // b[kb][nt]
-    uint2 d0, d1;              // {d[n][0], d[n][1]} for nt = 0, 1
-};
-
-// Issues the reads only: the registers are valid after ring_wait() names them.
-template <int XO, int WO>
-__device__ __forceinline__ void ring_read_frags(uint32_t xa0, uint32_t xa1, uint32_t wb0,
-                                                uint32_t wb1, uint32_t dd, RingFrags &f) {
-    asm volatile(
-        "ds_read_b128 %0, %10 offset:%15\n\t"
-        "ds_read_b128 %1, %10 offset:%16\n\t"
-        "ds_read_b128 %2, %11 offset:%15\n\t"
-        "ds_read_b128 %3, %11 offset:%16\n\t"
-        "ds_read_b128 %4, %12 offset:%17\n\t"
-        "ds_read_b128 %5, %12 offset:%18\n\t"
-        "ds_read_b128 %6, %13 offset:%17\n\t"
-        "ds_read_b128 %7, %13 offset:%18\n\t"
-        "ds_read_b64 %8, %14 offset:%17\n\t"
-        "ds_read_b64 %9, %14 offset:%19"
-        : "=&v"(f.a00), "=&v"(f.a01), "=&v"(f.a10), "=&v"(f.a11), "=&v"(f.b00), "=&v"(f.b01),
-          "=&v"(f.b10), "=&v"(f.b11), "=&v"(f.d0), "=&v"(f.d1)
-        : "v"(xa0), "v"(xa1), "v"(wb0), "v"(wb1), "v"(dd), "n"(XO), "n"(XO + 2048), "n"(WO),
-          "n"(WO + 2048), "n"(WO + 128)
-        : "memory");
-}
-
-// Three raw dwords of a W piece (separate addresses: dword 16 lives apart)
-// and the scale dword; issued only, valid after ring_wait().
-template <int OFF>
-__device__ __forceinline__ void ring_read_raw(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
-                                              uint32_t &d0, uint32_t &d1, uint32_t &d2,
-                                              uint32_t &d3) {
-    asm volatile(
-        "ds_read_b32 %0, %4 offset:%8\n\t"
-        "ds_read_b32 %1, %5 offset:%8\n\t"
-        "ds_read_b32 %2, %6 offset:%8\n\t"
-        "ds_read_b32 %3, %7 offset:%8"
-        : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3)
-        : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "n"(OFF)
-        : "memory");
-}
-
-template <int OFF, typename T>
-__device__ __forceinline__ void ring_read(uint32_t a, T &v) {
-    if constexpr (sizeof(T) == 16)
-        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
-    else
-        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
-}
-
-// Waits for every LDS read in flight.  The registers the reads write pass
-// through the statement, so no use of them can be scheduled before it.
-__device__ __forceinline__ void ring_wait(RingFrags &f, uint32_t &d0, uint32_t &d1, uint32_t &d2,
-                                          uint32_t &d3) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(f.a00), "+v"(f.a01), "+v"(f.a10), "+v"(f.a11), "+v"(f.b00), "+v"(f.b01),
-                   "+v"(f.b10), "+v"(f.b11), "+v"(f.d0), "+v"(f.d1), "+v"(d0), "+v"(d1), "+v"(d2),
-                   "+v"(d3)
-                 :
-                 : "memory");
-}
-
-template <int OFF>
-__device__ __forceinline__ void ring_store4(uint32_t addr, u32x4 v) {
-    asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF) : "memory");
-}
-
-template <int OFF>
-__device__ __forceinline__ void ring_store1(uint32_t addr, float v) {
-    asm volatile("ds_write_b32 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF) : "memory");
-}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 }  // namespace
-
-template <bool LOADERS>
-__global__ __launch_bounds__(LOADERS ? 640 : 512) void gemm_q8_0_bf16_ring_kernel(const uint8_t *__restrict__ W,
-                                                                  int64_t row_bytes,
-                                                                  const uint16_t *__restrict__ X,
-                                                                  float *__restrict__ Y, int M,
-                                                                  int N, int K, int S,
-                                                                  float *__restrict__ partials) {
-    constexpr int NS = kRgSlots;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kRgLds];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-
-    // Tile order: groups of up to four M tiles, N-major inside a group, so
-    // that the workgroups an XCD runs at one time (the contiguous range
-    // [j G/8, (j+1) G/8) when the grid divides by 8, workgroups being dealt
-    // to XCDs round robin) share their X rows and W rows in that XCD's L2.
-    // With S > 1 (split-K) the S workgroups of a tile are adjacent in this
-    // order and split k takes stages [k nst, (k + 1) nst) of K, writing its
-    // partial tile to partials[k] (summed in split order by a second kernel).
-    const int m_tiles = (M + kBigBM - 1) / kBigBM;
-    const int n_tiles = N / kBigBN;
-    const int G = (int)gridDim.x;
-    const int v = (G % 8 == 0) ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
-    const int t = v / S, split = v - t * S;
-    const int group = t / (4 * n_tiles);
-    const int first_m = 4 * group;
-    const int gm = m_tiles - first_m < 4 ? m_tiles - first_m : 4;
-    const int local = t - group * 4 * n_tiles;
-    const int mt_idx = first_m + local % gm, nt_idx = local / gm;
-    const int m0 = mt_idx * kBigBM, n0 = nt_idx * kBigBN;
-    const int nst = K / 64 / S;
-    const int s0 = split * nst;
-
-    // X rows m0.. (zeros past M), W rows n0.. (N % 64 == 0 by dispatch), both
-    // from the split's first column.  Loads of stages past the last one read
-    // the following bytes of the same buffers (or zeros past their ends) into
-    // slots that are never used.
-    const __amdgpu_buffer_rsrc_t xs = wave_buffer(
-        reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2 + (int64_t)s0 * 128,
-        (uint32_t)((int64_t)(M - m0 < kBigBM ? M - m0 : kBigBM) * K * 2 - (int64_t)s0 * 128));
-    const __amdgpu_buffer_rsrc_t ws = wave_buffer(W + (int64_t)n0 * row_bytes + (int64_t)s0 * 68,
-                                                  (uint32_t)(kBigBN * row_bytes - (int64_t)s0 * 68));
-
-    uint8_t *const sink = lds + NS * kRgSlot + kRgWbufs * kRgWbuf;
-    const uint32_t base0 = (uint32_t)(uintptr_t)(lds_ptr)lds;
-    const uint32_t base1 = base0 + 3u * kRgSlot;
-    const uint32_t wbase = base0 + (uint32_t)(NS * kRgSlot);
-
-    if constexpr (LOADERS) {
-        if (wave >= 8) {
-            // Loader waves (the eight compute waves issue no loads): wave 8
-            // moves X chunks 0..9 and dword 16 of every W row, wave 9 X chunks
-            // 10..15, the four W chunks and one sink load: 11 each per stage.
-            const int lw = wave - 8;
-            auto load_stage = [&](int st) {
-                uint8_t *slot = lds + (st % NS) * kRgSlot;
-                const uint32_t xk = (uint32_t)st * 128u, wk = (uint32_t)st * 68u;
-                if (lw == 0) {
-#pragma unroll
-                    for (int c = 0; c < 10; c++) {
-                        const int p = 64 * c + lane;
-                        const int r = p >> 3, kc = (p & 7) ^ ((r >> 1) & 7);
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                            xs, (lds_ptr)(slot + 1024 * c), 16,
-                            (uint32_t)r * (uint32_t)(2 * K) + 16u * (uint32_t)kc + xk, 0, 0, 0);
-                    }
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)(slot + kRgXBytes + kRgWQBytes), 4,
-                                                             (uint32_t)lane * (uint32_t)row_bytes + 64u + wk, 0,
-                                                             0, 0);
-                } else {
-#pragma unroll
-                    for (int c = 10; c < 16; c++) {
-                        const int p = 64 * c + lane;
-                        const int r = p >> 3, kc = (p & 7) ^ ((r >> 1) & 7);
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                            xs, (lds_ptr)(slot + 1024 * c), 16,
-                            (uint32_t)r * (uint32_t)(2 * K) + 16u * (uint32_t)kc + xk, 0, 0, 0);
-                    }
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int q = 64 * c + lane;
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                            ws, (lds_ptr)(slot + kRgXBytes + 1024 * c), 16,
-                            (uint32_t)(q >> 2) * (uint32_t)row_bytes + 16u * (uint32_t)(q & 3) + wk, 0, 0, 0);
-                    }
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)sink, 4, kMaskedOffset, 0, 0, 0);
-                }
-            };
-            for (int st = 0; st < NS - 1; st++) load_stage(st);
-            // The compute waves' two prologue barriers: stages 0..2 landed,
-            // then stages 0 and 1 widened.
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(11 * (NS - 3)) : "memory");
-            asm volatile("s_barrier" ::: "memory");
-            for (int st = 0; st < nst; st++) {
-                // Stage st + 2 has landed; stage st - 1's slot is free.
-                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(11 * (NS - 4)) : "memory");
-                load_stage(st + NS - 1);
-            }
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            return;
-        }
-    }
-
-    // Loads of a stage.  X: wave w moves LDS chunks 64 (2w + i) + lane of the
-    // slot, i.e. row r = chunk / 8 at swizzled position chunk % 8, which holds
-    // the row's 16-byte column chunk kc = position ^ ((r >> 1) & 7).  W: waves
-    // 0..3 move 16-byte chunks (row = chunk / 4, part chunk % 4) of dwords
-    // 0..15, wave 4 moves dword 16 of every row, waves 5..7 issue a masked
-    // load into a sink so that every wave has the same count in flight.
-    uint32_t xo[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int p = 64 * (2 * wave + i) + lane;
-        const int r = p >> 3, kc = (p & 7) ^ ((r >> 1) & 7);
-        xo[i] = (uint32_t)r * (uint32_t)(2 * K) + 16u * (uint32_t)kc;
-    }
-    const int wp = 64 * wave + lane;
-    const uint32_t wo = wave < 4 ? (uint32_t)(wp >> 2) * (uint32_t)row_bytes + 16u * (uint32_t)(wp & 3)
-                                 : (uint32_t)lane * (uint32_t)row_bytes + 64u;
-    auto issue_x = [&](int s, uint8_t *slot, int i) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, (lds_ptr)(slot + 1024 * (2 * wave + i)), 16,
-                                                 xo[i] + (uint32_t)s * 128u, 0, 0, 0);
-    };
-    auto issue_w = [&](int s, uint8_t *slot) {
-        const uint32_t wk = (uint32_t)s * 68u;
-        if (wave < 4)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)(slot + kRgXBytes + 1024 * wave), 16,
-                                                     wo + wk, 0, 0, 0);
-        else if (wave == 4)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)(slot + kRgXBytes + kRgWQBytes), 4,
-                                                     wo + wk, 0, 0, 0);
-        else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, (lds_ptr)sink, 4, kMaskedOffset, 0, 0, 0);
-    };
-    auto issue = [&](int s, uint8_t *slot) {
-        issue_x(s, slot, 0);
-        issue_x(s, slot, 1);
-        issue_w(s, slot);
-    };
-
-    // Widening role: row cn, block cb, quants 8 cu .. 8 cu + 7 of the block,
-    // which start in raw dword i0 = 2 cu (block 0: at byte 2) or 9 + 2 cu
-    // (block 1: aligned).  Dword 16 of a row lives in the separate array.
-    // Waves 6 and 7 also widen the block-0 / block-1 scale of row `lane`.
-    const int cn = tid >> 3, cb = (tid >> 2) & 1, cu = tid & 3;
-    const int ci0 = cb ? 9 + 2 * cu : 2 * cu;
-    const uint32_t csh = cb ? 0u : 2u;
-    auto raw_at = [&](int i) {
-        return (uint32_t)(i < 16 ? kRgXBytes + 64 * cn + 4 * i : kRgXBytes + kRgWQBytes + 4 * cn);
-    };
-    const uint32_t cr0 = raw_at(ci0), cr1 = raw_at(ci0 + 1), cr2 = raw_at(ci0 + 2);
-    const uint32_t cr0_g[2] = {base0 + cr0, base1 + cr0}, cr1_g[2] = {base0 + cr1, base1 + cr1},
-                   cr2_g[2] = {base0 + cr2, base1 + cr2};
-    const uint32_t cw = wbase + swz(cn, 4 * cb + cu);
-    const int sb = wave - 6;  // scale block of waves 6 and 7
-    const uint32_t cs_g[2] = {base0 + (uint32_t)(kRgXBytes + 64 * lane + 32 * sb),
-                              base1 + (uint32_t)(kRgXBytes + 64 * lane + 32 * sb)};
-    const uint32_t cd = wbase + (uint32_t)(kRgWbBytes + 8 * lane + 4 * sb);
-    // Waves below 6 read their first quant dword again instead of a scale.
-    const uint32_t cs_g2[2] = {wave >= 6 ? cs_g[0] : cr0_g[0], wave >= 6 ? cs_g[1] : cr0_g[1]};
-    uint32_t rw[4];
-    auto widen_read = [&](auto SLOT) {
-        constexpr int so = (decltype(SLOT)::value % 3) * kRgSlot;
-        constexpr int g = decltype(SLOT)::value / 3;
-        ring_read_raw<so>(cr0_g[g], cr1_g[g], cr2_g[g], cs_g2[g], rw[0], rw[1], rw[2], rw[3]);
-    };
-    auto widen_write = [&](auto WB) {
-        constexpr int wbo = decltype(WB)::value * kRgWbuf;
-        const uint32_t q0 = __builtin_amdgcn_alignbyte(rw[1], rw[0], csh);
-        const uint32_t q1 = __builtin_amdgcn_alignbyte(rw[2], rw[1], csh);
-        uint32_t o[4];
-        i8x4_to_bf16(q0, o[0], o[1]);
-        i8x4_to_bf16(q1, o[2], o[3]);
-        ring_store4<wbo>(cw, u32x4{o[0], o[1], o[2], o[3]});
-        if (wave >= 6) ring_store1<wbo>(cd, half_bits_to_float_fast(sb ? rw[3] >> 16 : rw[3] & 0xFFFFu));
-    };
-
-    // Fragment addresses (per lane; the slot / buffer offset is an immediate).
-    const int lr = lane & 15, lk = lane >> 4;
-    const uint32_t f_xa0 = swz(32 * wm + lr, lk), f_xa1 = swz(32 * wm + lr, 4 + lk);
-    const uint32_t xa0_g[2] = {base0 + f_xa0, base1 + f_xa0}, xa1_g[2] = {base0 + f_xa1, base1 + f_xa1};
-    const uint32_t wb0 = wbase + swz(32 * wn + lr, lk), wb1 = wbase + swz(32 * wn + lr, 4 + lk);
-    const uint32_t wdd = wbase + (uint32_t)(kRgWbBytes + 8 * (32 * wn + lr));
-    auto read_frags = [&](auto SLOT, auto WB, RingFrags &f) {
-        constexpr int so = (decltype(SLOT)::value % 3) * kRgSlot;
-        constexpr int g = decltype(SLOT)::value / 3;
-        constexpr int wbo = decltype(WB)::value * kRgWbuf;
-        ring_read_frags<so, wbo>(xa0_g[g], xa1_g[g], wb0, wb1, wdd, f);
-    };
-
-    f32x4 acc[2][2];
-    f32x4 part[2][2][2][2];  // [set][kb][mt][nt]
-    float dsc[2][2][2];      // [set][kb][nt]
-#pragma unroll
-    for (int a = 0; a < 2; a++)
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            acc[a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                part[1][c][a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                dsc[1][c][a] = 0.0f;
-            }
-        }
-    RingFrags F[2];
-
-    auto mfma_one = [&](int set, const RingFrags &f, int q) {
-        const int kb = q >> 2, mt = (q >> 1) & 1, nt = q & 1;
-        const u32x4 a = kb ? (mt ? f.a11 : f.a10) : (mt ? f.a01 : f.a00);
-        const u32x4 b = kb ? (nt ? f.b11 : f.b10) : (nt ? f.b01 : f.b00);
-        part[set][kb][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            as_bf16x8(a), as_bf16x8(b), f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-    };
-    auto scale_q = [&](int set, int q) {
-        const int kb = q >> 2, nt = (q >> 1) & 1, mt = q & 1;
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-            acc[mt][nt][v] = fmaf(dsc[set][kb][nt], part[set][kb][mt][nt][v], acc[mt][nt][v]);
-    };
-    auto pin_acc = [&]() {
-        asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
-    };
-    auto scale = [&](int set) {
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++)
-                        acc[mt][nt][v] = fmaf(dsc[set][kb][nt], part[set][kb][mt][nt][v], acc[mt][nt][v]);
-    };
-
-    // Prologue: stages 0..4 in flight; stages 0 and 1 widened; fragments of 0 read.
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    if constexpr (!LOADERS) {
-        issue(0, lds);
-        issue(1, lds + kRgSlot);
-        issue(2, lds + 2 * kRgSlot);
-        issue(3, lds + 3 * kRgSlot);
-        issue(4, lds + 4 * kRgSlot);
-    }
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kRgDmaPerWave * (NS - 3)) : "memory");
-    widen_read(I0{});
-    ring_wait(F[1], rw[0], rw[1], rw[2], rw[3]);
-    widen_write(I0{});
-    widen_read(I1{});
-    ring_wait(F[1], rw[0], rw[1], rw[2], rw[3]);
-    widen_write(I1{});
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    read_frags(I0{}, I0{}, F[0]);
-    ring_wait(F[0], rw[0], rw[1], rw[2], rw[3]);
-
-    // Stage s = 6 c + j sits in slot j, its widened W in buffer s % 3 = j % 3.
-    auto stage = [&](auto J, int s) {
-        constexpr int j = decltype(J)::value;
-        constexpr int cur = j & 1, nxt = cur ^ 1;
-        // Stage s + 2 has landed for every wave; stage s + 1 is widened.
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier"
-                     :
-                     : "n"(kRgDmaPerWave * (NS - 4))
-                     : "memory");
-        // Eight groups, one MFMA of stage s each, with four scale FMAs of
-        // stage s - 1 and the LDS reads of stages s + 2 (raw W) and s + 1
-        // (fragments) or a load issue, so that the LDS, the matrix core, the
-        // VALU and the load path each see a steady stream.
-        constexpr int sn = (j + 1) % NS, gn = sn / 3, so_n = (sn % 3) * kRgSlot;
-        constexpr int wo_n = ((j + 1) % 3) * kRgWbuf;
-        constexpr int sd = (j + NS - 1) % NS;
-        RingFrags &f = F[cur];
-        RingFrags &fn = F[nxt];
-        dsc[cur][0][0] = __uint_as_float(f.d0.x);
-        dsc[cur][1][0] = __uint_as_float(f.d0.y);
-        dsc[cur][0][1] = __uint_as_float(f.d1.x);
-        dsc[cur][1][1] = __uint_as_float(f.d1.y);
-        {
-            widen_read(std::integral_constant<int, (j + 2) % NS>{});
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_one(cur, f, 0);
-            scale_q(nxt, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            ring_read<so_n>(xa0_g[gn], fn.a00);
-            ring_read<so_n + 2048>(xa0_g[gn], fn.a01);
-            mfma_one(cur, f, 1);
-            scale_q(nxt, 1);
-            __builtin_amdgcn_sched_barrier(0);
-            ring_read<so_n>(xa1_g[gn], fn.a10);
-            ring_read<so_n + 2048>(xa1_g[gn], fn.a11);
-            mfma_one(cur, f, 2);
-            scale_q(nxt, 2);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (!LOADERS) issue_x(s + NS - 1, lds + sd * kRgSlot, 0);
-            else asm volatile("" ::: "memory");
-            ring_read<wo_n>(wb0, fn.b00);
-            ring_read<wo_n + 2048>(wb0, fn.b01);
-            mfma_one(cur, f, 3);
-            scale_q(nxt, 3);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (!LOADERS) issue_x(s + NS - 1, lds + sd * kRgSlot, 1);
-            else asm volatile("" ::: "memory");
-            ring_read<wo_n>(wb1, fn.b10);
-            ring_read<wo_n + 2048>(wb1, fn.b11);
-            mfma_one(cur, f, 4);
-            scale_q(nxt, 4);
-            pin_acc();
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (!LOADERS) issue_w(s + NS - 1, lds + sd * kRgSlot);
-            else asm volatile("" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-            ring_read<wo_n>(wdd, fn.d0);
-            ring_read<wo_n + 128>(wdd, fn.d1);
-            mfma_one(cur, f, 5);
-            scale_q(nxt, 5);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_one(cur, f, 6);
-            scale_q(nxt, 6);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_one(cur, f, 7);
-            scale_q(nxt, 7);
-            pin_acc();
-            __builtin_amdgcn_sched_barrier(0);
-            ring_wait(F[nxt], rw[0], rw[1], rw[2], rw[3]);
-            widen_write(std::integral_constant<int, (j + 2) % 3>{});
-        }
-        if (s + 1 == nst) scale(cur);
-    };
-    for (int s = 0; s < nst; s += NS) {
-        stage(std::integral_constant<int, 0>{}, s);
-        if (s + 1 >= nst) break;
-        stage(std::integral_constant<int, 1>{}, s + 1);
-        if (s + 2 >= nst) break;
-        stage(std::integral_constant<int, 2>{}, s + 2);
-        if (s + 3 >= nst) break;
-        stage(std::integral_constant<int, 3>{}, s + 3);
-        if (s + 4 >= nst) break;
-        stage(std::integral_constant<int, 4>{}, s + 4);
-        if (s + 5 >= nst) break;
-        stage(std::integral_constant<int, 5>{}, s + 5);
-    }
-    // Drain the loads issued past the last stage before the workgroup ends.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-    // D layout of a 16x16 tile: lane holds column lane & 15, rows 4 (lane >> 4) + v.
-    float *const out = partials != nullptr ? partials + (int64_t)split * M * N : Y;
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + 32 * wm + 16 * mt + 4 * lk + r;
-                const int n = n0 + 32 * wn + 16 * nt + lr;
-                if (m < M) out[(int64_t)m * N + n] = acc[mt][nt][r];
-            }
-}
-
-// y = part[0] + part[1] + ... + part[S - 1], in that order (4 floats a
-// thread, S <= 8): every partial is loaded before the first add, so the
-// reduction costs one memory round trip.
-__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__restrict__ part, int S,
-                                                                 int64_t mn, float *__restrict__ y) {
-    const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (i >= mn) return;
-    // only the S partials are read (S is uniform); the sum runs in split order
-    float4 b[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-        if (k < S) b[k] = *reinterpret_cast<const float4 *>(part + (int64_t)k * mn + i);
-    float4 a = b[0];
-#pragma unroll
-    for (int k = 1; k < 8; k++) {
-        if (k < S) {
-            a.x += b[k].x;
-            a.y += b[k].y;
-            a.z += b[k].z;
-            a.w += b[k].w;
-        }
-    }
-    *reinterpret_cast<float4 *>(y + i) = a;
-}
 
 // ---- small-M ring kernel --------------------------------------------------------
 //
@@ -1187,6 +480,56 @@ __global__ __launch_bounds__(256) void gemm_q8_0_generic_kernel(const uint8_t *_
     Y[(int64_t)m * N + n] = acc;
 }
 
+// Any shape, Q4_0 or Q4_K: one thread per output, fp32, the reference's block
+// structure (Q4_0: d * sum((q - 8) x); Q4_K per sub-block: fl(d sc) sum(q x) -
+// fl(dmin m) sum(x), the min term skipped for a zero min code).
+template <int T>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t *__restrict__ W, int64_t row_bytes,
+                                                           const uint16_t *__restrict__ X, float *__restrict__ Y,
+                                                           int M, int N, int K) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)M * N) return;
+    const int m = (int)(t / N), n = (int)(t - (int64_t)m * N);
+    const uint8_t *row = W + (int64_t)n * row_bytes;
+    const uint16_t *xr = X + (int64_t)m * K;
+    auto xv = [&](int k) { return __uint_as_float((uint32_t)xr[k] << 16); };
+    float acc = 0.0f;
+    if constexpr (T == kQ4_0) {
+        for (int b = 0; b < K / 32; b++) {
+            const uint8_t *blk = row + (int64_t)b * kQ4BlockBytes;
+            const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            float s = 0.0f;
+            for (int i = 0; i < 16; i++) {
+                const int q = blk[2 + i];
+                s = fmaf((float)((q & 15) - 8), xv(32 * b + i), s);
+                s = fmaf((float)((q >> 4) - 8), xv(32 * b + 16 + i), s);
+            }
+            acc = fmaf(d, s, acc);
+        }
+    } else {
+        for (int sb = 0; sb < K / kQK; sb++) {
+            const uint8_t *blk = row + (int64_t)sb * kQKBlockBytes;
+            const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            const float dmin = half_bits_to_float_fast((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+            for (int j = 0; j < 8; j++) {
+                int sc, mc;
+                q4k_code(blk + 4, j, &sc, &mc);
+                const uint8_t *q = blk + 16 + 32 * (j >> 1);
+                const int sh = 4 * (j & 1);
+                float s = 0.0f, sx = 0.0f;
+                for (int i = 0; i < 32; i++) {
+                    const float x = xv(kQK * sb + 32 * j + i);
+                    s = fmaf((float)((q[i] >> sh) & 15), x, s);
+                    sx += x;
+                }
+                acc = fmaf(d * (float)sc, s, acc);
+                if (mc != 0) acc = fmaf(-(dmin * (float)mc), sx, acc);
+            }
+        }
+    }
+    Y[(int64_t)m * N + n] = acc;
+}
+
 namespace {
 
 template <int BM, int BN, int WM, int WN, int WK>
@@ -1200,105 +543,44 @@ hipError_t launch_tiled(const uint8_t *w, int64_t row_bytes, const uint16_t *x, 
 
 }  // namespace
 
-namespace {
-
-// Splits of K for the large-M ring kernel: enough that the workgroups cover
-// the CUs (up to 8), dividing the K stages evenly.
-int ring_splits(int M, int N, int K) {
-    const int tiles = (M + kBigBM - 1) / kBigBM * (N / kBigBN);
-    const int nst = K / 64;
-    int S = 1;
-    while (S < 8 && tiles * 2 * S <= device_cus() && nst % (2 * S) == 0) S *= 2;
-    return S;
+size_t gemm_workspace_bytes(int type_id, int M, int N, int K) {
+    if (type_id == kQ8_0 && M <= 32) return 0;  // the skinny kernel
+    return gemm_tile_workspace_bytes(type_id, M, N, K);
 }
 
-bool ring_applies(int M, int N, int K, int64_t row_bytes) {
-    return N % kBigBN == 0 && K % 64 == 0 && (int64_t)kBigBN * row_bytes < ((int64_t)1 << 31) &&
-           (int64_t)kBigBM * K * 2 < ((int64_t)1 << 31);
-}
-
-}  // namespace
-
-size_t gemm_workspace_bytes(int M, int N, int K) {
-    if (M <= 32 || N % kBigBN != 0 || K % 64 != 0) return 0;
-    const int S = ring_splits(M, N, K);
-    return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
-}
-
-// The need of m peaks at multiples of the 128-row tile and is zero once the
-// tiles cover half the CUs; S tiles <= cu_count (ring_splits) bounds it by
-// cu_count tiles of 128 x 64 floats (8 MiB on 256 CUs, at m = 128).
-size_t gemm_workspace_max_bytes(int N, int K) {
+// The need peaks at multiples of the 128-row tile and is zero once the tiles
+// cover the CUs; the splits keep (S - 1) tiles' partials per tile, below
+// cu_count 128 x 128 floats (16 MiB on 256 CUs).
+size_t gemm_workspace_max_bytes(int type_id, int N, int K) {
     size_t most = 0;
-    for (int mt = 1; gemm_workspace_bytes(128 * mt, N, K) > 0; mt++) {
-        const size_t b = gemm_workspace_bytes(128 * mt, N, K);
+    for (int mt = 1; mt <= 64; mt++) {
+        const size_t b = gemm_workspace_bytes(type_id, 128 * mt, N, K);
         if (b > most) most = b;
     }
     return most;
 }
 
-hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
-                                 int M, int N, int K, hipStream_t stream, float *workspace,
-                                 size_t workspace_bytes) {
+hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
+                            int M, int N, int K, hipStream_t stream, float *workspace, size_t workspace_bytes) {
     if (M <= 0) return hipSuccess;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (row_bytes & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-    const int v = tuning().gemm_variant;
-    // M > 32: 128 x 64 tiles (v == 2 forces them where the shape allows, v == 3
-    // keeps the register-pipelined LDS tiles below M = 256), split over K
-    // when the tiles alone leave CUs idle and a workspace is given.
-    if (aligned && v != 1 && ring_applies(M, N, K, row_bytes) && (M >= 256 || v == 2 || (M > 32 && v != 3))) {
-        const unsigned tiles = (unsigned)(((M + kBigBM - 1) / kBigBM) * (N / kBigBN));
-        const unsigned grid = tiles;
-        const int nst = K / 64;
-        const int cfg = tuning().gemm_big_config;
-        int S = ring_splits(M, N, K);
-        // The reduction moves 16-byte vectors of y and the workspace.
-        if (S > 1 && (workspace == nullptr || workspace_bytes < (size_t)S * M * N * sizeof(float) ||
-                      ((reinterpret_cast<uintptr_t>(workspace) | reinterpret_cast<uintptr_t>(y)) & 15u) != 0))
-            S = 1;
-#define GOLLEK_BIG(P, WMW, WNW)                                                                \
-    hipLaunchKernelGGL((gemm_q8_0_bf16_big_kernel<P, WMW, WNW>), dim3(grid),                \
-                       dim3(64 * (WMW) * (WNW)), 0, stream, w, row_bytes, x, y, M, N, K)
-        // Configs 1..4 select the register-pipelined kernel (sweeps); the
-        // default is the buffer->LDS ring.
-        if (nst % 4 == 0 && cfg == 1) GOLLEK_BIG(4, 4, 2);
-        else if (nst % 8 == 0 && cfg == 2) GOLLEK_BIG(8, 4, 2);
-        else if (nst % 2 == 0 && cfg == 3) GOLLEK_BIG(2, 4, 2);
-        else if (nst % 4 == 0 && cfg == 4) GOLLEK_BIG(4, 2, 2);
-        else {
-            if (cfg == 5)
-                hipLaunchKernelGGL(gemm_q8_0_bf16_ring_kernel<false>, dim3(tiles * S), dim3(512), 0, stream, w,
-                                   row_bytes, x, y, M, N, K, S, S > 1 ? workspace : nullptr);
-            else
-                hipLaunchKernelGGL(gemm_q8_0_bf16_ring_kernel<true>, dim3(tiles * S), dim3(640), 0, stream, w,
-                                   row_bytes, x, y, M, N, K, S, S > 1 ? workspace : nullptr);
-            if (S > 1) {
-                const int64_t mn = (int64_t)M * N;
-                hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((mn / 4 + 255) / 256)),
-                                   dim3(256), 0, stream, workspace, S, mn, y);
-            }
-        }
-#undef GOLLEK_BIG
-        return hipGetLastError();
-    }
-    // Small M: the buffer->LDS ring over 16-row column tiles (v == 3 keeps
-    // the register-pipelined tiles below, for sweeps).
-    if (aligned && v != 1 && v != 3 && M <= 32 && N % 16 == 0 && K % 256 == 0 &&
+    // M <= 32 with Q8_0 weights: the buffer->LDS ring over 16-row column tiles.
+    if (type_id == kQ8_0 && aligned && M <= 32 && N % 16 == 0 && K % 256 == 0 &&
         (int64_t)16 * row_bytes < ((int64_t)1 << 31) && (int64_t)M * K * 2 < ((int64_t)1 << 31)) {
-        const int cfg = tuning().gemm_big_config;
-#define GOLLEK_SKINNY(TT, NS)                                                                      \
-    hipLaunchKernelGGL((gemm_q8_0_bf16_skinny_kernel<TT, NS>), dim3(N / 16), dim3(256), 0, stream, w, \
-                       row_bytes, x, y, M, N, K)
-        // Measured on MI355X (4096 x 4096): four slots per wave beat deeper
-        // rings (which only queue more requests at the HBM).
-        if (M <= 16 && cfg == 18) GOLLEK_SKINNY(1, 8);
-        else if (M <= 16) GOLLEK_SKINNY(1, 4);
-        else GOLLEK_SKINNY(2, 4);
-#undef GOLLEK_SKINNY
+        if (M <= 16)
+            hipLaunchKernelGGL((gemm_q8_0_bf16_skinny_kernel<1, 4>), dim3(N / 16), dim3(256), 0, stream, w,
+                               row_bytes, x, y, M, N, K);
+        else
+            hipLaunchKernelGGL((gemm_q8_0_bf16_skinny_kernel<2, 4>), dim3(N / 16), dim3(256), 0, stream, w,
+                               row_bytes, x, y, M, N, K);
         return hipGetLastError();
     }
-    if (aligned && v != 1) {
+    // 128 x 128 tiles for Q8_0, Q4_0 and Q4_K (K a multiple of 256).
+    if (gemm_tile_supported(type_id, row_bytes, M, N, K, w, x, y))
+        return launch_gemm_tile(type_id, w, row_bytes, x, y, M, N, K, stream, workspace, workspace_bytes);
+    // Other shapes and alignments.
+    if (type_id == kQ8_0 && aligned) {
         if (M <= 16 && N % 16 == 0 && K % 256 == 0)
             return launch_tiled<16, 16, 16, 16, 4>(w, row_bytes, x, y, M, N, K, stream);
         if (M <= 128 && N % 16 == 0 && K % 64 == 0)
@@ -1307,8 +589,20 @@ hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint
             return launch_tiled<128, 64, 64, 32, 1>(w, row_bytes, x, y, M, N, K, stream);
     }
     const int64_t total = (int64_t)M * N;
-    hipLaunchKernelGGL(gemm_q8_0_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
-                       0, stream, w, row_bytes, x, y, M, N, K);
+    const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    switch (type_id) {
+    case kQ8_0:
+        hipLaunchKernelGGL(gemm_q8_0_generic_kernel, grid, block, 0, stream, w, row_bytes, x, y, M, N, K);
+        break;
+    case kQ4_0:
+        hipLaunchKernelGGL(gemm_generic_kernel<kQ4_0>, grid, block, 0, stream, w, row_bytes, x, y, M, N, K);
+        break;
+    case kQ4_K:
+        hipLaunchKernelGGL(gemm_generic_kernel<kQ4_K>, grid, block, 0, stream, w, row_bytes, x, y, M, N, K);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -361,14 +361,8 @@ hipError_t launch_gemv_ring(int type_id, const uint8_t *w, int64_t row_bytes, in
                             const float *x, float *y, int64_t rows, hipStream_t stream) {
     // Measured on MI355X (Q8_0 4096 x 4096, Q4_0 11008 x 4096): three slots
     // per wave beat deeper rings, which only queue more requests at the HBM;
-    // the streaming cache policy makes no difference.  gemm_big_config 16
-    // selects six slots (sweeps).
-    const int cfg = tuning().gemm_big_config;
-    if (type_id == kQ8_0) {
-        if (cfg == 16) return launch_ring<kQ8_0, 6>(w, row_bytes, cols, x, y, rows, stream);
-        return launch_ring<kQ8_0, 3>(w, row_bytes, cols, x, y, rows, stream);
-    }
-    if (cfg == 16) return launch_ring<kQ4_0, 6>(w, row_bytes, cols, x, y, rows, stream);
+    // the streaming cache policy makes no difference.
+    if (type_id == kQ8_0) return launch_ring<kQ8_0, 3>(w, row_bytes, cols, x, y, rows, stream);
     return launch_ring<kQ4_0, 3>(w, row_bytes, cols, x, y, rows, stream);
 }
 

@@ -19,8 +19,6 @@ struct LaunchTuning {
     std::atomic<int64_t> gemv_rows_per_wave{0};
     std::atomic<int> gemv_row_batch{0};      // rows per load batch (1, 2, 4, 8)
     std::atomic<int> gemv_waves_per_cu{8};   // target resident waves per CU
-    std::atomic<int> gemm_variant{0};
-    std::atomic<int> gemm_big_config{0};     // large-M GEMM: 0 buffer->LDS ring, 1..4 register-pipelined
     std::atomic<int> gemv_variant{0};        // 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring (Q4_K),
                                              // 3 Q4_K on shared tiles for K <= 4096, 4 Q8_0 / Q4_0
                                              // rings and Q5_K / Q6_K fp32
@@ -99,16 +97,24 @@ bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, int64_t rows, const voi
 hipError_t launch_gemv_q4k_dot4(const uint8_t *w, int64_t row_bytes, int64_t cols,
                                 const float *x, float *y, int64_t rows, hipStream_t stream);
 
-// Y[M, N] = X[M, K] (bf16 bits) . W[N, K]^T for Q8_0 W (gguf_gemm.hip).
-// Shapes whose output tiles leave CUs idle are split over K into partial
-// tiles in `workspace` (device memory of gemm_workspace_bytes(M, N, K)
-// bytes; without it they run unsplit) and summed in split order.
-size_t gemm_workspace_bytes(int M, int N, int K);
-// The largest gemm_workspace_bytes(M, N, K) over every M.
-size_t gemm_workspace_max_bytes(int N, int K);
-hipError_t launch_gemm_q8_0_bf16(const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
-                                 int M, int N, int K, hipStream_t stream, float *workspace = nullptr,
-                                 size_t workspace_bytes = 0);
+// Y[M, N] = X[M, K] (bf16 bits) . W[N, K]^T for Q8_0, Q4_0 or Q4_K W
+// (gguf_gemm.hip, gguf_gemm_tile.hip).  Shapes whose output tiles leave CUs
+// idle are split over K into partial tiles in `workspace` (device memory of
+// gemm_workspace_bytes(type, M, N, K) bytes; with less they split less or
+// run unsplit) and added in split order.
+size_t gemm_workspace_bytes(int type_id, int M, int N, int K);
+// The largest gemm_workspace_bytes(type, M, N, K) over every M.
+size_t gemm_workspace_max_bytes(int type_id, int N, int K);
+hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
+                            int M, int N, int K, hipStream_t stream, float *workspace = nullptr,
+                            size_t workspace_bytes = 0);
+// The 128 x 128 tile kernel (gguf_gemm_tile.hip).
+bool gemm_tile_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w,
+                         const void *x, const void *y);
+size_t gemm_tile_workspace_bytes(int type_id, int M, int N, int K);
+hipError_t launch_gemm_tile(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x,
+                            float *y, int M, int N, int K, hipStream_t stream, float *workspace,
+                            size_t workspace_bytes);
 
 // Workspace layout of the grouped MoE FFN (byte offsets; gguf_moe.hip).
 struct MoeLayout {

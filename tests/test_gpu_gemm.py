@@ -1,4 +1,5 @@
-"""GPU parity of the Q8_0 x bf16 MFMA GEMM (small-M prefill / batched decode).
+"""GPU parity of the Q8_0 / Q4_0 / Q4_K x bf16 MFMA GEMM (small-M prefill /
+batched decode).
 
 Bar: rel_err <= 1e-2 against the fp64 product of the bf16 activations and the
 bit-exact dequantized weights (the quants are contracted exactly and each
@@ -64,43 +65,80 @@ def test_gemm_odd_shapes(rows, cols, m):
     t.close()
 
 
-@pytest.mark.parametrize("rows,cols,m,variant", [(128, 256, 300, 0), (64, 128, 5, 2), (192, 4096, 257, 0),
-                                                  (64, 64, 128, 2), (4096, 192, 384, 0)])
-def test_gemm_large_m_kernel_shapes(rows, cols, m, variant):
-    # The 128 x 64 tiled kernel: partial last M tile (rows past M read zeros),
-    # several N tiles, K down to one block pair; variant 2 forces it below M = 256.
-    print(f"[gpu] gemm large-m rows={rows} cols={cols} m={m} variant={variant}", flush=True)
-    data = syn.q8_0_matrix(rows, cols, seed=rows * 7 + cols)
-    t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
-    x = syn.activation_bf16(m, cols, seed=m + 3)
+MATRIX = {syn.Q8_0: syn.q8_0_matrix, syn.Q4_0: syn.q4_0_matrix, syn.Q4_K: syn.q4_k_matrix}
+TYPES = [syn.Q8_0, syn.Q4_0, syn.Q4_K]
+
+
+def _gemm_case(type_id, rows, cols, m, seed):
+    data = MATRIX[type_id](rows, cols, seed=seed)
+    t = ops.GgufTensor("w", (cols, rows), type_id, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=seed + 1)
     y = np.full((m, rows), np.nan, np.float32)
-    ops.set_option("gemm_variant", variant)
     try:
         ops.gemm_bf16(t, x, y)
     finally:
-        ops.set_option("gemm_variant", 0)
-    assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
-    t.close()
+        t.close()
+    return y, o.gemm_reference(type_id, data, cols, x)
 
 
-@pytest.mark.parametrize("cfg", [0, 5, 1, 3])
-@pytest.mark.parametrize("rows,cols,m", [(192, 4096, 300), (4096, 192, 257), (64, 64, 130)])
-def test_gemm_large_m_configs(rows, cols, m, cfg):
-    # The large-M kernels: the buffer->LDS ring fed by loader waves (cfg 0)
-    # or by every wave (cfg 5), K from one block pair, fewer stages than ring
-    # slots, up to 64 stages; and two register-pipelined configurations.
-    print(f"[gpu] gemm large-m cfg={cfg} rows={rows} cols={cols} m={m}", flush=True)
-    data = syn.q8_0_matrix(rows, cols, seed=rows + cols + cfg)
-    t = ops.GgufTensor("w", (cols, rows), syn.Q8_0, data.reshape(-1))
-    x = syn.activation_bf16(m, cols, seed=m + cfg)
+@pytest.mark.parametrize("type_id", TYPES)
+@pytest.mark.parametrize("rows,cols,m", [(128, 256, 33), (192, 4096, 300), (80, 512, 129), (4096, 256, 257),
+                                          (1000, 1024, 64), (256, 2048, 1024), (64, 4096, 40)])
+def test_gemm_tile_kernel_shapes(type_id, rows, cols, m):
+    # The 128 x 128 tile kernel: K from one four-stage round (256) up, a
+    # partial last M tile (rows past M read zeros) and N tile (rows past N),
+    # one to many tiles, grids that are and are not a multiple of 8, and the
+    # K splits the CU count allows (none for K = 256, up to 8).
+    print(f"[gpu] gemm tile type={type_id} rows={rows} cols={cols} m={m}", flush=True)
+    y, ref = _gemm_case(type_id, rows, cols, m, seed=rows + 3 * cols + m + type_id)
+    err = o.rel_err(y, ref)
+    print(f"[gpu] gemm tile type={type_id} rel_err={err:.3e}", flush=True)
+    assert err <= GEMM_TOL
+
+
+@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K])
+@pytest.mark.parametrize("m", [16, 128, 512])
+def test_gemm_q4_parity_14336(type_id, m):
+    # Q4_0 / Q4_K weights at the FFN shape K = 4096, N = 14336.
+    print(f"[gpu] gemm q4 type={type_id} m={m} 14336x4096", flush=True)
+    y, ref = _gemm_case(type_id, 14336, 4096, m, seed=1400 + m)
+    err = o.rel_err(y, ref)
+    print(f"[gpu] gemm q4 type={type_id} m={m} rel_err={err:.3e}", flush=True)
+    assert err <= GEMM_TOL
+
+
+@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K])
+@pytest.mark.parametrize("rows,cols,m", [(48, 96, 3), (16, 64, 20), (40, 512, 7), (20, 768, 5)])
+def test_gemm_q4_generic_shapes(type_id, rows, cols, m):
+    # Shapes the tile kernel does not take (K not a multiple of 256): the
+    # one-thread-per-output kernel.
+    if type_id == syn.Q4_K and cols % 256:
+        pytest.skip("Q4_K rows are whole 256-element superblocks")
+    print(f"[gpu] gemm generic type={type_id} rows={rows} cols={cols} m={m}", flush=True)
+    y, ref = _gemm_case(type_id, rows, cols, m, seed=rows + cols + m)
+    assert o.rel_err(y, ref) <= GEMM_TOL
+
+
+def test_gemm_q4k_special_headers():
+    # Q4_K superblocks with zero min codes under a NaN dmin (the min term is
+    # skipped, as RT/GgufKQuantLayout.java:67-69), zero d, and a subnormal
+    # dmin: the tile kernel equals the fp64 product of the bit-exact rows.
+    rows, cols, m = 256, 1024, 160
+    data = syn.q4_k_matrix(rows, cols, seed=17).copy()
+    blocks = data.reshape(rows, cols // 256, 144)
+    blocks[0:16, :, 2:4] = np.frombuffer(np.float16(np.nan).tobytes(), np.uint8)
+    blocks[0:16, :, 8:12] = 0  # m codes 0..3 (low 6 bits) and the high bits of 4..7
+    blocks[0:16, :, 12:16] &= 0x0F  # low 4 bits of m codes 4..7
+    blocks[16:32, :, 0:2] = 0
+    blocks[32:48, :, 2:4] = np.frombuffer(np.uint16(1).tobytes(), np.uint8)
+    t = ops.GgufTensor("w", (cols, rows), syn.Q4_K, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=3)
     y = np.full((m, rows), np.nan, np.float32)
-    ops.set_option("gemm_big_config", cfg)
-    try:
-        ops.gemm_bf16(t, x, y)
-    finally:
-        ops.set_option("gemm_big_config", 0)
-    assert o.rel_err(y, o.gemm_reference(syn.Q8_0, data, cols, x)) <= GEMM_TOL
+    ops.gemm_bf16(t, x, y)
     t.close()
+    ref = o.gemm_reference(syn.Q4_K, data, cols, x)
+    assert np.isfinite(ref).all()
+    assert o.rel_err(y, ref) <= GEMM_TOL
 
 
 @pytest.mark.parametrize("rows,cols,m", [(16, 256, 1), (16, 256, 16), (48, 512, 17), (32, 1280, 32),
@@ -135,8 +173,8 @@ def test_gemm_split_k_shapes(rows, cols, m):
 
 
 def test_gemm_rejects_other_types_and_short_buffers():
-    data = syn.q4_k_matrix(16, 256, seed=1)
-    t = ops.GgufTensor("w", (256, 16), syn.Q4_K, data.reshape(-1))
+    data = syn.q6_k_matrix(16, 256, seed=1)
+    t = ops.GgufTensor("w", (256, 16), syn.Q6_K, data.reshape(-1))
     with pytest.raises(ops.UnsupportedOperationError):
         ops.gemm_bf16(t, np.zeros((2, 256), np.uint16), np.zeros((2, 16), np.float32))
     t.close()
@@ -147,10 +185,11 @@ def test_gemm_rejects_other_types_and_short_buffers():
     t.close()
 
 
-def test_gemm_device_entry_matches_host(q8_4096):
+@pytest.mark.parametrize("m", [128, 512])
+def test_gemm_device_entry_matches_host(q8_4096, m):
+    # m = 128: eight K splits; m = 512: two (the same kernels in both entries).
     import torch
     data, t = q8_4096
-    m = 128
     x = syn.activation_bf16(m, 4096, seed=5)
     yh = np.zeros((m, 4096), np.float32)
     ops.gemm_bf16(t, x, yh)
@@ -187,5 +226,34 @@ def test_gemm_device_entry_split_k_workspace(m):
                 torch.cuda.synchronize()
                 got = y_view.cpu().numpy().reshape(mm, rows)
                 assert o.rel_err(got, ref) <= GEMM_TOL
+    finally:
+        dw.close()
+
+
+@pytest.mark.parametrize("type_id,rows,m", [(syn.Q8_0, 4096, 512), (syn.Q4_K, 4096, 512), (syn.Q4_0, 2048, 1024)])
+def test_gemm_two_split_repeatable(type_id, rows, m):
+    # Two K splits added in split order by the reduction kernel: the same
+    # bits on every call, within the bar of the oracle, on repeated calls
+    # with the handle's workspace reused.
+    import torch
+    cols = 4096
+    data = MATRIX[type_id](rows, cols, seed=rows + m)
+    w_dev = torch.from_numpy(data.reshape(-1)).cuda()
+    dw = ops.DeviceWeight(type_id, w_dev.data_ptr(), rows, cols)
+    stream = torch.cuda.current_stream().cuda_stream
+    try:
+        for seed in (1, 2):
+            print(f"[gpu] gemm two-split type={type_id} rows={rows} m={m} seed={seed}", flush=True)
+            x = syn.activation_bf16(m, cols, seed=seed)
+            x_dev = torch.from_numpy(x.view(np.int16)).cuda()
+            outs = []
+            for _ in range(3):
+                y_dev = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+                dw.gemm_bf16(x_dev.data_ptr(), m, y_dev.data_ptr(), stream)
+                torch.cuda.synchronize()
+                outs.append(y_dev.cpu().numpy())
+            for o_ in outs[1:]:
+                assert np.array_equal(o_.view(np.uint32), outs[0].view(np.uint32))
+            assert o.rel_err(outs[0], o.gemm_reference(type_id, data, cols, x)) <= GEMM_TOL
     finally:
         dw.close()

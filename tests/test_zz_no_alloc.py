@@ -4,9 +4,10 @@ The no-allocation entry point runs the same kernels with its split-K
 partials in the library's static per-GPU scratch instead of the handle's
 workspace, so its output must equal the allocating entry point's bit for
 bit, and both must be within the GEMM bar (rel_err <= 1e-2) of the fp64
-oracle.  Two calls in a row on one handle, the second with fewer rows of X
-(both shapes split over K at 4096 weight rows, so both use the scratch and
-the second reads none of the first call's partials).
+oracle.  Three calls in a row on one handle, each with fewer rows of X than
+the one before (all three split over K at 4096 weight rows, so all use the
+scratch -- m = 512 with two splits, the others with more -- and none reads
+an earlier call's partials).
 """
 import ctypes
 
@@ -34,7 +35,7 @@ def test_noalloc_gemm_matches_allocating_entry_point():
     dw = ops.DeviceWeight(syn.Q8_0, w_dev.data_ptr(), rows, cols)
     stream = torch.cuda.current_stream().cuda_stream
     err = _native.ErrBuf()
-    for m in (200, 48):
+    for m in (512, 200, 48):
         print(f"[gpu] noalloc gemm m={m} n={rows} k={cols}", flush=True)
         xb = syn.activation_bf16(m, cols, seed=m)
         x = torch.from_numpy(xb.view("int16")).cuda()
@@ -58,9 +59,9 @@ def test_noalloc_gemm_checks_arguments():
 
     ops.init(0)
     lib = _native.load()
-    data = syn.q4_k_matrix(64, 256, seed=5)
+    data = syn.q6_k_matrix(64, 256, seed=5)
     w_dev = torch.from_numpy(data.reshape(-1)).cuda()
-    dw = ops.DeviceWeight(syn.Q4_K, w_dev.data_ptr(), 64, 256)
+    dw = ops.DeviceWeight(syn.Q6_K, w_dev.data_ptr(), 64, 256)
     err = _native.ErrBuf()
     buf = torch.zeros(64 * 256, dtype=torch.float32, device="cuda")
     rc = lib.gollek_hip_gemm_bf16_device_noalloc(dw.handle, ctypes.c_void_p(buf.data_ptr()), 1,
