@@ -634,15 +634,28 @@ struct MoeShape {
     int down_type;
 };
 
+static bool moe_type(int32_t t) {
+    return t == GOLLEK_HIP_Q4_0 || t == GOLLEK_HIP_Q8_0 || t == GOLLEK_HIP_Q4_K || t == GOLLEK_HIP_Q5_K ||
+           t == GOLLEK_HIP_Q6_K;
+}
+
+// The grouped expert FFN on the kernels that take the types and shape.
+static hipError_t moe_launch(const MoeShape &sh, gollek_hip_weight *gate, gollek_hip_weight *up,
+                             gollek_hip_weight *down, const float *x, const int32_t *ids, const float *w,
+                             int64_t tokens, int64_t top_k, float *out, uint8_t *ws, hipStream_t s) {
+    return gollek::launch_moe(gate->type_id, up->type_id, down->type_id, gate->data, up->data, down->data,
+                              gate->row_bytes, up->row_bytes, down->row_bytes, sh.E, sh.H, sh.I, x, ids, w,
+                              (int)tokens, (int)top_k, out, ws, s);
+}
+
 static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_hip_weight *down,
                          int64_t n_experts, int64_t tokens, int64_t top_k, MoeShape *shape,
                          char *err, size_t err_len) {
     if (gate == nullptr || up == nullptr || down == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "expert weights");
-    if (gate->type_id != GOLLEK_HIP_Q4_K || up->type_id != GOLLEK_HIP_Q4_K ||
-        (down->type_id != GOLLEK_HIP_Q4_K && down->type_id != GOLLEK_HIP_Q6_K))
+    if (!moe_type(gate->type_id) || !moe_type(up->type_id) || !moe_type(down->type_id))
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "Unsupported MoE expert weight types %d/%d/%d (Q4_K gate/up, Q4_K or Q6_K down)",
+                    "Unsupported MoE expert weight types %d/%d/%d (Q8_0, Q4_0, Q4_K, Q5_K or Q6_K)",
                     gate->type_id, up->type_id, down->type_id);
     if (n_experts <= 0 || gate->rows % n_experts != 0)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Gate rows %lld are not a multiple of %lld experts",
@@ -653,21 +666,9 @@ static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_
                     "Expert shapes disagree: gate %lldx%lld up %lldx%lld down %lldx%lld",
                     (long long)gate->rows, (long long)gate->cols, (long long)up->rows,
                     (long long)up->cols, (long long)down->rows, (long long)down->cols);
-    if (H > 4096 || I > 4096)
-        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "MoE hidden %lld / inter %lld above 4096 are not supported", (long long)H,
-                    (long long)I);
     if (tokens < 0 || top_k <= 0 || tokens * top_k > (1 << 24))
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Invalid tokens %lld / top_k %lld",
                     (long long)tokens, (long long)top_k);
-    if (down->type_id == GOLLEK_HIP_Q6_K &&
-        !gollek::moe_q6k_down_supported((int)n_experts, (int)H, (int)I, (int)tokens, (int)top_k))
-        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "Q6_K down experts need hidden <= 4096 (past 2048 an even multiple of 256), "
-                    "inter <= 1024 (multiples of 256), <= 256 experts, top_k <= 64 and tokens * top_k <= 2048");
-    for (gollek_hip_weight *w : {gate, up, down})
-        if ((reinterpret_cast<uintptr_t>(w->data) & 15u) != 0)
-            return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Expert weights must be 16-byte aligned");
     shape->E = (int)n_experts;
     shape->H = (int)H;
     shape->I = (int)I;
@@ -696,18 +697,13 @@ int32_t gollek_hip_moe_grouped_device(gollek_hip_weight *gate, gollek_hip_weight
     }
     if (x == nullptr || ids == nullptr || weights == nullptr || out == nullptr || workspace == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE buffers");
-    if (sh.down_type == GOLLEK_HIP_Q6_K && (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
-        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "x must be 16-byte aligned with Q6_K down experts");
     const int64_t need = gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
     if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
                     "Workspace of %lld bytes (256-byte aligned) needed, got %lld",
                     (long long)need, (long long)workspace_bytes);
-    hipError_t e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
-                                          down->row_bytes, sh.E, sh.H, sh.I, x, ids, weights,
-                                          (int)tokens, (int)top_k, out,
-                                          static_cast<uint8_t *>(workspace),
-                                          static_cast<hipStream_t>(stream), sh.down_type);
+    hipError_t e = moe_launch(sh, gate, up, down, x, ids, weights, tokens, top_k, out,
+                              static_cast<uint8_t *>(workspace), static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "moe launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -762,9 +758,7 @@ int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
     }
     float *k_out = hs != nullptr ? reinterpret_cast<float *>(hs + xb) : d_out;
     if (e == hipSuccess)
-        e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
-                                   down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
-                                   (int)top_k, k_out, d_ws, s, sh.down_type);
+        e = moe_launch(sh, gate, up, down, d_x, d_ids, d_w, tokens, top_k, k_out, d_ws, s);
     if (e == hipSuccess && hs == nullptr) e = hipMemcpyAsync(out, d_out, xn, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "moe", err, err_len);
@@ -873,8 +867,6 @@ int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *
     if (x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr || out == nullptr ||
         workspace == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "MoE block buffers");
-    if (sh.down_type == GOLLEK_HIP_Q6_K && (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
-        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "x must be 16-byte aligned with Q6_K down experts");
     const int64_t need = gollek_hip_moe_workspace_bytes(tokens, top_k, sh.H, sh.I, sh.E);
     if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
@@ -884,9 +876,8 @@ int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *
     hipError_t e = gollek::launch_moe_topk(logits, (int)tokens, sh.E, (int)top_k,
                                            scoring == GOLLEK_HIP_ROUTER_SIGMOID, ids, weights, s);
     if (e == hipSuccess)
-        e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes, down->row_bytes,
-                                   sh.E, sh.H, sh.I, x, ids, weights, (int)tokens, (int)top_k, out,
-                                   static_cast<uint8_t *>(workspace), s, sh.down_type);
+        e = moe_launch(sh, gate, up, down, x, ids, weights, tokens, top_k, out,
+                       static_cast<uint8_t *>(workspace), s);
     if (e != hipSuccess) return hip_fail(e, "moe block launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -945,9 +936,7 @@ int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
         e = gollek::launch_moe_topk(d_l, (int)tokens, sh.E, (int)top_k,
                                     scoring == GOLLEK_HIP_ROUTER_SIGMOID, d_ids, d_w, s);
     if (e == hipSuccess)
-        e = gollek::launch_moe_q4k(gate->data, up->data, down->data, gate->row_bytes,
-                                   down->row_bytes, sh.E, sh.H, sh.I, d_x, d_ids, d_w, (int)tokens,
-                                   (int)top_k, k_out, d_ws, s, sh.down_type);
+        e = moe_launch(sh, gate, up, down, d_x, d_ids, d_w, tokens, top_k, k_out, d_ws, s);
     if (e == hipSuccess && hs == nullptr) e = hipMemcpyAsync(out, d_out, xn, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "moe block", err, err_len);

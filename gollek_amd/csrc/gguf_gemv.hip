@@ -23,6 +23,7 @@
 //    RB * (bytes per row) in flight.
 #include <algorithm>
 
+#include "gguf_block_dot.hpp"
 #include "gguf_blocks.hpp"
 #include "gguf_kernels.hpp"
 
@@ -346,65 +347,6 @@ __global__ __launch_bounds__(256) void gemv_q4_0_kernel(const uint8_t *__restric
 // loads.  Used for shapes the fast kernels do not cover (odd block counts,
 // very long rows, unaligned borrowed buffers: x not 16-byte aligned, or
 // weights off the alignment a fast kernel reads them at).
-__device__ float generic_block_dot(int type_id, const uint8_t *blk, const float *xb) {
-    if (type_id == kQ8_0) {
-        const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-        float s = 0.0f;
-        for (int i = 0; i < 32; i++) s = fmaf((float)(int)(int8_t)blk[2 + i], xb[i], s);
-        return d * s;
-    }
-    if (type_id == kQ4_0) {
-        const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-        float s = 0.0f;
-        for (int i = 0; i < 16; i++) {
-            const int q = blk[2 + i];
-            s = fmaf((float)((q & 0x0F) - 8), xb[i], s);
-            s = fmaf((float)((q >> 4) - 8), xb[16 + i], s);
-        }
-        return d * s;
-    }
-    if (type_id == kQ6_K) {  // element e: scale e / 16, code - 32
-        const float d = half_bits_to_float_fast((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
-        float total = 0.0f;
-        for (int g = 0; g < 16; g++) {
-            float s = 0.0f;
-            for (int k = 0; k < 16; k++) {
-                const int e = 16 * g + k, h = e >> 7, j = (e >> 5) & 3, l = e & 31;
-                const int ql = blk[64 * h + 32 * (j & 1) + l];
-                const int q = ((j < 2 ? ql : ql >> 4) & 0x0F) | (((blk[128 + 32 * h + l] >> (2 * j)) & 3) << 4);
-                s = fmaf((float)(q - 32), xb[e], s);
-            }
-            total = fmaf(d * (float)(int8_t)blk[192 + g], s, total);
-        }
-        return total;
-    }
-    // Q4_K, or Q5_K (qh[32] at 16, quants at 48; bit 2c / 2c+1 of qh[i] adds 16)
-    const bool q5 = type_id == kQ5_K;
-    const int qs = q5 ? 48 : 16;
-    const float d = half_bits_to_float_fast((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    const float dmin = half_bits_to_float_fast((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
-    float total = 0.0f;
-    for (int c = 0; c < 4; c++) {
-        int sc1, mc1, sc2, mc2;
-        q4k_code(blk + 4, 2 * c, &sc1, &mc1);
-        q4k_code(blk + 4, 2 * c + 1, &sc2, &mc2);
-        float a1 = 0.0f, a2 = 0.0f, v1 = 0.0f, v2 = 0.0f;
-        for (int i = 0; i < 32; i++) {
-            const int q = blk[qs + 32 * c + i];
-            const int hb = q5 ? blk[16 + i] : 0;
-            const float x1 = xb[64 * c + i], x2 = xb[64 * c + 32 + i];
-            a1 = fmaf((float)((q & 0x0F) + (((hb >> (2 * c)) & 1) << 4)), x1, a1);
-            a2 = fmaf((float)((q >> 4) + (((hb >> (2 * c + 1)) & 1) << 4)), x2, a2);
-            v1 += x1;
-            v2 += x2;
-        }
-        const float m1 = mc1 ? dmin * (float)mc1 : 0.0f;
-        const float m2 = mc2 ? dmin * (float)mc2 : 0.0f;
-        total += d * (float)sc1 * a1 + d * (float)sc2 * a2 - (m1 * v1 + m2 * v2);
-    }
-    return total;
-}
-
 __global__ __launch_bounds__(256) void gemv_generic_kernel(int type_id,
                                                            const uint8_t *__restrict__ w,
                                                            int64_t row_bytes, int nb, int bs,

@@ -123,14 +123,20 @@ struct MoeLayout {
 };
 MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inter, int64_t experts);
 
-// out[T, H] = sum_j w[t,j] down_e(silu(gate_e x_t) * up_e x_t) for Q4_K stacked
-// gate / up experts and Q4_K or (down_type kQ6_K, where
-// moe_q6k_down_supported) Q6_K down experts; ws must hold
+// out[T, H] = sum_j w[t,j] down_e(silu(gate_e x_t) * up_e x_t) for stacked
+// gate / up / down experts of types Q8_0, Q4_0, Q4_K, Q5_K or Q6_K (each
+// matrix its own type): the matrix-core passes for Q4_K gate / up with Q4_K
+// or Q6_K down where they take the shape, the v_dot4 passes for all-Q4_K
+// otherwise, the generic passes for everything else; ws must hold
 // moe_layout(...).total bytes.
-hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                          int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
-                          const float *x, const int32_t *ids, const float *wts, int T, int top_k,
-                          float *out, uint8_t *ws, hipStream_t stream, int down_type = 12);
+hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *gate, const uint8_t *up,
+                      const uint8_t *down, int64_t gate_row_bytes, int64_t up_row_bytes,
+                      int64_t down_row_bytes, int E, int H, int I, const float *x, const int32_t *ids,
+                      const float *wts, int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);
+hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                               int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
+                               const float *x, const int32_t *ids, const float *wts, int T, int top_k,
+                               float *out, uint8_t *ws, hipStream_t stream);
 // Whether the matrix-core passes can take Q6_K down experts of this shape
 // (the token-major down pass; x must also be 16-byte aligned).
 bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k);

@@ -22,6 +22,7 @@
 //   5. down: per (used expert, row tile), y_pair = down_e h;
 //   6. combine: out[t] = sum_j w[t,j] y_pair[t,j] in j order (plain fp32
 //      multiply then add, as MFP:461-472 accumulates).
+#include "gguf_block_dot.hpp"
 #include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"
 
@@ -275,6 +276,48 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *__restr
     out[i] = acc;
 }
 
+// Any expert types (Q8_0, Q4_0, Q4_K, Q5_K, Q6_K), any alignment: rows
+// [r0, r0 + rows_per_block) of expert e against each of the expert's
+// vectors, one wave per row and one lane per block (fp32, byte loads).
+// GATED: out[p][r] = silu(w0 . v) * (w1 . v) with w0, w1 of types t0, t1,
+// else out[p][r] = w0 . v.  Vector of pair p: vec[(by_pair ? p : p / top_k)
+// * vec_stride].  The expert's rows are re-read per route from the caches.
+template <bool GATED>
+__global__ __launch_bounds__(256) void moe_generic_expert_kernel(
+    int t0, int t1, const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, int64_t rb0,
+    int64_t rb1, int cols, int rows_per_expert, int rows_per_block, const float *__restrict__ vec,
+    int64_t vec_stride, int by_pair, int top_k, const int32_t *__restrict__ meta, int E, int P,
+    float *__restrict__ out, int64_t out_stride) {
+    const int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
+    const int32_t *used = pairs + P;
+    if ((int)blockIdx.y >= used[E]) return;
+    const int e = used[blockIdx.y];
+    const int cnt = counts[e], p0 = offsets[e];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bs0 = block_elems(t0), bb0 = block_bytes(t0), bs1 = block_elems(t1), bb1 = block_bytes(t1);
+    const int nb0 = cols / bs0, nb1 = GATED ? cols / bs1 : 0;
+    const int r_lo = blockIdx.x * rows_per_block;
+    const int r_hi = min(rows_per_expert, r_lo + rows_per_block);
+    for (int r = r_lo + wave; r < r_hi; r += 4) {
+        const uint8_t *row0 = w0 + ((int64_t)e * rows_per_expert + r) * rb0;
+        const uint8_t *row1 = GATED ? w1 + ((int64_t)e * rows_per_expert + r) * rb1 : nullptr;
+        for (int c = 0; c < cnt; c++) {
+            const int p = pairs[p0 + c];
+            const float *v = vec + (int64_t)(by_pair ? p : p / top_k) * vec_stride;
+            float a = 0.0f;
+            for (int b = lane; b < nb0; b += 64) a += generic_block_dot(t0, row0 + (int64_t)b * bb0, v + b * bs0);
+            a = group_sum<64>(a);
+            if (GATED) {
+                float u = 0.0f;
+                for (int b = lane; b < nb1; b += 64) u += generic_block_dot(t1, row1 + (int64_t)b * bb1, v + b * bs1);
+                u = group_sum<64>(u);
+                a = a / (1.0f + expf(-a)) * u;  // silu(gate) * up
+            }
+            if (lane == 0) out[(int64_t)p * out_stride + r] = a;
+        }
+    }
+}
+
 namespace {
 
 template <bool GATED>
@@ -318,17 +361,58 @@ hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float 
     return hipGetLastError();
 }
 
-hipError_t launch_moe_q4k(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                          int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
-                          const float *x, const int32_t *ids, const float *wts, int T, int top_k,
-                          float *out, uint8_t *ws, hipStream_t stream, int down_type) {
-    if (down_type == kQ6_K) {  // the matrix-core passes only
-        if (!moe_q4k_mfma_supported(E, H, I, T * top_k, x) || !moe_q6k_down_supported(E, H, I, T, top_k))
-            return hipErrorInvalidValue;
+// Expert FFN on the generic kernels: routing, gate/up (h = silu(g) u into
+// the workspace's h), down (per-route rows into ypair), route-order combine.
+hipError_t launch_moe_generic(int gate_type, int up_type, int down_type, const uint8_t *gate,
+                              const uint8_t *up, const uint8_t *down, int64_t gate_row_bytes,
+                              int64_t up_row_bytes, int64_t down_row_bytes, int E, int H, int I,
+                              const float *x, const int32_t *ids, const float *wts, int T, int top_k,
+                              float *out, uint8_t *ws, hipStream_t stream) {
+    const MoeLayout L = moe_layout(T, top_k, H, I, E);
+    const int P = T * top_k;
+    int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
+    hipError_t err = launch_moe_route(ids, wts, P, E, 0, 0, meta, stream);
+    if (err != hipSuccess) return err;
+    float *h = reinterpret_cast<float *>(ws + L.h);
+    float *ypair = reinterpret_cast<float *>(ws + L.ypair);
+    constexpr int kRows = 64;
+    hipLaunchKernelGGL(moe_generic_expert_kernel<true>, dim3((I + kRows - 1) / kRows, E), dim3(256), 0, stream,
+                       gate_type, up_type, gate, up, gate_row_bytes, up_row_bytes, H, I, kRows, x, (int64_t)H, 0,
+                       top_k, meta, E, P, h, (int64_t)I);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(moe_generic_expert_kernel<false>, dim3((H + kRows - 1) / kRows, E), dim3(256), 0, stream,
+                       down_type, down_type, down, down, down_row_bytes, down_row_bytes, I, H, kRows, h,
+                       (int64_t)I, 1, top_k, meta, E, P, ypair, (int64_t)H);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_moe_combine(ids, wts, ypair, T, top_k, H, E, out, stream);
+}
+
+hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *gate, const uint8_t *up,
+                      const uint8_t *down, int64_t gate_row_bytes, int64_t up_row_bytes,
+                      int64_t down_row_bytes, int E, int H, int I, const float *x, const int32_t *ids,
+                      const float *wts, int T, int top_k, float *out, uint8_t *ws, hipStream_t stream) {
+    const bool aligned = ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
+                           reinterpret_cast<uintptr_t>(down) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+    const bool q4k_gu = gate_type == kQ4_K && up_type == kQ4_K;
+    // Q4_K gate / up with Q4_K or (where the token-major down pass takes the
+    // shape) Q6_K down: the matrix-core passes.
+    if (aligned && q4k_gu && tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, T * top_k, x) &&
+        (down_type == kQ4_K || (down_type == kQ6_K && moe_q6k_down_supported(E, H, I, T, top_k))))
         return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream, down_type);
-    }
-    if (tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, T * top_k, x))
-        return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream, down_type);
+    // All Q4_K up to hidden / inter 4096: the v_dot4 passes.
+    if (aligned && q4k_gu && down_type == kQ4_K && H % kQK == 0 && I % kQK == 0 && H <= 4096 && I <= 4096)
+        return launch_moe_q4k_dot4(gate, up, down, gate_row_bytes, down_row_bytes, E, H, I, x, ids, wts, T,
+                                   top_k, out, ws, stream);
+    return launch_moe_generic(gate_type, up_type, down_type, gate, up, down, gate_row_bytes, up_row_bytes,
+                              down_row_bytes, E, H, I, x, ids, wts, T, top_k, out, ws, stream);
+}
+
+hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                               int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
+                               const float *x, const int32_t *ids, const float *wts, int T, int top_k,
+                               float *out, uint8_t *ws, hipStream_t stream) {
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);

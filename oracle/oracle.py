@@ -234,15 +234,16 @@ def moe_reference(gate_w: np.ndarray, up_w: np.ndarray, down_w: np.ndarray, x: n
 
 def moe_reference_q4k(gate: np.ndarray, up: np.ndarray, down: np.ndarray, n_experts: int,
                       x: np.ndarray, ids: np.ndarray, weights: np.ndarray,
-                      down_type: int = Q4_K) -> np.ndarray:
-    """moe_reference over packed stacked Q4_K gate / up experts and Q4_K or
-    Q6_K (down_type) down experts, dequantizing only the experts the routes
-    use (bit-exact dequantization, fp64 arithmetic).
+                      down_type: int = Q4_K, gate_type: int = Q4_K) -> np.ndarray:
+    """moe_reference over packed stacked gate / up experts of gate_type and
+    down experts of down_type (Q8_0, Q4_0, Q4_K, Q5_K or Q6_K), dequantizing
+    only the experts the routes use (bit-exact dequantization, fp64
+    arithmetic).
 
-    gate, up: (E * I, H / 256 * 144) bytes; down: (E * H, I / 256 * block
-    bytes of down_type).  Routes with an id outside [0, E) or a zero weight
+    gate, up: (E * I, row bytes of H columns); down: (E * H, row bytes of I
+    columns); x: (T, H).  Routes with an id outside [0, E) or a zero weight
     are skipped (MoeForwardPass.java:222)."""
-    H = gate.shape[1] // 144 * 256
+    H = np.asarray(x).shape[1]
     I = gate.shape[0] // n_experts
     T, k = ids.shape
     out = np.zeros((T, H), dtype=np.float64)
@@ -254,8 +255,8 @@ def moe_reference_q4k(gate: np.ndarray, up: np.ndarray, down: np.ndarray, n_expe
             if e < 0 or e >= n_experts or wj == 0.0:
                 continue
             if e not in cache:
-                cache[e] = (dequantize(Q4_K, gate[e * I:(e + 1) * I], H).astype(np.float64),
-                            dequantize(Q4_K, up[e * I:(e + 1) * I], H).astype(np.float64),
+                cache[e] = (dequantize(gate_type, gate[e * I:(e + 1) * I], H).astype(np.float64),
+                            dequantize(gate_type, up[e * I:(e + 1) * I], H).astype(np.float64),
                             dequantize(down_type, down[e * H:(e + 1) * H], I).astype(np.float64))
             g, u, d = cache[e]
             h = silu(g @ xt) * (u @ xt)

@@ -20,12 +20,12 @@ def _init():
     ops.init(0)
 
 
-def _experts(E, H, I, seed, down_type=syn.Q4_K):
-    gate = syn.q4_k_matrix(E * I, H, seed)
-    up = syn.q4_k_matrix(E * I, H, seed + 1)
+def _experts(E, H, I, seed, down_type=syn.Q4_K, gate_type=syn.Q4_K):
+    gate = syn.matrix(gate_type, E * I, H, seed)
+    up = syn.matrix(gate_type, E * I, H, seed + 1)
     down = syn.matrix(down_type, E * H, I, seed + 2)
-    tg = ops.GgufTensor("blk.0.ffn_gate_exps.weight", (H, I, E), syn.Q4_K, gate.reshape(-1))
-    tu = ops.GgufTensor("blk.0.ffn_up_exps.weight", (H, I, E), syn.Q4_K, up.reshape(-1))
+    tg = ops.GgufTensor("blk.0.ffn_gate_exps.weight", (H, I, E), gate_type, gate.reshape(-1))
+    tu = ops.GgufTensor("blk.0.ffn_up_exps.weight", (H, I, E), gate_type, up.reshape(-1))
     td = ops.GgufTensor("blk.0.ffn_down_exps.weight", (I, H, E), down_type, down.reshape(-1))
     return gate, up, down, tg, tu, td
 
@@ -80,18 +80,29 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
         t.close()
 
 
-def test_moe_q6_k_down_rejects_unsupported_shapes():
-    # Q6_K down experts run only on the matrix-core passes' token-major down
-    # pass: inter above 1024, or hidden past 2048 with an odd number of
-    # superblocks (no equal K-halves) -> UNSUPPORTED; Q5_K down is not taken.
-    for (E, H, I, dt) in [(4, 512, 1280, syn.Q6_K), (4, 2304, 256, syn.Q6_K), (4, 512, 256, syn.Q5_K)]:
-        gate, up, down, tg, tu, td = _experts(E, H, I, seed=1, down_type=dt)
-        x = syn.activation(2 * H, seed=2).reshape(2, H)
-        ids, w = syn.moe_routing(2, E, 2, seed=3)
-        with pytest.raises(ops.UnsupportedOperationError):
-            ops.moe_grouped(tg, tu, td, E, x, ids, w)
-        for t in (tg, tu, td):
-            t.close()
+# Expert types and shapes the matrix-core passes do not take run on the
+# generic passes: Q8_0 / Q4_0 / Q5_K / Q6_K gate and up, Q8_0 / Q4_0 / Q5_K
+# down, and Q6_K down beyond the token-major down pass (inter above 1024,
+# hidden past 2048 with an odd superblock count, more than 2048 routes).
+@pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
+    (syn.Q8_0, syn.Q8_0, 128, 2048, 768, 16, 8), (syn.Q4_0, syn.Q4_0, 128, 2048, 768, 16, 8),
+    (syn.Q8_0, syn.Q6_K, 16, 1024, 512, 9, 4), (syn.Q4_0, syn.Q5_K, 16, 512, 256, 7, 2),
+    (syn.Q4_K, syn.Q5_K, 8, 512, 256, 5, 2), (syn.Q5_K, syn.Q4_K, 8, 512, 256, 5, 2),
+    (syn.Q6_K, syn.Q6_K, 8, 512, 256, 5, 2), (syn.Q4_K, syn.Q8_0, 8, 512, 256, 5, 2),
+    (syn.Q4_K, syn.Q6_K, 4, 512, 1280, 6, 2), (syn.Q4_K, syn.Q6_K, 4, 2304, 256, 6, 2),
+    (syn.Q4_K, syn.Q6_K, 16, 512, 256, 300, 8), (syn.Q8_0, syn.Q4_0, 8, 96, 160, 5, 2)])
+def test_moe_other_types_parity(gt, dt, E, H, I, T, k):
+    print(f"[gpu] moe types gate={gt} down={dt} E={E} H={H} I={I} T={T} k={k}", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + I, down_type=dt, gate_type=gt)
+    ids, w = syn.moe_routing(T, E, k, seed=5)
+    x = syn.activation(T * H, seed=6).reshape(T, H)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=gt)
+    err = o.rel_err(out, ref)
+    print(f"[gpu] moe types rel_err={err:.3e}", flush=True)
+    assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
 
 
 @pytest.fixture
