@@ -39,7 +39,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gollek_hip_init": (_I32, [_I32, _CHARP, _SZ]),
     "gollek_hip_last_error": (_CHARP, []),
     "gollek_hip_last_status": (_I32, []),
-    "gollek_hip_set_option": (_I32, [_CHARP, _I64, _CHARP, _SZ]),
     "gollek_hip_weight_upload": (_P, [_I32, _P, _I64, _I64, _I64, _CHARP, _SZ]),
     "gollek_hip_weight_wrap_device": (_P, [_I32, _P, _I64, _I64, _I64, _CHARP, _SZ]),
     "gollek_hip_weight_free": (None, [_P]),
@@ -73,6 +72,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gollek_hip_gguf_upload": (_P, [_P, _I64, _CHARP, _SZ]),
 }
 
+# Test-only export (gollek_amd/csrc/gollek_hip_testing.h; not part of the
+# drop-in ABI): forces a GEMV / MoE kernel family onto shapes another one
+# is picked for, so the parity tests reach every family.
+TESTING_SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "gollek_hip_testing_set_option": (_I32, [_CHARP, _I64, _CHARP, _SZ]),
+}
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -89,7 +95,7 @@ def load() -> ctypes.CDLL:
                 f"{path} is not built; build it with "
                 "`python -c 'import __graft_entry__ as g; g.build()'`")
         lib = ctypes.CDLL(str(path))
-        for name, (restype, argtypes) in SIGNATURES.items():
+        for name, (restype, argtypes) in {**SIGNATURES, **TESTING_SIGNATURES}.items():
             fn = getattr(lib, name, None)
             if fn is None:
                 continue  # symbol tests report missing exports explicitly

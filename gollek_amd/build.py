@@ -28,7 +28,6 @@ HIP_SOURCES = (
     "gguf_file.hip",
     "gguf_gemv.hip",
     "gguf_k56.hip",
-    "gguf_gemv_dot4.hip",
     "gguf_gemv_mfma.hip",
     "gguf_gemv_q6k_mfma.hip",
     "gguf_gemv_ring.hip",

@@ -17,6 +17,7 @@
 
 #include "gguf_kernels.hpp"
 #include "gollek_hip.h"
+#include "gollek_hip_testing.h"
 
 struct gollek_hip_weight {
     int32_t type_id = 0;
@@ -252,15 +253,13 @@ const char *gollek_hip_last_error(void) { return g_last_error.c_str(); }
 
 int32_t gollek_hip_last_status(void) { return g_last_status; }
 
-int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t err_len) {
+int32_t gollek_hip_testing_set_option(const char *key, int64_t value, char *err, size_t err_len) {
     if (key == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "key");
     gollek::LaunchTuning &t = gollek::tuning();
-    if (strcmp(key, "gemv_rows_per_wave") == 0) t.gemv_rows_per_wave = value;
-    else if (strcmp(key, "gemv_row_batch") == 0) t.gemv_row_batch = (int)value;
-    else if (strcmp(key, "gemv_waves_per_cu") == 0) t.gemv_waves_per_cu = value > 0 ? (int)value : 8;
-    else if (strcmp(key, "gemv_variant") == 0) t.gemv_variant = (int)value;
-    else if (strcmp(key, "moe_variant") == 0) t.moe_variant = (int)value;
-    else return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Unknown option %s", key);
+    if (strcmp(key, "gemv_variant") == 0 && (value == 0 || value == 1 || value == 3 || value == 4))
+        t.gemv_variant = (int)value;
+    else if (strcmp(key, "moe_variant") == 0 && (value == 0 || value == 1)) t.moe_variant = (int)value;
+    else return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Unknown option %s = %lld", key, (long long)value);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }

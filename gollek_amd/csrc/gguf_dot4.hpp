@@ -1,5 +1,5 @@
-// gguf_dot4.hpp -- shared device code of the Q4_K integer-dot kernels
-// (GEMV in gguf_gemv_dot4.hip, MoE expert FFN in gguf_moe.hip).
+// gguf_dot4.hpp -- device code of the Q4_K integer-dot MoE expert passes
+// (gguf_moe.hip) and buffer / LDS helpers the matrix-core kernels share.
 //
 // A vector x is held as "digit planes": per 32-element group g, a power-of-two
 // scale s_g = 2^(e-23) with max|x_g| < 2^e, the exact integers

@@ -127,14 +127,10 @@ __device__ __forceinline__ void u8x4_bf16(uint32_t w, uint32_t &a, uint32_t &b) 
     b = pack_bf16x2(byte_f(w, 2), byte_f(w, 3));
 }
 
-// 16-byte and 4-byte buffer->LDS loads (plain __device__ functions: the
-// builtin used directly in a kernel template's body drops hipcc's host launch
-// stub).
+// 16-byte buffer->LDS load (a plain __device__ function: the builtin used
+// directly in a kernel template's body drops hipcc's host launch stub).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, void *dst, uint32_t off) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 16, off, 0, 0, 0);
-}
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rs, void *dst, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)dst, 4, off, 0, 0, 0);
 }
 
 // Stage barriers (compiler memory barriers too): a loader wave first waits

@@ -399,12 +399,9 @@ template <int LPR, int ROUNDS, int RB>
 hipError_t launch_fixed(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                         const float *x, float *y, int64_t rows, hipStream_t stream) {
     constexpr int RG = 64 / LPR;
-    const LaunchTuning &t = tuning();
-    int64_t rpw = t.gemv_rows_per_wave;
-    if (rpw <= 0) {
-        const int64_t target_waves = (int64_t)device_cus() * t.gemv_waves_per_cu;
-        rpw = (rows + target_waves - 1) / target_waves;
-    }
+    // About eight waves per CU, each over a run of whole row groups.
+    const int64_t target_waves = (int64_t)device_cus() * 8;
+    int64_t rpw = (rows + target_waves - 1) / target_waves;
     rpw = ((rpw + RG - 1) / RG) * RG;  // whole row groups
     if (rpw < RG) rpw = RG;
     const int64_t waves = (rows + rpw - 1) / rpw;
@@ -425,8 +422,7 @@ hipError_t launch_fixed(int type_id, const uint8_t *w, int64_t row_bytes, int64_
 template <int LPR, int ROUNDS>
 hipError_t launch_rb(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                      const float *x, float *y, int64_t rows, hipStream_t stream) {
-    int rb = tuning().gemv_row_batch;
-    if (rb <= 0) rb = (type_id == kQ4_K) ? 4 : 2;
+    const int rb = (type_id == kQ4_K) ? 4 : 2;  // rows per load batch
     if (rb >= 4 && ROUNDS <= 2) return launch_fixed<LPR, ROUNDS, 4>(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (rb >= 2) return launch_fixed<LPR, ROUNDS, 2>(type_id, w, row_bytes, cols, x, y, rows, stream);
     return launch_fixed<LPR, ROUNDS, 1>(type_id, w, row_bytes, cols, x, y, rows, stream);
@@ -443,7 +439,6 @@ const char *gemv_variant_name(int type_id, int64_t row_bytes, int64_t cols, cons
         return gemv_k56_supported(type_id, row_bytes, w, x) ? "gemv_k56_kernel" : "gemv_generic_kernel";
     const GemvPlan p = plan_for(type_id, row_bytes, cols, w, x);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_mfma_kernel";
-    if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, 1, w, x)) return "gemv_q4_k_dot4_kernel";
     if (gemv_ring_supported(type_id, row_bytes, cols, 1, w, x)) return "gemv_ring_kernel";
     if (p.lpr == 0) return "gemv_generic_kernel";
     if (type_id == kQ4_K) return "gemv_q4_k_kernel";
@@ -465,8 +460,6 @@ hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t
         return launch_gemv_k56(type_id, w, row_bytes, cols, x, y, rows, stream);
     if (type_id == kQ4_K && q4k_mfma_supported(row_bytes, cols, rows, w, x))
         return launch_gemv_q4k_mfma(w, row_bytes, cols, x, y, rows, stream, prep, prep_rows);
-    if (type_id == kQ4_K && q4k_dot4_supported(row_bytes, cols, rows, w, x))
-        return launch_gemv_q4k_dot4(w, row_bytes, cols, x, y, rows, stream);
     if (gemv_ring_supported(type_id, row_bytes, cols, rows, w, x))
         return launch_gemv_ring(type_id, w, row_bytes, cols, x, y, rows, stream);
     const GemvPlan p = is_k56(type_id) ? GemvPlan() : plan_for(type_id, row_bytes, cols, w, x);

@@ -998,7 +998,7 @@ MfmaPlan plan_mfma(int64_t rows, int nsb) {
 bool q4k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
                         const float *x) {
     (void)rows;  // a workgroup's descriptor spans <= kMaxParts rows of <= 64 superblocks
-    if (tuning().gemv_variant == 1 || tuning().gemv_variant == 2) return false;
+    if (tuning().gemv_variant == 1) return false;
     const int64_t nsb = cols / kQK;
     return nsb >= 1 && nsb <= 64 && row_bytes == nsb * kQKBlockBytes &&
            (reinterpret_cast<uintptr_t>(w) & 15u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
@@ -1058,7 +1058,7 @@ hipError_t launch_gemv_q4k_mfma(const uint8_t *w, int64_t row_bytes, int64_t col
 bool q5k_wide_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x) {
     (void)rows;
     const int v = tuning().gemv_variant;
-    if (v == 1 || v == 2 || v == 4) return false;  // the fp32 kernel stays selectable
+    if (v == 1 || v == 4) return false;  // the fp32 kernel stays selectable
     if (cols <= 0 || cols % kQK != 0) return false;
     const int64_t nsb = cols / kQK;
     return nsb > 16 && nsb <= 64 && row_bytes == nsb * kQ5KBlockBytes &&
@@ -1082,7 +1082,7 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
                         const float *x) {
     if (type_id != kQ4_0 && type_id != kQ8_0 && type_id != kQ5_K) return false;
     const int v = tuning().gemv_variant;
-    if (v == 1 || v == 2 || v == 4) return false;  // fp32 / ring / Q5_K fp32 paths kept selectable
+    if (v == 1 || v == 4) return false;  // fp32 / ring / Q5_K fp32 paths kept selectable
     if (cols <= 0 || cols % kQK != 0 || cols / kQK > 16 * kWideMaxCols || rows <= 0) return false;
     const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     if (row_bytes != cols / kQK * piece || (row_bytes & 15) != 0) return false;
@@ -1130,12 +1130,12 @@ int64_t col_layout_rows(int type_id, int64_t rows, int64_t cols) {
     if (nsb > 16 * kWideMaxCols) return 0;
     if (type_id == kQ4_K) {
         const int v = tuning().gemv_variant;
-        if (v == 1 || v == 2 || v == 3) return 0;
+        if (v == 1 || v == 3) return 0;
         return per <= ColGeom<kQ4_K>::kMaxRows ? per : 0;
     }
     if (type_id != kQ4_0 && type_id != kQ8_0 && type_id != kQ5_K) return 0;
     const int v = tuning().gemv_variant;
-    if (v == 1 || v == 2 || v == 4) return 0;
+    if (v == 1 || v == 4) return 0;
     const int64_t most = type_id == kQ8_0   ? ColGeom<kQ8_0>::kMaxRows
                          : type_id == kQ5_K ? ColGeom<kQ5_K>::kMaxRows
                                             : ColGeom<kQ4_0>::kMaxRows;

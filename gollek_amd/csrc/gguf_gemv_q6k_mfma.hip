@@ -449,7 +449,7 @@ __global__ __launch_bounds__(kQ6Threads) void gemv_q6_k_mfma_tile_kernel(
 
 bool q6k_mfma_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w, const float *x) {
     const int v = tuning().gemv_variant;
-    if (v == 1 || v == 2 || v == 4) return false;  // the fp32 kernel stays selectable
+    if (v == 1 || v == 4) return false;  // the fp32 kernel stays selectable
     if (cols <= 0 || cols % kQK != 0) return false;
     const int64_t nsb = cols / kQK;
     if (nsb % kQ6HalfSb != 0 || nsb > kQ6MaxSbLds) return false;  // whole items; x fits LDS

@@ -304,8 +304,7 @@ hipError_t launch_gemv_k56(int type_id, const uint8_t *w, int64_t row_bytes, int
     // Rows per batch R: 4 (x reused over 4 rows) when that still gives the
     // target wave count, else fewer, so small matrices keep enough waves in
     // flight to cover the load latency.
-    const LaunchTuning &t = tuning();
-    const int64_t target_waves = (int64_t)device_cus() * t.gemv_waves_per_cu;
+    const int64_t target_waves = (int64_t)device_cus() * 8;
     const int R = rows >= 4 * target_waves ? 4 : (rows >= 2 * target_waves ? 2 : 1);
     int64_t rpw = (rows + target_waves - 1) / target_waves;
     rpw = (rpw + R - 1) / R * R;

@@ -10,16 +10,13 @@
 
 namespace gollek {
 
-// Kernel selection knobs read by the launchers (gollek_hip_set_option).
+// Kernel selection read by the launchers (gollek_hip_testing_set_option).
 // Process-wide and atomic: a set_option call on one thread and launches on
 // others do not race, and a launch sees either the old or the new value.
 // Zero means "pick automatically".
 struct LaunchTuning {
     std::atomic<int> cu_count{256};          // compute units of the current device
-    std::atomic<int64_t> gemv_rows_per_wave{0};
-    std::atomic<int> gemv_row_batch{0};      // rows per load batch (1, 2, 4, 8)
-    std::atomic<int> gemv_waves_per_cu{8};   // target resident waves per CU
-    std::atomic<int> gemv_variant{0};        // 0 auto (matrix cores), 1 fp32 kernels, 2 v_dot4 ring (Q4_K),
+    std::atomic<int> gemv_variant{0};        // 0 auto (matrix cores), 1 fp32 kernels,
                                              // 3 Q4_K on shared tiles for K <= 4096, 4 Q8_0 / Q4_0
                                              // rings and Q5_K / Q6_K fp32
     std::atomic<int> moe_variant{0};         // 0 auto (matrix cores), 1 v_dot4 expert kernels
@@ -91,11 +88,6 @@ bool gemv_k56_supported(int type_id, int64_t row_bytes, const void *w, const flo
 hipError_t launch_gemv_k56(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,
                            const float *x, float *y, int64_t rows, hipStream_t stream);
 
-// Q4_K GEMV with integer dot products (gguf_gemv_dot4.hip).
-bool q4k_dot4_supported(int64_t row_bytes, int64_t cols, int64_t rows, const void *w,
-                        const float *x);
-hipError_t launch_gemv_q4k_dot4(const uint8_t *w, int64_t row_bytes, int64_t cols,
-                                const float *x, float *y, int64_t rows, hipStream_t stream);
 
 // Y[M, N] = X[M, K] (bf16 bits) . W[N, K]^T for Q8_0, Q4_0 or Q4_K W
 // (gguf_gemm.hip, gguf_gemm_tile.hip).  Shapes whose output tiles leave CUs

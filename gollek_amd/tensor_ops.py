@@ -77,9 +77,12 @@ def init(device: int = 0) -> None:
 
 
 def set_option(key: str, value: int) -> None:
+    """Test-only kernel-family switch (gollek_hip_testing_set_option): the
+    parity tests force each GEMV / MoE kernel family onto shapes another one
+    is picked for.  Not part of the reference's interface."""
     lib = _native.load()
     err = _native.ErrBuf()
-    check(lib.gollek_hip_set_option(key.encode(), int(value), err.buf, err.size), err)
+    check(lib.gollek_hip_testing_set_option(key.encode(), int(value), err.buf, err.size), err)
 
 
 @dataclass

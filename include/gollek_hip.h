@@ -78,25 +78,6 @@ const char *gollek_hip_last_error(void);
  * success).  Lets a caller map a NULL handle back to the exception type. */
 int32_t gollek_hip_last_status(void);
 
-/* Kernel selection for tests, benchmarks and sweeps; the Java adapter never
- * calls it, and the defaults are the measured choices.  The setting is
- * process-wide (every device and thread) and atomic: launches on other
- * threads see the old or the new value, never a torn one.  Keys: "gemv_rows_per_wave",
- * "gemv_row_batch", "gemv_waves_per_cu", "gemv_variant", "gemm_variant",
- * "gemm_big_config", "moe_variant").  gemv_variant selects the GEMV kernels:
- * 0 = the matrix-core kernels (Q4_K; Q8_0 and Q4_0 with K up to 16384 and at most
- * 32 / 64 rows per CU; Q5_K with K up to 16384; Q6_K with K a multiple of 2048 up
- * to 14336), the buffer->LDS ring kernels (Q8_0, Q4_0
- * otherwise) and the fp32 Q5_K / Q6_K kernel where they apply, 1 = the
- * fp32 kernels, 2 = the v_dot4 kernel (Q4_K, K <= 4096), 3 = as 0 but Q4_K
- * with K <= 4096 always on the shared-tile matrix-core kernel, 4 = as 0 but
- * Q8_0 and Q4_0 on the ring kernels and Q5_K / Q6_K on the fp32 kernel;
- * moe_variant 1 selects the v_dot4 MoE
- * expert kernels instead of the matrix-core passes.  No reference
- * counterpart; the reference reads JVM properties instead
- * (RT/GgufParallelConfig.java:87-101). */
-int32_t gollek_hip_set_option(const char *key, int64_t value, char *err, size_t err_len);
-
 /* Copy a GGUF row-major matrix (rows x cols, cols contiguous; row_bytes =
  * cols / block_size * block_bytes) from host memory to a device handle.  The
  * bytes are the tensor's bytes at dataStart + offset in the mmapped file

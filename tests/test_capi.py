@@ -101,10 +101,16 @@ def test_error_buffer_truncates():
     assert len(small.value) == 7
 
 
-def test_set_option():
-    ops.set_option("gemv_rows_per_wave", 0)
+def test_testing_option_is_outside_the_public_abi():
+    # The kernel-family switch the parity tests use is exported by a
+    # test-only header, not by include/gollek_hip.h.
+    assert "gollek_hip_testing_set_option" not in declared_functions()
+    assert "gollek_hip_set_option" not in declared_functions()
+    ops.set_option("gemv_variant", 0)
     with pytest.raises(ops.IllegalArgumentError):
         ops.set_option("no_such_option", 1)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.set_option("gemv_variant", 2)
 
 
 def test_tensor_shape_rules():

@@ -17,7 +17,7 @@ import pytest
 
 from gollek_amd import build
 
-RING_SOURCES = ["gguf_gemm.hip", "gguf_gemm_tile.hip", "gguf_gemv_dot4.hip", "gguf_gemv_mfma.hip", "gguf_gemv_q6k_mfma.hip",
+RING_SOURCES = ["gguf_gemm.hip", "gguf_gemm_tile.hip", "gguf_gemv_mfma.hip", "gguf_gemv_q6k_mfma.hip",
                 "gguf_gemv_ring.hip", "gguf_moe_mfma.hip"]
 
 
