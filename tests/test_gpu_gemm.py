@@ -107,13 +107,16 @@ def test_gemm_q4_parity_14336(type_id, m):
     assert err <= GEMM_TOL
 
 
-@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K])
-@pytest.mark.parametrize("rows,cols,m", [(48, 96, 3), (16, 64, 20), (40, 512, 7), (20, 768, 5)])
+# Q4_K rows are whole 256-element superblocks, so only Q4_0 takes the
+# K = 64 and K = 96 cases.
+@pytest.mark.parametrize(
+    "type_id,rows,cols,m",
+    [(syn.Q4_0, 48, 96, 3), (syn.Q4_0, 16, 64, 20), (syn.Q4_0, 40, 512, 7), (syn.Q4_0, 20, 768, 5),
+     (syn.Q4_K, 40, 512, 7), (syn.Q4_K, 20, 768, 5)])
 def test_gemm_q4_generic_shapes(type_id, rows, cols, m):
-    # Shapes the tile kernel does not take (K not a multiple of 256): the
-    # one-thread-per-output kernel.
-    if type_id == syn.Q4_K and cols % 256:
-        pytest.skip("Q4_K rows are whole 256-element superblocks")
+    # K = 64 and 96 are not multiples of 256: the one-thread-per-output
+    # kernel.  K = 512 and 768 with fewer than 128 rows and tokens: one
+    # partial tile of the tile kernel.
     print(f"[gpu] gemm generic type={type_id} rows={rows} cols={cols} m={m}", flush=True)
     y, ref = _gemm_case(type_id, rows, cols, m, seed=rows + cols + m)
     assert o.rel_err(y, ref) <= GEMM_TOL
