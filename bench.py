@@ -64,6 +64,9 @@ def parse() -> argparse.Namespace:
                    help="only measure the device's attainable figures: single-launch HBM read "
                         "time by size and grid (plain streaming kernels), the empty-launch "
                         "floor, and a hipBLASLt bf16 GEMM at M = 512 (one JSON line each)")
+    p.add_argument("--ceiling-sizes", default="",
+                   help="with --ceilings: comma list of byte sizes to sweep (default: all), "
+                        "e.g. one size so a kernel trace maps each grid to its size")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 256 MiB device-to-device copy 10 times (known HBM bytes, "
                         "used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -458,7 +461,7 @@ def cpu_moe(gate, up, down, E: int, H: int, I: int, x, ids, wts):
                        f"warm-ups, {threads} threads per mat-vec; oracle")}
 
 
-def ceilings(torch, steps: int, warmup: int) -> int:
+def ceilings(torch, steps: int, warmup: int, only_sizes=()) -> int:
     """Attainable HBM read time per launch (libgollek_ceiling.so: plain
     streaming reads, every load issued up front) by size, load kind and grid;
     the empty-launch floor; a hipBLASLt bf16 GEMM (torch.nn.functional.linear)
@@ -500,6 +503,8 @@ def ceilings(torch, steps: int, warmup: int) -> int:
 
     sizes = (33030144, 2 * 2 ** 20, 8 * 2 ** 20, 17825792, 25362432, 64 * 2 ** 20,
              128 * 2 ** 20, 295501824)
+    if only_sizes:
+        sizes = tuple(only_sizes)
     for nbytes in sizes:
         copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
@@ -568,7 +573,8 @@ def main() -> int:
         return 0
     if args.ceilings:
         import torch
-        return ceilings(torch, min(args.steps, 400), args.warmup)
+        return ceilings(torch, min(args.steps, 400), args.warmup,
+                        [int(v) for v in args.ceiling_sizes.split(",") if v])
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: this path runs on one GPU; "
                                    f"--gpus {args.gpus} is not supported (use --gpus 1)"}))

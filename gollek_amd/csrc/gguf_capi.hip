@@ -356,6 +356,23 @@ int32_t gollek_hip_weight_prepare(gollek_hip_weight *w, char *err, size_t err_le
     return GOLLEK_HIP_OK;
 }
 
+int32_t gollek_hip_weight_unprepare(gollek_hip_weight *w, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    std::lock_guard<std::mutex> lock(w->mu);
+    if (w->prep != nullptr) {
+        const int32_t rc = use_device(w->device, err, err_len);
+        if (rc != GOLLEK_HIP_OK) return rc;
+        // The host entries' launches that read the copy ran on this stream.
+        hipError_t e = hipStreamSynchronize(w->stream);
+        if (e == hipSuccess) e = hipFree(w->prep);
+        w->prep = nullptr;
+        w->prep_rows = 0;
+        if (e != hipSuccess) return hip_fail(e, "unprepare", err, err_len);
+    }
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
 int32_t gollek_hip_weight_info(const gollek_hip_weight *w, int32_t *type_id, int64_t *rows,
                                int64_t *cols, int64_t *row_bytes) {
     if (w == nullptr) return GOLLEK_HIP_ERR_NULL;

@@ -14,13 +14,17 @@
 //
 // Exactness.  Each v_mfma_f32_16x16x32_bf16 contracts one 32-element block
 // (or Q4_K sub-block) of X with the block's integer codes, which bf16 holds
-// exactly (Q8_0 q in [-127, 127], Q4_0 q - 8 in [-8, 7], Q4_K q in [0, 15]);
-// the block's fp32 scale is applied to that fp32 result in one FMA per
-// output, the reference's block structure.  The Q4_K min term needs sum(x)
-// over the sub-block per X row: one more MFMA per 16-row tile with an all-
-// ones B operand puts it in the same lanes as the products, and a second
-// FMA subtracts fl(dmin * m) times it (nothing when the min code is 0, so a
-// non-finite dmin stays out as in RT/GgufKQuantLayout.java:67-69).
+// exactly (Q8_0 q in [-127, 127], Q4_0 q - 8 in [-8, 7]; Q4_K as 128 + q,
+// q in [0, 15]); the block's fp32 scale is applied to that fp32 result in
+// one FMA per output, the reference's block structure.  The Q4_K min term
+// needs sum(x) over the sub-block per X row: one more MFMA per 16-row tile
+// with an all-ones B operand puts it in the same lanes as the products, and
+// a second FMA subtracts (dmin * m + 128 * d) times it, which also removes
+// the codes' offset of 128 (dmin * m is 0 when the min code is 0, so a
+// non-finite dmin stays out as in RT/GgufKQuantLayout.java:67-69).  The
+// offset makes the fp32 sums run at ~128 |x| instead of ~8 |x|: about 2^-17
+// of sum |x| of absolute error per sub-block, far inside the 1e-2 bar, and a
+// non-finite d gives NaN rather than +-inf.
 //
 // Tiling.  A workgroup owns a 128 x 128 tile of Y: 8 compute waves and 2
 // loader waves.  K advances in stages of 64 columns (two blocks).  Compute
@@ -61,9 +65,8 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTileM = 128, kTileN = 128;
+constexpr int kTileMMax = 128, kTileN = 128;  // a tile is 16 MT x 128, MT = 1, 2, 4 or 8
 constexpr int kRowB = 128;                     // LDS bytes per X row per stage (64 bf16)
-constexpr int kXBytes = kTileM * kRowB;        // X stage
 constexpr int kThreads = 640;                  // 8 compute waves + 2 loader waves
 constexpr int kCompute = 512;
 constexpr int kStagePitch = kTileN + 4;        // floats per row of the output staging
@@ -90,19 +93,26 @@ struct RawW<kQ4_K> {
     static constexpr int kChunks = 3, kStageBytes = 0, kSlots = 6;  // 144 bytes per four stages
 };
 
-template <int T>
+// Geometry of a 16 MT x 128 tile: MT row tiles of 16 rows of X.  Tiles of
+// fewer rows (small M) are load-latency bound and use the LDS they leave free
+// for a deeper ring, as deep as the loader waves' vmcnt waits can count.
+template <int T, int MT>
 struct TileGeom {
+    static constexpr int kTileM = 16 * MT;
+    static constexpr int kXBytes = kTileM * kRowB;  // X of a stage
     static constexpr int kPitch = 16 * RawW<T>::kChunks;
     static constexpr int kRawBytes = kTileN * kPitch;
     static constexpr int kSlot = kXBytes + kRawBytes;
-    static constexpr int kSlots = RawW<T>::kSlots;
-    static constexpr int kRing = kSlots * kSlot;
     static constexpr int kInstr = kTileN * RawW<T>::kChunks / 64;  // 16-byte W DMA instructions
     static_assert(kInstr % 2 == 0, "W loads split evenly over the two loader waves");
-    static constexpr int kLoads = 8 + kInstr / 2;                  // loads per loader wave per stage
+    static constexpr int kLoads = MT + kInstr / 2;                 // loads per loader wave per stage
+    static constexpr int kDeep = (160 * 1024 / kSlot) < (63 / kLoads + 2) ? (160 * 1024 / kSlot) : (63 / kLoads + 2);
+    static constexpr int kSlots = MT == 8 ? RawW<T>::kSlots : (kDeep < 8 ? kDeep : 8);
+    static constexpr int kRing = kSlots * kSlot;
     static constexpr bool kMins = T == kQ4_K;
     static_assert(kRing <= 160 * 1024, "LDS budget");
-    static_assert(kRing >= 4 * 8 * 2 * 1024 && kRing >= kTileM * kStagePitch * 4, "epilogue staging");
+    static_assert(kLoads * (kSlots - 2) <= 63, "vmcnt range of the loader waits");
+    static_assert(kRing >= 4 * MT * 2 * 1024 && kRing >= kTileM * kStagePitch * 4, "epilogue staging");
 };
 
 __device__ __forceinline__ uint32_t swz(int r, int kc) {
@@ -121,10 +131,13 @@ __device__ __forceinline__ void s8x4_bf16(uint32_t w, uint32_t &a, uint32_t &b) 
     b = pack_bf16x2((float)(int)(int8_t)((w >> 16) & 0xFFu), (float)(int)(int8_t)(w >> 24));
 }
 
-// Four unsigned bytes -> two dwords of bf16 pairs (v_cvt_f32_ubyteN).
-__device__ __forceinline__ void u8x4_bf16(uint32_t w, uint32_t &a, uint32_t &b) {
-    a = pack_bf16x2(byte_f(w, 0), byte_f(w, 1));
-    b = pack_bf16x2(byte_f(w, 2), byte_f(w, 3));
+// Four 4-bit codes q (one per byte of w) -> two dwords of bf16 pairs
+// holding 128 + q exactly: the bf16 bit pattern 0x4300 | q is 128 + q (at
+// 128 a bf16 step is 1), so one byte permute per pair instead of two
+// conversions.
+__device__ __forceinline__ void q4x4_bf16_128(uint32_t w, uint32_t &a, uint32_t &b) {
+    a = __builtin_amdgcn_perm(0x43434343u, w, 0x04010400u);  // {w.b0, 0x43, w.b1, 0x43}
+    b = __builtin_amdgcn_perm(0x43434343u, w, 0x04030402u);  // {w.b2, 0x43, w.b3, 0x43}
 }
 
 // 16-byte buffer->LDS load (a plain __device__ function: the builtin used
@@ -139,6 +152,16 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, void *dst, uint
 template <int N>
 __device__ __forceinline__ void loader_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+// loader_barrier<KL * later> for a wave-uniform 0 <= later <= L.
+template <int KL, int L>
+__device__ __forceinline__ void loader_barrier_n(int later) {
+    if constexpr (L == 0) {
+        loader_barrier<0>();
+    } else {
+        if (later >= L) loader_barrier<KL * L>();
+        else loader_barrier_n<KL, L - 1>(later);
+    }
 }
 __device__ __forceinline__ void compute_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
@@ -155,10 +178,11 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b) {
 //
 // One stage's operands of a wave: per column tile i (rows 16 apart: +RP
 // bytes) the raw code dwords (q0..q2 at b; Q4_K: q0, q1) and the scale dword
-// (at s; Q4_K: the 16-byte header), then A (8 row tiles of X, at a +
-// 2048 i).  The reads are issued in that order and complete in order, so
-// the raw codes can be widened once ops_wait_raw returns while the A tiles
-// still arrive, and row tile i waits only for its own data (ops_wait_a<i>).
+// (at s; Q4_K: the 16-byte header), then A (MT row tiles of X, at a +
+// 2048 i), each read by its own statement in that order (volatile asm keeps
+// the order).  LDS reads complete in order, so the raw codes can be widened
+// once ops_wait_raw returns while the A tiles still arrive, and row tile i
+// waits only for its own data (ops_wait_a).
 struct Ops {
     u32x4 a[8];
     uint32_t q[2][3], sc[2];  // Q8_0, Q4_0
@@ -166,77 +190,98 @@ struct Ops {
     u32x4 hd[2];              // Q4_K
 };
 template <int RP>
-__device__ __forceinline__ void ops_read_q32(uint32_t a, uint32_t b, uint32_t s, Ops &o) {
+__device__ __forceinline__ void ops_read_q32(uint32_t b, uint32_t s, Ops &o) {
     asm volatile(
-        "ds_read_b32 %0, %16\n\t"
-        "ds_read_b32 %1, %16 offset:4\n\t"
-        "ds_read_b32 %2, %16 offset:8\n\t"
-        "ds_read_b32 %3, %17\n\t"
-        "ds_read_b32 %4, %16 offset:%19\n\t"
-        "ds_read_b32 %5, %16 offset:%20\n\t"
-        "ds_read_b32 %6, %16 offset:%21\n\t"
-        "ds_read_b32 %7, %17 offset:%19\n\t"
-        "ds_read_b128 %8, %18\n\t"
-        "ds_read_b128 %9, %18 offset:2048\n\t"
-        "ds_read_b128 %10, %18 offset:4096\n\t"
-        "ds_read_b128 %11, %18 offset:6144\n\t"
-        "ds_read_b128 %12, %18 offset:8192\n\t"
-        "ds_read_b128 %13, %18 offset:10240\n\t"
-        "ds_read_b128 %14, %18 offset:12288\n\t"
-        "ds_read_b128 %15, %18 offset:14336"
+        "ds_read_b32 %0, %8\n\t"
+        "ds_read_b32 %1, %8 offset:4\n\t"
+        "ds_read_b32 %2, %8 offset:8\n\t"
+        "ds_read_b32 %3, %9\n\t"
+        "ds_read_b32 %4, %8 offset:%10\n\t"
+        "ds_read_b32 %5, %8 offset:%11\n\t"
+        "ds_read_b32 %6, %8 offset:%12\n\t"
+        "ds_read_b32 %7, %9 offset:%10"
         : "=&v"(o.q[0][0]), "=&v"(o.q[0][1]), "=&v"(o.q[0][2]), "=&v"(o.sc[0]), "=&v"(o.q[1][0]),
-          "=&v"(o.q[1][1]), "=&v"(o.q[1][2]), "=&v"(o.sc[1]), "=&v"(o.a[0]), "=&v"(o.a[1]), "=&v"(o.a[2]),
-          "=&v"(o.a[3]), "=&v"(o.a[4]), "=&v"(o.a[5]), "=&v"(o.a[6]), "=&v"(o.a[7])
-        : "v"(b), "v"(s), "v"(a), "n"(RP), "n"(RP + 4), "n"(RP + 8)
+          "=&v"(o.q[1][1]), "=&v"(o.q[1][2]), "=&v"(o.sc[1])
+        : "v"(b), "v"(s), "n"(RP), "n"(RP + 4), "n"(RP + 8)
         : "memory");
 }
 template <int RP>
-__device__ __forceinline__ void ops_read_q4k(uint32_t a, uint32_t b, uint32_t s, Ops &o) {
+__device__ __forceinline__ void ops_read_q4k(uint32_t b, uint32_t s, Ops &o) {
     asm volatile(
-        "ds_read_b64 %0, %12\n\t"
-        "ds_read_b128 %1, %13\n\t"
-        "ds_read_b64 %2, %12 offset:%15\n\t"
-        "ds_read_b128 %3, %13 offset:%15\n\t"
-        "ds_read_b128 %4, %14\n\t"
-        "ds_read_b128 %5, %14 offset:2048\n\t"
-        "ds_read_b128 %6, %14 offset:4096\n\t"
-        "ds_read_b128 %7, %14 offset:6144\n\t"
-        "ds_read_b128 %8, %14 offset:8192\n\t"
-        "ds_read_b128 %9, %14 offset:10240\n\t"
-        "ds_read_b128 %10, %14 offset:12288\n\t"
-        "ds_read_b128 %11, %14 offset:14336"
-        : "=&v"(o.q2[0]), "=&v"(o.hd[0]), "=&v"(o.q2[1]), "=&v"(o.hd[1]), "=&v"(o.a[0]), "=&v"(o.a[1]),
-          "=&v"(o.a[2]), "=&v"(o.a[3]), "=&v"(o.a[4]), "=&v"(o.a[5]), "=&v"(o.a[6]), "=&v"(o.a[7])
-        : "v"(b), "v"(s), "v"(a), "n"(RP)
+        "ds_read_b64 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b64 %2, %4 offset:%6\n\t"
+        "ds_read_b128 %3, %5 offset:%6"
+        : "=&v"(o.q2[0]), "=&v"(o.hd[0]), "=&v"(o.q2[1]), "=&v"(o.hd[1])
+        : "v"(b), "v"(s), "n"(RP)
         : "memory");
 }
-// The raw dwords have arrived (8 A reads may still be outstanding).
+template <int I>
+__device__ __forceinline__ void ops_read_a(uint32_t a, Ops &o) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(o.a[I]) : "v"(a), "n"(2048 * I) : "memory");
+}
+// Row tiles 0 .. MT - 1, in order.
+template <int MT>
+__device__ __forceinline__ void ops_read_as(uint32_t a, Ops &o) {
+    ops_read_a<0>(a, o);
+    if constexpr (MT > 1) ops_read_a<1>(a, o);
+    if constexpr (MT > 2) {
+        ops_read_a<2>(a, o);
+        ops_read_a<3>(a, o);
+    }
+    if constexpr (MT > 4) {
+        ops_read_a<4>(a, o);
+        ops_read_a<5>(a, o);
+        ops_read_a<6>(a, o);
+        ops_read_a<7>(a, o);
+    }
+}
+// The raw dwords have arrived (the MT A reads may still be outstanding).
+template <int MT>
 __device__ __forceinline__ void ops_wait_raw(Ops &o) {
-    asm volatile("s_waitcnt lgkmcnt(8)"
+    asm volatile("s_waitcnt lgkmcnt(%12)"
                  : "+v"(o.q[0][0]), "+v"(o.q[0][1]), "+v"(o.q[0][2]), "+v"(o.sc[0]), "+v"(o.q[1][0]),
                    "+v"(o.q[1][1]), "+v"(o.q[1][2]), "+v"(o.sc[1]), "+v"(o.q2[0]), "+v"(o.q2[1]),
                    "+v"(o.hd[0]), "+v"(o.hd[1])
-                 :
+                 : "n"(MT)
                  : "memory");
 }
-// Row tile I has arrived (the 7 - I later ones may still be outstanding).
-template <int I>
+// Row tile I has arrived (the MT - 1 - I later ones may still be outstanding).
+template <int MT, int I>
 __device__ __forceinline__ void ops_wait_a(Ops &o) {
-    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(o.a[I]) : "n"(7 - I) : "memory");
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(o.a[I]) : "n"(MT - 1 - I) : "memory");
+}
+// ops_wait_a for row tile i (a constant after unrolling).
+template <int MT>
+__device__ __forceinline__ void ops_wait_row(int i, Ops &o) {
+    if (i == 0) ops_wait_a<MT, 0>(o);
+    if constexpr (MT > 1)
+        if (i == 1) ops_wait_a<MT, 1>(o);
+    if constexpr (MT > 2) {
+        if (i == 2) ops_wait_a<MT, 2>(o);
+        if (i == 3) ops_wait_a<MT, 3>(o);
+    }
+    if constexpr (MT > 4) {
+        if (i == 4) ops_wait_a<MT, 4>(o);
+        if (i == 5) ops_wait_a<MT, 5>(o);
+        if (i == 6) ops_wait_a<MT, 6>(o);
+        if (i == 7) ops_wait_a<MT, 7>(o);
+    }
 }
 
 }  // namespace
 
-// One 128 x 128 tile of Y (or of split `split`'s partial sum) per workgroup.
-template <int T>
+// One 16 MT x 128 tile of Y (or of split `split`'s partial sum) per workgroup.
+template <int T, int MT>
 __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__restrict__ W,
                                                             int64_t row_bytes,
                                                             const uint16_t *__restrict__ X,
                                                             float *__restrict__ Y, int M, int N,
                                                             int K, int S, float *__restrict__ part) {
-    using G = TileGeom<T>;
+    using G = TileGeom<T, MT>;
     using R = RawW<T>;
     constexpr int NS = G::kSlots;
+    constexpr int kTileM = G::kTileM, kXBytes = G::kXBytes;
     // The ring: X and raw W of NS stages; at the end the output staging.
     __shared__ __attribute__((aligned(16))) uint8_t ring[G::kRing];
 
@@ -273,7 +318,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
                                                   (uint32_t)((int64_t)nrows * row_bytes - w_split));
 
     // ---- loads of a stage (loader waves 8 and 9) ---------------------------
-    // X: loader l moves LDS chunks p = 64 (8 l + i) + lane (i < 8): row p / 8
+    // X: loader l moves LDS chunks p = 64 (MT l + i) + lane (i < MT): row p / 8
     // at swizzled position p % 8, holding the row's column chunk
     // position ^ ((row >> 1) & 7).  W: instruction j moves lane-chunks q =
     // 64 j + lane (row q / kChunks, part q % kChunks) to LDS offset 16 q;
@@ -284,10 +329,10 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
         uint8_t *const xs = ring + (ls % NS) * G::kSlot;
         uint8_t *const rs = xs + kXBytes;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int p = 64 * (8 * ldr + i) + lane;
+        for (int i = 0; i < MT; i++) {
+            const int p = 64 * (MT * ldr + i) + lane;
             const int r = p >> 3, kc = (p & 7) ^ ((r >> 1) & 7);
-            dma16(xr, xs + 1024 * (8 * ldr + i),
+            dma16(xr, xs + 1024 * (MT * ldr + i),
                   (uint32_t)r * (uint32_t)(2 * K) + 16u * (uint32_t)kc + 128u * (uint32_t)ls);
         }
 #pragma unroll
@@ -306,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
 
     // ---- a wave's operands -----------------------------------------------
     // Wave w: block kg = w / 4 of each stage, tile columns 32 nq .. 32 nq + 31
-    // (nq = w % 4) in two 16-column tiles, all 128 rows in eight 16-row tiles.
+    // (nq = w % 4) in two 16-column tiles, all 16 MT rows in MT 16-row tiles.
     // Lane: A row (and B column) lane & 15, k group lk = lane >> 4 (k 8 lk ..
     // 8 lk + 7 of the block).
     const int kg = wave >> 2, nq = wave & 3;
@@ -338,25 +383,26 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
     }
     const int nib = T == kQ4_0 ? 4 * (lk >> 1) : 4 * kg;  // nibble shift (Q4_0, Q4_K)
 
-    f32x4 acc[8][2];
+    f32x4 acc[MT][2];
 #pragma unroll
-    for (int a = 0; a < 8; a++)
+    for (int a = 0; a < MT; a++)
 #pragma unroll
         for (int b = 0; b < 2; b++) acc[a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
-    // Per stage: 16 MFMAs (8 row tiles x 2 column tiles; Q4_K: a third per
-    // row tile for the sums of x) and one FMA (Q4_K: two) per output.  The
-    // FMAs of row tile mt - 1 are interleaved with the MFMAs of row tile mt,
-    // so that no FMA waits for the MFMA it consumes.
+    // Per stage: 2 MT MFMAs (MT row tiles x 2 column tiles; Q4_K: one more
+    // per row tile for the sums of x) and one FMA (Q4_K: two) per output.
+    // The FMAs of each MFMA are issued two MFMAs later, so that no FMA waits
+    // for the MFMA it consumes.
     auto compute = [&](int ls) {
         const uint32_t so = (uint32_t)((ls % NS) * G::kSlot);
         Ops o;
         if constexpr (T == kQ4_K)
-            ops_read_q4k<16 * G::kPitch>(xa + so, wrow + so + qoff, wrow + so + soff, o);
+            ops_read_q4k<16 * G::kPitch>(wrow + so + qoff, wrow + so + soff, o);
         else
-            ops_read_q32<16 * G::kPitch>(xa + so, wrow + so + qoff, wrow + so + soff, o);
-        ops_wait_raw(o);
+            ops_read_q32<16 * G::kPitch>(wrow + so + qoff, wrow + so + soff, o);
+        ops_read_as<MT>(xa + so, o);
+        ops_wait_raw<MT>(o);
         bf16x8 B[2];
         float d[2], dm[2];
         // Column tile i's codes as bf16 (B operand) and its scale / min term.
@@ -376,23 +422,26 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
                 s8x4_bf16((w1 + 0x78787878u) ^ 0x80808080u, c[2], c[3]);
                 d[i] = half_bits_to_float_fast(o.sc[i] >> nsh);
             } else {
-                u8x4_bf16(opaque((o.q2[i].x >> nib) & 0x0F0F0F0Fu), c[0], c[1]);
-                u8x4_bf16(opaque((o.q2[i].y >> nib) & 0x0F0F0F0Fu), c[2], c[3]);
+                // B holds 128 + q; the 128 sum(x) it adds comes off with the
+                // min term: d (P - 128 sx) - dmin m sx = d P - (dmin m + 128 d) sx.
+                q4x4_bf16_128((o.q2[i].x >> nib) & 0x0F0F0F0Fu, c[0], c[1]);
+                q4x4_bf16_128((o.q2[i].y >> nib) & 0x0F0F0F0Fu, c[2], c[3]);
                 uint32_t scp, mnp;
                 q4k_pair_codes(o.hd[i].y, o.hd[i].z, o.hd[i].w, ls & 3, &scp, &mnp);
                 const uint32_t scj = (scp >> (8 * kg)) & 0xFFu, mj = (mnp >> (8 * kg)) & 0xFFu;
                 d[i] = half_bits_to_float_fast(o.hd[i].x & 0xFFFFu) * (float)scj;
-                dm[i] = mj == 0u ? 0.0f : half_bits_to_float_fast(o.hd[i].x >> 16) * (float)mj;
+                dm[i] = fmaf(128.0f, d[i], mj == 0u ? 0.0f : half_bits_to_float_fast(o.hd[i].x >> 16) * (float)mj);
             }
             B[i] = __builtin_bit_cast(bf16x8, u32x4{c[0], c[1], c[2], c[3]});
         };
-        // MFMA k = 0..15 is (row tile k % 8, column tile k / 8): column tile
-        // 1 is widened while column tile 0's first MFMAs run, and the FMAs of
-        // MFMA k - 2 are issued with MFMA k, so that none waits for its MFMA.
-        // Q4_K: the sums of x of row tile mt come with its column-0 MFMA.
-        f32x4 p[3], sx[8];
+        // MFMA k = 0 .. 2 MT - 1 is (row tile k % MT, column tile k / MT):
+        // column tile 1 is widened while column tile 0's first MFMAs run, and
+        // the FMAs of MFMA k - 2 are issued with MFMA k, so that none waits
+        // for its MFMA.  Q4_K: the sums of x of row tile mt come with its
+        // column-0 MFMA.
+        f32x4 p[3], sx[MT];
         auto fmas = [&](int k) {
-            const int mt = k & 7, nt = k >> 3;
+            const int mt = k % MT, nt = k / MT;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 acc[mt][nt][r] = fmaf(d[nt], p[k % 3][r], acc[mt][nt][r]);
@@ -401,20 +450,13 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
         };
         widen(0);
 #pragma unroll
-        for (int k = 0; k < 18; k++) {
+        for (int k = 0; k < 2 * MT + 2; k++) {
             __builtin_amdgcn_sched_barrier(0);
-            if (k < 16) {
-                const int mt = k & 7, nt = k >> 3;
-                if (k == 0) ops_wait_a<0>(o);
-                if (k == 1) ops_wait_a<1>(o);
-                if (k == 2) ops_wait_a<2>(o);
-                if (k == 3) ops_wait_a<3>(o);
-                if (k == 4) ops_wait_a<4>(o);
-                if (k == 5) ops_wait_a<5>(o);
-                if (k == 6) ops_wait_a<6>(o);
-                if (k == 7) ops_wait_a<7>(o);
+            if (k < 2 * MT) {
+                const int mt = k % MT, nt = k / MT;
+                if (k < MT) ops_wait_row<MT>(k, o);
                 const bf16x8 A = __builtin_bit_cast(bf16x8, o.a[mt]);
-                if (k == 2) widen(1);
+                if (k == (MT < 2 ? MT : 2)) widen(1);
                 if constexpr (G::kMins)
                     if (nt == 0) sx[mt] = mfma_bf16(A, ones);
                 p[k % 3] = mfma_bf16(A, B[nt]);
@@ -438,11 +480,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
         for (int s = 0; s < nst; s++) {
             // stages issued after s: min(nst - 1, s + NS - 2) - s
             const int later = nst - 1 - s < NS - 2 ? nst - 1 - s : NS - 2;
-            if (later >= 4) loader_barrier<G::kLoads * 4>();
-            else if (later == 3) loader_barrier<G::kLoads * 3>();
-            else if (later == 2) loader_barrier<G::kLoads * 2>();
-            else if (later == 1) loader_barrier<G::kLoads * 1>();
-            else loader_barrier<0>();
+            loader_barrier_n<G::kLoads, NS - 2>(later);
             if (s + NS - 1 < nst) issue(s + NS - 1);
         }
     } else {
@@ -451,26 +489,25 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
             compute(s);
         }
     }
-    static_assert(NS - 2 <= 4, "loader waits");
 
     // ---- epilogue ----------------------------------------------------------
     // Block 1's waves hand their tiles to block 0's waves through the ring
-    // (wave nq's quarter at 16 KiB nq); those add them (first-block sum +
+    // (wave nq's quarter at 2 MT KiB nq); those add them (first-block sum +
     // second-block sum) and write the tile row-major into the ring (row pitch
     // kStagePitch floats); then the compute waves store whole rows, 16 bytes
     // a lane.  Every wave (the loaders too) passes the same barriers.
     __syncthreads();
-    f32x4 *const hand = reinterpret_cast<f32x4 *>(ring + 16384 * nq);
+    f32x4 *const hand = reinterpret_cast<f32x4 *>(ring + 2048 * MT * nq);
     if (wave < 8 && kg == 1) {
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++)
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) hand[(mt * 2 + nt) * 64 + lane] = acc[mt][nt];
     }
     __syncthreads();
     if (wave < 8 && kg == 0) {
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++)
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) acc[mt][nt] += hand[(mt * 2 + nt) * 64 + lane];
     }
@@ -479,7 +516,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
     if (wave < 8 && kg == 0) {
         // D layout of a 16 x 16 tile: lane holds column lane & 15, rows 4 (lane >> 4) + r.
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++)
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
 #pragma unroll
@@ -534,8 +571,13 @@ __global__ __launch_bounds__(256) void gemm_tile_reduce_kernel(const float *__re
 
 namespace {
 
+// Row tiles per workgroup: the smallest of 1, 2, 4, 8 that covers M, so
+// that small M computes no padding rows.
+int tile_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+
 int tile_splits(int type_id, int M, int N, int K, size_t workspace_bytes) {
-    const int tiles = (M + kTileM - 1) / kTileM * ((N + kTileN - 1) / kTileN);
+    const int tm = 16 * tile_mt(M);
+    const int tiles = (M + tm - 1) / tm * ((N + kTileN - 1) / kTileN);
     const int nst = K / 64;
     // A split holds a whole number of four-stage rounds (and so of Q4_K
     // superblocks).
@@ -555,7 +597,7 @@ bool gemm_tile_supported(int type_id, int64_t row_bytes, int M, int N, int K, co
     if (((reinterpret_cast<uintptr_t>(w) | (uintptr_t)row_bytes) & 3u) != 0) return false;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(y) & 15u) != 0) return false;
     // 32-bit buffer offsets: a tile's rows of X and W
-    return (int64_t)kTileM * K * 2 < ((int64_t)1 << 31) && (int64_t)kTileN * row_bytes < ((int64_t)1 << 31);
+    return (int64_t)kTileMMax * K * 2 < ((int64_t)1 << 31) && (int64_t)kTileN * row_bytes < ((int64_t)1 << 31);
 }
 
 size_t gemm_tile_workspace_bytes(int type_id, int M, int N, int K) {
@@ -569,22 +611,39 @@ hipError_t launch_gemm_tile(int type_id, const uint8_t *w, int64_t row_bytes, co
     if (M <= 0) return hipSuccess;
     int S = tile_splits(type_id, M, N, K, workspace != nullptr ? workspace_bytes : 0);
     if (((int64_t)M * N) % 4 != 0 || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) S = 1;
-    const unsigned tiles = (unsigned)(((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN));
+    const int mt = tile_mt(M), tm = 16 * mt;
+    const unsigned tiles = (unsigned)(((M + tm - 1) / tm) * ((N + kTileN - 1) / kTileN));
     const dim3 grid(tiles * (unsigned)S), block(kThreads);
     float *part = S > 1 ? workspace : nullptr;
+#define GOLLEK_TILE_LAUNCH(TY)                                                                        \
+    do {                                                                                              \
+        if (mt == 1)                                                                                  \
+            hipLaunchKernelGGL((gemm_tile_kernel<TY, 1>), grid, block, 0, stream, w, row_bytes, x, y, M, N, \
+                               K, S, part);                                                           \
+        else if (mt == 2)                                                                             \
+            hipLaunchKernelGGL((gemm_tile_kernel<TY, 2>), grid, block, 0, stream, w, row_bytes, x, y, M, N, \
+                               K, S, part);                                                           \
+        else if (mt == 4)                                                                             \
+            hipLaunchKernelGGL((gemm_tile_kernel<TY, 4>), grid, block, 0, stream, w, row_bytes, x, y, M, N, \
+                               K, S, part);                                                           \
+        else                                                                                          \
+            hipLaunchKernelGGL((gemm_tile_kernel<TY, 8>), grid, block, 0, stream, w, row_bytes, x, y, M, N, \
+                               K, S, part);                                                           \
+    } while (0)
     switch (type_id) {
     case kQ8_0:
-        hipLaunchKernelGGL(gemm_tile_kernel<kQ8_0>, grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S, part);
+        GOLLEK_TILE_LAUNCH(kQ8_0);
         break;
     case kQ4_0:
-        hipLaunchKernelGGL(gemm_tile_kernel<kQ4_0>, grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S, part);
+        GOLLEK_TILE_LAUNCH(kQ4_0);
         break;
     case kQ4_K:
-        hipLaunchKernelGGL(gemm_tile_kernel<kQ4_K>, grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S, part);
+        GOLLEK_TILE_LAUNCH(kQ4_K);
         break;
     default:
         return hipErrorInvalidValue;
     }
+#undef GOLLEK_TILE_LAUNCH
     if (S > 1) {
         const int64_t mn = (int64_t)M * N;
         hipLaunchKernelGGL(gemm_tile_reduce_kernel, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0,

@@ -55,6 +55,15 @@ import java.util.WeakHashMap;
  * JavaNativeGgufBackend.java:157-180), and
  * the device handle lives until release(model).</p>
  *
+ * <p>A prepared layout is a second device copy of the tensor.  Like the
+ * reference's prepared caches (RT/GgufPreparedCachePolicy.java:29-42) the
+ * copies are admitted under a byte budget, gollek.hip.prepare.max_bytes
+ * (default: no limit; the tensor's whole size is charged when prepare is
+ * asked for).  When an upload finds the device full, every prepared copy is
+ * freed (the handles then read the GGUF bytes, with the same results),
+ * preparing stops for the rest of the process, and the upload is tried once
+ * more; a prepare that finds no memory only stops preparing.</p>
+ *
  * <p>Status codes map back to the exceptions the Java route throws
  * (RT/GgufMatVec.java:32-35, 65-71, 196-200; RT/GgufRowDot.java:77-82;
  * GC/core/GgmlType.java:70-81): NULL to NullPointerException, ARG to
@@ -75,6 +84,10 @@ final class GgufHipMatVec {
 
     /** Device handles per model and tensor (GGUFTensorInfo is a record over an array: identity keys). */
     private static final Map<GGUFModel, Map<GGUFTensorInfo, MemorySegment>> HANDLES = new WeakHashMap<>();
+    /** Handles holding a prepared copy, with the bytes charged for it (guarded by HANDLES). */
+    private static final Map<MemorySegment, Long> PREPARED = new IdentityHashMap<>();
+    private static long preparedBytes;
+    private static boolean preparingStopped;
 
     private GgufHipMatVec() {
     }
@@ -140,6 +153,14 @@ final class GgufHipMatVec {
         Map<GGUFTensorInfo, MemorySegment> handles;
         synchronized (HANDLES) {
             handles = HANDLES.remove(model);
+            if (handles != null) {
+                for (MemorySegment w : handles.values()) {
+                    Long charged = PREPARED.remove(w);
+                    if (charged != null) {
+                        preparedBytes -= charged.longValue();
+                    }
+                }
+            }
         }
         if (b == null || handles == null) {
             return;
@@ -161,16 +182,27 @@ final class GgufHipMatVec {
             try (Arena arena = Arena.ofConfined()) {
                 MemorySegment err = arena.allocate(ERR_LEN);
                 w = b.weightUpload(tensor.typeId(), bytes, rows, (long) columns, rowBytes, err, (long) ERR_LEN);
+                if (w.address() == 0L && b.lastStatus() == ERR_NOMEM && dropPreparedCopies(b, err)) {
+                    // Earlier tensors' prepared copies filled the device: their memory is back.
+                    w = b.weightUpload(tensor.typeId(), bytes, rows, (long) columns, rowBytes, err, (long) ERR_LEN);
+                }
                 if (w.address() == 0L) {
                     check(b.lastStatus(), err);
                     throw new IllegalStateException("gollek_hip_weight_upload returned no handle");
                 }
                 // The prepared mat-vec layout, built once like the reference's prepared
-                // matrices (gollek.gguf.java_native.auto_prepare); without device memory
-                // for it the handle keeps reading the GGUF bytes.
-                if (!"false".equals(System.getProperty("gollek.hip.prepare", "true"))) {
+                // matrices (gollek.gguf.java_native.auto_prepare) within the byte budget;
+                // without it the handle keeps reading the GGUF bytes.
+                long size = rows * rowBytes;
+                if (!preparingStopped && !"false".equals(System.getProperty("gollek.hip.prepare", "true"))
+                        && preparedBytes <= Long.getLong("gollek.hip.prepare.max_bytes", Long.MAX_VALUE) - size) {
                     int rc = b.weightPrepare(w, err, (long) ERR_LEN);
-                    if (rc != OK && rc != ERR_NOMEM) {
+                    if (rc == OK) {
+                        PREPARED.put(w, size);
+                        preparedBytes += size;
+                    } else if (rc == ERR_NOMEM) {
+                        preparingStopped = true;
+                    } else {
                         b.weightFree(w);
                         check(rc, err);
                     }
@@ -179,6 +211,20 @@ final class GgufHipMatVec {
             perModel.put(tensor, w);
             return w;
         }
+    }
+
+    /** Frees every prepared copy (caller holds HANDLES) and stops preparing; false when there was none. */
+    private static boolean dropPreparedCopies(Binding b, MemorySegment err) {
+        preparingStopped = true;
+        if (PREPARED.isEmpty()) {
+            return false;
+        }
+        for (MemorySegment w : PREPARED.keySet()) {
+            check(b.weightUnprepare(w, err, (long) ERR_LEN), err);
+        }
+        PREPARED.clear();
+        preparedBytes = 0L;
+        return true;
     }
 
     private static void check(int rc, MemorySegment err) {
@@ -206,6 +252,7 @@ final class GgufHipMatVec {
         private final MethodHandle weightUpload;
         private final MethodHandle weightFree;
         private final MethodHandle weightPrepare;
+        private final MethodHandle weightUnprepare;
         private final MethodHandle matvecRows;
         private final MethodHandle dotRow;
         private final MethodHandle dequantizeRows;
@@ -266,6 +313,9 @@ final class GgufHipMatVec {
             this.weightFree = downcall(linker, lookup, "gollek_hip_weight_free",
                     FunctionDescriptor.ofVoid(ValueLayout.ADDRESS), false);
             this.weightPrepare = downcall(linker, lookup, "gollek_hip_weight_prepare",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
+            this.weightUnprepare = downcall(linker, lookup, "gollek_hip_weight_unprepare",
                     FunctionDescriptor.of(ValueLayout.JAVA_INT,
                             ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
             // The float[] arguments are passed as heap segments: critical downcalls with heap access.
@@ -335,6 +385,14 @@ final class GgufHipMatVec {
         int weightPrepare(MemorySegment weight, MemorySegment err, long errLen) {
             try {
                 return (int) weightPrepare.invokeExact(weight, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int weightUnprepare(MemorySegment weight, MemorySegment err, long errLen) {
+            try {
+                return (int) weightUnprepare.invokeExact(weight, err, errLen);
             } catch (Throwable t) {
                 throw propagate(t);
             }

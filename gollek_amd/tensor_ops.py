@@ -138,6 +138,13 @@ class GgufTensor:
         err = _native.ErrBuf()
         check(_native.load().gollek_hip_weight_prepare(self.handle(), err.buf, err.size), err)
 
+    def unprepare(self) -> None:
+        """Free the prepared layout (gollek_hip_weight_unprepare); full
+        mat-vecs read the GGUF bytes again (the prepared-cache clear)."""
+        if self._handle is not None:
+            err = _native.ErrBuf()
+            check(_native.load().gollek_hip_weight_unprepare(self._handle, err.buf, err.size), err)
+
     def close(self) -> None:
         if self._handle is not None:
             _native.load().gollek_hip_weight_free(self._handle)
@@ -350,6 +357,11 @@ class DeviceWeight:
         """Build the handle's prepared mat-vec layout (gollek_hip_weight_prepare)."""
         err = _native.ErrBuf()
         check(_native.load().gollek_hip_weight_prepare(self.handle, err.buf, err.size), err)
+
+    def unprepare(self) -> None:
+        """Free the prepared layout (gollek_hip_weight_unprepare)."""
+        err = _native.ErrBuf()
+        check(_native.load().gollek_hip_weight_unprepare(self.handle, err.buf, err.size), err)
 
     def close(self) -> None:
         if self.handle:

@@ -102,8 +102,12 @@ gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *de
  * Q8_0, Q4_0 and Q5_K with K up to 16384 and at most 64 / 32 / 64 / 48 rows
  * per CU; measured 7.8 us against 8.8 us for Q4_K 14336 x 4096).  Later full mat-vecs
  * (row_count == rows) on the handle read it; every other entry point keeps
- * reading the GGUF bytes.  The layout follows the device's CU count and
- * gemv_variant at the time of the call; a no-op (OK) for other shapes.
+ * reading the GGUF bytes.  The layout follows the device's CU count at the
+ * time of the call; a no-op (OK) for other shapes.  The copy is a snapshot:
+ * a caller that rewrites a borrowed buffer (gollek_hip_weight_wrap_device)
+ * after this call must call gollek_hip_weight_unprepare, or this again,
+ * before the next full mat-vec.  The copy costs the matrix's bytes a second
+ * time in device memory.
  * Call it before the handle's device mat-vecs start, or with none in
  * flight: a call that finds a copy for another partition frees it, and the
  * _device entry points read the copy on the caller's stream without the
@@ -113,6 +117,14 @@ gollek_hip_weight *gollek_hip_weight_wrap_device(int32_t type_id, const void *de
  * .java:157-180), which likewise keeps a prepared copy beside the raw
  * bytes.  Freed with the handle.  Device memory exhausted -> NOMEM. */
 int32_t gollek_hip_weight_prepare(gollek_hip_weight *weight, char *err, size_t err_len);
+
+/* Free the prepared copy of gollek_hip_weight_prepare, if any (OK when there
+ * is none); later full mat-vecs read the GGUF bytes again, with identical
+ * results.  Gives a caller the device memory back while keeping the handle,
+ * as the reference's per-family prepared-cache clear keeps the raw tensor
+ * (RT/GgufPreparedMatrixStore.java:129-131).  Same rule as prepare: no
+ * _device call on the handle may be in flight. */
+int32_t gollek_hip_weight_unprepare(gollek_hip_weight *weight, char *err, size_t err_len);
 
 /* Release a handle (device memory it owns, its stream and staging buffers).
  * Replaces clearPreparedMatrixCaches on backend close
@@ -150,18 +162,20 @@ int32_t gollek_hip_matvec_rows(gollek_hip_weight *weight, const float *x, int64_
 
 /* Y[m, n] = sum_k X[m, k] W[n, k] (Y = X W^T, the Linear convention of
  * runner/safetensor/gollek-safetensor-core/src/main/java/tech/kayys/gollek/
- * safetensor/core/tensor/AccelOps.java:370-376) for a Q8_0 weight, X given
- * as m x cols bf16 bit patterns (row-major), Y m x rows fp32.  Small-M prefill
- * and batched decode.  The reference has no GGUF GEMM: it runs m independent
- * RT/GgufTensorOps.matVecRows calls (RT/GgufTensorOps.java:666-674), which
- * this replaces.  x_len < m * cols or y_len < m * rows -> ARG; a weight type
- * other than Q8_0 -> UNSUPPORTED. */
+ * safetensor/core/tensor/AccelOps.java:370-376) for a Q8_0, Q4_0 or Q4_K
+ * weight, X given as m x cols bf16 bit patterns (row-major), Y m x rows fp32.
+ * Small-M prefill and batched decode.  The reference has no GGUF GEMM: it
+ * runs m independent RT/GgufTensorOps.matVecRows calls
+ * (RT/GgufTensorOps.java:666-674), which this replaces.  x_len < m * cols or
+ * y_len < m * rows -> ARG; a weight type other than Q8_0, Q4_0 and Q4_K ->
+ * UNSUPPORTED. */
 int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t x_len,
                              int64_t m, float *y, int64_t y_len, char *err, size_t err_len);
 
-/* Grouped MoE expert FFN over Q4_K gate / up and Q4_K or Q6_K down expert
- * weights (Q4_K_M files store some layers' ffn_down_exps as Q6_K), stacked
- * as GGUF stores them:
+/* Grouped MoE expert FFN over expert weights of any type this library takes
+ * (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K; gate, up and down may differ, as in Q4_K_M
+ * files whose ffn_down_exps are Q6_K in some layers), stacked as GGUF stores
+ * them:
  * gate and up have n_experts * inter rows of `hidden` columns, down has
  * n_experts * hidden rows of `inter` columns.  For each token t (x row-major
  * tokens x hidden) and route j < top_k (ids / weights row-major tokens x
@@ -171,10 +185,9 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, 
  * route) expert loop of runner/safetensor/gollek-safetensor-engine/src/main/
  * java/tech/kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:
  * 217-240 with :461-472 (swigluFfn: .../engine/forward/
- * DirectForwardFfnService.java:40-61), reading each used expert once.  Other
- * weight types, hidden / inter above 4096, or Q6_K down experts beyond
- * hidden 4096 (past 2048: an even multiple of 256) / inter 1024 / 256
- * experts / top_k 64 / 2048 routes -> UNSUPPORTED. */
+ * DirectForwardFfnService.java:40-61), reading each used expert once.
+ * Other weight types -> UNSUPPORTED; gate rows not a multiple of n_experts,
+ * shapes that disagree, or tokens * top_k above 2^24 -> ARG. */
 int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
                                gollek_hip_weight *down, int64_t n_experts, const float *x,
                                int64_t tokens, const int32_t *ids, const float *weights,
@@ -196,22 +209,24 @@ int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *weight, int64_t row
 int32_t gollek_hip_matvec_device(gollek_hip_weight *weight, const float *x, float *y,
                                  int64_t row_count, void *stream, char *err, size_t err_len);
 
-/* Shapes whose output tiles leave CUs idle (m = 33..256 for 4096 rows) are
- * split over K into partial tiles held in a workspace of the handle,
- * allocated at the first such call (at most 8 MiB on 256 CUs) and freed with
- * the handle; splitting calls on one handle share it and must not overlap (calls
- * on different handles may).  A y that is not 16-byte aligned runs unsplit. */
+/* Shapes whose output tiles leave CUs idle (few 128 x 128 tiles for the
+ * chip) are split over K into partial tiles held in a workspace of the
+ * handle, allocated at the first such call (below 16 MiB on 256 CUs) and
+ * freed with the handle; splitting calls on one handle share it and must not
+ * overlap (calls on different handles may).  A y that is not 16-byte aligned
+ * runs unsplit. */
 int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t m,
                                     float *y, void *stream, char *err, size_t err_len);
 
 /* gollek_hip_gemm_bf16_device without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops).  The split-K partial tiles
- * go to a static per-GPU scratch of 8 MiB (held from library load until the
- * process ends; enough for every m on a 256-CU MI355X) instead of the
- * handle's lazily allocated workspace.  All calls on one GPU share that
- * scratch, so calls that overlap on a GPU race; shapes needing more than
- * 8 MiB -> ARG.  Same checks and results as gollek_hip_gemm_bf16_device. */
+ * go to a static per-GPU scratch of 16 MiB (held from library load until the
+ * process ends; enough for every shape on a 256-CU MI355X) instead of the
+ * handle's lazily allocated workspace; a shape whose splits would need more
+ * is split less, down to none.  All calls on one GPU share that scratch, so
+ * calls that overlap on a GPU race.  Same checks and results as
+ * gollek_hip_gemm_bf16_device. */
 int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *weight, const uint16_t *x_bf16,
                                             int64_t m, float *y, void *stream, char *err,
                                             size_t err_len);

@@ -85,7 +85,8 @@ def _gemm_case(type_id, rows, cols, m, seed):
 @pytest.mark.parametrize("rows,cols,m", [(128, 256, 33), (192, 4096, 300), (80, 512, 129), (4096, 256, 257),
                                           (1000, 1024, 64), (256, 2048, 1024), (64, 4096, 40)])
 def test_gemm_tile_kernel_shapes(type_id, rows, cols, m):
-    # The 128 x 128 tile kernel: K from one four-stage round (256) up, a
+    # The tile kernel (16 MT x 128 tiles: MT = 8 past M = 64, 4 for M = 33
+    # .. 64): K from one four-stage round (256) up, a
     # partial last M tile (rows past M read zeros) and N tile (rows past N),
     # one to many tiles, grids that are and are not a multiple of 8, and the
     # K splits the CU count allows (none for K = 256, up to 8).
@@ -93,6 +94,19 @@ def test_gemm_tile_kernel_shapes(type_id, rows, cols, m):
     y, ref = _gemm_case(type_id, rows, cols, m, seed=rows + 3 * cols + m + type_id)
     err = o.rel_err(y, ref)
     print(f"[gpu] gemm tile type={type_id} rel_err={err:.3e}", flush=True)
+    assert err <= GEMM_TOL
+
+
+@pytest.mark.parametrize("type_id", TYPES)
+@pytest.mark.parametrize("rows,cols,m", [(100, 512, 5), (1000, 1024, 16), (64, 256, 1), (200, 2048, 32),
+                                          (520, 4096, 17), (3000, 4096, 48), (14336, 4096, 8)])
+def test_gemm_tile_kernel_small_m(type_id, rows, cols, m):
+    # Tiles of 16, 32 and 64 rows of X for M up to 16, 32 and 64 (Q8_0 with
+    # 16-row multiples of N and M <= 32 takes the skinny kernel instead).
+    print(f"[gpu] gemm small-m type={type_id} rows={rows} cols={cols} m={m}", flush=True)
+    y, ref = _gemm_case(type_id, rows, cols, m, seed=rows + 5 * cols + m + type_id)
+    err = o.rel_err(y, ref)
+    print(f"[gpu] gemm small-m type={type_id} rel_err={err:.3e}", flush=True)
     assert err <= GEMM_TOL
 
 

@@ -492,6 +492,59 @@ def test_prepared_layout_matches_gguf_bytes(type_id, rows, cols):
     dw.close()
 
 
+def test_unprepare_returns_to_the_gguf_bytes():
+    # prepare() snapshots a borrowed buffer: after the caller rewrites it, a
+    # full mat-vec still reads the old copy until unprepare(), and then
+    # equals a never-prepared handle on the new bytes.  Repeated unprepare
+    # calls and unprepare without a copy are no-ops.
+    import torch
+    rows, cols = 14336, 4096
+    print(f"[gpu] unprepare Q4_K {rows}x{cols}", flush=True)
+    old = syn.matrix(syn.Q4_K, rows, cols, seed=61)
+    new = syn.matrix(syn.Q4_K, rows, cols, seed=62)
+    x_dev = torch.from_numpy(syn.activation(cols, seed=63)).cuda()
+    y_dev = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    w_dev = torch.from_numpy(old.reshape(-1)).cuda()
+
+    def run(dw):
+        y_dev.fill_(-7.0)
+        dw.matvec(x_dev.data_ptr(), y_dev.data_ptr(), rows, stream)
+        torch.cuda.synchronize()
+        return y_dev.cpu().numpy().copy()
+
+    dw = ops.DeviceWeight(syn.Q4_K, w_dev.data_ptr(), rows, cols)
+    dw.unprepare()  # nothing to free
+    y_old = run(dw)
+    dw.prepare()
+    assert np.array_equal(run(dw), y_old)
+    w_dev.copy_(torch.from_numpy(new.reshape(-1)))
+    torch.cuda.synchronize()
+    assert np.array_equal(run(dw), y_old)  # the snapshot
+    dw.unprepare()
+    dw.unprepare()
+    y_new = run(dw)
+    fresh = ops.DeviceWeight(syn.Q4_K, w_dev.data_ptr(), rows, cols)
+    assert np.array_equal(y_new, run(fresh))
+    assert not np.array_equal(y_new, y_old)
+    dw.prepare()  # a new snapshot of the new bytes
+    assert np.array_equal(run(dw), y_new)
+    fresh.close()
+    dw.close()
+
+    t = _tensor(syn.Q4_K, new, cols)
+    t.unprepare()  # no handle yet: nothing to do
+    x = x_dev.cpu().numpy()
+    y0 = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y0)
+    t.prepare()
+    t.unprepare()
+    y1 = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y1)
+    assert np.array_equal(y0, y1) and np.array_equal(y0, y_new)
+    t.close()
+
+
 # ---- Q5_K / Q6_K -----------------------------------------------------------
 
 K56_SHAPES = [(syn.Q5_K, 1, 256), (syn.Q5_K, 7, 768), (syn.Q5_K, 4096, 4096), (syn.Q5_K, 33, 16384),

@@ -92,6 +92,7 @@ WRAPPERS = {  # typed wrapper -> the symbol whose handle it invokes
     "weightUpload": "gollek_hip_weight_upload",
     "weightFree": "gollek_hip_weight_free",
     "weightPrepare": "gollek_hip_weight_prepare",
+    "weightUnprepare": "gollek_hip_weight_unprepare",
     "matvecRows": "gollek_hip_matvec_rows",
     "dotRow": "gollek_hip_dot_row",
     "dequantizeRows": "gollek_hip_dequantize_rows",
