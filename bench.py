@@ -222,18 +222,20 @@ def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int, type_id: in
 
 
 def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048, 768, 16),
-                 copies: int = 3, routed: bool = True):
-    """Grouped expert FFN over Q4_K experts, shape (experts, top_k, hidden,
-    inter, tokens); with `routed`, also the routed block (router -> top-k ->
-    the same FFN).  Weights rotate over `copies` whole layers."""
+                 copies: int = 3, routed: bool = True, types=None):
+    """Grouped expert FFN, shape (experts, top_k, hidden, inter, tokens),
+    expert types (gate, up, down) (default Q4_K); with `routed`, also the
+    routed block (router -> top-k -> the same FFN).  Weights rotate over
+    `copies` whole layers."""
     import numpy as np
 
     from gollek_amd import synthetic as syn
     from gollek_amd import tensor_ops as ops
     E, k, H, I, T = shape
-    gate = syn.q4_k_matrix(E * I, H, seed)
-    up = syn.q4_k_matrix(E * I, H, seed + 1)
-    down = syn.q4_k_matrix(E * H, I, seed + 2)
+    tg, tu, td = types or (syn.Q4_K, syn.Q4_K, syn.Q4_K)
+    gate = syn.matrix(tg, E * I, H, seed)
+    up = syn.matrix(tu, E * I, H, seed + 1)
+    down = syn.matrix(td, E * H, I, seed + 2)
     ids, w = syn.moe_routing(T, E, k, seed + 3)
     x = syn.activation(T * H, seed + 4).reshape(T, H)
     # At 128 x 2048 x 768, three copies of the whole layer (3 x 340 MB): a copy
@@ -242,9 +244,9 @@ def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048,
     layers = []
     for _ in range(copies):
         bufs = [torch.from_numpy(a.reshape(-1)).cuda() for a in (gate, up, down)]
-        handles = (ops.DeviceWeight(syn.Q4_K, bufs[0].data_ptr(), E * I, H),
-                   ops.DeviceWeight(syn.Q4_K, bufs[1].data_ptr(), E * I, H),
-                   ops.DeviceWeight(syn.Q4_K, bufs[2].data_ptr(), E * H, I))
+        handles = (ops.DeviceWeight(tg, bufs[0].data_ptr(), E * I, H),
+                   ops.DeviceWeight(tu, bufs[1].data_ptr(), E * I, H),
+                   ops.DeviceWeight(td, bufs[2].data_ptr(), E * H, I))
         layers.append((bufs, handles))
     ws_bytes = ops.moe_workspace_bytes(T, k, H, I, E)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
@@ -260,7 +262,7 @@ def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048,
 
     ms, n = graph_time(torch, launch, copies, steps, warmup)
     used = len(np.unique(ids))
-    bytes_used = used * (gate.shape[1] * I + up.shape[1] * I + down.shape[1] * H) + 2 * T * H * 4
+    bytes_used = used * (gate.size // E + up.size // E + down.size // E) + 2 * T * H * 4
     res = {"ms_per_step": ms, "steps": n, "experts_touched": int(used),
            "algo_bytes": int(bytes_used), "algo_gbs": bytes_used / (ms * 1e-3) / 1e9,
            "hbm_frac": bytes_used / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -286,7 +288,7 @@ def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048,
 
     bms, bn = graph_time(torch, launch_block, copies, steps, warmup)
     bused = len(np.unique(bids.cpu().numpy()))
-    bbytes = bused * (gate.shape[1] * I + up.shape[1] * I + down.shape[1] * H) + 2 * T * H * 4 \
+    bbytes = bused * (gate.size // E + up.size // E + down.size // E) + 2 * T * H * 4 \
         + T * E * 4
     res["routed_block"] = {"ms_per_step": bms, "steps": bn, "experts_touched": int(bused),
                            "scoring": "sigmoid", "algo_bytes": int(bbytes),
@@ -652,6 +654,15 @@ def main() -> int:
             extra["moe_q4_k_e128_top8_t16_h4096"] = moe_workload(
                 torch, args.steps, args.warmup, seed=13, shape=(128, 8, 4096, 1536, 16), copies=2,
                 routed=False)[0]
+        # Other expert types at the same shape: Q4_K gate / up with Q6_K down
+        # (a Q4_K_M file's layers), and all-Q8_0 / all-Q4_0 experts.
+        for name, types in (("moe_q4_k_q6_k_down_e128_top8_t16", (syn.Q4_K, syn.Q4_K, syn.Q6_K)),
+                            ("moe_q8_0_e128_top8_t16", (syn.Q8_0, syn.Q8_0, syn.Q8_0)),
+                            ("moe_q4_0_e128_top8_t16", (syn.Q4_0, syn.Q4_0, syn.Q4_0))):
+            if _has_symbol("gollek_hip_moe_grouped_device") and want(name):
+                log(f"extra {name}")
+                extra[name] = moe_workload(torch, args.steps, args.warmup, seed=11, routed=False,
+                                           types=types)[0]
         if _has_symbol("gollek_hip_gguf_upload") and want("gguf_upload_q4_k_4096x14336"):
             log("extra gguf upload")
             extra["gguf_upload_q4_k_4096x14336"] = gguf_upload_workload(host, 14336, 4096)

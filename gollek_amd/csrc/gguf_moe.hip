@@ -318,6 +318,198 @@ __global__ __launch_bounds__(256) void moe_generic_expert_kernel(
     }
 }
 
+// Q8_0 / Q4_0 expert rows against the vectors of up to four routes of the
+// expert at a time.  The routes' vectors are staged in LDS, 36 floats per
+// 32-element block: the block's 32 values, then (Q4_0) their sum, which
+// takes the codes' offset of 8 out as -8 sum(x); the padding also puts the
+// blocks that neighbouring lanes read on distinct banks.  LPR lanes per row
+// (64 / LPR rows of a wave at a time), lane s of a row taking blocks s,
+// s + LPR, ... in chunks of KPL blocks whose bytes are loaded together (dword
+// loads through a buffer descriptor over the expert's rows, realigned by the
+// block's offset within a dword).  Each block's codes are widened once and
+// contracted with every staged route in fp32: d * sum(q x) per block, as the
+// reference's block dot.  GATED: the expert's gate and up rows r,
+// h = silu(gate . x) * (up . x).
+template <int T>
+struct Q32Raw {
+    static constexpr int kDw = T == kQ8_0 ? 9 : 5;  // dwords covering a block from its offset & ~3
+    uint32_t w[kDw];
+};
+
+template <int T>
+__device__ __forceinline__ void q32_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, Q32Raw<T> &r) {
+    const uint32_t base = off & ~3u;
+#pragma unroll
+    for (int i = 0; i < Q32Raw<T>::kDw; i++)
+        r.w[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, base + 4u * i, 0, kStreamLoad);
+}
+
+// The block's codes as floats (Q4_0: the nibble 0..15, without the -8) and d;
+// sh = the block's byte offset within its first dword (0 or 2: blocks start
+// at even bytes).
+template <int T>
+__device__ __forceinline__ void q32_codes(const Q32Raw<T> &r, uint32_t sh, float (&q)[32], float &d) {
+    d = half_bits_to_float_fast(sh ? r.w[0] >> 16 : r.w[0] & 0xFFFFu);
+    constexpr int kQd = T == kQ8_0 ? 8 : 4;  // code dwords
+    uint32_t c[kQd];
+#pragma unroll
+    for (int i = 0; i < kQd; i++) c[i] = sh ? r.w[i + 1] : __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
+    if constexpr (T == kQ8_0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[4 * i + k] = sbyte_f(c[i], k);
+    } else {
+        // element j < 16: low nibble of code byte j; j >= 16: high nibble of byte j - 16
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                q[4 * i + k] = byte_f(c[i] & 0x0F0F0F0Fu, k);
+                q[16 + 4 * i + k] = byte_f((c[i] >> 4) & 0x0F0F0F0Fu, k);
+            }
+    }
+}
+
+constexpr int kQ32Group = 4;
+
+template <int T, bool GATED, int LPR>
+__global__ __launch_bounds__(256) void moe_q32_expert_kernel(
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, int64_t row_bytes, int cols,
+    int rows_per_expert, int rows_per_block, const float *__restrict__ vec, int64_t vec_stride, int by_pair,
+    int top_k, const int32_t *__restrict__ meta, int E, int P, int group, float *__restrict__ out,
+    int64_t out_stride) {
+    extern __shared__ float xs[];  // group x nb x 36 floats
+    constexpr int kBB = T == kQ8_0 ? 34 : 18;
+    constexpr int KPL = (T == kQ8_0 && GATED) ? 2 : 4;  // blocks a lane loads together
+    constexpr int RPW = 64 / LPR;                         // rows of a wave at a time
+    const int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
+    const int32_t *used = pairs + P;
+    if ((int)blockIdx.y >= used[E]) return;
+    const int e = used[blockIdx.y];
+    const int cnt = counts[e], p0 = offsets[e];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rsub = lane / LPR;
+    const int nb = cols / 32, c4 = cols / 4;
+    const int r_lo = blockIdx.x * rows_per_block;
+    const int r_hi = min(rows_per_expert, r_lo + rows_per_block);
+    const int64_t ebytes = (int64_t)rows_per_expert * row_bytes;
+    const __amdgpu_buffer_rsrc_t rs0 = wave_buffer(w0 + (int64_t)e * ebytes, (uint32_t)ebytes);
+    const __amdgpu_buffer_rsrc_t rs1 = wave_buffer((GATED ? w1 : w0) + (int64_t)e * ebytes, (uint32_t)ebytes);
+    for (int g0 = 0; g0 < cnt; g0 += group) {
+        const int gn = min(group, cnt - g0);
+        __syncthreads();  // the previous group's vectors are no longer read
+        for (int i = threadIdx.x; i < gn * c4; i += 256) {
+            const int q = i / c4, j = 4 * (i - q * c4);
+            const int p = pairs[p0 + g0 + q];
+            const float4 v = *reinterpret_cast<const float4 *>(vec + (int64_t)(by_pair ? p : p / top_k) * vec_stride + j);
+            *reinterpret_cast<float4 *>(xs + (q * nb + (j >> 5)) * 36 + (j & 31)) = v;
+        }
+        if constexpr (T == kQ4_0) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < gn * nb; i += 256) {
+                const float *xb = xs + i * 36;
+                float t = 0.0f;
+                for (int k = 0; k < 32; k++) t += xb[k];
+                xs[i * 36 + 32] = t;
+            }
+        }
+        __syncthreads();
+        for (int r0 = r_lo + wave * RPW; r0 < r_hi; r0 += 4 * RPW) {
+            const int r = r0 + rsub;
+            const bool live = r < r_hi;
+            const uint32_t row_off = live ? (uint32_t)((int64_t)r * row_bytes) : 0u;
+            float a[kQ32Group], u[kQ32Group];
+#pragma unroll
+            for (int q = 0; q < kQ32Group; q++) a[q] = u[q] = 0.0f;
+            for (int b0 = 0; b0 < nb; b0 += KPL * LPR) {
+                Q32Raw<T> raw0[KPL], raw1[KPL];
+#pragma unroll
+                for (int k = 0; k < KPL; k++) {
+                    const int b = b0 + sub + LPR * k;
+                    if (live && b < nb) {
+                        q32_load<T>(rs0, row_off + (uint32_t)(b * kBB), raw0[k]);
+                        if constexpr (GATED) q32_load<T>(rs1, row_off + (uint32_t)(b * kBB), raw1[k]);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < KPL; k++) {
+                    const int b = b0 + sub + LPR * k;
+                    if (!(live && b < nb)) continue;
+                    const uint32_t sh = (row_off + (uint32_t)(b * kBB)) & 3u;
+                    float cq[32], d0, cu[32], d1 = 0.0f;
+                    q32_codes<T>(raw0[k], sh, cq, d0);
+                    if constexpr (GATED) q32_codes<T>(raw1[k], sh, cu, d1);
+#pragma unroll
+                    for (int q = 0; q < kQ32Group; q++) {
+                        if (q < gn) {
+                            const float4 *xb = reinterpret_cast<const float4 *>(xs + (q * nb + b) * 36);
+                            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                            for (int i = 0; i < 8; i++) {
+                                const float4 xv = xb[i];
+                                s0 = fmaf(cq[4 * i], xv.x, s0);
+                                s0 = fmaf(cq[4 * i + 1], xv.y, s0);
+                                s0 = fmaf(cq[4 * i + 2], xv.z, s0);
+                                s0 = fmaf(cq[4 * i + 3], xv.w, s0);
+                                if constexpr (GATED) {
+                                    s1 = fmaf(cu[4 * i], xv.x, s1);
+                                    s1 = fmaf(cu[4 * i + 1], xv.y, s1);
+                                    s1 = fmaf(cu[4 * i + 2], xv.z, s1);
+                                    s1 = fmaf(cu[4 * i + 3], xv.w, s1);
+                                }
+                            }
+                            if constexpr (T == kQ4_0) {
+                                const float xsum = xs[(q * nb + b) * 36 + 32];
+                                s0 = fmaf(-8.0f, xsum, s0);
+                                if constexpr (GATED) s1 = fmaf(-8.0f, xsum, s1);
+                            }
+                            a[q] = fmaf(d0, s0, a[q]);
+                            if constexpr (GATED) u[q] = fmaf(d1, s1, u[q]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kQ32Group; q++) {
+                if (q < gn) {
+                    float v = group_sum<LPR>(a[q]);
+                    if constexpr (GATED) {
+                        const float uu = group_sum<LPR>(u[q]);
+                        v = v / (1.0f + expf(-v)) * uu;  // silu(gate) * up
+                    }
+                    if (sub == 0 && live) out[(int64_t)pairs[p0 + g0 + q] * out_stride + r] = v;
+                }
+            }
+        }
+    }
+}
+
+// Lanes per row for rows of nb blocks: about four blocks per lane, 8 .. 64.
+inline int q32_lanes_per_row(int nb) {
+    int l = 8;
+    while (l < 64 && 4 * l < nb) l *= 2;
+    return l;
+}
+
+template <int T, bool GATED>
+hipError_t launch_q32_expert(dim3 grid, size_t lds, hipStream_t stream, const uint8_t *w0, const uint8_t *w1,
+                             int64_t row_bytes, int cols, int rows_per_expert, int rows_per_block,
+                             const float *vec, int64_t vec_stride, int by_pair, int top_k, const int32_t *meta,
+                             int E, int P, int group, float *out, int64_t out_stride) {
+    const int lpr = q32_lanes_per_row(cols / 32);
+#define GOLLEK_Q32_LAUNCH(L)                                                                              \
+    hipLaunchKernelGGL((moe_q32_expert_kernel<T, GATED, L>), grid, dim3(256), lds, stream, w0, w1, row_bytes, \
+                       cols, rows_per_expert, rows_per_block, vec, vec_stride, by_pair, top_k, meta, E, P,  \
+                       group, out, out_stride)
+    if (lpr == 8) GOLLEK_Q32_LAUNCH(8);
+    else if (lpr == 16) GOLLEK_Q32_LAUNCH(16);
+    else if (lpr == 32) GOLLEK_Q32_LAUNCH(32);
+    else GOLLEK_Q32_LAUNCH(64);
+#undef GOLLEK_Q32_LAUNCH
+    return hipGetLastError();
+}
+
 namespace {
 
 template <bool GATED>
@@ -376,15 +568,46 @@ hipError_t launch_moe_generic(int gate_type, int up_type, int down_type, const u
     float *h = reinterpret_cast<float *>(ws + L.h);
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
     constexpr int kRows = 64;
-    hipLaunchKernelGGL(moe_generic_expert_kernel<true>, dim3((I + kRows - 1) / kRows, E), dim3(256), 0, stream,
-                       gate_type, up_type, gate, up, gate_row_bytes, up_row_bytes, H, I, kRows, x, (int64_t)H, 0,
-                       top_k, meta, E, P, h, (int64_t)I);
-    err = hipGetLastError();
+    // Q8_0 / Q4_0 passes: the route vectors of a group in LDS (at most 96 KiB).
+    auto q32_group = [](int cols) {
+        const int g = (96 * 1024) / ((cols / 32) * 144);
+        return g < kQ32Group ? g : kQ32Group;
+    };
+    const bool x_aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    const int g_gu = q32_group(H), g_dn = q32_group(I);
+    if (gate_type == up_type && (gate_type == kQ8_0 || gate_type == kQ4_0) && x_aligned && g_gu > 0 &&
+        gate_row_bytes == up_row_bytes && (int64_t)I * gate_row_bytes < ((int64_t)1 << 31)) {
+        const size_t lds = (size_t)g_gu * (H / 32) * 144;
+        const dim3 grid((I + kRows - 1) / kRows, E);
+        if (gate_type == kQ8_0)
+            err = launch_q32_expert<kQ8_0, true>(grid, lds, stream, gate, up, gate_row_bytes, H, I, kRows, x, (int64_t)H, 0,
+                                           top_k, meta, E, P, g_gu, h, (int64_t)I);
+        else
+            err = launch_q32_expert<kQ4_0, true>(grid, lds, stream, gate, up, gate_row_bytes, H, I, kRows, x, (int64_t)H, 0,
+                                           top_k, meta, E, P, g_gu, h, (int64_t)I);
+    } else {
+        hipLaunchKernelGGL(moe_generic_expert_kernel<true>, dim3((I + kRows - 1) / kRows, E), dim3(256), 0, stream,
+                           gate_type, up_type, gate, up, gate_row_bytes, up_row_bytes, H, I, kRows, x, (int64_t)H, 0,
+                           top_k, meta, E, P, h, (int64_t)I);
+        err = hipGetLastError();
+    }
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(moe_generic_expert_kernel<false>, dim3((H + kRows - 1) / kRows, E), dim3(256), 0, stream,
-                       down_type, down_type, down, down, down_row_bytes, down_row_bytes, I, H, kRows, h,
-                       (int64_t)I, 1, top_k, meta, E, P, ypair, (int64_t)H);
-    err = hipGetLastError();
+    if ((down_type == kQ8_0 || down_type == kQ4_0) && g_dn > 0 &&
+        (int64_t)H * down_row_bytes < ((int64_t)1 << 31)) {
+        const size_t lds = (size_t)g_dn * (I / 32) * 144;
+        const dim3 grid((H + kRows - 1) / kRows, E);
+        if (down_type == kQ8_0)
+            err = launch_q32_expert<kQ8_0, false>(grid, lds, stream, down, down, down_row_bytes, I, H, kRows, h, (int64_t)I,
+                                            1, top_k, meta, E, P, g_dn, ypair, (int64_t)H);
+        else
+            err = launch_q32_expert<kQ4_0, false>(grid, lds, stream, down, down, down_row_bytes, I, H, kRows, h, (int64_t)I,
+                                            1, top_k, meta, E, P, g_dn, ypair, (int64_t)H);
+    } else {
+        hipLaunchKernelGGL(moe_generic_expert_kernel<false>, dim3((H + kRows - 1) / kRows, E), dim3(256), 0, stream,
+                           down_type, down_type, down, down, down_row_bytes, down_row_bytes, I, H, kRows, h,
+                           (int64_t)I, 1, top_k, meta, E, P, ypair, (int64_t)H);
+        err = hipGetLastError();
+    }
     if (err != hipSuccess) return err;
     return launch_moe_combine(ids, wts, ypair, T, top_k, H, E, out, stream);
 }

@@ -80,12 +80,16 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
         t.close()
 
 
-# Expert types and shapes the matrix-core passes do not take run on the
-# generic passes: Q8_0 / Q4_0 / Q5_K / Q6_K gate and up, Q8_0 / Q4_0 / Q5_K
-# down, and Q6_K down beyond the token-major down pass (inter above 1024,
-# hidden past 2048 with an odd superblock count, more than 2048 routes).
+# Expert types and shapes the matrix-core passes do not take: Q8_0 / Q4_0
+# gate and up or down on the fp32 row kernels (rows of 3 to 448 blocks, 8 to
+# 64 lanes per row, route groups limited by LDS, experts with many routes),
+# Q5_K / Q6_K gate and up and Q5_K down on the generic passes, and Q6_K down
+# beyond the token-major down pass (inter above 1024, hidden past 2048 with
+# an odd superblock count, more than 2048 routes).
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q8_0, syn.Q8_0, 128, 2048, 768, 16, 8), (syn.Q4_0, syn.Q4_0, 128, 2048, 768, 16, 8),
+    (syn.Q4_0, syn.Q4_0, 4, 512, 14336, 12, 2), (syn.Q8_0, syn.Q8_0, 2, 4096, 1024, 20, 2),
+    (syn.Q4_0, syn.Q8_0, 3, 2048, 2048, 33, 3),
     (syn.Q8_0, syn.Q6_K, 16, 1024, 512, 9, 4), (syn.Q4_0, syn.Q5_K, 16, 512, 256, 7, 2),
     (syn.Q4_K, syn.Q5_K, 8, 512, 256, 5, 2), (syn.Q5_K, syn.Q4_K, 8, 512, 256, 5, 2),
     (syn.Q6_K, syn.Q6_K, 8, 512, 256, 5, 2), (syn.Q4_K, syn.Q8_0, 8, 512, 256, 5, 2),
