@@ -132,6 +132,12 @@ hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uin
 // Whether the matrix-core passes can take Q6_K down experts of this shape
 // (the token-major down pass; x must also be 16-byte aligned).
 bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k);
+// All-Q4_0 experts on the matrix-core passes (hidden up to 2048, hidden and
+// inter multiples of 256; x 16-byte aligned).
+bool moe_q40_mfma_supported(int E, int H, int I, int P, const float *x);
+hipError_t launch_moe_q40_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E, int H, int I,
+                               const float *x, const int32_t *ids, const float *wts, int T, int top_k, float *out,
+                               uint8_t *ws, hipStream_t stream);
 
 // Pieces of the MoE pipeline shared by its two implementations (gguf_moe.hip,
 // gguf_moe_mfma.hip): routing (meta layout of moe_layout; tiles0 / tiles1 =

@@ -624,6 +624,10 @@ hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *
     if (aligned && q4k_gu && tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, T * top_k, x) &&
         (down_type == kQ4_K || (down_type == kQ6_K && moe_q6k_down_supported(E, H, I, T, top_k))))
         return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream, down_type);
+    // All Q4_0 (hidden up to 2048): the matrix-core passes with Q4_0 rows.
+    if (aligned && gate_type == kQ4_0 && up_type == kQ4_0 && down_type == kQ4_0 && tuning().moe_variant != 1 &&
+        moe_q40_mfma_supported(E, H, I, T * top_k, x))
+        return launch_moe_q40_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream);
     // All Q4_K up to hidden / inter 4096: the v_dot4 passes.
     if (aligned && q4k_gu && down_type == kQ4_K && H % kQK == 0 && I % kQK == 0 && H <= 4096 && I <= 4096)
         return launch_moe_q4k_dot4(gate, up, down, gate_row_bytes, down_row_bytes, E, H, I, x, ids, wts, T,

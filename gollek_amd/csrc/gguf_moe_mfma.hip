@@ -215,13 +215,14 @@ constexpr int kRecDwords = 14;
 // tile's two halves are consecutive items, each wave keeps both halves' x
 // operands, and the first half's gate / up row sums wait in LDS (hsave)
 // for the second's, so h = silu(gate) * up is formed once per row.
-template <int MODE, bool REC, int HV = 1>
+template <int MODE, bool REC, int HV = 1, int WT = kQ4_K>
 __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, MoeTileGeom G,
     const float *__restrict__ vec, int top_k, const int32_t *__restrict__ ids,
     const float *__restrict__ wts, int E, int P, float *__restrict__ out) {
     static_assert(MODE == 0 || !REC, "records are pass 0's output");
     static_assert(HV == 1 || (HV == 2 && MODE == 0), "K-halves in pass 0 only");
+    static_assert(WT == kQ4_K || (WT == kQ4_0 && HV == 1), "Q4_0 rows in one half");
     __shared__ __attribute__((aligned(16))) uint8_t ring[kMoSlots * kMoSlot + 1024];  // + sink
     // digit build; HV = 2: + the (half, route) x sums and scales from 768
     __shared__ __attribute__((aligned(16))) uint8_t scratch[kMoWaves][HV == 2 ? 1088 : 1024];
@@ -634,7 +635,82 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kMoDmaPerWave * (kMoSlots - 2)) : "memory");
         if (have_prev) reduce_prev(prev, i - 1);
         issue(slot == 0 ? kMoSlots - 1 : slot - 1, i + kMoSlots - 1);
-        if (active) {
+        if (active && WT == kQ4_0) {
+            // Q4_0: a 144-byte piece is eight 18-byte blocks; chunk c (64
+            // columns) is blocks 2c and 2c + 1.  Lane group g takes elements
+            // 8 g .. 8 g + 7 of each: quant bytes 8 (g & 1) .. + 7 of the
+            // block, nibble g >> 1 (elements 16 .. 31 are the high nibbles),
+            // so B = {block 2c's 8 codes, block 2c + 1's 8 codes} as bytes
+            // 0..15 against A's {elements 64c + 8g .., 64c + 32 + 8g ..}.
+            // Output half h (= g & 1) sums block 2c + h; its d is read with
+            // the codes.  value = sum_c d_(2c+h) (scale S_c - 8 sum x), the
+            // reference's d * sum((q - 8) x) per block.
+            const uint32_t off = (uint32_t)slot * kMoSlot;
+            const uint32_t pbase = a_h0 + off;            // row n's piece
+            const uint32_t qb = pbase + 8u * (uint32_t)h;  // + quant offset 8 (g & 1)
+            const uint32_t db = pbase + 16u * (uint32_t)h; // d of block 2c + h at + 36 c (half h)
+            uint32_t w[4][3], v[4][2], dd[4];
+            asm volatile(
+                "ds_read_b32 %0, %24\n\t"
+                "ds_read_b32 %1, %24 offset:4\n\t"
+                "ds_read_b32 %2, %24 offset:8\n\t"
+                "ds_read_b32 %3, %24 offset:20\n\t"
+                "ds_read_b32 %4, %24 offset:24\n\t"
+                "ds_read_b32 %5, %25\n\t"
+                "ds_read_b32 %6, %24 offset:36\n\t"
+                "ds_read_b32 %7, %24 offset:40\n\t"
+                "ds_read_b32 %8, %24 offset:44\n\t"
+                "ds_read_b32 %9, %24 offset:56\n\t"
+                "ds_read_b32 %10, %24 offset:60\n\t"
+                "ds_read_b32 %11, %25 offset:36\n\t"
+                "ds_read_b32 %12, %24 offset:72\n\t"
+                "ds_read_b32 %13, %24 offset:76\n\t"
+                "ds_read_b32 %14, %24 offset:80\n\t"
+                "ds_read_b32 %15, %24 offset:92\n\t"
+                "ds_read_b32 %16, %24 offset:96\n\t"
+                "ds_read_b32 %17, %25 offset:72\n\t"
+                "ds_read_b32 %18, %24 offset:108\n\t"
+                "ds_read_b32 %19, %24 offset:112\n\t"
+                "ds_read_b32 %20, %24 offset:116\n\t"
+                "ds_read_b32 %21, %24 offset:128\n\t"
+                "ds_read_b32 %22, %24 offset:132\n\t"
+                "ds_read_b32 %23, %25 offset:108\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(w[0][0]), "=&v"(w[0][1]), "=&v"(w[0][2]), "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(dd[0]),
+                  "=&v"(w[1][0]), "=&v"(w[1][1]), "=&v"(w[1][2]), "=&v"(v[1][0]), "=&v"(v[1][1]), "=&v"(dd[1]),
+                  "=&v"(w[2][0]), "=&v"(w[2][1]), "=&v"(w[2][2]), "=&v"(v[2][0]), "=&v"(v[2][1]), "=&v"(dd[2]),
+                  "=&v"(w[3][0]), "=&v"(w[3][1]), "=&v"(w[3][2]), "=&v"(v[3][0]), "=&v"(v[3][1]), "=&v"(dd[3])
+                : "v"(qb), "v"(db)
+                : "memory");
+            const uint32_t nib = 4u * (uint32_t)tq;  // g >> 1
+            i32x4 B[4];
+            float dq[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                // block 2c's codes start 2 bytes into the first dword
+                const uint32_t b0 = __builtin_amdgcn_alignbyte(w[c][1], w[c][0], 2);
+                const uint32_t b1 = __builtin_amdgcn_alignbyte(w[c][2], w[c][1], 2);
+                B[c] = i32x4{(int)((b0 >> nib) & 0x0F0F0F0Fu), (int)((b1 >> nib) & 0x0F0F0F0Fu),
+                             (int)((v[c][0] >> nib) & 0x0F0F0F0Fu), (int)((v[c][1] >> nib) & 0x0F0F0F0Fu)};
+                dq[c] = half_bits_to_float_fast(h ? dd[c] >> 16 : dd[c] & 0xFFFFu);
+            }
+            const int npairs = (cur.ntok + 1) >> 1;
+#pragma unroll
+            for (int pp = 0; pp < 2; pp++) {
+                if (pp >= npairs) break;  // uniform
+                i32x4 D[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[pp][c], B[c], zero4, 0, 0, 0);
+                float val = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int S = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
+                    val = fmaf(dq[c], fmaf(xs[pp], (float)S, -8.0f * xs4[pp][c]), val);
+                }
+                const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(val), 0x401F));
+                if (h == 0) part[i & 1][2 * pp + tq][wv][n] = val + other;
+            }
+        } else if (active) {
             u32x4 hv;
             uint2 q[4];
             const uint32_t off = (uint32_t)slot * kMoSlot;
@@ -785,7 +861,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 if (h == 0) part[i & 1][2 * pp + tq][wv][n] = v + other;
             }
             }
-        }
+                }
         prev = cur;
         have_prev = true;
         slot = slot == kMoSlots - 1 ? 0 : slot + 1;
@@ -1371,6 +1447,11 @@ bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x) {
     return true;
 }
 
+bool moe_q40_mfma_supported(int E, int H, int I, int P, const float *x) {
+    // gate / up rows in one half (hidden up to 2048)
+    return H <= 8 * kQK && moe_q4k_mfma_supported(E, H, I, P, x);
+}
+
 bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k) {
     MoeDownGeom g;
     int waves = 0;
@@ -1437,6 +1518,27 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
     hipLaunchKernelGGL((moe_expert_tile_kernel<1, false>), dim3(grid), dim3(kMoThreads), 0, stream, down,
                        (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_moe_combine(ids, wts, ypair, T, top_k, H, E, out, stream);
+}
+
+// All-Q4_0 experts: gate/up (fp32 h), the expert-major down pass and the
+// combine, the Q4_K kernels' passes with Q4_0's contraction.  The caller has
+// checked moe_q40_mfma_supported.
+hipError_t launch_moe_q40_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E, int H, int I,
+                               const float *x, const int32_t *ids, const float *wts, int T, int top_k, float *out,
+                               uint8_t *ws, hipStream_t stream) {
+    const MoeLayout L = moe_layout(T, top_k, H, I, E);
+    const int P = T * top_k;
+    const MoeTileGeom g0 = make_geom(0, E, H, I), g1 = make_geom(1, E, H, I);
+    const unsigned grid = (unsigned)device_cus();
+    float *hbuf = reinterpret_cast<float *>(ws + L.h);
+    float *ypair = reinterpret_cast<float *>(ws + L.ypair);
+    hipLaunchKernelGGL((moe_expert_tile_kernel<0, false, 1, kQ4_0>), dim3(grid), dim3(kMoThreads), 0, stream, gate,
+                       up, g0, x, top_k, ids, wts, E, P, hbuf);
+    hipLaunchKernelGGL((moe_expert_tile_kernel<1, false, 1, kQ4_0>), dim3(grid), dim3(kMoThreads), 0, stream, down,
+                       (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_moe_combine(ids, wts, ypair, T, top_k, H, E, out, stream);
 }

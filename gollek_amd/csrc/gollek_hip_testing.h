@@ -13,7 +13,8 @@
  *                   matrix-core kernel; 4 = Q8_0 / Q4_0 on the buffer->LDS
  *                   ring kernels and Q5_K / Q6_K on the fp32 kernel.
  *   "moe_variant":  0 = automatic; 1 = all-Q4_K experts on the v_dot4 passes
- *                   instead of the matrix-core passes.
+ *                   and all-Q4_0 experts on the fp32 row kernels instead of
+ *                   the matrix-core passes.
  * Unknown keys -> GOLLEK_HIP_ERR_ARG.
  */
 #ifndef GOLLEK_HIP_TESTING_H

@@ -80,6 +80,8 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
         t.close()
 
 
+# All-Q4_0 experts up to hidden 2048 take the matrix-core passes with Q4_0
+# rows (odd and even superblock counts, inter up to 4096, many routes).
 # Expert types and shapes the matrix-core passes do not take: Q8_0 / Q4_0
 # gate and up or down on the fp32 row kernels (rows of 3 to 448 blocks, 8 to
 # 64 lanes per row, route groups limited by LDS, experts with many routes),
@@ -89,7 +91,8 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q8_0, syn.Q8_0, 128, 2048, 768, 16, 8), (syn.Q4_0, syn.Q4_0, 128, 2048, 768, 16, 8),
     (syn.Q4_0, syn.Q4_0, 4, 512, 14336, 12, 2), (syn.Q8_0, syn.Q8_0, 2, 4096, 1024, 20, 2),
-    (syn.Q4_0, syn.Q8_0, 3, 2048, 2048, 33, 3),
+    (syn.Q4_0, syn.Q8_0, 3, 2048, 2048, 33, 3), (syn.Q4_0, syn.Q4_0, 16, 1280, 512, 9, 4),
+    (syn.Q4_0, syn.Q4_0, 8, 256, 4096, 5, 2), (syn.Q4_0, syn.Q4_0, 32, 512, 256, 300, 2),
     (syn.Q8_0, syn.Q6_K, 16, 1024, 512, 9, 4), (syn.Q4_0, syn.Q5_K, 16, 512, 256, 7, 2),
     (syn.Q4_K, syn.Q5_K, 8, 512, 256, 5, 2), (syn.Q5_K, syn.Q4_K, 8, 512, 256, 5, 2),
     (syn.Q6_K, syn.Q6_K, 8, 512, 256, 5, 2), (syn.Q4_K, syn.Q8_0, 8, 512, 256, 5, 2),
@@ -115,6 +118,24 @@ def moe_variant():
         ops.set_option("moe_variant", v)
     yield set_variant
     ops.set_option("moe_variant", 0)
+
+
+def test_moe_q4_0_matrix_core_equals_row_kernels(moe_variant):
+    # All-Q4_0 experts: the matrix-core passes (22-bit x digits) against the
+    # fp32 row kernels (moe_variant 1), both against the oracle.
+    E, H, I, T, k = 32, 2048, 768, 16, 8
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=21, down_type=syn.Q4_0, gate_type=syn.Q4_0)
+    ids, w = syn.moe_routing(T, E, k, seed=22)
+    x = syn.activation(T * H, seed=23).reshape(T, H)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=syn.Q4_0, gate_type=syn.Q4_0)
+    out_mc = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    moe_variant(1)
+    out_rows = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    for out in (out_mc, out_rows):
+        assert o.rel_err(out, ref) <= MOE_TOL
+    assert o.rel_err(out_mc, out_rows) <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
 
 
 def test_moe_v_dot4_variant_parity(moe_variant):
