@@ -4,10 +4,11 @@ The no-allocation entry point runs the same kernels with its split-K
 partials in the library's static per-GPU scratch instead of the handle's
 workspace, so its output must equal the allocating entry point's bit for
 bit, and both must be within the GEMM bar (rel_err <= 1e-2) of the fp64
-oracle.  Three calls in a row on one handle, each with fewer rows of X than
-the one before (all three split over K at 4096 weight rows, so all use the
-scratch -- m = 512 with two splits, the others with more -- and none reads
-an earlier call's partials).
+oracle.  Calls in a row on one handle, each with fewer rows of X than the
+one before, all split over K so all use the scratch, and none may read an
+earlier call's partials: Q8_0 at 4096 rows (m = 512 with two splits, the
+others with more), Q4_K at 14336 rows (m = 128 in 128-row tiles, m = 16 in
+16-row tiles) and Q4_0 at 4096 rows (m = 300, then 20 in 32-row tiles).
 """
 import ctypes
 
@@ -24,19 +25,21 @@ pytestmark = pytest.mark.gpu
 GEMM_TOL = 1e-2
 
 
-def test_noalloc_gemm_matches_allocating_entry_point():
+@pytest.mark.parametrize("type_id,rows,cols,ms", [(syn.Q8_0, 4096, 4096, (512, 200, 48)),
+                                                  (syn.Q4_K, 14336, 4096, (128, 16)),
+                                                  (syn.Q4_0, 4096, 4096, (300, 20))])
+def test_noalloc_gemm_matches_allocating_entry_point(type_id, rows, cols, ms):
     import torch
 
     ops.init(0)
     lib = _native.load()
-    rows = cols = 4096
-    data = syn.q8_0_matrix(rows, cols, seed=404)
+    data = syn.matrix(type_id, rows, cols, seed=404)
     w_dev = torch.from_numpy(data.reshape(-1)).cuda()
-    dw = ops.DeviceWeight(syn.Q8_0, w_dev.data_ptr(), rows, cols)
+    dw = ops.DeviceWeight(type_id, w_dev.data_ptr(), rows, cols)
     stream = torch.cuda.current_stream().cuda_stream
     err = _native.ErrBuf()
-    for m in (512, 200, 48):
-        print(f"[gpu] noalloc gemm m={m} n={rows} k={cols}", flush=True)
+    for m in ms:
+        print(f"[gpu] noalloc gemm type={type_id} m={m} n={rows} k={cols}", flush=True)
         xb = syn.activation_bf16(m, cols, seed=m)
         x = torch.from_numpy(xb.view("int16")).cuda()
         y_ref = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
@@ -49,7 +52,7 @@ def test_noalloc_gemm_matches_allocating_entry_point():
         assert rc == 0, err.text
         got, ref = y.cpu().numpy(), y_ref.cpu().numpy()
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), m
-        exp = o.gemm_reference(syn.Q8_0, data, cols, xb)
+        exp = o.gemm_reference(type_id, data, cols, xb)
         assert o.rel_err(got.reshape(-1), exp.reshape(-1)) <= GEMM_TOL, m
     dw.close()
 
