@@ -336,12 +336,14 @@ struct Q32Raw {
     uint32_t w[kDw];
 };
 
+// Default cache policy, as for the K-quant rows below: a block's dword loads
+// revisit its lines (streaming hints: 162 against 119 us for a Q8_0 layer).
 template <int T>
 __device__ __forceinline__ void q32_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, Q32Raw<T> &r) {
     const uint32_t base = off & ~3u;
 #pragma unroll
     for (int i = 0; i < Q32Raw<T>::kDw; i++)
-        r.w[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, base + 4u * i, 0, kStreamLoad);
+        r.w[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, base + 4u * i, 0, 0);
 }
 
 // The block's codes as floats (Q4_0: the nibble 0..15, without the -8) and d;
@@ -485,6 +487,234 @@ __global__ __launch_bounds__(256) void moe_q32_expert_kernel(
     }
 }
 
+// K-quant (Q4_K, Q5_K, Q6_K) expert rows, in the form of the Q8_0 / Q4_0
+// row kernel above: up to four routes' vectors staged in LDS at 36 floats
+// per 32 elements, each group's two 16-element sums in its padding (the
+// min terms and Q6_K's -32 take sums of x); LPR lanes per row, lane s taking
+// superblocks s, s + LPR, ...; routes one at a time; a superblock's bytes
+// (gate's and up's together) are loaded as dwords through a buffer
+// descriptor (Q6_K's 210-byte superblocks realigned when they start 2 bytes
+// into a dword) and its codes widened as they are contracted in fp32, with the per-sub-block scales and mins of the
+// reference's dequantizers (RT/GgufKBlockDequantizer.java:31-170, 319-432)
+// folded into the dot as in gguf_block_dot.hpp.
+// Default cache policy: each 128-byte line is read by several of a lane's
+// loads in turn (a superblock spans lines, a line several superblocks'
+// pieces), and a streaming hint had each load fetch its line again (227
+// against 76 us for the loads of a Q5_K / Q6_K layer).
+__device__ __forceinline__ uint32_t kq_ld(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+}
+
+// sum over 4 codes (bytes of q4, values 0..63) times 4 staged x values
+__device__ __forceinline__ float kq_dot4(uint32_t q4, float4 xv, float s) {
+    s = fmaf(byte_f(q4, 0), xv.x, s);
+    s = fmaf(byte_f(q4, 1), xv.y, s);
+    s = fmaf(byte_f(q4, 2), xv.z, s);
+    return fmaf(byte_f(q4, 3), xv.w, s);
+}
+
+// A superblock's dwords from its offset & ~3 (Q6_K's 210-byte superblocks
+// start 0 or 2 bytes into a dword; the others are 16-byte aligned).
+template <int T>
+struct KqRaw {
+    static constexpr int kDw = T == kQ4_K ? 36 : T == kQ5_K ? 44 : 54;
+    uint32_t w[kDw];
+};
+
+template <int T>
+__device__ __forceinline__ void kq_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, KqRaw<T> &r) {
+    const uint32_t base = off & ~3u;
+#pragma unroll
+    for (int i = 0; i < KqRaw<T>::kDw; i++) r.w[i] = kq_ld(rs, base + 4u * i);
+}
+
+// One superblock (its dwords in r, realigned in place for Q6_K; sh = its
+// offset within the first dword) against one route's staged x (xg: its 8
+// groups of 36 floats).  The 64- (32-) element chunks run in a loop that is
+// not unrolled, each picking its code dwords from the registers with one
+// select, so only one chunk's x is held at a time.
+template <int T>
+__device__ __forceinline__ float kq_dot(KqRaw<T> &r, uint32_t sh, const float *xg) {
+    if constexpr (T == kQ6_K) {
+#pragma unroll
+        for (int k = 0; k < 53; k++) r.w[k] = __builtin_amdgcn_alignbyte(r.w[k + 1], r.w[k], sh);
+        const float d = half_bits_to_float_fast(r.w[52] & 0xFFFFu);
+        float total = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll 1
+            for (int j = 0; j < 4; j++) {
+                // elements 128 h + 32 j + i: ql byte 64 h + 32 (j & 1) + i, nibble j >> 1;
+                // qh byte 128 + 32 h + i, bits 2 j
+                const int grp = 4 * h + j;
+                const float4 *xb = reinterpret_cast<const float4 *>(xg + 36 * grp);
+                const uint32_t nsh = 4u * (uint32_t)(j >> 1), hsh = 2u * (uint32_t)j;
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t ql = (j & 1) ? r.w[16 * h + 8 + k] : r.w[16 * h + k];
+                    const uint32_t qh = r.w[32 + 8 * h + k];
+                    const uint32_t q4 = ((ql >> nsh) & 0x0F0F0F0Fu) | (((qh >> hsh) & 0x03030303u) << 4);
+                    if (k < 4) s0 = kq_dot4(q4, xb[k], s0);
+                    else s1 = kq_dot4(q4, xb[k], s1);
+                }
+                // scale bytes 2 grp, 2 grp + 1 (dword 48 + 2 h + (j >> 1))
+                const uint32_t scd = (j >> 1) ? r.w[48 + 2 * h + 1] : r.w[48 + 2 * h];
+                const float sc0 = sbyte_f(scd, 2 * (j & 1)), sc1 = sbyte_f(scd, 2 * (j & 1) + 1);
+                s0 = fmaf(-32.0f, xg[36 * grp + 32], s0);
+                s1 = fmaf(-32.0f, xg[36 * grp + 33], s1);
+                total = fmaf(d * sc0, s0, total);
+                total = fmaf(d * sc1, s1, total);
+            }
+        }
+        return total;
+    } else {
+        (void)sh;
+        constexpr bool q5 = T == kQ5_K;
+        constexpr int qs = q5 ? 12 : 4;  // first quant dword
+        const float d = half_bits_to_float_fast(r.w[0] & 0xFFFFu);
+        const float dmin = half_bits_to_float_fast(r.w[0] >> 16);
+        float total = 0.0f;
+#pragma unroll
+        for (int c2 = 0; c2 < 2; c2++) {
+#pragma unroll 1
+            for (int c1 = 0; c1 < 2; c1++) {
+                const int c = 2 * c2 + c1;  // sub-blocks 2c, 2c + 1
+                uint32_t scp, mnp;
+                q4k_pair_codes(r.w[1], r.w[2], r.w[3], c, &scp, &mnp);
+                const float4 *x1 = reinterpret_cast<const float4 *>(xg + 36 * (2 * c));
+                const float4 *x2 = reinterpret_cast<const float4 *>(xg + 36 * (2 * c + 1));
+                float a1 = 0.0f, a2 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t qd = c1 ? r.w[qs + 8 * (2 * c2 + 1) + k] : r.w[qs + 8 * (2 * c2) + k];
+                    uint32_t lo = qd & 0x0F0F0F0Fu, hi = (qd >> 4) & 0x0F0F0F0Fu;
+                    if constexpr (q5) {
+                        const uint32_t qh = r.w[4 + k];  // qh bytes 4 k .. 4 k + 3
+                        lo |= ((qh >> (2 * c)) & 0x01010101u) << 4;
+                        hi |= ((qh >> (2 * c + 1)) & 0x01010101u) << 4;
+                    }
+                    a1 = kq_dot4(lo, x1[k], a1);
+                    a2 = kq_dot4(hi, x2[k], a2);
+                }
+                const float sc1 = (float)(scp & 0xFFu), sc2 = (float)((scp >> 8) & 0xFFu);
+                const uint32_t mc1 = mnp & 0xFFu, mc2 = (mnp >> 8) & 0xFFu;
+                const float m1 = mc1 ? dmin * (float)mc1 : 0.0f, m2 = mc2 ? dmin * (float)mc2 : 0.0f;
+                const float v1 = xg[36 * (2 * c) + 32] + xg[36 * (2 * c) + 33];
+                const float v2 = xg[36 * (2 * c + 1) + 32] + xg[36 * (2 * c + 1) + 33];
+                total += d * sc1 * a1 + d * sc2 * a2 - (m1 * v1 + m2 * v2);
+            }
+        }
+        return total;
+    }
+}
+
+template <int T, bool GATED, int LPR>
+__global__ __launch_bounds__(256) void moe_kq_expert_kernel(
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, int64_t row_bytes, int cols,
+    int rows_per_expert, int rows_per_block, const float *__restrict__ vec, int64_t vec_stride, int by_pair,
+    int top_k, const int32_t *__restrict__ meta, int E, int P, int group, float *__restrict__ out,
+    int64_t out_stride) {
+    // group x (cols / 32 groups of 36 floats, plus 4 after every 8 groups:
+    // superblocks 292 floats apart, so the lanes of a row, one superblock
+    // each, read distinct banks)
+    extern __shared__ float xs[];
+    constexpr int kSB = T == kQ4_K ? 144 : T == kQ5_K ? 176 : 210;
+    constexpr int RPW = 64 / LPR;  // rows of a wave at a time
+    const int32_t *counts = meta, *offsets = meta + E, *pairs = meta + 2 * E + 1;
+    const int32_t *used = pairs + P;
+    if ((int)blockIdx.y >= used[E]) return;
+    const int e = used[blockIdx.y];
+    const int cnt = counts[e], p0 = offsets[e];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rsub = lane / LPR;
+    const int ng = cols / 32, nsb = cols / 256, c4 = cols / 4;
+    const int rstride = ng * 36 + nsb * 4;  // floats per route
+    auto goff = [&](int g) { return g * 36 + (g >> 3) * 4; };
+    const int r_lo = blockIdx.x * rows_per_block;
+    const int r_hi = min(rows_per_expert, r_lo + rows_per_block);
+    const int64_t ebytes = (int64_t)rows_per_expert * row_bytes;
+    const __amdgpu_buffer_rsrc_t rs0 = wave_buffer(w0 + (int64_t)e * ebytes, (uint32_t)ebytes);
+    const __amdgpu_buffer_rsrc_t rs1 = wave_buffer((GATED ? w1 : w0) + (int64_t)e * ebytes, (uint32_t)ebytes);
+    for (int g0 = 0; g0 < cnt; g0 += group) {
+        const int gn = min(group, cnt - g0);
+        __syncthreads();  // the previous group's vectors are no longer read
+        for (int i = threadIdx.x; i < gn * c4; i += 256) {
+            const int q = i / c4, j = 4 * (i - q * c4);
+            const int p = pairs[p0 + g0 + q];
+            const float4 v = *reinterpret_cast<const float4 *>(vec + (int64_t)(by_pair ? p : p / top_k) * vec_stride + j);
+            *reinterpret_cast<float4 *>(xs + q * rstride + goff(j >> 5) + (j & 31)) = v;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < 2 * gn * ng; i += 256) {  // the 16-element sums
+            const int qg = i >> 1, q = qg / ng, g = qg - q * ng;
+            float *xb = xs + q * rstride + goff(g);
+            float t = 0.0f;
+            for (int k = 0; k < 16; k++) t += xb[16 * (i & 1) + k];
+            xb[32 + (i & 1)] = t;
+        }
+        __syncthreads();
+        for (int r0 = r_lo + wave * RPW; r0 < r_hi; r0 += 4 * RPW) {
+            const int r = r0 + rsub;
+            const bool live = r < r_hi;
+            const uint32_t row_off = live ? (uint32_t)((int64_t)r * row_bytes) : 0u;
+            // One route at a time, gate then up (later routes re-read the
+            // rows from the caches).
+#pragma unroll 1
+            for (int q = 0; q < gn; q++) {
+                float a = 0.0f, u = 0.0f;
+#pragma unroll 1
+                for (int b = sub; b < nsb; b += LPR) {
+                    if (!live) break;
+                    const uint32_t off = row_off + (uint32_t)(b * kSB);
+                    const float *xg = xs + q * rstride + 292 * b;
+                    // gate and up dwords in flight together, then each contracted
+                    KqRaw<T> raw0, raw1;
+                    kq_load<T>(rs0, off, raw0);
+                    if constexpr (GATED) kq_load<T>(rs1, off, raw1);
+                    a += kq_dot<T>(raw0, off & 3u, xg);
+                    if constexpr (GATED) u += kq_dot<T>(raw1, off & 3u, xg);
+                }
+                float v = group_sum<LPR>(a);
+                if constexpr (GATED) {
+                    const float uu = group_sum<LPR>(u);
+                    v = v / (1.0f + expf(-v)) * uu;  // silu(gate) * up
+                }
+                if (sub == 0 && live) out[(int64_t)pairs[p0 + g0 + q] * out_stride + r] = v;
+            }
+        }
+    }
+}
+
+// Lanes per row for rows of nsb superblocks: one superblock per lane (up
+// to 64 lanes), so a row's loads are one round trip.
+inline int kq_lanes_per_row(int nsb) {
+    int l = 1;
+    while (l < 64 && l < nsb) l *= 2;
+    return l;
+}
+
+template <int T, bool GATED>
+hipError_t launch_kq_expert(dim3 grid, size_t lds, hipStream_t stream, const uint8_t *w0, const uint8_t *w1,
+                            int64_t row_bytes, int cols, int rows_per_expert, int rows_per_block,
+                            const float *vec, int64_t vec_stride, int by_pair, int top_k, const int32_t *meta,
+                            int E, int P, int group, float *out, int64_t out_stride) {
+    const int lpr = kq_lanes_per_row(cols / 256);
+#define GOLLEK_KQ_LAUNCH(L)                                                                              \
+    hipLaunchKernelGGL((moe_kq_expert_kernel<T, GATED, L>), grid, dim3(256), lds, stream, w0, w1, row_bytes, \
+                       cols, rows_per_expert, rows_per_block, vec, vec_stride, by_pair, top_k, meta, E, P, \
+                       group, out, out_stride)
+    if (lpr == 1) GOLLEK_KQ_LAUNCH(1);
+    else if (lpr == 2) GOLLEK_KQ_LAUNCH(2);
+    else if (lpr == 4) GOLLEK_KQ_LAUNCH(4);
+    else if (lpr == 8) GOLLEK_KQ_LAUNCH(8);
+    else if (lpr == 16) GOLLEK_KQ_LAUNCH(16);
+    else if (lpr == 32) GOLLEK_KQ_LAUNCH(32);
+    else GOLLEK_KQ_LAUNCH(64);
+#undef GOLLEK_KQ_LAUNCH
+    return hipGetLastError();
+}
+
 // Lanes per row for rows of nb blocks: about four blocks per lane, 8 .. 64.
 inline int q32_lanes_per_row(int nb) {
     int l = 8;
@@ -573,6 +803,12 @@ hipError_t launch_moe_generic(int gate_type, int up_type, int down_type, const u
         const int g = (96 * 1024) / ((cols / 32) * 144);
         return g < kQ32Group ? g : kQ32Group;
     };
+    // K-quant passes: 36 floats per 32 elements and 4 more per superblock.
+    auto kq_route_bytes = [](int cols) { return (size_t)((cols / 32) * 36 + (cols / 256) * 4) * 4; };
+    auto kq_group = [&](int cols) {
+        const int g = (int)((96 * 1024) / kq_route_bytes(cols));
+        return g < kQ32Group ? g : kQ32Group;
+    };
     const bool x_aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     const int g_gu = q32_group(H), g_dn = q32_group(I);
     if (gate_type == up_type && (gate_type == kQ8_0 || gate_type == kQ4_0) && x_aligned && g_gu > 0 &&
@@ -585,6 +821,21 @@ hipError_t launch_moe_generic(int gate_type, int up_type, int down_type, const u
         else
             err = launch_q32_expert<kQ4_0, true>(grid, lds, stream, gate, up, gate_row_bytes, H, I, kRows, x, (int64_t)H, 0,
                                            top_k, meta, E, P, g_gu, h, (int64_t)I);
+    } else if (gate_type == up_type && (gate_type == kQ4_K || gate_type == kQ5_K || gate_type == kQ6_K) &&
+               x_aligned && kq_group(H) > 0 && H % 256 == 0 && gate_row_bytes == up_row_bytes &&
+               (int64_t)I * gate_row_bytes < ((int64_t)1 << 31)) {
+        const int g_kq = kq_group(H);
+        const size_t lds = (size_t)g_kq * kq_route_bytes(H);
+        const dim3 grid((I + kRows - 1) / kRows, E);
+        if (gate_type == kQ4_K)
+            err = launch_kq_expert<kQ4_K, true>(grid, lds, stream, gate, up, gate_row_bytes, H, I, kRows, x, (int64_t)H,
+                                                0, top_k, meta, E, P, g_kq, h, (int64_t)I);
+        else if (gate_type == kQ5_K)
+            err = launch_kq_expert<kQ5_K, true>(grid, lds, stream, gate, up, gate_row_bytes, H, I, kRows, x, (int64_t)H,
+                                                0, top_k, meta, E, P, g_kq, h, (int64_t)I);
+        else
+            err = launch_kq_expert<kQ6_K, true>(grid, lds, stream, gate, up, gate_row_bytes, H, I, kRows, x, (int64_t)H,
+                                                0, top_k, meta, E, P, g_kq, h, (int64_t)I);
     } else {
         hipLaunchKernelGGL(moe_generic_expert_kernel<true>, dim3((I + kRows - 1) / kRows, E), dim3(256), 0, stream,
                            gate_type, up_type, gate, up, gate_row_bytes, up_row_bytes, H, I, kRows, x, (int64_t)H, 0,
@@ -602,6 +853,20 @@ hipError_t launch_moe_generic(int gate_type, int up_type, int down_type, const u
         else
             err = launch_q32_expert<kQ4_0, false>(grid, lds, stream, down, down, down_row_bytes, I, H, kRows, h, (int64_t)I,
                                             1, top_k, meta, E, P, g_dn, ypair, (int64_t)H);
+    } else if ((down_type == kQ4_K || down_type == kQ5_K || down_type == kQ6_K) && kq_group(I) > 0 &&
+               I % 256 == 0 && (int64_t)H * down_row_bytes < ((int64_t)1 << 31)) {
+        const int g_kq = kq_group(I);
+        const size_t lds = (size_t)g_kq * kq_route_bytes(I);
+        const dim3 grid((H + kRows - 1) / kRows, E);
+        if (down_type == kQ4_K)
+            err = launch_kq_expert<kQ4_K, false>(grid, lds, stream, down, down, down_row_bytes, I, H, kRows, h,
+                                                 (int64_t)I, 1, top_k, meta, E, P, g_kq, ypair, (int64_t)H);
+        else if (down_type == kQ5_K)
+            err = launch_kq_expert<kQ5_K, false>(grid, lds, stream, down, down, down_row_bytes, I, H, kRows, h,
+                                                 (int64_t)I, 1, top_k, meta, E, P, g_kq, ypair, (int64_t)H);
+        else
+            err = launch_kq_expert<kQ6_K, false>(grid, lds, stream, down, down, down_row_bytes, I, H, kRows, h,
+                                                 (int64_t)I, 1, top_k, meta, E, P, g_kq, ypair, (int64_t)H);
     } else {
         hipLaunchKernelGGL(moe_generic_expert_kernel<false>, dim3((H + kRows - 1) / kRows, E), dim3(256), 0, stream,
                            down_type, down_type, down, down, down_row_bytes, down_row_bytes, I, H, kRows, h,
