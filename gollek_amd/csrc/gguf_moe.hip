@@ -1,4 +1,6 @@
-// gguf_moe.hip -- grouped Q4_K MoE expert FFN on gfx950.
+// gguf_moe.hip -- grouped MoE expert FFN on gfx950: the dispatch by expert
+// type and shape, the routing and route-order combine kernels, and the
+// passes that do not use the matrix cores (gguf_moe_mfma.hip has those).
 //
 // Semantics of runner/safetensor/gollek-safetensor-engine/src/main/java/tech/
 // kayys/gollek/safetensor/engine/generation/moe/MoeForwardPass.java:217-240 and
@@ -7,21 +9,27 @@
 // accumulated in routing order; routes with an out-of-range expert id or a
 // zero weight are skipped (MFP:222).  swigluFfn = down(silu(gate x) * up x)
 // (.../engine/forward/DirectForwardFfnService.java:40-61).  Expert weights are
-// GGUF Q4_K, stacked the way GGUF stores experts: gate/up have experts * inter
-// rows of `hidden` columns, down has experts * hidden rows of `inter` columns.
+// GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K, stacked the way GGUF stores experts:
+// gate/up have experts * inter rows of `hidden` columns, down has experts *
+// hidden rows of `inter` columns.
 //
 // The reference runs every (token, route) pair separately and so re-reads an
 // expert's weights once per pair.  Here the pairs are grouped by expert on the
-// device and every used expert's weights stream from HBM once:
+// device and every used expert's weights stream from HBM once per group of
+// up to four of its routes:
 //   1. route: count pairs per expert, stable-sort the pair list by expert,
 //      list the used experts (one workgroup);
-//   2. digits: each token's x as integer digit planes (gguf_dot4.hpp);
-//   3. gate/up: per (used expert, row tile) the gate and up rows are loaded
-//      once and contracted against all of the expert's tokens; h = silu(g) u;
-//   4. digits of every pair's h;
-//   5. down: per (used expert, row tile), y_pair = down_e h;
-//   6. combine: out[t] = sum_j w[t,j] y_pair[t,j] in j order (plain fp32
+//   2. gate/up: per (used expert, row tile) the gate and up rows are loaded
+//      once and contracted against the expert's routes; h = silu(g) u;
+//   3. down: per (used expert, row tile), y_pair = down_e h;
+//   4. combine: out[t] = sum_j w[t,j] y_pair[t,j] in j order (plain fp32
 //      multiply then add, as MFP:461-472 accumulates).
+// Passes 2 and 3 per type: Q8_0 / Q4_0 rows on moe_q32_expert_kernel, Q4_K /
+// Q5_K / Q6_K rows on moe_kq_expert_kernel (fp32, the routes' vectors staged
+// in LDS), all-Q4_K layers up to hidden 4096 on the v_dot4 kernels
+// (moe_expert_kernel, x and h as integer digit planes, gguf_dot4.hpp), and
+// anything else on moe_generic_expert_kernel (byte loads, any alignment).
+// launch_moe sends the shapes the matrix-core passes take there first.
 #include "gguf_block_dot.hpp"
 #include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"
