@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gollek_hip_weight_free": (None, [_P]),
     "gollek_hip_weight_prepare": (_I32, [_P, _CHARP, _SZ]),
     "gollek_hip_weight_unprepare": (_I32, [_P, _CHARP, _SZ]),
+    "gollek_hip_weight_compact": (_I32, [_P, _CHARP, _SZ]),
     "gollek_hip_weight_info": (_I32, [_P, _P, _P, _P, _P]),
     "gollek_hip_dequantize_rows": (_I32, [_P, _I64, _I64, _P, _I64, _CHARP, _SZ]),
     "gollek_hip_dot_row": (_I32, [_P, _I64, _P, _I64, _P, _CHARP, _SZ]),

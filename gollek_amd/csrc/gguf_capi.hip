@@ -33,6 +33,9 @@ struct gollek_hip_weight {
     size_t gemm_ws_bytes = 0;
     uint8_t *prep = nullptr;       // prepared column layout (gollek_hip_weight_prepare)
     int64_t prep_rows = 0;         // its rows per workgroup
+    bool compact = false;          // GGUF bytes freed (gollek_hip_weight_compact): prep only
+    uint8_t *ctmp = nullptr;       // device temporaries of a compact handle's _device entries
+    size_t ctmp_bytes = 0;
     uint8_t *hstage = nullptr;     // pinned host staging for host x / y / dst
     size_t hstage_bytes = 0;
 };
@@ -203,6 +206,27 @@ int32_t ensure_staging(gollek_hip_weight *w, size_t bytes, char *err, size_t err
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// A compact handle's device temporaries (grown on demand; the _device entries
+// that use them must not overlap on one handle).
+int32_t ensure_ctmp(gollek_hip_weight *w, size_t bytes, char *err, size_t err_len) {
+    if (w->ctmp_bytes >= bytes) return GOLLEK_HIP_OK;
+    if (w->ctmp != nullptr) {
+        (void)hipFree(w->ctmp);
+        w->ctmp = nullptr;
+        w->ctmp_bytes = 0;
+    }
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&w->ctmp), bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(compact temporaries)", err, err_len);
+    w->ctmp_bytes = bytes;
+    return GOLLEK_HIP_OK;
+}
+
+int32_t compact_unsupported(const gollek_hip_weight *w, const char *what, char *err, size_t err_len) {
+    return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                "%s reads GGUF rows, which a compacted handle (type %d, %lld x %lld) no longer holds", what,
+                w->type_id, (long long)w->rows, (long long)w->cols);
+}
+
 gollek_hip_weight *make_weight(int32_t type_id, int64_t rows, int64_t cols, int64_t row_bytes,
                                char *err, size_t err_len) {
     if (check_shape(type_id, rows, cols, row_bytes, err, err_len) != GOLLEK_HIP_OK) return nullptr;
@@ -311,6 +335,7 @@ void gollek_hip_weight_free(gollek_hip_weight *w) {
     if (w->staging != nullptr) (void)hipFree(w->staging);
     if (w->gemm_ws != nullptr) (void)hipFree(w->gemm_ws);
     if (w->prep != nullptr) (void)hipFree(w->prep);
+    if (w->ctmp != nullptr) (void)hipFree(w->ctmp);
     if (w->hstage != nullptr) (void)hipHostFree(w->hstage);
     if (w->stream != nullptr) (void)hipStreamDestroy(w->stream);
     delete w;
@@ -323,6 +348,15 @@ int32_t gollek_hip_weight_prepare(gollek_hip_weight *w, char *err, size_t err_le
     if (rc != GOLLEK_HIP_OK) return rc;
     // Only shapes the column kernel takes for a full mat-vec have a layout.
     const int64_t per = gollek::col_layout_rows(w->type_id, w->rows, w->cols);
+    if (w->compact) {  // its layout is all it holds
+        if (per == w->prep_rows) {
+            ok(err, err_len);
+            return GOLLEK_HIP_OK;
+        }
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "compacted handle: its prepared layout is for %lld rows per workgroup, the kernels now use %lld",
+                    (long long)w->prep_rows, (long long)per);
+    }
     const bool takes = per > 0 && (gollek::q32_mfma_supported(w->type_id, w->row_bytes, w->cols, w->rows, w->data,
                                                               nullptr) ||
                                    (w->type_id == GOLLEK_HIP_Q4_K &&
@@ -359,6 +393,24 @@ int32_t gollek_hip_weight_prepare(gollek_hip_weight *w, char *err, size_t err_le
 int32_t gollek_hip_weight_unprepare(gollek_hip_weight *w, char *err, size_t err_len) {
     if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
     std::lock_guard<std::mutex> lock(w->mu);
+    if (w->compact) {
+        // The GGUF rows are rebuilt from the layout first.
+        const int32_t rc = use_device(w->device, err, err_len);
+        if (rc != GOLLEK_HIP_OK) return rc;
+        uint8_t *d = nullptr;
+        const size_t bytes = (size_t)(w->rows * w->row_bytes);
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&d), bytes);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(GGUF rows)", err, err_len);
+        e = gollek::launch_gather_col_rows(w->type_id, w->prep, d, w->rows, w->row_bytes, w->prep_rows, 0, w->rows,
+                                           w->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return hip_fail(e, "unprepare (rebuild GGUF rows)", err, err_len);
+        }
+        w->data = d;
+        w->compact = false;
+    }
     if (w->prep != nullptr) {
         const int32_t rc = use_device(w->device, err, err_len);
         if (rc != GOLLEK_HIP_OK) return rc;
@@ -369,6 +421,30 @@ int32_t gollek_hip_weight_unprepare(gollek_hip_weight *w, char *err, size_t err_
         w->prep_rows = 0;
         if (e != hipSuccess) return hip_fail(e, "unprepare", err, err_len);
     }
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_weight_compact(gollek_hip_weight *w, char *err, size_t err_len) {
+    if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
+    std::lock_guard<std::mutex> lock(w->mu);
+    if (w->compact) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    if (!w->owned)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "the handle borrows its bytes (wrap_device): nothing to free");
+    if (w->prep == nullptr)
+        return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                    "no prepared layout to keep (prepare first; type %d, %lld x %lld has none when prepare is a no-op)",
+                    w->type_id, (long long)w->rows, (long long)w->cols);
+    const int32_t rc = use_device(w->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    hipError_t e = hipStreamSynchronize(w->stream);
+    if (e == hipSuccess && w->data != nullptr) e = hipFree(w->data);
+    if (e != hipSuccess) return hip_fail(e, "compact", err, err_len);
+    w->data = nullptr;
+    w->compact = true;
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }
@@ -403,18 +479,30 @@ int32_t gollek_hip_dequantize_rows(gollek_hip_weight *w, int64_t row0, int64_t n
     int32_t rc = use_device(w->device, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     const size_t bytes = (size_t)nrows * (size_t)w->cols * sizeof(float);
+    // A compact handle's rows are first gathered from its prepared layout
+    // into device staging (the same bytes, so the same bits).
+    const size_t gbytes = w->compact ? align_up((size_t)(nrows * w->row_bytes), 256) : 0;
     // With the pinned staging the kernel stores the rows there itself (the
     // buffer is mapped for the device); otherwise through device staging and
     // a device-to-host copy.
     uint8_t *hs = host_staging(w, bytes);
     float *d_out = reinterpret_cast<float *>(hs);
-    if (hs == nullptr) {
-        rc = ensure_staging(w, bytes, err, err_len);
+    if (hs == nullptr || gbytes > 0) {
+        rc = ensure_staging(w, gbytes + (hs == nullptr ? bytes : 0), err, err_len);
         if (rc != GOLLEK_HIP_OK) return rc;
-        d_out = reinterpret_cast<float *>(w->staging);
+        if (hs == nullptr) d_out = reinterpret_cast<float *>(w->staging + gbytes);
     }
-    hipError_t e = gollek::launch_dequant(w->type_id, w->data, w->row_bytes, w->cols, row0, nrows,
-                                          d_out, w->stream);
+    const uint8_t *src = w->data;
+    int64_t srow0 = row0;
+    hipError_t e = hipSuccess;
+    if (w->compact) {
+        e = gollek::launch_gather_col_rows(w->type_id, w->prep, w->staging, w->rows, w->row_bytes, w->prep_rows,
+                                           row0, nrows, w->stream);
+        src = w->staging;
+        srow0 = 0;
+    }
+    if (e == hipSuccess)
+        e = gollek::launch_dequant(w->type_id, src, w->row_bytes, w->cols, srow0, nrows, d_out, w->stream);
     if (e == hipSuccess && hs == nullptr)
         e = hipMemcpyAsync(dst, d_out, bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
@@ -424,13 +512,17 @@ int32_t gollek_hip_dequantize_rows(gollek_hip_weight *w, int64_t row0, int64_t n
     return GOLLEK_HIP_OK;
 }
 
-static int32_t matvec_host(gollek_hip_weight *w, const uint8_t *rows_base, int64_t nrows,
-                           const float *x, float *y, char *err, size_t err_len) {
+// Rows row0 .. row0 + nrows - 1 of W x.  A compact handle runs the full
+// mat-vec from its prepared layout and returns the requested rows (the same
+// bits as its full call).
+static int32_t matvec_host(gollek_hip_weight *w, int64_t row0, int64_t nrows, const float *x, float *y,
+                           char *err, size_t err_len) {
     std::lock_guard<std::mutex> lock(w->mu);
     int32_t rc = use_device(w->device, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
+    const int64_t krows = w->compact ? w->rows : nrows;  // rows the kernel computes
     const size_t x_bytes = align_up((size_t)w->cols * sizeof(float), 256);
-    const size_t y_bytes = (size_t)nrows * sizeof(float);
+    const size_t y_bytes = (size_t)krows * sizeof(float);
     rc = ensure_staging(w, x_bytes + y_bytes, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     float *d_x = reinterpret_cast<float *>(w->staging);
@@ -441,19 +533,28 @@ static int32_t matvec_host(gollek_hip_weight *w, const uint8_t *rows_base, int64
     hipError_t e =
         hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
     // the prepared layout covers full mat-vecs only (its partition depends on the row count)
-    const bool full = rows_base == w->data && nrows == w->rows;
+    const bool full = row0 == 0 && nrows == w->rows;
     // With the pinned staging the kernel stores y there itself (the buffer is
     // mapped for the device; the stream synchronisation below makes the
     // stores visible to the host), which saves the device-to-host copy.
     float *k_y = hs != nullptr ? reinterpret_cast<float *>(hs + x_bytes) : d_y;
-    if (e == hipSuccess)
-        e = gollek::launch_gemv(w->type_id, rows_base, w->row_bytes, w->cols, d_x, k_y, nrows,
+    if (e == hipSuccess && w->compact) {
+        e = gollek::launch_gemv_prepared(w->type_id, w->prep, w->row_bytes, w->cols, d_x, k_y, w->rows, w->prep_rows,
+                                         w->stream);
+        if (e == hipErrorInvalidValue)
+            return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                        "compacted handle: the column kernel's partition is no longer its layout's");
+    } else if (e == hipSuccess) {
+        e = gollek::launch_gemv(w->type_id, w->data + row0 * w->row_bytes, w->row_bytes, w->cols, d_x, k_y, nrows,
                                 w->stream, full ? w->prep : nullptr, full ? w->prep_rows : 0);
+    }
+    const int64_t first = w->compact ? row0 : 0;  // the caller's rows in the kernel's y
+    const size_t out_bytes = (size_t)nrows * sizeof(float);
     if (e == hipSuccess && hs == nullptr)
-        e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
+        e = hipMemcpyAsync(y, d_y + first, out_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     if (e != hipSuccess) return hip_fail(e, "matvec", err, err_len);
-    if (hs != nullptr) std::memcpy(y, hs + x_bytes, y_bytes);
+    if (hs != nullptr) std::memcpy(y, hs + x_bytes + first * sizeof(float), out_bytes);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
 }
@@ -469,7 +570,7 @@ int32_t gollek_hip_dot_row(gollek_hip_weight *w, int64_t row, const float *x, in
     if (row < 0 || row >= w->rows)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Row %lld is outside tensor row count %lld",
                     (long long)row, (long long)w->rows);
-    return matvec_host(w, w->data + row * w->row_bytes, 1, x, out, err, err_len);
+    return matvec_host(w, row, 1, x, out, err, err_len);
 }
 
 int32_t gollek_hip_matvec_rows(gollek_hip_weight *w, const float *x, int64_t x_len, float *y,
@@ -492,7 +593,7 @@ int32_t gollek_hip_matvec_rows(gollek_hip_weight *w, const float *x, int64_t x_l
         ok(err, err_len);
         return GOLLEK_HIP_OK;
     }
-    return matvec_host(w, w->data, row_count, x, y, err, err_len);
+    return matvec_host(w, 0, row_count, x, y, err, err_len);
 }
 
 int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *w, int64_t row0, int64_t nrows,
@@ -502,8 +603,22 @@ int32_t gollek_hip_dequantize_rows_device(gollek_hip_weight *w, int64_t row0, in
     if (nrows < 0 || row0 < 0 || row0 + nrows > w->rows)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Rows [%lld, %lld) are outside tensor row count %lld",
                     (long long)row0, (long long)(row0 + nrows), (long long)w->rows);
-    hipError_t e = gollek::launch_dequant(w->type_id, w->data, w->row_bytes, w->cols, row0, nrows,
-                                          dst, static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint8_t *src = w->data;
+    int64_t srow0 = row0;
+    hipError_t e = hipSuccess;
+    if (w->compact && nrows > 0) {  // the rows gathered from the prepared layout first
+        {
+            std::lock_guard<std::mutex> lock(w->mu);
+            const int32_t rc = ensure_ctmp(w, (size_t)(nrows * w->row_bytes), err, err_len);
+            if (rc != GOLLEK_HIP_OK) return rc;
+        }
+        e = gollek::launch_gather_col_rows(w->type_id, w->prep, w->ctmp, w->rows, w->row_bytes, w->prep_rows, row0,
+                                           nrows, st);
+        src = w->ctmp;
+        srow0 = 0;
+    }
+    if (e == hipSuccess) e = gollek::launch_dequant(w->type_id, src, w->row_bytes, w->cols, srow0, nrows, dst, st);
     if (e != hipSuccess) return hip_fail(e, "dequantize launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -518,9 +633,37 @@ int32_t gollek_hip_matvec_device(gollek_hip_weight *w, const float *x, float *y,
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Requested row count %lld is outside tensor rows %lld",
                     (long long)row_count, (long long)w->rows);
     const bool full = row_count == w->rows;  // the prepared layout covers full mat-vecs only
-    hipError_t e = gollek::launch_gemv(w->type_id, w->data, w->row_bytes, w->cols, x, y, row_count,
-                                       static_cast<hipStream_t>(stream), full ? w->prep : nullptr,
-                                       full ? w->prep_rows : 0);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    if (w->compact && row_count > 0) {
+        // The full mat-vec from the prepared layout; a prefix goes through a
+        // temporary y, an unaligned x through an aligned copy.
+        const bool x_ok = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+        const size_t x_bytes = x_ok ? 0 : align_up((size_t)w->cols * sizeof(float), 256);
+        const size_t need = x_bytes + (full ? 0 : (size_t)w->rows * sizeof(float));
+        if (need > 0) {
+            std::lock_guard<std::mutex> lock(w->mu);
+            const int32_t rc = ensure_ctmp(w, need, err, err_len);
+            if (rc != GOLLEK_HIP_OK) return rc;
+        }
+        const float *kx = x;
+        if (!x_ok) {
+            e = hipMemcpyAsync(w->ctmp, x, (size_t)w->cols * sizeof(float), hipMemcpyDeviceToDevice, st);
+            kx = reinterpret_cast<const float *>(w->ctmp);
+        }
+        float *ky = full ? y : reinterpret_cast<float *>(w->ctmp + x_bytes);
+        if (e == hipSuccess)
+            e = gollek::launch_gemv_prepared(w->type_id, w->prep, w->row_bytes, w->cols, kx, ky, w->rows,
+                                             w->prep_rows, st);
+        if (e == hipErrorInvalidValue)
+            return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
+                        "compacted handle: the column kernel's partition is no longer its layout's");
+        if (e == hipSuccess && !full)
+            e = hipMemcpyAsync(y, ky, (size_t)row_count * sizeof(float), hipMemcpyDeviceToDevice, st);
+    } else if (!w->compact) {
+        e = gollek::launch_gemv(w->type_id, w->data, w->row_bytes, w->cols, x, y, row_count, st,
+                                full ? w->prep : nullptr, full ? w->prep_rows : 0);
+    }
     if (e != hipSuccess) return hip_fail(e, "matvec launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -534,6 +677,7 @@ static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, in
     if (w->type_id != GOLLEK_HIP_Q8_0 && w->type_id != GOLLEK_HIP_Q4_0 && w->type_id != GOLLEK_HIP_Q4_K)
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
                     "Unsupported GGUF bf16 GEMM type id: %d (Q8_0, Q4_0 or Q4_K)", w->type_id);
+    if (w->compact) return compact_unsupported(w, "GEMM", err, err_len);
     if (m < 0 || m > (int64_t)0x7FFFFFFF || w->rows > 0x7FFFFFFF || w->cols > 0x7FFFFFFF)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "GEMM shape %lld x %lld x %lld is out of range",
                     (long long)m, (long long)w->rows, (long long)w->cols);
@@ -669,6 +813,8 @@ static int32_t check_moe(gollek_hip_weight *gate, gollek_hip_weight *up, gollek_
                          char *err, size_t err_len) {
     if (gate == nullptr || up == nullptr || down == nullptr)
         return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "expert weights");
+    for (const gollek_hip_weight *t : {gate, up, down})
+        if (t->compact) return compact_unsupported(t, "The MoE expert FFN", err, err_len);
     if (!moe_type(gate->type_id) || !moe_type(up->type_id) || !moe_type(down->type_id))
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
                     "Unsupported MoE expert weight types %d/%d/%d (Q8_0, Q4_0, Q4_K, Q5_K or Q6_K)",

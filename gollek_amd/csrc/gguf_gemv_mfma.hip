@@ -1160,7 +1160,47 @@ __global__ void prepare_col_kernel(const uint8_t *__restrict__ raw, uint8_t *__r
     }
 }
 
+// The inverse: GGUF rows row0 .. row0 + nrows - 1 (row_bytes each, packed
+// into dst) gathered from the prepared layout.
+__global__ void gather_col_rows_kernel(const uint8_t *__restrict__ prep, uint8_t *__restrict__ dst, int64_t rows,
+                                       int64_t row_bytes, int64_t per, int pb, int64_t row0, int64_t nrows) {
+    const int64_t units = nrows * row_bytes / 16;
+    for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units;
+         u += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t byte = 16 * u, rl = byte / row_bytes, c = byte - rl * row_bytes;
+        const int64_t r = row0 + rl, b = r / per, rr = r - b * per;
+        const int64_t nb = rows - b * per < per ? rows - b * per : per;
+        const int64_t col = c / pb, cc = c - col * pb;
+        const int64_t src = b * per * row_bytes + col * nb * pb + rr * pb + cc;
+        *reinterpret_cast<uint4 *>(dst + byte) = *reinterpret_cast<const uint4 *>(prep + src);
+    }
+}
+
 }  // namespace
+
+// A full mat-vec from the prepared layout alone (a handle that no longer
+// holds its GGUF bytes): the column / wide kernels, never a kernel that reads
+// GGUF rows.  The partition must still be prep_rows and x 16-byte aligned.
+hipError_t launch_gemv_prepared(int type_id, const uint8_t *prep, int64_t row_bytes, int64_t cols, const float *x,
+                                float *y, int64_t rows, int64_t prep_rows, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (prep == nullptr || prep_rows <= 0 || col_layout_rows(type_id, rows, cols) != prep_rows ||
+        (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
+        return hipErrorInvalidValue;
+    if (type_id == kQ4_K) return launch_gemv_q4k_mfma(prep, row_bytes, cols, x, y, rows, stream, prep, prep_rows);
+    return launch_gemv_q32_mfma(type_id, prep, row_bytes, cols, x, y, rows, stream, prep, prep_rows);
+}
+
+hipError_t launch_gather_col_rows(int type_id, const uint8_t *prep, uint8_t *dst, int64_t rows, int64_t row_bytes,
+                                  int64_t per, int64_t row0, int64_t nrows, hipStream_t stream) {
+    if (nrows <= 0) return hipSuccess;
+    const int pb = type_id == kQ8_0 ? ColGeom<kQ8_0>::PB : type_id == kQ5_K ? ColGeom<kQ5_K>::PB : ColGeom<kQ4_K>::PB;
+    const int64_t units = nrows * row_bytes / 16;
+    const int64_t blocks = (units + 255) / 256 < 65536 ? (units + 255) / 256 : 65536;
+    hipLaunchKernelGGL(gather_col_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, prep, dst, rows,
+                       row_bytes, per, pb, row0, nrows);
+    return hipGetLastError();
+}
 
 // The column kernel's prepared layout of a full matrix (rows x row_bytes)
 // for col_layout_rows(...) = per rows per workgroup; every piece is a whole

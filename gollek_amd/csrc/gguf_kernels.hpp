@@ -46,6 +46,14 @@ hipError_t launch_gemv(int type_id, const uint8_t *w, int64_t row_bytes, int64_t
 int64_t col_layout_rows(int type_id, int64_t rows, int64_t cols);
 hipError_t launch_prepare_col_layout(int type_id, const uint8_t *raw, uint8_t *prep, int64_t rows,
                                      int64_t row_bytes, int64_t per, hipStream_t stream);
+// A full mat-vec read from the prepared layout only (hipErrorInvalidValue
+// when the partition is no longer prep_rows or x is not 16-byte aligned).
+hipError_t launch_gemv_prepared(int type_id, const uint8_t *prep, int64_t row_bytes, int64_t cols, const float *x,
+                                float *y, int64_t rows, int64_t prep_rows, hipStream_t stream);
+// The inverse for rows row0 .. row0 + nrows - 1 of the prepared layout:
+// their GGUF bytes, packed (nrows x row_bytes) into dst.
+hipError_t launch_gather_col_rows(int type_id, const uint8_t *prep, uint8_t *dst, int64_t rows, int64_t row_bytes,
+                                  int64_t per, int64_t row0, int64_t nrows, hipStream_t stream);
 
 // Q4_K GEMV on the matrix cores (gguf_gemv_mfma.hip).
 // Q8_0 / Q4_0 GEMV through per-wave buffer->LDS rings (gguf_gemv_ring.hip).

@@ -55,11 +55,15 @@ import java.util.WeakHashMap;
  * JavaNativeGgufBackend.java:157-180), and
  * the device handle lives until release(model).</p>
  *
- * <p>A prepared layout is a second device copy of the tensor.  Like the
- * reference's prepared caches (RT/GgufPreparedCachePolicy.java:29-42) the
+ * <p>A prepared tensor is then compacted (gollek_hip_weight_compact) unless
+ * gollek.hip.compact is "false": its GGUF copy is freed and the prepared
+ * layout is the one device copy, which serves every call this class makes
+ * (mat-vec, row prefixes, dotRow, dequantizeRow) with the same results.  A
+ * prepared layout that is not compacted is a second device copy.  Like the
+ * reference's prepared caches (RT/GgufPreparedCachePolicy.java:29-42) such
  * copies are admitted under a byte budget, gollek.hip.prepare.max_bytes
  * (default: no limit; the tensor's whole size is charged when prepare is
- * asked for).  When an upload finds the device full, every prepared copy is
+ * asked for).  When an upload finds the device full, every such copy is
  * freed (the handles then read the GGUF bytes, with the same results),
  * preparing stops for the rest of the process, and the upload is tried once
  * more; a prepare that finds no memory only stops preparing.</p>
@@ -198,8 +202,13 @@ final class GgufHipMatVec {
                         && preparedBytes <= Long.getLong("gollek.hip.prepare.max_bytes", Long.MAX_VALUE) - size) {
                     int rc = b.weightPrepare(w, err, (long) ERR_LEN);
                     if (rc == OK) {
-                        PREPARED.put(w, size);
-                        preparedBytes += size;
+                        // one copy when compacted; otherwise a second one, charged
+                        boolean compacted = !"false".equals(System.getProperty("gollek.hip.compact", "true"))
+                                && b.weightCompact(w, err, (long) ERR_LEN) == OK;
+                        if (!compacted) {
+                            PREPARED.put(w, size);
+                            preparedBytes += size;
+                        }
                     } else if (rc == ERR_NOMEM) {
                         preparingStopped = true;
                     } else {
@@ -253,6 +262,7 @@ final class GgufHipMatVec {
         private final MethodHandle weightFree;
         private final MethodHandle weightPrepare;
         private final MethodHandle weightUnprepare;
+        private final MethodHandle weightCompact;
         private final MethodHandle matvecRows;
         private final MethodHandle dotRow;
         private final MethodHandle dequantizeRows;
@@ -316,6 +326,9 @@ final class GgufHipMatVec {
                     FunctionDescriptor.of(ValueLayout.JAVA_INT,
                             ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
             this.weightUnprepare = downcall(linker, lookup, "gollek_hip_weight_unprepare",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
+            this.weightCompact = downcall(linker, lookup, "gollek_hip_weight_compact",
                     FunctionDescriptor.of(ValueLayout.JAVA_INT,
                             ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), false);
             // The float[] arguments are passed as heap segments: critical downcalls with heap access.
@@ -393,6 +406,14 @@ final class GgufHipMatVec {
         int weightUnprepare(MemorySegment weight, MemorySegment err, long errLen) {
             try {
                 return (int) weightUnprepare.invokeExact(weight, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int weightCompact(MemorySegment weight, MemorySegment err, long errLen) {
+            try {
+                return (int) weightCompact.invokeExact(weight, err, errLen);
             } catch (Throwable t) {
                 throw propagate(t);
             }

@@ -145,6 +145,13 @@ class GgufTensor:
             err = _native.ErrBuf()
             check(_native.load().gollek_hip_weight_unprepare(self._handle, err.buf, err.size), err)
 
+    def compact(self) -> None:
+        """Keep only the prepared layout (gollek_hip_weight_compact): the
+        packed bytes are held once; GEMM and MoE then raise
+        UnsupportedOperationError."""
+        err = _native.ErrBuf()
+        check(_native.load().gollek_hip_weight_compact(self.handle(), err.buf, err.size), err)
+
     def close(self) -> None:
         if self._handle is not None:
             _native.load().gollek_hip_weight_free(self._handle)
@@ -363,6 +370,11 @@ class DeviceWeight:
         err = _native.ErrBuf()
         check(_native.load().gollek_hip_weight_unprepare(self.handle, err.buf, err.size), err)
 
+    def compact(self) -> None:
+        """Keep only the prepared layout (gollek_hip_weight_compact)."""
+        err = _native.ErrBuf()
+        check(_native.load().gollek_hip_weight_compact(self.handle, err.buf, err.size), err)
+
     def close(self) -> None:
         if self.handle:
             _native.load().gollek_hip_weight_free(self.handle)
@@ -402,7 +414,7 @@ class DeviceWeight:
 
 
 def gemm_bf16(tensor: GgufTensor, x_bf16: np.ndarray, output: np.ndarray) -> None:
-    """Y = X W^T for a Q8_0 tensor: x_bf16 (m, columns) uint16 bf16 bit patterns,
+    """Y = X W^T for a Q8_0, Q4_0 or Q4_K tensor: x_bf16 (m, columns) uint16 bf16 bit patterns,
     output (m, rows) float32.  The reference runs m matVecRows calls instead
     (RT/GgufTensorOps.java:666-674)."""
     if tensor is None:
@@ -420,8 +432,8 @@ def gemm_bf16(tensor: GgufTensor, x_bf16: np.ndarray, output: np.ndarray) -> Non
 
 def moe_grouped(gate: GgufTensor, up: GgufTensor, down: GgufTensor, n_experts: int, x, ids,
                 weights) -> np.ndarray:
-    """Grouped MoE expert FFN over Q4_K gate / up and Q4_K or Q6_K down experts
-    (the expert loop of MoeForwardPass.computeAccel,
+    """Grouped MoE expert FFN over Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K experts
+    (gate, up and down may differ; the expert loop of MoeForwardPass.computeAccel,
     runner/safetensor/gollek-safetensor-engine/src/main/java/tech/kayys/gollek/
     safetensor/engine/generation/moe/MoeForwardPass.java:217-240): x (tokens,
     hidden) float32, ids (tokens, top_k) int32, weights (tokens, top_k) float32

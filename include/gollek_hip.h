@@ -126,6 +126,23 @@ int32_t gollek_hip_weight_prepare(gollek_hip_weight *weight, char *err, size_t e
  * _device call on the handle may be in flight. */
 int32_t gollek_hip_weight_unprepare(gollek_hip_weight *weight, char *err, size_t err_len);
 
+/* Keep only the prepared layout: free the handle's GGUF copy, so the packed
+ * bytes are held once.  Full and prefix mat-vecs (matvec_rows, dot_row and
+ * the _device form) then run the full mat-vec from the layout, so a prefix
+ * or a single row returns exactly the full call's bits for its rows;
+ * dequantize_rows gathers the rows' bytes back from the layout first (the
+ * same bytes, so the same bits).  The GEMM and MoE entry points read GGUF
+ * rows and return UNSUPPORTED for a compacted handle;
+ * gollek_hip_weight_unprepare rebuilds the GGUF copy (and frees the
+ * layout).  Needs a prepared handle that owns its bytes: a borrowed
+ * (wrap_device) buffer -> ARG, no layout -> UNSUPPORTED.  Replaces keeping
+ * the raw tensor beside the prepared one (RT/GgufPreparedMatrixStore.java:
+ * 120-131 keeps one prepared representation per tensor).  No _device call
+ * on the handle may be in flight; the _device entries of a compacted handle
+ * share temporaries of the handle (grown on demand), so they must not
+ * overlap on one handle. */
+int32_t gollek_hip_weight_compact(gollek_hip_weight *weight, char *err, size_t err_len);
+
 /* Release a handle (device memory it owns, its stream and staging buffers).
  * Replaces clearPreparedMatrixCaches on backend close
  * (PRG/JavaNativeGgufBackend.java:139-143).  NULL is ignored. */

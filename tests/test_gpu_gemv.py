@@ -11,6 +11,7 @@ import zlib
 import numpy as np
 import pytest
 
+from gollek_amd import _native
 from gollek_amd import synthetic as syn
 from gollek_amd import tensor_ops as ops
 from oracle import oracle as o
@@ -543,6 +544,115 @@ def test_unprepare_returns_to_the_gguf_bytes():
     ops.mat_vec(t, x, y1)
     assert np.array_equal(y0, y1) and np.array_equal(y0, y_new)
     t.close()
+
+
+COMPACT_SHAPES = [(syn.Q4_K, 14336, 4096), (syn.Q8_0, 4096, 4096), (syn.Q4_0, 11008, 4096),
+                  (syn.Q5_K, 4096, 4096), (syn.Q4_K, 4096, 14336), (syn.Q4_K, 1001, 2304)]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", COMPACT_SHAPES,
+                         ids=[f"type{t}_{r}x{c}" for t, r, c in COMPACT_SHAPES])
+def test_compact_handle_holds_one_copy(type_id, rows, cols):
+    # After compact() only the prepared layout is held.  Full mat-vecs equal
+    # the prepared handle's bit for bit; a prefix and dot_row return exactly
+    # the full call's rows; dequantization gathers the rows back from the
+    # layout and stays bit-exact; GEMM raises (it reads GGUF rows);
+    # unprepare() rebuilds the GGUF copy.
+    import ctypes
+
+    import torch
+    print(f"[gpu] compact type={type_id} {rows}x{cols}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=70 + rows + type_id)
+    x = syn.activation(cols, seed=71)
+    ref = o.matvec_fp64(type_id, data, cols, x)
+    t = _tensor(type_id, data, cols)
+    t.prepare()
+    y_full = np.zeros(rows, np.float32)
+    ops.mat_vec(t, x, y_full)
+    assert o.rel_err(y_full, ref) <= GEMV_TOL
+    rows_sel = [0, rows // 3, rows - 1]
+    deq = {r: np.zeros(cols, np.float32) for r in rows_sel}
+    for r, dst in deq.items():
+        ops.dequantize_row(t, r, dst)
+    block = ops.dequantize_rows(t, rows // 2, min(5, rows - rows // 2))
+    t.close()
+
+    c = _tensor(type_id, data, cols)
+    c.prepare()
+    c.compact()
+    c.compact()  # idempotent
+    y = np.zeros(rows, np.float32)
+    ops.mat_vec(c, x, y)
+    assert np.array_equal(y, y_full)
+    part = np.full(rows, -3.0, np.float32)
+    ops.mat_vec_rows(c, x, part, rows - 1, True)
+    assert np.array_equal(part[:rows - 1], y_full[:rows - 1]) and part[-1] == -3.0
+    for r in rows_sel:
+        assert ops.dot_row(c, r, x) == y_full[r]
+        got = np.zeros(cols, np.float32)
+        ops.dequantize_row(c, r, got)
+        assert np.array_equal(got.view(np.uint32), deq[r].view(np.uint32))
+    got = ops.dequantize_rows(c, rows // 2, min(5, rows - rows // 2))
+    assert np.array_equal(got.view(np.uint32), block.view(np.uint32))
+    if type_id in (syn.Q8_0, syn.Q4_0, syn.Q4_K):
+        with pytest.raises(ops.UnsupportedOperationError):
+            ops.gemm_bf16(c, syn.activation_bf16(2, cols, seed=1), np.zeros((2, rows), np.float32))
+
+    # the device entries of the compact handle (through the C ABI)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    stream = torch.cuda.current_stream().cuda_stream
+    xs = torch.zeros(cols + 1, dtype=torch.float32, device="cuda")
+    xs[1:] = torch.from_numpy(x).cuda()
+    for x_dev in (xs[1:].clone(), xs[1:]):  # 16-byte aligned, then 4 bytes off
+        y_dev = torch.full((rows,), -7.0, dtype=torch.float32, device="cuda")
+        for n in (rows, rows // 2):
+            y_dev.fill_(-7.0)
+            rc = lib.gollek_hip_matvec_device(c.handle(), ctypes.c_void_p(x_dev.data_ptr()),
+                                              ctypes.c_void_p(y_dev.data_ptr()), n,
+                                              ctypes.c_void_p(stream), err.buf, err.size)
+            torch.cuda.synchronize()
+            assert rc == 0, err.text
+            got = y_dev.cpu().numpy()
+            assert np.array_equal(got[:n], y_full[:n]) and np.all(got[n:] == -7.0), n
+    d_dev = torch.zeros((3, cols), dtype=torch.float32, device="cuda")
+    rc = lib.gollek_hip_dequantize_rows_device(c.handle(), rows // 2, min(3, rows - rows // 2),
+                                               ctypes.c_void_p(d_dev.data_ptr()), ctypes.c_void_p(stream),
+                                               err.buf, err.size)
+    torch.cuda.synchronize()
+    assert rc == 0, err.text
+    n3 = min(3, rows - rows // 2)
+    assert np.array_equal(d_dev.cpu().numpy()[:n3].view(np.uint32), block[:n3].view(np.uint32))
+
+    c.unprepare()  # the GGUF rows again, from the layout
+    y_raw = np.zeros(rows, np.float32)
+    ops.mat_vec(c, x, y_raw)
+    assert o.rel_err(y_raw, ref) <= GEMV_TOL
+    got = ops.dequantize_rows(c, rows // 2, min(5, rows - rows // 2))
+    assert np.array_equal(got.view(np.uint32), block.view(np.uint32))
+    c.prepare()
+    y2 = np.zeros(rows, np.float32)
+    ops.mat_vec(c, x, y2)
+    assert np.array_equal(y2, y_full)
+    c.close()
+
+
+def test_compact_needs_an_owned_prepared_handle():
+    import torch
+    rows, cols = 4096, 4096
+    data = syn.matrix(syn.Q6_K, rows, cols, seed=3)
+    t = _tensor(syn.Q6_K, data, cols)
+    t.prepare()  # no prepared layout for Q6_K: a no-op
+    with pytest.raises(ops.UnsupportedOperationError):
+        t.compact()
+    t.close()
+    q = syn.matrix(syn.Q4_K, rows, cols, seed=4)
+    w_dev = torch.from_numpy(q.reshape(-1)).cuda()
+    dw = ops.DeviceWeight(syn.Q4_K, w_dev.data_ptr(), rows, cols)
+    dw.prepare()
+    with pytest.raises(ops.IllegalArgumentError):
+        dw.compact()  # borrowed bytes
+    dw.close()
 
 
 # ---- Q5_K / Q6_K -----------------------------------------------------------

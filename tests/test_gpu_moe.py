@@ -138,6 +138,24 @@ def test_moe_q4_0_matrix_core_equals_row_kernels(moe_variant):
         t.close()
 
 
+def test_moe_rejects_compacted_experts():
+    # A compacted handle holds only the mat-vec layout; the expert passes
+    # read GGUF rows and refuse it.
+    E, H, I = 8, 512, 256
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=5)
+    tg.prepare()
+    tg.compact()
+    ids, w = syn.moe_routing(3, E, 2, seed=6)
+    x = syn.activation(3 * H, seed=7).reshape(3, H)
+    with pytest.raises(ops.UnsupportedOperationError):
+        ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    tg.unprepare()  # GGUF rows rebuilt: the layer runs again
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    assert o.rel_err(out, o.moe_reference_q4k(gate, up, down, E, x, ids, w)) <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
 def test_moe_v_dot4_variant_parity(moe_variant):
     # moe_variant 1: the v_dot4 expert kernels at a shape the matrix-core
     # passes also take.

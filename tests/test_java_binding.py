@@ -93,6 +93,7 @@ WRAPPERS = {  # typed wrapper -> the symbol whose handle it invokes
     "weightFree": "gollek_hip_weight_free",
     "weightPrepare": "gollek_hip_weight_prepare",
     "weightUnprepare": "gollek_hip_weight_unprepare",
+    "weightCompact": "gollek_hip_weight_compact",
     "matvecRows": "gollek_hip_matvec_rows",
     "dotRow": "gollek_hip_dot_row",
     "dequantizeRows": "gollek_hip_dequantize_rows",
