@@ -125,10 +125,10 @@ MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inte
 
 // out[T, H] = sum_j w[t,j] down_e(silu(gate_e x_t) * up_e x_t) for stacked
 // gate / up / down experts of types Q8_0, Q4_0, Q4_K, Q5_K or Q6_K (each
-// matrix its own type): the matrix-core passes for Q4_K gate / up with Q4_K
-// or Q6_K down where they take the shape, the v_dot4 passes for all-Q4_K
-// otherwise, the generic passes for everything else; ws must hold
-// moe_layout(...).total bytes.
+// matrix its own type): the matrix-core passes for Q4_K or Q5_K gate / up
+// (moe_kq_mfma_supported) and for all-Q4_0 where they take the shape, the
+// v_dot4 passes for all-Q4_K otherwise, the row kernels for everything else;
+// ws must hold moe_layout(...).total bytes.
 hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *gate, const uint8_t *up,
                       const uint8_t *down, int64_t gate_row_bytes, int64_t up_row_bytes,
                       int64_t down_row_bytes, int E, int H, int I, const float *x, const int32_t *ids,
@@ -137,9 +137,16 @@ hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uin
                                int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                                const float *x, const int32_t *ids, const float *wts, int T, int top_k,
                                float *out, uint8_t *ws, hipStream_t stream);
-// Whether the matrix-core passes can take Q6_K down experts of this shape
-// (the token-major down pass; x must also be 16-byte aligned).
-bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k);
+// K-quant experts on the matrix-core passes (gguf_moe_mfma.hip): gate / up
+// both Q4_K (hidden up to 4096) or both Q5_K (hidden up to 3072); down rows
+// Q4_K or Q6_K through the token-major pass (inter up to 1024), else Q4_K or
+// Q5_K through the expert-major pass; hidden and inter multiples of 256, x
+// 16-byte aligned.
+bool moe_kq_mfma_supported(int gate_type, int down_type, int E, int H, int I, int T, int top_k,
+                           const float *x);
+hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate, const uint8_t *up,
+                              const uint8_t *down, int E, int H, int I, const float *x, const int32_t *ids,
+                              const float *wts, int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);
 // All-Q4_0 experts on the matrix-core passes (hidden up to 2048, hidden and
 // inter multiples of 256; x 16-byte aligned).
 bool moe_q40_mfma_supported(int E, int H, int I, int P, const float *x);
@@ -160,11 +167,6 @@ hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float 
 size_t moe_topk_lds_bytes(int E, int K);
 hipError_t launch_moe_topk(const float *logits, int T, int E, int K, int sigmoid, int32_t *ids,
                            float *wts, hipStream_t stream);
-bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x);
-hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
-                               int H, int I, const float *x, const int32_t *ids, const float *wts,
-                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream,
-                               int down_type);
 
 }  // namespace gollek
 

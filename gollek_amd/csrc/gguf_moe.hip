@@ -892,11 +892,11 @@ hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *
     const bool aligned = ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
                            reinterpret_cast<uintptr_t>(down) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
     const bool q4k_gu = gate_type == kQ4_K && up_type == kQ4_K;
-    // Q4_K gate / up with Q4_K or (where the token-major down pass takes the
-    // shape) Q6_K down: the matrix-core passes.
-    if (aligned && q4k_gu && tuning().moe_variant != 1 && moe_q4k_mfma_supported(E, H, I, T * top_k, x) &&
-        (down_type == kQ4_K || (down_type == kQ6_K && moe_q6k_down_supported(E, H, I, T, top_k))))
-        return launch_moe_q4k_mfma(gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws, stream, down_type);
+    // Q4_K or Q5_K gate / up with the down types the matrix-core passes take.
+    if (aligned && gate_type == up_type && tuning().moe_variant != 1 &&
+        moe_kq_mfma_supported(gate_type, down_type, E, H, I, T, top_k, x))
+        return launch_moe_kq_mfma(gate_type, down_type, gate, up, down, E, H, I, x, ids, wts, T, top_k, out, ws,
+                                  stream);
     // All Q4_0 (hidden up to 2048): the matrix-core passes with Q4_0 rows.
     if (aligned && gate_type == kQ4_0 && up_type == kQ4_0 && down_type == kQ4_0 && tuning().moe_variant != 1 &&
         moe_q40_mfma_supported(E, H, I, T * top_k, x))

@@ -1,4 +1,6 @@
-// gguf_moe_mfma.hip -- grouped Q4_K MoE expert FFN on the gfx950 matrix cores.
+// gguf_moe_mfma.hip -- grouped MoE expert FFN on the gfx950 matrix cores:
+// Q4_K or Q5_K gate / up experts with Q4_K, Q5_K or Q6_K down experts, and
+// all-Q4_0 experts.
 //
 // Semantics as gguf_moe.hip (MoeForwardPass.java:217-240, :461-472; swigluFfn
 // DirectForwardFfnService.java:40-61): h_pair = silu(gate_e x_t) * (up_e x_t),
@@ -12,13 +14,18 @@
 //     up to 4 of its routes).  A slot holds the tile's 16 gate rows and 16 up
 //     rows; wave w < nsb contracts gate superblock w, wave nsb + w up
 //     superblock w; h = silu(g) u per route and row.
-//   pass 1 (down): item = (used expert, RT = 16 / nsb 16-row tiles of its H
-//     rows, route group); wave w = (row tile w / nsb, superblock w % nsb).
-// The Q4_K contraction is the one of gguf_gemv_mfma.hip's kernels
+//   pass 1 (down): item = (used expert, RT (at most 16 / nsb, as a slot
+//     holds) 16-row tiles of its H rows, route group); wave w = (row tile
+//     w / nsb, superblock w % nsb).  With inter sizes up to 1024 and Q4_K or
+//     Q6_K down rows, pass 0 leaves h as digit records and the token-major
+//     moe_down_combine_kernel replaces pass 1 and the combine.
+// The K-quant contraction is the one of gguf_gemv_mfma.hip's kernels
 // (v_mfma_i32_16x16x64_i8 over balanced 22-bit digits of the vector, low and
-// high nibbles as bytes 0..15), with two routes per MFMA: A rows 8 t + 4 h + p hold route t's digits, so its
+// high nibbles as bytes 0..15, Q5_K's fifth bits from qh added as bit 4),
+// with two routes per MFMA: A rows 8 t + 4 h + p hold route t's digits, so its
 // results sit in output lanes 32 t + 16 h + n and the second route costs no
-// extra epilogue instructions.
+// extra epilogue instructions.  Q4_0 rows are read as 144-byte pieces of
+// eight blocks.
 //
 // Every used expert's weights stream from HBM once per group of four routes
 // (routing spreads 16 tokens x top-8 over 128 experts at ~1 route per
@@ -222,7 +229,10 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const float *__restrict__ wts, int E, int P, float *__restrict__ out) {
     static_assert(MODE == 0 || !REC, "records are pass 0's output");
     static_assert(HV == 1 || (HV == 2 && MODE == 0), "K-halves in pass 0 only");
-    static_assert(WT == kQ4_K || (WT == kQ4_0 && HV == 1), "Q4_0 rows in one half");
+    static_assert(WT == kQ4_K || WT == kQ5_K || (WT == kQ4_0 && HV == 1), "Q4_0 rows in one half");
+    // bytes of a 256-column piece of a row (eight Q4_0 blocks are 144, as a
+    // Q4_K superblock)
+    constexpr uint32_t PB = WT == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     __shared__ __attribute__((aligned(16))) uint8_t ring[kMoSlots * kMoSlot + 1024];  // + sink
     // digit build; HV = 2: + the (half, route) x sums and scales from 768
     __shared__ __attribute__((aligned(16))) uint8_t scratch[kMoWaves][HV == 2 ? 1088 : 1024];
@@ -358,7 +368,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const int n = lane & 15, g = lane >> 4, h = (lane >> 4) & 1, tq = lane >> 5;
     const uint32_t part_off = (uint32_t)(G.part_dma * 1024);
     const uint32_t ring_base = (uint32_t)(uintptr_t)(lds_ptr)ring;
-    const uint32_t a_h0 = ring_base + mat * part_off + (rtile * 16 + n) * G.pitch + sb * kQKBlockBytes;
+    const uint32_t a_h0 = ring_base + mat * part_off + (rtile * 16 + n) * G.pitch + sb * PB;
     const uint32_t a_q0 = a_h0 + 16 + 8 * g;
     const i32x4 zero4 = {0, 0, 0, 0};
 
@@ -405,9 +415,12 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 #pragma unroll
         for (int j = 0; j < kMoGroup; j++) {
             const int p = pairs[offsets[it.e] + kMoGroup * it.group + min(j, it.ntok - 1)];
-            if (wv == 0 && lane == 0) gid[j] = p;  // route ids for the reductions
             vrow[j] = MODE == 0 ? p / top_k : p;
         }
+        // route ids for the reductions (lane-indexed: four constant LDS
+        // addresses would each hold a register across the item loop)
+        if (wv == 0 && lane < kMoGroup)
+            gid[lane] = pairs[offsets[it.e] + kMoGroup * it.group + min(lane, it.ntok - 1)];
         // A half at a time (HV = 2: the second half's vectors are loaded once
         // the first half's digits are built, which keeps the registers in
         // bounds; their wait also covers the ring loads issued before them).
@@ -532,19 +545,23 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     int nout = 0;  // buffered results (every wave keeps the same count)
     auto reduce = [&](const Item &it, int buf, int base) {
         if (MODE == 0) {
-            if (lane < it.ntok * 16) {
-                const int tk = lane >> 4, r = lane & 15;
+            // the lane's LDS addresses are formed here, not kept live across
+            // the item loop
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            if (ln < it.ntok * 16) {
+                const int tk = ln >> 4, r = ln & 15;
                 if (r < it.nrows) {
                     // the second half continues the first half's sums
-                    float gs = HV == 2 && it.half == 1 ? hsave[lane][0] : 0.0f;
-                    float us = HV == 2 && it.half == 1 ? hsave[lane][1] : 0.0f;
+                    float gs = HV == 2 && it.half == 1 ? hsave[ln][0] : 0.0f;
+                    float us = HV == 2 && it.half == 1 ? hsave[ln][1] : 0.0f;
                     for (int s = 0; s < G.nsb; s++) {
                         gs += part[buf][tk][s][r];
                         us += part[buf][tk][G.nsb + s][r];
                     }
                     if (HV == 2 && it.half == 0) {  // uniform: no result yet
-                        hsave[lane][0] = gs;
-                        hsave[lane][1] = us;
+                        hsave[ln][0] = gs;
+                        hsave[ln][1] = us;
                         return;
                     }
                     const int p = gid[tk];
@@ -712,23 +729,58 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             }
         } else if (active) {
             u32x4 hv;
-            uint2 q[4];
+            uint2 q[4], qh;
             const uint32_t off = (uint32_t)slot * kMoSlot;
-            asm volatile(
-                "ds_read_b128 %0, %5\n\t"
-                "ds_read_b64 %1, %6\n\t"
-                "ds_read_b64 %2, %6 offset:32\n\t"
-                "ds_read_b64 %3, %6 offset:64\n\t"
-                "ds_read_b64 %4, %6 offset:96\n\t"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(hv), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
-                : "v"(a_h0 + off), "v"(a_q0 + off)
-                : "memory");
+            if constexpr (WT == kQ5_K) {
+                // Q5_K: header, then qh (32 bytes: bit 2c / 2c + 1 of byte i
+                // is the fifth bit of element i of sub-blocks 2c / 2c + 1),
+                // then the quants at + 48
+                asm volatile(
+                    "ds_read_b128 %0, %6\n\t"
+                    "ds_read_b64 %1, %7 offset:32\n\t"
+                    "ds_read_b64 %2, %7 offset:64\n\t"
+                    "ds_read_b64 %3, %7 offset:96\n\t"
+                    "ds_read_b64 %4, %7 offset:128\n\t"
+                    "ds_read_b64 %5, %7\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(hv), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(qh)
+                    : "v"(a_h0 + off), "v"(a_q0 + off)
+                    : "memory");
+            } else {
+                asm volatile(
+                    "ds_read_b128 %0, %5\n\t"
+                    "ds_read_b64 %1, %6\n\t"
+                    "ds_read_b64 %2, %6 offset:32\n\t"
+                    "ds_read_b64 %3, %6 offset:64\n\t"
+                    "ds_read_b64 %4, %6 offset:96\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(hv), "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+                    : "v"(a_h0 + off), "v"(a_q0 + off)
+                    : "memory");
+            }
             i32x4 B[4];
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-                B[c] = i32x4{(int)(q[c].x & 0x0F0F0F0Fu), (int)(q[c].y & 0x0F0F0F0Fu),
-                             (int)((q[c].x >> 4) & 0x0F0F0F0Fu), (int)((q[c].y >> 4) & 0x0F0F0F0Fu)};
+            for (int c = 0; c < 4; c++) {
+                uint32_t l0 = q[c].x & 0x0F0F0F0Fu, l1 = q[c].y & 0x0F0F0F0Fu;
+                uint32_t h0 = (q[c].x >> 4) & 0x0F0F0F0Fu, h1 = (q[c].y >> 4) & 0x0F0F0F0Fu;
+                if constexpr (WT == kQ5_K) {  // codes 0..31
+                    l0 |= ((qh.x >> (2 * c)) & 0x01010101u) << 4;
+                    l1 |= ((qh.y >> (2 * c)) & 0x01010101u) << 4;
+                    h0 |= ((qh.x >> (2 * c + 1)) & 0x01010101u) << 4;
+                    h1 |= ((qh.y >> (2 * c + 1)) & 0x01010101u) << 4;
+                }
+                B[c] = i32x4{(int)l0, (int)l1, (int)h0, (int)h1};
+            }
+            // The plane sums combined (a sub-block's 32 products): exactly in
+            // int32 for Q4_K (|sum q X| <= 32 * 15 * 2^22 < 2^31); in fp32 for
+            // Q5_K, whose 32 * 31 * 2^22 does not fit (two roundings, relative
+            // error under 2^-23).
+            auto plane_sum = [](const i32x4 &Dc) {
+                if constexpr (WT == kQ5_K)
+                    return fmaf((float)Dc[2], 65536.0f, (float)(Dc[0] + 256 * Dc[1]));
+                else
+                    return (float)(int)(((uint32_t)Dc[2] << 16) + (((uint32_t)Dc[1] << 8) + (uint32_t)Dc[0]));
+            };
             const float d = half_bits_to_float_fast(hv.x);
             const float dmin = half_bits_to_float_fast(hv.x >> 16);
             // 6-bit codes (RT/GgufKQuantLayout.java:37-49) of sub-blocks h, 2 + h, 4 + h, 6 + h
@@ -787,16 +839,15 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                     }
                     D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[c], zero4, 0, 0, 0);
                 }
-                int S[4];
+                float S[4];
 #pragma unroll
-                for (int c = 0; c < 4; c++)
-                    S[c] = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
+                for (int c = 0; c < 4; c++) S[c] = plane_sum(D[c]);
                 float v;
                 if (fin) {
                     float qs = 0.0f, mm = 0.0f;
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        qs = fmaf(scf[c], (float)S[c], qs);
+                        qs = fmaf(scf[c], S[c], qs);
                         mm = fmaf(mnf[c], xs4h[c], mm);
                     }
                     v = fmaf(d * xsh, qs, -(dmin * mm));
@@ -806,7 +857,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                     float qs = 0.0f, mm = 0.0f;
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        qs = fmaf(d * scf[c], xsh * (float)S[c], qs);
+                        qs = fmaf(d * scf[c], xsh * S[c], qs);
                         mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4h[c], mm);
                     }
                     v = qs - mm;
@@ -832,16 +883,15 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 i32x4 D[4];
 #pragma unroll
                 for (int c = 0; c < 4; c++) D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[pp][c], B[c], zero4, 0, 0, 0);
-                int S[4];
+                float S[4];
 #pragma unroll
-                for (int c = 0; c < 4; c++)
-                    S[c] = (int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
+                for (int c = 0; c < 4; c++) S[c] = plane_sum(D[c]);
                 float v;
                 if (fin) {
                     float qs = 0.0f, mm = 0.0f;
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        qs = fmaf(scf[c], (float)S[c], qs);
+                        qs = fmaf(scf[c], S[c], qs);
                         mm = fmaf(mnf[c], xs4[pp][c], mm);
                     }
                     v = fmaf(d * xs[pp], qs, -(dmin * mm));
@@ -851,7 +901,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                     float qs = 0.0f, mm = 0.0f;
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        qs = fmaf(d * scf[c], xs[pp] * (float)S[c], qs);
+                        qs = fmaf(d * scf[c], xs[pp] * S[c], qs);
                         mm = fmaf(mnf[c] != 0.0f ? dmin * mnf[c] : 0.0f, xs4[pp][c], mm);
                     }
                     v = qs - mm;
@@ -1390,22 +1440,36 @@ __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
 
 namespace {
 
-MoeTileGeom make_geom(int mode, int E, int H, int I) {
+// Bytes of a row's 256-column piece: a Q4_K superblock (144, as eight Q4_0
+// blocks) or a Q5_K superblock (176).
+constexpr uint32_t piece_bytes(int type) { return type == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes; }
+
+// Geometry of pass `mode` over rows of `pb`-byte pieces.  The caller has
+// checked that H and I are multiples of 256 in [256, 4096].
+MoeTileGeom make_geom(int mode, int E, int H, int I, uint32_t pb) {
     MoeTileGeom g{};
     const int K = mode == 0 ? H : I;
-    // Gate/up items hold 16 rows of both matrices over at most 8
-    // superblocks: longer rows (an even count up to 16) are cut in halves.
-    g.halves = mode == 0 && K / kQK > 8 ? 2 : 1;
+    // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all banks
+    auto pitch_of = [pb](int nsb) {
+        const uint32_t rb = (uint32_t)nsb * pb;
+        return (rb / 16) % 2 == 1 ? rb : rb + 16;
+    };
+    auto part_dma_of = [&](int nsb, int rt) { return (16 * rt * (int)pitch_of(nsb) + 1023) / 1024; };
+    // Gate/up items hold 16 rows of both matrices, one wave per superblock
+    // and matrix (so at most 8 superblocks), both within a slot: longer rows
+    // (an even count of superblocks) are cut in halves.
+    g.halves = mode == 0 && (K / kQK > 8 || 2 * part_dma_of(K / kQK, 1) > kMoMaxDma) ? 2 : 1;
     g.nsb = K / kQK / g.halves;
     g.rows_e = mode == 0 ? I : H;
+    // Down items: as many 16-row tiles as waves (one per tile and
+    // superblock, at most 8 tiles) and a slot take.
     g.rt = mode == 0 ? 1 : min(16 / g.nsb, 8);
+    while (g.rt > 1 && part_dma_of(g.nsb, g.rt) > kMoMaxDma) g.rt--;
     g.tiles_e = g.halves * ((g.rows_e + 16 * g.rt - 1) / (16 * g.rt));
-    g.row_bytes = (uint32_t)(g.nsb * kQKBlockBytes);
+    g.row_bytes = (uint32_t)g.nsb * pb;
     g.stride = (uint32_t)(g.halves * g.row_bytes);
-    // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all banks
-    g.pitch = ((g.row_bytes / 16) % 2 == 1) ? g.row_bytes : g.row_bytes + 16;
-    const int part_bytes = 16 * g.rt * (int)g.pitch;
-    g.part_dma = (part_bytes + 1023) / 1024;
+    g.pitch = pitch_of(g.nsb);
+    g.part_dma = part_dma_of(g.nsb, g.rt);
     g.ndma = mode == 0 ? 2 * g.part_dma : g.part_dma;
     g.vec_len = K;
     g.out_len = g.rows_e;
@@ -1432,57 +1496,78 @@ bool make_down_geom(int E, int H, int I, int T, int top_k, bool q6, MoeDownGeom 
     return waves >= 1;
 }
 
+// Shapes every tile pass takes: hidden and inter multiples of 256 up to
+// 4096, the routing tables in LDS, x 16-byte aligned (nullptr: shape only).
+bool tile_shape_ok(int E, int H, int I, int P, const float *x) {
+    return H >= kQK && I >= kQK && H % kQK == 0 && I % kQK == 0 && H <= 16 * kQK && I <= 16 * kQK &&
+           E <= kMoMaxExperts && P <= kMoMaxRoutes && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+// Whether pass `mode` over `type` rows fits the kernel (after tile_shape_ok).
+bool tile_pass_ok(int mode, int E, int H, int I, int type) {
+    const MoeTileGeom g = make_geom(mode, E, H, I, piece_bytes(type));
+    if (g.halves == 2 && ((mode == 0 ? H : I) / kQK) % 2 != 0) return false;  // halves of equal length
+    if ((mode == 0 ? 2 * g.nsb : g.rt * g.nsb) > kMoWaves) return false;
+    return g.ndma <= kMoMaxDma && g.w_bytes < (int64_t)kMaskedOffset && 2 * kMoGroup * 16 * g.rt <= kMoOutCap;
+}
+
+// The token-major down pass takes Q4_K and Q6_K rows where its geometry fits.
+bool token_major_down(int down_type, int E, int H, int I, int T, int top_k, MoeDownGeom &gd, int &waves) {
+    return (down_type == kQ4_K || down_type == kQ6_K) &&
+           make_down_geom(E, H, I, T, top_k, down_type == kQ6_K, gd, waves);
+}
+
 }  // namespace
 
-bool moe_q4k_mfma_supported(int E, int H, int I, int P, const float *x) {
-    if (H % kQK != 0 || I % kQK != 0 || H > 16 * kQK || I > 16 * kQK) return false;
-    if (H > 8 * kQK && (H / kQK) % 2 != 0) return false;  // halves of equal length
-    if (E > kMoMaxExperts || P > kMoMaxRoutes) return false;
-    if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return false;  // (nullptr: shape only)
-    for (int mode = 0; mode < 2; mode++) {
-        const MoeTileGeom g = make_geom(mode, E, H, I);
-        if (g.ndma > kMoMaxDma || g.w_bytes >= (int64_t)kMaskedOffset) return false;
-        if (2 * kMoGroup * 16 * g.rt > kMoOutCap) return false;
-    }
-    return true;
+bool moe_kq_mfma_supported(int gate_type, int down_type, int E, int H, int I, int T, int top_k,
+                           const float *x) {
+    if (gate_type != kQ4_K && gate_type != kQ5_K) return false;
+    if (!tile_shape_ok(E, H, I, T * top_k, x) || !tile_pass_ok(0, E, H, I, gate_type)) return false;
+    MoeDownGeom gd;
+    int waves = 0;
+    if (token_major_down(down_type, E, H, I, T, top_k, gd, waves)) return true;
+    return (down_type == kQ4_K || down_type == kQ5_K) && tile_pass_ok(1, E, H, I, down_type);
 }
 
 bool moe_q40_mfma_supported(int E, int H, int I, int P, const float *x) {
     // gate / up rows in one half (hidden up to 2048)
-    return H <= 8 * kQK && moe_q4k_mfma_supported(E, H, I, P, x);
+    return H <= 8 * kQK && tile_shape_ok(E, H, I, P, x) && tile_pass_ok(0, E, H, I, kQ4_0) &&
+           tile_pass_ok(1, E, H, I, kQ4_0);
 }
 
-bool moe_q6k_down_supported(int E, int H, int I, int T, int top_k) {
-    MoeDownGeom g;
-    int waves = 0;
-    return moe_q4k_mfma_supported(E, H, I, T * top_k, nullptr) && make_down_geom(E, H, I, T, top_k, true, g, waves);
-}
-
-// Gate/up then down: with the token-major down pass (I <= 1024) two
-// launches, h as digit records; otherwise gate/up, the expert-major down
-// pass and the combine.  Each pass routes in LDS first.  The caller has
-// checked moe_q4k_mfma_supported (and, for Q6_K down rows,
-// moe_q6k_down_supported).
-hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
-                               int H, int I, const float *x, const int32_t *ids, const float *wts,
-                               int T, int top_k, float *out, uint8_t *ws, hipStream_t stream,
-                               int down_type) {
-    const bool q6 = down_type == kQ6_K;
+// Gate/up then down: with the token-major down pass two launches, h as
+// digit records; otherwise gate/up, the expert-major down pass and the
+// combine.  Each pass routes in LDS first.  The caller has checked
+// moe_kq_mfma_supported.
+hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate, const uint8_t *up,
+                              const uint8_t *down, int E, int H, int I, const float *x, const int32_t *ids,
+                              const float *wts, int T, int top_k, float *out, uint8_t *ws, hipStream_t stream) {
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
-    const MoeTileGeom g0 = make_geom(0, E, H, I), g1 = make_geom(1, E, H, I);
+    const MoeTileGeom g0 = make_geom(0, E, H, I, piece_bytes(gate_type));
     const unsigned grid = (unsigned)device_cus();
     float *hbuf = reinterpret_cast<float *>(ws + L.h);
     // h records (P I 3.5 bytes) fit the fp32 h region.
     MoeDownGeom gd;
     int waves = 0;
-    if (make_down_geom(E, H, I, T, top_k, q6, gd, waves)) {
-        if (g0.halves == 2)
-            hipLaunchKernelGGL((moe_expert_tile_kernel<0, true, 2>), dim3(grid), dim3(kMoThreads), 0, stream, gate,
-                               up, g0, x, top_k, ids, wts, E, P, hbuf);
-        else
-            hipLaunchKernelGGL((moe_expert_tile_kernel<0, true>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
-                               g0, x, top_k, ids, wts, E, P, hbuf);
+    const bool rec = token_major_down(down_type, E, H, I, T, top_k, gd, waves);
+    if (!rec && down_type != kQ4_K && down_type != kQ5_K) return hipErrorNotSupported;
+    auto gate_up = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0, x, top_k, ids, wts, E, P,
+                           hbuf);
+    };
+    switch ((gate_type == kQ5_K ? 4 : 0) + (rec ? 2 : 0) + (g0.halves == 2 ? 1 : 0)) {
+    case 0: gate_up(&moe_expert_tile_kernel<0, false, 1, kQ4_K>); break;
+    case 1: gate_up(&moe_expert_tile_kernel<0, false, 2, kQ4_K>); break;
+    case 2: gate_up(&moe_expert_tile_kernel<0, true, 1, kQ4_K>); break;
+    case 3: gate_up(&moe_expert_tile_kernel<0, true, 2, kQ4_K>); break;
+    case 4: gate_up(&moe_expert_tile_kernel<0, false, 1, kQ5_K>); break;
+    case 5: gate_up(&moe_expert_tile_kernel<0, false, 2, kQ5_K>); break;
+    case 6: gate_up(&moe_expert_tile_kernel<0, true, 1, kQ5_K>); break;
+    default: gate_up(&moe_expert_tile_kernel<0, true, 2, kQ5_K>); break;
+    }
+    if (rec) {
+        const bool q6 = down_type == kQ6_K;
         const dim3 dgrid((unsigned)(H / 16), (unsigned)((T + gd.tg - 1) / gd.tg));
         const size_t lds = 1024 + (size_t)waves * gd.wave_bytes;
         const uint8_t *hrec = ws + L.h;
@@ -1507,16 +1592,14 @@ hipError_t launch_moe_q4k_mfma(const uint8_t *gate, const uint8_t *up, const uin
         default: return run(&moe_down_combine_kernel<4, true>);
         }
     }
-    if (q6) return hipErrorNotSupported;  // only the token-major down pass reads Q6_K rows
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
-    if (g0.halves == 2)
-        hipLaunchKernelGGL((moe_expert_tile_kernel<0, false, 2>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up,
-                           g0, x, top_k, ids, wts, E, P, hbuf);
+    const MoeTileGeom g1 = make_geom(1, E, H, I, piece_bytes(down_type));
+    if (down_type == kQ5_K)
+        hipLaunchKernelGGL((moe_expert_tile_kernel<1, false, 1, kQ5_K>), dim3(grid), dim3(kMoThreads), 0, stream,
+                           down, (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
     else
-        hipLaunchKernelGGL((moe_expert_tile_kernel<0, false>), dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0,
-                           x, top_k, ids, wts, E, P, hbuf);
-    hipLaunchKernelGGL((moe_expert_tile_kernel<1, false>), dim3(grid), dim3(kMoThreads), 0, stream, down,
-                       (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
+        hipLaunchKernelGGL((moe_expert_tile_kernel<1, false, 1, kQ4_K>), dim3(grid), dim3(kMoThreads), 0, stream,
+                           down, (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_moe_combine(ids, wts, ypair, T, top_k, H, E, out, stream);
@@ -1530,7 +1613,7 @@ hipError_t launch_moe_q40_mfma(const uint8_t *gate, const uint8_t *up, const uin
                                uint8_t *ws, hipStream_t stream) {
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
-    const MoeTileGeom g0 = make_geom(0, E, H, I), g1 = make_geom(1, E, H, I);
+    const MoeTileGeom g0 = make_geom(0, E, H, I, kQKBlockBytes), g1 = make_geom(1, E, H, I, kQKBlockBytes);
     const unsigned grid = (unsigned)device_cus();
     float *hbuf = reinterpret_cast<float *>(ws + L.h);
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);

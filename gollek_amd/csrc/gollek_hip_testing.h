@@ -12,9 +12,9 @@
  *                   3 = Q4_K with K <= 4096 always on the shared-tile
  *                   matrix-core kernel; 4 = Q8_0 / Q4_0 on the buffer->LDS
  *                   ring kernels and Q5_K / Q6_K on the fp32 kernel.
- *   "moe_variant":  0 = automatic; 1 = all-Q4_K experts on the v_dot4 passes
- *                   and all-Q4_0 experts on the fp32 row kernels instead of
- *                   the matrix-core passes.
+ *   "moe_variant":  0 = automatic; 1 = no matrix-core passes: all-Q4_K
+ *                   experts on the v_dot4 passes, every other type on the
+ *                   row kernels.
  * Unknown keys -> GOLLEK_HIP_ERR_ARG.
  */
 #ifndef GOLLEK_HIP_TESTING_H

@@ -80,14 +80,41 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
         t.close()
 
 
+# Q5_K gate / up on the matrix-core passes (Q5_K_M / Q5_K_S layers): hidden
+# 2048 and 3072 cut into K-halves of 4 and 6 superblocks (a 176-byte
+# superblock fills an item slot sooner than a 144-byte one), 1536 and 512 in
+# one half; down rows Q6_K / Q4_K on the token-major pass, Q5_K on the
+# expert-major pass (2 to 8 row tiles per item); Q4_K gate / up with Q5_K
+# down; the even split at 300 tokens x top-2.
+@pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
+    (syn.Q5_K, syn.Q6_K, 128, 2048, 768, 16, 8), (syn.Q5_K, syn.Q5_K, 128, 2048, 768, 16, 8),
+    (syn.Q5_K, syn.Q4_K, 16, 1536, 512, 9, 4), (syn.Q5_K, syn.Q5_K, 8, 3072, 1536, 9, 2),
+    (syn.Q5_K, syn.Q5_K, 32, 512, 256, 300, 2), (syn.Q4_K, syn.Q5_K, 16, 1024, 1280, 9, 4),
+    (syn.Q5_K, syn.Q6_K, 8, 2048, 1024, 40, 2)])
+def test_moe_q5_k_parity(gt, dt, E, H, I, T, k):
+    print(f"[gpu] moe q5_k gate={gt} down={dt} E={E} H={H} I={I} T={T} k={k}", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + I + 2, down_type=dt, gate_type=gt)
+    ids, w = syn.moe_routing(T, E, k, seed=7)
+    x = syn.activation(T * H, seed=8).reshape(T, H)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=gt)
+    err = o.rel_err(out, ref)
+    print(f"[gpu] moe q5_k rel_err={err:.3e}", flush=True)
+    assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
 # All-Q4_0 experts up to hidden 2048 take the matrix-core passes with Q4_0
 # rows (odd and even superblock counts, inter up to 4096, many routes).
 # Expert types and shapes the matrix-core passes do not take: Q8_0 / Q4_0
 # gate and up or down on the fp32 row kernels (rows of 3 to 448 blocks, 8 to
 # 64 lanes per row, route groups limited by LDS, experts with many routes),
-# Q5_K / Q6_K gate and up and Q5_K down on the generic passes, and Q6_K down
-# beyond the token-major down pass (inter above 1024, hidden past 2048 with
-# an odd superblock count, more than 2048 routes).
+# Q6_K gate and up on the K-quant row kernels, mixed gate / up types, Q5_K
+# gate / up past what an item slot holds (hidden 4096: halves of 8
+# superblocks; 1792: an odd count), and Q6_K down beyond the token-major down
+# pass (inter above 1024, hidden past 2048 with an odd superblock count, more
+# than 2048 routes).
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q8_0, syn.Q8_0, 128, 2048, 768, 16, 8), (syn.Q4_0, syn.Q4_0, 128, 2048, 768, 16, 8),
     (syn.Q4_0, syn.Q4_0, 4, 512, 14336, 12, 2), (syn.Q8_0, syn.Q8_0, 2, 4096, 1024, 20, 2),
@@ -97,7 +124,8 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
     (syn.Q4_K, syn.Q5_K, 8, 512, 256, 5, 2), (syn.Q5_K, syn.Q4_K, 8, 512, 256, 5, 2),
     (syn.Q6_K, syn.Q6_K, 8, 512, 256, 5, 2), (syn.Q4_K, syn.Q8_0, 8, 512, 256, 5, 2),
     (syn.Q4_K, syn.Q6_K, 4, 512, 1280, 6, 2), (syn.Q4_K, syn.Q6_K, 4, 2304, 256, 6, 2),
-    (syn.Q4_K, syn.Q6_K, 16, 512, 256, 300, 8), (syn.Q8_0, syn.Q4_0, 8, 96, 160, 5, 2)])
+    (syn.Q4_K, syn.Q6_K, 16, 512, 256, 300, 8), (syn.Q8_0, syn.Q4_0, 8, 96, 160, 5, 2),
+    (syn.Q5_K, syn.Q6_K, 4, 4096, 512, 6, 2), (syn.Q5_K, syn.Q5_K, 4, 1792, 512, 6, 2)])
 def test_moe_other_types_parity(gt, dt, E, H, I, T, k):
     print(f"[gpu] moe types gate={gt} down={dt} E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + I, down_type=dt, gate_type=gt)
@@ -120,14 +148,15 @@ def moe_variant():
     ops.set_option("moe_variant", 0)
 
 
-def test_moe_q4_0_matrix_core_equals_row_kernels(moe_variant):
-    # All-Q4_0 experts: the matrix-core passes (22-bit x digits) against the
-    # fp32 row kernels (moe_variant 1), both against the oracle.
+@pytest.mark.parametrize("gt,dt", [(syn.Q4_0, syn.Q4_0), (syn.Q5_K, syn.Q6_K), (syn.Q5_K, syn.Q5_K)])
+def test_moe_matrix_core_equals_row_kernels(gt, dt, moe_variant):
+    # All-Q4_0 and Q5_K experts: the matrix-core passes (22-bit x digits)
+    # against the fp32 row kernels (moe_variant 1), both against the oracle.
     E, H, I, T, k = 32, 2048, 768, 16, 8
-    gate, up, down, tg, tu, td = _experts(E, H, I, seed=21, down_type=syn.Q4_0, gate_type=syn.Q4_0)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=21, down_type=dt, gate_type=gt)
     ids, w = syn.moe_routing(T, E, k, seed=22)
     x = syn.activation(T * H, seed=23).reshape(T, H)
-    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=syn.Q4_0, gate_type=syn.Q4_0)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=gt)
     out_mc = ops.moe_grouped(tg, tu, td, E, x, ids, w)
     moe_variant(1)
     out_rows = ops.moe_grouped(tg, tu, td, E, x, ids, w)
