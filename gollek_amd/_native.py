@@ -66,6 +66,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                     _SZ]),
     "gollek_hip_moe_block_device": (_I32, [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I32, _P, _P, _P,
                                            _P, _I64, _P, _CHARP, _SZ]),
+    "gollek_hip_moe_shared_expert": (_I32, [_P, _P, _P, _P, _P, _I64, _P, _I64, _CHARP, _SZ]),
+    "gollek_hip_moe_shared_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "gollek_hip_moe_shared_expert_device": (_I32, [_P, _P, _P, _P, _P, _I64, _P, _P, _I64, _P, _CHARP,
+                                                   _SZ]),
     "gollek_hip_gguf_open": (_P, [_CHARP, _CHARP, _SZ]),
     "gollek_hip_gguf_close": (None, [_P]),
     "gollek_hip_gguf_info": (_I32, [_P, _P, _P, _P, _P, _P, _P]),

@@ -929,6 +929,82 @@ int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
     return GOLLEK_HIP_OK;
 }
 
+int64_t gollek_hip_moe_shared_workspace_bytes(int64_t tokens, int64_t hidden, int64_t inter) {
+    if (tokens < 0 || hidden <= 0 || inter <= 0) return -1;
+    return (int64_t)gollek::moe_shared_layout(tokens, hidden, inter).total;
+}
+
+int32_t gollek_hip_moe_shared_expert_device(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                            gollek_hip_weight *down, const float *gate_inp, const float *x,
+                                            int64_t tokens, float *out, void *workspace,
+                                            int64_t workspace_bytes, void *stream, char *err,
+                                            size_t err_len) {
+    MoeShape sh;
+    int32_t rc = check_moe(gate, up, down, 1, tokens, 1, &sh, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    if (x == nullptr || out == nullptr || workspace == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "shared expert buffers");
+    const int64_t need = gollek_hip_moe_shared_workspace_bytes(tokens, sh.H, sh.I);
+    if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len,
+                    "Workspace of %lld bytes (256-byte aligned) needed, got %lld",
+                    (long long)need, (long long)workspace_bytes);
+    const hipError_t e = gollek::launch_moe_shared(
+        gate->type_id, up->type_id, down->type_id, gate->data, up->data, down->data, gate->row_bytes,
+        up->row_bytes, down->row_bytes, sh.H, sh.I, x, gate_inp, (int)tokens, out,
+        static_cast<uint8_t *>(workspace), static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "shared expert launch", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
+int32_t gollek_hip_moe_shared_expert(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                     gollek_hip_weight *down, const float *gate_inp, const float *x,
+                                     int64_t tokens, float *out, int64_t out_len, char *err,
+                                     size_t err_len) {
+    MoeShape sh;
+    int32_t rc = check_moe(gate, up, down, 1, tokens, 1, &sh, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    if (x == nullptr || out == nullptr)
+        return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "shared expert buffers");
+    if (out_len < tokens * sh.H)
+        return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Output length %lld is smaller than %lld x %d",
+                    (long long)out_len, (long long)tokens, sh.H);
+    if (tokens == 0) {
+        ok(err, err_len);
+        return GOLLEK_HIP_OK;
+    }
+    std::lock_guard<std::mutex> lock(gate->mu);
+    rc = use_device(gate->device, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    const size_t xn = (size_t)(tokens * sh.H) * 4, gn = (size_t)sh.H * 4;
+    const size_t xb = align_up(xn, 256), gb = align_up(gn, 256);
+    const size_t ws = (size_t)gollek_hip_moe_shared_workspace_bytes(tokens, sh.H, sh.I);
+    rc = ensure_staging(gate, 2 * xb + gb + ws, err, err_len);
+    if (rc != GOLLEK_HIP_OK) return rc;
+    uint8_t *base = gate->staging;
+    float *d_x = reinterpret_cast<float *>(base);
+    float *d_out = reinterpret_cast<float *>(base + xb);
+    float *d_gi = gate_inp != nullptr ? reinterpret_cast<float *>(base + 2 * xb) : nullptr;
+    hipStream_t s = gate->stream;
+    hipError_t e = hipMemcpyAsync(d_x, x, xn, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d_out, out, xn, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && d_gi != nullptr) e = hipMemcpyAsync(d_gi, gate_inp, gn, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = gollek::launch_moe_shared(gate->type_id, up->type_id, down->type_id, gate->data, up->data, down->data,
+                                      gate->row_bytes, up->row_bytes, down->row_bytes, sh.H, sh.I, d_x, d_gi,
+                                      (int)tokens, d_out, base + 2 * xb + gb, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, d_out, xn, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "shared expert", err, err_len);
+    ok(err, err_len);
+    return GOLLEK_HIP_OK;
+}
+
 }  // extern "C"
 
 // ---- MoE router ---------------------------------------------------------

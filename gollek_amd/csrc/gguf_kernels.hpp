@@ -133,6 +133,17 @@ hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *
                       const uint8_t *down, int64_t gate_row_bytes, int64_t up_row_bytes,
                       int64_t down_row_bytes, int E, int H, int I, const float *x, const int32_t *ids,
                       const float *wts, int T, int top_k, float *out, uint8_t *ws, hipStream_t stream);
+// The shared expert (gguf_moe.hip): out[t] += g_t * ffn(x_t) over one
+// expert of `inter` rows, g_t from the gate_inp row (nullptr: 1); ws holds
+// moe_shared_layout(...).total bytes (y, the routes, the FFN's workspace).
+struct MoeSharedLayout {
+    size_t y, ids, wts, ffn, total;
+};
+MoeSharedLayout moe_shared_layout(int64_t tokens, int64_t hidden, int64_t inter);
+hipError_t launch_moe_shared(int gate_type, int up_type, int down_type, const uint8_t *gate, const uint8_t *up,
+                             const uint8_t *down, int64_t gate_row_bytes, int64_t up_row_bytes,
+                             int64_t down_row_bytes, int H, int I, const float *x, const float *gate_inp, int T,
+                             float *out, uint8_t *ws, hipStream_t stream);
 hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                                int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                                const float *x, const int32_t *ids, const float *wts, int T, int top_k,

@@ -284,6 +284,46 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *__restr
     out[i] = acc;
 }
 
+// The shared expert's routes: every token to expert 0 with weight 1.
+__global__ __launch_bounds__(256) void moe_shared_routes_kernel(int32_t *__restrict__ ids,
+                                                                float *__restrict__ wts, int T) {
+    const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (t < T) {
+        ids[t] = 0;
+        wts[t] = 1.0f;
+    }
+}
+
+// The shared expert added after token t's routes (MoeForwardPass.java:240-247):
+// out[t] = out[t] + g * y[t], the product rounded first (AccelOps.mulScalar,
+// then addToTokenRow).  g = 1 / (1 + (float)exp(-s)) in float with exp in
+// double (resolveSharedExpertGate, :428-442), s = x_t . gate_inp rounded
+// to float (the sum in fp64, whose products of two floats are exact); g = 1
+// without gate_inp.  One workgroup per token.
+__global__ __launch_bounds__(256) void moe_shared_add_kernel(const float *__restrict__ x,
+                                                             const float *__restrict__ gate_inp,
+                                                             const float *__restrict__ y, int H,
+                                                             float *__restrict__ out) {
+#pragma clang fp contract(off)
+    __shared__ double part[4];
+    const int t = (int)blockIdx.x;
+    const int64_t row = (int64_t)t * H;
+    float g = 1.0f;
+    if (gate_inp != nullptr) {  // uniform
+        double s = 0.0;
+        for (int i = (int)threadIdx.x; i < H; i += 256) s += (double)x[row + i] * (double)gate_inp[i];
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+        __syncthreads();
+        const float sf = (float)(((part[0] + part[1]) + part[2]) + part[3]);
+        g = 1.0f / (1.0f + (float)exp((double)(-sf)));
+    }
+    for (int i = (int)threadIdx.x; i < H; i += 256) {
+        const float scaled = g * y[row + i];
+        out[row + i] = out[row + i] + scaled;
+    }
+}
+
 // Any expert types (Q8_0, Q4_0, Q4_K, Q5_K, Q6_K), any alignment: rows
 // [r0, r0 + rows_per_block) of expert e against each of the expert's
 // vectors, one wave per row and one lane per block (fp32, byte loads).
@@ -788,6 +828,37 @@ hipError_t launch_moe_combine(const int32_t *ids, const float *wts, const float 
     const int64_t total = (int64_t)T * H;
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        stream, ids, wts, ypair, T, top_k, H, E, out);
+    return hipGetLastError();
+}
+
+MoeSharedLayout moe_shared_layout(int64_t tokens, int64_t hidden, int64_t inter) {
+    auto up256 = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    MoeSharedLayout L;
+    L.y = 0;
+    L.ids = up256((size_t)(tokens * hidden) * 4);
+    L.wts = L.ids + up256((size_t)tokens * 4);
+    L.ffn = L.wts + up256((size_t)tokens * 4);
+    L.total = L.ffn + moe_layout(tokens, 1, hidden, inter, 1).total;
+    return L;
+}
+
+hipError_t launch_moe_shared(int gate_type, int up_type, int down_type, const uint8_t *gate, const uint8_t *up,
+                             const uint8_t *down, int64_t gate_row_bytes, int64_t up_row_bytes,
+                             int64_t down_row_bytes, int H, int I, const float *x, const float *gate_inp, int T,
+                             float *out, uint8_t *ws, hipStream_t stream) {
+    const MoeSharedLayout L = moe_shared_layout(T, H, I);
+    float *y = reinterpret_cast<float *>(ws + L.y);
+    int32_t *ids = reinterpret_cast<int32_t *>(ws + L.ids);
+    float *wts = reinterpret_cast<float *>(ws + L.wts);
+    hipLaunchKernelGGL(moe_shared_routes_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, stream, ids, wts,
+                       T);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // y[t] = 0 + 1 * ffn(x_t): the expert's output exactly
+    e = launch_moe(gate_type, up_type, down_type, gate, up, down, gate_row_bytes, up_row_bytes, down_row_bytes, 1,
+                   H, I, x, ids, wts, T, 1, y, ws + L.ffn, stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(moe_shared_add_kernel, dim3((unsigned)T), dim3(256), 0, stream, x, gate_inp, y, H, out);
     return hipGetLastError();
 }
 

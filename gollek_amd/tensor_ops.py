@@ -505,8 +505,8 @@ def moe_select_topk(logits, top_k: int, scoring: int):
 def moe_block(gate: GgufTensor, up: GgufTensor, down: GgufTensor, n_experts: int, x, logits,
               top_k: int, scoring: int) -> np.ndarray:
     """The routed MoE block (MoeForwardPass.java:174-240 after the router
-    linear): router on `logits`, then the grouped expert FFN (Q4_K gate / up,
-    Q4_K or Q6_K down)."""
+    linear): router on `logits`, then the grouped expert FFN (expert types as
+    moe_grouped)."""
     for name, t in (("gate", gate), ("up", up), ("down", down)):
         if t is None:
             raise NullPointerError(name)
@@ -533,4 +533,44 @@ def moe_block_device(gate: DeviceWeight, up: DeviceWeight, down: DeviceWeight, n
                                          V(x_ptr), V(logits_ptr), tokens, top_k, scoring,
                                          V(ids_ptr), V(w_ptr), V(out_ptr), V(ws_ptr), ws_bytes,
                                          V(stream), err.buf, err.size)
+    check(rc, err)
+
+
+def moe_shared_expert(gate: GgufTensor, up: GgufTensor, down: GgufTensor, x, out,
+                      gate_inp=None) -> np.ndarray:
+    """The shared expert added to the routed output `out` (MoeForwardPass.java:
+    240-247, runSharedExpert :418-426, resolveSharedExpertGate :428-442):
+    out[t] + g_t * down(silu(gate x_t) * (up x_t)) with g_t = sigmoid(x_t .
+    gate_inp) (1 without gate_inp).  Returns the new output; `out` is not
+    modified."""
+    for name, t in (("gate", gate), ("up", up), ("down", down)):
+        if t is None:
+            raise NullPointerError(name)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    res = np.array(out, dtype=np.float32, order="C", copy=True)
+    gi = None if gate_inp is None else np.ascontiguousarray(gate_inp, dtype=np.float32)
+    lib = _native.load()
+    err = _native.ErrBuf()
+    V = ctypes.c_void_p
+    check(lib.gollek_hip_moe_shared_expert(gate.handle(), up.handle(), down.handle(),
+                                           V(None) if gi is None else V(gi.ctypes.data),
+                                           V(xv.ctypes.data), xv.shape[0], V(res.ctypes.data),
+                                           res.size, err.buf, err.size), err)
+    return res
+
+
+def moe_shared_workspace_bytes(tokens: int, hidden: int, inter: int) -> int:
+    return int(_native.load().gollek_hip_moe_shared_workspace_bytes(tokens, hidden, inter))
+
+
+def moe_shared_expert_device(gate: DeviceWeight, up: DeviceWeight, down: DeviceWeight,
+                             gate_inp_ptr: int, x_ptr: int, tokens: int, out_ptr: int, ws_ptr: int,
+                             ws_bytes: int, stream: int = 0) -> None:
+    lib = _native.load()
+    err = _native.ErrBuf()
+    V = ctypes.c_void_p
+    rc = lib.gollek_hip_moe_shared_expert_device(gate.handle, up.handle, down.handle,
+                                                 V(gate_inp_ptr or None), V(x_ptr), tokens,
+                                                 V(out_ptr), V(ws_ptr), ws_bytes, V(stream),
+                                                 err.buf, err.size)
     check(rc, err)

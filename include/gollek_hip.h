@@ -288,8 +288,8 @@ int32_t gollek_hip_moe_select_topk_device(const float *logits, int64_t tokens, i
 /* The routed MoE block: gollek_hip_moe_select_topk on `logits` followed by
  * gollek_hip_moe_grouped with the ids and weights it chose, on one stream
  * (MoeForwardPass.java:174-240 after the router linear).  The shared expert
- * (:240-247) is a plain SwiGLU FFN the caller adds.  Checks of both calls
- * apply. */
+ * (:240-247) follows with gollek_hip_moe_shared_expert on the same `out`.
+ * Checks of both calls apply. */
 int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
                              gollek_hip_weight *down, int64_t n_experts, const float *x,
                              int64_t tokens, const float *logits, int64_t top_k, int32_t scoring,
@@ -303,6 +303,31 @@ int32_t gollek_hip_moe_block_device(gollek_hip_weight *gate, gollek_hip_weight *
                                     int32_t scoring, int32_t *ids, float *weights, float *out,
                                     void *workspace, int64_t workspace_bytes, void *stream,
                                     char *err, size_t err_len);
+
+/* The shared expert, added to the routed output of the same tokens
+ * (SFE/generation/moe/MoeForwardPass.java:240-247 with runSharedExpert
+ * :418-426 and resolveSharedExpertGate :428-442): for each token t
+ *   out[t] = out[t] + g_t * y_t   (the product rounded, then the sum),
+ *   y_t = down(silu(gate x_t) * (up x_t)),
+ *   g_t = 1 / (1 + (float)exp(-s_t)) with exp in double, s_t = x_t . gate_inp
+ *         rounded to float (gate_inp: `hidden` floats, the shared_expert_gate
+ *         row); g_t = 1 when gate_inp is NULL (the reference's missing gate).
+ * gate / up: inter x hidden, down: hidden x inter, of any types
+ * gollek_hip_moe_grouped takes.  Errors as gollek_hip_moe_grouped with one
+ * expert (x and out NULL -> NULL; out_len < tokens * hidden -> ARG). */
+int32_t gollek_hip_moe_shared_expert(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                     gollek_hip_weight *down, const float *gate_inp, const float *x,
+                                     int64_t tokens, float *out, int64_t out_len, char *err,
+                                     size_t err_len);
+/* Device workspace bytes gollek_hip_moe_shared_expert_device needs. */
+int64_t gollek_hip_moe_shared_workspace_bytes(int64_t tokens, int64_t hidden, int64_t inter);
+/* Device variant (x, gate_inp, out on the device; `workspace` as for
+ * gollek_hip_moe_grouped_device, >= gollek_hip_moe_shared_workspace_bytes). */
+int32_t gollek_hip_moe_shared_expert_device(gollek_hip_weight *gate, gollek_hip_weight *up,
+                                            gollek_hip_weight *down, const float *gate_inp, const float *x,
+                                            int64_t tokens, float *out, void *workspace,
+                                            int64_t workspace_bytes, void *stream, char *err,
+                                            size_t err_len);
 
 /* ---- GGUF files --------------------------------------------------------- */
 /* GC/ = runner/gguf/gollek-gguf-core/src/main/java/tech/kayys/gollek/gguf/. */

@@ -16,6 +16,9 @@ HIP library; it is not a fallback for it.
     gollek/safetensor/engine/generation/moe/MoeForwardPass.java:217-240,
     :461-472) with swigluFfn = down(silu(gate x) * up x)
     (.../engine/forward/DirectForwardFfnService.java:40-61).
+  * moe_shared_expert_reference: the shared expert added after the routes
+    (MoeForwardPass.java:240-247, runSharedExpert :418-426,
+    resolveSharedExpertGate :428-442).
   * rel_err: the tolerance metric, max_i |y_i - r_i| / max(|r_i|, 1e-3 ||r||_inf).
 """
 from __future__ import annotations
@@ -262,6 +265,35 @@ def moe_reference_q4k(gate: np.ndarray, up: np.ndarray, down: np.ndarray, n_expe
             h = silu(g @ xt) * (u @ xt)
             out[t] += wj * (d @ h)
     return out
+
+
+def shared_expert_gate(x_t: np.ndarray, gate_inp) -> np.float32:
+    """resolveSharedExpertGate (MoeForwardPass.java:428-442): 1 without the
+    gate row, else 1.0f / (1.0f + (float)Math.exp(-s)) in float with exp in
+    double, s = x_t . gate_inp as a float (here the exact dot rounded once)."""
+    if gate_inp is None:
+        return np.float32(1.0)
+    s = np.float32(np.dot(np.asarray(x_t, np.float64), np.asarray(gate_inp, np.float64)))
+    with np.errstate(over="ignore"):
+        e = np.float32(np.exp(np.float64(-s)))
+    return np.float32(np.float32(1.0) / (np.float32(1.0) + e))
+
+
+def moe_shared_expert_reference(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x: np.ndarray,
+                                out: np.ndarray, gate_inp=None, gate_type: int = Q4_K,
+                                down_type: int = Q4_K) -> np.ndarray:
+    """out[t] + g_t * y_t for every token (MoeForwardPass.java:240-247): y_t =
+    down(silu(gate x_t) * (up x_t)) (runSharedExpert :418-426, one expert of
+    the packed gate / up (I, row bytes of H) and down (H, row bytes of I), in
+    fp64 over the bit-exact dequantized weights) and g_t from
+    shared_expert_gate; the sum in fp64."""
+    x = np.asarray(x, dtype=np.float32)
+    T = x.shape[0]
+    ids = np.zeros((T, 1), np.int32)
+    w = np.ones((T, 1), np.float32)
+    y = moe_reference_q4k(gate, up, down, 1, x, ids, w, down_type=down_type, gate_type=gate_type)
+    g = np.array([shared_expert_gate(x[t], gate_inp) for t in range(T)], np.float64)
+    return np.asarray(out, np.float64) + g[:, None] * y
 
 
 def rel_err(y, ref) -> float:

@@ -9,7 +9,8 @@ import pytest
 from gollek_amd import synthetic as syn
 from gollek_amd import tensor_ops as ops
 from oracle import oracle as o
-from tests.test_oracle import MOE_CF_E, moe_closed_form_case, moe_closed_form_expected
+from tests.test_oracle import (MOE_CF_E, moe_closed_form_case, moe_closed_form_expected,
+                               shared_closed_form_case, shared_closed_form_expected)
 
 pytestmark = pytest.mark.gpu
 MOE_TOL = 1e-3
@@ -288,6 +289,101 @@ def test_moe_device_entry_matches_host():
     for d in (dg, du, dd):
         d.close()
     for t in (tg, tu, td):
+        t.close()
+
+
+# ---- shared expert --------------------------------------------------------------
+
+# The shared expert (one expert, every token, weight g_t) after a routed
+# output: Qwen1.5-MoE's shape (hidden 2048, shared inter 5632: past the
+# matrix-core passes, on the row kernels), a DeepSeek-style 2 x 1408 (the
+# matrix-core passes with Q6_K down), Q8_0 and Q5_K experts, with and
+# without the shared_expert_gate row.
+@pytest.mark.parametrize("gt,dt,H,I,T,gated", [
+    (syn.Q4_K, syn.Q4_K, 2048, 5632, 16, True), (syn.Q4_K, syn.Q6_K, 2048, 2816, 16, True),
+    (syn.Q8_0, syn.Q8_0, 1024, 512, 5, False), (syn.Q5_K, syn.Q5_K, 2048, 768, 9, True),
+    (syn.Q4_0, syn.Q4_0, 512, 1024, 1, True)])
+def test_moe_shared_expert_parity(gt, dt, H, I, T, gated):
+    print(f"[gpu] moe shared gate={gt} down={dt} H={H} I={I} T={T} gated={gated}", flush=True)
+    gate, up, down, tg, tu, td = _experts(1, H, I, seed=H + I + T, down_type=dt, gate_type=gt)
+    x = syn.activation(T * H, seed=9).reshape(T, H)
+    routed = syn.activation(T * H, seed=10).reshape(T, H)
+    gi = (np.random.default_rng(11).standard_normal(H) / np.sqrt(H)).astype(np.float32) if gated else None
+    got = ops.moe_shared_expert(tg, tu, td, x, routed, gate_inp=gi)
+    ref = o.moe_shared_expert_reference(gate, up, down, x, routed, gate_inp=gi, gate_type=gt,
+                                        down_type=dt)
+    err = o.rel_err(got, ref)
+    print(f"[gpu] moe shared rel_err={err:.3e}", flush=True)
+    assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+def test_moe_shared_expert_closed_form():
+    gate, up, down, x, gi = shared_closed_form_case()
+    H, I = x.shape[1], gate.shape[0]
+    routed = moe_closed_form_expected().astype(np.float32)
+    ts = [ops.GgufTensor("blk.0.ffn_gate_shexp.weight", (H, I), syn.Q4_K, gate.reshape(-1)),
+          ops.GgufTensor("blk.0.ffn_up_shexp.weight", (H, I), syn.Q4_K, up.reshape(-1)),
+          ops.GgufTensor("blk.0.ffn_down_shexp.weight", (I, H), syn.Q4_K, down.reshape(-1))]
+    for gate_inp, gated in ((gi, True), (None, False)):
+        got = ops.moe_shared_expert(*ts, x, routed, gate_inp=gate_inp)
+        exp = shared_closed_form_expected(routed, gated=gated)
+        assert o.rel_err(got, exp) <= MOE_TOL
+    # a zero gate row gives g = 1/2 exactly: the shared part is half of the ungated one
+    half = ops.moe_shared_expert(*ts, x, np.zeros_like(routed), gate_inp=np.zeros(H, np.float32))
+    full = ops.moe_shared_expert(*ts, x, np.zeros_like(routed))
+    assert np.array_equal(half, np.float32(0.5) * full)
+    for t in ts:
+        t.close()
+
+
+def test_moe_shared_expert_device_entry_matches_host():
+    import torch
+    H, I, T = 1024, 768, 7
+    gate, up, down, tg, tu, td = _experts(1, H, I, seed=41)
+    x = syn.activation(T * H, seed=42).reshape(T, H)
+    routed = syn.activation(T * H, seed=43).reshape(T, H)
+    gi = (np.random.default_rng(44).standard_normal(H) / np.sqrt(H)).astype(np.float32)
+    host = ops.moe_shared_expert(tg, tu, td, x, routed, gate_inp=gi)
+    bufs = [torch.from_numpy(a.reshape(-1)).cuda() for a in (gate, up, down)]
+    dg = ops.DeviceWeight(syn.Q4_K, bufs[0].data_ptr(), I, H)
+    du = ops.DeviceWeight(syn.Q4_K, bufs[1].data_ptr(), I, H)
+    dd = ops.DeviceWeight(syn.Q4_K, bufs[2].data_ptr(), H, I)
+    nbytes = ops.moe_shared_workspace_bytes(T, H, I)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    xd, gd = torch.from_numpy(x).cuda(), torch.from_numpy(gi).cuda()
+    out = torch.from_numpy(routed.copy()).cuda()
+    ops.moe_shared_expert_device(dg, du, dd, gd.data_ptr(), xd.data_ptr(), T, out.data_ptr(),
+                                 ws.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), host)
+    for d in (dg, du, dd):
+        d.close()
+    for t in (tg, tu, td):
+        t.close()
+
+
+def test_moe_shared_expert_rejects_bad_arguments():
+    H, I, T = 512, 256, 2
+    gate, up, down, tg, tu, td = _experts(1, H, I, seed=51)
+    x = syn.activation(T * H, seed=52).reshape(T, H)
+    with pytest.raises(ops.NullPointerError):
+        ops.moe_shared_expert(tg, tu, None, x, np.zeros((T, H), np.float32))
+    # the output must hold tokens x hidden floats
+    lib = ops._native.load()
+    err = ops._native.ErrBuf()
+    short = np.zeros(T * H - 1, np.float32)
+    rc = lib.gollek_hip_moe_shared_expert(tg.handle(), tu.handle(), td.handle(), None,
+                                          x.ctypes.data, T, short.ctypes.data, short.size,
+                                          err.buf, err.size)
+    assert rc == ops._native.ERR_ARG
+    # up and gate disagree (gate of 2 experts' rows)
+    g2, _, _, tg2, tu2, td2 = _experts(2, H, I, seed=53)
+    with pytest.raises(ops.IllegalArgumentError):
+        ops.moe_shared_expert(tg2, tu, td, x, np.zeros((T, H), np.float32))
+    assert ops.moe_shared_workspace_bytes(-1, H, I) == -1
+    for t in (tg, tu, td, tg2, tu2, td2):
         t.close()
 
 

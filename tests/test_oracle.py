@@ -292,6 +292,67 @@ def test_moe_reference_closed_form():
         assert np.max(np.abs(mut - exp)) > 0.05 * np.max(np.abs(exp)), name
 
 
+# Shared expert: expert 0 of the closed-form experts (gate 2.0, up -0.75,
+# down 0.125) and a constant shared_expert_gate row of 2.0, so s_t = 2 S_t.
+SHARED_CF_GATE_INP = 2.0
+
+
+def shared_closed_form_case():
+    H, I = MOE_CF_H, MOE_CF_I
+    gate = _const_q4k(I, H, *MOE_CF_GATE[0])
+    up = _const_q4k(I, H, *MOE_CF_UP[0])
+    down = _const_q4k(H, I, *MOE_CF_DOWN[0])
+    x = np.stack([np.full(H, v, np.float32) for v in MOE_CF_XV])
+    return gate, up, down, x, np.full(H, SHARED_CF_GATE_INP, np.float32)
+
+
+def shared_closed_form_expected(out, gated=True, gate_sign=1.0, gate_power=1, swap=False):
+    res = np.array(out, np.float64, copy=True)
+    for t, xv in enumerate(MOE_CF_XV):
+        S = xv * MOE_CF_H
+        a, b = _value(MOE_CF_GATE[0]) * S, _value(MOE_CF_UP[0]) * S
+        if swap:
+            a, b = b, a
+        y = _value(MOE_CF_DOWN[0]) * MOE_CF_I * (a / (1.0 + math.exp(-a))) * b
+        g = 1.0 / (1.0 + math.exp(-gate_sign * SHARED_CF_GATE_INP * S)) if gated else 1.0
+        res[t] += g ** gate_power * y
+    return res
+
+
+def test_moe_shared_expert_reference_closed_form():
+    gate, up, down, x, gi = shared_closed_form_case()
+    out = moe_closed_form_expected().astype(np.float32)  # the routed output
+    got = o.moe_shared_expert_reference(gate, up, down, x, out, gate_inp=gi)
+    exp = shared_closed_form_expected(out)
+    assert np.allclose(got, exp, rtol=1e-6, atol=1e-9)  # g is a float
+    assert np.allclose(o.moe_shared_expert_reference(gate, up, down, x, out),
+                       shared_closed_form_expected(out, gated=False), rtol=1e-12, atol=1e-12)
+    # Each plausible mistake moves the answer by at least 5 % of the shared
+    # expert's contribution.
+    scale = np.max(np.abs(exp - out))
+    mutants = {
+        "gate ignored": shared_closed_form_expected(out, gated=False),
+        "sigmoid(+s) for sigmoid(-s)": shared_closed_form_expected(out, gate_sign=-1.0),
+        "gate applied twice": shared_closed_form_expected(out, gate_power=2),
+        "gate/up swapped": shared_closed_form_expected(out, swap=True),
+        "routed output dropped": shared_closed_form_expected(np.zeros_like(out)),
+    }
+    for name, mut in mutants.items():
+        assert np.max(np.abs(mut - exp)) > 0.05 * scale, name
+
+
+def test_shared_expert_gate_special_values():
+    x = np.full(8, 0.25, np.float32)
+    assert o.shared_expert_gate(x, None) == np.float32(1.0)
+    assert o.shared_expert_gate(x, np.zeros(8, np.float32)) == np.float32(0.5)
+    # s = 8 * 0.25 * ln 3 / 2 = ln 3: 1 / (1 + 1/3) = 0.75 (to a float ulp)
+    g = o.shared_expert_gate(x, np.full(8, math.log(3.0) / 2, np.float32))
+    assert abs(float(g) - 0.75) <= 2 ** -23
+    # exp(-s) overflows to inf for s far below zero: the gate is exactly 0
+    assert o.shared_expert_gate(x, np.full(8, -1e4, np.float32)) == np.float32(0.0)
+    assert o.shared_expert_gate(x, np.full(8, 1e4, np.float32)) == np.float32(1.0)
+
+
 def _moe_reference_mutant(kind, gate, up, down, E, x, ids, w):
     """moe_reference_q4k with one planted mistake (CPU only)."""
     H = gate.shape[1] // 144 * 256
