@@ -40,6 +40,12 @@ import java.util.WeakHashMap;
  * <li>GgufTensorOps.clearPreparedMatrixCaches, which JavaNativeGgufBackend.close
  * calls (core/plugin/gollek-plugin-runner-gguf/.../JavaNativeGgufBackend.java:139-143):
  * {@code GgufHipMatVec.release(model)}.</li>
+ * <li>A GGUF MoE layer (stacked ffn_gate_exps / ffn_up_exps / ffn_down_exps
+ * and, where present, the ffn_*_shexp shared expert): {@code tryMoeLayer} in
+ * place of the router probabilities, selectTopK, the per-(token, route)
+ * expert loop and the shared expert of MoeForwardPass
+ * (runner/safetensor/gollek-safetensor-engine/src/main/java/tech/kayys/gollek/
+ * safetensor/engine/generation/moe/MoeForwardPass.java:174-247).</li>
  * </ul>
  *
  * <p>The route is taken when the system property gollek.hip.enabled is not
@@ -82,6 +88,8 @@ final class GgufHipMatVec {
     static final int ERR_UNSUPPORTED = -3;
     static final int ERR_DEVICE = -4;
     static final int ERR_NOMEM = -5;
+    static final int ROUTER_SOFTMAX = 0;
+    static final int ROUTER_SIGMOID = 1;
 
     private static final int ABI_MAJOR = 1;
     private static final int ERR_LEN = 512;
@@ -151,6 +159,72 @@ final class GgufHipMatVec {
         return true;
     }
 
+    /**
+     * One MoE layer's experts for {@code tokens} tokens: the router on
+     * {@code logits} (row-major tokens x nExperts, the router linear's output)
+     * with the reference's scoring (sigmoid when the model type contains
+     * "qwen" or "moe", softmax otherwise; MoeForwardPass.java:174-197), the
+     * top-{@code topK} routes (selectTopK, :286-306), the routed SwiGLU experts
+     * summed in route order (:217-240) into {@code out} (row-major tokens x
+     * hidden), then, when sharedGate / sharedUp / sharedDown are non-null, the
+     * shared expert added per token (:240-247), scaled by sigmoid(x_t .
+     * sharedGateRow) when that row (the shared_expert_gate weight, hidden
+     * floats) is non-null.  Experts are stacked as GGUF files store them:
+     * gate and up of shape {hidden, inter, nExperts}, down {inter, hidden,
+     * nExperts}; the shared expert's {hidden, sharedInter} and {sharedInter,
+     * hidden}.  They stay in their GGUF layout on the device (no prepared
+     * copy).  False when the route is not taken.
+     */
+    static boolean tryMoeLayer(GGUFModel model, GGUFTensorInfo gate, GGUFTensorInfo up, GGUFTensorInfo down,
+                               int nExperts, float[] x, int tokens, float[] logits, int topK, String modelType,
+                               GGUFTensorInfo sharedGate, GGUFTensorInfo sharedUp, GGUFTensorInfo sharedDown,
+                               float[] sharedGateRow, float[] out) {
+        Binding b = Binding.get();
+        boolean shared = sharedGate != null && sharedUp != null && sharedDown != null;
+        if (b == null || !supportsType(gate.typeId()) || !supportsType(up.typeId()) || !supportsType(down.typeId())
+                || (shared && (!supportsType(sharedGate.typeId()) || !supportsType(sharedUp.typeId())
+                        || !supportsType(sharedDown.typeId())))) {
+            return false;
+        }
+        // The library reads x, logits and the gate row by these lengths.
+        long hidden = gate.shape()[0];
+        if (tokens < 0 || (long) x.length < (long) tokens * hidden
+                || (long) logits.length < (long) tokens * (long) nExperts
+                || (sharedGateRow != null && (long) sharedGateRow.length < hidden)) {
+            throw new IllegalArgumentException("MoE layer inputs are shorter than tokens x hidden / experts");
+        }
+        String mt = modelType != null ? modelType : "";
+        int scoring = mt.contains("qwen") || mt.contains("moe") ? ROUTER_SIGMOID : ROUTER_SOFTMAX;
+        MemorySegment g = expertHandle(b, model, gate);
+        MemorySegment u = expertHandle(b, model, up);
+        MemorySegment d = expertHandle(b, model, down);
+        try (Arena arena = Arena.ofConfined()) {
+            MemorySegment err = arena.allocate(ERR_LEN);
+            int rc = b.moeBlock(g, u, d, (long) nExperts, MemorySegment.ofArray(x), (long) tokens,
+                    MemorySegment.ofArray(logits), (long) topK, scoring, MemorySegment.ofArray(out), (long) out.length,
+                    err, (long) ERR_LEN);
+            check(rc, err);
+            if (shared) {
+                MemorySegment row = sharedGateRow != null ? MemorySegment.ofArray(sharedGateRow) : MemorySegment.NULL;
+                rc = b.moeSharedExpert(expertHandle(b, model, sharedGate), expertHandle(b, model, sharedUp),
+                        expertHandle(b, model, sharedDown), row, MemorySegment.ofArray(x), (long) tokens,
+                        MemorySegment.ofArray(out), (long) out.length, err, (long) ERR_LEN);
+                check(rc, err);
+            }
+        }
+        return true;
+    }
+
+    /** An expert tensor's handle: rows = the product of its outer dimensions, the GGUF bytes as stored. */
+    private static MemorySegment expertHandle(Binding b, GGUFModel model, GGUFTensorInfo tensor) {
+        long[] shape = tensor.shape();
+        long rows = 1L;
+        for (int i = 1; i < shape.length; i++) {
+            rows *= shape[i];
+        }
+        return handle(b, model, tensor, rows, Math.toIntExact(shape[0]), tensor.sizeInBytes() / rows, false);
+    }
+
     /** Frees every device handle of the model (the prepared-cache clear). */
     static void release(GGUFModel model) {
         Binding b = Binding.get();
@@ -176,6 +250,11 @@ final class GgufHipMatVec {
 
     private static MemorySegment handle(Binding b, GGUFModel model, GGUFTensorInfo tensor, long rows, int columns,
                                         long rowBytes) {
+        return handle(b, model, tensor, rows, columns, rowBytes, true);
+    }
+
+    private static MemorySegment handle(Binding b, GGUFModel model, GGUFTensorInfo tensor, long rows, int columns,
+                                        long rowBytes, boolean prepare) {
         synchronized (HANDLES) {
             Map<GGUFTensorInfo, MemorySegment> perModel = HANDLES.computeIfAbsent(model, m -> new IdentityHashMap<>());
             MemorySegment w = perModel.get(tensor);
@@ -198,7 +277,7 @@ final class GgufHipMatVec {
                 // matrices (gollek.gguf.java_native.auto_prepare) within the byte budget;
                 // without it the handle keeps reading the GGUF bytes.
                 long size = rows * rowBytes;
-                if (!preparingStopped && !"false".equals(System.getProperty("gollek.hip.prepare", "true"))
+                if (prepare && !preparingStopped && !"false".equals(System.getProperty("gollek.hip.prepare", "true"))
                         && preparedBytes <= Long.getLong("gollek.hip.prepare.max_bytes", Long.MAX_VALUE) - size) {
                     int rc = b.weightPrepare(w, err, (long) ERR_LEN);
                     if (rc == OK) {
@@ -266,6 +345,8 @@ final class GgufHipMatVec {
         private final MethodHandle matvecRows;
         private final MethodHandle dotRow;
         private final MethodHandle dequantizeRows;
+        private final MethodHandle moeBlock;
+        private final MethodHandle moeSharedExpert;
 
         /** The binding, or null when the route is disabled or the library cannot be used here. */
         static Binding get() {
@@ -345,6 +426,17 @@ final class GgufHipMatVec {
                     FunctionDescriptor.of(ValueLayout.JAVA_INT,
                             ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS,
                             ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), true);
+            this.moeBlock = downcall(linker, lookup, "gollek_hip_moe_block",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG,
+                            ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG,
+                            ValueLayout.JAVA_INT, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS,
+                            ValueLayout.JAVA_LONG), true);
+            this.moeSharedExpert = downcall(linker, lookup, "gollek_hip_moe_shared_expert",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.ADDRESS,
+                            ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG,
+                            ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), true);
             int abi = (int) version.invokeExact();
             if (abi / 10000 != ABI_MAJOR) {
                 throw new IllegalStateException("libgollek_hip ABI " + abi + " is not major " + ABI_MAJOR);
@@ -441,6 +533,27 @@ final class GgufHipMatVec {
                            MemorySegment err, long errLen) {
             try {
                 return (int) dequantizeRows.invokeExact(weight, row0, nrows, dst, dstLen, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int moeBlock(MemorySegment gate, MemorySegment up, MemorySegment down, long nExperts, MemorySegment x,
+                     long tokens, MemorySegment logits, long topK, int scoring, MemorySegment out, long outLen,
+                     MemorySegment err, long errLen) {
+            try {
+                return (int) moeBlock.invokeExact(gate, up, down, nExperts, x, tokens, logits, topK, scoring, out, outLen,
+                        err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int moeSharedExpert(MemorySegment gate, MemorySegment up, MemorySegment down, MemorySegment gateRow,
+                            MemorySegment x, long tokens, MemorySegment out, long outLen, MemorySegment err,
+                            long errLen) {
+            try {
+                return (int) moeSharedExpert.invokeExact(gate, up, down, gateRow, x, tokens, out, outLen, err, errLen);
             } catch (Throwable t) {
                 throw propagate(t);
             }

@@ -81,9 +81,10 @@ def test_heap_array_arguments_use_critical_downcalls():
     # only critical downcalls with heap access accept.
     text = java_text()
     desc = java_descriptors()
-    for fn in ("matvecRows", "dotRow", "dequantizeRows"):
+    for fn in ("matvecRows", "dotRow", "dequantizeRows", "moeBlock", "moeSharedExpert"):
         assert re.search(rf"b\.{fn}\([^;]*MemorySegment\.ofArray", text), fn
-    for sym in ("gollek_hip_matvec_rows", "gollek_hip_dot_row", "gollek_hip_dequantize_rows"):
+    for sym in ("gollek_hip_matvec_rows", "gollek_hip_dot_row", "gollek_hip_dequantize_rows",
+                "gollek_hip_moe_block", "gollek_hip_moe_shared_expert"):
         assert desc[sym][2], sym
 
 
@@ -97,6 +98,8 @@ WRAPPERS = {  # typed wrapper -> the symbol whose handle it invokes
     "matvecRows": "gollek_hip_matvec_rows",
     "dotRow": "gollek_hip_dot_row",
     "dequantizeRows": "gollek_hip_dequantize_rows",
+    "moeBlock": "gollek_hip_moe_block",
+    "moeSharedExpert": "gollek_hip_moe_shared_expert",
 }
 
 
@@ -137,6 +140,28 @@ def test_status_codes_match_the_header():
         assert h and j and int(h.group(1)) == int(j.group(1)), name
 
 
+def test_router_scoring_constants_match_the_header():
+    text = java_text()
+    hdr = HEADER.read_text()
+    for name in ("ROUTER_SOFTMAX", "ROUTER_SIGMOID"):
+        h = re.search(rf"#define GOLLEK_HIP_{name} (\d+)", hdr)
+        j = re.search(rf"static final int {name} = (\d+);", text)
+        assert h and j and int(h.group(1)) == int(j.group(1)), name
+    # the reference's model-type test, restated in tryMoeLayer
+    assert 'mt.contains("qwen") || mt.contains("moe") ? ROUTER_SIGMOID : ROUTER_SOFTMAX' in text
+
+
+def test_moe_layer_checks_the_lengths_the_library_reads():
+    # moe_block and moe_shared_expert take x, logits and the gate row without
+    # lengths: the adapter checks them before handing heap arrays over.
+    text = java_text()
+    body = re.search(r"static boolean tryMoeLayer\((.*?)\n    \}", text, flags=re.S).group(1)
+    for cond in ("x.length < (long) tokens * hidden", "logits.length < (long) tokens * (long) nExperts",
+                 "sharedGateRow.length < hidden"):
+        assert cond in body, cond
+    assert body.index("IllegalArgumentException") < body.index("b.moeBlock(")
+
+
 def test_supported_types_match_the_header():
     text = java_text()
     hdr = HEADER.read_text()
@@ -164,3 +189,10 @@ def test_reference_methods_the_adapter_calls_exist():
     java = java_text()
     assert "package tech.kayys.gollek.gguf.runtime;" in java
     assert "GgufTensorData.tensorData(model, tensor)" in java
+    # tryMoeLayer: GGUFTensorInfo.shape() and sizeInBytes(), and the
+    # MoeForwardPass lines it replaces
+    assert "long[] shape" in info and "long sizeInBytes" in info
+    moe = (REFERENCE / "runner/safetensor/gollek-safetensor-engine/src/main/java/tech/kayys/gollek/"
+           "safetensor/engine/generation/moe/MoeForwardPass.java").read_text()
+    assert 'modelType.contains("qwen") || modelType.contains("moe")' in moe
+    assert "runSharedExpert(" in moe and "resolveSharedExpertGate(" in moe
