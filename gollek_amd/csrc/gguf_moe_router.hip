@@ -16,11 +16,12 @@
 //     the expert count keep id 0 and weight 0.
 //
 // One 256-thread workgroup per token.  Each thread owns experts e = tid,
-// tid + 256, ...; the two order-dependent float sums run on one thread from
-// LDS (E and top_k adds), everything else is parallel.  A thread finds the
-// rank of its expert by counting, over all experts, the keys above its own
-// plus the equal keys at lower indices: the position a stable descending
-// sort gives it.
+// tid + 256, ...; the two order-dependent float sums run in one lane of wave
+// 0 over values the wave loaded together (E and top_k adds, one lane read
+// each), everything else is parallel.  A thread finds the rank of its expert
+// by counting, over all experts (four keys per LDS read), the keys above its
+// own plus the equal keys at lower indices: the position a stable
+// descending sort gives it.
 #include <hip/hip_runtime.h>
 
 #include "gguf_kernels.hpp"
@@ -46,17 +47,34 @@ __device__ inline float java_max(float a, float b) {
     return a > b ? a : b;
 }
 
+// Sum of v[0, n) in index order (s = ((0 + v0) + v1) + ...), v in LDS: wave 0
+// loads 64 values at a time and one lane adds them in order.  Every lane of
+// wave 0 calls this; the sum is returned in all of them.
+__device__ inline float ordered_sum(const float *v, int n, int lane) {
+#pragma clang fp contract(off)
+    float s = 0.0f;
+    for (int base = 0; base < n; base += 64) {
+        const float mine = base + lane < n ? v[base + lane] : 0.0f;
+        const int m = n - base < 64 ? n - base : 64;
+        for (int j = 0; j < m; j++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), j));
+    }
+    return s;
+}
+
 __global__ __launch_bounds__(kRouterThreads) void moe_topk_kernel(
     const float *__restrict__ logits, int E, int K, int sigmoid, int32_t *__restrict__ ids,
     float *__restrict__ wts) {
 #pragma clang fp contract(off)
-    extern __shared__ float sh[];  // p[E], key[E] (as int), sel[K], red[kRouterThreads / 64]
-    float *p = sh;
-    int *key = reinterpret_cast<int *>(sh + E);
-    int *sel = key + E;
+    // key[E4] (as int, padded to a multiple of 4 with keys that count for
+    // nothing), p[E], sel[K], red[kRouterThreads / 64]
+    extern __shared__ __attribute__((aligned(16))) int sh[];
+    const int E4 = (E + 3) & ~3;
+    int *key = sh;
+    float *p = reinterpret_cast<float *>(sh + E4);
+    int *sel = reinterpret_cast<int *>(p + E);
     float *red = reinterpret_cast<float *>(sel + K);
     __shared__ float s_max, s_sum;
-    const int t = blockIdx.x, tid = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float *row = logits + (size_t)t * E;
 
     if (sigmoid) {
@@ -79,10 +97,9 @@ __global__ __launch_bounds__(kRouterThreads) void moe_topk_kernel(
         const float mx = s_max;
         for (int e = tid; e < E; e += kRouterThreads) p[e] = (float)exp((double)(row[e] - mx));
         __syncthreads();
-        if (tid == 0) {
-            float s = 0.0f;
-            for (int e = 0; e < E; e++) s += p[e];
-            s_sum = s;
+        if (tid < 64) {
+            const float s = ordered_sum(p, E, lane);
+            if (tid == 0) s_sum = s;
         }
         __syncthreads();
         const float s = s_sum;
@@ -90,23 +107,59 @@ __global__ __launch_bounds__(kRouterThreads) void moe_topk_kernel(
     }
     for (int k = tid; k < K; k += kRouterThreads) sel[k] = -1;
     __syncthreads();
-    for (int e = tid; e < E; e += kRouterThreads) key[e] = order_key(p[e]);
+    // INT_MIN is below every key order_key gives (-inf maps above it) and
+    // equal to none: the padding adds nothing to a rank.
+    for (int e = tid; e < E4; e += kRouterThreads) key[e] = e < E ? order_key(p[e]) : INT_MIN;
     __syncthreads();
-    for (int e = tid; e < E; e += kRouterThreads) {
+    // Keys above key[e] plus equal keys below e, over keys [j0, j1).
+    auto count = [&](int e, int j0, int j1) {
         const int me = key[e];
         int rank = 0;
-        for (int j = 0; j < E; j++) {
-            const int kj = key[j];
-            rank += (kj > me) | ((kj == me) & (j < e));
+#pragma unroll 4
+        for (int j = j0; j < j1; j += 4) {
+            const int4 k4 = *reinterpret_cast<const int4 *>(key + j);
+            rank += (k4.x > me) | ((k4.x == me) & (j < e));
+            rank += (k4.y > me) | ((k4.y == me) & (j + 1 < e));
+            rank += (k4.z > me) | ((k4.z == me) & (j + 2 < e));
+            rank += (k4.w > me) | ((k4.w == me) & (j + 3 < e));
         }
-        if (rank < K) sel[rank] = e;
+        return rank;
+    };
+    // Up to 8 threads per expert when the experts leave threads idle, each
+    // counting one span of the keys; the spans' counts are added in LDS.
+    int tpe = 1;
+    while (tpe < 8 && 2 * tpe * E <= kRouterThreads) tpe *= 2;  // uniform
+    if (tpe == 1) {
+        for (int e = tid; e < E; e += kRouterThreads) {
+            const int rank = count(e, 0, E4);
+            if (rank < K) sel[rank] = e;
+        }
+    } else {
+        __shared__ int prank[kRouterThreads];
+        const int span = (E4 / tpe + 3) & ~3;
+        if (tid < tpe * E) {
+            const int e = tid % E, part = tid / E;
+            const int j0 = part * span, j1 = j0 + span < E4 ? j0 + span : E4;
+            prank[tid] = count(e, j0, j1);
+        }
+        __syncthreads();
+        if (tid < E) {
+            int rank = 0;
+            for (int q = 0; q < tpe; q++) rank += prank[q * E + tid];
+            if (rank < K) sel[rank] = tid;
+        }
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
+        // chosen probabilities of ranks k < n, summed in rank order
         const int n = K < E ? K : E;
         float s = 0.0f;
-        for (int k = 0; k < n; k++) s += p[sel[k]];
-        for (int k = 0; k < K; k++) {
+        for (int base = 0; base < n; base += 64) {
+            const float mine = base + lane < n ? p[sel[base + lane]] : 0.0f;
+            const int m = n - base < 64 ? n - base : 64;
+            for (int j = 0; j < m; j++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), j));
+        }
+        for (int k = lane; k < K; k += 64) {
             const bool have = k < n;
             float w = have ? p[sel[k]] : 0.0f;
             if (s > 0.0f) w = w / s;
@@ -119,7 +172,7 @@ __global__ __launch_bounds__(kRouterThreads) void moe_topk_kernel(
 }  // namespace
 
 size_t moe_topk_lds_bytes(int E, int K) {
-    return (size_t)E * 8 + (size_t)K * 4 + (kRouterThreads / 64) * 4;
+    return (size_t)((E + 3) & ~3) * 4 + (size_t)E * 4 + (size_t)K * 4 + (kRouterThreads / 64) * 4;
 }
 
 hipError_t launch_moe_topk(const float *logits, int T, int E, int K, int sigmoid, int32_t *ids,
