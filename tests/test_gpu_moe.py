@@ -235,6 +235,49 @@ def test_moe_nan_activation_poisons_only_its_token(variant, moe_variant):
         t.close()
 
 
+def _nan_dmin_zero_mins(blocks, pb, rows, every=3):
+    """Every `every`-th superblock of the given rows: dmin = NaN and all
+    eight min codes 0 (scale codes 5), which the reference's minContribution
+    (RT/GgufKQuantLayout.java:67-69) keeps out of the sum."""
+    b = blocks.reshape(blocks.shape[0], -1, pb)
+    hdr = syn.pack_q4k_scales(np.full(8, 5), np.zeros(8, np.int64))
+    for r in rows:
+        for j in range(0, b.shape[1], every):
+            b[r, j, 2], b[r, j, 3] = 0x00, 0x7E  # fp16 NaN
+            b[r, j, 4:16] = hdr
+    return b.reshape(blocks.shape)
+
+
+# K-quant experts whose superblocks carry a NaN dmin with all min codes 0:
+# the matrix-core passes' non-finite branch (and the row kernels) give the
+# reference's finite values for them, on gate / up and on Q4_K / Q5_K down rows.
+@pytest.mark.parametrize("gt,dt", [(syn.Q4_K, syn.Q4_K), (syn.Q5_K, syn.Q6_K), (syn.Q5_K, syn.Q5_K),
+                                   (syn.Q4_K, syn.Q5_K)])
+def test_moe_nan_dmin_with_zero_min_codes(gt, dt):
+    E, H, I, T, k = 8, 512, 256, 5, 2
+    pb = {syn.Q4_K: 144, syn.Q5_K: 176}
+    gate = syn.matrix(gt, E * I, H, 61)
+    up = syn.matrix(gt, E * I, H, 62)
+    down = syn.matrix(dt, E * H, I, 63)
+    rows = range(0, E * I, 5)
+    gate = _nan_dmin_zero_mins(gate, pb[gt], rows)
+    up = _nan_dmin_zero_mins(up, pb[gt], rows[1:])
+    if dt in pb:
+        down = _nan_dmin_zero_mins(down, pb[dt], range(0, E * H, 7), every=1)
+    ts = [ops.GgufTensor("blk.0.ffn_gate_exps.weight", (H, I, E), gt, gate.reshape(-1)),
+          ops.GgufTensor("blk.0.ffn_up_exps.weight", (H, I, E), gt, up.reshape(-1)),
+          ops.GgufTensor("blk.0.ffn_down_exps.weight", (I, H, E), dt, down.reshape(-1))]
+    ids, w = syn.moe_routing(T, E, k, seed=64)
+    x = syn.activation(T * H, seed=65).reshape(T, H)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=gt)
+    assert np.all(np.isfinite(ref))
+    out = ops.moe_grouped(*ts, E, x, ids, w)
+    assert np.all(np.isfinite(out))
+    assert o.rel_err(out, ref) <= MOE_TOL
+    for t in ts:
+        t.close()
+
+
 def test_moe_skips_invalid_routes_and_shares_experts():
     E, H, I, T, k = 8, 512, 256, 6, 3
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=11)
