@@ -36,7 +36,8 @@
 // and whenever the route group changes, which drains the load pipeline
 // once.  Results collect in LDS and are stored at those drains, when the
 // buffer fills and at the end: on gfx9 stores share the load counter the
-// ring waits on.
+// ring waits on.  Items stream through a ring of slots in LDS (MoRing):
+// three of 38 KB, or for Q5_K rows two of 46 KB.
 #include <type_traits>
 
 #include "gguf_dot4.hpp"
@@ -52,10 +53,16 @@ namespace {
 constexpr int kMoWaves = 16;
 constexpr int kMoThreads = kMoWaves * 64;
 constexpr int kMoGroup = 4;          // routes per group (two MFMA pairs)
-constexpr int kMoMaxDma = 38;        // 1 KB loads per item slot
-constexpr int kMoDmaPerWave = (kMoMaxDma + kMoWaves - 1) / kMoWaves;
-constexpr int kMoSlot = kMoMaxDma * 1024;
-constexpr int kMoSlots = 3;
+// The item ring: three slots of 38 KB; for Q5_K rows (176-byte
+// superblocks) two slots of 46 KB, so that 16 gate and 16 up rows of 8
+// superblocks (hidden 2048) fit one slot.
+template <int WT>
+struct MoRing {
+    static constexpr int kMaxDma = WT == kQ5_K ? 46 : 38;  // 1 KB loads per item slot
+    static constexpr int kSlots = WT == kQ5_K ? 2 : 3;
+    static constexpr int kSlot = kMaxDma * 1024;
+    static constexpr int kDmaPerWave = (kMaxDma + kMoWaves - 1) / kMoWaves;
+};
 constexpr int kMoOutCap = 1536;      // buffered results (value, index)
 constexpr int kMoMaxExperts = 256;   // routing tables held in LDS
 constexpr int kMoMaxRoutes = 2048;
@@ -233,6 +240,9 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     // bytes of a 256-column piece of a row (eight Q4_0 blocks are 144, as a
     // Q4_K superblock)
     constexpr uint32_t PB = WT == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+    using RG = MoRing<WT>;
+    constexpr int kMoMaxDma = RG::kMaxDma, kMoSlots = RG::kSlots, kMoSlot = RG::kSlot;
+    constexpr int kMoDmaPerWave = RG::kDmaPerWave;
     __shared__ __attribute__((aligned(16))) uint8_t ring[kMoSlots * kMoSlot + 1024];  // + sink
     // digit build; HV = 2: + the (half, route) x sums and scales from 768
     __shared__ __attribute__((aligned(16))) uint8_t scratch[kMoWaves][HV == 2 ? 1088 : 1024];
@@ -1444,9 +1454,16 @@ namespace {
 // blocks) or a Q5_K superblock (176).
 constexpr uint32_t piece_bytes(int type) { return type == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes; }
 
-// Geometry of pass `mode` over rows of `pb`-byte pieces.  The caller has
-// checked that H and I are multiples of 256 in [256, 4096].
-MoeTileGeom make_geom(int mode, int E, int H, int I, uint32_t pb) {
+// 1 KB loads an item slot holds for `type` rows.
+int max_dma(int type) {
+    return type == kQ5_K ? MoRing<kQ5_K>::kMaxDma : type == kQ4_0 ? MoRing<kQ4_0>::kMaxDma : MoRing<kQ4_K>::kMaxDma;
+}
+
+// Geometry of pass `mode` over `type` rows.  The caller has checked that H
+// and I are multiples of 256 in [256, 4096].
+MoeTileGeom make_geom(int mode, int E, int H, int I, int type) {
+    const uint32_t pb = piece_bytes(type);
+    const int kMoMaxDma = max_dma(type);
     MoeTileGeom g{};
     const int K = mode == 0 ? H : I;
     // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all banks
@@ -1505,10 +1522,10 @@ bool tile_shape_ok(int E, int H, int I, int P, const float *x) {
 
 // Whether pass `mode` over `type` rows fits the kernel (after tile_shape_ok).
 bool tile_pass_ok(int mode, int E, int H, int I, int type) {
-    const MoeTileGeom g = make_geom(mode, E, H, I, piece_bytes(type));
+    const MoeTileGeom g = make_geom(mode, E, H, I, type);
     if (g.halves == 2 && ((mode == 0 ? H : I) / kQK) % 2 != 0) return false;  // halves of equal length
     if ((mode == 0 ? 2 * g.nsb : g.rt * g.nsb) > kMoWaves) return false;
-    return g.ndma <= kMoMaxDma && g.w_bytes < (int64_t)kMaskedOffset && 2 * kMoGroup * 16 * g.rt <= kMoOutCap;
+    return g.ndma <= max_dma(type) && g.w_bytes < (int64_t)kMaskedOffset && 2 * kMoGroup * 16 * g.rt <= kMoOutCap;
 }
 
 // The token-major down pass takes Q4_K and Q6_K rows where its geometry fits.
@@ -1544,7 +1561,7 @@ hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate,
                               const float *wts, int T, int top_k, float *out, uint8_t *ws, hipStream_t stream) {
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
-    const MoeTileGeom g0 = make_geom(0, E, H, I, piece_bytes(gate_type));
+    const MoeTileGeom g0 = make_geom(0, E, H, I, gate_type);
     const unsigned grid = (unsigned)device_cus();
     float *hbuf = reinterpret_cast<float *>(ws + L.h);
     // h records (P I 3.5 bytes) fit the fp32 h region.
@@ -1593,7 +1610,7 @@ hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate,
         }
     }
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);
-    const MoeTileGeom g1 = make_geom(1, E, H, I, piece_bytes(down_type));
+    const MoeTileGeom g1 = make_geom(1, E, H, I, down_type);
     if (down_type == kQ5_K)
         hipLaunchKernelGGL((moe_expert_tile_kernel<1, false, 1, kQ5_K>), dim3(grid), dim3(kMoThreads), 0, stream,
                            down, (const uint8_t *)nullptr, g1, (const float *)hbuf, top_k, ids, wts, E, P, ypair);
@@ -1613,7 +1630,7 @@ hipError_t launch_moe_q40_mfma(const uint8_t *gate, const uint8_t *up, const uin
                                uint8_t *ws, hipStream_t stream) {
     const MoeLayout L = moe_layout(T, top_k, H, I, E);
     const int P = T * top_k;
-    const MoeTileGeom g0 = make_geom(0, E, H, I, kQKBlockBytes), g1 = make_geom(1, E, H, I, kQKBlockBytes);
+    const MoeTileGeom g0 = make_geom(0, E, H, I, kQ4_0), g1 = make_geom(1, E, H, I, kQ4_0);
     const unsigned grid = (unsigned)device_cus();
     float *hbuf = reinterpret_cast<float *>(ws + L.h);
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);

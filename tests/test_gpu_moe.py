@@ -81,12 +81,11 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
         t.close()
 
 
-# Q5_K gate / up on the matrix-core passes (Q5_K_M / Q5_K_S layers): hidden
-# 2048 and 3072 cut into K-halves of 4 and 6 superblocks (a 176-byte
-# superblock fills an item slot sooner than a 144-byte one), 1536 and 512 in
-# one half; down rows Q6_K / Q4_K on the token-major pass, Q5_K on the
-# expert-major pass (2 to 8 row tiles per item); Q4_K gate / up with Q5_K
-# down; the even split at 300 tokens x top-2.
+# Q5_K gate / up on the matrix-core passes (Q5_K_M / Q5_K_S layers; their
+# ring has two 46 KB slots): hidden 512 .. 2048 in one half, 3072 cut into
+# K-halves of 6 superblocks; down rows Q6_K / Q4_K on the token-major pass,
+# Q5_K on the expert-major pass (2 to 8 row tiles per item); Q4_K gate / up
+# with Q5_K down; the even split at 300 tokens x top-2.
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q5_K, syn.Q6_K, 128, 2048, 768, 16, 8), (syn.Q5_K, syn.Q5_K, 128, 2048, 768, 16, 8),
     (syn.Q5_K, syn.Q4_K, 16, 1536, 512, 9, 4), (syn.Q5_K, syn.Q5_K, 8, 3072, 1536, 9, 2),
@@ -111,11 +110,11 @@ def test_moe_q5_k_parity(gt, dt, E, H, I, T, k):
 # Expert types and shapes the matrix-core passes do not take: Q8_0 / Q4_0
 # gate and up or down on the fp32 row kernels (rows of 3 to 448 blocks, 8 to
 # 64 lanes per row, route groups limited by LDS, experts with many routes),
-# Q6_K gate and up on the K-quant row kernels, mixed gate / up types, Q5_K
-# gate / up past what an item slot holds (hidden 4096: halves of 8
-# superblocks; 1792: an odd count), and Q6_K down beyond the token-major down
-# pass (inter above 1024, hidden past 2048 with an odd superblock count, more
-# than 2048 routes).
+# Q6_K gate and up on the K-quant row kernels, mixed gate / up types, and
+# Q6_K down beyond the token-major down pass (inter above 1024, hidden past
+# 2048 with an odd superblock count, more than 2048 routes); also Q5_K gate /
+# up at hidden 4096 (K-halves of 8) and 1792 (7 superblocks in one half) on
+# the matrix-core passes.
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q8_0, syn.Q8_0, 128, 2048, 768, 16, 8), (syn.Q4_0, syn.Q4_0, 128, 2048, 768, 16, 8),
     (syn.Q4_0, syn.Q4_0, 4, 512, 14336, 12, 2), (syn.Q8_0, syn.Q8_0, 2, 4096, 1024, 20, 2),
