@@ -631,8 +631,9 @@ def main() -> int:
             if have_gemm and want(name):
                 log(f"extra {name}")
                 extra[name], gemm_host = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
-        # Q4_K / Q4_0 weights at the FFN shape (K 4096, N 14336).
-        for tname, t, ms in (("q4_k", syn.Q4_K, (16, 128, 512)), ("q4_0", syn.Q4_0, (128, 512))):
+        # Q4_K / Q4_0 / Q5_K weights at the FFN shape (K 4096, N 14336).
+        for tname, t, ms in (("q4_k", syn.Q4_K, (16, 128, 512)), ("q4_0", syn.Q4_0, (128, 512)),
+                             ("q5_k", syn.Q5_K, (16, 128, 512))):
             for m in ms:
                 name = f"{tname}_gemm_bf16_m{m}_4096x14336"
                 if have_gemm and want(name):
@@ -695,7 +696,8 @@ def main() -> int:
             if m > 128:
                 continue  # the m = 128 line's rate stands for it (m mat-vecs each)
             log(f"cpu baseline {name}")
-            cpus[name] = cpu_gemm(hosts[name], m, seed=8, type_id=syn.Q4_K if name.startswith("q4_k") else syn.Q4_0)
+            tid = {"q4_k": syn.Q4_K, "q4_0": syn.Q4_0, "q5_k": syn.Q5_K}[name[:4]]
+            cpus[name] = cpu_gemm(hosts[name], m, seed=8, type_id=tid)
         if moe_inputs is not None:
             log("cpu baseline moe")
             cpus["moe_q4_k_e128_top8_t16"] = cpu_moe(*moe_inputs)

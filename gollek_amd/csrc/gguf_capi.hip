@@ -674,9 +674,10 @@ static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, in
     if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
     if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "input");
     if (y == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "output");
-    if (w->type_id != GOLLEK_HIP_Q8_0 && w->type_id != GOLLEK_HIP_Q4_0 && w->type_id != GOLLEK_HIP_Q4_K)
+    if (w->type_id != GOLLEK_HIP_Q8_0 && w->type_id != GOLLEK_HIP_Q4_0 && w->type_id != GOLLEK_HIP_Q4_K &&
+        w->type_id != GOLLEK_HIP_Q5_K && w->type_id != GOLLEK_HIP_Q6_K)
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
-                    "Unsupported GGUF bf16 GEMM type id: %d (Q8_0, Q4_0 or Q4_K)", w->type_id);
+                    "Unsupported GGUF bf16 GEMM type id: %d (Q8_0, Q4_0, Q4_K, Q5_K or Q6_K)", w->type_id);
     if (w->compact) return compact_unsupported(w, "GEMM", err, err_len);
     if (m < 0 || m > (int64_t)0x7FFFFFFF || w->rows > 0x7FFFFFFF || w->cols > 0x7FFFFFFF)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "GEMM shape %lld x %lld x %lld is out of range",

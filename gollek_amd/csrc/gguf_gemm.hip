@@ -27,6 +27,7 @@
 // gemm_generic_kernel).
 #include <type_traits>
 
+#include "gguf_block_dot.hpp"
 #include "gguf_blocks.hpp"
 #include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"
@@ -530,6 +531,38 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t *__rest
     Y[(int64_t)m * N + n] = acc;
 }
 
+// Q5_K / Q6_K: 16 x 16 outputs per workgroup, one per thread.  Per
+// superblock the 16 X rows' 256 values (as fp32) and the 16 W rows'
+// superblocks are staged in LDS, then each output adds its block's
+// generic_block_dot (the dequantizers' block formulas folded into a dot;
+// gguf_block_dot.hpp) in superblock order.
+template <int T>
+__global__ __launch_bounds__(256) void gemm_kquant_generic_kernel(const uint8_t *__restrict__ W,
+                                                                  int64_t row_bytes,
+                                                                  const uint16_t *__restrict__ X,
+                                                                  float *__restrict__ Y, int M, int N, int K) {
+    constexpr int PB = T == kQ6_K ? 210 : kQ5KBlockBytes;
+    __shared__ float xs[16][kQK];
+    __shared__ uint8_t ws[16][PB];
+    const int n0 = (int)blockIdx.x * 16, m0 = (int)blockIdx.y * 16;
+    const int tid = (int)threadIdx.x, n = tid & 15, m = tid >> 4;
+    float acc = 0.0f;
+    for (int sb = 0; sb < K / kQK; sb++) {
+        __syncthreads();
+        for (int i = tid; i < 16 * kQK; i += 256) {
+            const int r = i / kQK, c = i - r * kQK;
+            xs[r][c] = m0 + r < M ? __uint_as_float((uint32_t)X[(int64_t)(m0 + r) * K + kQK * sb + c] << 16) : 0.0f;
+        }
+        for (int i = tid; i < 16 * PB; i += 256) {
+            const int r = i / PB, c = i - r * PB;
+            ws[r][c] = n0 + r < N ? W[(int64_t)(n0 + r) * row_bytes + (int64_t)PB * sb + c] : (uint8_t)0;
+        }
+        __syncthreads();
+        acc += generic_block_dot(T, ws[n], xs[m]);
+    }
+    if (m0 + m < M && n0 + n < N) Y[(int64_t)(m0 + m) * N + n0 + n] = acc;
+}
+
 namespace {
 
 template <int BM, int BN, int WM, int WN, int WK>
@@ -545,6 +578,7 @@ hipError_t launch_tiled(const uint8_t *w, int64_t row_bytes, const uint16_t *x, 
 
 size_t gemm_workspace_bytes(int type_id, int M, int N, int K) {
     if (type_id == kQ8_0 && M <= 32) return 0;  // the skinny kernel
+    if (type_id == kQ6_K) return 0;  // no split-K
     return gemm_tile_workspace_bytes(type_id, M, N, K);
 }
 
@@ -587,6 +621,16 @@ hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, co
             return launch_tiled<128, 16, 32, 16, 1>(w, row_bytes, x, y, M, N, K, stream);
         if (N % 64 == 0 && K % 64 == 0)
             return launch_tiled<128, 64, 64, 32, 1>(w, row_bytes, x, y, M, N, K, stream);
+    }
+    if (type_id == kQ5_K || type_id == kQ6_K) {
+        const dim3 g16((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+        if (type_id == kQ5_K)
+            hipLaunchKernelGGL(gemm_kquant_generic_kernel<kQ5_K>, g16, dim3(256), 0, stream, w, row_bytes, x, y, M,
+                               N, K);
+        else
+            hipLaunchKernelGGL(gemm_kquant_generic_kernel<kQ6_K>, g16, dim3(256), 0, stream, w, row_bytes, x, y, M,
+                               N, K);
+        return hipGetLastError();
     }
     const int64_t total = (int64_t)M * N;
     const dim3 grid((unsigned)((total + 255) / 256)), block(256);

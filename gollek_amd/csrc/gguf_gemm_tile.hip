@@ -78,6 +78,8 @@ constexpr int kStagePitch = kTileN + 4;        // floats per row of the output s
 //   Q4_0: two 18-byte blocks (36 bytes; 3 chunks, 12 unused)
 //   Q4_K: the superblock header (16 bytes: d, dmin, 12 scale bytes) and the
 //         32 quant bytes of the stage's chunk c (sub-blocks 2c, 2c + 1)
+//   Q5_K: the header, the superblock's 32 qh bytes (bits 2c, 2c + 1 are the
+//         chunk's fifth bits) and the chunk's 32 quant bytes (80 bytes)
 template <int T>
 struct RawW;
 template <>
@@ -91,6 +93,10 @@ struct RawW<kQ4_0> {
 template <>
 struct RawW<kQ4_K> {
     static constexpr int kChunks = 3, kStageBytes = 0, kSlots = 6;  // 144 bytes per four stages
+};
+template <>
+struct RawW<kQ5_K> {
+    static constexpr int kChunks = 5, kStageBytes = 0, kSlots = 6;  // 176 bytes per four stages
 };
 
 // Geometry of a 16 MT x 128 tile: MT row tiles of 16 rows of X.  Tiles of
@@ -109,7 +115,7 @@ struct TileGeom {
     static constexpr int kDeep = (160 * 1024 / kSlot) < (63 / kLoads + 2) ? (160 * 1024 / kSlot) : (63 / kLoads + 2);
     static constexpr int kSlots = MT == 8 ? RawW<T>::kSlots : (kDeep < 8 ? kDeep : 8);
     static constexpr int kRing = kSlots * kSlot;
-    static constexpr bool kMins = T == kQ4_K;
+    static constexpr bool kMins = T == kQ4_K || T == kQ5_K;
     static_assert(kRing <= 160 * 1024, "LDS budget");
     static_assert(kLoads * (kSlots - 2) <= 63, "vmcnt range of the loader waits");
     static_assert(kRing >= 4 * MT * 2 * 1024 && kRing >= kTileM * kStagePitch * 4, "epilogue staging");
@@ -186,8 +192,9 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b) {
 struct Ops {
     u32x4 a[8];
     uint32_t q[2][3], sc[2];  // Q8_0, Q4_0
-    uint2 q2[2];              // Q4_K
-    u32x4 hd[2];              // Q4_K
+    uint2 q2[2];              // Q4_K, Q5_K
+    u32x4 hd[2];              // Q4_K, Q5_K
+    uint2 qh[2];              // Q5_K
 };
 template <int RP>
 __device__ __forceinline__ void ops_read_q32(uint32_t b, uint32_t s, Ops &o) {
@@ -216,6 +223,20 @@ __device__ __forceinline__ void ops_read_q4k(uint32_t b, uint32_t s, Ops &o) {
         : "v"(b), "v"(s), "n"(RP)
         : "memory");
 }
+// Q5_K: ops_read_q4k plus the lane's 8 qh bytes of each column tile (at h).
+template <int RP>
+__device__ __forceinline__ void ops_read_q5k(uint32_t b, uint32_t s, uint32_t h, Ops &o) {
+    asm volatile(
+        "ds_read_b64 %0, %6\n\t"
+        "ds_read_b64 %1, %8\n\t"
+        "ds_read_b128 %2, %7\n\t"
+        "ds_read_b64 %3, %6 offset:%9\n\t"
+        "ds_read_b64 %4, %8 offset:%9\n\t"
+        "ds_read_b128 %5, %7 offset:%9"
+        : "=&v"(o.q2[0]), "=&v"(o.qh[0]), "=&v"(o.hd[0]), "=&v"(o.q2[1]), "=&v"(o.qh[1]), "=&v"(o.hd[1])
+        : "v"(b), "v"(s), "v"(h), "n"(RP)
+        : "memory");
+}
 template <int I>
 __device__ __forceinline__ void ops_read_a(uint32_t a, Ops &o) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(o.a[I]) : "v"(a), "n"(2048 * I) : "memory");
@@ -239,10 +260,10 @@ __device__ __forceinline__ void ops_read_as(uint32_t a, Ops &o) {
 // The raw dwords have arrived (the MT A reads may still be outstanding).
 template <int MT>
 __device__ __forceinline__ void ops_wait_raw(Ops &o) {
-    asm volatile("s_waitcnt lgkmcnt(%12)"
+    asm volatile("s_waitcnt lgkmcnt(%14)"
                  : "+v"(o.q[0][0]), "+v"(o.q[0][1]), "+v"(o.q[0][2]), "+v"(o.sc[0]), "+v"(o.q[1][0]),
                    "+v"(o.q[1][1]), "+v"(o.q[1][2]), "+v"(o.sc[1]), "+v"(o.q2[0]), "+v"(o.q2[1]),
-                   "+v"(o.hd[0]), "+v"(o.hd[1])
+                   "+v"(o.hd[0]), "+v"(o.hd[1]), "+v"(o.qh[0]), "+v"(o.qh[1])
                  : "n"(MT)
                  : "memory");
 }
@@ -310,7 +331,9 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
     // the end read as zeros.
     const int mrows = M - m0 < kTileM ? M - m0 : kTileM;
     const int nrows = N - n0 < kTileN ? N - n0 : kTileN;
-    const int64_t w_split = T == kQ4_K ? (int64_t)(s0 / 4) * 144 : (int64_t)s0 * R::kStageBytes;
+    const int64_t w_split = T == kQ4_K   ? (int64_t)(s0 / 4) * 144
+                            : T == kQ5_K ? (int64_t)(s0 / 4) * kQ5KBlockBytes
+                                         : (int64_t)s0 * R::kStageBytes;
     const __amdgpu_buffer_rsrc_t xr = wave_buffer(
         reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2 + (int64_t)s0 * 128,
         (uint32_t)((int64_t)mrows * K * 2 - (int64_t)s0 * 128));
@@ -343,6 +366,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
             uint32_t off = (uint32_t)row * (uint32_t)row_bytes + (uint32_t)(16 * part);
             if constexpr (T == kQ4_K)
                 off += (uint32_t)(144 * (ls >> 2)) + (part != 0 ? (uint32_t)(32 * (ls & 3)) : 0u);
+            else if constexpr (T == kQ5_K)  // parts 0..2: header, qh; 3, 4: the chunk's quants at 48
+                off += (uint32_t)(kQ5KBlockBytes * (ls >> 2)) + (part >= 3 ? (uint32_t)(32 * (ls & 3)) : 0u);
             else
                 off += (uint32_t)(R::kStageBytes * ls);
             dma16(wr, rs + 1024 * j, off);
@@ -375,13 +400,15 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
         soff = (uint32_t)(16 * kg);
         nsh = 16u * (uint32_t)kg;
     } else {
-        // quant bytes 8 lk .. 8 lk + 7 of the chunk at 16 + 8 lk; header at 0
-        qoff = (uint32_t)(16 + 8 * lk);
+        // quant bytes 8 lk .. 8 lk + 7 of the chunk at 16 + 8 lk (Q5_K: at
+        // 48 + 8 lk, its qh bytes 8 lk .. 8 lk + 7 at 16 + 8 lk); header at 0
+        qoff = (uint32_t)((T == kQ5_K ? 48 : 16) + 8 * lk);
         qsh = 0u;
         soff = 0u;
         nsh = 0u;
     }
-    const int nib = T == kQ4_0 ? 4 * (lk >> 1) : 4 * kg;  // nibble shift (Q4_0, Q4_K)
+    const uint32_t qhoff = (uint32_t)(16 + 8 * lk);       // Q5_K
+    const int nib = T == kQ4_0 ? 4 * (lk >> 1) : 4 * kg;  // nibble shift (Q4_0, Q4_K, Q5_K)
 
     f32x4 acc[MT][2];
 #pragma unroll
@@ -399,6 +426,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
         Ops o;
         if constexpr (T == kQ4_K)
             ops_read_q4k<16 * G::kPitch>(wrow + so + qoff, wrow + so + soff, o);
+        else if constexpr (T == kQ5_K)
+            ops_read_q5k<16 * G::kPitch>(wrow + so + qoff, wrow + so + soff, wrow + so + qhoff, o);
         else
             ops_read_q32<16 * G::kPitch>(wrow + so + qoff, wrow + so + soff, o);
         ops_read_as<MT>(xa + so, o);
@@ -424,8 +453,15 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
             } else {
                 // B holds 128 + q; the 128 sum(x) it adds comes off with the
                 // min term: d (P - 128 sx) - dmin m sx = d P - (dmin m + 128 d) sx.
-                q4x4_bf16_128((o.q2[i].x >> nib) & 0x0F0F0F0Fu, c[0], c[1]);
-                q4x4_bf16_128((o.q2[i].y >> nib) & 0x0F0F0F0Fu, c[2], c[3]);
+                // Q5_K: q's fifth bit is bit 2 c + kg of its qh byte (c = ls & 3).
+                uint32_t lo = (o.q2[i].x >> nib) & 0x0F0F0F0Fu, hi = (o.q2[i].y >> nib) & 0x0F0F0F0Fu;
+                if constexpr (T == kQ5_K) {
+                    const int hb = 2 * (ls & 3) + kg;
+                    lo |= ((o.qh[i].x >> hb) & 0x01010101u) << 4;
+                    hi |= ((o.qh[i].y >> hb) & 0x01010101u) << 4;
+                }
+                q4x4_bf16_128(lo, c[0], c[1]);
+                q4x4_bf16_128(hi, c[2], c[3]);
                 uint32_t scp, mnp;
                 q4k_pair_codes(o.hd[i].y, o.hd[i].z, o.hd[i].w, ls & 3, &scp, &mnp);
                 const uint32_t scj = (scp >> (8 * kg)) & 0xFFu, mj = (mnp >> (8 * kg)) & 0xFFu;
@@ -592,7 +628,7 @@ int tile_splits(int type_id, int M, int N, int K, size_t workspace_bytes) {
 
 bool gemm_tile_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w,
                          const void *x, const void *y) {
-    if (type_id != kQ8_0 && type_id != kQ4_0 && type_id != kQ4_K) return false;
+    if (type_id != kQ8_0 && type_id != kQ4_0 && type_id != kQ4_K && type_id != kQ5_K) return false;
     if (M <= 0 || N <= 0 || K % 256 != 0) return false;
     if (((reinterpret_cast<uintptr_t>(w) | (uintptr_t)row_bytes) & 3u) != 0) return false;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(y) & 15u) != 0) return false;
@@ -639,6 +675,9 @@ hipError_t launch_gemm_tile(int type_id, const uint8_t *w, int64_t row_bytes, co
         break;
     case kQ4_K:
         GOLLEK_TILE_LAUNCH(kQ4_K);
+        break;
+    case kQ5_K:
+        GOLLEK_TILE_LAUNCH(kQ5_K);
         break;
     default:
         return hipErrorInvalidValue;

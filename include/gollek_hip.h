@@ -179,13 +179,13 @@ int32_t gollek_hip_matvec_rows(gollek_hip_weight *weight, const float *x, int64_
 
 /* Y[m, n] = sum_k X[m, k] W[n, k] (Y = X W^T, the Linear convention of
  * runner/safetensor/gollek-safetensor-core/src/main/java/tech/kayys/gollek/
- * safetensor/core/tensor/AccelOps.java:370-376) for a Q8_0, Q4_0 or Q4_K
- * weight, X given as m x cols bf16 bit patterns (row-major), Y m x rows fp32.
- * Small-M prefill and batched decode.  The reference has no GGUF GEMM: it
- * runs m independent RT/GgufTensorOps.matVecRows calls
- * (RT/GgufTensorOps.java:666-674), which this replaces.  x_len < m * cols or
- * y_len < m * rows -> ARG; a weight type other than Q8_0, Q4_0 and Q4_K ->
- * UNSUPPORTED. */
+ * safetensor/core/tensor/AccelOps.java:370-376) for a weight of any type
+ * this library takes (Q8_0, Q4_0, Q4_K and Q5_K on the matrix cores; Q6_K
+ * on an fp32 kernel of the dequantizers' block formulas), X given as
+ * m x cols bf16 bit patterns (row-major), Y m x rows fp32.  Small-M prefill
+ * and batched decode.  The reference has no GGUF GEMM: it runs m independent
+ * RT/GgufTensorOps.matVecRows calls (RT/GgufTensorOps.java:666-674), which
+ * this replaces.  x_len < m * cols or y_len < m * rows -> ARG. */
 int32_t gollek_hip_gemm_bf16(gollek_hip_weight *weight, const uint16_t *x_bf16, int64_t x_len,
                              int64_t m, float *y, int64_t y_len, char *err, size_t err_len);
 

@@ -1,5 +1,5 @@
-"""GPU parity of the Q8_0 / Q4_0 / Q4_K x bf16 MFMA GEMM (small-M prefill /
-batched decode).
+"""GPU parity of the Q8_0 / Q4_0 / Q4_K / Q5_K x bf16 MFMA GEMM and the Q6_K
+fp32 GEMM (small-M prefill / batched decode).
 
 Bar: rel_err <= 1e-2 against the fp64 product of the bf16 activations and the
 bit-exact dequantized weights (the quants are contracted exactly and each
@@ -65,8 +65,9 @@ def test_gemm_odd_shapes(rows, cols, m):
     t.close()
 
 
-MATRIX = {syn.Q8_0: syn.q8_0_matrix, syn.Q4_0: syn.q4_0_matrix, syn.Q4_K: syn.q4_k_matrix}
-TYPES = [syn.Q8_0, syn.Q4_0, syn.Q4_K]
+MATRIX = {syn.Q8_0: syn.q8_0_matrix, syn.Q4_0: syn.q4_0_matrix, syn.Q4_K: syn.q4_k_matrix,
+          syn.Q5_K: syn.q5_k_matrix}
+TYPES = [syn.Q8_0, syn.Q4_0, syn.Q4_K, syn.Q5_K]
 
 
 def _gemm_case(type_id, rows, cols, m, seed):
@@ -110,10 +111,10 @@ def test_gemm_tile_kernel_small_m(type_id, rows, cols, m):
     assert err <= GEMM_TOL
 
 
-@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K])
+@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K, syn.Q5_K])
 @pytest.mark.parametrize("m", [16, 128, 512])
 def test_gemm_q4_parity_14336(type_id, m):
-    # Q4_0 / Q4_K weights at the FFN shape K = 4096, N = 14336.
+    # Q4_0 / Q4_K / Q5_K weights at the FFN shape K = 4096, N = 14336.
     print(f"[gpu] gemm q4 type={type_id} m={m} 14336x4096", flush=True)
     y, ref = _gemm_case(type_id, 14336, 4096, m, seed=1400 + m)
     err = o.rel_err(y, ref)
@@ -189,12 +190,45 @@ def test_gemm_split_k_shapes(rows, cols, m):
     t.close()
 
 
-def test_gemm_rejects_other_types_and_short_buffers():
-    data = syn.q6_k_matrix(16, 256, seed=1)
-    t = ops.GgufTensor("w", (256, 16), syn.Q6_K, data.reshape(-1))
-    with pytest.raises(ops.UnsupportedOperationError):
-        ops.gemm_bf16(t, np.zeros((2, 256), np.uint16), np.zeros((2, 16), np.float32))
+# Q6_K weights (the Q6_K tensors of Q4_K_M files), and Q5_K where the tile
+# kernel does not take the call: the fp32 kernel of the dequantizers' block
+# formulas, 16 x 16 outputs per workgroup, with partial tiles on both sides.
+@pytest.mark.parametrize("tid,rows,cols,m", [(syn.Q6_K, 4096, 4096, 16), (syn.Q6_K, 33, 768, 1),
+                                             (syn.Q6_K, 1024, 4096, 128), (syn.Q6_K, 100, 512, 37)])
+def test_gemm_q5_k_q6_k(tid, rows, cols, m):
+    print(f"[gpu] gemm type={tid} rows={rows} cols={cols} m={m}", flush=True)
+    data = syn.matrix(tid, rows, cols, rows + cols + m)
+    t = ops.GgufTensor("w", (cols, rows), tid, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=m + 31)
+    y = np.full((m, rows), np.nan, np.float32)
+    ops.gemm_bf16(t, x, y)
     t.close()
+    err = o.rel_err(y, o.gemm_reference(tid, data, cols, x))
+    print(f"[gpu] gemm type={tid} rel_err={err:.3e}", flush=True)
+    assert err <= GEMM_TOL
+
+
+def test_gemm_q5_k_unaligned_x_takes_the_fp32_kernel():
+    # x 2 bytes past a 16-byte boundary: the tile kernel's loads need 16, so
+    # the device entry runs the fp32 kernel, with the same values.
+    import torch
+    rows, cols, m = 272, 1024, 9
+    data = syn.q5_k_matrix(rows, cols, seed=77)
+    x = syn.activation_bf16(m, cols, seed=78)
+    w_dev = torch.from_numpy(data.reshape(-1)).cuda()
+    dw = ops.DeviceWeight(syn.Q5_K, w_dev.data_ptr(), rows, cols)
+    try:
+        buf = torch.zeros(m * cols + 8, dtype=torch.int16, device="cuda")
+        buf[1:1 + m * cols] = torch.from_numpy(x.view(np.int16).reshape(-1)).cuda()
+        y_dev = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+        dw.gemm_bf16(buf.data_ptr() + 2, m, y_dev.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert o.rel_err(y_dev.cpu().numpy(), o.gemm_reference(syn.Q5_K, data, cols, x)) <= GEMM_TOL
+    finally:
+        dw.close()
+
+
+def test_gemm_rejects_short_buffers():
     data = syn.q8_0_matrix(16, 64, seed=1)
     t = ops.GgufTensor("w", (64, 16), syn.Q8_0, data.reshape(-1))
     with pytest.raises(ops.IllegalArgumentError):
@@ -247,7 +281,8 @@ def test_gemm_device_entry_split_k_workspace(m):
         dw.close()
 
 
-@pytest.mark.parametrize("type_id,rows,m", [(syn.Q8_0, 4096, 512), (syn.Q4_K, 4096, 512), (syn.Q4_0, 2048, 1024)])
+@pytest.mark.parametrize("type_id,rows,m", [(syn.Q8_0, 4096, 512), (syn.Q4_K, 4096, 512), (syn.Q4_0, 2048, 1024),
+                                           (syn.Q5_K, 4096, 128)])
 def test_gemm_two_split_repeatable(type_id, rows, m):
     # Two K splits added in split order by the reduction kernel: the same
     # bits on every call, within the bar of the oracle, on repeated calls
