@@ -78,10 +78,11 @@ def parse() -> argparse.Namespace:
 class Rotation:
     """Device copies of one packed weight matrix, launched round robin."""
 
-    def __init__(self, torch, host_bytes, type_id: int, rows: int, cols: int, prepared: bool = False):
+    def __init__(self, torch, host_bytes, type_id: int, rows: int, cols: int, prepared: bool = False,
+                 copies: int = 0):
         from gollek_amd import tensor_ops as ops
         nbytes = host_bytes.size
-        self.copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
+        self.copies = copies or max(2, math.ceil(ROTATION_BYTES / nbytes))
         base = torch.from_numpy(host_bytes.reshape(-1)).cuda()
         self.buffers = [base] + [base.clone() for _ in range(self.copies - 1)]
         self.weights = [ops.DeviceWeight(type_id, b.data_ptr(), rows, cols) for b in self.buffers]
@@ -174,10 +175,10 @@ def graph_time(torch, launch, copies: int, steps: int, warmup: int):
 # ---- workloads ----------------------------------------------------------------
 
 def gemv_workload(torch, type_id: int, rows: int, cols: int, steps: int, warmup: int, seed: int,
-                  prepared: bool = True):
+                  prepared: bool = True, copies: int = 0):
     from gollek_amd import synthetic as syn
     host = syn.matrix(type_id, rows, cols, seed)
-    rot = Rotation(torch, host, type_id, rows, cols, prepared)
+    rot = Rotation(torch, host, type_id, rows, cols, prepared, copies)
     x = torch.from_numpy(syn.activation(cols, seed + 1)).cuda()
     y = torch.empty(rows, dtype=torch.float32, device="cuda")
 
@@ -222,11 +223,14 @@ def gemm_workload(torch, m: int, steps: int, warmup: int, seed: int, type_id: in
 
 
 def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048, 768, 16),
-                 copies: int = 3, routed: bool = True, types=None):
+                 copies: int = 3, routed: bool = True, types=None, global_experts: int = 0):
     """Grouped expert FFN, shape (experts, top_k, hidden, inter, tokens),
     expert types (gate, up, down) (default Q4_K); with `routed`, also the
     routed block (router -> top-k -> the same FFN).  Weights rotate over
-    `copies` whole layers."""
+    `copies` whole layers.  global_experts > experts: one GPU's share of an
+    expert-parallel layer -- the routes are drawn over the global experts
+    and those outside this GPU's (the first `experts`) carry id -1, which
+    the grouped FFN skips."""
     import numpy as np
 
     from gollek_amd import synthetic as syn
@@ -236,7 +240,8 @@ def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048,
     gate = syn.matrix(tg, E * I, H, seed)
     up = syn.matrix(tu, E * I, H, seed + 1)
     down = syn.matrix(td, E * H, I, seed + 2)
-    ids, w = syn.moe_routing(T, E, k, seed + 3)
+    ids, w = syn.moe_routing(T, global_experts or E, k, seed + 3)
+    ids = np.where(ids < E, ids, -1).astype(np.int32)
     x = syn.activation(T * H, seed + 4).reshape(T, H)
     # At 128 x 2048 x 768, three copies of the whole layer (3 x 340 MB): a copy
     # is reused only after the other two layers' touched experts (> 400 MB)
@@ -261,12 +266,15 @@ def moe_workload(torch, steps: int, warmup: int, seed: int, shape=(128, 8, 2048,
                                out.data_ptr(), ws.data_ptr(), ws_bytes, stream)
 
     ms, n = graph_time(torch, launch, copies, steps, warmup)
-    used = len(np.unique(ids))
+    used = len(np.unique(ids[ids >= 0]))
     bytes_used = used * (gate.size // E + up.size // E + down.size // E) + 2 * T * H * 4
     res = {"ms_per_step": ms, "steps": n, "experts_touched": int(used),
            "algo_bytes": int(bytes_used), "algo_gbs": bytes_used / (ms * 1e-3) / 1e9,
            "hbm_frac": bytes_used / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-           "shape": {"experts": E, "top_k": k, "hidden": H, "inter": I, "tokens": T}}
+           "shape": {"experts": E, "top_k": k, "hidden": H, "inter": I, "tokens": T},
+           "routes": int((ids >= 0).sum())}
+    if global_experts:
+        res["shape"]["global_experts"] = global_experts
     if not routed:
         for _, handles in layers:
             for h in handles:
@@ -625,6 +633,24 @@ def main() -> int:
             r, _ = gemv_workload(torch, syn.Q4_K, 14336, 4096, args.steps, args.warmup, seed=2, prepared=False)
             r["hbm_frac"] = r["weight_gbs"] / HBM_PEAK_GBS
             extra["q4_k_gemv_4096x14336_gguf_layout"] = r
+        # One GPU's share of a sharded layer: the headline matrix at 8-way
+        # tensor parallelism (1792 of its 14336 rows, 4.13 MB) streamed from
+        # HBM over a rotation of copies and, as a sharded layer would run it,
+        # resident in the Infinity Cache (two copies); and one of 8
+        # expert-parallel GPUs of the MoE layer (16 of 128 experts, only the
+        # routes to them).
+        if want("q4_k_gemv_4096x1792_tp8_share"):
+            log("extra q4_k_gemv_4096x1792_tp8_share")
+            r, _ = gemv_workload(torch, syn.Q4_K, 1792, 4096, args.steps, args.warmup, seed=2)
+            r["hbm_frac"] = r["weight_gbs"] / HBM_PEAK_GBS
+            r["mall_resident"], _ = gemv_workload(torch, syn.Q4_K, 1792, 4096, args.steps, args.warmup,
+                                                  seed=2, copies=2)
+            extra["q4_k_gemv_4096x1792_tp8_share"] = r
+        if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e16_of_128_ep8_share"):
+            log("extra moe_q4_k_e16_of_128_ep8_share")
+            extra["moe_q4_k_e16_of_128_ep8_share"], _ = moe_workload(
+                torch, args.steps, args.warmup, seed=11, shape=(16, 8, 2048, 768, 16), copies=24,
+                routed=False, global_experts=128)
         have_gemm = hasattr(ops.DeviceWeight, "gemm_bf16") and _has_symbol("gollek_hip_gemm_bf16_device")
         for m in (16, 128, 512):
             name = f"q8_0_gemm_bf16_m{m}_4096x4096"
