@@ -150,9 +150,9 @@ hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uin
                                float *out, uint8_t *ws, hipStream_t stream);
 // K-quant experts on the matrix-core passes (gguf_moe_mfma.hip): gate / up
 // both Q4_K or both Q5_K (hidden up to 4096); down rows
-// Q4_K or Q6_K through the token-major pass (inter up to 1024), else Q4_K or
-// Q5_K through the expert-major pass; hidden and inter multiples of 256, x
-// 16-byte aligned.
+// Q4_K, Q5_K or Q6_K through the token-major pass (inter up to 1024), else
+// Q4_K or Q5_K through the expert-major pass; hidden and inter multiples of
+// 256, x 16-byte aligned.
 bool moe_kq_mfma_supported(int gate_type, int down_type, int E, int H, int I, int T, int top_k,
                            const float *x);
 hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate, const uint8_t *up,

@@ -16,9 +16,9 @@
 //     superblock w; h = silu(g) u per route and row.
 //   pass 1 (down): item = (used expert, RT (at most 16 / nsb, as a slot
 //     holds) 16-row tiles of its H rows, route group); wave w = (row tile
-//     w / nsb, superblock w % nsb).  With inter sizes up to 1024 and Q4_K or
-//     Q6_K down rows, pass 0 leaves h as digit records and the token-major
-//     moe_down_combine_kernel replaces pass 1 and the combine.
+//     w / nsb, superblock w % nsb).  With inter sizes up to 1024 and Q4_K,
+//     Q5_K or Q6_K down rows, pass 0 leaves h as digit records and the
+//     token-major moe_down_combine_kernel replaces pass 1 and the combine.
 // The K-quant contraction is the one of gguf_gemv_mfma.hip's kernels
 // (v_mfma_i32_16x16x64_i8 over balanced 22-bit digits of the vector, low and
 // high nibbles as bytes 0..15, Q5_K's fifth bits from qh added as bit 4),
@@ -961,16 +961,18 @@ constexpr int kMdRoutes = 64;  // routes per workgroup
 constexpr int kMdSlots = 2;    // tile and route slots per wave (units in flight + 1)
 
 constexpr int kQ6KBlockBytes = 210;
-// Down rows: Q4_K at a pitch of odd 16-byte units (the 16 rows' reads spread
-// over the banks); Q6_K (Q6) packed as stored: a 16-row tile of 210-byte
-// superblocks is one contiguous, 16-byte aligned run (16 x 210 = 3360).
-constexpr uint32_t md_row_bytes(int nsb, bool q6) { return nsb * (q6 ? kQ6KBlockBytes : kQKBlockBytes); }
-constexpr uint32_t md_pitch(int nsb, bool q6) {
-    return q6 || (md_row_bytes(nsb, false) / 16) % 2 == 1 ? md_row_bytes(nsb, q6) : md_row_bytes(nsb, q6) + 16;
+// Down rows (type dt): Q4_K and Q5_K at a pitch of odd 16-byte units (the 16
+// rows' reads spread over the banks); Q6_K packed as stored: a 16-row tile of
+// 210-byte superblocks is one contiguous, 16-byte aligned run (16 x 210 = 3360).
+constexpr uint32_t md_row_bytes(int nsb, int dt) {
+    return nsb * (dt == kQ6_K ? kQ6KBlockBytes : dt == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes);
+}
+constexpr uint32_t md_pitch(int nsb, int dt) {
+    return dt == kQ6_K || (md_row_bytes(nsb, dt) / 16) % 2 == 1 ? md_row_bytes(nsb, dt) : md_row_bytes(nsb, dt) + 16;
 }
 // A slot's bytes move as whole kilobytes (16 bytes a lane) plus a tail of
 // 256-byte loads (4 bytes a lane), so slots take no more LDS than they hold.
-constexpr int md_tile_bytes(int nsb, bool q6) { return 16 * (int)md_pitch(nsb, q6); }
+constexpr int md_tile_bytes(int nsb, int dt) { return 16 * (int)md_pitch(nsb, dt); }
 constexpr int md_route_bytes(int nsb) { return nsb * 16 * kRecDwords * 4; }
 constexpr int md_full(int bytes) { return bytes / 1024; }
 constexpr int md_tail(int bytes) { return (bytes % 1024 + 255) / 256; }
@@ -984,6 +986,7 @@ struct MdSb {
     u32x4 hv;
     uint2 qb[4], xl[4], xh[4];
     float2 xp[4];
+    uint2 qh;  // Q5_K: the lane's 8 qh bytes
 };
 // Reads of superblock s for one asm statement (named operands, so one
 // statement can read every superblock of a unit and wait once).
@@ -1039,9 +1042,67 @@ __device__ __forceinline__ void md_read_unit(MdSb (&o)[NSB], uint32_t a_h, uint3
                      : MD_SB_INS(0), MD_SB_INS(1), MD_SB_INS(2), MD_SB_INS(3)
                      : "memory");
 }
+// Q5_K: the same reads of superblock s plus the lane's qh bytes (at the
+// quant address of a Q4_K row; the quants 32 bytes later).
+#define MD5_SB_READS(s)                                                                            \
+    "ds_read_b128 %[hv" #s "], %[th" #s "]\n\t"                                                   \
+    "ds_read_b64 %[qh" #s "], %[tq" #s "]\n\t"                                                    \
+    "ds_read_b64 %[qa" #s "], %[tq" #s "] offset:32\n\t"                                          \
+    "ds_read_b64 %[qb" #s "], %[tq" #s "] offset:64\n\t"                                          \
+    "ds_read_b64 %[qc" #s "], %[tq" #s "] offset:96\n\t"                                          \
+    "ds_read_b64 %[qd" #s "], %[tq" #s "] offset:128\n\t"                                         \
+    "ds_read_b64 %[la" #s "], %[rl" #s "]\n\t"                                                    \
+    "ds_read_b64 %[lb" #s "], %[rl" #s "] offset:224\n\t"                                         \
+    "ds_read_b64 %[lc" #s "], %[rl" #s "] offset:448\n\t"                                         \
+    "ds_read_b64 %[ld" #s "], %[rl" #s "] offset:672\n\t"                                         \
+    "ds_read_b64 %[ha" #s "], %[rh" #s "]\n\t"                                                    \
+    "ds_read_b64 %[hb" #s "], %[rh" #s "] offset:224\n\t"                                         \
+    "ds_read_b64 %[hc" #s "], %[rh" #s "] offset:448\n\t"                                         \
+    "ds_read_b64 %[hd" #s "], %[rh" #s "] offset:672\n\t"                                         \
+    "ds_read_b64 %[pa" #s "], %[rp" #s "]\n\t"                                                    \
+    "ds_read_b64 %[pb" #s "], %[rp" #s "] offset:224\n\t"                                         \
+    "ds_read_b64 %[pc" #s "], %[rp" #s "] offset:448\n\t"                                         \
+    "ds_read_b64 %[pd" #s "], %[rp" #s "] offset:672\n\t"
+#define MD5_SB_OUTS(s)                                                                             \
+    [hv##s] "=&v"(o[s].hv), [qa##s] "=&v"(o[s].qb[0]), [qb##s] "=&v"(o[s].qb[1]),                  \
+        [qc##s] "=&v"(o[s].qb[2]), [qd##s] "=&v"(o[s].qb[3]), [la##s] "=&v"(o[s].xl[0]),            \
+        [lb##s] "=&v"(o[s].xl[1]), [lc##s] "=&v"(o[s].xl[2]), [ld##s] "=&v"(o[s].xl[3]),            \
+        [ha##s] "=&v"(o[s].xh[0]), [hb##s] "=&v"(o[s].xh[1]), [hc##s] "=&v"(o[s].xh[2]),            \
+        [hd##s] "=&v"(o[s].xh[3]), [pa##s] "=&v"(o[s].xp[0]), [pb##s] "=&v"(o[s].xp[1]),            \
+        [pc##s] "=&v"(o[s].xp[2]), [pd##s] "=&v"(o[s].xp[3]), [qh##s] "=&v"(o[s].qh)
+#define MD5_SB_INS(s)                                                                              \
+    [th##s] "v"(a_h + s * kQ5KBlockBytes), [tq##s] "v"(a_q + s * kQ5KBlockBytes),                     \
+        [rl##s] "v"(a_lo + s * lo_step), [rh##s] "v"(a_hi + s * hi_step), [rp##s] "v"(a_p + s * 896u)
+
+// Every LDS operand of a Q5_K unit, then one wait.
+template <int NSB>
+__device__ __forceinline__ void md_read_unit5(MdSb (&o)[NSB], uint32_t a_h, uint32_t a_q, uint32_t a_lo,
+                                             uint32_t lo_step, uint32_t a_hi, uint32_t hi_step, uint32_t a_p) {
+    static_assert(16 * 4 * kRecDwords == 896 && 4 * 4 * kRecDwords == 224, "record strides");
+    if constexpr (NSB == 1)
+        asm volatile(MD5_SB_READS(0) "s_waitcnt lgkmcnt(0)" : MD5_SB_OUTS(0) : MD5_SB_INS(0) : "memory");
+    else if constexpr (NSB == 2)
+        asm volatile(MD5_SB_READS(0) MD5_SB_READS(1) "s_waitcnt lgkmcnt(0)"
+                     : MD5_SB_OUTS(0), MD5_SB_OUTS(1)
+                     : MD5_SB_INS(0), MD5_SB_INS(1)
+                     : "memory");
+    else if constexpr (NSB == 3)
+        asm volatile(MD5_SB_READS(0) MD5_SB_READS(1) MD5_SB_READS(2) "s_waitcnt lgkmcnt(0)"
+                     : MD5_SB_OUTS(0), MD5_SB_OUTS(1), MD5_SB_OUTS(2)
+                     : MD5_SB_INS(0), MD5_SB_INS(1), MD5_SB_INS(2)
+                     : "memory");
+    else
+        asm volatile(MD5_SB_READS(0) MD5_SB_READS(1) MD5_SB_READS(2) MD5_SB_READS(3) "s_waitcnt lgkmcnt(0)"
+                     : MD5_SB_OUTS(0), MD5_SB_OUTS(1), MD5_SB_OUTS(2), MD5_SB_OUTS(3)
+                     : MD5_SB_INS(0), MD5_SB_INS(1), MD5_SB_INS(2), MD5_SB_INS(3)
+                     : "memory");
+}
 #undef MD_SB_READS
 #undef MD_SB_OUTS
 #undef MD_SB_INS
+#undef MD5_SB_READS
+#undef MD5_SB_OUTS
+#undef MD5_SB_INS
 
 // Lane 0 takes the next index from an LDS counter for the wave.
 __device__ __forceinline__ int wave_grab(int *counter) {
@@ -1056,17 +1117,19 @@ struct MoeDownGeom {
     uint32_t w_bytes, h_bytes;   // ranges: stacked down weights; h records
 };
 
-template <int NSB, bool Q6>
+// DT: the down rows' type (Q4_K, Q5_K or Q6_K).
+template <int NSB, int DT>
 __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
     const uint8_t *__restrict__ down, MoeDownGeom G, const uint8_t *__restrict__ hrec,
     const int32_t *__restrict__ ids, const float *__restrict__ wts, int T, int top_k, int H, int E,
     float *__restrict__ out) {
-    constexpr uint32_t kRowBytes = md_row_bytes(NSB, Q6), kPitch = md_pitch(NSB, Q6);
+    constexpr bool Q6 = DT == kQ6_K, Q5 = DT == kQ5_K;
+    constexpr uint32_t kRowBytes = md_row_bytes(NSB, DT), kPitch = md_pitch(NSB, DT);
     constexpr uint32_t kRecBytes = md_route_bytes(NSB);  // one route's records
-    constexpr int kTF = md_full(md_tile_bytes(NSB, Q6)), kTT = md_tail(md_tile_bytes(NSB, Q6));
+    constexpr int kTF = md_full(md_tile_bytes(NSB, DT)), kTT = md_tail(md_tile_bytes(NSB, DT));
     constexpr int kRF = md_full(md_route_bytes(NSB)), kRT = md_tail(md_route_bytes(NSB));
     constexpr int kUnitLoads = kTF + kTT + kRF + kRT;  // every unit issues exactly this many
-    constexpr uint32_t kTileSlot = md_slot(md_tile_bytes(NSB, Q6)), kRouteSlot = md_slot(md_route_bytes(NSB));
+    constexpr uint32_t kTileSlot = md_slot(md_tile_bytes(NSB, DT)), kRouteSlot = md_slot(md_route_bytes(NSB));
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // sink, then waves x wave_bytes
     __shared__ float ys[kMdRoutes][16];
     __shared__ float rw[kMdRoutes];
@@ -1249,7 +1312,10 @@ __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
         const uint32_t lo_step = lo_live ? 16u * 4 * kRecDwords : 0u, hi_step = hi_live ? 16u * 4 * kRecDwords : 0u;
         const uint32_t a_p0 = rb + 4 * kRecDwords * g + 48;
         MdSb o[NSB];
-        md_read_unit<NSB>(o, a_h0, a_q0, a_lo0, lo_step, a_hi0, hi_step, a_p0);
+        if constexpr (Q5)
+            md_read_unit5<NSB>(o, a_h0, a_q0, a_lo0, lo_step, a_hi0, hi_step, a_p0);
+        else
+            md_read_unit<NSB>(o, a_h0, a_q0, a_lo0, lo_step, a_hi0, hi_step, a_p0);
         // every superblock's products first, then their epilogues
         i32x4 Dall[NSB][4];
 #pragma unroll
@@ -1257,8 +1323,16 @@ __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const uint2 qv = o[s].qb[c];
-                const i32x4 B = {(int)(qv.x & 0x0F0F0F0Fu), (int)(qv.y & 0x0F0F0F0Fu),
-                                 (int)((qv.x >> 4) & 0x0F0F0F0Fu), (int)((qv.y >> 4) & 0x0F0F0F0Fu)};
+                uint32_t b0 = qv.x & 0x0F0F0F0Fu, b1 = qv.y & 0x0F0F0F0Fu;
+                uint32_t b2 = (qv.x >> 4) & 0x0F0F0F0Fu, b3 = (qv.y >> 4) & 0x0F0F0F0Fu;
+                if constexpr (Q5) {  // fifth bits: bit 2 c (low nibbles), 2 c + 1 (high) of qh
+                    const uint2 hq = o[s].qh;
+                    b0 |= ((hq.x >> (2 * c)) & 0x01010101u) << 4;
+                    b1 |= ((hq.y >> (2 * c)) & 0x01010101u) << 4;
+                    b2 |= ((hq.x >> (2 * c + 1)) & 0x01010101u) << 4;
+                    b3 |= ((hq.y >> (2 * c + 1)) & 0x01010101u) << 4;
+                }
+                const i32x4 B = {(int)b0, (int)b1, (int)b2, (int)b3};
                 const i32x4 A = {(int)o[s].xl[c].x, (int)o[s].xl[c].y, (int)o[s].xh[c].x, (int)o[s].xh[c].y};
                 Dall[s][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero4, 0, 0, 0);
             }
@@ -1499,12 +1573,12 @@ MoeTileGeom make_geom(int mode, int E, int H, int I, int type) {
 constexpr int kMdStaticLds = kMdRoutes * (16 * 4 + 4 + 4 + 4 + 8) + 16;  // ys, rw, rok, it_e, it_mask, counters
 constexpr int kLdsBytes = 163840;
 
-bool make_down_geom(int E, int H, int I, int T, int top_k, bool q6, MoeDownGeom &g, int &waves) {
+bool make_down_geom(int E, int H, int I, int T, int top_k, int dt, MoeDownGeom &g, int &waves) {
     const int nsb = I / kQK;
     if (nsb < 1 || nsb > 4 || top_k < 1 || top_k > kMdRoutes || H % 16 != 0) return false;
-    g.wave_bytes = (uint32_t)(kMdSlots * (md_slot(md_tile_bytes(nsb, q6)) + md_slot(md_route_bytes(nsb))));
+    g.wave_bytes = (uint32_t)(kMdSlots * (md_slot(md_tile_bytes(nsb, dt)) + md_slot(md_route_bytes(nsb))));
     g.tg = kMdRoutes / top_k;
-    const int64_t w_bytes = (int64_t)E * H * md_row_bytes(nsb, q6);
+    const int64_t w_bytes = (int64_t)E * H * md_row_bytes(nsb, dt);
     const int64_t h_bytes = (int64_t)T * top_k * (I / 16) * kRecDwords * 4;
     if (w_bytes >= (int64_t)kMaskedOffset || h_bytes >= (int64_t)kMaskedOffset) return false;
     g.w_bytes = (uint32_t)w_bytes;
@@ -1528,10 +1602,10 @@ bool tile_pass_ok(int mode, int E, int H, int I, int type) {
     return g.ndma <= max_dma(type) && g.w_bytes < (int64_t)kMaskedOffset && 2 * kMoGroup * 16 * g.rt <= kMoOutCap;
 }
 
-// The token-major down pass takes Q4_K and Q6_K rows where its geometry fits.
+// The token-major down pass takes Q4_K, Q5_K and Q6_K rows where its geometry fits.
 bool token_major_down(int down_type, int E, int H, int I, int T, int top_k, MoeDownGeom &gd, int &waves) {
-    return (down_type == kQ4_K || down_type == kQ6_K) &&
-           make_down_geom(E, H, I, T, top_k, down_type == kQ6_K, gd, waves);
+    return (down_type == kQ4_K || down_type == kQ5_K || down_type == kQ6_K) &&
+           make_down_geom(E, H, I, T, top_k, down_type, gd, waves);
 }
 
 }  // namespace
@@ -1584,7 +1658,6 @@ hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate,
     default: gate_up(&moe_expert_tile_kernel<0, true, 2, kQ5_K>); break;
     }
     if (rec) {
-        const bool q6 = down_type == kQ6_K;
         const dim3 dgrid((unsigned)(H / 16), (unsigned)((T + gd.tg - 1) / gd.tg));
         const size_t lds = 1024 + (size_t)waves * gd.wave_bytes;
         const uint8_t *hrec = ws + L.h;
@@ -1598,15 +1671,19 @@ hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate,
                                H, E, out);
             return hipGetLastError();
         };
-        switch (I / kQK + (q6 ? 4 : 0)) {
-        case 1: return run(&moe_down_combine_kernel<1, false>);
-        case 2: return run(&moe_down_combine_kernel<2, false>);
-        case 3: return run(&moe_down_combine_kernel<3, false>);
-        case 4: return run(&moe_down_combine_kernel<4, false>);
-        case 5: return run(&moe_down_combine_kernel<1, true>);
-        case 6: return run(&moe_down_combine_kernel<2, true>);
-        case 7: return run(&moe_down_combine_kernel<3, true>);
-        default: return run(&moe_down_combine_kernel<4, true>);
+        switch (I / kQK + (down_type == kQ6_K ? 4 : down_type == kQ5_K ? 8 : 0)) {
+        case 1: return run(&moe_down_combine_kernel<1, kQ4_K>);
+        case 2: return run(&moe_down_combine_kernel<2, kQ4_K>);
+        case 3: return run(&moe_down_combine_kernel<3, kQ4_K>);
+        case 4: return run(&moe_down_combine_kernel<4, kQ4_K>);
+        case 5: return run(&moe_down_combine_kernel<1, kQ6_K>);
+        case 6: return run(&moe_down_combine_kernel<2, kQ6_K>);
+        case 7: return run(&moe_down_combine_kernel<3, kQ6_K>);
+        case 8: return run(&moe_down_combine_kernel<4, kQ6_K>);
+        case 9: return run(&moe_down_combine_kernel<1, kQ5_K>);
+        case 10: return run(&moe_down_combine_kernel<2, kQ5_K>);
+        case 11: return run(&moe_down_combine_kernel<3, kQ5_K>);
+        default: return run(&moe_down_combine_kernel<4, kQ5_K>);
         }
     }
     float *ypair = reinterpret_cast<float *>(ws + L.ypair);

@@ -83,14 +83,16 @@ def test_moe_q6_k_down_parity(E, H, I, T, k):
 
 # Q5_K gate / up on the matrix-core passes (Q5_K_M / Q5_K_S layers; their
 # ring has two 46 KB slots): hidden 512 .. 2048 in one half, 3072 cut into
-# K-halves of 6 superblocks; down rows Q6_K / Q4_K on the token-major pass,
-# Q5_K on the expert-major pass (2 to 8 row tiles per item); Q4_K gate / up
-# with Q5_K down; the even split at 300 tokens x top-2.
+# K-halves of 6 superblocks; down rows Q6_K / Q4_K / Q5_K on the token-major
+# pass (inter 256 .. 1024), Q5_K on the expert-major pass past that (2 to 8
+# row tiles per item); Q4_K gate / up with Q5_K down; the even split at 300
+# tokens x top-2.
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q5_K, syn.Q6_K, 128, 2048, 768, 16, 8), (syn.Q5_K, syn.Q5_K, 128, 2048, 768, 16, 8),
     (syn.Q5_K, syn.Q4_K, 16, 1536, 512, 9, 4), (syn.Q5_K, syn.Q5_K, 8, 3072, 1536, 9, 2),
     (syn.Q5_K, syn.Q5_K, 32, 512, 256, 300, 2), (syn.Q4_K, syn.Q5_K, 16, 1024, 1280, 9, 4),
-    (syn.Q5_K, syn.Q6_K, 8, 2048, 1024, 40, 2)])
+    (syn.Q5_K, syn.Q6_K, 8, 2048, 1024, 40, 2), (syn.Q4_K, syn.Q5_K, 16, 1024, 1024, 40, 2),
+    (syn.Q5_K, syn.Q5_K, 8, 1024, 512, 9, 4)])
 def test_moe_q5_k_parity(gt, dt, E, H, I, T, k):
     print(f"[gpu] moe q5_k gate={gt} down={dt} E={E} H={H} I={I} T={T} k={k}", flush=True)
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + I + 2, down_type=dt, gate_type=gt)
