@@ -8,7 +8,8 @@ oracle.  Calls in a row on one handle, each with fewer rows of X than the
 one before, all split over K so all use the scratch, and none may read an
 earlier call's partials: Q8_0 at 4096 rows (m = 512 with two splits, the
 others with more), Q4_K at 14336 rows (m = 128 in 128-row tiles, m = 16 in
-16-row tiles) and Q4_0 at 4096 rows (m = 300, then 20 in 32-row tiles).
+16-row tiles), Q4_0 at 4096 rows (m = 300, then 20 in 32-row tiles) and
+Q5_K at 4096 rows (m = 64, then 16); Q6_K (the fp32 kernel, no split) too.
 """
 import ctypes
 
@@ -27,7 +28,9 @@ GEMM_TOL = 1e-2
 
 @pytest.mark.parametrize("type_id,rows,cols,ms", [(syn.Q8_0, 4096, 4096, (512, 200, 48)),
                                                   (syn.Q4_K, 14336, 4096, (128, 16)),
-                                                  (syn.Q4_0, 4096, 4096, (300, 20))])
+                                                  (syn.Q4_0, 4096, 4096, (300, 20)),
+                                                  (syn.Q5_K, 4096, 4096, (64, 16)),
+                                                  (syn.Q6_K, 1024, 2048, (37, 5))])
 def test_noalloc_gemm_matches_allocating_entry_point(type_id, rows, cols, ms):
     import torch
 
@@ -62,15 +65,16 @@ def test_noalloc_gemm_checks_arguments():
 
     ops.init(0)
     lib = _native.load()
-    data = syn.q6_k_matrix(64, 256, seed=5)
+    data = syn.q8_0_matrix(64, 256, seed=5)
     w_dev = torch.from_numpy(data.reshape(-1)).cuda()
-    dw = ops.DeviceWeight(syn.Q6_K, w_dev.data_ptr(), 64, 256)
+    dw = ops.DeviceWeight(syn.Q8_0, w_dev.data_ptr(), 64, 256)
     err = _native.ErrBuf()
     buf = torch.zeros(64 * 256, dtype=torch.float32, device="cuda")
-    rc = lib.gollek_hip_gemm_bf16_device_noalloc(dw.handle, ctypes.c_void_p(buf.data_ptr()), 1,
+    # a negative row count of X
+    rc = lib.gollek_hip_gemm_bf16_device_noalloc(dw.handle, ctypes.c_void_p(buf.data_ptr()), -1,
                                                  ctypes.c_void_p(buf.data_ptr()), None, err.buf,
                                                  err.size)
-    assert rc == _native.ERR_UNSUPPORTED
+    assert rc == _native.ERR_ARG
     rc = lib.gollek_hip_gemm_bf16_device_noalloc(None, ctypes.c_void_p(buf.data_ptr()), 1,
                                                  ctypes.c_void_p(buf.data_ptr()), None, err.buf,
                                                  err.size)
