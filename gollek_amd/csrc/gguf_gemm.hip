@@ -563,6 +563,138 @@ __global__ __launch_bounds__(256) void gemm_kquant_generic_kernel(const uint8_t 
     if (m0 + m < M && n0 + n < N) Y[(int64_t)(m0 + m) * N + n0 + n] = acc;
 }
 
+// Q6_K on the matrix cores in fp32: a workgroup owns 16 NT W rows and 16 MT
+// rows of X and walks K a superblock (256 columns) at a time.  Per
+// stage the W rows' 210-byte superblocks and the X rows' bf16 go to LDS
+// (both loaded into registers while the previous stage is contracted), the
+// W values are dequantized there in fp32 -- d sc (q - 32) is exact in fp32
+// (an 11-bit d times an 8-bit scale times a 6-bit code), so these are the
+// dequantizer's values (RT/GgufKBlockDequantizer.java Q6_K: element e's
+// code is a ql nibble and two qh bits, its scale the int8 of its 16) -- and
+// contracted with v_mfma_f32_16x16x4_f32.  NT = 4 (tiles of 64 X rows): wave
+// w owns W rows 16 w .. 16 w + 15 over all of the stage's columns, so X is
+// staged once for 64 W rows.  NT = 1 (up to 32 X rows): wave w takes a
+// quarter of the stage's columns and the four waves' sums meet in LDS in
+// wave order.  X rows must be 4-byte aligned and W 2-byte aligned
+// (launch_gemm_bf16 checks): W rows are read 2 bytes at a time (superblocks
+// start on even bytes).
+template <int MT, int NT>
+__global__ __launch_bounds__(256) void gemm_q6k_f32_kernel(const uint8_t *__restrict__ W, int64_t row_bytes,
+                                                           const uint16_t *__restrict__ X, float *__restrict__ Y,
+                                                           int M, int N, int K) {
+#pragma clang fp contract(off)
+    static_assert(NT == 1 || NT == 4, "one N tile split over the waves, or one per wave");
+    constexpr int BM = 16 * MT, BN = 16 * NT;
+    constexpr int SBS = 1;                       // superblocks per stage
+    constexpr int KS = kQK * SBS;                // columns per stage
+    constexpr int kPitch = KS + 4;                // floats per staged row (bank spread)
+    constexpr int kRowHalves = 105 * SBS;         // a W row's stage bytes as uint16
+    constexpr int kRawHalves = BN * kRowHalves;
+    constexpr int kRawPer = (kRawHalves + 255) / 256;
+    constexpr int kXDw = BM * KS / 2;             // the X rows' stage as dwords
+    constexpr int kXPer = kXDw / 256;
+    constexpr int kGroups = BN * KS / 16;         // scale groups of the stage
+    static_assert(kXDw % 256 == 0 && kGroups % 256 == 0, "whole rounds of the workgroup");
+    __shared__ float xs[BM][kPitch];
+    __shared__ float ws[BN][kPitch];
+    __shared__ uint16_t raw[kRawHalves];
+    __shared__ f32x4 red[NT == 1 ? 4 : 1][MT][64];
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = (int)blockIdx.x * BN, m0 = (int)blockIdx.y * BM;
+    const int nst = K / KS;
+    uint16_t wr[kRawPer];
+    uint32_t xr[kXPer];
+    auto load = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < kRawPer; i++) {
+            const int h = tid + 256 * i, r = h / kRowHalves, c = h - r * kRowHalves;
+            wr[i] = h < kRawHalves && n0 + r < N
+                        ? *reinterpret_cast<const uint16_t *>(W + (int64_t)(n0 + r) * row_bytes +
+                                                              (int64_t)(210 * SBS) * st + 2 * c)
+                        : (uint16_t)0;
+        }
+#pragma unroll
+        for (int i = 0; i < kXPer; i++) {
+            const int q = tid + 256 * i, r = q / (KS / 2), c = q - r * (KS / 2);
+            xr[i] = m0 + r < M ? *reinterpret_cast<const uint32_t *>(X + (int64_t)(m0 + r) * K + (int64_t)KS * st + 2 * c)
+                               : 0u;
+        }
+    };
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    load(0);
+    for (int st = 0; st < nst; st++) {
+        __syncthreads();  // the previous stage's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < kRawPer; i++)
+            if (tid + 256 * i < kRawHalves) raw[tid + 256 * i] = wr[i];
+#pragma unroll
+        for (int i = 0; i < kXPer; i++) {
+            const int q = tid + 256 * i, r = q / (KS / 2), c = q - r * (KS / 2);
+            xs[r][2 * c] = __uint_as_float(xr[i] << 16);
+            xs[r][2 * c + 1] = __uint_as_float(xr[i] & 0xFFFF0000u);
+        }
+        __syncthreads();
+        if (st + 1 < nst) load(st + 1);
+        // group u: W row u / (16 SBS), superblock (u / 16) % SBS, its 16
+        // elements of scale group u % 16
+#pragma unroll
+        for (int u = tid; u < kGroups; u += 256) {
+            const int r = u / (16 * SBS), sb = (u / 16) % SBS, gi = u & 15;
+            const uint8_t *b = reinterpret_cast<const uint8_t *>(raw) + 2 * kRowHalves * r + 210 * sb;
+            const float d = half_bits_to_float((uint32_t)b[208] | ((uint32_t)b[209] << 8));
+            const float dsc = d * (float)(int)(int8_t)b[192 + gi];
+            const int e0 = 16 * gi, h = e0 >> 7, j = (e0 >> 5) & 3, l0 = e0 & 31;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int l = l0 + i;
+                const int q = ((b[64 * h + 32 * (j & 1) + l] >> (4 * (j >> 1))) & 0x0F) |
+                              (((b[128 + 32 * h + l] >> (2 * j)) & 3) << 4);
+                ws[r][kQK * sb + e0 + i] = dsc * (float)(q - 32);
+            }
+        }
+        __syncthreads();
+        const int col = lane & 15;
+        // NT = 4: W rows of this wave's tile, every column; NT = 1: a quarter of the columns
+        const int wrow = NT == 4 ? 16 * wave + col : col;
+        const int kb = (NT == 4 ? 0 : (KS / 4) * wave) + (lane >> 4);
+        constexpr int kSteps = NT == 4 ? KS / 4 : KS / 16;
+#pragma unroll 4
+        for (int k4 = 0; k4 < kSteps; k4++) {
+            const float bv = ws[wrow][kb + 4 * k4];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[16 * mt + col][kb + 4 * k4], bv, acc[mt], 0, 0, 0);
+        }
+    }
+    // D layout: lane holds column lane & 15, rows 4 (lane >> 4) + r.
+    if constexpr (NT == 4) {
+        const int n = n0 + 16 * wave + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * mt + 4 * (lane >> 4) + r;
+                if (m < M && n < N) Y[(int64_t)m * N + n] = acc[mt][r];
+            }
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) red[wave][mt][lane] = acc[mt];
+        __syncthreads();
+        for (int o = tid; o < MT * 64; o += 256) {  // the wave sums in wave order
+            const int mt = o >> 6, ln = o & 63;
+            const f32x4 v = ((red[0][mt][ln] + red[1][mt][ln]) + red[2][mt][ln]) + red[3][mt][ln];
+            const int n = n0 + (ln & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * mt + 4 * (ln >> 4) + r;
+                if (m < M && n < N) Y[(int64_t)m * N + n] = v[r];
+            }
+        }
+    }
+}
+
 namespace {
 
 template <int BM, int BN, int WM, int WN, int WK>
@@ -621,6 +753,27 @@ hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, co
             return launch_tiled<128, 16, 32, 16, 1>(w, row_bytes, x, y, M, N, K, stream);
         if (N % 64 == 0 && K % 64 == 0)
             return launch_tiled<128, 64, 64, 32, 1>(w, row_bytes, x, y, M, N, K, stream);
+    }
+    // Q6_K with 4-byte aligned X rows: the fp32 matrix-core kernel, tiles of
+    // 16 W rows and 16 / 32 / 64 X rows, or 64 x 64 tiles when those still
+    // give every CU two workgroups (fewer re-reads of X).
+    if (type_id == kQ6_K && K % kQK == 0 && (reinterpret_cast<uintptr_t>(x) & 3u) == 0 &&
+        ((reinterpret_cast<uintptr_t>(w) | (uintptr_t)row_bytes) & 1u) == 0) {
+        const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+        const int64_t wide = (int64_t)((N + 63) / 64) * ((M + 63) / 64);
+        if (mt == 4 && wide >= 2 * (int64_t)device_cus()) {
+            const dim3 g6((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+            hipLaunchKernelGGL((gemm_q6k_f32_kernel<4, 4>), g6, dim3(256), 0, stream, w, row_bytes, x, y, M, N, K);
+        } else {
+            const dim3 g6((unsigned)((N + 15) / 16), (unsigned)((M + 16 * mt - 1) / (16 * mt)));
+            if (mt == 1)
+                hipLaunchKernelGGL((gemm_q6k_f32_kernel<1, 1>), g6, dim3(256), 0, stream, w, row_bytes, x, y, M, N, K);
+            else if (mt == 2)
+                hipLaunchKernelGGL((gemm_q6k_f32_kernel<2, 1>), g6, dim3(256), 0, stream, w, row_bytes, x, y, M, N, K);
+            else
+                hipLaunchKernelGGL((gemm_q6k_f32_kernel<4, 1>), g6, dim3(256), 0, stream, w, row_bytes, x, y, M, N, K);
+        }
+        return hipGetLastError();
     }
     if (type_id == kQ5_K || type_id == kQ6_K) {
         const dim3 g16((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));

@@ -1,5 +1,5 @@
 """GPU parity of the Q8_0 / Q4_0 / Q4_K / Q5_K x bf16 MFMA GEMM and the Q6_K
-fp32 GEMM (small-M prefill / batched decode).
+fp32 MFMA GEMM (small-M prefill / batched decode).
 
 Bar: rel_err <= 1e-2 against the fp64 product of the bf16 activations and the
 bit-exact dequantized weights (the quants are contracted exactly and each
@@ -190,11 +190,12 @@ def test_gemm_split_k_shapes(rows, cols, m):
     t.close()
 
 
-# Q6_K weights (the Q6_K tensors of Q4_K_M files), and Q5_K where the tile
-# kernel does not take the call: the fp32 kernel of the dequantizers' block
-# formulas, 16 x 16 outputs per workgroup, with partial tiles on both sides.
+# Q6_K weights (the Q6_K tensors of Q4_K_M files): the fp32 matrix-core
+# kernel (16 W rows x 16 / 32 / 64 X rows per workgroup), with partial tiles
+# on both sides, K = 14336 and M = 512.
 @pytest.mark.parametrize("tid,rows,cols,m", [(syn.Q6_K, 4096, 4096, 16), (syn.Q6_K, 33, 768, 1),
-                                             (syn.Q6_K, 1024, 4096, 128), (syn.Q6_K, 100, 512, 37)])
+                                             (syn.Q6_K, 1024, 4096, 128), (syn.Q6_K, 100, 512, 37),
+                                             (syn.Q6_K, 4096, 14336, 24), (syn.Q6_K, 14336, 4096, 512)])
 def test_gemm_q5_k_q6_k(tid, rows, cols, m):
     print(f"[gpu] gemm type={tid} rows={rows} cols={cols} m={m}", flush=True)
     data = syn.matrix(tid, rows, cols, rows + cols + m)
@@ -208,22 +209,24 @@ def test_gemm_q5_k_q6_k(tid, rows, cols, m):
     assert err <= GEMM_TOL
 
 
-def test_gemm_q5_k_unaligned_x_takes_the_fp32_kernel():
-    # x 2 bytes past a 16-byte boundary: the tile kernel's loads need 16, so
-    # the device entry runs the fp32 kernel, with the same values.
+@pytest.mark.parametrize("tid", [syn.Q5_K, syn.Q6_K])
+def test_gemm_k_quant_unaligned_x_takes_the_generic_kernel(tid):
+    # x 2 bytes past a 16-byte boundary: the Q5_K tile kernel's loads need
+    # 16 and the Q6_K kernel's 4, so the device entry runs the per-output
+    # fp32 kernel (gemm_kquant_generic_kernel), with the same values.
     import torch
     rows, cols, m = 272, 1024, 9
-    data = syn.q5_k_matrix(rows, cols, seed=77)
+    data = syn.matrix(tid, rows, cols, 77)
     x = syn.activation_bf16(m, cols, seed=78)
     w_dev = torch.from_numpy(data.reshape(-1)).cuda()
-    dw = ops.DeviceWeight(syn.Q5_K, w_dev.data_ptr(), rows, cols)
+    dw = ops.DeviceWeight(tid, w_dev.data_ptr(), rows, cols)
     try:
         buf = torch.zeros(m * cols + 8, dtype=torch.int16, device="cuda")
         buf[1:1 + m * cols] = torch.from_numpy(x.view(np.int16).reshape(-1)).cuda()
         y_dev = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
         dw.gemm_bf16(buf.data_ptr() + 2, m, y_dev.data_ptr(), torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
-        assert o.rel_err(y_dev.cpu().numpy(), o.gemm_reference(syn.Q5_K, data, cols, x)) <= GEMM_TOL
+        assert o.rel_err(y_dev.cpu().numpy(), o.gemm_reference(tid, data, cols, x)) <= GEMM_TOL
     finally:
         dw.close()
 
