@@ -657,9 +657,9 @@ def main() -> int:
             if have_gemm and want(name):
                 log(f"extra {name}")
                 extra[name], gemm_host = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
-        # Q4_K / Q4_0 / Q5_K weights at the FFN shape (K 4096, N 14336).
+        # Q4_K / Q4_0 / Q5_K / Q6_K weights at the FFN shape (K 4096, N 14336).
         for tname, t, ms in (("q4_k", syn.Q4_K, (16, 128, 512)), ("q4_0", syn.Q4_0, (128, 512)),
-                             ("q5_k", syn.Q5_K, (16, 128, 512))):
+                             ("q5_k", syn.Q5_K, (16, 128, 512)), ("q6_k", syn.Q6_K, (16, 128, 512))):
             for m in ms:
                 name = f"{tname}_gemm_bf16_m{m}_4096x14336"
                 if have_gemm and want(name):
@@ -724,7 +724,7 @@ def main() -> int:
             if m > 128:
                 continue  # the m = 128 line's rate stands for it (m mat-vecs each)
             log(f"cpu baseline {name}")
-            tid = {"q4_k": syn.Q4_K, "q4_0": syn.Q4_0, "q5_k": syn.Q5_K}[name[:4]]
+            tid = {"q4_k": syn.Q4_K, "q4_0": syn.Q4_0, "q5_k": syn.Q5_K, "q6_k": syn.Q6_K}[name[:4]]
             cpus[name] = cpu_gemm(hosts[name], m, seed=8, type_id=tid)
         if moe_inputs is not None:
             log("cpu baseline moe")

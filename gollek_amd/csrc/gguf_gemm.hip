@@ -710,7 +710,6 @@ hipError_t launch_tiled(const uint8_t *w, int64_t row_bytes, const uint16_t *x, 
 
 size_t gemm_workspace_bytes(int type_id, int M, int N, int K) {
     if (type_id == kQ8_0 && M <= 32) return 0;  // the skinny kernel
-    if (type_id == kQ6_K) return 0;  // no split-K
     return gemm_tile_workspace_bytes(type_id, M, N, K);
 }
 

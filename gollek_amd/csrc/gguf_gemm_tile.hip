@@ -80,6 +80,13 @@ constexpr int kStagePitch = kTileN + 4;        // floats per row of the output s
 //         32 quant bytes of the stage's chunk c (sub-blocks 2c, 2c + 1)
 //   Q5_K: the header, the superblock's 32 qh bytes (bits 2c, 2c + 1 are the
 //         chunk's fifth bits) and the chunk's 32 quant bytes (80 bytes)
+//   Q6_K: the chunk's half (h = c >> 1) of ql (64 bytes) and of qh (32)
+//         from 0 or 2 bytes before them (m: superblocks of odd index begin 2
+//         bytes past a dword), and 32 bytes holding the scales and d (bytes
+//         192 .. 209) from byte 192 (m = 0) or 178 (m = 2): 5 + 3 + 2 chunks
+//         (160 bytes).  Rows of an even superblock count end with an odd
+//         superblock, so no load runs past a row's end; an even superblock's
+//         last chunk reads 14 bytes of the next one.
 template <int T>
 struct RawW;
 template <>
@@ -97,6 +104,10 @@ struct RawW<kQ4_K> {
 template <>
 struct RawW<kQ5_K> {
     static constexpr int kChunks = 5, kStageBytes = 0, kSlots = 6;  // 176 bytes per four stages
+};
+template <>
+struct RawW<kQ6_K> {
+    static constexpr int kChunks = 10, kStageBytes = 0, kSlots = 4;  // 210 bytes per four stages
 };
 
 // Geometry of a 16 MT x 128 tile: MT row tiles of 16 rows of X.  Tiles of
@@ -195,6 +206,8 @@ struct Ops {
     uint2 q2[2];              // Q4_K, Q5_K
     u32x4 hd[2];              // Q4_K, Q5_K
     uint2 qh[2];              // Q5_K
+    uint32_t l6[2][3], h6[2][3], d6[2];  // Q6_K: ql, qh dwords, d
+    uint32_t s6[2][2];                   // Q6_K: scale bytes
 };
 template <int RP>
 __device__ __forceinline__ void ops_read_q32(uint32_t b, uint32_t s, Ops &o) {
@@ -237,6 +250,36 @@ __device__ __forceinline__ void ops_read_q5k(uint32_t b, uint32_t s, uint32_t h,
         : "v"(b), "v"(s), "v"(h), "n"(RP)
         : "memory");
 }
+// Q6_K: per column tile the lane's 3 ql dwords (at l), 3 qh dwords (at h),
+// the 2 dwords of scale bytes from s and the dword holding d (at dd).
+template <int RP>
+__device__ __forceinline__ void ops_read_q6k(uint32_t l, uint32_t h, uint32_t s, uint32_t dd, Ops &o) {
+    asm volatile(
+        "ds_read_b32 %0, %18\n\t"
+        "ds_read_b32 %1, %18 offset:4\n\t"
+        "ds_read_b32 %2, %18 offset:8\n\t"
+        "ds_read_b32 %3, %19\n\t"
+        "ds_read_b32 %4, %19 offset:4\n\t"
+        "ds_read_b32 %5, %19 offset:8\n\t"
+        "ds_read_b32 %6, %20\n\t"
+        "ds_read_b32 %7, %20 offset:4\n\t"
+        "ds_read_b32 %8, %21\n\t"
+        "ds_read_b32 %9, %18 offset:%22\n\t"
+        "ds_read_b32 %10, %18 offset:%23\n\t"
+        "ds_read_b32 %11, %18 offset:%24\n\t"
+        "ds_read_b32 %12, %19 offset:%22\n\t"
+        "ds_read_b32 %13, %19 offset:%23\n\t"
+        "ds_read_b32 %14, %19 offset:%24\n\t"
+        "ds_read_b32 %15, %20 offset:%22\n\t"
+        "ds_read_b32 %16, %20 offset:%23\n\t"
+        "ds_read_b32 %17, %21 offset:%22"
+        : "=&v"(o.l6[0][0]), "=&v"(o.l6[0][1]), "=&v"(o.l6[0][2]), "=&v"(o.h6[0][0]), "=&v"(o.h6[0][1]),
+          "=&v"(o.h6[0][2]), "=&v"(o.s6[0][0]), "=&v"(o.s6[0][1]), "=&v"(o.d6[0]), "=&v"(o.l6[1][0]),
+          "=&v"(o.l6[1][1]), "=&v"(o.l6[1][2]), "=&v"(o.h6[1][0]), "=&v"(o.h6[1][1]), "=&v"(o.h6[1][2]),
+          "=&v"(o.s6[1][0]), "=&v"(o.s6[1][1]), "=&v"(o.d6[1])
+        : "v"(l), "v"(h), "v"(s), "v"(dd), "n"(RP), "n"(RP + 4), "n"(RP + 8)
+        : "memory");
+}
 template <int I>
 __device__ __forceinline__ void ops_read_a(uint32_t a, Ops &o) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(o.a[I]) : "v"(a), "n"(2048 * I) : "memory");
@@ -264,6 +307,17 @@ __device__ __forceinline__ void ops_wait_raw(Ops &o) {
                  : "+v"(o.q[0][0]), "+v"(o.q[0][1]), "+v"(o.q[0][2]), "+v"(o.sc[0]), "+v"(o.q[1][0]),
                    "+v"(o.q[1][1]), "+v"(o.q[1][2]), "+v"(o.sc[1]), "+v"(o.q2[0]), "+v"(o.q2[1]),
                    "+v"(o.hd[0]), "+v"(o.hd[1]), "+v"(o.qh[0]), "+v"(o.qh[1])
+                 : "n"(MT)
+                 : "memory");
+}
+// Q6_K: the same wait for its raw dwords.
+template <int MT>
+__device__ __forceinline__ void ops_wait_raw6(Ops &o) {
+    asm volatile("s_waitcnt lgkmcnt(%18)"
+                 : "+v"(o.l6[0][0]), "+v"(o.l6[0][1]), "+v"(o.l6[0][2]), "+v"(o.h6[0][0]), "+v"(o.h6[0][1]),
+                   "+v"(o.h6[0][2]), "+v"(o.s6[0][0]), "+v"(o.s6[0][1]), "+v"(o.d6[0]), "+v"(o.l6[1][0]),
+                   "+v"(o.l6[1][1]), "+v"(o.l6[1][2]), "+v"(o.h6[1][0]), "+v"(o.h6[1][1]), "+v"(o.h6[1][2]),
+                   "+v"(o.s6[1][0]), "+v"(o.s6[1][1]), "+v"(o.d6[1])
                  : "n"(MT)
                  : "memory");
 }
@@ -331,8 +385,11 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
     // the end read as zeros.
     const int mrows = M - m0 < kTileM ? M - m0 : kTileM;
     const int nrows = N - n0 < kTileN ? N - n0 : kTileN;
+    // (Q6_K: none; its loads start up to 2 bytes before a superblock, so the
+    // offsets stay relative to the rows' first byte)
     const int64_t w_split = T == kQ4_K   ? (int64_t)(s0 / 4) * 144
                             : T == kQ5_K ? (int64_t)(s0 / 4) * kQ5KBlockBytes
+                            : T == kQ6_K ? 0
                                          : (int64_t)s0 * R::kStageBytes;
     const __amdgpu_buffer_rsrc_t xr = wave_buffer(
         reinterpret_cast<const uint8_t *>(X) + (int64_t)m0 * K * 2 + (int64_t)s0 * 128,
@@ -368,7 +425,16 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
                 off += (uint32_t)(144 * (ls >> 2)) + (part != 0 ? (uint32_t)(32 * (ls & 3)) : 0u);
             else if constexpr (T == kQ5_K)  // parts 0..2: header, qh; 3, 4: the chunk's quants at 48
                 off += (uint32_t)(kQ5KBlockBytes * (ls >> 2)) + (part >= 3 ? (uint32_t)(32 * (ls & 3)) : 0u);
-            else
+            else if constexpr (T == kQ6_K) {
+                // superblock sb from its dword at or before it (m = 2 (sb & 1)); parts
+                // 0..4: ql half h from 64 h, 5..7: qh half h from 128 + 32 h (both
+                // less m), 8, 9: from 192 (m = 0) or 178 (m = 2)
+                const int sb = (s0 >> 2) + (ls >> 2), h = (ls >> 1) & 1, m2 = sb & 1;
+                const int at = part < 5 ? 64 * h + 16 * part
+                               : part < 8 ? 128 + 32 * h + 16 * (part - 5)
+                                          : (m2 ? 180 : 192) + 16 * (part - 8);
+                off = (uint32_t)row * (uint32_t)row_bytes + (uint32_t)(210 * sb - 2 * (sb & 1) + at);
+            } else
                 off += (uint32_t)(R::kStageBytes * ls);
             dma16(wr, rs + 1024 * j, off);
         }
@@ -501,6 +567,75 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
         }
     };
 
+    // Q6_K: a 32-column block holds two 16-element scale groups, so each
+    // MFMA takes one group's codes (B_lo: lanes of k groups 0, 1; B_hi: 2, 3;
+    // the other lanes zero) as 128 + q (q = ql nibble | qh bits << 4, 0..63),
+    // starting from C = -160 sum(x) over the same lanes (an MFMA against a
+    // constant -160 B), so its result is sum((q - 32) x) of the group; the
+    // FMA applies fl(d sc) of the group (exact: an 11-bit d times an 8-bit
+    // scale).  Four MFMAs per row and column tile, two FMAs per output.
+    auto compute6 = [&](int ls) {
+        const uint32_t so = (uint32_t)((ls % NS) * G::kSlot);
+        const int c = ls & 3, m = 2 * (((s0 >> 2) + (ls >> 2)) & 1);
+        const uint32_t rb = wrow + so;  // this lane's W row: ql piece, qh piece at 80, tail at 128
+        Ops o;
+        ops_read_q6k<16 * G::kPitch>(rb + 32 * kg + 8 * lk, rb + 80 + 8 * lk, rb + 128 + 4 * c + 6 * m,
+                                     rb + 144 + 6 * m, o);
+        ops_read_as<MT>(xa + so, o);
+        ops_wait_raw6<MT>(o);
+        const int nib = 4 * (c & 1), hsh = 2 * (2 * (c & 1) + kg);
+        const bool lo_half = lk < 2;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        const u32x4 m160 = {0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u};  // bf16 -160
+        const bf16x8 m160lo = __builtin_bit_cast(bf16x8, lo_half ? m160 : zero);
+        const bf16x8 m160hi = __builtin_bit_cast(bf16x8, lo_half ? zero : m160);
+        bf16x8 Blo[2], Bhi[2];
+        float dlo[2], dhi[2];
+        auto widen6 = [&](int i) {
+            const uint32_t l0 = __builtin_amdgcn_alignbyte(o.l6[i][1], o.l6[i][0], m);
+            const uint32_t l1 = __builtin_amdgcn_alignbyte(o.l6[i][2], o.l6[i][1], m);
+            const uint32_t h0 = __builtin_amdgcn_alignbyte(o.h6[i][1], o.h6[i][0], m);
+            const uint32_t h1 = __builtin_amdgcn_alignbyte(o.h6[i][2], o.h6[i][1], m);
+            const uint32_t q0 = ((l0 >> nib) & 0x0F0F0F0Fu) | (((h0 >> hsh) & 0x03030303u) << 4);
+            const uint32_t q1 = ((l1 >> nib) & 0x0F0F0F0Fu) | (((h1 >> hsh) & 0x03030303u) << 4);
+            uint32_t cc[4];
+            q4x4_bf16_128(q0, cc[0], cc[1]);
+            q4x4_bf16_128(q1, cc[2], cc[3]);
+            const u32x4 v = {cc[0], cc[1], cc[2], cc[3]};
+            Blo[i] = __builtin_bit_cast(bf16x8, lo_half ? v : zero);
+            Bhi[i] = __builtin_bit_cast(bf16x8, lo_half ? zero : v);
+            // the row's scales of groups 2 kg, 2 kg + 1 of the chunk, and d
+            const uint64_t sw = (((uint64_t)o.s6[i][1] << 32) | o.s6[i][0]) >> (8 * (m + 2 * kg));
+            const float d = half_bits_to_float_fast(o.d6[i] >> (8 * m));
+            dlo[i] = d * (float)(int)(int8_t)(sw & 0xFFu);
+            dhi[i] = d * (float)(int)(int8_t)((sw >> 8) & 0xFFu);
+        };
+        f32x4 plo[3], phi[3];
+        auto fmas6 = [&](int k) {
+            const int mt = k % MT, nt = k / MT;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                acc[mt][nt][r] = fmaf(dlo[nt], plo[k % 3][r], acc[mt][nt][r]);
+                acc[mt][nt][r] = fmaf(dhi[nt], phi[k % 3][r], acc[mt][nt][r]);
+            }
+        };
+        widen6(0);
+#pragma unroll
+        for (int k = 0; k < 2 * MT + 2; k++) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (k < 2 * MT) {
+                const int mt = k % MT, nt = k / MT;
+                if (k < MT) ops_wait_row<MT>(k, o);
+                const bf16x8 A = __builtin_bit_cast(bf16x8, o.a[mt]);
+                if (k == (MT < 2 ? MT : 2)) widen6(1);
+                const f32x4 tlo = mfma_bf16(A, m160lo), thi = mfma_bf16(A, m160hi);
+                plo[k % 3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Blo[nt], tlo, 0, 0, 0);
+                phi[k % 3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bhi[nt], thi, 0, 0, 0);
+            }
+            if (k >= 2) fmas6(k - 2);
+        }
+    };
+
     // ---- pipeline ----------------------------------------------------------
     // Stage s sits in ring slot s % NS.  Iteration s: the loader waves wait
     // until their loads of stage s have landed (the later stages in flight
@@ -522,7 +657,10 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
     } else {
         for (int s = 0; s < nst; s++) {
             compute_barrier();
-            compute(s);
+            if constexpr (T == kQ6_K)
+                compute6(s);
+            else
+                compute(s);
         }
     }
 
@@ -609,10 +747,16 @@ namespace {
 
 // Row tiles per workgroup: the smallest of 1, 2, 4, 8 that covers M, so
 // that small M computes no padding rows.
-int tile_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+// Row tiles of X per workgroup: the smallest of 1, 2, 4, 8 that covers M
+// (Q6_K at most 4: its four MFMAs per row and column tile hold more
+// registers).
+int tile_mt(int type_id, int M) {
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    return type_id == kQ6_K && mt > 4 ? 4 : mt;
+}
 
 int tile_splits(int type_id, int M, int N, int K, size_t workspace_bytes) {
-    const int tm = 16 * tile_mt(M);
+    const int tm = 16 * tile_mt(type_id, M);
     const int tiles = (M + tm - 1) / tm * ((N + kTileN - 1) / kTileN);
     const int nst = K / 64;
     // A split holds a whole number of four-stage rounds (and so of Q4_K
@@ -628,7 +772,8 @@ int tile_splits(int type_id, int M, int N, int K, size_t workspace_bytes) {
 
 bool gemm_tile_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w,
                          const void *x, const void *y) {
-    if (type_id != kQ8_0 && type_id != kQ4_0 && type_id != kQ4_K && type_id != kQ5_K) return false;
+    if (type_id != kQ8_0 && type_id != kQ4_0 && type_id != kQ4_K && type_id != kQ5_K && type_id != kQ6_K)
+        return false;
     if (M <= 0 || N <= 0 || K % 256 != 0) return false;
     if (((reinterpret_cast<uintptr_t>(w) | (uintptr_t)row_bytes) & 3u) != 0) return false;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(y) & 15u) != 0) return false;
@@ -647,7 +792,7 @@ hipError_t launch_gemm_tile(int type_id, const uint8_t *w, int64_t row_bytes, co
     if (M <= 0) return hipSuccess;
     int S = tile_splits(type_id, M, N, K, workspace != nullptr ? workspace_bytes : 0);
     if (((int64_t)M * N) % 4 != 0 || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) S = 1;
-    const int mt = tile_mt(M), tm = 16 * mt;
+    const int mt = tile_mt(type_id, M), tm = 16 * mt;
     const unsigned tiles = (unsigned)(((M + tm - 1) / tm) * ((N + kTileN - 1) / kTileN));
     const dim3 grid(tiles * (unsigned)S), block(kThreads);
     float *part = S > 1 ? workspace : nullptr;
@@ -678,6 +823,17 @@ hipError_t launch_gemm_tile(int type_id, const uint8_t *w, int64_t row_bytes, co
         break;
     case kQ5_K:
         GOLLEK_TILE_LAUNCH(kQ5_K);
+        break;
+    case kQ6_K:  // mt <= 4
+        if (mt == 1)
+            hipLaunchKernelGGL((gemm_tile_kernel<kQ6_K, 1>), grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S,
+                               part);
+        else if (mt == 2)
+            hipLaunchKernelGGL((gemm_tile_kernel<kQ6_K, 2>), grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S,
+                               part);
+        else
+            hipLaunchKernelGGL((gemm_tile_kernel<kQ6_K, 4>), grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S,
+                               part);
         break;
     default:
         return hipErrorInvalidValue;

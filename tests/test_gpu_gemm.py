@@ -66,8 +66,10 @@ def test_gemm_odd_shapes(rows, cols, m):
 
 
 MATRIX = {syn.Q8_0: syn.q8_0_matrix, syn.Q4_0: syn.q4_0_matrix, syn.Q4_K: syn.q4_k_matrix,
-          syn.Q5_K: syn.q5_k_matrix}
-TYPES = [syn.Q8_0, syn.Q4_0, syn.Q4_K, syn.Q5_K]
+          syn.Q5_K: syn.q5_k_matrix, syn.Q6_K: syn.q6_k_matrix}
+# (Q6_K rows of an odd superblock count, K = 256 here, are not dword
+# multiples and take the fp32 Q6_K kernel instead of the tile kernel.)
+TYPES = [syn.Q8_0, syn.Q4_0, syn.Q4_K, syn.Q5_K, syn.Q6_K]
 
 
 def _gemm_case(type_id, rows, cols, m, seed):
@@ -111,10 +113,10 @@ def test_gemm_tile_kernel_small_m(type_id, rows, cols, m):
     assert err <= GEMM_TOL
 
 
-@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K, syn.Q5_K])
+@pytest.mark.parametrize("type_id", [syn.Q4_0, syn.Q4_K, syn.Q5_K, syn.Q6_K])
 @pytest.mark.parametrize("m", [16, 128, 512])
 def test_gemm_q4_parity_14336(type_id, m):
-    # Q4_0 / Q4_K / Q5_K weights at the FFN shape K = 4096, N = 14336.
+    # Q4_0 / Q4_K / Q5_K / Q6_K weights at the FFN shape K = 4096, N = 14336.
     print(f"[gpu] gemm q4 type={type_id} m={m} 14336x4096", flush=True)
     y, ref = _gemm_case(type_id, 14336, 4096, m, seed=1400 + m)
     err = o.rel_err(y, ref)
@@ -190,9 +192,10 @@ def test_gemm_split_k_shapes(rows, cols, m):
     t.close()
 
 
-# Q6_K weights (the Q6_K tensors of Q4_K_M files): the fp32 matrix-core
-# kernel (16 W rows x 16 / 32 / 64 X rows per workgroup), with partial tiles
-# on both sides, K = 14336 and M = 512.
+# Q6_K weights (the Q6_K tensors of Q4_K_M files): the tile kernel for rows
+# of an even superblock count (superblocks of odd index start 2 bytes past a
+# dword; K = 14336 and M = 512 too), the fp32 matrix-core kernel for odd
+# counts (K = 768), with partial tiles on both sides.
 @pytest.mark.parametrize("tid,rows,cols,m", [(syn.Q6_K, 4096, 4096, 16), (syn.Q6_K, 33, 768, 1),
                                              (syn.Q6_K, 1024, 4096, 128), (syn.Q6_K, 100, 512, 37),
                                              (syn.Q6_K, 4096, 14336, 24), (syn.Q6_K, 14336, 4096, 512)])
@@ -285,7 +288,7 @@ def test_gemm_device_entry_split_k_workspace(m):
 
 
 @pytest.mark.parametrize("type_id,rows,m", [(syn.Q8_0, 4096, 512), (syn.Q4_K, 4096, 512), (syn.Q4_0, 2048, 1024),
-                                           (syn.Q5_K, 4096, 128)])
+                                           (syn.Q5_K, 4096, 128), (syn.Q6_K, 4096, 128)])
 def test_gemm_two_split_repeatable(type_id, rows, m):
     # Two K splits added in split order by the reduction kernel: the same
     # bits on every call, within the bar of the oracle, on repeated calls
