@@ -180,8 +180,8 @@ int32_t gollek_hip_matvec_rows(gollek_hip_weight *weight, const float *x, int64_
 /* Y[m, n] = sum_k X[m, k] W[n, k] (Y = X W^T, the Linear convention of
  * runner/safetensor/gollek-safetensor-core/src/main/java/tech/kayys/gollek/
  * safetensor/core/tensor/AccelOps.java:370-376) for a weight of any type
- * this library takes (Q8_0, Q4_0, Q4_K and Q5_K on bf16 matrix cores, Q6_K
- * on fp32 ones over its exactly dequantized values), X given as
+ * this library takes (on bf16 matrix cores; Q6_K rows of an odd superblock
+ * count on fp32 ones over their exactly dequantized values), X given as
  * m x cols bf16 bit patterns (row-major), Y m x rows fp32.  Small-M prefill
  * and batched decode.  The reference has no GGUF GEMM: it runs m independent
  * RT/GgufTensorOps.matVecRows calls (RT/GgufTensorOps.java:666-674), which
