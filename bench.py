@@ -682,11 +682,12 @@ def main() -> int:
                 torch, args.steps, args.warmup, seed=13, shape=(128, 8, 4096, 1536, 16), copies=2,
                 routed=False)[0]
         # Other expert types at the same shape: Q4_K or Q5_K gate / up with
-        # Q6_K down (Q4_K_M / Q5_K_M files' layers), all-Q5_K (Q5_K_S), all-Q8_0
-        # and all-Q4_0.
+        # Q6_K down (Q4_K_M / Q5_K_M files' layers), all-Q5_K (Q5_K_S), all-Q6_K,
+        # all-Q8_0 and all-Q4_0.
         for name, types in (("moe_q4_k_q6_k_down_e128_top8_t16", (syn.Q4_K, syn.Q4_K, syn.Q6_K)),
                             ("moe_q5_k_q6_k_down_e128_top8_t16", (syn.Q5_K, syn.Q5_K, syn.Q6_K)),
                             ("moe_q5_k_e128_top8_t16", (syn.Q5_K, syn.Q5_K, syn.Q5_K)),
+                            ("moe_q6_k_e128_top8_t16", (syn.Q6_K, syn.Q6_K, syn.Q6_K)),
                             ("moe_q8_0_e128_top8_t16", (syn.Q8_0, syn.Q8_0, syn.Q8_0)),
                             ("moe_q4_0_e128_top8_t16", (syn.Q4_0, syn.Q4_0, syn.Q4_0))):
             if _has_symbol("gollek_hip_moe_grouped_device") and want(name):
