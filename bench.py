@@ -674,6 +674,14 @@ def main() -> int:
             log("extra moe")
             extra["moe_q4_k_e128_top8_t16"], moe_inputs = moe_workload(torch, args.steps, args.warmup,
                                                                       seed=11)
+        # Prefill: 256 and 512 tokens through the same layer (every expert
+        # takes tens of routes).
+        for T in (256, 512):
+            name = f"moe_q4_k_e128_top8_t{T}"
+            if _has_symbol("gollek_hip_moe_grouped_device") and want(name):
+                log(f"extra {name}")
+                extra[name] = moe_workload(torch, args.steps, args.warmup, seed=17,
+                                           shape=(128, 8, 2048, 768, T), routed=False)[0]
         if _has_symbol("gollek_hip_moe_grouped_device") and want("moe_q4_k_e128_top8_t16_h4096"):
             log("extra moe hidden 4096")
             # 128 experts, top-8, hidden 4096, inter 1536 (two 1.36 GB layers

@@ -148,6 +148,8 @@ hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uin
                                int64_t gate_row_bytes, int64_t down_row_bytes, int E, int H, int I,
                                const float *x, const int32_t *ids, const float *wts, int T, int top_k,
                                float *out, uint8_t *ws, hipStream_t stream);
+// Routes (tokens x top_k) one launch of the matrix-core passes routes in LDS.
+constexpr int kMoeMfmaMaxRoutes = 2048;
 // K-quant experts on the matrix-core passes (gguf_moe_mfma.hip): gate / up
 // both Q4_K or both Q5_K (hidden up to 4096); down rows
 // Q4_K, Q5_K or Q6_K through the token-major pass (inter up to 1024), else

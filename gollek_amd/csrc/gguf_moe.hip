@@ -963,6 +963,25 @@ hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *
     const bool aligned = ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
                            reinterpret_cast<uintptr_t>(down) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
     const bool q4k_gu = gate_type == kQ4_K && up_type == kQ4_K;
+    // More routes than the matrix-core passes route in LDS (prefill): token
+    // slices of at most kMoeMfmaMaxRoutes / top_k tokens, one after another on
+    // the stream, when a slice takes those passes (a token's output depends on
+    // its own routes only, so the results do not change).
+    const int tslice = kMoeMfmaMaxRoutes / top_k;
+    if (aligned && (int64_t)T * top_k > kMoeMfmaMaxRoutes && tslice >= 1 && tuning().moe_variant != 1 &&
+        ((gate_type == up_type && moe_kq_mfma_supported(gate_type, down_type, E, H, I, tslice, top_k, x)) ||
+         (gate_type == kQ4_0 && up_type == kQ4_0 && down_type == kQ4_0 &&
+          moe_q40_mfma_supported(E, H, I, tslice * top_k, x)))) {
+        for (int t0 = 0; t0 < T; t0 += tslice) {
+            const int tn = T - t0 < tslice ? T - t0 : tslice;
+            const hipError_t e = launch_moe(gate_type, up_type, down_type, gate, up, down, gate_row_bytes,
+                                            up_row_bytes, down_row_bytes, E, H, I, x + (int64_t)t0 * H,
+                                            ids + (int64_t)t0 * top_k, wts + (int64_t)t0 * top_k, tn, top_k,
+                                            out + (int64_t)t0 * H, ws, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     // Q4_K or Q5_K gate / up with the down types the matrix-core passes take.
     if (aligned && gate_type == up_type && tuning().moe_variant != 1 &&
         moe_kq_mfma_supported(gate_type, down_type, E, H, I, T, top_k, x))

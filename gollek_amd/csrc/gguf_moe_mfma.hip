@@ -65,7 +65,7 @@ struct MoRing {
 };
 constexpr int kMoOutCap = 1536;      // buffered results (value, index)
 constexpr int kMoMaxExperts = 256;   // routing tables held in LDS
-constexpr int kMoMaxRoutes = 2048;
+constexpr int kMoMaxRoutes = kMoeMfmaMaxRoutes;
 
 // Routing tables of one pass, built in LDS by every workgroup: the valid
 // routes (expert id in range, weight != 0; MoeForwardPass.java:222) stably

@@ -114,9 +114,9 @@ def test_moe_q5_k_parity(gt, dt, E, H, I, T, k):
 # 64 lanes per row, route groups limited by LDS, experts with many routes),
 # Q6_K gate and up on the K-quant row kernels, mixed gate / up types, and
 # Q6_K down beyond the token-major down pass (inter above 1024, hidden past
-# 2048 with an odd superblock count, more than 2048 routes); also Q5_K gate /
-# up at hidden 4096 (K-halves of 8) and 1792 (7 superblocks in one half) on
-# the matrix-core passes.
+# 2048 with an odd superblock count); also Q5_K gate / up at hidden 4096
+# (K-halves of 8) and 1792 (7 superblocks in one half) on the matrix-core
+# passes, and Q4_K gate / up with Q6_K down over 2400 routes (token slices).
 @pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
     (syn.Q8_0, syn.Q8_0, 128, 2048, 768, 16, 8), (syn.Q4_0, syn.Q4_0, 128, 2048, 768, 16, 8),
     (syn.Q4_0, syn.Q4_0, 4, 512, 14336, 12, 2), (syn.Q8_0, syn.Q8_0, 2, 4096, 1024, 20, 2),
@@ -138,6 +138,32 @@ def test_moe_other_types_parity(gt, dt, E, H, I, T, k):
     err = o.rel_err(out, ref)
     print(f"[gpu] moe types rel_err={err:.3e}", flush=True)
     assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+# Prefill: more than 2048 routes (tokens x top_k) run the matrix-core passes
+# over token slices of 2048 / top_k tokens (256 + 44 at top-8, 512 + 88 at
+# top-4, 1024 + 76 and 1024 + 6 at top-2; expert-major down at inter 1280).
+# A token's output depends on its own routes only, so the sliced call equals,
+# bit for bit, one call per slice, and both are within the bar of the oracle.
+@pytest.mark.parametrize("gt,dt,E,H,I,T,k", [
+    (syn.Q4_K, syn.Q4_K, 32, 512, 256, 300, 8), (syn.Q5_K, syn.Q6_K, 16, 1024, 512, 600, 4),
+    (syn.Q4_0, syn.Q4_0, 32, 512, 256, 1100, 2), (syn.Q4_K, syn.Q5_K, 8, 512, 1280, 1030, 2)])
+def test_moe_prefill_token_slices(gt, dt, E, H, I, T, k):
+    print(f"[gpu] moe prefill gate={gt} down={dt} E={E} H={H} I={I} T={T} k={k}", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + I, down_type=dt, gate_type=gt)
+    ids, w = syn.moe_routing(T, E, k, seed=31)
+    x = syn.activation(T * H, seed=32).reshape(T, H)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=gt)
+    err = o.rel_err(out, ref)
+    print(f"[gpu] moe prefill rel_err={err:.3e}", flush=True)
+    assert err <= MOE_TOL
+    step = 2048 // k
+    parts = [ops.moe_grouped(tg, tu, td, E, x[t0:t0 + step], ids[t0:t0 + step], w[t0:t0 + step])
+             for t0 in range(0, T, step)]
+    assert np.array_equal(out.view(np.uint32), np.concatenate(parts).view(np.uint32))
     for t in (tg, tu, td):
         t.close()
 
