@@ -573,7 +573,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
     // starting from C = -160 sum(x) over the same lanes (an MFMA against a
     // constant -160 B), so its result is sum((q - 32) x) of the group; the
     // FMA applies fl(d sc) of the group (exact: an 11-bit d times an 8-bit
-    // scale).  Four MFMAs per row and column tile, two FMAs per output.
+    // scale).  Per row tile two MFMAs for the starts and per column tile two
+    // more, two FMAs per output.
     auto compute6 = [&](int ls) {
         const uint32_t so = (uint32_t)((ls % NS) * G::kSlot);
         const int c = ls & 3, m = 2 * (((s0 >> 2) + (ls >> 2)) & 1);
@@ -611,8 +612,12 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
             dhi[i] = d * (float)(int)(int8_t)((sw >> 8) & 0xFFu);
         };
         f32x4 plo[3], phi[3];
+        // MFMA pair k = 0 .. 2 MT - 1 is (row tile k / 2, column tile k % 2):
+        // the -160 sum(x) starts depend on the row tile only, so the two
+        // column tiles of a row tile take the same ones (six MFMAs per row
+        // tile); both column tiles are widened before the first MFMA.
         auto fmas6 = [&](int k) {
-            const int mt = k % MT, nt = k / MT;
+            const int mt = k >> 1, nt = k & 1;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 acc[mt][nt][r] = fmaf(dlo[nt], plo[k % 3][r], acc[mt][nt][r]);
@@ -620,15 +625,19 @@ __global__ __launch_bounds__(kThreads) void gemm_tile_kernel(const uint8_t *__re
             }
         };
         widen6(0);
+        widen6(1);
+        f32x4 tlo, thi;
 #pragma unroll
         for (int k = 0; k < 2 * MT + 2; k++) {
             __builtin_amdgcn_sched_barrier(0);
             if (k < 2 * MT) {
-                const int mt = k % MT, nt = k / MT;
-                if (k < MT) ops_wait_row<MT>(k, o);
+                const int mt = k >> 1, nt = k & 1;
                 const bf16x8 A = __builtin_bit_cast(bf16x8, o.a[mt]);
-                if (k == (MT < 2 ? MT : 2)) widen6(1);
-                const f32x4 tlo = mfma_bf16(A, m160lo), thi = mfma_bf16(A, m160hi);
+                if (nt == 0) {
+                    ops_wait_row<MT>(mt, o);
+                    tlo = mfma_bf16(A, m160lo);
+                    thi = mfma_bf16(A, m160hi);
+                }
                 plo[k % 3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Blo[nt], tlo, 0, 0, 0);
                 phi[k % 3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, Bhi[nt], thi, 0, 0, 0);
             }
@@ -745,15 +754,9 @@ __global__ __launch_bounds__(256) void gemm_tile_reduce_kernel(const float *__re
 
 namespace {
 
-// Row tiles per workgroup: the smallest of 1, 2, 4, 8 that covers M, so
+// Row tiles of X per workgroup: the smallest of 1, 2, 4, 8 that covers M, so
 // that small M computes no padding rows.
-// Row tiles of X per workgroup: the smallest of 1, 2, 4, 8 that covers M
-// (Q6_K at most 4: its four MFMAs per row and column tile hold more
-// registers).
-int tile_mt(int type_id, int M) {
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-    return type_id == kQ6_K && mt > 4 ? 4 : mt;
-}
+int tile_mt(int, int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
 int tile_splits(int type_id, int M, int N, int K, size_t workspace_bytes) {
     const int tm = 16 * tile_mt(type_id, M);
@@ -824,16 +827,8 @@ hipError_t launch_gemm_tile(int type_id, const uint8_t *w, int64_t row_bytes, co
     case kQ5_K:
         GOLLEK_TILE_LAUNCH(kQ5_K);
         break;
-    case kQ6_K:  // mt <= 4
-        if (mt == 1)
-            hipLaunchKernelGGL((gemm_tile_kernel<kQ6_K, 1>), grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S,
-                               part);
-        else if (mt == 2)
-            hipLaunchKernelGGL((gemm_tile_kernel<kQ6_K, 2>), grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S,
-                               part);
-        else
-            hipLaunchKernelGGL((gemm_tile_kernel<kQ6_K, 4>), grid, block, 0, stream, w, row_bytes, x, y, M, N, K, S,
-                               part);
+    case kQ6_K:
+        GOLLEK_TILE_LAUNCH(kQ6_K);
         break;
     default:
         return hipErrorInvalidValue;
