@@ -191,6 +191,40 @@ uint8_t *host_staging(gollek_hip_weight *w, size_t bytes) {
     return w->hstage;
 }
 
+// Copies 16-byte units [0, na) and [na + gap, na + gap + nb) from the pinned
+// staging (mapped for the device) to the same offsets of device memory: for
+// the kilobytes of a call's inputs one kernel launch starts sooner than a
+// DMA-engine copy, and the gap (an output region) does not cross the bus.
+__global__ __launch_bounds__(256) void pull_staging_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                           int64_t na, int64_t gap, int64_t nb) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= na + nb) return;
+    if (i >= na) i += gap;
+    dst[i] = src[i];
+}
+
+// dst <- bytes [0, a) and [a + gap, a + gap + b) of the pinned staging at
+// src (offsets and pointers 16-byte aligned for the kernel): the pull kernel
+// up to kPullMax bytes, the DMA engine otherwise.
+constexpr size_t kPullMax = (size_t)1 << 20;
+hipError_t pull_staging(void *dst, const void *src, size_t a, hipStream_t stream, size_t gap = 0, size_t b = 0) {
+    if (a + b == 0) return hipSuccess;
+    const bool kernel = a + b <= kPullMax && (a | gap | b) % 16 == 0 &&
+                        ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
+    if (!kernel) {
+        hipError_t e = hipMemcpyAsync(dst, src, a, hipMemcpyHostToDevice, stream);
+        if (e == hipSuccess && b > 0)
+            e = hipMemcpyAsync(static_cast<uint8_t *>(dst) + a + gap, static_cast<const uint8_t *>(src) + a + gap, b,
+                               hipMemcpyHostToDevice, stream);
+        return e;
+    }
+    const int64_t n = (int64_t)((a + b) / 16);
+    hipLaunchKernelGGL(pull_staging_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const uint4 *>(src), reinterpret_cast<uint4 *>(dst), (int64_t)(a / 16),
+                       (int64_t)(gap / 16), (int64_t)(b / 16));
+    return hipGetLastError();
+}
+
 int32_t ensure_staging(gollek_hip_weight *w, size_t bytes, char *err, size_t err_len) {
     if (w->staging_bytes >= bytes) return GOLLEK_HIP_OK;
     if (w->staging != nullptr) {
@@ -530,8 +564,8 @@ static int32_t matvec_host(gollek_hip_weight *w, int64_t row0, int64_t nrows, co
     const size_t xn = (size_t)w->cols * sizeof(float);
     uint8_t *hs = host_staging(w, x_bytes + y_bytes);
     if (hs != nullptr) std::memcpy(hs, x, xn);
-    hipError_t e =
-        hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
+    hipError_t e = hs != nullptr ? pull_staging(d_x, hs, xn, w->stream)
+                                 : hipMemcpyAsync(d_x, x, xn, hipMemcpyHostToDevice, w->stream);
     // the prepared layout covers full mat-vecs only (its partition depends on the row count)
     const bool full = row0 == 0 && nrows == w->rows;
     // With the pinned staging the kernel stores y there itself (the buffer is
@@ -714,8 +748,8 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     const size_t xn = (size_t)(m * w->cols) * sizeof(uint16_t);
     uint8_t *hs = host_staging(w, x_bytes + y_bytes);
     if (hs != nullptr) std::memcpy(hs, x, xn);
-    hipError_t e =
-        hipMemcpyAsync(d_x, hs ? (const void *)hs : (const void *)x, xn, hipMemcpyHostToDevice, w->stream);
+    hipError_t e = hs != nullptr ? pull_staging(d_x, hs, xn, w->stream)
+                                 : hipMemcpyAsync(d_x, x, xn, hipMemcpyHostToDevice, w->stream);
     // With the pinned staging the kernels store Y there themselves (mapped
     // for the device; x_bytes keeps it 256-byte aligned, so the split-K
     // path stays available), which saves the device-to-host copy.
@@ -913,7 +947,7 @@ int32_t gollek_hip_moe_grouped(gollek_hip_weight *gate, gollek_hip_weight *up,
         std::memcpy(hs, x, xn);
         std::memcpy(hs + 2 * xb, ids, rn);
         std::memcpy(hs + 2 * xb + rb, weights, rn);
-        e = hipMemcpyAsync(d_x, hs, 2 * xb + 2 * rb, hipMemcpyHostToDevice, s);
+        e = pull_staging(d_x, hs, xn, s, 2 * xb - xn, 2 * rb);
     } else {
         e = hipMemcpyAsync(d_x, x, xn, hipMemcpyHostToDevice, s);
         if (e == hipSuccess) e = hipMemcpyAsync(d_ids, ids, rn, hipMemcpyHostToDevice, s);
@@ -1165,7 +1199,7 @@ int32_t gollek_hip_moe_block(gollek_hip_weight *gate, gollek_hip_weight *up,
     if (hs != nullptr) {
         std::memcpy(hs, x, xn);
         std::memcpy(hs + 2 * xb, logits, ln);
-        e = hipMemcpyAsync(d_x, hs, 2 * xb + lb, hipMemcpyHostToDevice, s);
+        e = pull_staging(d_x, hs, xn, s, 2 * xb - xn, lb);
     } else {
         e = hipMemcpyAsync(d_x, x, xn, hipMemcpyHostToDevice, s);
         if (e == hipSuccess) e = hipMemcpyAsync(d_l, logits, ln, hipMemcpyHostToDevice, s);
