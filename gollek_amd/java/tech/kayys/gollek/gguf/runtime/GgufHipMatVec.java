@@ -34,6 +34,8 @@ import java.util.WeakHashMap;
  *     return;
  * }
  * </pre></li>
+ * <li>A prefill that runs matVecRows once per prompt token (RT/GgufTensorOps.java:666-674):
+ * {@code tryMatVecBatch} with the tokens' vectors, one GEMM per weight.</li>
  * <li>GgufTensorOps.dotRow and dequantizeRow (RT/GgufTensorOps.java:636-650),
  * after checkLayoutRow: {@code tryDotRow} / {@code tryDequantizeRow}, falling
  * through to the Java code when they return false.</li>
@@ -98,6 +100,8 @@ final class GgufHipMatVec {
     private static final Map<GGUFModel, Map<GGUFTensorInfo, MemorySegment>> HANDLES = new WeakHashMap<>();
     /** Handles holding a prepared copy, with the bytes charged for it (guarded by HANDLES). */
     private static final Map<MemorySegment, Long> PREPARED = new IdentityHashMap<>();
+    /** Compacted handles: their prepared layout is their only copy (guarded by HANDLES). */
+    private static final Map<MemorySegment, Boolean> COMPACTED = new IdentityHashMap<>();
     private static long preparedBytes;
     private static boolean preparingStopped;
 
@@ -123,6 +127,58 @@ final class GgufHipMatVec {
             check(rc, err);
         }
         return true;
+    }
+
+    /**
+     * The prefill form of matVecRows: out[t * rows + r] = row r of the tensor
+     * . xRows[t * columns, (t + 1) * columns) for t < m and r < rows, i.e. the
+     * m matVecRows calls the reference makes per prompt
+     * (RT/GgufTensorOps.java:666-674) as one small-M GEMM on the matrix cores
+     * (gollek_hip_gemm_bf16), X rounded to bf16 (nearest, ties to even) as
+     * that GEMM takes it.  A tensor first seen here keeps its GGUF rows (no
+     * prepared copy); one already compacted by a mat-vec holds no GGUF rows,
+     * so this returns false and the caller runs the m mat-vecs.  False also
+     * when the route is not taken.
+     */
+    static boolean tryMatVecBatch(GGUFModel model, GGUFTensorInfo tensor, long rows, int columns, long rowBytes,
+                                  float[] xRows, int m, float[] out) {
+        Binding b = Binding.get();
+        if (b == null || !supportsType(tensor.typeId())) {
+            return false;
+        }
+        if (m < 0 || (long) xRows.length < (long) m * columns || (long) out.length < (long) m * rows) {
+            throw new IllegalArgumentException("Batch of " + m + " vectors needs " + ((long) m * columns)
+                    + " inputs and " + ((long) m * rows) + " outputs");
+        }
+        MemorySegment w = handle(b, model, tensor, rows, columns, rowBytes, false);
+        synchronized (HANDLES) {
+            if (COMPACTED.containsKey(w)) {
+                return false;
+            }
+        }
+        if (m == 0) {
+            return true;
+        }
+        short[] x = new short[Math.multiplyExact(m, columns)];
+        for (int i = 0; i < x.length; i++) {
+            x[i] = bf16(xRows[i]);
+        }
+        try (Arena arena = Arena.ofConfined()) {
+            MemorySegment err = arena.allocate(ERR_LEN);
+            int rc = b.gemmBf16(w, MemorySegment.ofArray(x), (long) x.length, (long) m, MemorySegment.ofArray(out),
+                    (long) out.length, err, (long) ERR_LEN);
+            check(rc, err);
+        }
+        return true;
+    }
+
+    /** The bf16 bit pattern nearest to v (ties to even); a NaN stays a (quiet) NaN. */
+    static short bf16(float v) {
+        int bits = Float.floatToRawIntBits(v);
+        if ((bits & 0x7FFFFFFF) > 0x7F800000) {
+            return (short) ((bits >>> 16) | 0x0040);
+        }
+        return (short) ((bits + 0x7FFF + ((bits >>> 16) & 1)) >>> 16);
     }
 
     /** Row {@code row} of the tensor . vector into out[0]; false when the route is not taken. */
@@ -233,6 +289,7 @@ final class GgufHipMatVec {
             handles = HANDLES.remove(model);
             if (handles != null) {
                 for (MemorySegment w : handles.values()) {
+                    COMPACTED.remove(w);
                     Long charged = PREPARED.remove(w);
                     if (charged != null) {
                         preparedBytes -= charged.longValue();
@@ -284,7 +341,9 @@ final class GgufHipMatVec {
                         // one copy when compacted; otherwise a second one, charged
                         boolean compacted = !"false".equals(System.getProperty("gollek.hip.compact", "true"))
                                 && b.weightCompact(w, err, (long) ERR_LEN) == OK;
-                        if (!compacted) {
+                        if (compacted) {
+                            COMPACTED.put(w, Boolean.TRUE);
+                        } else {
                             PREPARED.put(w, size);
                             preparedBytes += size;
                         }
@@ -347,6 +406,7 @@ final class GgufHipMatVec {
         private final MethodHandle dequantizeRows;
         private final MethodHandle moeBlock;
         private final MethodHandle moeSharedExpert;
+        private final MethodHandle gemmBf16;
 
         /** The binding, or null when the route is disabled or the library cannot be used here. */
         static Binding get() {
@@ -437,6 +497,11 @@ final class GgufHipMatVec {
                             ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.ADDRESS,
                             ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG,
                             ValueLayout.ADDRESS, ValueLayout.JAVA_LONG), true);
+            this.gemmBf16 = downcall(linker, lookup, "gollek_hip_gemm_bf16",
+                    FunctionDescriptor.of(ValueLayout.JAVA_INT,
+                            ValueLayout.ADDRESS, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.JAVA_LONG,
+                            ValueLayout.ADDRESS, ValueLayout.JAVA_LONG, ValueLayout.ADDRESS, ValueLayout.JAVA_LONG),
+                    true);
             int abi = (int) version.invokeExact();
             if (abi / 10000 != ABI_MAJOR) {
                 throw new IllegalStateException("libgollek_hip ABI " + abi + " is not major " + ABI_MAJOR);
@@ -554,6 +619,15 @@ final class GgufHipMatVec {
                             long errLen) {
             try {
                 return (int) moeSharedExpert.invokeExact(gate, up, down, gateRow, x, tokens, out, outLen, err, errLen);
+            } catch (Throwable t) {
+                throw propagate(t);
+            }
+        }
+
+        int gemmBf16(MemorySegment weight, MemorySegment x, long xLen, long m, MemorySegment y, long yLen,
+                     MemorySegment err, long errLen) {
+            try {
+                return (int) gemmBf16.invokeExact(weight, x, xLen, m, y, yLen, err, errLen);
             } catch (Throwable t) {
                 throw propagate(t);
             }

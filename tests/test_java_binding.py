@@ -81,10 +81,10 @@ def test_heap_array_arguments_use_critical_downcalls():
     # only critical downcalls with heap access accept.
     text = java_text()
     desc = java_descriptors()
-    for fn in ("matvecRows", "dotRow", "dequantizeRows", "moeBlock", "moeSharedExpert"):
+    for fn in ("matvecRows", "dotRow", "dequantizeRows", "moeBlock", "moeSharedExpert", "gemmBf16"):
         assert re.search(rf"b\.{fn}\([^;]*MemorySegment\.ofArray", text), fn
     for sym in ("gollek_hip_matvec_rows", "gollek_hip_dot_row", "gollek_hip_dequantize_rows",
-                "gollek_hip_moe_block", "gollek_hip_moe_shared_expert"):
+                "gollek_hip_moe_block", "gollek_hip_moe_shared_expert", "gollek_hip_gemm_bf16"):
         assert desc[sym][2], sym
 
 
@@ -100,6 +100,7 @@ WRAPPERS = {  # typed wrapper -> the symbol whose handle it invokes
     "dequantizeRows": "gollek_hip_dequantize_rows",
     "moeBlock": "gollek_hip_moe_block",
     "moeSharedExpert": "gollek_hip_moe_shared_expert",
+    "gemmBf16": "gollek_hip_gemm_bf16",
 }
 
 
@@ -168,6 +169,64 @@ def test_supported_types_match_the_header():
     ids = {int(v) for v in re.findall(r"#define GOLLEK_HIP_Q\w+ (\d+)", hdr)}
     m = re.search(r"static boolean supportsType\(int typeId\) \{\s*return (.*?);", text, flags=re.S)
     assert m and {int(v) for v in re.findall(r"typeId == (\d+)", m.group(1))} == ids
+
+
+def test_batch_checks_lengths_and_skips_compacted_handles():
+    # gemm_bf16 reads m * columns bf16 values and writes m * rows floats: the
+    # adapter checks both before handing heap arrays over, creates the handle
+    # without a prepared copy, and leaves compacted handles to the mat-vecs.
+    text = java_text()
+    body = re.search(r"static boolean tryMatVecBatch\((.*?)\n    \}", text, flags=re.S).group(1)
+    for cond in ("xRows.length < (long) m * columns", "out.length < (long) m * rows"):
+        assert cond in body, cond
+    assert "handle(b, model, tensor, rows, columns, rowBytes, false)" in body
+    assert body.index("COMPACTED.containsKey(w)") < body.index("b.gemmBf16(")
+    assert body.index("IllegalArgumentException") < body.index("b.gemmBf16(")
+
+
+def _java_bf16(v: float) -> int:
+    # GgufHipMatVec.bf16, statement for statement, on 32-bit ints
+    import struct
+    bits = struct.unpack("<i", struct.pack("<f", v))[0]
+    if (bits & 0x7FFFFFFF) > 0x7F800000:
+        return (((bits & 0xFFFFFFFF) >> 16) | 0x0040) & 0xFFFF
+    return (((bits + 0x7FFF + (((bits & 0xFFFFFFFF) >> 16) & 1)) & 0xFFFFFFFF) >> 16) & 0xFFFF
+
+
+def test_java_bf16_rounding_is_round_to_nearest_even():
+    # The adapter's float -> bf16 rounding, checked against numpy's exact
+    # nearest-even rounding through float64 on values around every rounding
+    # boundary class: ties to even both ways, carries into the exponent,
+    # the largest finite values (rounding to inf), subnormals, signed zeros,
+    # infinities and NaNs.
+    import numpy as np
+    text = java_text()
+    assert "return (short) ((bits + 0x7FFF + ((bits >>> 16) & 1)) >>> 16);" in text
+    assert "return (short) ((bits >>> 16) | 0x0040);" in text
+    rng = np.random.default_rng(7)
+    base = rng.integers(0, 1 << 32, 20000, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0x00000000, 0x80000000, 0x3F808000, 0x3F818000, 0x3F80FFFF, 0x3F7FFFFF, 0x7F7FFFFF,
+                         0x7F7F8000, 0x7F7F7FFF, 0x00008000, 0x00018000, 0x807FFFFF, 0x7F800000, 0xFF800000,
+                         0x7FC00000, 0x7F800001, 0xFFFFFFFF], dtype=np.uint32)
+    for u in np.concatenate([base, specials, base & 0xFFFF0000 | 0x8000]):
+        f = float(np.uint32(u).view(np.float32))
+        got = _java_bf16(f)
+        if np.isnan(f):
+            assert (got & 0x7F80) == 0x7F80 and (got & 0x7F) != 0, hex(int(u))
+            continue
+        if np.isinf(f):
+            assert got == int(u) >> 16, hex(int(u))
+            continue
+        # exact nearest-even between the two bf16 neighbours of the same sign
+        # (a neighbour past the largest finite bf16 counts as +-2^128)
+        lo = int(u) >> 16
+        hi = lo + 1
+        v_lo = float(np.uint32(lo << 16).view(np.float32))
+        v_hi = (float(np.uint32(hi << 16).view(np.float32)) if (hi & 0x7FFF) != 0x7F80
+                else float(np.copysign(2.0 ** 128, f)))
+        d_lo, d_hi = abs(f - v_lo), abs(v_hi - f)
+        want = lo if d_lo < d_hi or (d_lo == d_hi and lo % 2 == 0) else hi
+        assert got == (want & 0xFFFF), (hex(int(u)), hex(got), hex(want))
 
 
 @pytest.mark.skipif(not RT.exists(), reason="reference sources not present")
