@@ -125,8 +125,8 @@ MoeLayout moe_layout(int64_t tokens, int64_t top_k, int64_t hidden, int64_t inte
 
 // out[T, H] = sum_j w[t,j] down_e(silu(gate_e x_t) * up_e x_t) for stacked
 // gate / up / down experts of types Q8_0, Q4_0, Q4_K, Q5_K or Q6_K (each
-// matrix its own type): the matrix-core passes for Q4_K or Q5_K gate / up
-// (moe_kq_mfma_supported) and for all-Q4_0 where they take the shape, the
+// matrix its own type): the matrix-core passes for Q4_K, Q5_K or Q6_K gate /
+// up (moe_kq_mfma_supported) and for all-Q4_0 where they take the shape, the
 // v_dot4 passes for all-Q4_K otherwise, the row kernels for everything else;
 // ws must hold moe_layout(...).total bytes.
 hipError_t launch_moe(int gate_type, int up_type, int down_type, const uint8_t *gate, const uint8_t *up,
@@ -151,7 +151,8 @@ hipError_t launch_moe_q4k_dot4(const uint8_t *gate, const uint8_t *up, const uin
 // Routes (tokens x top_k) one launch of the matrix-core passes routes in LDS.
 constexpr int kMoeMfmaMaxRoutes = 2048;
 // K-quant experts on the matrix-core passes (gguf_moe_mfma.hip): gate / up
-// both Q4_K or both Q5_K (hidden up to 4096); down rows
+// both Q4_K or both Q5_K (hidden up to 4096) or both Q6_K (hidden up to 2048,
+// an even number of superblocks); down rows
 // Q4_K, Q5_K or Q6_K through the token-major pass (inter up to 1024), else
 // Q4_K or Q5_K through the expert-major pass; hidden and inter multiples of
 // 256, x 16-byte aligned.

@@ -29,7 +29,8 @@
 // in LDS), all-Q4_K layers up to hidden 4096 on the v_dot4 kernels
 // (moe_expert_kernel, x and h as integer digit planes, gguf_dot4.hpp), and
 // anything else on moe_generic_expert_kernel (byte loads, any alignment).
-// launch_moe sends the shapes the matrix-core passes take there first.
+// launch_moe sends the shapes the matrix-core passes take there first
+// (more than 2048 routes as token slices of at most 2048 / top_k tokens).
 #include "gguf_block_dot.hpp"
 #include "gguf_dot4.hpp"
 #include "gguf_kernels.hpp"

@@ -1,6 +1,6 @@
 // gguf_moe_mfma.hip -- grouped MoE expert FFN on the gfx950 matrix cores:
-// Q4_K or Q5_K gate / up experts with Q4_K, Q5_K or Q6_K down experts, and
-// all-Q4_0 experts.
+// Q4_K, Q5_K or Q6_K gate / up experts (Q6_K up to hidden 2048) with Q4_K,
+// Q5_K or Q6_K down experts, and all-Q4_0 experts.
 //
 // Semantics as gguf_moe.hip (MoeForwardPass.java:217-240, :461-472; swigluFfn
 // DirectForwardFfnService.java:40-61): h_pair = silu(gate_e x_t) * (up_e x_t),
@@ -54,12 +54,13 @@ constexpr int kMoWaves = 16;
 constexpr int kMoThreads = kMoWaves * 64;
 constexpr int kMoGroup = 4;          // routes per group (two MFMA pairs)
 // The item ring: three slots of 38 KB; for Q5_K rows (176-byte
-// superblocks) two slots of 46 KB, so that 16 gate and 16 up rows of 8
-// superblocks (hidden 2048) fit one slot.
+// superblocks) two slots of 46 KB and for Q6_K rows (210 bytes) two of 54
+// KB, so that 16 gate and 16 up rows of 8 superblocks (hidden 2048) fit one
+// slot.
 template <int WT>
 struct MoRing {
-    static constexpr int kMaxDma = WT == kQ5_K ? 46 : 38;  // 1 KB loads per item slot
-    static constexpr int kSlots = WT == kQ5_K ? 2 : 3;
+    static constexpr int kMaxDma = WT == kQ6_K ? 54 : WT == kQ5_K ? 46 : 38;  // 1 KB loads per item slot
+    static constexpr int kSlots = WT == kQ5_K || WT == kQ6_K ? 2 : 3;
     static constexpr int kSlot = kMaxDma * 1024;
     static constexpr int kDmaPerWave = (kMaxDma + kMoWaves - 1) / kMoWaves;
 };
@@ -92,7 +93,7 @@ __device__ __forceinline__ int wave_scan_incl(int v) {
     return v;
 }
 
-// Builds R for work units of tiles_e items per (expert, group of kMoGroup
+// Builds R for work units of tiles_e items per (expert, group of `group`
 // routes).  tmp: P + E ints of LDS that nothing else uses meanwhile.  Every
 // thread of the workgroup calls this; it ends with a barrier.  Counts by LDS
 // atomics, then wave 0 scans the experts in chunks of 64 (wave_scan_incl)
@@ -100,7 +101,7 @@ __device__ __forceinline__ int wave_scan_incl(int v) {
 // expert's running offset plus its rank among the chunk's equal keys (found
 // by ballots over the key bits).
 __device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__restrict__ wts, int P,
-                              int E, int tiles_e, MoeRouteLds &R, int32_t *tmp) {
+                              int E, int tiles_e, int group, MoeRouteLds &R, int32_t *tmp) {
     int32_t *keys = tmp, *run = tmp + P;
     const int tid = (int)threadIdx.x, lane = tid & 63;
     for (int e = tid; e < E; e += (int)blockDim.x) run[e] = 0;
@@ -118,7 +119,7 @@ __device__ void moe_route_lds(const int32_t *__restrict__ ids, const float *__re
         for (int base = 0; base < E; base += 64) {
             const int e = base + lane;
             const int c = e < E ? run[e] : 0;
-            const int units = tiles_e * ((c + kMoGroup - 1) / kMoGroup);
+            const int units = tiles_e * ((c + group - 1) / group);
             const int a = wave_scan_incl(c), b = wave_scan_incl(units);
             const uint64_t ub = __ballot(c > 0);
             if (e < E) {
@@ -236,10 +237,15 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     const float *__restrict__ wts, int E, int P, float *__restrict__ out) {
     static_assert(MODE == 0 || !REC, "records are pass 0's output");
     static_assert(HV == 1 || (HV == 2 && MODE == 0), "K-halves in pass 0 only");
-    static_assert(WT == kQ4_K || WT == kQ5_K || (WT == kQ4_0 && HV == 1), "Q4_0 rows in one half");
+    static_assert(WT == kQ4_K || WT == kQ5_K || (WT == kQ4_0 && HV == 1) || (WT == kQ6_K && HV == 1 && MODE == 0),
+                  "Q4_0 rows in one half; Q6_K gate / up rows in one half");
     // bytes of a 256-column piece of a row (eight Q4_0 blocks are 144, as a
     // Q4_K superblock)
-    constexpr uint32_t PB = WT == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+    constexpr uint32_t PB = WT == kQ6_K ? 210u : WT == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+    // routes per group: Q6_K takes one route per MFMA (its 16-element scale
+    // groups need 12 A rows), so two routes' operands fill the registers
+    // four take for the other types
+    constexpr int kGrp = WT == kQ6_K ? 2 : kMoGroup;
     using RG = MoRing<WT>;
     constexpr int kMoMaxDma = RG::kMaxDma, kMoSlots = RG::kSlots, kMoSlot = RG::kSlot;
     constexpr int kMoDmaPerWave = RG::kDmaPerWave;
@@ -254,7 +260,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
     __shared__ MoeRouteLds R;
 
     // Routing (the ring is free until the first loads below).
-    moe_route_lds(ids, wts, P, E, G.tiles_e, R, reinterpret_cast<int32_t *>(ring));
+    moe_route_lds(ids, wts, P, E, G.tiles_e, kGrp, R, reinterpret_cast<int32_t *>(ring));
     const int32_t *offsets = R.offsets, *used = R.used, *items = R.items;
     const uint16_t *pairs = R.pairs;
     const int nused = R.nused;
@@ -308,7 +314,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         c.u = lo;
         c.e = used[c.u];
         c.cnt = offsets[c.e + 1] - offsets[c.e];
-        c.groups = (c.cnt + kMoGroup - 1) / kMoGroup;
+        c.groups = (c.cnt + kGrp - 1) / kGrp;
         const int j = i - items[c.u];
         c.group = j / G.tiles_e;
         c.tile = j - c.group * G.tiles_e;
@@ -322,7 +328,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         if (++c.u < nused) {
             c.e = used[c.u];
             c.cnt = offsets[c.e + 1] - offsets[c.e];
-            c.groups = (c.cnt + kMoGroup - 1) / kMoGroup;
+            c.groups = (c.cnt + kGrp - 1) / kGrp;
         }
     };
     auto item_of = [&](const Cursor &c) {
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         it.group = c.group;
         it.tile = c.tile / HV;
         it.half = c.tile - HV * it.tile;
-        it.ntok = min(kMoGroup, c.cnt - kMoGroup * c.group);
+        it.ntok = min(kGrp, c.cnt - kGrp * c.group);
         it.row0 = it.tile * rows_item;
         it.nrows = min(rows_item, G.rows_e - it.row0);
         return it;
@@ -421,34 +427,37 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
             return;
         }
         const uint32_t sbase = (uint32_t)(uintptr_t)(lds_ptr)scratch[wv];
-        int vrow[kMoGroup];  // vector row of each route
+        int vrow[kGrp];  // vector row of each route
 #pragma unroll
-        for (int j = 0; j < kMoGroup; j++) {
-            const int p = pairs[offsets[it.e] + kMoGroup * it.group + min(j, it.ntok - 1)];
+        for (int j = 0; j < kGrp; j++) {
+            const int p = pairs[offsets[it.e] + kGrp * it.group + min(j, it.ntok - 1)];
             vrow[j] = MODE == 0 ? p / top_k : p;
         }
         // route ids for the reductions (lane-indexed: four constant LDS
         // addresses would each hold a register across the item loop)
-        if (wv == 0 && lane < kMoGroup)
-            gid[lane] = pairs[offsets[it.e] + kMoGroup * it.group + min(lane, it.ntok - 1)];
+        if (wv == 0 && lane < kGrp)
+            gid[lane] = pairs[offsets[it.e] + kGrp * it.group + min(lane, it.ntok - 1)];
         // A half at a time (HV = 2: the second half's vectors are loaded once
         // the first half's digits are built, which keeps the registers in
         // bounds; their wait also covers the ring loads issued before them).
 #pragma unroll
         for (int hf = 0; hf < HV; hf++) {
-        float4 v[kMoGroup];
+        float4 v[kGrp];
         // loads first, then one wait (this also drains the ring's loads)
 #pragma unroll
-        for (int j = 0; j < kMoGroup; j++)
+        for (int j = 0; j < kGrp; j++)
             v[j] = reinterpret_cast<const float4 *>(vec + (int64_t)vrow[j] * G.vec_len + (sb + hf * G.nsb) * kQK)[lane];
         if (hf == 0) between();
         if (drain || hf > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         // Consume every loaded vector so the compiler's own wait comes here
         // (it cannot see the one above): a load it still thought outstanding
         // would make it wait for all loads before the next write of its registers.
-        asm volatile("" ::"v"(v[0].x), "v"(v[1].x), "v"(v[2].x), "v"(v[3].x));
+        if constexpr (kGrp == 2)
+            asm volatile("" ::"v"(v[0].x), "v"(v[1].x));
+        else
+            asm volatile("" ::"v"(v[0].x), "v"(v[1].x), "v"(v[2].x), "v"(v[3].x));
 #pragma unroll
-        for (int j = 0; j < kMoGroup; j++) {
+        for (int j = 0; j < kGrp; j++) {
             if (j >= it.ntok) break;  // uniform
             const float vv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
             uint32_t mb = 0;
@@ -472,10 +481,15 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 d2 |= ((uint32_t)c2 & 0xFFu) << (8 * k);
                 sx += X;
             }
-            sx = sum8_i(sx);
+            if constexpr (WT == kQ6_K) {  // sums over 16 elements (four lanes)
+                sx += dpp_i<0xB1>(sx);
+                sx += dpp_i<0x4E>(sx);
+            } else {
+                sx = sum8_i(sx);
+            }
             const float scale = finite ? ldexpf(1.0f, ex - 22) : __builtin_nanf("");
-            // scratch: planes at 0 / 256 / 512, sub-block sums (fp32) at 768 + 4 j,
-            // scale at 832
+            // scratch: planes at 0 / 256 / 512, sub-block sums (fp32) at 768 + 4 j
+            // (Q6_K: 16-element sums at 768 + 4 quarter), scale at 832
             asm volatile(
                 "ds_write_b32 %0, %1\n\t"
                 "ds_write_b32 %0, %2 offset:256\n\t"
@@ -483,7 +497,15 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                 :
                 : "v"(sbase + 4 * lane), "v"(d0), "v"(d1), "v"(d2)
                 : "memory");
-            if constexpr (HV == 1) {
+            if constexpr (WT == kQ6_K) {
+                if ((lane & 3) == 0)
+                    asm volatile("ds_write_b32 %0, %1 offset:768"
+                                 :
+                                 : "v"(sbase + 4 * (lane >> 2)), "v"(__float_as_int((float)sx * scale))
+                                 : "memory");
+                if (lane == 0)
+                    asm volatile("ds_write_b32 %0, %1 offset:832" : : "v"(sbase), "v"(__float_as_int(scale)) : "memory");
+            } else if constexpr (HV == 1) {
                 if ((lane & 7) == 0)
                     asm volatile("ds_write_b32 %0, %1 offset:768"
                                  :
@@ -504,6 +526,46 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
                                  : "memory");
                 if (lane == 0)
                     asm volatile("ds_write_b32 %0, %1 offset:32" : : "v"(slot), "v"(__float_as_int(scale)) : "memory");
+            }
+            if constexpr (WT == kQ6_K) {
+                // Q6_K: one route per MFMA.  Chunk c covers elements 128 (c >> 1)
+                // + 32 (c & 1) + l and + 64 (l < 32); A row m = 4 q + p holds
+                // plane p < 3 of quarter q (16 elements), live on the lanes g
+                // with g >> 1 == q & 1, in bytes 0..7 (q < 2, l = 8 g ..) or
+                // 8..15 (q >= 2, + 64).  Output lane n + 16 g: quarter g, whose
+                // sum of x is quarter 8 (c >> 1) + 2 (c & 1) + 4 (g >> 1) + (g & 1).
+                const int m = lane & 15, p = m & 3, q = m >> 2;
+                uint2 lo[4], hi[4];
+                float xq[4], sc;
+                asm volatile(
+                    "ds_read_b64 %0, %13\n\t"
+                    "ds_read_b64 %1, %13 offset:32\n\t"
+                    "ds_read_b64 %2, %13 offset:128\n\t"
+                    "ds_read_b64 %3, %13 offset:160\n\t"
+                    "ds_read_b64 %4, %13 offset:64\n\t"
+                    "ds_read_b64 %5, %13 offset:96\n\t"
+                    "ds_read_b64 %6, %13 offset:192\n\t"
+                    "ds_read_b64 %7, %13 offset:224\n\t"
+                    "ds_read_b32 %8, %14 offset:768\n\t"
+                    "ds_read_b32 %9, %14 offset:776\n\t"
+                    "ds_read_b32 %10, %14 offset:800\n\t"
+                    "ds_read_b32 %11, %14 offset:808\n\t"
+                    "ds_read_b32 %12, %15 offset:832\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(lo[0]), "=&v"(lo[1]), "=&v"(lo[2]), "=&v"(lo[3]), "=&v"(hi[0]), "=&v"(hi[1]),
+                      "=&v"(hi[2]), "=&v"(hi[3]), "=&v"(xq[0]), "=&v"(xq[1]), "=&v"(xq[2]), "=&v"(xq[3]), "=&v"(sc)
+                    : "v"(sbase + (p < 3 ? p : 0) * 256 + 8 * g), "v"(sbase + 16 * (g >> 1) + 4 * (g & 1)),
+                      "v"(sbase)
+                    : "memory");
+                const bool lo_live = p < 3 && q == (g >> 1), hi_live = p < 3 && q == 2 + (g >> 1);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    A[j][c] = i32x4{lo_live ? (int)lo[c].x : 0, lo_live ? (int)lo[c].y : 0,
+                                    hi_live ? (int)hi[c].x : 0, hi_live ? (int)hi[c].y : 0};
+                    xs4[j][c] = xq[c];
+                }
+                xs[j] = sc;
+                continue;
             }
             // A rows of route j: m = 8 (j & 1) + 4 ha + p in lanes m + 16 g; this
             // output lane's sub-blocks 2 c + h.
@@ -662,7 +724,99 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kMoDmaPerWave * (kMoSlots - 2)) : "memory");
         if (have_prev) reduce_prev(prev, i - 1);
         issue(slot == 0 ? kMoSlots - 1 : slot - 1, i + kMoSlots - 1);
-        if (active && WT == kQ4_0) {
+        if constexpr (WT == kQ6_K) {
+            if (active) {
+                // Q6_K rows (210-byte superblocks: ql[128], qh[64], 16 int8
+                // scales, d), 0 or 2 bytes past a dword in the slot: aligned
+                // dwords, realigned.  Chunk c = (half c >> 1, part c & 1) is ql
+                // bytes 32 c + l, low nibbles for elements 128 (c >> 1) + 32 (c &
+                // 1) + l and high nibbles for + 64, the two high bits from qh
+                // byte 32 (c >> 1) + l (bits 2 (c & 1), and 4 + 2 (c & 1)); lane
+                // group g takes l = 8 g .. 8 g + 7 as B bytes 0..7 and 8..15.
+                // Codes q = 0..63 against one route's x digits per MFMA; output
+                // lane n + 16 g holds quarter g's plane sums, whose sum q X can
+                // reach 16 * 63 * 2^22 and so combine in fp32.  value = d sum
+                // sc (xs S - 32 X) over the quarters, the reference's d sc (q -
+                // 32) per element.
+                const uint32_t sa = a_h0 + (uint32_t)slot * kMoSlot;
+                const uint32_t sh = sa & 3u, ab = sa - sh, aq = ab + 8u * (uint32_t)g;
+                uint2 p01[6], s01, s23;
+                uint32_t p2[6], s4;
+                asm volatile(
+                    "ds_read2_b32 %0, %15 offset1:1\n\t"
+                    "ds_read_b32 %6, %15 offset:8\n\t"
+                    "ds_read2_b32 %1, %15 offset0:8 offset1:9\n\t"
+                    "ds_read_b32 %7, %15 offset:40\n\t"
+                    "ds_read2_b32 %2, %15 offset0:16 offset1:17\n\t"
+                    "ds_read_b32 %8, %15 offset:72\n\t"
+                    "ds_read2_b32 %3, %15 offset0:24 offset1:25\n\t"
+                    "ds_read_b32 %9, %15 offset:104\n\t"
+                    "ds_read2_b32 %4, %15 offset0:32 offset1:33\n\t"
+                    "ds_read_b32 %10, %15 offset:136\n\t"
+                    "ds_read2_b32 %5, %15 offset0:40 offset1:41\n\t"
+                    "ds_read_b32 %11, %15 offset:168\n\t"
+                    "ds_read2_b32 %12, %16 offset0:48 offset1:49\n\t"
+                    "ds_read2_b32 %13, %16 offset0:50 offset1:51\n\t"
+                    "ds_read_b32 %14, %16 offset:208\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(p01[0]), "=&v"(p01[1]), "=&v"(p01[2]), "=&v"(p01[3]), "=&v"(p01[4]), "=&v"(p01[5]),
+                      "=&v"(p2[0]), "=&v"(p2[1]), "=&v"(p2[2]), "=&v"(p2[3]), "=&v"(p2[4]), "=&v"(p2[5]),
+                      "=&v"(s01), "=&v"(s23), "=&v"(s4)
+                    : "v"(aq), "v"(ab)
+                    : "memory");
+                uint32_t ql[4][2], qh[2][2];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    ql[c][0] = __builtin_amdgcn_alignbyte(p01[c].y, p01[c].x, sh);
+                    ql[c][1] = __builtin_amdgcn_alignbyte(p2[c], p01[c].y, sh);
+                }
+#pragma unroll
+                for (int ip = 0; ip < 2; ip++) {
+                    qh[ip][0] = __builtin_amdgcn_alignbyte(p01[4 + ip].y, p01[4 + ip].x, sh);
+                    qh[ip][1] = __builtin_amdgcn_alignbyte(p2[4 + ip], p01[4 + ip].y, sh);
+                }
+                const uint32_t s0 = __builtin_amdgcn_alignbyte(s01.y, s01.x, sh);
+                const uint32_t s1 = __builtin_amdgcn_alignbyte(s23.x, s01.y, sh);
+                const uint32_t s2 = __builtin_amdgcn_alignbyte(s23.y, s23.x, sh);
+                const uint32_t s3 = __builtin_amdgcn_alignbyte(s4, s23.y, sh);
+                const float d = half_bits_to_float_fast(s4 >> (8 * sh));
+                i32x4 B[4];
+                float scq[4];
+                // quarter g's scale: byte 2 (c & 1) + (g & 1) of scale dword 2 (c >> 1) + (g >> 1)
+                const uint32_t slo = (g >> 1) ? s1 : s0, shi = (g >> 1) ? s3 : s2;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int ip = c >> 1, pt = c & 1;
+                    uint32_t b[4];
+#pragma unroll
+                    for (int k = 0; k < 2; k++) {
+                        const uint32_t hq = qh[ip][k];
+                        b[k] = (ql[c][k] & 0x0F0F0F0Fu) | ((pt == 0 ? hq << 4 : hq << 2) & 0x30303030u);
+                        b[2 + k] = ((ql[c][k] >> 4) & 0x0F0F0F0Fu) | ((pt == 0 ? hq : hq >> 2) & 0x30303030u);
+                    }
+                    B[c] = i32x4{(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+                    const uint32_t sw = ip ? shi : slo;
+                    scq[c] = (float)(int)(int8_t)((sw >> (8 * ((g & 1) + 2 * pt))) & 0xFFu);
+                }
+#pragma unroll
+                for (int j = 0; j < kGrp; j++) {
+                    if (j >= cur.ntok) break;  // uniform
+                    i32x4 D[4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) D[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j][c], B[c], zero4, 0, 0, 0);
+                    float v = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float S = fmaf((float)D[c][2], 65536.0f, (float)(D[c][0] + 256 * D[c][1]));
+                        v = fmaf(scq[c], fmaf(S, xs[j], -32.0f * xs4[j][c]), v);
+                    }
+                    v *= d;
+                    v += __shfl_xor(v, 16);
+                    v += __shfl_xor(v, 32);
+                    if (g == 0) part[i & 1][j][wv][n] = v;
+                }
+            }
+        } else if (active && WT == kQ4_0) {
             // Q4_0: a 144-byte piece is eight 18-byte blocks; chunk c (64
             // columns) is blocks 2c and 2c + 1.  Lane group g takes elements
             // 8 g .. 8 g + 7 of each: quant bytes 8 (g & 1) .. + 7 of the
@@ -952,8 +1106,10 @@ __global__ __launch_bounds__(kMoThreads) void moe_expert_tile_kernel(
 // half q & 1 of sub-block 2 c + (q >> 1)), live on the lanes g with
 // g >> 1 == q & 1, in bytes 0..7 (q < 2, low nibbles) or 8..15; output lane
 // n + 16 g holds the plane sums of row n and quarter g,
-// D0 + 256 D1 + 65536 D2 = sum q X exactly (|.| <= 16 * 15 * 2^22), which it
-// scales by the quarter's scale before the sub-block's d sc.
+// D0 + 256 D1 + 65536 D2 = sum q X, exactly in int32 for Q4_K and Q5_K
+// codes (|.| <= 16 * 31 * 2^22 < 2^31) and in fp32 for Q6_K's (up to
+// 16 * 63 * 2^22), which it scales by the quarter's scale before the
+// sub-block's d sc.
 namespace {
 
 constexpr int kMdMaxWaves = 8;
@@ -1480,8 +1636,9 @@ __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
             for (int c = 0; c < 4; c++) {
                 const uint32_t sw = (c >> 1) ? shi : slo;
                 const float scv = (float)(int)(int8_t)((sw >> (8 * ((g & 1) + 2 * (c & 1)))) & 0xFFu);
-                const float S =
-                    (float)(int)(((uint32_t)D[c][2] << 16) + (((uint32_t)D[c][1] << 8) + (uint32_t)D[c][0]));
+                // sum q X over the quarter can reach 16 * 63 * 2^22 > 2^31:
+                // the planes combine in fp32 (relative error under 2^-23)
+                const float S = fmaf((float)D[c][2], 65536.0f, (float)(D[c][0] + 256 * D[c][1]));
                 vs = fmaf(scv, fmaf(S, xp[c].x, -32.0f * xp[c].y), vs);
             }
             v = fmaf(d, vs, v);
@@ -1525,12 +1682,17 @@ __global__ __launch_bounds__(kMdMaxWaves * 64) void moe_down_combine_kernel(
 namespace {
 
 // Bytes of a row's 256-column piece: a Q4_K superblock (144, as eight Q4_0
-// blocks) or a Q5_K superblock (176).
-constexpr uint32_t piece_bytes(int type) { return type == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes; }
+// blocks), a Q5_K superblock (176) or a Q6_K superblock (210).
+constexpr uint32_t piece_bytes(int type) {
+    return type == kQ6_K ? 210u : type == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+}
 
 // 1 KB loads an item slot holds for `type` rows.
 int max_dma(int type) {
-    return type == kQ5_K ? MoRing<kQ5_K>::kMaxDma : type == kQ4_0 ? MoRing<kQ4_0>::kMaxDma : MoRing<kQ4_K>::kMaxDma;
+    return type == kQ6_K   ? MoRing<kQ6_K>::kMaxDma
+           : type == kQ5_K ? MoRing<kQ5_K>::kMaxDma
+           : type == kQ4_0 ? MoRing<kQ4_0>::kMaxDma
+                           : MoRing<kQ4_K>::kMaxDma;
 }
 
 // Geometry of pass `mode` over `type` rows.  The caller has checked that H
@@ -1540,9 +1702,10 @@ MoeTileGeom make_geom(int mode, int E, int H, int I, int type) {
     const int kMoMaxDma = max_dma(type);
     MoeTileGeom g{};
     const int K = mode == 0 ? H : I;
-    // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all banks
+    // a pitch whose 16-byte units are odd modulo 16 spreads 16 rows over all
+    // banks (Q6_K rows, 210 bytes a superblock, rounded up to 16 bytes first)
     auto pitch_of = [pb](int nsb) {
-        const uint32_t rb = (uint32_t)nsb * pb;
+        const uint32_t rb = ((uint32_t)nsb * pb + 15u) / 16u * 16u;
         return (rb / 16) % 2 == 1 ? rb : rb + 16;
     };
     auto part_dma_of = [&](int nsb, int rt) { return (16 * rt * (int)pitch_of(nsb) + 1023) / 1024; };
@@ -1612,8 +1775,11 @@ bool token_major_down(int down_type, int E, int H, int I, int T, int top_k, MoeD
 
 bool moe_kq_mfma_supported(int gate_type, int down_type, int E, int H, int I, int T, int top_k,
                            const float *x) {
-    if (gate_type != kQ4_K && gate_type != kQ5_K) return false;
+    if (gate_type != kQ4_K && gate_type != kQ5_K && gate_type != kQ6_K) return false;
     if (!tile_shape_ok(E, H, I, T * top_k, x) || !tile_pass_ok(0, E, H, I, gate_type)) return false;
+    // Q6_K gate / up: one half (hidden up to 2048) of rows that start on a
+    // dword (an even superblock count), as the loads into the ring need
+    if (gate_type == kQ6_K && (make_geom(0, E, H, I, kQ6_K).halves != 1 || (H / kQK) % 2 != 0)) return false;
     MoeDownGeom gd;
     int waves = 0;
     if (token_major_down(down_type, E, H, I, T, top_k, gd, waves)) return true;
@@ -1647,7 +1813,9 @@ hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate,
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMoThreads), 0, stream, gate, up, g0, x, top_k, ids, wts, E, P,
                            hbuf);
     };
-    switch ((gate_type == kQ5_K ? 4 : 0) + (rec ? 2 : 0) + (g0.halves == 2 ? 1 : 0)) {
+    switch ((gate_type == kQ6_K ? 8 : gate_type == kQ5_K ? 4 : 0) + (rec ? 2 : 0) + (g0.halves == 2 ? 1 : 0)) {
+    case 8: gate_up(&moe_expert_tile_kernel<0, false, 1, kQ6_K>); break;
+    case 10: gate_up(&moe_expert_tile_kernel<0, true, 1, kQ6_K>); break;
     case 0: gate_up(&moe_expert_tile_kernel<0, false, 1, kQ4_K>); break;
     case 1: gate_up(&moe_expert_tile_kernel<0, false, 2, kQ4_K>); break;
     case 2: gate_up(&moe_expert_tile_kernel<0, true, 1, kQ4_K>); break;
@@ -1655,7 +1823,8 @@ hipError_t launch_moe_kq_mfma(int gate_type, int down_type, const uint8_t *gate,
     case 4: gate_up(&moe_expert_tile_kernel<0, false, 1, kQ5_K>); break;
     case 5: gate_up(&moe_expert_tile_kernel<0, false, 2, kQ5_K>); break;
     case 6: gate_up(&moe_expert_tile_kernel<0, true, 1, kQ5_K>); break;
-    default: gate_up(&moe_expert_tile_kernel<0, true, 2, kQ5_K>); break;
+    case 7: gate_up(&moe_expert_tile_kernel<0, true, 2, kQ5_K>); break;
+    default: return hipErrorNotSupported;  // Q6_K in halves: moe_kq_mfma_supported refuses it
     }
     if (rec) {
         const dim3 dgrid((unsigned)(H / 16), (unsigned)((T + gd.tg - 1) / gd.tg));

@@ -112,7 +112,8 @@ def test_moe_q5_k_parity(gt, dt, E, H, I, T, k):
 # Expert types and shapes the matrix-core passes do not take: Q8_0 / Q4_0
 # gate and up or down on the fp32 row kernels (rows of 3 to 448 blocks, 8 to
 # 64 lanes per row, route groups limited by LDS, experts with many routes),
-# Q6_K gate and up on the K-quant row kernels, mixed gate / up types, and
+# Q6_K gate and up at hidden 512 (the matrix-core gate/up pass since it takes
+# Q6_K rows), mixed gate / up types, and
 # Q6_K down beyond the token-major down pass (inter above 1024, hidden past
 # 2048 with an odd superblock count); also Q5_K gate / up at hidden 4096
 # (K-halves of 8) and 1792 (7 superblocks in one half) on the matrix-core
@@ -137,6 +138,30 @@ def test_moe_other_types_parity(gt, dt, E, H, I, T, k):
     ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=gt)
     err = o.rel_err(out, ref)
     print(f"[gpu] moe types rel_err={err:.3e}", flush=True)
+    assert err <= MOE_TOL
+    for t in (tg, tu, td):
+        t.close()
+
+
+# Q6_K gate / up experts on the matrix-core gate/up pass (one route per
+# MFMA, route groups of two, 210-byte superblocks realigned in LDS): the
+# 128-expert layer with Q6_K down (token-major), Q4_K down, Q5_K down past
+# inter 1024 (the expert-major down pass), 300 tokens x top-2 (the even
+# split), 600 x top-4 (token slices); odd superblock counts (hidden 768) and
+# hidden 4096 stay on the row kernels.
+@pytest.mark.parametrize("dt,E,H,I,T,k", [
+    (syn.Q6_K, 128, 2048, 768, 16, 8), (syn.Q4_K, 16, 1024, 512, 9, 4), (syn.Q5_K, 8, 1536, 1280, 9, 2),
+    (syn.Q6_K, 32, 512, 256, 300, 2), (syn.Q6_K, 8, 2048, 1024, 40, 2), (syn.Q6_K, 16, 1024, 512, 600, 4),
+    (syn.Q6_K, 8, 768, 256, 5, 2), (syn.Q6_K, 4, 4096, 512, 6, 2)])
+def test_moe_q6_k_gate_up_parity(dt, E, H, I, T, k):
+    print(f"[gpu] moe q6_k gate/up down={dt} E={E} H={H} I={I} T={T} k={k}", flush=True)
+    gate, up, down, tg, tu, td = _experts(E, H, I, seed=E + H + I + 5, down_type=dt, gate_type=syn.Q6_K)
+    ids, w = syn.moe_routing(T, E, k, seed=41)
+    x = syn.activation(T * H, seed=42).reshape(T, H)
+    out = ops.moe_grouped(tg, tu, td, E, x, ids, w)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=dt, gate_type=syn.Q6_K)
+    err = o.rel_err(out, ref)
+    print(f"[gpu] moe q6_k gate/up rel_err={err:.3e}", flush=True)
     assert err <= MOE_TOL
     for t in (tg, tu, td):
         t.close()
@@ -176,9 +201,10 @@ def moe_variant():
     ops.set_option("moe_variant", 0)
 
 
-@pytest.mark.parametrize("gt,dt", [(syn.Q4_0, syn.Q4_0), (syn.Q5_K, syn.Q6_K), (syn.Q5_K, syn.Q5_K)])
+@pytest.mark.parametrize("gt,dt", [(syn.Q4_0, syn.Q4_0), (syn.Q5_K, syn.Q6_K), (syn.Q5_K, syn.Q5_K),
+                                   (syn.Q6_K, syn.Q6_K)])
 def test_moe_matrix_core_equals_row_kernels(gt, dt, moe_variant):
-    # All-Q4_0 and Q5_K experts: the matrix-core passes (22-bit x digits)
+    # All-Q4_0, Q5_K and Q6_K experts: the matrix-core passes (22-bit x digits)
     # against the fp32 row kernels (moe_variant 1), both against the oracle.
     E, H, I, T, k = 32, 2048, 768, 16, 8
     gate, up, down, tg, tu, td = _experts(E, H, I, seed=21, down_type=dt, gate_type=gt)
@@ -300,6 +326,32 @@ def test_moe_nan_dmin_with_zero_min_codes(gt, dt):
     assert np.all(np.isfinite(ref))
     out = ops.moe_grouped(*ts, E, x, ids, w)
     assert np.all(np.isfinite(out))
+    assert o.rel_err(out, ref) <= MOE_TOL
+    for t in ts:
+        t.close()
+
+
+# Q6_K down rows whose codes are all 63 against h that is the same over each
+# 16-element quarter (every gate / up row identical, so h is constant per
+# token): the quarter's sum q X reaches 16 * 63 * 2^22 * m (m in [0.5, 1)
+# the h mantissa), past int32 for nearly every token, so the token-major
+# down pass must combine those planes in fp32.
+def test_moe_q6_k_down_sums_past_int32():
+    E, H, I, T, k = 2, 512, 256, 6, 2
+    gate = np.tile(syn.matrix(syn.Q4_K, 1, H, 71), (E * I, 1))
+    up = np.tile(syn.matrix(syn.Q4_K, 1, H, 72), (E * I, 1))
+    down = syn.matrix(syn.Q6_K, E * H, I, 73).reshape(E * H, I // 256, 210).copy()
+    down[..., :192] = 0xFF  # ql nibbles 15, qh bits 3: q = 63
+    down[..., 192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    down = down.reshape(E * H, -1)
+    ts = [ops.GgufTensor("blk.0.ffn_gate_exps.weight", (H, I, E), syn.Q4_K, gate.reshape(-1)),
+          ops.GgufTensor("blk.0.ffn_up_exps.weight", (H, I, E), syn.Q4_K, up.reshape(-1)),
+          ops.GgufTensor("blk.0.ffn_down_exps.weight", (I, H, E), syn.Q6_K, down.reshape(-1))]
+    ids = np.tile(np.arange(E, dtype=np.int32), (T, 1))
+    w = np.full((T, k), 0.5, np.float32)
+    x = syn.activation(T * H, seed=74).reshape(T, H)
+    ref = o.moe_reference_q4k(gate, up, down, E, x, ids, w, down_type=syn.Q6_K, gate_type=syn.Q4_K)
+    out = ops.moe_grouped(*ts, E, x, ids, w)
     assert o.rel_err(out, ref) <= MOE_TOL
     for t in ts:
         t.close()
