@@ -674,9 +674,9 @@ def main() -> int:
             log("extra moe")
             extra["moe_q4_k_e128_top8_t16"], moe_inputs = moe_workload(torch, args.steps, args.warmup,
                                                                       seed=11)
-        # Prefill: 256 and 512 tokens through the same layer (every expert
-        # takes tens of routes).
-        for T in (256, 512):
+        # Batched decode and prefill: 64, 256 and 512 tokens through the same
+        # layer (every expert takes several to tens of routes).
+        for T in (64, 256, 512):
             name = f"moe_q4_k_e128_top8_t{T}"
             if _has_symbol("gollek_hip_moe_grouped_device") and want(name):
                 log(f"extra {name}")

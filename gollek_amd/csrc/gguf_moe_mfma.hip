@@ -1765,10 +1765,17 @@ bool tile_pass_ok(int mode, int E, int H, int I, int type) {
     return g.ndma <= max_dma(type) && g.w_bytes < (int64_t)kMaskedOffset && 2 * kMoGroup * 16 * g.rt <= kMoOutCap;
 }
 
-// The token-major down pass takes Q4_K, Q5_K and Q6_K rows where its geometry fits.
+// The token-major down pass takes Q4_K, Q5_K and Q6_K rows where its
+// geometry fits.  It reads an expert's down tile once per token group (64 /
+// top_k tokens) that routes to it, the expert-major pass once per group of
+// four of its routes: past kTokenMajorMaxGroups token groups (prefill) the
+// expert-major pass moves fewer bytes and takes the Q4_K / Q5_K rows.
+constexpr int kTokenMajorMaxGroups = 4;
 bool token_major_down(int down_type, int E, int H, int I, int T, int top_k, MoeDownGeom &gd, int &waves) {
-    return (down_type == kQ4_K || down_type == kQ5_K || down_type == kQ6_K) &&
-           make_down_geom(E, H, I, T, top_k, down_type, gd, waves);
+    if (down_type != kQ4_K && down_type != kQ5_K && down_type != kQ6_K) return false;
+    if (!make_down_geom(E, H, I, T, top_k, down_type, gd, waves)) return false;
+    return down_type == kQ6_K || (T + gd.tg - 1) / gd.tg <= kTokenMajorMaxGroups ||
+           !tile_pass_ok(1, E, H, I, down_type);
 }
 
 }  // namespace
