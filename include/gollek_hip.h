@@ -56,8 +56,8 @@ extern "C" {
 #define GOLLEK_HIP_Q4_0 2
 #define GOLLEK_HIP_Q8_0 8
 #define GOLLEK_HIP_Q4_K 12
-#define GOLLEK_HIP_Q5_K 13 /* GC/core/GgmlType.java:22; dequantize, dot and mat-vec only */
-#define GOLLEK_HIP_Q6_K 14 /* GC/core/GgmlType.java:23; dequantize, dot and mat-vec only */
+#define GOLLEK_HIP_Q5_K 13 /* GC/core/GgmlType.java:22 */
+#define GOLLEK_HIP_Q6_K 14 /* GC/core/GgmlType.java:23 */
 
 /* Opaque device-resident weight matrix. */
 typedef struct gollek_hip_weight gollek_hip_weight;
