@@ -719,7 +719,13 @@ struct ColGeom {
 // 4.92 us: its 768-byte tail takes three loads).
 // Also measured and dropped: the first four waves taking the last tile of
 // columns 12..15 (whose tiles arrive last), 8.2 us.
-template <int TYPE, bool PREP>
+//
+// NV = 2 (the small-M GEMM's M = 2): the second vector's digits sit in A
+// rows 8..15, which the single vector leaves zero, so each MFMA serves both
+// and output lanes 32..63 hold the second vector's sums; vector v is x + v
+// K, its results y + v rows.  XB: x holds bf16 bit patterns (the GEMM's
+// input), widened to fp32 exactly as they load.
+template <int TYPE, bool PREP, int NV = 1, bool XB = false>
 __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int rows_per_wg) {
@@ -772,7 +778,19 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
         // x first, then tile 0, then the digit planes while it flies.  Pacing:
         // each next tile is issued once the previous one has arrived (see
         // above).
-        const float4 xv = reinterpret_cast<const float4 *>(x)[64 * wv + lane];
+        auto load_x = [&](int v) {
+            if constexpr (XB) {
+                const uint2 u = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(x) +
+                                                                (int64_t)v * nsb * kQK)[64 * wv + lane];
+                return float4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u),
+                              __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xFFFF0000u)};
+            } else {
+                return reinterpret_cast<const float4 *>(x + (int64_t)v * nsb * kQK)[64 * wv + lane];
+            }
+        };
+        const float4 xv = load_x(0);
+        float4 xv2 = xv;
+        if constexpr (NV == 2) xv2 = load_x(1);
         __builtin_amdgcn_sched_barrier(0);
         issue(0);
         __builtin_amdgcn_sched_barrier(0);
@@ -780,7 +798,25 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
         XOps4 xo;
         float4 xr = xv;  // the conversion stays below the tile's loads
         asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
-        x_operands4(xr, rbase + G::kW, xo);
+        if constexpr (NV == 1) {
+            x_operands4(xr, rbase + G::kW, xo);
+        } else {
+            // vector 0 in A rows 0..7 and output lanes 0..31, vector 1 in rows
+            // 8..15 and lanes 32..63
+            float4 xr2 = xv2;
+            asm volatile("" : "+v"(xr2.x), "+v"(xr2.y), "+v"(xr2.z), "+v"(xr2.w));
+            XOpsC c0, c1;
+            x_operands4c(xr, rbase + G::kW, c0);
+            x_operands4c<true>(xr2, rbase + G::kW, c1);
+            const bool second = lane >= 32;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                c0.d[k] = uint2{c0.d[k].x | c1.d[k].x, c0.d[k].y | c1.d[k].y};
+                c0.xs4[k] = second ? c1.xs4[k] : c0.xs4[k];
+            }
+            c0.xs = second ? c1.xs : c0.xs;
+            xo = x_expand(c0);
+        }
 
         const int n = lane & 15, g = lane >> 4;
         for (int t = 0; t < tiles; t++) {
@@ -809,14 +845,21 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
                 v = q32_tile_piece<TYPE>(raw, dh, xo);
             }
             // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until the
-            // row sums; the tile has been read (read_* wait for their reads)
+            // row sums; the tile has been read (read_* wait for their reads).
+            // NV = 2: lanes 32..63 (the second vector) 128 bytes further.
             if (lane < 32) lds_store_f32(a_t + 8 * n + 4 * g, v);
+            else if (NV == 2) lds_store_f32(a_t + 128 + 8 * n + 4 * (g & 1), v);
         }
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    // Row sums in superblock order.
-    for (int r = threadIdx.x; r < nr; r += kColThreads) {
-        const int off = TB * (r >> 4) + 8 * (r & 15);
+    // Row sums in superblock order (NV = 2: the second vector's at + 128).
+    for (int q = threadIdx.x; q < NV * nr; q += kColThreads) {
+        int v = 0, r = q;
+        if constexpr (NV == 2) {
+            v = q >= nr ? 1 : 0;
+            r = q - v * nr;
+        }
+        const int off = TB * (r >> 4) + 128 * v + 8 * (r & 15);
         float2 p[kColWaves];
 #pragma unroll
         for (int k = 0; k < kColWaves; k++)
@@ -824,7 +867,7 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < kColWaves; k++) s += p[k].x + p[k].y;
-        y[r0 + r] = s;
+        y[(int64_t)v * rows + r0 + r] = s;
     }
 }
 
@@ -1087,6 +1130,44 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
     const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     if (row_bytes != cols / kQK * piece || (row_bytes & 15) != 0) return false;
     return ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
+}
+
+// The small-M GEMM at M = 1 and 2 on the column kernel (X: M bf16 rows of K,
+// Y: M rows of N floats): the GEMV's stream of the weights once, both
+// vectors in each MFMA.  Weights of a type the column kernel takes, K a
+// multiple of 256 up to 4096, a row count its partition takes, 16-byte
+// aligned weights and 8-byte aligned X.
+bool gemm_col_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w, const void *x) {
+    if (M < 1 || M > 2 || N <= 0 || K <= 0 || K % kQK != 0 || K / kQK > kColWaves) return false;
+    if (type_id != kQ4_K && type_id != kQ5_K && type_id != kQ4_0 && type_id != kQ8_0) return false;
+    const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
+    if (row_bytes != (int64_t)(K / kQK) * piece) return false;
+    if ((reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(x) & 7u) != 0) return false;
+    return col_layout_rows(type_id, N, K) > 0;
+}
+
+hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y, int M,
+                           int N, int K, hipStream_t stream) {
+    const int nsb = K / kQK;
+    const int64_t col_rows = col_layout_rows(type_id, N, K);
+    if (col_rows <= 0) return hipErrorInvalidValue;  // callers check gemm_col_supported first
+    const dim3 grid((unsigned)((N + col_rows - 1) / col_rows));
+    const float *xf = reinterpret_cast<const float *>(x);
+#define GOLLEK_GEMM_COL(T)                                                                                      \
+    do {                                                                                                        \
+        if (M == 1)                                                                                             \
+            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, 1, true>), grid, dim3(kColThreads), 0, stream, w, \
+                               row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                              \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, 2, true>), grid, dim3(kColThreads), 0, stream, w, \
+                               row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                              \
+    } while (0)
+    if (type_id == kQ4_K) GOLLEK_GEMM_COL(kQ4_K);
+    else if (type_id == kQ5_K) GOLLEK_GEMM_COL(kQ5_K);
+    else if (type_id == kQ8_0) GOLLEK_GEMM_COL(kQ8_0);
+    else GOLLEK_GEMM_COL(kQ4_0);
+#undef GOLLEK_GEMM_COL
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_q32_mfma(int type_id, const uint8_t *w, int64_t row_bytes, int64_t cols,

@@ -144,7 +144,8 @@ struct XOps4 {
 // The same operands held compactly (13 registers instead of 21) by kernels
 // that keep several superblocks' operands at once: d[c] = the eight bytes
 // of A[c] this lane holds, which x_expand places at A[c] bytes 0..7 (A rows
-// m < 4) or 8..15 (4 <= m < 8); rows m >= 8 hold zeros.
+// m & 7 < 4) or 8..15 (m & 7 >= 4); rows m >= 8 hold zeros, or a second
+// vector's operands (x_operands4c<true>).
 struct XOpsC {
     uint2 d[4];
     float xs4[4], xs;
@@ -153,6 +154,9 @@ struct XOpsC {
 // Wave-wide: lane l holds elements 4 l .. 4 l + 3 of a superblock of x.
 // Writes the digit planes to `scratch` (1 KB of LDS private to the wave),
 // reads them back in the A operand layout and leaves the scratch free.
+// UPPER: the operands go to A rows 8..15 (m - 8 as m), rows 0..7 are zero
+// (a second vector beside the first in one MFMA).
+template <bool UPPER = false>
 __device__ __forceinline__ void x_operands4c(const float4 xv, uint32_t scratch, XOpsC &o) {
     const int lane = threadIdx.x & 63;
     const float v[4] = {xv.x, xv.y, xv.z, xv.w};
@@ -184,11 +188,11 @@ __device__ __forceinline__ void x_operands4c(const float4 xv, uint32_t scratch, 
         : "v"(scratch + 256 * p + 8 * g + 32 * ha)
         : "memory");
 #pragma unroll
-    for (int c = 0; c < 4; c++) o.d[c] = m < 8 ? d[c] : uint2{0u, 0u};
+    for (int c = 0; c < 4; c++) o.d[c] = (m >= 8) == UPPER ? d[c] : uint2{0u, 0u};
 }
 
 __device__ __forceinline__ XOps4 x_expand(const XOpsC &c) {
-    const bool lo = (threadIdx.x & 15) < 4;
+    const bool lo = (threadIdx.x & 4) == 0;  // rows 0..3 and 8..11: bytes 0..7
     XOps4 o;
 #pragma unroll
     for (int k = 0; k < 4; k++) {

@@ -54,6 +54,30 @@ def test_gemm_row_equals_gemv(q8_4096):
         assert o.rel_err(y[r], g) <= 1e-4
 
 
+# M = 1 and 2 run the GEMV's column kernel with both vectors in each MFMA
+# (the second in A rows 8..15): every row of Y equals, bit for bit, the
+# mat-vec of that row of X widened to fp32 (the same digits, products and
+# sums), and sits within the GEMM bar of the fp64 oracle.  Row counts that
+# end in a partial 16-row tile (4000) included.
+@pytest.mark.parametrize("type_id,rows,cols", [(syn.Q4_K, 14336, 4096), (syn.Q5_K, 4096, 4096),
+                                               (syn.Q4_0, 11008, 4096), (syn.Q8_0, 4096, 4096),
+                                               (syn.Q8_0, 4000, 2048), (syn.Q4_K, 1792, 4096)])
+@pytest.mark.parametrize("m", [1, 2])
+def test_gemm_small_m_on_the_column_kernel_equals_gemv(type_id, rows, cols, m):
+    print(f"[gpu] gemm column kernel type={type_id} m={m} n={rows} k={cols}", flush=True)
+    data = syn.matrix(type_id, rows, cols, seed=rows + m)
+    t = ops.GgufTensor("w", (cols, rows), type_id, data.reshape(-1))
+    x = syn.activation_bf16(m, cols, seed=11 + m)
+    y = np.full((m, rows), np.nan, np.float32)
+    ops.gemm_bf16(t, x, y)
+    for r in range(m):
+        g = np.zeros(rows, np.float32)
+        ops.mat_vec(t, syn.bf16_to_f32(x[r]), g)
+        assert np.array_equal(y[r].view(np.uint32), g.view(np.uint32)), r
+    t.close()
+    assert o.rel_err(y, o.gemm_reference(type_id, data, cols, x)) <= GEMM_TOL
+
+
 @pytest.mark.parametrize("rows,cols,m", [(48, 96, 3), (16, 64, 20), (80, 4096, 7), (4096, 192, 130)])
 def test_gemm_odd_shapes(rows, cols, m):
     data = syn.q8_0_matrix(rows, cols, seed=rows + cols)
