@@ -658,7 +658,7 @@ def main() -> int:
                 log(f"extra {name}")
                 extra[name], gemm_host = gemm_workload(torch, m, args.steps, args.warmup, seed=7)
         # Q4_K / Q4_0 / Q5_K / Q6_K weights at the FFN shape (K 4096, N 14336).
-        for tname, t, ms in (("q4_k", syn.Q4_K, (2, 16, 128, 512)), ("q4_0", syn.Q4_0, (128, 512)),
+        for tname, t, ms in (("q4_k", syn.Q4_K, (2, 4, 16, 128, 512)), ("q4_0", syn.Q4_0, (128, 512)),
                              ("q5_k", syn.Q5_K, (16, 128, 512)), ("q6_k", syn.Q6_K, (16, 128, 512))):
             for m in ms:
                 name = f"{tname}_gemm_bf16_m{m}_4096x14336"

@@ -730,7 +730,7 @@ hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, co
     if (M <= 0) return hipSuccess;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (row_bytes & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-    // M <= 2: the GEMV's column kernel, both vectors in each MFMA.
+    // M <= 4: the GEMV's column kernel, two vectors in each MFMA.
     if (gemm_col_supported(type_id, row_bytes, M, N, K, w, x))
         return launch_gemm_col(type_id, w, row_bytes, x, y, M, N, K, stream);
     // M <= 32 with Q8_0 weights: the buffer->LDS ring over 16-row column tiles.

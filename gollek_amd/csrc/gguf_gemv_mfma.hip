@@ -720,11 +720,12 @@ struct ColGeom {
 // Also measured and dropped: the first four waves taking the last tile of
 // columns 12..15 (whose tiles arrive last), 8.2 us.
 //
-// NV = 2 (the small-M GEMM's M = 2): the second vector's digits sit in A
+// NV = 2 .. 4 (the small-M GEMM's M): the second vector's digits sit in A
 // rows 8..15, which the single vector leaves zero, so each MFMA serves both
-// and output lanes 32..63 hold the second vector's sums; vector v is x + v
-// K, its results y + v rows.  XB: x holds bf16 bit patterns (the GEMM's
-// input), widened to fp32 exactly as they load.
+// and output lanes 32..63 hold the second vector's sums; vectors 2 and 3
+// take a second operand set (a second MFMA per chunk on the same B).
+// Vector v is x + v K, its results y + v rows.  XB: x holds bf16 bit
+// patterns (the GEMM's input), widened to fp32 exactly as they load.
 template <int TYPE, bool PREP, int NV = 1, bool XB = false>
 __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
@@ -789,25 +790,25 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
             }
         };
         const float4 xv = load_x(0);
-        float4 xv2 = xv;
-        if constexpr (NV == 2) xv2 = load_x(1);
+        float4 xv2 = xv, xv3 = xv, xv4 = xv;
+        if constexpr (NV >= 2) xv2 = load_x(1);
+        if constexpr (NV >= 3) xv3 = load_x(2);
+        if constexpr (NV >= 4) xv4 = load_x(3);
         __builtin_amdgcn_sched_barrier(0);
         issue(0);
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t rbase = lds0 + wv * G::kRegion;
-        XOps4 xo;
+        XOps4 xo, xo2;
         float4 xr = xv;  // the conversion stays below the tile's loads
         asm volatile("" : "+v"(xr.x), "+v"(xr.y), "+v"(xr.z), "+v"(xr.w));
-        if constexpr (NV == 1) {
-            x_operands4(xr, rbase + G::kW, xo);
-        } else {
-            // vector 0 in A rows 0..7 and output lanes 0..31, vector 1 in rows
-            // 8..15 and lanes 32..63
-            float4 xr2 = xv2;
-            asm volatile("" : "+v"(xr2.x), "+v"(xr2.y), "+v"(xr2.z), "+v"(xr2.w));
+        // vectors a (A rows 0..7, output lanes 0..31) and b (rows 8..15,
+        // lanes 32..63) in one operand set; b absent: rows 8..15 zero
+        auto pair_operands = [&](float4 a, float4 b, bool has_b) {
+            asm volatile("" : "+v"(b.x), "+v"(b.y), "+v"(b.z), "+v"(b.w));
             XOpsC c0, c1;
-            x_operands4c(xr, rbase + G::kW, c0);
-            x_operands4c<true>(xr2, rbase + G::kW, c1);
+            x_operands4c(a, rbase + G::kW, c0);
+            if (!has_b) return x_expand(c0);
+            x_operands4c<true>(b, rbase + G::kW, c1);
             const bool second = lane >= 32;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -815,7 +816,17 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
                 c0.xs4[k] = second ? c1.xs4[k] : c0.xs4[k];
             }
             c0.xs = second ? c1.xs : c0.xs;
-            xo = x_expand(c0);
+            return x_expand(c0);
+        };
+        if constexpr (NV == 1) {
+            x_operands4(xr, rbase + G::kW, xo);
+        } else {
+            xo = pair_operands(xr, xv2, true);
+            if constexpr (NV >= 3) {
+                float4 xr3 = xv3;
+                asm volatile("" : "+v"(xr3.x), "+v"(xr3.y), "+v"(xr3.z), "+v"(xr3.w));
+                xo2 = pair_operands(xr3, xv4, NV == 4);
+            }
         }
 
         const int n = lane & 15, g = lane >> 4;
@@ -826,37 +837,44 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
             // quants and scales (see read_tile_piece32).
             const uint32_t a_t = rbase + TB * t;
             const uint32_t a_h = a_t + n * PB;
-            float v;
+            float v, v2 = 0.0f;
             if constexpr (TYPE == kQ4_K) {
                 u32x4 hv;
                 uint2 q[4];
                 read_tile_superblock(a_h, a_h + 16 + 8 * g, hv, q);
                 v = q4k_tile_superblock4(hv, q, xo);
+                if constexpr (NV >= 3) v2 = q4k_tile_superblock4(hv, q, xo2);
             } else if constexpr (TYPE == kQ5_K) {
                 u32x4 hv;
                 uint2 qh, q[4];
                 read_tile_superblock5(a_h, a_h + 16 + 8 * g, a_h + 48 + 8 * g, hv, qh, q);
                 v = q4k_tile_superblock4<true>(hv, q, xo, qh);
+                if constexpr (NV >= 3) v2 = q4k_tile_superblock4<true>(hv, q, xo2, qh);
             } else {
                 uint32_t raw[20], dh[4];
                 const uint32_t a_q = a_h + 8 * (TYPE == kQ4_0 ? (g & 1) : g);
                 const uint32_t a_d = a_h + (TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes) * (g & 1);
                 read_tile_piece32<TYPE == kQ8_0 ? kQ8BlockBytes : kQ4BlockBytes>(a_q, a_d, raw, dh);
                 v = q32_tile_piece<TYPE>(raw, dh, xo);
+                if constexpr (NV >= 3) v2 = q32_tile_piece<TYPE>(raw, dh, xo2);
             }
             // lane n + 16 h: sub-blocks 2 c + h of row n, kept apart until the
             // row sums; the tile has been read (read_* wait for their reads).
-            // NV = 2: lanes 32..63 (the second vector) 128 bytes further.
+            // Vector j's sums at + 128 j (lanes 32..63 hold vectors 1 and 3).
             if (lane < 32) lds_store_f32(a_t + 8 * n + 4 * g, v);
-            else if (NV == 2) lds_store_f32(a_t + 128 + 8 * n + 4 * (g & 1), v);
+            else if (NV >= 2) lds_store_f32(a_t + 128 + 8 * n + 4 * (g & 1), v);
+            if constexpr (NV >= 3) {
+                if (lane < 32) lds_store_f32(a_t + 256 + 8 * n + 4 * g, v2);
+                else if (NV == 4) lds_store_f32(a_t + 384 + 8 * n + 4 * (g & 1), v2);
+            }
         }
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    // Row sums in superblock order (NV = 2: the second vector's at + 128).
+    // Row sums in superblock order (vector v's at + 128 v).
     for (int q = threadIdx.x; q < NV * nr; q += kColThreads) {
         int v = 0, r = q;
-        if constexpr (NV == 2) {
-            v = q >= nr ? 1 : 0;
+        if constexpr (NV > 1) {
+            v = q / nr;
             r = q - v * nr;
         }
         const int off = TB * (r >> 4) + 128 * v + 8 * (r & 15);
@@ -1132,13 +1150,13 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
     return ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15u) == 0;
 }
 
-// The small-M GEMM at M = 1 and 2 on the column kernel (X: M bf16 rows of K,
-// Y: M rows of N floats): the GEMV's stream of the weights once, both
+// The small-M GEMM at M = 1 .. 4 on the column kernel (X: M bf16 rows of K,
+// Y: M rows of N floats): the GEMV's stream of the weights once, two
 // vectors in each MFMA.  Weights of a type the column kernel takes, K a
 // multiple of 256 up to 4096, a row count its partition takes, 16-byte
 // aligned weights and 8-byte aligned X.
 bool gemm_col_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w, const void *x) {
-    if (M < 1 || M > 2 || N <= 0 || K <= 0 || K % kQK != 0 || K / kQK > kColWaves) return false;
+    if (M < 1 || M > 4 || N <= 0 || K <= 0 || K % kQK != 0 || K / kQK > kColWaves) return false;
     if (type_id != kQ4_K && type_id != kQ5_K && type_id != kQ4_0 && type_id != kQ8_0) return false;
     const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     if (row_bytes != (int64_t)(K / kQK) * piece) return false;
@@ -1153,20 +1171,22 @@ hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, con
     if (col_rows <= 0) return hipErrorInvalidValue;  // callers check gemm_col_supported first
     const dim3 grid((unsigned)((N + col_rows - 1) / col_rows));
     const float *xf = reinterpret_cast<const float *>(x);
+#define GOLLEK_GEMM_COL_NV(T, NV)                                                                             \
+    hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, NV, true>), grid, dim3(kColThreads), 0, stream, w,      \
+                       row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows)
 #define GOLLEK_GEMM_COL(T)                                                                                      \
     do {                                                                                                        \
-        if (M == 1)                                                                                             \
-            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, 1, true>), grid, dim3(kColThreads), 0, stream, w, \
-                               row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                              \
-        else                                                                                                    \
-            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, 2, true>), grid, dim3(kColThreads), 0, stream, w, \
-                               row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                              \
+        if (M == 1) GOLLEK_GEMM_COL_NV(T, 1);                                                                   \
+        else if (M == 2) GOLLEK_GEMM_COL_NV(T, 2);                                                              \
+        else if (M == 3) GOLLEK_GEMM_COL_NV(T, 3);                                                              \
+        else GOLLEK_GEMM_COL_NV(T, 4);                                                                          \
     } while (0)
     if (type_id == kQ4_K) GOLLEK_GEMM_COL(kQ4_K);
     else if (type_id == kQ5_K) GOLLEK_GEMM_COL(kQ5_K);
     else if (type_id == kQ8_0) GOLLEK_GEMM_COL(kQ8_0);
     else GOLLEK_GEMM_COL(kQ4_0);
 #undef GOLLEK_GEMM_COL
+#undef GOLLEK_GEMM_COL_NV
     return hipGetLastError();
 }
 

@@ -108,8 +108,8 @@ size_t gemm_workspace_max_bytes(int type_id, int N, int K);
 hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
                             int M, int N, int K, hipStream_t stream, float *workspace = nullptr,
                             size_t workspace_bytes = 0);
-// M = 1 and 2 on the GEMV's column kernel (gguf_gemv_mfma.hip): both
-// vectors in each MFMA over one stream of the weights.
+// M = 1 .. 4 on the GEMV's column kernel (gguf_gemv_mfma.hip): two vectors
+// in each MFMA over one stream of the weights.
 bool gemm_col_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w, const void *x);
 hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y, int M,
                            int N, int K, hipStream_t stream);
