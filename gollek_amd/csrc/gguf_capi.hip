@@ -703,7 +703,9 @@ int32_t gollek_hip_matvec_device(gollek_hip_weight *w, const float *x, float *y,
     return GOLLEK_HIP_OK;
 }
 
-static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, int64_t m,
+// x_dev: whether the kernels read x where the caller put it (the _device
+// entries) rather than from the staging buffer.
+static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, int64_t m, bool x_dev,
                           char *err, size_t err_len) {
     if (w == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "tensor");
     if (x == nullptr) return fail(GOLLEK_HIP_ERR_NULL, err, err_len, "input");
@@ -712,7 +714,14 @@ static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, in
         w->type_id != GOLLEK_HIP_Q5_K && w->type_id != GOLLEK_HIP_Q6_K)
         return fail(GOLLEK_HIP_ERR_UNSUPPORTED, err, err_len,
                     "Unsupported GGUF bf16 GEMM type id: %d (Q8_0, Q4_0, Q4_K, Q5_K or Q6_K)", w->type_id);
-    if (w->compact) return compact_unsupported(w, "GEMM", err, err_len);
+    // A compacted handle holds the prepared column layout only, which the
+    // GEMM reads for up to four rows of X while its partition is still the
+    // column kernel's.
+    if (w->compact && !(m >= 0 && m <= 4 && w->rows <= 0x7FFFFFFF && w->cols <= 0x7FFFFFFF &&
+                        gollek::col_layout_rows(w->type_id, w->rows, w->cols) == w->prep_rows &&
+                        (m == 0 || gollek::gemm_col_supported(w->type_id, w->row_bytes, (int)m, (int)w->rows,
+                                                              (int)w->cols, w->prep, x_dev ? x : w->prep))))
+        return compact_unsupported(w, "GEMM past 4 rows of X (or of 8-byte misaligned X)", err, err_len);
     if (m < 0 || m > (int64_t)0x7FFFFFFF || w->rows > 0x7FFFFFFF || w->cols > 0x7FFFFFFF)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "GEMM shape %lld x %lld x %lld is out of range",
                     (long long)m, (long long)w->rows, (long long)w->cols);
@@ -721,7 +730,7 @@ static int32_t check_gemm(gollek_hip_weight *w, const void *x, const void *y, in
 
 int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_len, int64_t m,
                              float *y, int64_t y_len, char *err, size_t err_len) {
-    int32_t rc = check_gemm(w, x, y, m, err, err_len);
+    int32_t rc = check_gemm(w, x, y, m, false, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     if (x_len < m * w->cols)
         return fail(GOLLEK_HIP_ERR_ARG, err, err_len, "Input length %lld is smaller than %lld x %lld",
@@ -756,7 +765,7 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
     float *k_y = hs != nullptr ? reinterpret_cast<float *>(hs + x_bytes) : d_y;
     if (e == hipSuccess)
         e = gollek::launch_gemm_bf16(w->type_id, w->data, w->row_bytes, d_x, k_y, (int)m, (int)w->rows,
-                                     (int)w->cols, w->stream, d_ws, ws_bytes);
+                                     (int)w->cols, w->stream, d_ws, ws_bytes, w->prep, w->prep_rows);
     if (e == hipSuccess && hs == nullptr)
         e = hipMemcpyAsync(y, d_y, y_bytes, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
@@ -768,7 +777,7 @@ int32_t gollek_hip_gemm_bf16(gollek_hip_weight *w, const uint16_t *x, int64_t x_
 
 int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int64_t m, float *y,
                                     void *stream, char *err, size_t err_len) {
-    const int32_t rc = check_gemm(w, x, y, m, err, err_len);
+    const int32_t rc = check_gemm(w, x, y, m, true, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     // The handle's split-K workspace: allocated at the first call that splits,
     // for the largest split any m of this weight uses (below 16 MiB on 256
@@ -792,7 +801,7 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
     }
     hipError_t e = gollek::launch_gemm_bf16(w->type_id, w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
                                             (int)w->cols, static_cast<hipStream_t>(stream),
-                                            need ? w->gemm_ws : nullptr, w->gemm_ws_bytes);
+                                            need ? w->gemm_ws : nullptr, w->gemm_ws_bytes, w->prep, w->prep_rows);
     if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;
@@ -800,7 +809,7 @@ int32_t gollek_hip_gemm_bf16_device(gollek_hip_weight *w, const uint16_t *x, int
 
 int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *w, const uint16_t *x, int64_t m,
                                             float *y, void *stream, char *err, size_t err_len) {
-    const int32_t rc = check_gemm(w, x, y, m, err, err_len);
+    const int32_t rc = check_gemm(w, x, y, m, true, err, err_len);
     if (rc != GOLLEK_HIP_OK) return rc;
     // The split-K partials go to this GPU's static scratch: no allocation,
     // and every call on the GPU shares it (each split writes its whole
@@ -818,7 +827,7 @@ int32_t gollek_hip_gemm_bf16_device_noalloc(gollek_hip_weight *w, const uint16_t
     }
     hipError_t e = gollek::launch_gemm_bf16(w->type_id, w->data, w->row_bytes, x, y, (int)m, (int)w->rows,
                                             (int)w->cols, static_cast<hipStream_t>(stream), ws,
-                                            ws != nullptr ? kGemmScratchBytes : 0);
+                                            ws != nullptr ? kGemmScratchBytes : 0, w->prep, w->prep_rows);
     if (e != hipSuccess) return hip_fail(e, "gemm launch", err, err_len);
     ok(err, err_len);
     return GOLLEK_HIP_OK;

@@ -726,13 +726,16 @@ size_t gemm_workspace_max_bytes(int type_id, int N, int K) {
 }
 
 hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
-                            int M, int N, int K, hipStream_t stream, float *workspace, size_t workspace_bytes) {
+                            int M, int N, int K, hipStream_t stream, float *workspace, size_t workspace_bytes,
+                            const uint8_t *prep, int64_t prep_rows) {
     if (M <= 0) return hipSuccess;
     const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (row_bytes & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-    // M <= 4: the GEMV's column kernel, two vectors in each MFMA.
-    if (gemm_col_supported(type_id, row_bytes, M, N, K, w, x))
-        return launch_gemm_col(type_id, w, row_bytes, x, y, M, N, K, stream);
+    // M <= 4: the GEMV's column kernel, two vectors in each MFMA (on the
+    // prepared column layout when there is one for its partition).
+    if (gemm_col_supported(type_id, row_bytes, M, N, K, w != nullptr ? w : prep, x))
+        return launch_gemm_col(type_id, w, row_bytes, x, y, M, N, K, stream, prep, prep_rows);
+    if (w == nullptr) return hipErrorInvalidValue;  // the GGUF rows are needed
     // M <= 32 with Q8_0 weights: the buffer->LDS ring over 16-row column tiles.
     if (type_id == kQ8_0 && aligned && M <= 32 && N % 16 == 0 && K % 256 == 0 &&
         (int64_t)16 * row_bytes < ((int64_t)1 << 31) && (int64_t)M * K * 2 < ((int64_t)1 << 31)) {

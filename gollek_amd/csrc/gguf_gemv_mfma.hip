@@ -1165,15 +1165,24 @@ bool gemm_col_supported(int type_id, int64_t row_bytes, int M, int N, int K, con
 }
 
 hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y, int M,
-                           int N, int K, hipStream_t stream) {
+                           int N, int K, hipStream_t stream, const uint8_t *prep, int64_t prep_rows) {
     const int nsb = K / kQK;
     const int64_t col_rows = col_layout_rows(type_id, N, K);
     if (col_rows <= 0) return hipErrorInvalidValue;  // callers check gemm_col_supported first
+    const bool use_prep = prep != nullptr && prep_rows == col_rows;
+    const uint8_t *src = use_prep ? prep : w;
+    if (src == nullptr) return hipErrorInvalidValue;  // no GGUF rows and no layout for this partition
     const dim3 grid((unsigned)((N + col_rows - 1) / col_rows));
     const float *xf = reinterpret_cast<const float *>(x);
-#define GOLLEK_GEMM_COL_NV(T, NV)                                                                             \
-    hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, NV, true>), grid, dim3(kColThreads), 0, stream, w,      \
-                       row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows)
+#define GOLLEK_GEMM_COL_NV(T, NV)                                                                              \
+    do {                                                                                                       \
+        if (use_prep)                                                                                          \
+            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, true, NV, true>), grid, dim3(kColThreads), 0, stream,   \
+                               src, row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                        \
+        else                                                                                                   \
+            hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, NV, true>), grid, dim3(kColThreads), 0, stream,  \
+                               src, row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                        \
+    } while (0)
 #define GOLLEK_GEMM_COL(T)                                                                                      \
     do {                                                                                                        \
         if (M == 1) GOLLEK_GEMM_COL_NV(T, 1);                                                                   \

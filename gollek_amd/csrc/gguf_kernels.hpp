@@ -105,14 +105,18 @@ hipError_t launch_gemv_k56(int type_id, const uint8_t *w, int64_t row_bytes, int
 size_t gemm_workspace_bytes(int type_id, int M, int N, int K);
 // The largest gemm_workspace_bytes(type, M, N, K) over every M.
 size_t gemm_workspace_max_bytes(int type_id, int N, int K);
+// prep / prep_rows: the weight's prepared column layout (M <= 4 reads it
+// when its partition is the column kernel's; w may then be nullptr, a
+// compacted handle, and the call fails for shapes that need the GGUF rows).
 hipError_t launch_gemm_bf16(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y,
                             int M, int N, int K, hipStream_t stream, float *workspace = nullptr,
-                            size_t workspace_bytes = 0);
+                            size_t workspace_bytes = 0, const uint8_t *prep = nullptr, int64_t prep_rows = 0);
 // M = 1 .. 4 on the GEMV's column kernel (gguf_gemv_mfma.hip): two vectors
 // in each MFMA over one stream of the weights.
 bool gemm_col_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w, const void *x);
 hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, const uint16_t *x, float *y, int M,
-                           int N, int K, hipStream_t stream);
+                           int N, int K, hipStream_t stream, const uint8_t *prep = nullptr,
+                           int64_t prep_rows = 0);
 // The 128 x 128 tile kernel (gguf_gemm_tile.hip).
 bool gemm_tile_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w,
                          const void *x, const void *y);

@@ -136,8 +136,10 @@ final class GgufHipMatVec {
      * (RT/GgufTensorOps.java:666-674) as one small-M GEMM on the matrix cores
      * (gollek_hip_gemm_bf16), X rounded to bf16 (nearest, ties to even) as
      * that GEMM takes it.  A tensor first seen here keeps its GGUF rows (no
-     * prepared copy); one already compacted by a mat-vec holds no GGUF rows,
-     * so this returns false and the caller runs the m mat-vecs.  False also
+     * prepared copy); one already compacted by a mat-vec holds only its
+     * mat-vec layout, which serves up to four vectors of at most 4096
+     * columns (the rows then equal its mat-vecs bit for bit), so past that
+     * this returns false and the caller runs the m mat-vecs.  False also
      * when the route is not taken.
      */
     static boolean tryMatVecBatch(GGUFModel model, GGUFTensorInfo tensor, long rows, int columns, long rowBytes,
@@ -152,7 +154,9 @@ final class GgufHipMatVec {
         }
         MemorySegment w = handle(b, model, tensor, rows, columns, rowBytes, false);
         synchronized (HANDLES) {
-            if (COMPACTED.containsKey(w)) {
+            // a compacted handle keeps the mat-vec layout only, which the GEMM
+            // reads for up to four vectors of at most 4096 columns
+            if (COMPACTED.containsKey(w) && (m > 4 || columns > 4096)) {
                 return false;
             }
         }

@@ -556,8 +556,8 @@ def test_compact_handle_holds_one_copy(type_id, rows, cols):
     # After compact() only the prepared layout is held.  Full mat-vecs equal
     # the prepared handle's bit for bit; a prefix and dot_row return exactly
     # the full call's rows; dequantization gathers the rows back from the
-    # layout and stays bit-exact; GEMM raises (it reads GGUF rows);
-    # unprepare() rebuilds the GGUF copy.
+    # layout and stays bit-exact; GEMM runs up to four rows of X on the
+    # layout and raises past that; unprepare() rebuilds the GGUF copy.
     import ctypes
 
     import torch
@@ -594,9 +594,23 @@ def test_compact_handle_holds_one_copy(type_id, rows, cols):
         assert np.array_equal(got.view(np.uint32), deq[r].view(np.uint32))
     got = ops.dequantize_rows(c, rows // 2, min(5, rows - rows // 2))
     assert np.array_equal(got.view(np.uint32), block.view(np.uint32))
-    if type_id in (syn.Q8_0, syn.Q4_0, syn.Q4_K):
-        with pytest.raises(ops.UnsupportedOperationError):
-            ops.gemm_bf16(c, syn.activation_bf16(2, cols, seed=1), np.zeros((2, rows), np.float32))
+    # GEMM: up to four rows of X run the column kernel on the layout (each row
+    # of Y the mat-vec's bits on that X row); more rows, or K past 4096,
+    # need the GGUF rows and raise
+    xb = syn.activation_bf16(4, cols, seed=1)
+    for m in (1, 2, 4):
+        yb = np.full((m, rows), np.nan, np.float32)
+        if cols > 4096:
+            with pytest.raises(ops.UnsupportedOperationError):
+                ops.gemm_bf16(c, xb[:m], yb)
+            continue
+        ops.gemm_bf16(c, xb[:m], yb)
+        for r in range(m):
+            g = np.zeros(rows, np.float32)
+            ops.mat_vec(c, syn.bf16_to_f32(xb[r]), g)
+            assert np.array_equal(yb[r].view(np.uint32), g.view(np.uint32)), (m, r)
+    with pytest.raises(ops.UnsupportedOperationError):
+        ops.gemm_bf16(c, syn.activation_bf16(5, cols, seed=2), np.zeros((5, rows), np.float32))
 
     # the device entries of the compact handle (through the C ABI)
     lib = _native.load()
