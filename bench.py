@@ -666,6 +666,12 @@ def main() -> int:
                     log(f"extra {name}")
                     extra[name], hosts[name] = gemm_workload(torch, m, args.steps, args.warmup, seed=9,
                                                              type_id=t, rows=14336, cols=4096)
+        # Batched decode through the FFN down projection (K 14336, N 4096).
+        name = "q4_k_gemm_bf16_m2_14336x4096"
+        if have_gemm and want(name):
+            log(f"extra {name}")
+            extra[name], hosts[name] = gemm_workload(torch, 2, args.steps, args.warmup, seed=9,
+                                                     type_id=syn.Q4_K, rows=4096, cols=14336)
         if want("q4_k_gemv_host_entry_4096x14336"):
             log("extra host-buffer entry point")
             extra["q4_k_gemv_host_entry_4096x14336"] = host_entry_workload(

@@ -903,7 +903,10 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_col_kernel(
 // row r at part[w][r][h]) and meet at the end in wave order.
 constexpr int kWideMaxCols = 4;  // columns per wave (K <= 16384)
 
-template <int TYPE, bool PREP>
+// NV = 2, XB: as the column kernel's (the small-M GEMM's M = 2 on bf16 X):
+// the second vector's digits in A rows 8..15 of the same compact operands,
+// its sums in output lanes 32..63 and a second row-sum buffer.
+template <int TYPE, bool PREP, int NV = 1, bool XB = false>
 __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes64, int nsb, const float *__restrict__ x,
     float *__restrict__ y, int64_t rows, int rows_per_wg) {
@@ -913,8 +916,9 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
     constexpr int kFull = TB / 1024;
     constexpr int kTail = (TB % 1024) / 256;
     constexpr int kRegionW = 2 * TB + kColX;  // two unit slots, then the x scratch
+    static_assert(NV == 1 || NV == 2, "one or two vectors");
     __shared__ __attribute__((aligned(16))) uint8_t lds[kColWaves * kRegionW];
-    __shared__ float part[kColWaves][G::kMaxRows][2];
+    __shared__ float part[NV][kColWaves][G::kMaxRows][2];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
@@ -922,6 +926,17 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
     const uint32_t row_bytes = (uint32_t)row_bytes64;
     const int tiles = (nr + kTileRows - 1) / kTileRows;
     const int ncol = wv < nsb ? (nsb - wv + kColWaves - 1) / kColWaves : 0;  // wave-uniform
+    // superblock c of vector v (XB: bf16 bits widened exactly)
+    auto load_x = [&](int v, int c) {
+        if constexpr (XB) {
+            const uint2 u = reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(x) +
+                                                            (int64_t)v * nsb * kQK)[64 * c + lane];
+            return float4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u),
+                          __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xFFFF0000u)};
+        } else {
+            return reinterpret_cast<const float4 *>(x + (int64_t)v * nsb * kQK)[64 * c + lane];
+        }
+    };
 
     if (ncol > 0) {
         // The workgroup's block: nr rows (PREP: column c is nr PB-byte pieces
@@ -956,19 +971,35 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
         // unit 0, then every column's operands while unit 0 flies (built
         // between units instead, they held up the units: 9.3 against 8.0 us
         // for Q4_K 4096 x 14336).
-        float4 xq[kWideMaxCols];
+        float4 xq[kWideMaxCols], xq2[kWideMaxCols];
 #pragma unroll
         for (int i = 0; i < kWideMaxCols; i++) {
             const int c = wv + kColWaves * i;
-            xq[i] = reinterpret_cast<const float4 *>(x)[64 * (c < nsb ? c : wv) + lane];
+            xq[i] = load_x(0, c < nsb ? c : wv);
+            if constexpr (NV == 2) xq2[i] = load_x(1, c < nsb ? c : wv);
         }
         __builtin_amdgcn_sched_barrier(0);
         issue(0);
         __builtin_amdgcn_sched_barrier(0);
         XOpsC xc[kWideMaxCols];
 #pragma unroll
-        for (int i = 0; i < kWideMaxCols; i++)
-            if (i < ncol) x_operands4c(xq[i], rbase + 2 * TB, xc[i]);
+        for (int i = 0; i < kWideMaxCols; i++) {
+            if (i < ncol) {
+                x_operands4c(xq[i], rbase + 2 * TB, xc[i]);
+                if constexpr (NV == 2) {
+                    // the second vector in rows 8..15 of the same registers
+                    XOpsC c1;
+                    x_operands4c<true>(xq2[i], rbase + 2 * TB, c1);
+                    const bool second = lane >= 32;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        xc[i].d[k] = uint2{xc[i].d[k].x | c1.d[k].x, xc[i].d[k].y | c1.d[k].y};
+                        xc[i].xs4[k] = second ? c1.xs4[k] : xc[i].xs4[k];
+                    }
+                    xc[i].xs = second ? c1.xs : xc[i].xs;
+                }
+            }
+        }
 
         const int n = lane & 15, g = lane >> 4;
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per tile, summed over the wave's columns in order
@@ -1005,15 +1036,22 @@ __global__ __launch_bounds__(kColThreads) void gemv_mfma_wide_kernel(
                 for (int j = 0; j < 4; j++) acc[j] += t == j ? v : 0.0f;
             }
         }
-        if (lane < 32)
-            for (int t = 0; t < tiles; t++) part[wv][16 * t + n][g] = t == 0 ? acc[0] : t == 1 ? acc[1] : t == 2 ? acc[2] : acc[3];
+        if (lane < 32 || NV == 2)
+            for (int t = 0; t < tiles; t++)
+                part[lane >> 5][wv][16 * t + n][g & 1] =
+                    t == 0 ? acc[0] : t == 1 ? acc[1] : t == 2 ? acc[2] : acc[3];
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const int nw = nsb < kColWaves ? nsb : kColWaves;
-    for (int r = threadIdx.x; r < nr; r += kColThreads) {
+    for (int q = threadIdx.x; q < NV * nr; q += kColThreads) {
+        int v = 0, r = q;
+        if constexpr (NV == 2) {
+            v = q >= nr ? 1 : 0;
+            r = q - v * nr;
+        }
         float s = 0.0f;
-        for (int k = 0; k < nw; k++) s += part[k][r][0] + part[k][r][1];
-        y[r0 + r] = s;
+        for (int k = 0; k < nw; k++) s += part[v][k][r][0] + part[v][k][r][1];
+        y[(int64_t)v * rows + r0 + r] = s;
     }
 }
 
@@ -1152,11 +1190,12 @@ bool q32_mfma_supported(int type_id, int64_t row_bytes, int64_t cols, int64_t ro
 
 // The small-M GEMM at M = 1 .. 4 on the column kernel (X: M bf16 rows of K,
 // Y: M rows of N floats): the GEMV's stream of the weights once, two
-// vectors in each MFMA.  Weights of a type the column kernel takes, K a
-// multiple of 256 up to 4096, a row count its partition takes, 16-byte
-// aligned weights and 8-byte aligned X.
+// vectors in each MFMA; past K = 4096 (up to 16384) the wide kernel, M up
+// to 2.  Weights of a type those kernels take, K a multiple of 256, a row
+// count their partition takes, 16-byte aligned weights and 8-byte aligned X.
 bool gemm_col_supported(int type_id, int64_t row_bytes, int M, int N, int K, const void *w, const void *x) {
-    if (M < 1 || M > 4 || N <= 0 || K <= 0 || K % kQK != 0 || K / kQK > kColWaves) return false;
+    if (M < 1 || M > 4 || N <= 0 || K <= 0 || K % kQK != 0 || K / kQK > kColWaves * kWideMaxCols) return false;
+    if (K / kQK > kColWaves && M > 2) return false;  // the wide kernel holds two vectors
     if (type_id != kQ4_K && type_id != kQ5_K && type_id != kQ4_0 && type_id != kQ8_0) return false;
     const int64_t piece = type_id == kQ8_0 ? 8 * kQ8BlockBytes : type_id == kQ5_K ? kQ5KBlockBytes : kQKBlockBytes;
     if (row_bytes != (int64_t)(K / kQK) * piece) return false;
@@ -1183,9 +1222,21 @@ hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, con
             hipLaunchKernelGGL((gemv_mfma_col_kernel<T, false, NV, true>), grid, dim3(kColThreads), 0, stream,  \
                                src, row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                        \
     } while (0)
+#define GOLLEK_GEMM_WIDE_NV(T, NV)                                                                             \
+    do {                                                                                                       \
+        if (use_prep)                                                                                          \
+            hipLaunchKernelGGL((gemv_mfma_wide_kernel<T, true, NV, true>), grid, dim3(kColThreads), 0, stream,  \
+                               src, row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                        \
+        else                                                                                                   \
+            hipLaunchKernelGGL((gemv_mfma_wide_kernel<T, false, NV, true>), grid, dim3(kColThreads), 0, stream, \
+                               src, row_bytes, nsb, xf, y, (int64_t)N, (int)col_rows);                        \
+    } while (0)
 #define GOLLEK_GEMM_COL(T)                                                                                      \
     do {                                                                                                        \
-        if (M == 1) GOLLEK_GEMM_COL_NV(T, 1);                                                                   \
+        if (nsb > kColWaves) {                                                                                  \
+            if (M == 1) GOLLEK_GEMM_WIDE_NV(T, 1);                                                              \
+            else GOLLEK_GEMM_WIDE_NV(T, 2);                                                                     \
+        } else if (M == 1) GOLLEK_GEMM_COL_NV(T, 1);                                                            \
         else if (M == 2) GOLLEK_GEMM_COL_NV(T, 2);                                                              \
         else if (M == 3) GOLLEK_GEMM_COL_NV(T, 3);                                                              \
         else GOLLEK_GEMM_COL_NV(T, 4);                                                                          \
@@ -1195,6 +1246,7 @@ hipError_t launch_gemm_col(int type_id, const uint8_t *w, int64_t row_bytes, con
     else if (type_id == kQ8_0) GOLLEK_GEMM_COL(kQ8_0);
     else GOLLEK_GEMM_COL(kQ4_0);
 #undef GOLLEK_GEMM_COL
+#undef GOLLEK_GEMM_WIDE_NV
 #undef GOLLEK_GEMM_COL_NV
     return hipGetLastError();
 }

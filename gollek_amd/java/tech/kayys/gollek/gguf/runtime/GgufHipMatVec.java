@@ -138,7 +138,8 @@ final class GgufHipMatVec {
      * that GEMM takes it.  A tensor first seen here keeps its GGUF rows (no
      * prepared copy); one already compacted by a mat-vec holds only its
      * mat-vec layout, which serves up to four vectors of at most 4096
-     * columns (the rows then equal its mat-vecs bit for bit), so past that
+     * columns or two of at most 16384 (the rows then equal its mat-vecs bit
+     * for bit), so past that
      * this returns false and the caller runs the m mat-vecs.  False also
      * when the route is not taken.
      */
@@ -155,8 +156,9 @@ final class GgufHipMatVec {
         MemorySegment w = handle(b, model, tensor, rows, columns, rowBytes, false);
         synchronized (HANDLES) {
             // a compacted handle keeps the mat-vec layout only, which the GEMM
-            // reads for up to four vectors of at most 4096 columns
-            if (COMPACTED.containsKey(w) && (m > 4 || columns > 4096)) {
+            // reads for up to four vectors of at most 4096 columns (two of at
+            // most 16384)
+            if (COMPACTED.containsKey(w) && (m > (columns > 4096 ? 2 : 4) || columns > 16384)) {
                 return false;
             }
         }

@@ -132,7 +132,8 @@ int32_t gollek_hip_weight_unprepare(gollek_hip_weight *weight, char *err, size_t
  * or a single row returns exactly the full call's bits for its rows;
  * dequantize_rows gathers the rows' bytes back from the layout first (the
  * same bytes, so the same bits).  The GEMM entry points run up to four
- * rows of X (8-byte aligned) on the layout when K <= 4096; other GEMM shapes
+ * rows of X (8-byte aligned) on the layout when K <= 4096, two up to K =
+ * 16384; other GEMM shapes
  * and the MoE entry points read GGUF rows and return UNSUPPORTED for a
  * compacted handle;
  * gollek_hip_weight_unprepare rebuilds the GGUF copy (and frees the

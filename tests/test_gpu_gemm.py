@@ -56,14 +56,21 @@ def test_gemm_row_equals_gemv(q8_4096):
 
 # M = 1 .. 4 run the GEMV's column kernel with two vectors in each MFMA (the
 # second of a pair in A rows 8..15; vectors 2 and 3 in a second operand
-# set): every row of Y equals, bit for bit, the
+# set), and M = 1, 2 past K = 4096 its wide kernel: every row of Y equals,
+# bit for bit, the
 # mat-vec of that row of X widened to fp32 (the same digits, products and
 # sums), and sits within the GEMM bar of the fp64 oracle.  Row counts that
 # end in a partial 16-row tile (4000) included.
-@pytest.mark.parametrize("type_id,rows,cols", [(syn.Q4_K, 14336, 4096), (syn.Q5_K, 4096, 4096),
-                                               (syn.Q4_0, 11008, 4096), (syn.Q8_0, 4096, 4096),
-                                               (syn.Q8_0, 4000, 2048), (syn.Q4_K, 1792, 4096)])
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+COLUMN_GEMM_CASES = [(t, r, c, m) for t, r, c in [(syn.Q4_K, 14336, 4096), (syn.Q5_K, 4096, 4096),
+                                                   (syn.Q4_0, 11008, 4096), (syn.Q8_0, 4096, 4096),
+                                                   (syn.Q8_0, 4000, 2048), (syn.Q4_K, 1792, 4096)]
+                     for m in (1, 2, 3, 4)] + \
+                    [(t, r, c, m) for t, r, c in [(syn.Q4_K, 4096, 14336), (syn.Q5_K, 4096, 14336),
+                                                   (syn.Q4_0, 4096, 11008), (syn.Q8_0, 4096, 8192)]
+                     for m in (1, 2)]
+
+
+@pytest.mark.parametrize("type_id,rows,cols,m", COLUMN_GEMM_CASES)
 def test_gemm_small_m_on_the_column_kernel_equals_gemv(type_id, rows, cols, m):
     print(f"[gpu] gemm column kernel type={type_id} m={m} n={rows} k={cols}", flush=True)
     data = syn.matrix(type_id, rows, cols, seed=rows + m)

@@ -180,7 +180,7 @@ def test_batch_checks_lengths_and_skips_compacted_handles():
     for cond in ("xRows.length < (long) m * columns", "out.length < (long) m * rows"):
         assert cond in body, cond
     assert "handle(b, model, tensor, rows, columns, rowBytes, false)" in body
-    assert "COMPACTED.containsKey(w) && (m > 4 || columns > 4096)" in body
+    assert "COMPACTED.containsKey(w) && (m > (columns > 4096 ? 2 : 4) || columns > 16384)" in body
     assert body.index("COMPACTED.containsKey(w)") < body.index("b.gemmBf16(")
     assert body.index("IllegalArgumentException") < body.index("b.gemmBf16(")
 
