@@ -118,10 +118,11 @@ def _gemm_case(type_id, rows, cols, m, seed):
 
 @pytest.mark.parametrize("type_id", TYPES)
 @pytest.mark.parametrize("rows,cols,m", [(128, 256, 33), (192, 4096, 300), (80, 512, 129), (4096, 256, 257),
-                                          (1000, 1024, 64), (256, 2048, 1024), (64, 4096, 40)])
+                                          (1000, 1024, 64), (256, 2048, 1024), (64, 4096, 40), (300, 1024, 96)])
 def test_gemm_tile_kernel_shapes(type_id, rows, cols, m):
     # The tile kernel (16 MT x 128 tiles: MT = 8 past M = 64, 4 for M = 33
-    # .. 64): K from one four-stage round (256) up, a
+    # .. 64 and for Q8_0 up to 128 when N has at most 32 column tiles, as
+    # at M = 96 here): K from one four-stage round (256) up, a
     # partial last M tile (rows past M read zeros) and N tile (rows past N),
     # one to many tiles, grids that are and are not a multiple of 8, and the
     # K splits the CU count allows (none for K = 256, up to 8).
