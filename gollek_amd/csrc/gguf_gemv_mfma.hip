@@ -1301,7 +1301,11 @@ int64_t col_layout_rows(int type_id, int64_t rows, int64_t cols) {
     const int64_t most = type_id == kQ8_0   ? ColGeom<kQ8_0>::kMaxRows
                          : type_id == kQ5_K ? ColGeom<kQ5_K>::kMaxRows
                                             : ColGeom<kQ4_0>::kMaxRows;
-    return per < most ? per : most;
+    // Q4_0 with K <= 4096: whole 16-row tiles per workgroup (4096 x 11008:
+    // 48 rows on 230 workgroups, 7.0 us, against 43 on 256 with a last tile
+    // of 11 rows, 7.3 us; the GGUF rows in place 7.43 against 7.47 us).
+    const int64_t pp = type_id == kQ4_0 && nsb <= kColWaves ? (per + kTileRows - 1) / kTileRows * kTileRows : per;
+    return pp < most ? pp : most;
 }
 
 namespace {

@@ -423,7 +423,9 @@ def test_device_pointer_entry_points_match_host():
 
 # Column-kernel shapes (at most 64 / 48 / 32 rows per CU for Q4_K and Q4_0
 # / Q5_K / Q8_0, the last two capped by more workgroups; K <= 4096 one
-# column per wave, up to 16384 several), a ragged one, and shapes with no
+# column per wave, up to 16384 several; Q4_0 with K <= 4096 in whole 16-row
+# tiles per workgroup, as 3001 x 2048: 16 rows on 188 workgroups, the last
+# one 9), a ragged one, and shapes with no
 # prepared layout (too many rows per CU, Q6_K, K > 16384) where prepare() is
 # a no-op.
 PREP_SHAPES = [(syn.Q4_K, 14336, 4096), (syn.Q4_K, 1001, 2304), (syn.Q4_K, 4000, 256),
@@ -431,7 +433,7 @@ PREP_SHAPES = [(syn.Q4_K, 14336, 4096), (syn.Q4_K, 1001, 2304), (syn.Q4_K, 4000,
                (syn.Q5_K, 4096, 4096), (syn.Q5_K, 12289, 4096), (syn.Q4_K, 16385, 4096),
                (syn.Q6_K, 4096, 4096), (syn.Q4_K, 33, 8192), (syn.Q4_K, 4096, 14336),
                (syn.Q8_0, 4096, 11008), (syn.Q4_0, 1001, 16384), (syn.Q5_K, 3000, 14336),
-               (syn.Q4_K, 20000, 6144), (syn.Q8_0, 200, 16896)]
+               (syn.Q4_K, 20000, 6144), (syn.Q8_0, 200, 16896), (syn.Q4_0, 3001, 2048)]
 
 
 @pytest.mark.parametrize("type_id,rows,cols", PREP_SHAPES,
